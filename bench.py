@@ -1,0 +1,388 @@
+"""Benchmark of the MI355X WKV-7 + .rwkvq hot path (one GPU).
+
+Headline (`value`): one-token decode of the 0.1B x070 shape (12 layers,
+n_embd 768, FFN 3072, vocab 65536), batch 1: every decode GEMV of the token
+(r/k/v/o 768x768, ffn key 3072x768, ffn value 768x3072, head 65536x768; sb6
+4-bit weights encoded from seeded N(0, 0.02)) plus the WKV-7 decode step and
+the tmix tail of each layer.  A step = one token.  The token's 97 launches are
+captured once per weight copy into a HIP graph; steps rotate over
+`--copies` copies of the weights (> 256 MB in total) so they stream from HBM
+instead of the MALL.  Inputs are resident in HBM before the timed region.
+
+Also reported (`extra`): WKV-7 forward tokens/s at B1 T1024 H12 fp32, WKV-7
+forward and forward+backward tokens/s at B8 T4096 H32 bf16 (checkpointed),
+the head-GEMV HBM GB/s, and the CPU restatement of the WKV forward.
+
+`roofline` is for the dominant kernel, the head sb6 GEMV; `cpu_baseline`
+times the oracle's restatement of the reference's non-kernel decode path
+(dequantise to fp32, x·Wᵀ) on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "WKV-7 tokens/s (fwd, fwd+bwd); .rwkvq GEMV GB/s; 1.5B decode tok/s"
+HBM_PEAK_GBPS = 8000.0
+VALU_PEAK_TFLOPS = 157.3
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--copies", type=int, default=6)
+    p.add_argument("--skip-cpu", action="store_true")
+    p.add_argument("--skip-wkv", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    return p.parse_args()
+
+
+# ───────────────────────────── decode model ─────────────────────────────
+
+class DecodeModel:
+    """Packed weights of all projections (K3 layout on the device), per copy."""
+
+    def __init__(self, shape, copies, dev, nthreads):
+        import numpy as np
+        import torch
+        from swiftrwkv_amd import quant as Q
+
+        self.shape = shape
+        self.host = {}
+        self.dev = [dict() for _ in range(copies)]
+        self.bytes_per_token = 0
+        t0 = time.time()
+        for idx, (key, OUT, IN) in enumerate(shape.projections()):
+            rng = np.random.default_rng(1000 + idx)
+            w = (rng.standard_normal((OUT, IN), dtype=np.float32) * np.float32(0.02))
+            disk = Q.encode_sb6(w, 4, nthreads)
+            qblk, qsqm, ddm, xb = Q.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"],
+                                                    disk["gw_dm"], None, None, (OUT, IN))
+            self.host[key] = (qblk, qsqm, ddm, OUT, IN)
+            base = (torch.from_numpy(qblk).to(dev), torch.from_numpy(qsqm).to(dev),
+                    torch.from_numpy(ddm.view(np.float16)).to(dev))
+            self.dev[0][key] = base
+            for c in range(1, copies):
+                self.dev[c][key] = tuple(z.clone() for z in base)
+            self.bytes_per_token += qblk.nbytes + qsqm.nbytes + ddm.nbytes + 4 * (IN + OUT)
+        log(f"encoded {len(self.host)} matrices of {shape.name} in {time.time() - t0:.1f}s, "
+            f"{self.bytes_per_token / 1e6:.1f} MB per token, {copies} device copies")
+
+
+class DecodeStep:
+    """Buffers and the launch sequence of one decode token (batch B)."""
+
+    def __init__(self, model: DecodeModel, dev, B=1, seed=0):
+        import numpy as np
+        import torch
+        from swiftrwkv_amd import synthetic as syn
+
+        s = model.shape
+        self.model, self.B, self.L, self.H, self.D, self.F = model, B, s.n_layer, s.n_head, s.n_embd, s.ffn
+        rng = np.random.default_rng(seed)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+        self.xD = t(rng.standard_normal((B, self.D)))
+        self.xF = t(np.maximum(rng.standard_normal((B, self.F)), 0) ** 2 * 0.1)
+        self.y_rkv = torch.empty((3, B, self.D), device=dev)
+        self.y_o = torch.empty((B, self.D), device=dev)
+        self.y_k = torch.empty((B, self.F), device=dev)
+        self.y_v = torch.empty((B, self.D), device=dev)
+        self.logits = torch.empty((B, s.vocab), device=dev)
+        self.wkv = torch.empty((B, self.H, 64), device=dev)
+        self.tail = torch.empty((B, self.D), device=dev)
+        vec = syn.wkv_inputs_config0(self.L, B, self.H, seed=seed + 1)   # [L, B, H, 64] per input
+        self.rwkvab = [t(z) for z in vec]
+        self.state = torch.zeros((self.L, B, self.H, 64, 64), device=dev)
+        self.rk = t(rng.standard_normal((self.L, self.D)) * 0.1)
+        self.lnw = t(rng.standard_normal((self.L, self.D)) * 0.5 + 1)
+        self.lnb = t(rng.standard_normal((self.L, self.D)) * 0.1)
+        self.g = t(rng.standard_normal((self.L, B, self.D)))
+
+    def launch(self, copy: int, stream: int):
+        from swiftrwkv_amd import _lib
+        L = _lib.lib()
+        W = self.model.dev[copy]
+        B, D, F, H = self.B, self.D, self.F, self.H
+
+        def gemv(x, key, y):
+            q = W[key]
+            OUT, IN = self.model.host[key][3], self.model.host[key][4]
+            _lib.check(L.rwkv_sb6_gemv(x.data_ptr(), B, q[0].data_ptr(), q[1].data_ptr(), q[2].data_ptr(),
+                                       y.data_ptr(), OUT, IN, 0, stream))
+
+        for l in range(self.L):
+            for j, m in enumerate(("receptance", "key", "value")):
+                gemv(self.xD, f"blocks.{l}.att.{m}.weight", self.y_rkv[j])
+            r, w, k, v, a, b = (z[l] for z in self.rwkvab)
+            st = self.state[l]
+            _lib.check(L.rwkv_wkv7_step(r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(), a.data_ptr(),
+                                        b.data_ptr(), 0, st.data_ptr(), self.wkv.data_ptr(), st.data_ptr(), B, H,
+                                        stream))
+            _lib.check(L.rwkv_wkv_tail(self.wkv.data_ptr(), r.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                       self.rk[l].data_ptr(), self.lnw[l].data_ptr(), self.lnb[l].data_ptr(),
+                                       self.g[l].data_ptr(), self.tail.data_ptr(), B, H, 64,
+                                       float(64e-5), stream))
+            gemv(self.tail, f"blocks.{l}.att.output.weight", self.y_o)
+            gemv(self.xD, f"blocks.{l}.ffn.key.weight", self.y_k)
+            gemv(self.xF, f"blocks.{l}.ffn.value.weight", self.y_v)
+        gemv(self.xD, "head.weight", self.logits)
+
+
+def bench_decode(args, dev):
+    import torch
+    from swiftrwkv_amd import synthetic as syn
+
+    model = DecodeModel(syn.X070_0B1, args.copies, dev, nthreads=min(16, os.cpu_count() or 1))
+    step = DecodeStep(model, dev)
+    stream = torch.cuda.Stream(device=dev)
+    # eager reference token from a known state, then graphs (one per weight copy)
+    with torch.cuda.stream(stream):
+        s0 = step.state.clone()
+        step.launch(0, stream.cuda_stream)
+        eager = step.logits.clone()
+        eager_state = step.state.clone()
+        torch.cuda.synchronize()
+        graphs = []
+        for c in range(args.copies):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step.launch(c, torch.cuda.current_stream().cuda_stream)
+            graphs.append(g)
+        torch.cuda.synchronize()
+        for rep in range(3):   # every replay reproduces the eager token bitwise
+            step.state.copy_(s0)
+            torch.cuda.synchronize()
+            graphs[rep % args.copies].replay()
+            torch.cuda.synchronize()
+            if not (torch.equal(step.logits, eager) and torch.equal(step.state, eager_state)):
+                raise RuntimeError(f"graph replay {rep} differs from the eager decode token")
+        step.state.copy_(s0)
+        for i in range(args.warmup):
+            graphs[i % args.copies].replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(args.steps):
+            graphs[i % args.copies].replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    gpu_ms = e0.elapsed_time(e1)
+    log(f"decode 0.1B: {args.steps} tokens, wall {wall * 1e3:.2f} ms, gpu {gpu_ms:.2f} ms")
+    return model, step, wall, gpu_ms
+
+
+def bench_head_gemv(model, dev, reps=60):
+    """Average duration of the head GEMV over rotated weight copies (HBM)."""
+    import torch
+    from swiftrwkv_amd import _lib
+
+    key = "head.weight"
+    qblk, qsqm, ddm, OUT, IN = model.host[key]
+    x = torch.randn((1, IN), device=dev)
+    y = torch.empty((1, OUT), device=dev)
+    L = _lib.lib()
+    stream = torch.cuda.current_stream(dev)
+    copies = len(model.dev)
+
+    def launch(c):
+        q = model.dev[c][key]
+        _lib.check(L.rwkv_sb6_gemv(x.data_ptr(), 1, q[0].data_ptr(), q[1].data_ptr(), q[2].data_ptr(), y.data_ptr(),
+                                   OUT, IN, 0, stream.cuda_stream))
+
+    for i in range(10):
+        launch(i % copies)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i in range(reps):
+        evs[i][0].record(stream)
+        launch(i % copies)
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    durs = sorted(a.elapsed_time(b) for a, b in evs)
+    avg_ms = sum(durs) / len(durs)
+    nbytes = qblk.nbytes + qsqm.nbytes + ddm.nbytes + 4 * (IN + OUT)
+    return nbytes, avg_ms, durs[len(durs) // 2]
+
+
+def bench_wkv(dev, reps=5):
+    import numpy as np
+    import torch
+    from swiftrwkv_amd import kernel as K, synthetic as syn
+
+    res = {}
+    # config 0: B1 T1024 H12 fp32 forward
+    x = [torch.from_numpy(z).to(dev) for z in syn.wkv_inputs_config0(1, 1024, 12, seed=0)]
+    for _ in range(3):
+        K.wkv7_sequence_forward(*x)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps * 4):
+        K.wkv7_sequence_forward(*x)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * 4)
+    res["wkv7_fwd_B1_T1024_H12_fp32"] = {"ms": ms, "tok_s": 1024 / (ms * 1e-3),
+                                         "valu_roofline_frac": (1024 * 12 * 9 * 64 * 64 / (ms * 1e-3)) / (VALU_PEAK_TFLOPS * 1e12)}
+    del x
+    # config 3: B8 T4096 H32 bf16 training forward (checkpointed) + backward
+    B, T, H = 8, 4096, 32
+    rng = np.random.default_rng(3)
+    xs = syn.wkv_inputs_config0(B, T, H, seed=3)
+    ins = [torch.from_numpy(z).to(dev).to(torch.bfloat16) for z in xs]
+    del xs
+    dy = torch.from_numpy(rng.standard_normal((B, T, H, 64), dtype=np.float32)).to(dev)
+    ins_p, dt = K._prep(ins)
+    grads = [torch.empty((B, T, H, 64), dtype=torch.bfloat16, device=dev) for _ in range(6)]
+    dh_in = torch.empty((B, H, 64, 64), device=dev)
+    from swiftrwkv_amd import _lib
+
+    def fwd():
+        return K._train_forward(ins_p, dt, None)
+
+    def bwd(sa, ck):
+        _lib.call("rwkv_wkv7_train_bwd", *[z.data_ptr() for z in ins_p], dt, ck.data_ptr(), sa.data_ptr(),
+                  dy.data_ptr(), None, *[g.data_ptr() for g in grads], _lib.BF16, dh_in.data_ptr(), B, T, H, 2,
+                  torch.cuda.current_stream().cuda_stream)
+
+    out, h_out, sa, ck = fwd()
+    bwd(sa, ck)
+    torch.cuda.synchronize()
+    ef = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    tf = tb = 0.0
+    for _ in range(reps):
+        ef[0].record()
+        out, h_out, sa, ck = fwd()
+        ef[1].record()
+        bwd(sa, ck)
+        ef[2].record()
+        torch.cuda.synchronize()
+        tf += ef[0].elapsed_time(ef[1])
+        tb += ef[1].elapsed_time(ef[2])
+    tf /= reps
+    tb /= reps
+    th = B * T * H
+    res["wkv7_B8_T4096_H32_bf16"] = {
+        "fwd_ms": tf, "bwd_ms": tb, "fwd_tok_s": B * T / (tf * 1e-3), "fwdbwd_tok_s": B * T / ((tf + tb) * 1e-3),
+        "fwd_valu_roofline_frac": th * 9 * 4096 / (tf * 1e-3) / (VALU_PEAK_TFLOPS * 1e12),
+        "bwd_valu_roofline_frac": th * 24 * 4096 / (tb * 1e-3) / (VALU_PEAK_TFLOPS * 1e12)}
+    return res
+
+
+def cpu_baseline(model, step, seconds):
+    """The oracle's restatement of the non-kernel decode path on the host."""
+    import numpy as np
+    from oracle import oracle as orc
+
+    nthreads = min(16, orc.max_threads())
+    xD = step.xD.cpu().numpy()[0]
+    xF = step.xF.cpu().numpy()[0]
+    vecs = [z.cpu().numpy() for z in step.rwkvab]
+    state = np.zeros((step.L, 1, step.H, 64, 64), np.float32)
+    out = np.empty((1, step.H, 64), np.float32)
+    ys = {}
+
+    def token():
+        for key, (qblk, qsqm, ddm, OUT, IN) in model.host.items():
+            x = xF if IN == step.F else xD
+            ys[key] = orc.cpu_sb6_dequant_matvec(x, qblk, qsqm, ddm, OUT, IN, 0, nthreads)
+        for l in range(step.L):
+            r, w, k, v, a, b = (np.ascontiguousarray(z[l]) for z in vecs)
+            orc.cpu_wkv7_step(r, w, k, v, a, b, state[l], out, 1, step.H, nthreads)
+
+    token()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds and n < 2000:
+        token()
+        n += 1
+    el = time.perf_counter() - t0
+    # check the CPU head against the GPU head GEMV of copy 0 (same bytes, same x)
+    return {"value": n / el, "unit": "tok/s", "cores": nthreads, "kind": "port",
+            "sample": f"{n} decode tokens of the 0.1B shape (73 sb6 dequant+fp32 matvecs + 12 WKV steps), "
+                      f"{el:.1f} s, OpenMP over output rows"}
+
+
+def cpu_wkv_baseline():
+    import numpy as np
+    from oracle import oracle as orc
+    from swiftrwkv_amd import synthetic as syn
+
+    x = syn.wkv_inputs_config0(1, 1024, 12, seed=0)
+    nthreads = min(16, orc.max_threads())
+    orc.wkv7_fwd_f32(*x, nthreads=nthreads)
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < 2.0:
+        orc.wkv7_fwd_f32(*x, nthreads=nthreads)
+        n += 1
+    el = (time.perf_counter() - t0) / n
+    return {"value": 1024 / el, "unit": "tok/s", "cores": nthreads, "kind": "port",
+            "sample": f"WKV-7 forward B1 T1024 H12 fp32 x{n}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU runs are not part of this build", file=sys.stderr)
+        sys.exit(1)
+    import torch
+    from swiftrwkv_amd import _lib
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    log(f"device {torch.cuda.get_device_name(0)}")
+    model, step, wall, gpu_ms = bench_decode(args, dev)
+    nbytes, head_avg_ms, head_med_ms = bench_head_gemv(model, dev)
+    achieved = nbytes / (head_avg_ms * 1e-3) / 1e9
+    log(f"head GEMV: {nbytes / 1e6:.2f} MB, avg {head_avg_ms * 1e3:.1f} us -> {achieved:.0f} GB/s")
+    extra = {
+        "decode_gpu_ms_per_token": gpu_ms / args.steps,
+        "decode_gemv_bytes_per_token": model.bytes_per_token,
+        "decode_effective_GBps": model.bytes_per_token / (gpu_ms * 1e-3 / args.steps) / 1e9,
+        "head_gemv_65536x768": {"bytes": nbytes, "avg_us": head_avg_ms * 1e3, "median_us": head_med_ms * 1e3,
+                                "GBps": achieved},
+    }
+    if not args.skip_wkv:
+        extra.update(bench_wkv(dev))
+        log("wkv done")
+    cpu = None
+    if not args.skip_cpu:
+        cpu = cpu_baseline(model, step, args.cpu_seconds)
+        extra["cpu_wkv7_fwd_B1_T1024_H12"] = cpu_wkv_baseline()
+        log("cpu baseline done")
+    value = args.steps / wall
+    line = {
+        "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "one-token decode, 0.1B x070 shape: 73 sb6 4-bit GEMVs (r/k/v/o 768x768, "
+                               "ffn 3072x768 + 768x3072, head 65536x768) + 12 WKV-7 steps + 12 tails, batch 1",
+                   "n_layer": 12, "n_embd": 768, "ffn": 3072, "vocab": 65536, "batch": 1,
+                   "weights": "sb6 4-bit from seeded N(0,0.02)", "weight_copies_rotated": args.copies,
+                   "hip_graph_per_token": True},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "sb6_gemv head 65536x768 (4-bit), bytes = packed weights + x + y"},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,225 @@
+/*
+ * rwkv_hip.h — C ABI of the MI355X (gfx950) WKV-7 + .rwkvq hot path.
+ *
+ * Drop-in replacement for the MLX/Metal kernel dispatch of SwiftRWKV's
+ * RWKVKernel and RWKVQuant modules.  Each entry point names the Swift
+ * function (RafaelUI/SwiftRWKV, file:line) whose kernel launch it replaces.
+ *
+ * Conventions
+ *  - Plain C, no C++ or torch types.  All tensors are caller-allocated device
+ *    buffers (HIP device pointers), row-major, densely packed.
+ *  - Shapes: WKV inputs [B,T,H,64]; state [B,H,64(dv),64(dk)] (value index =
+ *    row, key index = column); train checkpoints [B,H,T/16,64,64].
+ *  - A NULL `h_in` / `d_h_out` means an all-zero state / cotangent (the
+ *    reference's `hIn: nil`, `MLXArray.zeros`).
+ *  - Every call takes a `hipStream_t` (passed as void*; NULL = default stream)
+ *    and is asynchronous on it.  Nothing allocates device memory.
+ *  - Errors come back as rwkv_status instead of the reference's
+ *    precondition traps; rwkv_last_error() holds a message (thread-local).
+ *  - "applies" predicates return 1/0 exactly like the reference's
+ *    *Applies functions, so a caller falls back the same way.
+ *  - Launch counters mirror the reference's test counters
+ *    (wkv7SequenceLaunches, wkv7TrainForwardLaunches, rwkvq*Calls).
+ */
+#ifndef RWKV_HIP_H
+#define RWKV_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RWKV_HIP_ABI_VERSION 1
+
+typedef enum {
+    RWKV_OK = 0,
+    RWKV_E_SHAPE = 1,        /* shape precondition violated (T, D, OUT, IN, rows ...) */
+    RWKV_E_DTYPE = 2,        /* unsupported dtype code */
+    RWKV_E_UNSUPPORTED = 3,  /* valid request this build does not implement */
+    RWKV_E_FORMAT = 4,       /* malformed .rwkvq / safetensors container or manifest */
+    RWKV_E_HIP = 5,          /* HIP runtime error (launch, device) */
+    RWKV_E_NULL = 6,         /* required pointer is NULL */
+    RWKV_E_IO = 7            /* file missing / unreadable */
+} rwkv_status;
+
+typedef enum { RWKV_F32 = 0, RWKV_BF16 = 1, RWKV_F16 = 2 } rwkv_dtype;
+
+/* Library identity and error reporting. */
+int rwkv_abi_version(void);
+const char* rwkv_status_string(rwkv_status s);
+const char* rwkv_last_error(void);
+
+/* WKV7_HEAD_SIZE / WKV7_CHUNK — Sources/RWKVKernel/WKV7.swift:7-8. */
+int rwkv_wkv7_head_size(void);
+int rwkv_wkv7_chunk(void);
+
+/* ───────────────────────────── RWKVKernel: WKV-7 ───────────────────────────── */
+
+/* Whole-sequence frozen forward, any T >= 1, one launch.
+ * Replaces wkv7SequenceForward (Sources/RWKVKernel/WKV7.swift:242-264).
+ * r..b: [B,T,H,64] of in_dt (widened to fp32 in registers, exactly like the
+ * reference's asType(.float32)); h_in [B,H,64,64] fp32 or NULL;
+ * out [B,T,H,64] fp32; h_out [B,H,64,64] fp32. */
+rwkv_status rwkv_wkv7_seq_fwd(const void* r, const void* w, const void* k, const void* v,
+                              const void* a, const void* b, rwkv_dtype in_dt,
+                              const float* h_in, float* out, float* h_out,
+                              int64_t B, int64_t T, int64_t H, void* stream);
+
+/* One 16-token chunk, also emitting sa = S·a per step.
+ * Replaces wkv7ChunkForward (WKV7.swift:64-82).  T must equal 16.
+ * h_in is required (the reference passes an explicit state). */
+rwkv_status rwkv_wkv7_chunk_fwd(const void* r, const void* w, const void* k, const void* v,
+                                const void* a, const void* b, rwkv_dtype in_dt,
+                                const float* h_in, float* out, float* h_out, float* sa_out,
+                                int64_t B, int64_t T, int64_t H, void* stream);
+
+/* Training forward: out, h_out, sa [B,T,H,64] and the state after every
+ * 16-token chunk, h_ckpt [B,H,T/16,64,64].  T % 16 == 0.  Bitwise equal to
+ * rwkv_wkv7_seq_fwd on out/h_out.  Replaces ckptFwdKernel launched by
+ * wkv7TrainWithState (Sources/RWKVKernel/WKV7Train.swift:26-97,390-397). */
+rwkv_status rwkv_wkv7_train_fwd(const void* r, const void* w, const void* k, const void* v,
+                                const void* a, const void* b, rwkv_dtype in_dt,
+                                const float* h_in, float* out, float* h_out,
+                                float* sa_out, float* h_ckpt,
+                                int64_t B, int64_t T, int64_t H, void* stream);
+
+/* Backward from checkpoints.  Replaces ckptBwdKernelV2 / ckptBwdKernel
+ * launched by the VJP of wkv7TrainWithState (WKV7Train.swift:99-339,410-420).
+ * d_out [B,T,H,64] fp32; d_h_out [B,H,64,64] fp32 or NULL.  Gradients
+ * dr..db [B,T,H,64] are written in g_dt (the primal's dtype, :440,462);
+ * dh_in [B,H,64,64] fp32.  variant: 2 = column-owned state (reference
+ * default, wkv7BackwardV2 = true), 1 = row-owned state (the v1 kernel).
+ * The two variants sum in different orders, as in the reference. */
+rwkv_status rwkv_wkv7_train_bwd(const void* r, const void* w, const void* k, const void* v,
+                                const void* a, const void* b, rwkv_dtype in_dt,
+                                const float* h_ckpt, const float* sa,
+                                const float* d_out, const float* d_h_out,
+                                void* dr, void* dw, void* dk, void* dv, void* da, void* db,
+                                rwkv_dtype g_dt, float* dh_in,
+                                int64_t B, int64_t T, int64_t H, int variant, void* stream);
+
+/* One-token decode step for B rows.  r..b [B,H,64]; h_in/h_out [B,H,64,64]
+ * fp32 (may alias: in-place update is safe); out [B,H,64] fp32.
+ * Replaces wkv7StepForward (Sources/RWKVKernel/WKV7DecodeKernels.swift:73-89),
+ * which is B = 1 only; bitwise equal to rwkv_wkv7_seq_fwd at T = 1. */
+rwkv_status rwkv_wkv7_step(const void* r, const void* w, const void* k, const void* v,
+                           const void* a, const void* b, rwkv_dtype in_dt,
+                           const float* h_in, float* out, float* h_out,
+                           int64_t B, int64_t H, void* stream);
+
+/* wkvTailApplies (WKV7DecodeKernels.swift:92): S % 32 == 0. */
+int rwkv_wkv_tail_applies(int64_t S);
+
+/* tmix tail over N rows: ((gn(wkv)·lnw + lnb) + Σ(r·k·rk)·v)·g, two-pass
+ * group norm per (row, head).  wkv, r, k, v, g, out [N, H·S] fp32;
+ * rk, lnw, lnb [H·S] fp32.  Replaces wkvTail (WKV7DecodeKernels.swift:106-178). */
+rwkv_status rwkv_wkv_tail(const float* wkv, const float* r, const float* k, const float* v,
+                          const float* rk, const float* lnw, const float* lnb, const float* g,
+                          float* out, int64_t N, int64_t H, int64_t S, float eps, void* stream);
+
+/* ───────────────────────────── RWKVQuant: dequant / GEMV ───────────────────────────── */
+
+/* sb6 K3 interleave → dense [OUT, IN] in out_dt (combine always in fp32).
+ * qblk [OUT, IN/32·(16+4·xbits)] u8; qsqm [OUT, IN/32·2] u8; ddm [OUT, IN/256·2]
+ * fp16 bits.  Replaces rwkvqDequantDense (Sources/RWKVQuant/RwkvqDequant.swift:160-183). */
+rwkv_status rwkv_sb6_dequant(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
+                             void* out, rwkv_dtype out_dt, int64_t OUT, int64_t IN, int xbits,
+                             void* stream);
+
+/* sym interleave → dense.  bits 8: qblk [OUT, IN] int8 (IN % 16 == 0);
+ * bits 6: qblk [OUT, IN/32·24] (IN % 32 == 0).  qs [OUT, IN/16] int8;
+ * d [OUT, ceil(IN/256)] fp16 bits.  Replaces rwkvqDequantSym and its
+ * off-superblock chain rwkvqDequantSymReference (RwkvqDequant.swift:409-466). */
+rwkv_status rwkv_sym_dequant(const uint8_t* qblk, const uint8_t* qs, const uint16_t* d,
+                             void* out, rwkv_dtype out_dt, int64_t OUT, int64_t IN, int bits,
+                             void* stream);
+
+/* rwkvqSb6GEMVApplies (Sources/RWKVQuant/RwkvqSb6GEMV.swift:159-164), same table. */
+int rwkv_sb6_gemv_applies(int64_t OUT, int64_t IN, int xbits, int super_block, int64_t rows);
+
+/* y[N, OUT] = x[N, IN] · Wᵀ straight from the K3 bytes, fp32.  N >= 1 rows
+ * share one pass over the weights (the reference launches one row at a time);
+ * xbsum is computed inside.  Replaces rwkvqSb6GEMV (RwkvqSb6GEMV.swift:170-190). */
+rwkv_status rwkv_sb6_gemv(const float* x, int64_t N,
+                          const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
+                          float* y, int64_t OUT, int64_t IN, int xbits, void* stream);
+
+/* rwkvqSymGEMVApplies (Sources/RWKVQuant/RwkvqSymGEMV.swift:213-218), same table. */
+int rwkv_sym_gemv_applies(int64_t OUT, int64_t IN, int bits, int64_t rows);
+
+/* sym GEMV.  out_per == OUT: y[N, OUT] = x[N, IN]·Wᵀ (rwkvqSymGEMV, :223-247).
+ * out_per < OUT: K = OUT/out_per row-concatenated matrices; row `o` of input
+ * row n uses x[n·K + o/out_per] (symGEMVFused, :343-358).  x holds N·K rows. */
+rwkv_status rwkv_sym_gemv(const float* x, int64_t N,
+                          const uint8_t* qblk, const uint8_t* qs, const uint16_t* d,
+                          float* y, int64_t OUT, int64_t IN, int bits, int64_t out_per,
+                          void* stream);
+
+/* ───────────────────────────── host-side format work (CPU) ───────────────────────────── */
+
+/* rwkvqUnpack6x8 (Sources/RWKVQuant/RwkvqFile.swift:171-181): n_groups × 6 bytes
+ * → n_groups × 8 values in 0..63, LSB-first. */
+rwkv_status rwkv_unpack6x8(const uint8_t* in, int64_t n_groups, int32_t* out);
+
+/* rwkvqSb6ToK3 (RwkvqFile.swift:189-212).  Disk buffers: codes_packed
+ * [OUT, IN/32·16], qh / qh2 [OUT, IN/32·4] (NULL when absent), gw_qsqm
+ * [OUT, IN/256, 12], gw_d / gw_dm [OUT, IN/256] fp16 bits.  Writes the K3
+ * qblk / qsqm / ddm described at rwkv_sb6_dequant.  Pure byte permutation. */
+rwkv_status rwkv_sb6_to_k3(const uint8_t* codes_packed, const uint8_t* qh, const uint8_t* qh2,
+                           const uint8_t* gw_qsqm, const uint16_t* gw_d, const uint16_t* gw_dm,
+                           int64_t OUT, int64_t IN, uint8_t* qblk, uint8_t* qsqm, uint16_t* ddm);
+
+/* sym 6-bit interleave (RwkvqFile.swift:437-449): per 32-column pair
+ * codes_packed[16] ‖ qh[4] ‖ qh2[4]. */
+rwkv_status rwkv_sym_interleave(const uint8_t* codes_packed, const uint8_t* qh, const uint8_t* qh2,
+                                int64_t OUT, int64_t IN, uint8_t* qblk);
+
+/* Encoders.  NOT in the reference (its files come from the external
+ * rwkv-quant project); min/max per block + 6-bit super-block scales, see
+ * swiftrwkv_amd/csrc/host.cpp.  Outputs are the DISK layout above. */
+rwkv_status rwkvq_encode_sb6(const float* w, int64_t OUT, int64_t IN, int bits,
+                             uint8_t* codes_packed, uint8_t* qh, uint8_t* qh2,
+                             uint8_t* gw_qsqm, uint16_t* gw_d, uint16_t* gw_dm, int nthreads);
+rwkv_status rwkvq_encode_sym(const float* w, int64_t OUT, int64_t IN, int bits,
+                             uint8_t* codes, uint8_t* codes_packed, uint8_t* qh, uint8_t* qh2,
+                             uint8_t* gw_qs, uint16_t* gw_d, int nthreads);
+
+/* Read-only memory-mapped safetensors container (RwkvqContainer,
+ * RwkvqFile.swift:31-162): rejects torch zip/pickle files, header lengths
+ * outside the file, unknown dtypes and data offsets that disagree with
+ * shape × dtype. */
+typedef struct rwkvq_file rwkvq_file;
+rwkv_status rwkvq_open(const char* path, rwkvq_file** out);
+void rwkvq_close(rwkvq_file* f);
+int64_t rwkvq_count(const rwkvq_file* f);
+/* Entry `i` in name order.  dtype is the safetensors name ("U8", "F16" ...). */
+rwkv_status rwkvq_entry(const rwkvq_file* f, int64_t i, const char** name, const char** dtype,
+                        int* ndim, const int64_t** shape, const void** data, int64_t* nbytes);
+/* "__metadata__" string value for `key`, or NULL. */
+const char* rwkvq_metadata(const rwkvq_file* f, const char* key);
+
+/* ───────────────────────────── counters ───────────────────────────── */
+
+typedef struct {
+    int64_t seq_fwd;        /* wkv7SequenceLaunches (WKV7.swift:181) */
+    int64_t chunk_fwd;
+    int64_t train_fwd;      /* wkv7TrainForwardLaunches (WKV7Train.swift:358) */
+    int64_t train_bwd;
+    int64_t step;           /* stepKernelCalls (X070Backbone.swift) */
+    int64_t tail;
+    int64_t sb6_dequant;
+    int64_t sym_dequant;
+    int64_t sb6_gemv;       /* rwkvqSb6GEMVCalls */
+    int64_t sym_gemv;       /* rwkvqSymGEMVCalls */
+    int64_t sym_fused;      /* rwkvqSymFusedCalls */
+} rwkv_counters;
+
+void rwkv_get_counters(rwkv_counters* out);
+void rwkv_reset_counters(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RWKV_HIP_H */

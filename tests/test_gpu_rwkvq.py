@@ -1,0 +1,241 @@
+"""GPU parity of the .rwkvq dequant and GEMV kernels.
+
+Dequant: bit-exact against the oracle (pure functions of bytes), all layouts
+and storage types (RwkvqFileTests, RwkvqDTypeTests).  GEMV: ≤ 2e-5 relative
+to an fp64 matmul with the dequantised weights (the reference's own bound,
+RwkvqSb6GEMVTests.swift:53-77), bit-exact on one-hot inputs, fused ==
+separate bitwise (RwkvqSymGEMVTests.swift:164-201).
+"""
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from swiftrwkv_amd import quant as Q
+from tests.test_oracle import GOLD, make_sb6, make_sym
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GEMV_TOL = 2e-5
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def rel(ref, got):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(ref - np.asarray(got, np.float64)).max() / (np.abs(ref).max() + 1e-30))
+
+
+def sb6_tensor(orc, OUT, IN, xbits, seed, degenerate=False):
+    rng = np.random.default_rng(seed)
+    t = make_sb6(OUT, IN, xbits, rng, degenerate)
+    qblk, qsqm, ddm, xb = orc.sb6_to_k3(t["cp"], t["qh"], t["qh2"], t["qsqm_disk"], t["d"].view(np.uint16),
+                                        t["dm"].view(np.uint16), OUT, IN)
+    return qblk, qsqm, ddm.view(np.float16)
+
+
+def sym_tensor(orc, OUT, IN, bits, seed):
+    rng = np.random.default_rng(seed)
+    t = make_sym(OUT, IN, bits, rng)
+    qblk = t["qblk"] if bits == 8 else orc.sym_interleave(t["cp"], t["qh"], t["qh2"], OUT, IN)
+    return qblk, t["qs"].view(np.uint8), t["d"]
+
+
+DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def as_bits(t: torch.Tensor):
+    if t.dtype == torch.float32:
+        return t.cpu().numpy()
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("xbits", [0, 1, 2])
+def test_sb6_dequant_bit_exact(orc, xbits):
+    OUT, IN = 48, 768
+    case(f"sb6 dequant xbits={xbits}")
+    qblk, qsqm, ddm = sb6_tensor(orc, OUT, IN, xbits, seed=xbits, degenerate=True)
+    for name, dt in DT.items():
+        got = Q.rwkvq_dequant_dense(dev(qblk), dev(qsqm), dev(ddm), OUT, IN, 8, xbits, dt)
+        want = orc.sb6_dequant(qblk, qsqm, ddm.view(np.uint16), OUT, IN, xbits, name)
+        assert got.dtype == dt and np.array_equal(as_bits(got).view(want.dtype), want), name
+
+
+@pytest.mark.parametrize("bits", [8, 6])
+def test_sym_dequant_bit_exact(orc, bits):
+    OUT, IN = 40, 1024
+    case(f"sym dequant bits={bits}")
+    qblk, qs, d = sym_tensor(orc, OUT, IN, bits, seed=bits)
+    for name, dt in DT.items():
+        got = Q.rwkvq_dequant_sym(dev(qblk), dev(qs), dev(d), OUT, IN, bits, dt)
+        want = orc.sym_dequant(qblk, qs, d.view(np.uint16), OUT, IN, bits, name)
+        assert np.array_equal(as_bits(got).view(want.dtype), want), name
+
+
+def test_sym_off_superblock_known_answer():
+    case("sym KAT IN=48 (RwkvqFileTests.swift:237-256)")
+    kat = json.load(open(os.path.join(GOLD, "sym8_kat.json")))
+    got = Q.rwkvq_dequant_sym(dev(np.array(kat["codes_u8"], np.uint8).reshape(2, 48)),
+                              dev(np.array(kat["qs_u8"], np.uint8).reshape(2, 3)),
+                              dev(np.array(kat["d_f16_bits"], np.uint16).view(np.float16).reshape(2, 1)),
+                              2, 48, 8, torch.float32)
+    assert np.array_equal(got.cpu().numpy().reshape(-1), np.array(kat["expected_f32"], np.float32))
+
+
+GEMV_SHAPES = [(768, 768), (3072, 768), (768, 3072), (2048, 2048), (24, 256)]
+
+
+@pytest.mark.parametrize("xbits", [0, 1, 2])
+@pytest.mark.parametrize("OUT,IN", GEMV_SHAPES)
+def test_sb6_gemv_matches_fp64(orc, xbits, OUT, IN):
+    case(f"sb6 gemv {OUT}x{IN} xbits={xbits}")
+    qblk, qsqm, ddm = sb6_tensor(orc, OUT, IN, xbits, seed=OUT + IN + xbits)
+    rng = np.random.default_rng(17)
+    for N in (1, 3, 6):
+        x = rng.standard_normal((N, IN)).astype(np.float32)
+        y = Q.rwkvq_sb6_gemv(dev(x), dev(qblk), dev(qsqm), dev(ddm), OUT, IN, xbits)
+        want = orc.sb6_gemv_f64(x, qblk, qsqm, ddm.view(np.uint16), OUT, IN, xbits)
+        assert y.shape == (N, OUT)
+        assert rel(want, y.cpu().numpy()) < GEMV_TOL, N
+
+
+def test_sb6_gemv_head_shape(orc):
+    OUT, IN = 65536, 768
+    case("sb6 gemv head 65536x768")
+    qblk, qsqm, ddm = sb6_tensor(orc, OUT, IN, 0, seed=99)
+    x = np.random.default_rng(1).standard_normal((1, IN)).astype(np.float32)
+    y = Q.rwkvq_sb6_gemv(dev(x), dev(qblk), dev(qsqm), dev(ddm), OUT, IN, 0)
+    want = orc.sb6_gemv_f64(x, qblk, qsqm, ddm.view(np.uint16), OUT, IN, 0)
+    assert rel(want, y.cpu().numpy()) < GEMV_TOL
+
+
+def test_gemv_one_hot_is_bit_exact_dequant_column(orc):
+    case("one-hot GEMV == dequant column")
+    OUT, IN = 512, 768
+    qblk, qsqm, ddm = sb6_tensor(orc, OUT, IN, 2, seed=5, degenerate=True)
+    W = orc.sb6_dequant(qblk, qsqm, ddm.view(np.uint16), OUT, IN, 2)
+    cols = [0, 31, 32, 400, 767]
+    x = np.zeros((len(cols), IN), np.float32)
+    x[np.arange(len(cols)), cols] = 1.0
+    y = Q.rwkvq_sb6_gemv(dev(x), dev(qblk), dev(qsqm), dev(ddm), OUT, IN, 2).cpu().numpy()
+    assert np.array_equal(y, W[:, cols].T)
+    for bits in (8, 6):
+        sq, qs, d = sym_tensor(orc, OUT, IN, bits, seed=bits)
+        Ws = orc.sym_dequant(sq, qs, d.view(np.uint16), OUT, IN, bits)
+        ys = Q.rwkvq_sym_gemv(dev(x), dev(sq), dev(qs), dev(d), OUT, IN, bits).cpu().numpy()
+        assert np.array_equal(ys, Ws[:, cols].T), bits
+    # zero input → exact zeros; linearity
+    z = Q.rwkvq_sb6_gemv(dev(np.zeros((1, IN), np.float32)), dev(qblk), dev(qsqm), dev(ddm), OUT, IN, 2)
+    assert z.abs().max().item() == 0.0
+
+
+@pytest.mark.parametrize("bits", [8, 6])
+@pytest.mark.parametrize("OUT,IN", [(768, 768), (3072, 768), (768, 3072), (16, 256)])
+def test_sym_gemv_matches_fp64(orc, bits, OUT, IN):
+    case(f"sym gemv {OUT}x{IN} bits={bits}")
+    qblk, qs, d = sym_tensor(orc, OUT, IN, bits, seed=OUT + bits)
+    rng = np.random.default_rng(7)
+    for N in (1, 2, 4, 5):
+        x = rng.standard_normal((N, IN)).astype(np.float32)
+        y = Q.rwkvq_sym_gemv(dev(x), dev(qblk), dev(qs), dev(d), OUT, IN, bits)
+        want = orc.sym_gemv_f64(x, qblk, qs, d.view(np.uint16), OUT, IN, bits)
+        assert rel(want, y.cpu().numpy()) < GEMV_TOL, N
+
+
+@pytest.mark.parametrize("bits", [8, 6])
+def test_fused_sym_gemv_equals_separate_bitwise(orc, bits):
+    case(f"fused r/k/v bits={bits}")
+    OUT, IN, Kn = 768, 768, 3
+    parts = [sym_tensor(orc, OUT, IN, bits, seed=bits * 10 + i) for i in range(Kn)]
+    qblk = np.concatenate([p[0] for p in parts])
+    qs = np.concatenate([p[1] for p in parts])
+    d = np.concatenate([p[2] for p in parts])
+    x = np.random.default_rng(21).standard_normal((Kn, IN)).astype(np.float32)
+    fused = Q.rwkvq_sym_gemv(dev(x), dev(qblk), dev(qs), dev(d), OUT * Kn, IN, bits, out_per=OUT)
+    assert fused.shape == (1, OUT * Kn)
+    for i, p in enumerate(parts):
+        alone = Q.rwkvq_sym_gemv(dev(x[i:i + 1]), *[dev(z) for z in p], OUT, IN, bits)
+        assert torch.equal(fused[:, i * OUT:(i + 1) * OUT], alone)
+    want = orc.sym_gemv_f64(x, qblk, qs, d.view(np.uint16), OUT * Kn, IN, bits, out_per=OUT)
+    assert rel(want, fused.cpu().numpy()) < GEMV_TOL
+
+
+def test_gemv_is_deterministic(orc):
+    case("gemv determinism")
+    qblk, qsqm, ddm = sb6_tensor(orc, 3072, 768, 1, seed=3)
+    x = dev(np.random.default_rng(0).standard_normal((2, 768)).astype(np.float32))
+    a = Q.rwkvq_sb6_gemv(x, dev(qblk), dev(qsqm), dev(ddm), 3072, 768, 1)
+    b = Q.rwkvq_sb6_gemv(x, dev(qblk), dev(qsqm), dev(ddm), 3072, 768, 1)
+    assert torch.equal(a, b)
+    # a row of a batch equals the same row alone
+    c = Q.rwkvq_sb6_gemv(x[1:2], dev(qblk), dev(qsqm), dev(ddm), 3072, 768, 1)
+    assert torch.equal(a[1:2], c)
+
+
+# ───────────────────────────── sidecar end to end ─────────────────────────────
+
+def synth_file(path, kind, bits):
+    rng = np.random.default_rng(42)
+    tensors = {}
+    for l in range(2):
+        for m in ("receptance", "key", "value", "output"):
+            w = (rng.standard_normal((256, 256)) * 0.02).astype(np.float32)
+            tensors[f"blocks.{l}.att.{m}.weight"] = Q.sb6_entry(w, bits) if kind == "sb6" else Q.sym_entry(w, bits)
+        w = (rng.standard_normal((1024, 256)) * 0.02).astype(np.float32)
+        tensors[f"blocks.{l}.ffn.key.weight"] = Q.sb6_entry(w, bits) if kind == "sb6" else Q.sym_entry(w, bits)
+    ln = (rng.standard_normal(256)).astype(np.float32)
+    tensors["ln_out.weight"] = ({"kind": "dense", "shape": [256]}, {"dense": ln})
+    Q.write_rwkvq(path, tensors, n_layer=2, n_embd=256, vocab_size=1024)
+    return tensors
+
+
+@pytest.mark.parametrize("kind,bits", [("sb6", 4), ("sb6", 6), ("sym", 8), ("sym", 6)])
+def test_sidecar_end_to_end(tmp_path, orc, kind, bits):
+    case(f"sidecar {kind}{bits}")
+    p = str(tmp_path / f"{kind}{bits}.rwkvq")
+    synth_file(p, kind, bits)
+    groups = {"att0": [f"blocks.0.att.{m}.weight" for m in ("receptance", "key", "value")]}
+    sc = Q.RwkvqSidecar.from_rwkvq(p, fusing_sym=groups)
+    key = "blocks.1.att.key.weight"
+    info = sc.tensors[key]
+    deq = sc.dequantize(key)
+    if kind == "sb6":
+        want = orc.sb6_dequant(*[sc.arrays[f"{key}::{f}"].cpu().numpy() for f in ("qblk", "qsqm")],
+                               sc.arrays[f"{key}::ddm"].view(torch.int16).cpu().numpy().view(np.uint16),
+                               256, 256, info.xbits)
+    else:
+        want = orc.sym_dequant(sc.arrays[f"{key}::qblk"].cpu().numpy(), sc.arrays[f"{key}::qs"].cpu().numpy(),
+                               sc.arrays[f"{key}::d"].view(torch.int16).cpu().numpy().view(np.uint16), 256, 256, bits)
+    assert np.array_equal(deq.cpu().numpy(), want)
+    assert torch.equal(sc.dequantize(key, torch.bfloat16), deq.to(torch.bfloat16))
+    x = torch.randn((1, 256), device=DEV, generator=torch.Generator(DEV).manual_seed(0))
+    y = sc.sb6_gemv(key, x) if kind == "sb6" else sc.sym_gemv(key, x)
+    assert y is not None
+    assert rel((x.double() @ deq.double().T).cpu().numpy(), y.cpu().numpy()) < GEMV_TOL
+    # declines what it cannot take (RwkvqSb6GEMVTests.swift:88-100)
+    other = sc.sym_gemv if kind == "sb6" else sc.sb6_gemv
+    assert other(key, x) is None
+    assert (sc.sb6_gemv if kind == "sb6" else sc.sym_gemv)(key, torch.zeros((1, 128), device=DEV)) is None
+    if kind == "sb6":
+        assert sc.sb6_gemv(key, torch.zeros((2, 256), device=DEV)) is None
+        assert not sc.sym_fused
+    else:
+        assert sc.sym_gemv(key, torch.zeros((5, 256), device=DEV)) is None
+        assert set(sc.sym_fused) == {"att0"}
+        xs = torch.randn((3, 256), device=DEV)
+        fused = sc.sym_gemv_fused("att0", xs)
+        for i, k in enumerate(groups["att0"]):
+            assert torch.equal(fused[i:i + 1], sc.sym_gemv(k, xs[i:i + 1]))
+        assert sc.sym_gemv_fused("att0", torch.zeros((2, 256), device=DEV)) is None
+        assert sc.sym_gemv_fused("none", xs) is None
+    assert torch.equal(sc.dequantize("ln_out.weight"), sc.arrays["ln_out.weight::dense"].float())

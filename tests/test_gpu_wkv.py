@@ -1,0 +1,352 @@
+"""GPU parity of the WKV-7 kernels against the oracle and the reference's own
+bitwise invariants (WKV7SequenceTests, WKV7StateTests, WKV7TrainKernelTests,
+WKV7KernelParityTests, DecodeKernelTests).  Tolerance: max|got−ref| / max|ref|
+≤ 1e-5 in fp32 against the fp64 oracle; ≤ 1e-2 when gradients are stored in
+bf16."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from swiftrwkv_amd import _lib, kernel as K
+from swiftrwkv_amd import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-5
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(x, dt=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV).to(dt)
+
+
+def host(t):
+    return t.detach().float().cpu().numpy()
+
+
+def rel(ref, got):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(ref - np.asarray(got, np.float64)).max() / (np.abs(ref).max() + 1e-30))
+
+
+def same(a, b):
+    return torch.equal(a, b)
+
+
+# ───────────────────────────── forward ─────────────────────────────
+
+def test_seq_fwd_config0_matches_oracle(orc):
+    case("seq fwd B1 T1024 H12 config-0 inputs, fp32")
+    x = syn.wkv_inputs_config0(1, 1024, 12, seed=0)
+    out, h = K.wkv7_sequence_forward(*[dev(z) for z in x])
+    torch.cuda.synchronize()
+    o64, h64 = orc.wkv7_fwd_f64(*x)
+    ro, rh = rel(o64, host(out)), rel(h64, host(h))
+    print(f"config0 rel out {ro:.2e} state {rh:.2e}")
+    assert ro < TOL and rh < TOL
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_seq_fwd_half_inputs_widened_exactly(orc, dt):
+    case(f"seq fwd half inputs {dt}")
+    x = syn.wkv_inputs_train(2, 40, 3, seed=1)
+    xd = [dev(z, dt) for z in x]
+    h0 = syn.state(2, 3)
+    out, h = K.wkv7_sequence_forward(*xd, h_in=dev(h0))
+    # the kernel widens in registers: identical to widening first
+    out32, h32 = K.wkv7_sequence_forward(*[z.float() for z in xd], h_in=dev(h0))
+    assert same(out, out32) and same(h, h32)
+    o64, h64 = orc.wkv7_fwd_f64(*[host(z) for z in xd], h_in=h0)
+    assert rel(o64, host(out)) < TOL and rel(h64, host(h)) < TOL
+
+
+SHAPES = [(1, 1, 2), (1, 5, 3), (1, 16, 2), (1, 17, 4), (2, 53, 3), (1, 512, 12), (3, 32, 1)]
+
+
+@pytest.mark.parametrize("B,T,H", SHAPES)
+def test_whole_sequence_equals_chunked_bitwise(orc, B, T, H):
+    case(f"whole vs chunked B{B} T{T} H{H}")
+    x = [dev(z) for z in syn.wkv_inputs_seq(B, T, H, seed=1000 + T)]
+    h0 = dev(syn.state(B, H, seed=T))
+    for h_in in (None, h0):
+        o1, s1 = K.wkv7_sequence_forward(*x, h_in=h_in)
+        o2, s2 = K.wkv7_forward_chunked(*x, h_in=h_in)
+        assert same(o1, o2) and same(s1, s2)
+        assert o1.abs().sum() > 0 and not torch.isnan(o1).any()
+        assert o1[B - 1, T - 1].abs().sum() > 0
+        o64, s64 = orc.wkv7_fwd_f64(*[host(z) for z in x], h_in=None if h_in is None else host(h_in))
+        assert rel(o64, host(o1)) < TOL and rel(s64, host(s1)) < TOL
+
+
+def test_state_carries_across_calls_bitwise():
+    case("split == contiguous")
+    x = [dev(z) for z in syn.wkv_inputs_train(2, 64, 4, seed=0)]
+    full, hfull = K.wkv7_forward_with_state(*x)
+    for cuts in ([32], [20], [5], [16, 48], [19, 41]):
+        parts, h, prev = [], None, 0
+        for c in cuts + [64]:
+            o, h = K.wkv7_forward_with_state(*[z[:, prev:c] for z in x], h_in=h)
+            parts.append(o)
+            prev = c
+        assert same(torch.cat(parts, 1), full) and same(h, hfull), cuts
+    # and the state is really used
+    o_with, _ = K.wkv7_sequence_forward(*[z[:, 19:] for z in x],
+                                        h_in=K.wkv7_sequence_forward(*[z[:, :19] for z in x])[1])
+    o_without, _ = K.wkv7_sequence_forward(*[z[:, 19:] for z in x])
+    assert not same(o_with, o_without)
+
+
+def test_switch_and_launch_counter():
+    case("switch selects the path")
+    x = [dev(z) for z in syn.wkv_inputs_seq(1, 40, 2, seed=3)]
+    before = K.wkv7_sequence_launches()
+    a, ha = K.wkv7_forward_with_state(*x)
+    assert K.wkv7_sequence_launches() - before == 1
+    K.wkv7_whole_sequence_forward = False
+    try:
+        before = K.wkv7_sequence_launches()
+        b, hb = K.wkv7_forward_with_state(*x)
+        assert K.wkv7_sequence_launches() == before
+    finally:
+        K.wkv7_whole_sequence_forward = True
+    assert same(a, b) and same(ha, hb)
+
+
+def test_train_forward_equals_frozen_bitwise(orc):
+    case("train fwd == frozen fwd, checkpoints, sa")
+    xn = syn.wkv_inputs_train(2, 64, 4, seed=0)
+    h0n = syn.state(2, 4)
+    x = [dev(z) for z in xn]
+    h0 = dev(h0n)
+    oF, hF = K.wkv7_forward_with_state(*x, h_in=h0)
+    oT, hT = K.wkv7_train_with_state(*x, h_in=h0)
+    assert same(oF, oT) and same(hF, hT)
+    ins, dt = K._prep(x)
+    out, h_out, sa, ck = K._train_forward(ins, dt, h0)
+    assert same(out, oF)
+    _, _, sa_o, ck_o = orc.wkv7_fwd_f32(*xn, h_in=h0n, want_sa=True, want_ckpt=True)
+    o64, h64, sa64 = orc.wkv7_fwd_f64(*xn, h_in=h0n, want_sa=True)
+    assert rel(sa64, host(sa)) < TOL
+    assert rel(ck_o, host(ck)) < TOL
+    assert same(ck[:, :, -1], hT)
+    assert rel(o64, host(oT)) < TOL
+
+
+def test_chunk_forward_contract():
+    case("chunk forward T == 16")
+    x = [dev(z) for z in syn.wkv_inputs_train(1, 16, 3, seed=2)]
+    h0 = torch.zeros((1, 3, 64, 64), device=DEV)
+    o, h, sa = K.wkv7_chunk_forward(*x, h0)
+    o2, h2 = K.wkv7_sequence_forward(*x)
+    assert same(o, o2) and same(h, h2) and sa.shape == o.shape
+    with pytest.raises(ValueError):
+        K.wkv7_chunk_forward(*[z[:, :15] for z in x], h0)
+
+
+# ───────────────────────────── decode step ─────────────────────────────
+
+def decode_inputs(H, seed):
+    rng = np.random.default_rng(seed)
+    n = lambda s: (rng.standard_normal((H, 64)) * s).astype(np.float32)
+    r, k, v, a, b = n(0.5), n(0.5), n(0.5), n(0.1), n(0.1)
+    w = np.exp(-0.606531 / (1 + np.exp(-n(1.0)))).astype(np.float32)
+    h = (rng.standard_normal((H, 64, 64)) * 0.3).astype(np.float32)
+    return [r, w, k, v, a, b], h
+
+
+@pytest.mark.parametrize("H,seed", [(12, 1), (3, 2), (32, 3)])
+def test_step_equals_sequence_kernel_on_one_token(H, seed):
+    case(f"step == seq at T=1, H={H}")
+    xn, hn = decode_inputs(H, seed)
+    x = [dev(z) for z in xn]
+    out, h_new = K.wkv7_step_forward(*x, dev(hn))
+    ref_o, ref_h = K.wkv7_forward_with_state(*[z.reshape(1, 1, H, 64) for z in x], h_in=dev(hn).reshape(1, H, 64, 64))
+    assert out.shape == (H, 64) and h_new.shape == (H, 64, 64)
+    assert same(out, ref_o.reshape(H, 64)) and same(h_new, ref_h.reshape(H, 64, 64))
+    assert out.abs().max() > 0
+
+
+def test_step_input_types_and_in_place():
+    case("step dtype invariance, in-place")
+    xn, hn = decode_inputs(12, 5)
+    outs = {}
+    for dt in (torch.bfloat16, torch.float32, torch.float16):
+        xs = [dev(z, dt) for z in xn]
+        outs[dt] = K.wkv7_step_forward(*xs, dev(hn))[0]
+        assert same(outs[dt], K.wkv7_step_forward(*[z.float() for z in xs], dev(hn))[0])
+    # batched, in place
+    B = 5
+    xb = [dev(np.stack([z] * B)) for z in xn]
+    hb = dev(np.stack([hn] * B))
+    ref_o, ref_h = K.wkv7_step_forward(*xb, hb.clone())
+    o = K.wkv7_step_(*xb, hb)
+    assert same(o, ref_o) and same(hb, ref_h)
+    assert same(o[3], K.wkv7_step_forward(*[z[3] for z in xb], dev(hn))[0])
+
+
+def test_tail_matches_oracle(orc):
+    rng = np.random.default_rng(7)
+    for H, N in ((12, 1), (32, 1), (12, 37)):
+        case(f"tail H={H} N={N}")
+        S, D = 64, H * 64
+        wkv = (rng.standard_normal((N, H, S)) * 3).astype(np.float32)
+        r, k, v = (rng.standard_normal((N, H, S)).astype(np.float32) for _ in range(3))
+        rk = (rng.standard_normal((H, S)) * 0.1).astype(np.float32)
+        lnw = (rng.standard_normal(D) * 0.5 + 1).astype(np.float32)
+        lnb = (rng.standard_normal(D) * 0.1).astype(np.float32)
+        g = rng.standard_normal((N, D)).astype(np.float32)
+        got = K.wkv_tail(dev(wkv), dev(r), dev(k), dev(v), dev(rk), dev(lnw), dev(lnb), dev(g), H, S, rows=N)
+        want = orc.wkv_tail_f64(wkv, r, k, v, rk, lnw, lnb, g, N, H, S)
+        assert got.shape == (N, D)
+        assert rel(want, host(got)) < TOL
+    with pytest.raises(ValueError):
+        K.wkv_tail(dev(wkv), dev(r), dev(k), dev(v), dev(rk), dev(lnw), dev(lnb), dev(g), H, 48, rows=N)
+
+
+# ───────────────────────────── backward ─────────────────────────────
+
+def train_case(B=2, T=48, H=3, seed=0):
+    x = syn.wkv_inputs_train(B, T, H, seed=seed)
+    h0 = syn.state(B, H, scale=0.1, seed=seed + 100)
+    rng = np.random.default_rng(seed + 200)
+    g = rng.standard_normal((B, T, H, 64)).astype(np.float32)
+    gh = (rng.standard_normal((B, H, 64, 64)) * 0.3).astype(np.float32)
+    return x, h0, g, gh
+
+
+def kernel_grads(x, h0, g, gh, v2=True, keep=True, dt=torch.float32):
+    K.wkv7_backward_v2, K.wkv7_keep_forward_outputs = v2, keep
+    try:
+        ins = [dev(z, dt).requires_grad_(True) for z in x]
+        hin = dev(h0).requires_grad_(True)
+        o, h = K.wkv7_train_with_state(*ins, h_in=hin)
+        loss = (o * dev(g)).sum() + (h * dev(gh)).sum()
+        loss.backward()
+        return [z.grad for z in ins] + [hin.grad]
+    finally:
+        K.wkv7_backward_v2, K.wkv7_keep_forward_outputs = True, True
+
+
+NAMES = ["dr", "dw", "dk", "dv", "da", "db", "dh_in"]
+
+
+@pytest.mark.parametrize("v2", [True, False])
+def test_backward_matches_fp64_oracle(orc, v2):
+    case(f"backward v{2 if v2 else 1} vs fp64 oracle B2 T48 H3")
+    x, h0, g, gh = train_case()
+    got = kernel_grads(x, h0, g, gh, v2=v2)
+    want = orc.wkv7_bwd_f64(*x, h0, g, gh)
+    errs = [rel(w_, host(g_)) for w_, g_ in zip(want, got)]
+    print("bwd v%d rel: %s" % (2 if v2 else 1, ", ".join(f"{n} {e:.1e}" for n, e in zip(NAMES, errs))))
+    for n, e, g_ in zip(NAMES, errs, got):
+        assert e < TOL, n
+        assert g_.abs().max() > 0, n
+
+
+def test_backward_config0_distribution(orc):
+    case("backward config-0 inputs B1 T128 H2")
+    x = syn.wkv_inputs_config0(1, 128, 2, seed=4)
+    rng = np.random.default_rng(4)
+    g = rng.standard_normal((1, 128, 2, 64)).astype(np.float32)
+    got = kernel_grads(x, np.zeros((1, 2, 64, 64), np.float32), g, np.zeros((1, 2, 64, 64), np.float32))
+    want = orc.wkv7_bwd_f64(*x, None, g, None)
+    errs = [rel(w_, host(g_)) for w_, g_ in zip(want, got)]
+    print("bwd config0 rel: " + ", ".join(f"{n} {e:.1e}" for n, e in zip(NAMES, errs)))
+    assert max(errs) < TOL
+
+
+def test_backward_is_deterministic_and_variants_differ():
+    case("backward determinism, v1 vs v2")
+    x, h0, g, gh = train_case(seed=3)
+    a = kernel_grads(x, h0, g, gh)
+    b = kernel_grads(x, h0, g, gh)
+    assert all(same(p, q) for p, q in zip(a, b))
+    old = kernel_grads(x, h0, g, gh, v2=False)
+    for n, p, q in zip(NAMES, old, a):
+        assert rel(host(q), host(p)) < 1e-4, n
+    assert sum(int((p != q).sum()) for p, q in zip(old, a)) > 0
+
+
+@pytest.mark.parametrize("v2", [True, False])
+def test_keep_equals_recompute_and_launch_counts(v2):
+    case(f"keep vs recompute v{2 if v2 else 1}")
+    x, h0, g, gh = train_case(seed=5)
+    n = K.wkv7_train_forward_launches()
+    kept = kernel_grads(x, h0, g, gh, v2=v2, keep=True)
+    assert K.wkv7_train_forward_launches() - n == 1
+    n = K.wkv7_train_forward_launches()
+    rec = kernel_grads(x, h0, g, gh, v2=v2, keep=False)
+    assert K.wkv7_train_forward_launches() - n == 2
+    assert all(same(p, q) for p, q in zip(kept, rec))
+
+
+def test_dr_through_final_state_only_is_zero():
+    case("dr through h_out only")
+    x, _, _, gh = train_case(T=32, seed=6)
+    r = dev(x[0]).requires_grad_(True)
+    k = dev(x[2]).requires_grad_(True)
+    _, h = K.wkv7_train_with_state(r, dev(x[1]), k, dev(x[3]), dev(x[4]), dev(x[5]))
+    (h * dev(gh)).sum().backward()
+    assert r.grad.abs().max().item() == 0.0
+    assert k.grad.abs().max().item() > 0.0
+
+
+def test_gradient_reaches_a_parameter_above_the_kernel():
+    case("chain rule through a scale on r")
+    x, h0, g, gh = train_case(seed=13)
+    dr = kernel_grads(x, h0, g, gh)[0]
+    for keep in (True, False):
+        K.wkv7_keep_forward_outputs = keep
+        try:
+            p = torch.ones((), device=DEV, requires_grad=True)
+            o, h = K.wkv7_train_with_state(dev(x[0]) * p, *[dev(z) for z in x[1:]], h_in=dev(h0))
+            ((o * dev(g)).sum() + (h * dev(gh)).sum()).backward()
+        finally:
+            K.wkv7_keep_forward_outputs = True
+        want = (dr * dev(x[0])).sum().item()
+        assert abs(p.grad.item() - want) <= abs(want) * 1e-4 + 1e-4
+
+
+def test_bf16_training_within_tolerance(orc):
+    case("bf16 inputs and gradients")
+    x, h0, g, gh = train_case(seed=8)
+    xb = [host(dev(z, torch.bfloat16)) for z in x]
+    got = kernel_grads(xb, h0, g, gh, dt=torch.bfloat16)
+    assert all(t.dtype == torch.bfloat16 for t in got[:6]) and got[6].dtype == torch.float32
+    want = orc.wkv7_bwd_f64(*xb, h0, g, gh)
+    for n, w_, g_ in zip(NAMES, want, got):
+        assert rel(w_, host(g_)) < 1e-2, n
+
+
+def test_steps_are_differentiable_at_any_length(orc):
+    case("wkv7_steps T=5 gradients (padded to CHUNK)")
+    x, h0, g, gh = train_case(B=1, T=5, H=2, seed=9)
+    ins = [dev(z).requires_grad_(True) for z in x]
+    hin = dev(h0).requires_grad_(True)
+    o, h = K.wkv7_steps(*ins, h_in=hin)
+    ((o * dev(g)).sum() + (h * dev(gh)).sum()).backward()
+    want = orc.wkv7_bwd_f64(*x, h0, g, gh)
+    for n, w_, t in zip(NAMES, want, ins + [hin]):
+        assert rel(w_, host(t.grad)) < TOL, n
+    with torch.no_grad():
+        o2, h2 = K.wkv7_steps(*[dev(z) for z in x], h_in=dev(h0))
+    assert same(o2, o.detach()) and same(h2, h.detach())
+
+
+def test_preconditions_raise():
+    case("preconditions")
+    x = [dev(z) for z in syn.wkv_inputs_train(1, 17, 1, seed=0)]
+    with pytest.raises(ValueError):
+        K.wkv7_train_with_state(*x)
+    y = [torch.zeros((1, 4, 1, 32), device=DEV) for _ in range(6)]
+    with pytest.raises(ValueError):
+        K.wkv7_sequence_forward(*y)
+    with pytest.raises(_lib.RwkvHipError):
+        _lib.call("rwkv_wkv7_train_bwd", *[z.data_ptr() for z in x], 0, x[0].data_ptr(), x[0].data_ptr(),
+                  x[0].data_ptr(), None, *[z.data_ptr() for z in x], 0, x[0].data_ptr(), 1, 16, 1, 7, None)

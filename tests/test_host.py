@@ -1,0 +1,252 @@
+"""CPU tests of the product's host side: the C ABI library loads and exports
+every symbol include/rwkv_hip.h declares; the host-side .rwkvq format work
+(unpack6, K3 repack, sym interleave, container, manifest validation,
+encoders) against the oracle; the reference's applicability tables.
+No device computation happens here."""
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from swiftrwkv_amd import _lib, quant
+from tests.test_oracle import make_sb6, make_sym
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "rwkv_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rwkvq?_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    declared = header_symbols()
+    assert len(declared) >= 30
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, missing
+    # and the Python binding knows every one of them
+    assert set(declared) <= set(_lib.exported_symbols()) | {"rwkv_get_counters", "rwkv_reset_counters"}
+    assert lib.rwkv_abi_version() == 1
+    assert lib.rwkv_wkv7_head_size() == 64 and lib.rwkv_wkv7_chunk() == 16
+
+
+def test_status_strings_and_errors():
+    lib = _lib.lib()
+    assert [lib.rwkv_status_string(i).decode() for i in range(8)] == \
+        ["ok", "shape", "dtype", "unsupported", "format", "hip", "null", "io"]
+    # argument validation happens before any device work: a CPU-testable failure path
+    st = lib.rwkv_wkv7_seq_fwd(None, None, None, None, None, None, 0, None, None, None, 1, 1, 1, None)
+    assert st == 6 and b"non-null" in lib.rwkv_last_error()
+    dummy = 8
+    st = lib.rwkv_wkv7_train_fwd(*([dummy] * 6), 0, None, dummy, dummy, dummy, dummy, 1, 17, 1, None)
+    assert st == 1 and b"multiple of CHUNK" in lib.rwkv_last_error()
+    st = lib.rwkv_wkv7_chunk_fwd(*([dummy] * 6), 0, dummy, dummy, dummy, dummy, 1, 15, 1, None)
+    assert st == 1
+    st = lib.rwkv_wkv7_seq_fwd(*([dummy] * 6), 7, None, dummy, dummy, 1, 1, 1, None)
+    assert st == 2
+    st = lib.rwkv_wkv7_train_bwd(*([dummy] * 6), 0, dummy, dummy, dummy, None, *([dummy] * 6), 0, dummy, 1, 16, 1, 3, None)
+    assert st == 3
+    st = lib.rwkv_sb6_gemv(dummy, 1, dummy, dummy, dummy, dummy, 16, 200, 0, None)
+    assert st == 1
+    st = lib.rwkv_sym_gemv(dummy, 1, dummy, dummy, dummy, dummy, 48, 256, 8, 20, None)
+    assert st == 1
+    st = lib.rwkv_wkv_tail(*([dummy] * 9), 1, 12, 48, 64e-5, None)
+    assert st == 1
+
+
+def test_applies_tables_are_the_reference_ones():
+    # RwkvqSb6GEMVTests.swift:80-100
+    assert quant.rwkvq_sb6_gemv_config(65536, 2048, 0) == (4, 4)
+    assert quant.rwkvq_sb6_gemv_config(8192, 2048, 0) == (2, 2)
+    assert quant.rwkvq_sb6_gemv_config(8192, 2048, 1) == (4, 4)
+    assert quant.rwkvq_sb6_gemv_config(2048, 8192, 0) == (4, 4)
+    assert not quant.rwkvq_sb6_gemv_applies(24, 256, 0, 8, 1)
+    assert not quant.rwkvq_sb6_gemv_applies(16, 96, 0, 8, 1)
+    assert not quant.rwkvq_sb6_gemv_applies(16, 256, 0, 4, 1)
+    assert not quant.rwkvq_sb6_gemv_applies(768, 768, 0, 8, 2)
+    assert quant.rwkvq_sb6_gemv_applies(768, 768, 0, 8, 1)
+    assert quant.rwkvq_sb6_gemv_applies(8196, 768, 0, 8, 1)       # (2,2) ⇒ OUT % 4
+    assert not quant.rwkvq_sb6_gemv_applies(8196, 768, 1, 8, 1)   # (4,4) ⇒ OUT % 16
+    # RwkvqSymGEMVTests.swift:75-86
+    assert not quant.rwkvq_sym_gemv_applies(24, 256, 8, 1)
+    assert not quant.rwkvq_sym_gemv_applies(16, 48, 8, 1)
+    assert quant.rwkvq_sym_gemv_applies(16, 256, 6, 4)
+    assert not quant.rwkvq_sym_gemv_applies(16, 256, 6, 5)
+    assert quant.RWKVQ_SYM_GEMV_MAX_ROWS == 4
+    from swiftrwkv_amd import kernel
+    assert kernel.wkv_tail_applies(64) and not kernel.wkv_tail_applies(48)
+
+
+def test_unpack6_product_equals_oracle(orc):
+    rng = np.random.default_rng(0)
+    b = rng.integers(0, 256, (4096, 6), dtype=np.uint8)
+    assert np.array_equal(quant.rwkvq_unpack6x8(b), orc.unpack6x8(b))
+
+
+@pytest.mark.parametrize("xbits", [0, 1, 2])
+def test_sb6_to_k3_product_equals_oracle(orc, xbits):
+    rng = np.random.default_rng(xbits)
+    OUT, IN = 7, 512
+    t = make_sb6(OUT, IN, xbits, rng)
+    got = quant.rwkvq_sb6_to_k3(t["cp"], t["qsqm_disk"], t["d"], t["dm"], t["qh"], t["qh2"], (OUT, IN))
+    want = orc.sb6_to_k3(t["cp"], t["qh"], t["qh2"], t["qsqm_disk"], t["d"].view(np.uint16),
+                         t["dm"].view(np.uint16), OUT, IN)
+    for g, w in zip(got, want):
+        assert np.array_equal(np.asarray(g), np.asarray(w))
+
+
+def test_sym_interleave_product_equals_oracle(orc):
+    rng = np.random.default_rng(5)
+    t = make_sym(9, 768, 6, rng)
+    assert np.array_equal(quant.rwkvq_sym_interleave(t["cp"], t["qh"], t["qh2"], (9, 768)),
+                          orc.sym_interleave(t["cp"], t["qh"], t["qh2"], 9, 768))
+
+
+@pytest.mark.parametrize("bits", [4, 5, 6])
+def test_sb6_encoder_round_trip(orc, bits):
+    """Encoder (parity unpinned: not in the reference) — range and error invariants."""
+    rng = np.random.default_rng(bits)
+    OUT, IN = 32, 768
+    w = (rng.standard_normal((OUT, IN)) * 0.02).astype(np.float32)
+    disk = quant.encode_sb6(w, bits)
+    assert disk["gw_qsqm"].shape == (OUT, IN // 256, 12)
+    qblk, qsqm, ddm, xb = quant.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"], disk["gw_dm"],
+                                                disk.get("gw_qh"), disk.get("gw_qh2"), (OUT, IN))
+    assert xb == bits - 4
+    deq = orc.sb6_dequant(qblk, qsqm, ddm, OUT, IN, xb)
+    step = (w.reshape(OUT, -1, 32).max(-1) - w.reshape(OUT, -1, 32).min(-1)) / ((1 << bits) - 1)
+    err = np.abs(deq - w).reshape(OUT, -1, 32).max(-1)
+    # half a quantisation step plus the 6-bit scale / min rounding
+    assert np.all(err <= 0.5 * step + 0.04 * np.abs(w).reshape(OUT, -1, 32).max(-1) + 1e-6)
+    rel = np.linalg.norm(deq - w) / np.linalg.norm(w)
+    assert rel < {4: 0.12, 5: 0.06, 6: 0.035}[bits]
+
+
+@pytest.mark.parametrize("bits", [8, 6])
+def test_sym_encoder_round_trip(orc, bits):
+    rng = np.random.default_rng(bits)
+    OUT, IN = 16, 512
+    w = (rng.standard_normal((OUT, IN)) * 0.02).astype(np.float32)
+    disk = quant.encode_sym(w, bits)
+    qblk = disk["codes"].view(np.uint8) if bits == 8 else quant.rwkvq_sym_interleave(
+        disk["codes_packed"], disk["gw_qh"], disk["gw_qh2"], (OUT, IN))
+    deq = orc.sym_dequant(qblk, disk["gw_qs"].view(np.uint8), disk["gw_d"].view(np.uint16), OUT, IN, bits)
+    rel = np.linalg.norm(deq - w) / np.linalg.norm(w)
+    assert rel < {8: 0.01, 6: 0.04}[bits]
+
+
+# ───────────────────────────── container / manifest ─────────────────────────────
+
+def _small_file(path, kinds=("sb6",)):
+    rng = np.random.default_rng(0)
+    tensors = {}
+    for i, kind in enumerate(kinds):
+        w = (rng.standard_normal((32, 512)) * 0.02).astype(np.float32)
+        tensors[f"blocks.{i}.att.key.weight"] = quant.sb6_entry(w, 5) if kind == "sb6" else quant.sym_entry(w, 6)
+    quant.write_rwkvq(path, tensors, n_layer=len(kinds), n_embd=512, vocab_size=64)
+    return tensors
+
+
+def test_container_round_trip_and_host_load(tmp_path, orc):
+    p = str(tmp_path / "m.rwkvq")
+    tensors = _small_file(p, ("sb6", "sym"))
+    box = quant.RwkvqContainer(p)
+    assert "blocks.0.att.key.weight::gw_qsqm" in box.names
+    assert box.shape("blocks.0.att.key.weight::gw_qsqm") == (32, 2, 12)
+    assert box.dtype("blocks.0.att.key.weight::gw_d") == "F16"
+    assert np.array_equal(box.array("blocks.1.att.key.weight::gw_qs"), tensors["blocks.1.att.key.weight"][1]["gw_qs"])
+    box.close()
+    sc = quant.RwkvqSidecar.from_rwkvq(p, device="cpu")
+    assert sc.n_layer == 2 and sc.n_embd == 512 and sc.naming == "world"
+    info = sc.tensors["blocks.0.att.key.weight"]
+    assert info.kind == quant.RwkvqKind.sb6 and info.xbits == 1 and info.bits == 5 and info.is_quantized_base
+    assert sc.tensors["blocks.1.att.key.weight"].bits == 6
+    # buffers in loader layout, equal to the oracle repack of the disk buffers
+    disk = tensors["blocks.0.att.key.weight"][1]
+    want = orc.sb6_to_k3(disk["codes_packed"], disk["gw_qh"], None, disk["gw_qsqm"], disk["gw_d"].view(np.uint16),
+                         disk["gw_dm"].view(np.uint16), 32, 512)
+    assert np.array_equal(sc.arrays["blocks.0.att.key.weight::qblk"].numpy(), want[0])
+    assert np.array_equal(sc.arrays["blocks.0.att.key.weight::qsqm"].numpy(), want[1])
+    assert np.array_equal(sc.arrays["blocks.0.att.key.weight::ddm"].view(torch.int16).numpy().view(np.uint16), want[2])
+    # partial load: manifest validated in full, buffers only for the wanted tensor
+    part = quant.RwkvqSidecar.from_rwkvq(p, only=lambda k: k.startswith("blocks.1"), device="cpu")
+    assert part.contains("blocks.0.att.key.weight")
+    with pytest.raises(quant.MissingBuffer):
+        part.dequantize("blocks.0.att.key.weight")
+
+
+def test_container_rejects_foreign_files(tmp_path):
+    # RwkvqFileTests.swift:129-156
+    zipf = tmp_path / "old.rwkvq"
+    zipf.write_bytes(bytes([0x50, 0x4B, 0x03, 0x04]) + bytes(64))
+    with pytest.raises(quant.MalformedManifest, match="pickle"):
+        quant.RwkvqSidecar.from_rwkvq(str(zipf), device="cpu")
+    plain = tmp_path / "plain.safetensors"
+    quant.write_safetensors(str(plain), {"x": np.float32([1, 2, 3])})
+    with pytest.raises(quant.MalformedManifest, match="not .rwkvq"):
+        quant.RwkvqSidecar.from_rwkvq(str(plain), device="cpu")
+    good = tmp_path / "good.rwkvq"
+    _small_file(str(good))
+    cut = tmp_path / "cut.rwkvq"
+    cut.write_bytes(good.read_bytes()[:3000])
+    with pytest.raises(quant.MalformedManifest):
+        quant.RwkvqSidecar.from_rwkvq(str(cut), device="cpu")
+    with pytest.raises(quant.MissingFile):
+        quant.RwkvqSidecar.from_rwkvq(str(tmp_path / "no.rwkvq"), device="cpu")
+    short = tmp_path / "short.rwkvq"
+    short.write_bytes(b"\x01\x02")
+    with pytest.raises(quant.MalformedManifest):
+        quant.RwkvqContainer(str(short))
+    # header length beyond the file, unknown dtype, offsets that disagree with the shape
+    bad = tmp_path / "bad.rwkvq"
+    bad.write_bytes((10 ** 6).to_bytes(8, "little") + b"{}")
+    with pytest.raises(quant.MalformedManifest, match="outside the file"):
+        quant.RwkvqContainer(str(bad))
+    for hdr in (b'{"x":{"dtype":"Q7","shape":[1],"data_offsets":[0,1]}}',
+                b'{"x":{"dtype":"F32","shape":[2],"data_offsets":[0,4]}}'):
+        f = tmp_path / "hdr.rwkvq"
+        f.write_bytes(len(hdr).to_bytes(8, "little") + hdr + bytes(8))
+        with pytest.raises(quant.MalformedManifest):
+            quant.RwkvqContainer(str(f))
+
+
+def test_manifest_validation_errors(tmp_path):
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((16, 512)) * 0.02).astype(np.float32)
+    m, bufs = quant.sb6_entry(w, 4)
+
+    def write(entry, buffers, **kw):
+        p = str(tmp_path / "v.rwkvq")
+        quant.write_rwkvq(p, {"k.weight": (entry, buffers)}, **kw)
+        return p
+
+    with pytest.raises(quant.MalformedManifest, match="block 32"):
+        quant.RwkvqSidecar.from_rwkvq(write(dict(m, gw_gs=64), bufs), device="cpu")
+    with pytest.raises(quant.MalformedManifest, match="bit planes"):
+        quant.RwkvqSidecar.from_rwkvq(write(dict(m, bits=5), bufs), device="cpu")
+    with pytest.raises(quant.ShapeMismatch):
+        quant.RwkvqSidecar.from_rwkvq(write(m, dict(bufs, gw_qsqm=bufs["gw_qsqm"].reshape(16, 24))), device="cpu")
+    with pytest.raises(quant.MissingBuffer):
+        quant.RwkvqSidecar.from_rwkvq(write(m, {k: v for k, v in bufs.items() if k != "gw_dm"}), device="cpu")
+    with pytest.raises(quant.MalformedManifest, match="blocks"):
+        quant.RwkvqSidecar.from_rwkvq(write(dict(m, n_blocks=3), bufs), device="cpu")
+    with pytest.raises(quant.MalformedManifest, match="format_version"):
+        quant.RwkvqSidecar.from_rwkvq(write(m, bufs, format_version=3), device="cpu")
+    with pytest.raises(quant.MalformedManifest, match="unknown layout"):
+        quant.RwkvqSidecar.from_rwkvq(write(dict(m, kind="q9"), bufs), device="cpu")
+    sm, sbufs = quant.sym_entry(w, 8)
+    with pytest.raises(quant.MalformedManifest, match="codes buffer"):
+        quant.RwkvqSidecar.from_rwkvq(write(dict(sm, bits=6), sbufs), device="cpu")
+
+
+def test_lora_orientation_naming_rule():
+    # RwkvqFileTests.swift:123-127
+    assert quant.is_raw_lora_world("blocks.11.att.g2")
+    assert quant.is_raw_lora_world("blocks.0.att.w1")
+    assert not quant.is_raw_lora_world("blocks.0.att.w0")
+    assert not quant.is_raw_lora_world("blocks.0.att.key.weight")
+    assert not quant.is_raw_lora_world("blocks.0.ffn.w1")
