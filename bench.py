@@ -255,7 +255,7 @@ def bench_wkv(dev, reps=5):
         return K._train_forward(ins_p, dt, None)
 
     def bwd(sa, ck):
-        _lib.call("rwkv_wkv7_train_bwd", *[z.data_ptr() for z in ins_p], dt, ck.data_ptr(), sa.data_ptr(),
+        _lib.call("rwkv_wkv7_train_bwd", *[z.data_ptr() for z in ins_p], dt, None, ck.data_ptr(), sa.data_ptr(),
                   dy.data_ptr(), None, *[g.data_ptr() for g in grads], _lib.BF16, dh_in.data_ptr(), B, T, H, 2,
                   torch.cuda.current_stream().cuda_stream)
 

@@ -86,14 +86,18 @@ rwkv_status rwkv_wkv7_train_fwd(const void* r, const void* w, const void* k, con
 
 /* Backward from checkpoints.  Replaces ckptBwdKernelV2 / ckptBwdKernel
  * launched by the VJP of wkv7TrainWithState (WKV7Train.swift:99-339,410-420).
- * d_out [B,T,H,64] fp32; d_h_out [B,H,64,64] fp32 or NULL.  Gradients
- * dr..db [B,T,H,64] are written in g_dt (the primal's dtype, :440,462);
- * dh_in [B,H,64,64] fp32.  variant: 2 = column-owned state (reference
- * default, wkv7BackwardV2 = true), 1 = row-owned state (the v1 kernel).
- * The two variants sum in different orders, as in the reference. */
+ * h_in: the forward's initial state [B,H,64,64] fp32 or NULL (zeros) — the
+ * VJP's primal h0; the kernel recomputes each chunk's states forward from
+ * h_in / the previous checkpoint instead of dividing by w.
+ * h_ckpt, sa: the training forward's outputs.  d_out [B,T,H,64] fp32;
+ * d_h_out [B,H,64,64] fp32 or NULL.  Gradients dr..db [B,T,H,64] are written
+ * in g_dt (the primal's dtype, :440,462); dh_in [B,H,64,64] fp32.
+ * variant: 2 = the default (wkv7BackwardV2 = true), 1 = the alternative;
+ * both compute the same gradients and differ only in summation order, like
+ * the reference's v1 / v2 pair. */
 rwkv_status rwkv_wkv7_train_bwd(const void* r, const void* w, const void* k, const void* v,
                                 const void* a, const void* b, rwkv_dtype in_dt,
-                                const float* h_ckpt, const float* sa,
+                                const float* h_in, const float* h_ckpt, const float* sa,
                                 const float* d_out, const float* d_h_out,
                                 void* dr, void* dw, void* dk, void* dv, void* da, void* db,
                                 rwkv_dtype g_dt, float* dh_in,

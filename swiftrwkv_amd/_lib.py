@@ -50,7 +50,7 @@ _SIGS = {
     "rwkv_wkv7_seq_fwd": (I, [P] * 6 + [I, P, P, P, L, L, L, P]),
     "rwkv_wkv7_chunk_fwd": (I, [P] * 6 + [I, P, P, P, P, L, L, L, P]),
     "rwkv_wkv7_train_fwd": (I, [P] * 6 + [I, P, P, P, P, P, L, L, L, P]),
-    "rwkv_wkv7_train_bwd": (I, [P] * 6 + [I, P, P, P, P] + [P] * 6 + [I, P, L, L, L, I, P]),
+    "rwkv_wkv7_train_bwd": (I, [P] * 6 + [I, P, P, P, P, P] + [P] * 6 + [I, P, L, L, L, I, P]),
     "rwkv_wkv7_step": (I, [P] * 6 + [I, P, P, P, L, L, P]),
     "rwkv_wkv_tail_applies": (I, [L]),
     "rwkv_wkv_tail": (I, [P] * 9 + [L, L, L, F, P]),

@@ -5,29 +5,36 @@
 //   sa_i = Σ_j S_ij a_j ;  S_ij ← w_j S_ij + v_i k_j + sa_i b_j ;  y_i = Σ_j S_ij r_j
 // (Sources/RWKVKernel/WKV7.swift:207-224).
 //
-// Forward work split (one 256-thread workgroup per (b, h)):
-//   wave q (0..3) owns key columns J_q = [16q, 16q+16); lane i owns value row i.
-//   Each lane keeps its 16 state values in VGPRs for the whole sequence.  The
-//   per-step vectors a/w/k/b/r restricted to J_q are the same for all 64 lanes
-//   of a wave, so they are read with wave-uniform (scalar) loads and used as
-//   SGPR operands: no LDS fan-out of the step vectors.  The only exchange per
-//   step is sa: four partial sums per row through LDS (double-buffered by step
-//   parity, one barrier per step).  The four partial y's go to an LDS ring
-//   that is summed and stored (coalesced) once every 16 steps.
-//   The step kernel, the chunk kernel and the training forward are this same
-//   kernel with T = 1 / emitted sa / emitted checkpoints, so they agree
-//   bitwise by construction (the reference's own invariants:
-//   WKV7SequenceTests, WKV7StateTests.swift:178-186, DecodeKernelTests.swift:27-39).
+// Forward (one wave = 16 value rows × 64 key columns of one head, no LDS, no
+// barrier).  Lane l owns row 16·blk + (l & 15) and the 16 key columns of
+// column group g = l >> 4, holding those 16 state values in VGPRs for the
+// whole sequence.  The 16 lanes of a DPP row share g, so each step vector
+// (a, w, k, b, r) is held ONE value per lane (lane l keeps element 16g + (l & 15))
+// and broadcast into the FMAs with DPP row_newbcast — a single global_load per
+// vector per step, prefetched 8 steps ahead in a 16-slot register ring.  The
+// four column-group partials of sa and y of a row (lanes l, l^16, l^32, l^48)
+// are combined with v_permlane16_swap / v_permlane32_swap.  The next step's sa
+// partial is accumulated inside the update loop, so a step is 5 FMAs per
+// state element plus two lane swaps.
+// The decode step, the chunk kernel and the training forward are this same
+// kernel (T = 1 / emitted sa / emitted checkpoints), so they agree bitwise by
+// construction (the reference's invariants WKV7SequenceTests,
+// WKV7StateTests.swift:178-186, DecodeKernelTests.swift:27-39).
 //
-// Backward (variant 2, column-owned like ckptBwdKernelV2, WKV7Train.swift:234-339):
-//   lane i owns key column i; wave q owns value rows J_q.  A lane holds
-//   S[J_q, i], dS[J_q, i] and the row copy dS[i, J_q], so dr/dw/dk/db/da are
-//   in-lane partial dots over J_q and dv/dsa are in-lane partial dots of the
-//   row copy.  dsa is the one quantity exchanged within the step; every output
-//   is summed over the four waves through an LDS ring, 4 steps at a time.
+// Backward (column-owned, the scheme of ckptBwdKernelV2,
+// WKV7Train.swift:234-339).  Eight waves per head: lane i owns key column i,
+// wave q owns value rows J_q = [8q, 8q+8).  Instead of reconstructing earlier
+// states by dividing by w (which re-amplifies the forward's rounding by up to
+// 1/w^15), each 16-step chunk's states are recomputed forward from the
+// previous checkpoint (or h_in) with the stored sa and the forward kernel's
+// exact FMA sequence, so they are bitwise the forward's states.  The chunk is
+// handled as two 8-step windows whose states are held in registers.  Step
+// vectors are staged per chunk in LDS (coalesced loads issued one chunk
+// ahead); dsa is the one quantity exchanged inside a step (one barrier per
+// step); every output is summed over the eight waves from an LDS ring.
 //
-// All arithmetic is fp32 with fixed summation order, so every launch is
-// bitwise deterministic.
+// All arithmetic is fp32 with a fixed summation order: launches are bitwise
+// deterministic.
 
 #include <hip/hip_runtime.h>
 
@@ -37,42 +44,6 @@ namespace {
 
 constexpr int D = 64;   // WKV7_HEAD_SIZE
 constexpr int CH = 16;  // WKV7_CHUNK
-constexpr int NQ = 4;   // waves per workgroup
-constexpr int JW = 16;  // key columns (fwd) / value rows (bwd) per wave
-
-__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
-__device__ __forceinline__ float f16_lo(uint32_t u) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xffffu));
-}
-__device__ __forceinline__ float f16_hi(uint32_t u) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
-}
-
-// 16 consecutive elements starting at element `off` (off % 16 == 0), widened
-// to fp32.  Called with wave-uniform addresses, so the compiler can use scalar
-// loads.
-template <int DT>
-__device__ __forceinline__ void load16(const void* __restrict__ p, int64_t off, float (&o)[JW]) {
-    if constexpr (DT == RWKV_F32) {
-        const float* q = reinterpret_cast<const float*>(p) + off;
-#pragma unroll
-        for (int c = 0; c < JW; ++c) o[c] = q[c];
-    } else {
-        const uint32_t* q = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(p) + off);
-#pragma unroll
-        for (int c = 0; c < JW / 2; ++c) {
-            uint32_t u = q[c];
-            if constexpr (DT == RWKV_BF16) {
-                o[2 * c] = bf16_lo(u);
-                o[2 * c + 1] = bf16_hi(u);
-            } else {
-                o[2 * c] = f16_lo(u);
-                o[2 * c + 1] = f16_hi(u);
-            }
-        }
-    }
-}
 
 template <int DT>
 __device__ __forceinline__ float load1(const void* __restrict__ p, int64_t off) {
@@ -97,348 +68,415 @@ __device__ __forceinline__ void store1(void* __restrict__ p, int64_t off, float 
     }
 }
 
-__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+// ─────────────────────────────── DPP / lane-swap helpers ───────────────────────────────
+// row_newbcast:c broadcasts lane c of every 16-lane row to the whole row.  The
+// compiler does not fold a DPP move into an FMA, so the fused forms are written
+// as inline assembly.  Every block starts with `s_nop 1`: the two wait states a
+// VALU write of a broadcast source needs before its DPP read.
+#define RWKV_BC(n) " row_newbcast:" #n " row_mask:0xf bank_mask:0xf\n\t"
+
+// Sum of the four column-group partials of a row (lanes l, l^16, l^32, l^48),
+// associated as (g0+g1)+(g2+g3) in every lane, so all four hold the same bits.
+__device__ __forceinline__ float rowsum4(float x) {
+    float a = x, b = x;
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    const float s = a + b;
+    float c = s, d = s;
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
+    return c + d;
+}
+
+// Forward update of 8 state elements (columns c0..c0+7 of the lane's group):
+//   n = k·v ; n += b·sa ; n += w·S          (new state, one rounding per FMA)
+//   y += r·n ; p += a'·n                    (a' = next step's a)
+#define RWKV_UPD(c, S, N)                                    \
+    "v_mul_f32_dpp %[" N "], %[K], %[vv]" RWKV_BC(c)         \
+    "v_fmac_f32_dpp %[" N "], %[B], %[sa]" RWKV_BC(c)        \
+    "v_fmac_f32_dpp %[" N "], %[W], %[" S "]" RWKV_BC(c)     \
+    "v_fmac_f32_dpp %[y], %[R], %[" N "]" RWKV_BC(c)         \
+    "v_fmac_f32_dpp %[p], %[A], %[" N "]" RWKV_BC(c)
+
+#define RWKV_UPD_OPERANDS(S, N, o)                                                                              \
+    : [n0] "=&v"(N[o + 0]), [n1] "=&v"(N[o + 1]), [n2] "=&v"(N[o + 2]), [n3] "=&v"(N[o + 3]),                    \
+      [n4] "=&v"(N[o + 4]), [n5] "=&v"(N[o + 5]), [n6] "=&v"(N[o + 6]), [n7] "=&v"(N[o + 7]), [y] "+v"(y),        \
+      [p] "+v"(p)                                                                                                 \
+    : [s0] "v"(S[o + 0]), [s1] "v"(S[o + 1]), [s2] "v"(S[o + 2]), [s3] "v"(S[o + 3]), [s4] "v"(S[o + 4]),         \
+      [s5] "v"(S[o + 5]), [s6] "v"(S[o + 6]), [s7] "v"(S[o + 7]), [K] "v"(K), [B] "v"(B), [W] "v"(W), [R] "v"(R), \
+      [A] "v"(A), [vv] "v"(vv), [sa] "v"(sa)
+
+__device__ __forceinline__ void fwd_update16(const float (&S)[16], float (&N)[16], float K, float B, float W,
+                                             float R, float A, float vv, float sa, float& y, float& p) {
+    asm("s_nop 1\n\t"
+        RWKV_UPD(0, "s0", "n0") RWKV_UPD(1, "s1", "n1") RWKV_UPD(2, "s2", "n2") RWKV_UPD(3, "s3", "n3")
+        RWKV_UPD(4, "s4", "n4") RWKV_UPD(5, "s5", "n5") RWKV_UPD(6, "s6", "n6") RWKV_UPD(7, "s7", "n7")
+        RWKV_UPD_OPERANDS(S, N, 0));
+    asm("s_nop 1\n\t"
+        RWKV_UPD(8, "s0", "n0") RWKV_UPD(9, "s1", "n1") RWKV_UPD(10, "s2", "n2") RWKV_UPD(11, "s3", "n3")
+        RWKV_UPD(12, "s4", "n4") RWKV_UPD(13, "s5", "n5") RWKV_UPD(14, "s6", "n6") RWKV_UPD(15, "s7", "n7")
+        RWKV_UPD_OPERANDS(S, N, 8));
+}
+
+// p += Σ_c a_c·S_c over the lane's 16 columns (the first step's sa partial).
+#define RWKV_DOT(c, S) "v_fmac_f32_dpp %[p], %[A], %[" S "]" RWKV_BC(c)
+__device__ __forceinline__ void fwd_dot16(const float (&S)[16], float A, float& p) {
+    asm("s_nop 1\n\t"
+        RWKV_DOT(0, "s0") RWKV_DOT(1, "s1") RWKV_DOT(2, "s2") RWKV_DOT(3, "s3")
+        RWKV_DOT(4, "s4") RWKV_DOT(5, "s5") RWKV_DOT(6, "s6") RWKV_DOT(7, "s7")
+        : [p] "+v"(p)
+        : [s0] "v"(S[0]), [s1] "v"(S[1]), [s2] "v"(S[2]), [s3] "v"(S[3]), [s4] "v"(S[4]), [s5] "v"(S[5]),
+          [s6] "v"(S[6]), [s7] "v"(S[7]), [A] "v"(A));
+    asm("s_nop 1\n\t"
+        RWKV_DOT(8, "s0") RWKV_DOT(9, "s1") RWKV_DOT(10, "s2") RWKV_DOT(11, "s3")
+        RWKV_DOT(12, "s4") RWKV_DOT(13, "s5") RWKV_DOT(14, "s6") RWKV_DOT(15, "s7")
+        : [p] "+v"(p)
+        : [s0] "v"(S[8]), [s1] "v"(S[9]), [s2] "v"(S[10]), [s3] "v"(S[11]), [s4] "v"(S[12]), [s5] "v"(S[13]),
+          [s6] "v"(S[14]), [s7] "v"(S[15]), [A] "v"(A));
+}
 
 // ─────────────────────────────── forward ───────────────────────────────
+// Grid: 4 workgroups of one wave per (b, h); workgroup 4·(b·H + h) + blk owns
+// value rows 16·blk .. 16·blk + 15.
 template <int DT, bool EMIT_SA, bool EMIT_CK>
-__global__ __launch_bounds__(256) void wkv7_fwd_kernel(
+__global__ __launch_bounds__(64) void wkv7_fwd_kernel(
     const void* __restrict__ r, const void* __restrict__ w, const void* __restrict__ k,
     const void* __restrict__ v, const void* __restrict__ a, const void* __restrict__ b,
     const float* __restrict__ h_in, float* __restrict__ out, float* __restrict__ h_out,
     float* __restrict__ sa_out, float* __restrict__ ckpt, int T, int H) {
-    __shared__ float4 sa_part[2][D];      // [step parity][row] = partial sa of waves 0..3
-    __shared__ float4 y_ring[2][CH][D];   // [chunk parity][step][row] = partial y of waves 0..3
-
-    const int i = threadIdx.x & 63;
-    const int q = wave_id();
-    const int bh = blockIdx.x;
+    const int l = threadIdx.x;
+    const int ri = l & 15, g = l >> 4;
+    const int bh = blockIdx.x >> 2, blk = blockIdx.x & 3;
     const int bi = bh / H, hi = bh - bi * H;
-    const int64_t sbase = (int64_t)bh * D * D + (int64_t)i * D + JW * q;   // S[i, J_q]
+    const int row = 16 * blk + ri;
+    const int vidx = 16 * g + ri;   // step-vector element this lane broadcasts
     const int64_t strideT = (int64_t)H * D;
-    const int64_t base0 = ((int64_t)bi * T * H + hi) * D;                  // (bi, t=0, hi, 0)
+    const int64_t base0 = ((int64_t)bi * T * H + hi) * D;
+    const int64_t sbase = (int64_t)bh * D * D + (int64_t)row * D + 16 * g;
     const int NC = T / CH;
 
-    float S[JW];
+    float S[2][16];
     if (h_in) {
         const float4* src = reinterpret_cast<const float4*>(h_in + sbase);
 #pragma unroll
-        for (int c = 0; c < JW / 4; ++c) {
-            float4 f = src[c];
-            S[4 * c] = f.x; S[4 * c + 1] = f.y; S[4 * c + 2] = f.z; S[4 * c + 3] = f.w;
+        for (int m = 0; m < 4; ++m) {
+            const float4 f = src[m];
+            S[0][4 * m] = f.x; S[0][4 * m + 1] = f.y; S[0][4 * m + 2] = f.z; S[0][4 * m + 3] = f.w;
         }
     } else {
 #pragma unroll
-        for (int c = 0; c < JW; ++c) S[c] = 0.0f;
+        for (int c = 0; c < 16; ++c) S[0][c] = 0.0f;
     }
 
+    // ring slot: a, w, k, b, r (broadcast sources), v (own row)
+    float ring[CH][6];
+    auto fetch = [&](float (&slot)[6], int t) {
+        const int64_t bt = base0 + (int64_t)min(t, T - 1) * strideT;
+        slot[0] = load1<DT>(a, bt + vidx);
+        slot[1] = load1<DT>(w, bt + vidx);
+        slot[2] = load1<DT>(k, bt + vidx);
+        slot[3] = load1<DT>(b, bt + vidx);
+        slot[4] = load1<DT>(r, bt + vidx);
+        slot[5] = load1<DT>(v, bt + row);
+    };
+#pragma unroll
+    for (int s = 0; s < 8; ++s) fetch(ring[s], s);
+
+    float p = 0.0f;
+    fwd_dot16(S[0], ring[0][0], p);
+
     const int nchunks = (T + CH - 1) / CH;
+    int last = 0;
     for (int c = 0; c < nchunks; ++c) {
         const int t0 = c * CH;
         const int n = min(CH, T - t0);
-        const int half = c & 1;
-        float vreg[CH];
-#pragma unroll
-        for (int s = 0; s < CH; ++s) vreg[s] = (s < n) ? load1<DT>(v, base0 + (int64_t)(t0 + s) * strideT + i) : 0.0f;
-
+        last = n;
 #pragma unroll
         for (int s = 0; s < CH; ++s) {
             if (s < n) {
                 const int t = t0 + s;
+                fetch(ring[(s + 8) & (CH - 1)], t + 8);
+                const float sa = rowsum4(p);
+                float y = 0.0f;
+                p = 0.0f;
+                const float* sl = ring[s];
+                fwd_update16(S[s & 1], S[(s + 1) & 1], sl[2], sl[3], sl[1], sl[4], ring[(s + 1) & (CH - 1)][0],
+                             sl[5], sa, y, p);
+                y = rowsum4(y);
                 const int64_t bt = base0 + (int64_t)t * strideT;
-                float av[JW];
-                load16<DT>(a, bt + JW * q, av);
-                float p0 = 0.0f, p1 = 0.0f;
-#pragma unroll
-                for (int j = 0; j < JW; j += 2) {
-                    p0 = fmaf(S[j], av[j], p0);
-                    p1 = fmaf(S[j + 1], av[j + 1], p1);
+                if (g == 0) {
+                    out[bt + row] = y;
+                    if (EMIT_SA) sa_out[bt + row] = sa;
                 }
-                reinterpret_cast<float*>(&sa_part[t & 1][i])[q] = p0 + p1;
-                float wv[JW], kv[JW], bv[JW], rv[JW];
-                load16<DT>(w, bt + JW * q, wv);
-                load16<DT>(k, bt + JW * q, kv);
-                load16<DT>(b, bt + JW * q, bv);
-                load16<DT>(r, bt + JW * q, rv);
-                __syncthreads();
-                const float4 pp = sa_part[t & 1][i];
-                const float sa = (pp.x + pp.y) + (pp.z + pp.w);
-                if (EMIT_SA && q == 0) sa_out[bt + i] = sa;
-                const float vv = vreg[s];
-                float y0 = 0.0f, y1 = 0.0f;
-#pragma unroll
-                for (int j = 0; j < JW; j += 2) {
-                    S[j] = fmaf(wv[j], S[j], fmaf(sa, bv[j], vv * kv[j]));
-                    S[j + 1] = fmaf(wv[j + 1], S[j + 1], fmaf(sa, bv[j + 1], vv * kv[j + 1]));
-                    y0 = fmaf(S[j], rv[j], y0);
-                    y1 = fmaf(S[j + 1], rv[j + 1], y1);
-                }
-                reinterpret_cast<float*>(&y_ring[half][s][i])[q] = y0 + y1;
                 if (EMIT_CK && s == CH - 1) {
-                    float4* dst = reinterpret_cast<float4*>(ckpt + ((int64_t)bh * NC + c) * D * D + (int64_t)i * D + JW * q);
+                    float4* dst = reinterpret_cast<float4*>(ckpt + ((int64_t)bh * NC + c) * D * D + (int64_t)row * D + 16 * g);
 #pragma unroll
-                    for (int m = 0; m < JW / 4; ++m) dst[m] = make_float4(S[4 * m], S[4 * m + 1], S[4 * m + 2], S[4 * m + 3]);
+                    for (int m = 0; m < 4; ++m)
+                        dst[m] = make_float4(S[0][4 * m], S[0][4 * m + 1], S[0][4 * m + 2], S[0][4 * m + 3]);
                 }
             }
-        }
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < n * D; idx += NQ * 64) {
-            const int s = idx >> 6, row = idx & 63;
-            const float4 p = y_ring[half][s][row];
-            out[base0 + (int64_t)(t0 + s) * strideT + row] = (p.x + p.y) + (p.z + p.w);
         }
     }
     float4* dst = reinterpret_cast<float4*>(h_out + sbase);
+    if (last & 1) {
 #pragma unroll
-    for (int m = 0; m < JW / 4; ++m) dst[m] = make_float4(S[4 * m], S[4 * m + 1], S[4 * m + 2], S[4 * m + 3]);
+        for (int m = 0; m < 4; ++m) dst[m] = make_float4(S[1][4 * m], S[1][4 * m + 1], S[1][4 * m + 2], S[1][4 * m + 3]);
+    } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) dst[m] = make_float4(S[0][4 * m], S[0][4 * m + 1], S[0][4 * m + 2], S[0][4 * m + 3]);
+    }
 }
 
-// ─────────────────────────────── backward (column-owned) ───────────────────────────────
-constexpr int BG = 4;   // steps per output flush
-constexpr int NOUT = 6; // dr, dw, dk, db, dv, da
+// ─────────────────────────────── backward ───────────────────────────────
+constexpr int BQ = 8;     // waves per head
+constexpr int BJ = 8;     // value rows per wave
+constexpr int NVEC = 8;   // staged step vectors: r w k v a b dy sa
+constexpr int NOUT = 6;   // dr dw dk db dv da
+constexpr int WIN = 8;    // steps per register window (two per chunk)
 
-template <int DT, int GT>
-__global__ __launch_bounds__(256) void wkv7_bwd_v2_kernel(
+#define RWKV_BC8(n) RWKV_BC(n)
+
+// 8-wide broadcast helpers: lane l holds element 8q + (l & 7) of a step vector
+// over the wave's rows; row_newbcast:jj reads row jj of the wave's block.
+// (1) recompute: n_jj = v_j·k_i ; n_jj += sa_j·b_i      (then n += w_i·S in C++)
+#define RWKV_RC(jj) \
+    "v_mul_f32_dpp %[n" #jj "], %[V], %[ki]" RWKV_BC(jj) "v_fmac_f32_dpp %[n" #jj "], %[SA], %[bi]" RWKV_BC(jj)
+__device__ __forceinline__ void bwd_recompute8(const float (&S)[BJ], float (&N)[BJ], float V, float SA, float ki,
+                                               float bi, float wi) {
+    asm("s_nop 1\n\t" RWKV_RC(0) RWKV_RC(1) RWKV_RC(2) RWKV_RC(3) RWKV_RC(4) RWKV_RC(5) RWKV_RC(6) RWKV_RC(7)
+        : [n0] "=&v"(N[0]), [n1] "=&v"(N[1]), [n2] "=&v"(N[2]), [n3] "=&v"(N[3]), [n4] "=&v"(N[4]),
+          [n5] "=&v"(N[5]), [n6] "=&v"(N[6]), [n7] "=&v"(N[7])
+        : [V] "v"(V), [SA] "v"(SA), [ki] "v"(ki), [bi] "v"(bi));
+#pragma unroll
+    for (int jj = 0; jj < BJ; ++jj) N[jj] = fmaf(wi, S[jj], N[jj]);
+}
+
+// (2) first half of a reverse step, 4 rows at a time:
+//   dr += dy_j·S_j ; dT_j += dy_j·r_i ; dR_j += r_j·dy_i
+#define RWKV_B1(jj, e)                                              \
+    "v_fmac_f32_dpp %[dr], %[DY], %[sa" #e "]" RWKV_BC(jj)          \
+    "v_fmac_f32_dpp %[t" #e "], %[DY], %[ri]" RWKV_BC(jj)           \
+    "v_fmac_f32_dpp %[u" #e "], %[R], %[dyi]" RWKV_BC(jj)
+#define RWKV_B1_BLOCK(j0, j1, j2, j3, o)                                                                  \
+    asm("s_nop 1\n\t" RWKV_B1(j0, 0) RWKV_B1(j1, 1) RWKV_B1(j2, 2) RWKV_B1(j3, 3)                          \
+        : [dr] "+v"(pdr), [t0] "+v"(dT[o]), [t1] "+v"(dT[o + 1]), [t2] "+v"(dT[o + 2]), [t3] "+v"(dT[o + 3]), \
+          [u0] "+v"(dR[o]), [u1] "+v"(dR[o + 1]), [u2] "+v"(dR[o + 2]), [u3] "+v"(dR[o + 3])               \
+        : [sa0] "v"(Sa[o]), [sa1] "v"(Sa[o + 1]), [sa2] "v"(Sa[o + 2]), [sa3] "v"(Sa[o + 3]), [DY] "v"(DY),  \
+          [R] "v"(R), [ri] "v"(ri), [dyi] "v"(dyi))
+// (3) dk += v_j·dT_j ; db += sa_j·dT_j ; dv += k_j·dR_j ; dsa += b_j·dR_j
+#define RWKV_B2(jj, e)                                              \
+    "v_fmac_f32_dpp %[dk], %[V], %[t" #e "]" RWKV_BC(jj)            \
+    "v_fmac_f32_dpp %[db], %[SA], %[t" #e "]" RWKV_BC(jj)           \
+    "v_fmac_f32_dpp %[dv], %[K], %[u" #e "]" RWKV_BC(jj)            \
+    "v_fmac_f32_dpp %[ds], %[B], %[u" #e "]" RWKV_BC(jj)
+#define RWKV_B2_BLOCK(j0, j1, j2, j3, o)                                                                  \
+    asm("s_nop 1\n\t" RWKV_B2(j0, 0) RWKV_B2(j1, 1) RWKV_B2(j2, 2) RWKV_B2(j3, 3)                          \
+        : [dk] "+v"(pdk), [db] "+v"(pdb), [dv] "+v"(pdv), [ds] "+v"(pds)                                   \
+        : [t0] "v"(dT[o]), [t1] "v"(dT[o + 1]), [t2] "v"(dT[o + 2]), [t3] "v"(dT[o + 3]), [u0] "v"(dR[o]),    \
+          [u1] "v"(dR[o + 1]), [u2] "v"(dR[o + 2]), [u3] "v"(dR[o + 3]), [V] "v"(V), [SA] "v"(SA), [K] "v"(K), \
+          [B] "v"(B))
+// (4) da += dsa_j·Sp_j ; dR_j ← a_j·dsa_i + w_j·dR_j ; dT_j ← dsa_j·a_i (+ w_i·dT_j in C++)
+#define RWKV_B3(jj, e)                                              \
+    "v_fmac_f32_dpp %[da], %[DS], %[sp" #e "]" RWKV_BC(jj)          \
+    "v_mul_f32_dpp %[nu" #e "], %[A], %[dsi]" RWKV_BC(jj)           \
+    "v_fmac_f32_dpp %[nu" #e "], %[W], %[u" #e "]" RWKV_BC(jj)      \
+    "v_mul_f32_dpp %[nt" #e "], %[DS], %[ai]" RWKV_BC(jj)
+#define RWKV_B3_BLOCK(j0, j1, j2, j3, o)                                                                      \
+    asm("s_nop 1\n\t" RWKV_B3(j0, 0) RWKV_B3(j1, 1) RWKV_B3(j2, 2) RWKV_B3(j3, 3)                              \
+        : [da] "+v"(pda), [nu0] "=&v"(nR[o]), [nu1] "=&v"(nR[o + 1]), [nu2] "=&v"(nR[o + 2]),                  \
+          [nu3] "=&v"(nR[o + 3]), [nt0] "=&v"(nT[o]), [nt1] "=&v"(nT[o + 1]), [nt2] "=&v"(nT[o + 2]),           \
+          [nt3] "=&v"(nT[o + 3])                                                                               \
+        : [sp0] "v"(Sp[o]), [sp1] "v"(Sp[o + 1]), [sp2] "v"(Sp[o + 2]), [sp3] "v"(Sp[o + 3]), [u0] "v"(dR[o]), \
+          [u1] "v"(dR[o + 1]), [u2] "v"(dR[o + 2]), [u3] "v"(dR[o + 3]), [DS] "v"(DS), [A] "v"(A), [W] "v"(W),  \
+          [dsi] "v"(dsa_i), [ai] "v"(ai))
+
+template <bool SEQ>
+__device__ __forceinline__ float sum8(const float4 lo, const float4 hi) {
+    if constexpr (SEQ) return (((((((lo.x + lo.y) + lo.z) + lo.w) + hi.x) + hi.y) + hi.z) + hi.w);
+    return ((lo.x + lo.y) + (lo.z + lo.w)) + ((hi.x + hi.y) + (hi.z + hi.w));
+}
+
+// SEQ = false: variant 2 (pairwise sums).  SEQ = true: variant 1 — identical
+// math, every sum taken sequentially (a different rounding order).
+template <int DT, int GT, bool SEQ>
+__global__ __launch_bounds__(512) void wkv7_bwd_kernel(
     const void* __restrict__ r, const void* __restrict__ w, const void* __restrict__ k,
     const void* __restrict__ v, const void* __restrict__ a, const void* __restrict__ b,
-    const float* __restrict__ ckpt, const float* __restrict__ sa, const float* __restrict__ dout,
-    const float* __restrict__ dhout, void* __restrict__ g_dr, void* __restrict__ g_dw,
-    void* __restrict__ g_dk, void* __restrict__ g_dv, void* __restrict__ g_da, void* __restrict__ g_db,
-    float* __restrict__ dh_in, int T, int H) {
-    __shared__ float4 dsa_part[2][D];           // [parity][column i] partial dsa (rows of waves 0..3)
-    __shared__ float4 ring[2][BG][NOUT][D];     // [group parity][slot][output][column]
+    const float* __restrict__ h_in, const float* __restrict__ ckpt, const float* __restrict__ sa,
+    const float* __restrict__ dout, const float* __restrict__ dhout, void* __restrict__ g_dr,
+    void* __restrict__ g_dw, void* __restrict__ g_dk, void* __restrict__ g_dv, void* __restrict__ g_da,
+    void* __restrict__ g_db, float* __restrict__ dh_in, int T, int H) {
+    __shared__ float stage[2][NVEC][CH][D];        // step vectors of a chunk, fp32
+    __shared__ float4 dsa_part[2][D][2];           // [parity][column][waves 0-3 | 4-7]
+    __shared__ float4 ring[3][NOUT][D][2];         // output partials of the last steps
 
-    const int i = threadIdx.x & 63;   // key column owned by this lane
-    const int q = wave_id();          // value rows J_q
+    const int tid = threadIdx.x;
+    const int i = tid & 63;                                    // key column
+    const int q = __builtin_amdgcn_readfirstlane(tid >> 6);    // value rows 8q .. 8q+7
+    const int jl = 8 * q + (i & 7);                            // row this lane broadcasts
     const int bh = blockIdx.x;
     const int bi = bh / H, hi = bh - bi * H;
     const int64_t strideT = (int64_t)H * D;
     const int64_t base0 = ((int64_t)bi * T * H + hi) * D;
-    const int NC = T / CH;
     const int64_t hb = (int64_t)bh * D * D;
-
-    float sT[JW], dT[JW], dR[JW];   // S[J_q, i], dS[J_q, i], dS[i, J_q]
-    if (dhout) {
-#pragma unroll
-        for (int jj = 0; jj < JW; ++jj) dT[jj] = dhout[hb + (int64_t)(JW * q + jj) * D + i];
-        const float4* src = reinterpret_cast<const float4*>(dhout + hb + (int64_t)i * D + JW * q);
-#pragma unroll
-        for (int m = 0; m < JW / 4; ++m) {
-            float4 f = src[m];
-            dR[4 * m] = f.x; dR[4 * m + 1] = f.y; dR[4 * m + 2] = f.z; dR[4 * m + 3] = f.w;
-        }
-    } else {
-#pragma unroll
-        for (int jj = 0; jj < JW; ++jj) { dT[jj] = 0.0f; dR[jj] = 0.0f; }
-    }
-
-    void* const outs[NOUT] = {g_dr, g_dw, g_dk, g_db, g_dv, g_da};
-    int step = 0;   // reverse-step counter
-    for (int c = NC - 1; c >= 0; --c) {
-        const float* ck = ckpt + (hb * NC) + (int64_t)c * D * D;
-#pragma unroll
-        for (int jj = 0; jj < JW; ++jj) sT[jj] = ck[(int64_t)(JW * q + jj) * D + i];
-
-        for (int s = CH - 1; s >= 0; --s, ++step) {
-            const int t = c * CH + s;
-            const int64_t bt = base0 + (int64_t)t * strideT;
-            const int grp = step / BG, slot = step - grp * BG, gh = grp & 1;
-            const float ri = load1<DT>(r, bt + i), wi = load1<DT>(w, bt + i), ki = load1<DT>(k, bt + i);
-            const float ai = load1<DT>(a, bt + i), bI = load1<DT>(b, bt + i), dyi = dout[bt + i];
-
-            float dyj[JW], saj[JW], vj[JW], rj[JW];
-            load16<RWKV_F32>(dout, bt + JW * q, dyj);
-            load16<RWKV_F32>(sa, bt + JW * q, saj);
-            load16<DT>(v, bt + JW * q, vj);
-            load16<DT>(r, bt + JW * q, rj);
-
-            // dr_i = Σ_j S_ji dy_j  (state after the step)
-            float e0 = 0.0f, e1 = 0.0f;
-#pragma unroll
-            for (int jj = 0; jj < JW; jj += 2) { e0 = fmaf(sT[jj], dyj[jj], e0); e1 = fmaf(sT[jj + 1], dyj[jj + 1], e1); }
-            const float pdr = e0 + e1;
-            // S_ji ← (S_ji − v_j k_i − sa_j b_i) / w_i ;  dS += dy ⊗ r
-            const float iw = 1.0f / wi;
-#pragma unroll
-            for (int jj = 0; jj < JW; ++jj) {
-                sT[jj] = fmaf(-saj[jj], bI, fmaf(-vj[jj], ki, sT[jj])) * iw;
-                dT[jj] = fmaf(ri, dyj[jj], dT[jj]);
-                dR[jj] = fmaf(dyi, rj[jj], dR[jj]);
-            }
-            float kj[JW], bj[JW];
-            load16<DT>(k, bt + JW * q, kj);
-            load16<DT>(b, bt + JW * q, bj);
-            float w0 = 0, w1 = 0, k0 = 0, k1 = 0, b0 = 0, b1 = 0, v0 = 0, v1 = 0, s0 = 0, s1 = 0;
-#pragma unroll
-            for (int jj = 0; jj < JW; jj += 2) {
-                w0 = fmaf(dT[jj], sT[jj], w0);       w1 = fmaf(dT[jj + 1], sT[jj + 1], w1);
-                k0 = fmaf(dT[jj], vj[jj], k0);       k1 = fmaf(dT[jj + 1], vj[jj + 1], k1);
-                b0 = fmaf(dT[jj], saj[jj], b0);      b1 = fmaf(dT[jj + 1], saj[jj + 1], b1);
-                v0 = fmaf(dR[jj], kj[jj], v0);       v1 = fmaf(dR[jj + 1], kj[jj + 1], v1);
-                s0 = fmaf(dR[jj], bj[jj], s0);       s1 = fmaf(dR[jj + 1], bj[jj + 1], s1);
-            }
-            reinterpret_cast<float*>(&dsa_part[step & 1][i])[q] = s0 + s1;
-            reinterpret_cast<float*>(&ring[gh][slot][0][i])[q] = pdr;
-            reinterpret_cast<float*>(&ring[gh][slot][1][i])[q] = w0 + w1;
-            reinterpret_cast<float*>(&ring[gh][slot][2][i])[q] = k0 + k1;
-            reinterpret_cast<float*>(&ring[gh][slot][3][i])[q] = b0 + b1;
-            reinterpret_cast<float*>(&ring[gh][slot][4][i])[q] = v0 + v1;
-            float wj[JW], aj[JW];
-            load16<DT>(w, bt + JW * q, wj);
-            load16<DT>(a, bt + JW * q, aj);
-            __syncthreads();
-            const float4 pp = dsa_part[step & 1][i];
-            const float dsa_i = (pp.x + pp.y) + (pp.z + pp.w);
-            float dsaj[JW];
-#pragma unroll
-            for (int jj = 0; jj < JW; ++jj)
-                dsaj[jj] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dsa_i), JW * q + jj));
-            float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-            for (int jj = 0; jj < JW; jj += 2) { a0 = fmaf(sT[jj], dsaj[jj], a0); a1 = fmaf(sT[jj + 1], dsaj[jj + 1], a1); }
-            reinterpret_cast<float*>(&ring[gh][slot][5][i])[q] = a0 + a1;
-            // dS_ij ← dS_ij w_j + dsa_i a_j   (row copy and column copy)
-#pragma unroll
-            for (int jj = 0; jj < JW; ++jj) {
-                dR[jj] = fmaf(dR[jj], wj[jj], dsa_i * aj[jj]);
-                dT[jj] = fmaf(dT[jj], wi, ai * dsaj[jj]);
-            }
-            if (slot == BG - 1 || t == 0) {
-                __syncthreads();
-                const int nslot = slot + 1;
-                for (int idx = threadIdx.x; idx < nslot * NOUT * D; idx += NQ * 64) {
-                    const int sl = idx / (NOUT * D);
-                    const int rem = idx - sl * NOUT * D;
-                    const int o = rem >> 6, col = rem & 63;
-                    const float4 p = ring[gh][sl][o][col];
-                    const int tt = t + (slot - sl);   // slot sl of this group is time t + (slot - sl)
-                    store1<GT>(outs[o], base0 + (int64_t)tt * strideT + col, (p.x + p.y) + (p.z + p.w));
-                }
-            }
-        }
-    }
-    float4* dst = reinterpret_cast<float4*>(dh_in + hb + (int64_t)i * D + JW * q);
-#pragma unroll
-    for (int m = 0; m < JW / 4; ++m) dst[m] = make_float4(dR[4 * m], dR[4 * m + 1], dR[4 * m + 2], dR[4 * m + 3]);
-}
-
-// ─────────────────────────────── backward (row-owned, variant 1) ───────────────────────────────
-// Lane i owns value row i; wave q owns key columns J_q (the forward's split).
-// Row quantities (dv, dsa) are in-lane partial dots; column quantities (dr,
-// dk, db, dw, da) are reduced over the 64 rows of a wave with a butterfly and
-// then over the four waves through LDS.  Same math as variant 2, different
-// summation order (the reference's v1 / v2 pair, WKV7Train.swift:99-205).
-__device__ __forceinline__ float wave_sum64(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-    return x;
-}
-
-template <int DT, int GT>
-__global__ __launch_bounds__(256) void wkv7_bwd_v1_kernel(
-    const void* __restrict__ r, const void* __restrict__ w, const void* __restrict__ k,
-    const void* __restrict__ v, const void* __restrict__ a, const void* __restrict__ b,
-    const float* __restrict__ ckpt, const float* __restrict__ sa, const float* __restrict__ dout,
-    const float* __restrict__ dhout, void* __restrict__ g_dr, void* __restrict__ g_dw,
-    void* __restrict__ g_dk, void* __restrict__ g_dv, void* __restrict__ g_da, void* __restrict__ g_db,
-    float* __restrict__ dh_in, int T, int H) {
-    __shared__ float rowpart[2][2][D][NQ];   // [parity][dv, dsa][row][wave]
-    __shared__ float colsum[NOUT][D];        // per-step column sums (dr, dk, db, dw, da) by column
-
-    const int i = threadIdx.x & 63;   // value row
-    const int q = wave_id();          // key columns J_q
-    const int bh = blockIdx.x;
-    const int bi = bh / H, hi = bh - bi * H;
-    const int64_t strideT = (int64_t)H * D;
-    const int64_t base0 = ((int64_t)bi * T * H + hi) * D;
     const int NC = T / CH;
-    const int64_t sb = (int64_t)bh * D * D + (int64_t)i * D + JW * q;
+    const void* const vec_src[6] = {r, w, k, v, a, b};
+    void* const outs[NOUT] = {g_dr, g_dw, g_dk, g_db, g_dv, g_da};
 
-    float Sr[JW], dS[JW];   // S[i, J_q], dS[i, J_q]
+    // chunk staging: thread covers 16 floats of the chunk's 8 × 16 × 64 block
+    float stg[16];
+    auto stage_load = [&](int c) {
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            const int idx = tid + 512 * m;            // (vec, step, elem)
+            const int vi = idx >> 10, st = (idx >> 6) & 15, e = idx & 63;
+            const int64_t off = base0 + (int64_t)(c * CH + st) * strideT + e;
+            if (vi < 6) {
+                switch (vi) {
+                    case 0: stg[m] = load1<DT>(r, off); break;
+                    case 1: stg[m] = load1<DT>(w, off); break;
+                    case 2: stg[m] = load1<DT>(k, off); break;
+                    case 3: stg[m] = load1<DT>(v, off); break;
+                    case 4: stg[m] = load1<DT>(a, off); break;
+                    default: stg[m] = load1<DT>(b, off); break;
+                }
+            } else {
+                stg[m] = (vi == 6 ? dout : sa)[off];
+            }
+        }
+    };
+    auto stage_store = [&](int c) {
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            const int idx = tid + 512 * m;
+            stage[c & 1][idx >> 10][(idx >> 6) & 15][idx & 63] = stg[m];
+        }
+    };
+    (void)vec_src;
+
+    float dT[BJ], dR[BJ];   // dS[J_q, i] (column copy) and dS[i, J_q] (row copy)
     if (dhout) {
 #pragma unroll
-        for (int jj = 0; jj < JW; ++jj) dS[jj] = dhout[sb + jj];
+        for (int jj = 0; jj < BJ; ++jj) dT[jj] = dhout[hb + (int64_t)(8 * q + jj) * D + i];
+        const float4* src = reinterpret_cast<const float4*>(dhout + hb + (int64_t)i * D + 8 * q);
+        const float4 f0 = src[0], f1 = src[1];
+        dR[0] = f0.x; dR[1] = f0.y; dR[2] = f0.z; dR[3] = f0.w;
+        dR[4] = f1.x; dR[5] = f1.y; dR[6] = f1.z; dR[7] = f1.w;
     } else {
 #pragma unroll
-        for (int jj = 0; jj < JW; ++jj) dS[jj] = 0.0f;
+        for (int jj = 0; jj < BJ; ++jj) { dT[jj] = 0.0f; dR[jj] = 0.0f; }
     }
-    int step = 0;
+
+    stage_load(NC - 1);
+    stage_store(NC - 1);
+    int u = 0;   // reverse step counter (parity of dsa_part, ring slot)
+
+    auto flush = [&](int uu, int tt) {   // outputs of reverse step uu (time tt)
+        if (tid < NOUT * D) {
+            const int o = tid >> 6, col = tid & 63;
+            const float4* pp = ring[uu % 3][o][col];
+            store1<GT>(outs[o], base0 + (int64_t)tt * strideT + col, sum8<SEQ>(pp[0], pp[1]));
+        }
+    };
+
     for (int c = NC - 1; c >= 0; --c) {
-        const float* ck = ckpt + (int64_t)bh * NC * D * D + (int64_t)c * D * D + (int64_t)i * D + JW * q;
+        __syncthreads();   // chunk c staged; every read of the other buffer is done
+        if (c > 0) stage_load(c - 1);
+        float (*st)[CH][D] = stage[c & 1];
+
+        float Sst[BJ];     // state before the chunk
+        if (c > 0) {
+            const float* ck = ckpt + (hb * NC) + (int64_t)(c - 1) * D * D;
 #pragma unroll
-        for (int jj = 0; jj < JW; ++jj) Sr[jj] = ck[jj];
-        for (int s = CH - 1; s >= 0; --s, ++step) {
-            const int t = c * CH + s;
-            const int64_t bt = base0 + (int64_t)t * strideT;
-            const float dyi = dout[bt + i], vi = load1<DT>(v, bt + i), sai = sa[bt + i];
-            float rj[JW], kj[JW], bj[JW], wj[JW], aj[JW];
-            load16<DT>(r, bt + JW * q, rj);
-            load16<DT>(k, bt + JW * q, kj);
-            load16<DT>(b, bt + JW * q, bj);
-            load16<DT>(w, bt + JW * q, wj);
-            load16<DT>(a, bt + JW * q, aj);
-            float pv = 0.0f, ps = 0.0f;
+            for (int jj = 0; jj < BJ; ++jj) Sst[jj] = ck[(int64_t)(8 * q + jj) * D + i];
+        } else if (h_in) {
 #pragma unroll
-            for (int jj = 0; jj < JW; ++jj) {
-                dS[jj] = fmaf(dyi, rj[jj], dS[jj]);
-                pv = fmaf(dS[jj], kj[jj], pv);
-                ps = fmaf(dS[jj], bj[jj], ps);
-            }
-            rowpart[step & 1][0][i][q] = pv;
-            rowpart[step & 1][1][i][q] = ps;
-            // column sums over the 64 rows of this wave, for the columns J_q
-            float cdr[JW], cdk[JW], cdb[JW];
+            for (int jj = 0; jj < BJ; ++jj) Sst[jj] = h_in[hb + (int64_t)(8 * q + jj) * D + i];
+        } else {
 #pragma unroll
-            for (int jj = 0; jj < JW; ++jj) {
-                cdr[jj] = wave_sum64(Sr[jj] * dyi);
-                cdk[jj] = wave_sum64(dS[jj] * vi);
-                cdb[jj] = wave_sum64(dS[jj] * sai);
-            }
-            __syncthreads();
-            const float dsa_i = (rowpart[step & 1][1][i][0] + rowpart[step & 1][1][i][1]) +
-                                (rowpart[step & 1][1][i][2] + rowpart[step & 1][1][i][3]);
-            const float dv_i = (rowpart[step & 1][0][i][0] + rowpart[step & 1][0][i][1]) +
-                               (rowpart[step & 1][0][i][2] + rowpart[step & 1][0][i][3]);
-            float cdw[JW], cda[JW];
+            for (int jj = 0; jj < BJ; ++jj) Sst[jj] = 0.0f;
+        }
+
 #pragma unroll
-            for (int jj = 0; jj < JW; ++jj) {
-                const float prev = (fmaf(-sai, bj[jj], fmaf(-vi, kj[jj], Sr[jj]))) / wj[jj];
-                Sr[jj] = prev;
-                cdw[jj] = wave_sum64(prev * dS[jj]);
-                cda[jj] = wave_sum64(prev * dsa_i);
-                dS[jj] = fmaf(dS[jj], wj[jj], dsa_i * aj[jj]);
-            }
-            if (i < JW) {
-                // lane jj of wave q publishes the sums of column 16q + jj
+        for (int half = 1; half >= 0; --half) {
+            // states of the window: hist[m] = state before step WIN·half + m
+            float hist[WIN + 1][BJ];
+            float S0[BJ];
 #pragma unroll
-                for (int jj = 0; jj < JW; ++jj) {
-                    if (i == jj) {
-                        colsum[0][JW * q + jj] = cdr[jj];
-                        colsum[1][JW * q + jj] = cdk[jj];
-                        colsum[2][JW * q + jj] = cdb[jj];
-                        colsum[3][JW * q + jj] = cdw[jj];
-                        colsum[4][JW * q + jj] = cda[jj];
-                    }
+            for (int jj = 0; jj < BJ; ++jj) S0[jj] = Sst[jj];
+            if (half == 1) {
+#pragma unroll
+                for (int s = 0; s < WIN; ++s) {
+                    float N[BJ];
+                    bwd_recompute8(S0, N, st[3][s][jl], st[7][s][jl], st[2][s][i], st[5][s][i], st[1][s][i]);
+#pragma unroll
+                    for (int jj = 0; jj < BJ; ++jj) S0[jj] = N[jj];
                 }
             }
-            __syncthreads();
-            if (q == 0) {
-                store1<GT>(g_dr, bt + i, colsum[0][i]);
-                store1<GT>(g_dk, bt + i, colsum[1][i]);
-                store1<GT>(g_db, bt + i, colsum[2][i]);
-                store1<GT>(g_dw, bt + i, colsum[3][i]);
-                store1<GT>(g_da, bt + i, colsum[4][i]);
-                store1<GT>(g_dv, bt + i, dv_i);
-            }
-            __syncthreads();
-        }
-    }
 #pragma unroll
-    for (int jj = 0; jj < JW; ++jj) dh_in[sb + jj] = dS[jj];
+            for (int jj = 0; jj < BJ; ++jj) hist[0][jj] = S0[jj];
+#pragma unroll
+            for (int m = 0; m < WIN; ++m) {
+                const int s = WIN * half + m;
+                bwd_recompute8(hist[m], hist[m + 1], st[3][s][jl], st[7][s][jl], st[2][s][i], st[5][s][i],
+                               st[1][s][i]);
+            }
+#pragma unroll
+            for (int m = WIN - 1; m >= 0; --m, ++u) {
+                const int s = WIN * half + m;
+                const int t = c * CH + s;
+                const float (&Sa)[BJ] = hist[m + 1];
+                const float (&Sp)[BJ] = hist[m];
+                const float ri = st[0][s][i], wi = st[1][s][i], ai = st[4][s][i], dyi = st[6][s][i];
+                const float R = st[0][s][jl], W = st[1][s][jl], K = st[2][s][jl], V = st[3][s][jl];
+                const float A = st[4][s][jl], B = st[5][s][jl], DY = st[6][s][jl], SA = st[7][s][jl];
+                float pdr = 0.0f, pdk = 0.0f, pdb = 0.0f, pdv = 0.0f, pds = 0.0f, pdw = 0.0f, pda = 0.0f;
+                RWKV_B1_BLOCK(0, 1, 2, 3, 0);
+                RWKV_B1_BLOCK(4, 5, 6, 7, 4);
+                if constexpr (SEQ) {
+#pragma unroll
+                    for (int jj = 0; jj < BJ; ++jj) pdw = fmaf(dT[jj], Sp[jj], pdw);
+                } else {
+                    float w0 = 0.0f, w1 = 0.0f;
+#pragma unroll
+                    for (int jj = 0; jj < BJ; jj += 2) { w0 = fmaf(dT[jj], Sp[jj], w0); w1 = fmaf(dT[jj + 1], Sp[jj + 1], w1); }
+                    pdw = w0 + w1;
+                }
+                RWKV_B2_BLOCK(0, 1, 2, 3, 0);
+                RWKV_B2_BLOCK(4, 5, 6, 7, 4);
+                const int par = u & 1, slot = u % 3;
+                reinterpret_cast<float*>(&dsa_part[par][i][0])[q] = pds;
+                reinterpret_cast<float*>(&ring[slot][0][i][0])[q] = pdr;
+                reinterpret_cast<float*>(&ring[slot][1][i][0])[q] = pdw;
+                reinterpret_cast<float*>(&ring[slot][2][i][0])[q] = pdk;
+                reinterpret_cast<float*>(&ring[slot][3][i][0])[q] = pdb;
+                reinterpret_cast<float*>(&ring[slot][4][i][0])[q] = pdv;
+                __syncthreads();
+                const float dsa_i = sum8<SEQ>(dsa_part[par][i][0], dsa_part[par][i][1]);
+                const float DS = __shfl(dsa_i, jl, 64);   // dsa of row 8q + (i & 7)
+                float nR[BJ], nT[BJ];
+                RWKV_B3_BLOCK(0, 1, 2, 3, 0);
+                RWKV_B3_BLOCK(4, 5, 6, 7, 4);
+#pragma unroll
+                for (int jj = 0; jj < BJ; ++jj) {
+                    dR[jj] = nR[jj];
+                    dT[jj] = fmaf(wi, dT[jj], nT[jj]);
+                }
+                reinterpret_cast<float*>(&ring[slot][5][i][0])[q] = pda;
+                if (u > 0) flush(u - 1, t + 1);
+            }
+        }
+        if (c > 0) stage_store(c - 1);
+    }
+    __syncthreads();
+    flush(u - 1, 0);
+    float4* dst = reinterpret_cast<float4*>(dh_in + hb + (int64_t)i * D + 8 * q);
+    dst[0] = make_float4(dR[0], dR[1], dR[2], dR[3]);
+    dst[1] = make_float4(dR[4], dR[5], dR[6], dR[7]);
 }
 
 // ─────────────────────────────── tmix tail ───────────────────────────────
 __device__ __forceinline__ float wave_total(float x) {
-    x = wave_sum64(x);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
     return __shfl(x, 0, 64);   // one lane's association for everybody
 }
 
@@ -485,7 +523,7 @@ template <bool SA, bool CK>
 rwkv_status launch_fwd(const void* r, const void* w, const void* k, const void* v, const void* a, const void* b,
                        rwkv_dtype dt, const float* h_in, float* out, float* h_out, float* sa_out, float* ck,
                        int64_t B, int64_t T, int64_t H, void* stream) {
-    dim3 grid((unsigned)(B * H)), block(256);
+    dim3 grid((unsigned)(B * H * 4)), block(64);   // one wave per 16 value rows
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     switch (dt) {
         case RWKV_F32:
@@ -507,7 +545,7 @@ rwkv_status check_wkv_common(const void* r, const void* w, const void* k, const 
     RWKV_REQUIRE(rwkv::dtype_ok(dt), RWKV_E_DTYPE, "wkv7: input dtype code %d not in {f32, bf16, f16}", dt);
     RWKV_REQUIRE(B >= 1 && H >= 1, RWKV_E_SHAPE, "wkv7: B (%lld) and H (%lld) must be >= 1", (long long)B, (long long)H);
     RWKV_REQUIRE(T >= 1, RWKV_E_SHAPE, "wkv7: T (%lld) must be >= 1", (long long)T);
-    RWKV_REQUIRE(B * H <= INT32_MAX && T <= INT32_MAX && B * T * H * 64 <= (int64_t)1 << 46, RWKV_E_SHAPE,
+    RWKV_REQUIRE(B * H * 4 <= INT32_MAX && T <= INT32_MAX && B * T * H * 64 <= (int64_t)1 << 46, RWKV_E_SHAPE,
                  "wkv7: B·T·H too large");
     return RWKV_OK;
 }
@@ -566,9 +604,9 @@ rwkv_status rwkv_wkv7_step(const void* r, const void* w, const void* k, const vo
 }
 
 rwkv_status rwkv_wkv7_train_bwd(const void* r, const void* w, const void* k, const void* v, const void* a,
-                                const void* b, rwkv_dtype in_dt, const float* h_ckpt, const float* sa,
-                                const float* d_out, const float* d_h_out, void* dr, void* dw, void* dk,
-                                void* dv, void* da, void* db, rwkv_dtype g_dt, float* dh_in, int64_t B,
+                                const void* b, rwkv_dtype in_dt, const float* h_in, const float* h_ckpt,
+                                const float* sa, const float* d_out, const float* d_h_out, void* dr, void* dw,
+                                void* dk, void* dv, void* da, void* db, rwkv_dtype g_dt, float* dh_in, int64_t B,
                                 int64_t T, int64_t H, int variant, void* stream) {
     rwkv_status s = check_wkv_common(r, w, k, v, a, b, in_dt, B, T, H);
     if (s != RWKV_OK) return s;
@@ -577,27 +615,27 @@ rwkv_status rwkv_wkv7_train_bwd(const void* r, const void* w, const void* k, con
                  "wkv7_train_bwd: checkpoints, sa, d_out, gradients and dh_in must be non-null");
     RWKV_REQUIRE(rwkv::dtype_ok(g_dt), RWKV_E_DTYPE, "wkv7_train_bwd: gradient dtype code %d not in {f32, bf16, f16}", g_dt);
     RWKV_REQUIRE(variant == 1 || variant == 2, RWKV_E_UNSUPPORTED, "wkv7_train_bwd: variant %d not in {1, 2}", variant);
-    dim3 grid((unsigned)(B * H)), block(256);
+    dim3 grid((unsigned)(B * H)), block(512);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define RWKV_BWD_LAUNCH(KER, DT, GT)                                                                          \
-    hipLaunchKernelGGL((KER<DT, GT>), grid, block, 0, st, r, w, k, v, a, b, h_ckpt, sa, d_out, d_h_out, dr, dw, \
-                       dk, dv, da, db, dh_in, (int)T, (int)H)
-#define RWKV_BWD_GT(KER, DT)                                 \
-    switch (g_dt) {                                          \
-        case RWKV_F32: RWKV_BWD_LAUNCH(KER, DT, RWKV_F32); break;   \
-        case RWKV_BF16: RWKV_BWD_LAUNCH(KER, DT, RWKV_BF16); break; \
-        case RWKV_F16: RWKV_BWD_LAUNCH(KER, DT, RWKV_F16); break;   \
+#define RWKV_BWD_LAUNCH(DT, GT, SEQ)                                                                          \
+    hipLaunchKernelGGL((wkv7_bwd_kernel<DT, GT, SEQ>), grid, block, 0, st, r, w, k, v, a, b, h_in, h_ckpt, sa, \
+                       d_out, d_h_out, dr, dw, dk, dv, da, db, dh_in, (int)T, (int)H)
+#define RWKV_BWD_GT(DT, SEQ)                                         \
+    switch (g_dt) {                                                  \
+        case RWKV_F32: RWKV_BWD_LAUNCH(DT, RWKV_F32, SEQ); break;   \
+        case RWKV_BF16: RWKV_BWD_LAUNCH(DT, RWKV_BF16, SEQ); break; \
+        case RWKV_F16: RWKV_BWD_LAUNCH(DT, RWKV_F16, SEQ); break;   \
     }
-#define RWKV_BWD_DT(KER)                                 \
-    switch (in_dt) {                                     \
-        case RWKV_F32: RWKV_BWD_GT(KER, RWKV_F32); break;   \
-        case RWKV_BF16: RWKV_BWD_GT(KER, RWKV_BF16); break; \
-        case RWKV_F16: RWKV_BWD_GT(KER, RWKV_F16); break;   \
+#define RWKV_BWD_DT(SEQ)                                  \
+    switch (in_dt) {                                      \
+        case RWKV_F32: RWKV_BWD_GT(RWKV_F32, SEQ); break;   \
+        case RWKV_BF16: RWKV_BWD_GT(RWKV_BF16, SEQ); break; \
+        case RWKV_F16: RWKV_BWD_GT(RWKV_F16, SEQ); break;   \
     }
     if (variant == 2) {
-        RWKV_BWD_DT(wkv7_bwd_v2_kernel)
+        RWKV_BWD_DT(false)
     } else {
-        RWKV_BWD_DT(wkv7_bwd_v1_kernel)
+        RWKV_BWD_DT(true)
     }
 #undef RWKV_BWD_DT
 #undef RWKV_BWD_GT

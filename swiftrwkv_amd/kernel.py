@@ -202,7 +202,7 @@ class _WKV7Train(torch.autograd.Function):
         grads = [torch.empty((B, T, H, D), dtype=gdt, device=dev) for _ in range(6)]
         dh_in = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
         variant = 2 if wkv7_backward_v2 else 1
-        _lib.call("rwkv_wkv7_train_bwd", *[_ptr(x) for x in ins], ctx.dt, _ptr(ck), _ptr(sa), _ptr(d_out),
+        _lib.call("rwkv_wkv7_train_bwd", *[_ptr(x) for x in ins], ctx.dt, _ptr(h), _ptr(ck), _ptr(sa), _ptr(d_out),
                   _ptr(dho), *[_ptr(g) for g in grads], _DT[gdt], _ptr(dh_in), B, T, H, variant, _stream(r))
         grads = [g.to(t) for g, t in zip(grads, ctx.dtypes)]
         dh = None if ctx.h0_dtype is None else dh_in.to(ctx.h0_dtype)

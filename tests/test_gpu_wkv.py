@@ -348,5 +348,5 @@ def test_preconditions_raise():
     with pytest.raises(ValueError):
         K.wkv7_sequence_forward(*y)
     with pytest.raises(_lib.RwkvHipError):
-        _lib.call("rwkv_wkv7_train_bwd", *[z.data_ptr() for z in x], 0, x[0].data_ptr(), x[0].data_ptr(),
+        _lib.call("rwkv_wkv7_train_bwd", *[z.data_ptr() for z in x], 0, None, x[0].data_ptr(), x[0].data_ptr(),
                   x[0].data_ptr(), None, *[z.data_ptr() for z in x], 0, x[0].data_ptr(), 1, 16, 1, 7, None)

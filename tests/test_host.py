@@ -48,7 +48,7 @@ def test_status_strings_and_errors():
     assert st == 1
     st = lib.rwkv_wkv7_seq_fwd(*([dummy] * 6), 7, None, dummy, dummy, 1, 1, 1, None)
     assert st == 2
-    st = lib.rwkv_wkv7_train_bwd(*([dummy] * 6), 0, dummy, dummy, dummy, None, *([dummy] * 6), 0, dummy, 1, 16, 1, 3, None)
+    st = lib.rwkv_wkv7_train_bwd(*([dummy] * 6), 0, None, dummy, dummy, dummy, None, *([dummy] * 6), 0, dummy, 1, 16, 1, 3, None)
     assert st == 3
     st = lib.rwkv_sb6_gemv(dummy, 1, dummy, dummy, dummy, dummy, 16, 200, 0, None)
     assert st == 1
