@@ -46,7 +46,25 @@ def parse():
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-wkv", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--mode", choices=["bench", "kernels"], default="bench",
+                   help="kernels: run each dominant kernel alone (for rocprofv3 counter passes)")
     return p.parse_args()
+
+
+def kernel_ms(launch, stream=None) -> float:
+    """Duration of the single library kernel `launch()` enqueues, timed by the
+    kernel's own start / stop timestamps (rwkv_time_next_launch)."""
+    import torch
+    from swiftrwkv_amd import _lib
+
+    stream = stream or torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    e1.record(stream)
+    _lib.call("rwkv_time_next_launch", e0.cuda_event, e1.cuda_event)
+    launch()
+    e1.synchronize()
+    return e0.elapsed_time(e1)
 
 
 # ───────────────────────────── decode model ─────────────────────────────
@@ -206,13 +224,7 @@ def bench_head_gemv(model, dev, reps=60):
     for i in range(10):
         launch(i % copies)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for i in range(reps):
-        evs[i][0].record(stream)
-        launch(i % copies)
-        evs[i][1].record(stream)
-    torch.cuda.synchronize()
-    durs = sorted(a.elapsed_time(b) for a, b in evs)
+    durs = sorted(kernel_ms(lambda: launch(i % copies), stream) for i in range(reps))
     avg_ms = sum(durs) / len(durs)
     nbytes = qblk.nbytes + qsqm.nbytes + ddm.nbytes + 4 * (IN + OUT)
     return nbytes, avg_ms, durs[len(durs) // 2]
@@ -229,13 +241,7 @@ def bench_wkv(dev, reps=5):
     for _ in range(3):
         K.wkv7_sequence_forward(*x)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps * 4):
-        K.wkv7_sequence_forward(*x)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / (reps * 4)
+    ms = sum(kernel_ms(lambda: K.wkv7_sequence_forward(*x)) for _ in range(reps * 4)) / (reps * 4)
     res["wkv7_fwd_B1_T1024_H12_fp32"] = {"ms": ms, "tok_s": 1024 / (ms * 1e-3),
                                          "valu_roofline_frac": (1024 * 12 * 9 * 64 * 64 / (ms * 1e-3)) / (VALU_PEAK_TFLOPS * 1e12)}
     del x
@@ -262,17 +268,12 @@ def bench_wkv(dev, reps=5):
     out, h_out, sa, ck = fwd()
     bwd(sa, ck)
     torch.cuda.synchronize()
-    ef = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     tf = tb = 0.0
+    res_fwd = {}
     for _ in range(reps):
-        ef[0].record()
-        out, h_out, sa, ck = fwd()
-        ef[1].record()
-        bwd(sa, ck)
-        ef[2].record()
-        torch.cuda.synchronize()
-        tf += ef[0].elapsed_time(ef[1])
-        tb += ef[1].elapsed_time(ef[2])
+        tf += kernel_ms(lambda: res_fwd.update(o=fwd()))
+        out, h_out, sa, ck = res_fwd["o"]
+        tb += kernel_ms(lambda: bwd(sa, ck))
     tf /= reps
     tb /= reps
     th = B * T * H
@@ -334,6 +335,39 @@ def cpu_wkv_baseline():
             "sample": f"WKV-7 forward B1 T1024 H12 fp32 x{n}"}
 
 
+def profile_kernels(dev, reps=20):
+    """Each dominant kernel alone, plus a plain 256 MiB device copy whose
+    FETCH_SIZE / WRITE_SIZE calibrate the counters (2 × 256 MiB of traffic)."""
+    import numpy as np
+    import torch
+    from swiftrwkv_amd import _lib, kernel as K, synthetic as syn
+
+    src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    model = DecodeModel(syn.X070_0B1, 6, dev, nthreads=min(16, os.cpu_count() or 1))
+    bench_head_gemv(model, dev, reps=reps)
+    x = [torch.from_numpy(z).to(dev) for z in syn.wkv_inputs_config0(1, 1024, 12, seed=0)]
+    for _ in range(reps):
+        K.wkv7_sequence_forward(*x)
+    B, T, H = 8, 4096, 32
+    xs = syn.wkv_inputs_config0(B, T, H, seed=3)
+    ins = [torch.from_numpy(z).to(dev).to(torch.bfloat16) for z in xs]
+    ins_p, dt = K._prep(ins)
+    dy = torch.randn((B, T, H, 64), device=dev)
+    grads = [torch.empty((B, T, H, 64), dtype=torch.bfloat16, device=dev) for _ in range(6)]
+    dh_in = torch.empty((B, H, 64, 64), device=dev)
+    for _ in range(3):
+        out, h_out, sa, ck = K._train_forward(ins_p, dt, None)
+        _lib.call("rwkv_wkv7_train_bwd", *[z.data_ptr() for z in ins_p], dt, None, ck.data_ptr(), sa.data_ptr(),
+                  dy.data_ptr(), None, *[g.data_ptr() for g in grads], _lib.BF16, dh_in.data_ptr(), B, T, H, 2,
+                  torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    log("kernels done")
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -346,6 +380,9 @@ def main():
     _lib.lib()
     dev = torch.device("cuda:0")
     log(f"device {torch.cuda.get_device_name(0)}")
+    if args.mode == "kernels":
+        profile_kernels(dev)
+        return
     model, step, wall, gpu_ms = bench_decode(args, dev)
     nbytes, head_avg_ms, head_med_ms = bench_head_gemv(model, dev)
     achieved = nbytes / (head_avg_ms * 1e-3) / 1e9

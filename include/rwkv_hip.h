@@ -203,6 +203,15 @@ rwkv_status rwkvq_entry(const rwkvq_file* f, int64_t i, const char** name, const
 /* "__metadata__" string value for `key`, or NULL. */
 const char* rwkvq_metadata(const rwkvq_file* f, const char* key);
 
+/* ───────────────────────────── measurement ───────────────────────────── */
+
+/* Measurement hook, no counterpart in the reference (its benches time whole
+ * MLX evals).  Arms the NEXT kernel launch made by this library on the
+ * calling thread to record its own start / stop timestamps into the given
+ * hipEvent_t pair (hipExtLaunchKernelGGL), so elapsed time between them is
+ * the kernel alone.  NULL, NULL disarms. */
+rwkv_status rwkv_time_next_launch(void* start_event, void* stop_event);
+
 /* ───────────────────────────── counters ───────────────────────────── */
 
 typedef struct {

@@ -72,6 +72,7 @@ _SIGS = {
                         ctypes.POINTER(I), ctypes.POINTER(ctypes.POINTER(L)), ctypes.POINTER(P),
                         ctypes.POINTER(L)]),
     "rwkvq_metadata": (ctypes.c_char_p, [P, ctypes.c_char_p]),
+    "rwkv_time_next_launch": (I, [P, P]),
     "rwkv_get_counters": (None, [ctypes.POINTER(Counters)]),
     "rwkv_reset_counters": (None, []),
 }

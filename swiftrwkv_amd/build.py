@@ -22,7 +22,7 @@ HOST_SOURCES = ["host.cpp"]
 
 # Packed-FP32 VALU ops are disabled for every device compile.
 HIP_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=fast",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-ffp-contract=fast",
     # code object v5: loadable by the HIP 7.0 runtime torch bundles and by ROCm 7.2
     "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

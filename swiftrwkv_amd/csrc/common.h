@@ -22,6 +22,14 @@ struct Counters {
 };
 Counters& counters();
 
+// Events armed by rwkv_time_next_launch() for the calling thread; taking them
+// disarms the hook.
+struct TimingEvents {
+    void* start;
+    void* stop;
+};
+TimingEvents take_timing();
+
 inline bool dtype_ok(int dt) { return dt == RWKV_F32 || dt == RWKV_BF16 || dt == RWKV_F16; }
 inline int64_t dtype_size(int dt) { return dt == RWKV_F32 ? 4 : 2; }
 

@@ -38,6 +38,14 @@ Counters& counters() {
     return c;
 }
 
+static thread_local TimingEvents g_timing{nullptr, nullptr};
+
+TimingEvents take_timing() {
+    const TimingEvents t = g_timing;
+    g_timing = {nullptr, nullptr};
+    return t;
+}
+
 // IEEE binary16 with round-to-nearest-even (host copy; used by the encoders).
 static uint16_t f32_to_f16(float f) {
     uint32_t x;
@@ -121,6 +129,14 @@ const char* rwkv_status_string(rwkv_status s) {
 }
 
 const char* rwkv_last_error(void) { return rwkv::g_last_error.c_str(); }
+
+rwkv_status rwkv_time_next_launch(void* start_event, void* stop_event) {
+    RWKV_REQUIRE((start_event == nullptr) == (stop_event == nullptr), RWKV_E_NULL,
+                 "time_next_launch: give both events or neither");
+    rwkv::g_timing = {start_event, stop_event};
+    rwkv::clear_error();
+    return RWKV_OK;
+}
 
 void rwkv_get_counters(rwkv_counters* out) {
     if (!out) return;

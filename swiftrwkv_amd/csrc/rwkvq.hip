@@ -29,7 +29,7 @@
 
 #include <hip/hip_runtime.h>
 
-#include "common.h"
+#include "launch.h"
 
 namespace {
 
@@ -398,7 +398,7 @@ rwkv_status rwkv_sb6_dequant(const uint8_t* qblk, const uint8_t* qsqm, const uin
     RWKV_REQUIRE(total / 256 < INT32_MAX, RWKV_E_SHAPE, "sb6_dequant: tensor too large");
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define RWKV_DQ(XB, DT) hipLaunchKernelGGL((sb6_dequant_kernel<XB, DT>), grid, block, 0, st, qblk, qsqm, ddm, out, OUT, IN)
+#define RWKV_DQ(XB, DT) rwkv::launch(sb6_dequant_kernel<XB, DT>, grid, block, st, qblk, qsqm, ddm, out, OUT, IN)
 #define RWKV_DQ_DT(XB)                                  \
     switch (out_dt) {                                   \
         case RWKV_F32: RWKV_DQ(XB, RWKV_F32); break;    \
@@ -428,7 +428,7 @@ rwkv_status rwkv_sym_dequant(const uint8_t* qblk, const uint8_t* qs, const uint1
     RWKV_REQUIRE(total / 256 < INT32_MAX, RWKV_E_SHAPE, "sym_dequant: tensor too large");
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define RWKV_DQ(BITS, DT) hipLaunchKernelGGL((sym_dequant_kernel<BITS, DT>), grid, block, 0, st, qblk, qs, d, out, OUT, IN)
+#define RWKV_DQ(BITS, DT) rwkv::launch(sym_dequant_kernel<BITS, DT>, grid, block, st, qblk, qs, d, out, OUT, IN)
 #define RWKV_DQ_DT(BITS)                                  \
     switch (out_dt) {                                     \
         case RWKV_F32: RWKV_DQ(BITS, RWKV_F32); break;    \
@@ -468,7 +468,7 @@ rwkv_status rwkv_sb6_gemv(const float* x, int64_t N, const uint8_t* qblk, const 
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int nt = pick_nt(N);
 #define RWKV_GV(XB, RL, NT) \
-    hipLaunchKernelGGL((sb6_gemv_kernel<XB, RL, NT>), grid, block, 0, st, x, (int)N, qblk, qsqm, ddm, y, (int)OUT, (int)IN, geo)
+    rwkv::launch(sb6_gemv_kernel<XB, RL, NT>, grid, block, st, x, (int)N, qblk, qsqm, ddm, y, (int)OUT, (int)IN, geo)
 #define RWKV_GV_NT(XB, RL)                  \
     if (nt == 4) RWKV_GV(XB, RL, 4);        \
     else if (nt == 2) RWKV_GV(XB, RL, 2);   \
@@ -508,7 +508,7 @@ rwkv_status rwkv_sym_gemv(const float* x, int64_t N, const uint8_t* qblk, const 
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int nt = pick_nt(N);
 #define RWKV_GV(BITS, RL, NT)                                                                                   \
-    hipLaunchKernelGGL((sym_gemv_kernel<BITS, RL, NT>), grid, block, 0, st, x, (int)N, qblk, qs, d, y, (int)OUT, \
+    rwkv::launch(sym_gemv_kernel<BITS, RL, NT>, grid, block, st, x, (int)N, qblk, qs, d, y, (int)OUT, \
                        (int)IN, (int)out_per, geo)
 #define RWKV_GV_NT(BITS, RL)                  \
     if (nt == 4) RWKV_GV(BITS, RL, 4);        \

@@ -38,7 +38,10 @@
 
 #include <hip/hip_runtime.h>
 
-#include "common.h"
+#include <type_traits>
+#include <utility>
+
+#include "launch.h"
 
 namespace {
 
@@ -135,23 +138,47 @@ __device__ __forceinline__ void fwd_dot16(const float (&S)[16], float A, float& 
 
 // ─────────────────────────────── forward ───────────────────────────────
 // Grid: 4 workgroups of one wave per (b, h); workgroup 4·(b·H + h) + blk owns
-// value rows 16·blk .. 16·blk + 15.
+// value rows 16·blk .. 16·blk + 15.  Offsets inside one (b, h) sequence are
+// 32-bit (the host checks T·H·64·4 < 2^32), so loads use an SGPR base.
+template <int DT>
+struct FwdIn {
+    using E = typename std::conditional<DT == RWKV_F32, float, uint16_t>::type;
+    const E* a;
+    const E* w;
+    const E* k;
+    const E* b;
+    const E* r;
+    const E* v;
+    __device__ __forceinline__ static float cvt(E x) {
+        if constexpr (DT == RWKV_F32) return x;
+        else if constexpr (DT == RWKV_BF16) return __uint_as_float((uint32_t)x << 16);
+        else return (float)__builtin_bit_cast(_Float16, x);
+    }
+};
+
 template <int DT, bool EMIT_SA, bool EMIT_CK>
 __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
     const void* __restrict__ r, const void* __restrict__ w, const void* __restrict__ k,
     const void* __restrict__ v, const void* __restrict__ a, const void* __restrict__ b,
     const float* __restrict__ h_in, float* __restrict__ out, float* __restrict__ h_out,
     float* __restrict__ sa_out, float* __restrict__ ckpt, int T, int H) {
+    using In = FwdIn<DT>;
+    using E = typename In::E;
     const int l = threadIdx.x;
     const int ri = l & 15, g = l >> 4;
     const int bh = blockIdx.x >> 2, blk = blockIdx.x & 3;
     const int bi = bh / H, hi = bh - bi * H;
     const int row = 16 * blk + ri;
-    const int vidx = 16 * g + ri;   // step-vector element this lane broadcasts
-    const int64_t strideT = (int64_t)H * D;
+    const uint32_t vidx = 16 * g + ri;   // step-vector element this lane broadcasts
+    const uint32_t strideT = (uint32_t)H * D;
     const int64_t base0 = ((int64_t)bi * T * H + hi) * D;
     const int64_t sbase = (int64_t)bh * D * D + (int64_t)row * D + 16 * g;
     const int NC = T / CH;
+    In in{reinterpret_cast<const E*>(a) + base0, reinterpret_cast<const E*>(w) + base0,
+          reinterpret_cast<const E*>(k) + base0, reinterpret_cast<const E*>(b) + base0,
+          reinterpret_cast<const E*>(r) + base0, reinterpret_cast<const E*>(v) + base0};
+    float* const outp = out + base0;
+    float* const sap = EMIT_SA ? sa_out + base0 : nullptr;
 
     float S[2][16];
     if (h_in) {
@@ -166,57 +193,62 @@ __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
         for (int c = 0; c < 16; ++c) S[0][c] = 0.0f;
     }
 
-    // ring slot: a, w, k, b, r (broadcast sources), v (own row)
-    float ring[CH][6];
-    auto fetch = [&](float (&slot)[6], int t) {
-        const int64_t bt = base0 + (int64_t)min(t, T - 1) * strideT;
-        slot[0] = load1<DT>(a, bt + vidx);
-        slot[1] = load1<DT>(w, bt + vidx);
-        slot[2] = load1<DT>(k, bt + vidx);
-        slot[3] = load1<DT>(b, bt + vidx);
-        slot[4] = load1<DT>(r, bt + vidx);
-        slot[5] = load1<DT>(v, bt + row);
+    // ring slot: a, w, k, b, r (broadcast sources), v (own row), as raw elements
+    E ring[CH][6];
+    auto fetch = [&](E (&slot)[6], int t) {
+        const uint32_t o = (uint32_t)min(t, T - 1) * strideT;
+        slot[0] = in.a[o + vidx];
+        slot[1] = in.w[o + vidx];
+        slot[2] = in.k[o + vidx];
+        slot[3] = in.b[o + vidx];
+        slot[4] = in.r[o + vidx];
+        slot[5] = in.v[o + row];
     };
 #pragma unroll
     for (int s = 0; s < 8; ++s) fetch(ring[s], s);
 
     float p = 0.0f;
-    fwd_dot16(S[0], ring[0][0], p);
+    fwd_dot16(S[0], In::cvt(ring[0][0]), p);
 
-    const int nchunks = (T + CH - 1) / CH;
-    int last = 0;
-    for (int c = 0; c < nchunks; ++c) {
-        const int t0 = c * CH;
-        const int n = min(CH, T - t0);
-        last = n;
+    // one step at chunk position s (compile-time) and time t
+    auto step = [&](auto sc, int t, int c) {
+        constexpr int s = decltype(sc)::value;
+        fetch(ring[(s + 8) & (CH - 1)], t + 8);
+        const float sa = rowsum4(p);
+        float y = 0.0f;
+        p = 0.0f;
+        const E* sl = ring[s];
+        fwd_update16(S[s & 1], S[(s + 1) & 1], In::cvt(sl[2]), In::cvt(sl[3]), In::cvt(sl[1]), In::cvt(sl[4]),
+                     In::cvt(ring[(s + 1) & (CH - 1)][0]), In::cvt(sl[5]), sa, y, p);
+        y = rowsum4(y);
+        const uint32_t o = (uint32_t)t * strideT + row;
+        outp[o] = y;   // the four lanes of a row store the same bits
+        if constexpr (EMIT_SA) sap[o] = sa;
+        if constexpr (EMIT_CK && s == CH - 1) {
+            float4* dst = reinterpret_cast<float4*>(ckpt + ((int64_t)bh * NC + c) * D * D + (int64_t)row * D + 16 * g);
 #pragma unroll
-        for (int s = 0; s < CH; ++s) {
-            if (s < n) {
-                const int t = t0 + s;
-                fetch(ring[(s + 8) & (CH - 1)], t + 8);
-                const float sa = rowsum4(p);
-                float y = 0.0f;
-                p = 0.0f;
-                const float* sl = ring[s];
-                fwd_update16(S[s & 1], S[(s + 1) & 1], sl[2], sl[3], sl[1], sl[4], ring[(s + 1) & (CH - 1)][0],
-                             sl[5], sa, y, p);
-                y = rowsum4(y);
-                const int64_t bt = base0 + (int64_t)t * strideT;
-                if (g == 0) {
-                    out[bt + row] = y;
-                    if (EMIT_SA) sa_out[bt + row] = sa;
-                }
-                if (EMIT_CK && s == CH - 1) {
-                    float4* dst = reinterpret_cast<float4*>(ckpt + ((int64_t)bh * NC + c) * D * D + (int64_t)row * D + 16 * g);
-#pragma unroll
-                    for (int m = 0; m < 4; ++m)
-                        dst[m] = make_float4(S[0][4 * m], S[0][4 * m + 1], S[0][4 * m + 2], S[0][4 * m + 3]);
-                }
-            }
+            for (int m = 0; m < 4; ++m)
+                dst[m] = make_float4(S[0][4 * m], S[0][4 * m + 1], S[0][4 * m + 2], S[0][4 * m + 3]);
         }
-    }
+    };
+    auto body = [&](int c, int n) {
+        const int t0 = c * CH;
+        [&]<int... s>(std::integer_sequence<int, s...>) {
+            ((n > s ? step(std::integral_constant<int, s>{}, t0 + s, c) : void()), ...);
+        }(std::make_integer_sequence<int, CH>{});
+    };
+    auto body_full = [&](int c) {
+        const int t0 = c * CH;
+        [&]<int... s>(std::integer_sequence<int, s...>) {
+            (step(std::integral_constant<int, s>{}, t0 + s, c), ...);
+        }(std::make_integer_sequence<int, CH>{});
+    };
+    for (int c = 0; c < NC; ++c) body_full(c);   // branch-free: exact wait counts
+    const int tail = T - NC * CH;
+    if (tail) body(NC, tail);
+
     float4* dst = reinterpret_cast<float4*>(h_out + sbase);
-    if (last & 1) {
+    if (tail & 1) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) dst[m] = make_float4(S[1][4 * m], S[1][4 * m + 1], S[1][4 * m + 2], S[1][4 * m + 3]);
     } else {
@@ -527,13 +559,13 @@ rwkv_status launch_fwd(const void* r, const void* w, const void* k, const void* 
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     switch (dt) {
         case RWKV_F32:
-            hipLaunchKernelGGL((wkv7_fwd_kernel<RWKV_F32, SA, CK>), grid, block, 0, st, r, w, k, v, a, b, h_in, out, h_out, sa_out, ck, (int)T, (int)H);
+            rwkv::launch(wkv7_fwd_kernel<RWKV_F32, SA, CK>, grid, block, st, r, w, k, v, a, b, h_in, out, h_out, sa_out, ck, (int)T, (int)H);
             break;
         case RWKV_BF16:
-            hipLaunchKernelGGL((wkv7_fwd_kernel<RWKV_BF16, SA, CK>), grid, block, 0, st, r, w, k, v, a, b, h_in, out, h_out, sa_out, ck, (int)T, (int)H);
+            rwkv::launch(wkv7_fwd_kernel<RWKV_BF16, SA, CK>, grid, block, st, r, w, k, v, a, b, h_in, out, h_out, sa_out, ck, (int)T, (int)H);
             break;
         case RWKV_F16:
-            hipLaunchKernelGGL((wkv7_fwd_kernel<RWKV_F16, SA, CK>), grid, block, 0, st, r, w, k, v, a, b, h_in, out, h_out, sa_out, ck, (int)T, (int)H);
+            rwkv::launch(wkv7_fwd_kernel<RWKV_F16, SA, CK>, grid, block, st, r, w, k, v, a, b, h_in, out, h_out, sa_out, ck, (int)T, (int)H);
             break;
     }
     return launch_status("wkv7 forward launch");
@@ -545,8 +577,8 @@ rwkv_status check_wkv_common(const void* r, const void* w, const void* k, const 
     RWKV_REQUIRE(rwkv::dtype_ok(dt), RWKV_E_DTYPE, "wkv7: input dtype code %d not in {f32, bf16, f16}", dt);
     RWKV_REQUIRE(B >= 1 && H >= 1, RWKV_E_SHAPE, "wkv7: B (%lld) and H (%lld) must be >= 1", (long long)B, (long long)H);
     RWKV_REQUIRE(T >= 1, RWKV_E_SHAPE, "wkv7: T (%lld) must be >= 1", (long long)T);
-    RWKV_REQUIRE(B * H * 4 <= INT32_MAX && T <= INT32_MAX && B * T * H * 64 <= (int64_t)1 << 46, RWKV_E_SHAPE,
-                 "wkv7: B·T·H too large");
+    RWKV_REQUIRE(B * H * 4 <= INT32_MAX && T * H * 64 * 4 < ((int64_t)1 << 32) && B * T * H * 64 <= (int64_t)1 << 46,
+                 RWKV_E_SHAPE, "wkv7: B·T·H too large (one sequence must stay under 2^32 bytes)");
     return RWKV_OK;
 }
 
@@ -618,7 +650,7 @@ rwkv_status rwkv_wkv7_train_bwd(const void* r, const void* w, const void* k, con
     dim3 grid((unsigned)(B * H)), block(512);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 #define RWKV_BWD_LAUNCH(DT, GT, SEQ)                                                                          \
-    hipLaunchKernelGGL((wkv7_bwd_kernel<DT, GT, SEQ>), grid, block, 0, st, r, w, k, v, a, b, h_in, h_ckpt, sa, \
+    rwkv::launch(wkv7_bwd_kernel<DT, GT, SEQ>, grid, block, st, r, w, k, v, a, b, h_in, h_ckpt, sa, \
                        d_out, d_h_out, dr, dw, dk, dv, da, db, dh_in, (int)T, (int)H)
 #define RWKV_BWD_GT(DT, SEQ)                                         \
     switch (g_dt) {                                                  \
@@ -653,7 +685,7 @@ rwkv_status rwkv_wkv_tail(const float* wkv, const float* r, const float* k, cons
     RWKV_REQUIRE(wkv && r && k && v && rk && lnw && lnb && g && out, RWKV_E_NULL, "wkv_tail: null buffer");
     RWKV_REQUIRE(rwkv_wkv_tail_applies(S), RWKV_E_SHAPE, "wkv_tail: S=%lld is not a multiple of 32", (long long)S);
     RWKV_REQUIRE(N >= 1 && H >= 1 && N * H <= INT32_MAX && S <= 1 << 20, RWKV_E_SHAPE, "wkv_tail: bad N/H/S");
-    hipLaunchKernelGGL(wkv_tail_kernel, dim3((unsigned)(N * H)), dim3(64), 0, reinterpret_cast<hipStream_t>(stream),
+    rwkv::launch(wkv_tail_kernel, dim3((unsigned)(N * H)), dim3(64), reinterpret_cast<hipStream_t>(stream),
                        wkv, r, k, v, rk, lnw, lnb, g, out, (int)H, (int)S, eps);
     rwkv_status s = launch_status("wkv_tail launch");
     if (s == RWKV_OK) rwkv::counters().tail++;
