@@ -72,7 +72,7 @@ def kernel_ms(launch, stream=None) -> float:
 class DecodeModel:
     """Packed weights of all projections (K3 layout on the device), per copy."""
 
-    def __init__(self, shape, copies, dev, nthreads):
+    def __init__(self, shape, copies, dev, nthreads, only=None):
         import numpy as np
         import torch
         from swiftrwkv_amd import quant as Q
@@ -83,6 +83,8 @@ class DecodeModel:
         self.bytes_per_token = 0
         t0 = time.time()
         for idx, (key, OUT, IN) in enumerate(shape.projections()):
+            if only is not None and key not in only:
+                continue
             rng = np.random.default_rng(1000 + idx)
             w = (rng.standard_normal((OUT, IN), dtype=np.float32) * np.float32(0.02))
             disk = Q.encode_sb6(w, 4, nthreads)
@@ -347,7 +349,7 @@ def profile_kernels(dev, reps=20):
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    model = DecodeModel(syn.X070_0B1, 6, dev, nthreads=min(16, os.cpu_count() or 1))
+    model = DecodeModel(syn.X070_0B1, 6, dev, nthreads=min(16, os.cpu_count() or 1), only={"head.weight"})
     bench_head_gemv(model, dev, reps=reps)
     x = [torch.from_numpy(z).to(dev) for z in syn.wkv_inputs_config0(1, 1024, 12, seed=0)]
     for _ in range(reps):

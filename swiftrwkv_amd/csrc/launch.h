@@ -11,15 +11,21 @@
 
 namespace rwkv {
 
+// `lds` bytes of dynamic shared memory.
 template <typename Kernel, typename... Args>
-inline void launch(Kernel kernel, dim3 grid, dim3 block, hipStream_t stream, Args... args) {
+inline void launch_lds(Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
     const TimingEvents ev = take_timing();
     if (ev.start && ev.stop) {
-        hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, reinterpret_cast<hipEvent_t>(ev.start),
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, reinterpret_cast<hipEvent_t>(ev.start),
                               reinterpret_cast<hipEvent_t>(ev.stop), 0, args...);
     } else {
-        hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
     }
+}
+
+template <typename Kernel, typename... Args>
+inline void launch(Kernel kernel, dim3 grid, dim3 block, hipStream_t stream, Args... args) {
+    launch_lds(kernel, grid, block, 0, stream, args...);
 }
 
 }  // namespace rwkv

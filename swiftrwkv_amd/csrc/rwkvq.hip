@@ -12,22 +12,28 @@
 //     ‖ qh ‖ qh2, codes stored +32;  qs int8 [OUT, IN/16];  d fp16 [OUT, IN/256]
 //     w = (q [−32])·half(qs·d) (RwkvqDequant.swift:350-388)
 //
-// GEMV (decode) mapping.  A row of IN columns is a sequence of NU "units"
-// (sb6: one 32-column block; sym: 32 columns = 2 blocks).  G lanes (the largest
-// power of two ≤ 64 dividing NU) cover one row; each lane owns the units
-// g, g+G, ... of that row for every row it processes, so its x slice (32
-// floats per unit) is loaded once into registers and reused across the RL
-// consecutive rows assigned to it ("x-stationary").  Weight bytes are streamed
-// exactly once: at fixed (unit, row) the G lanes read G consecutive units, so
-// each wave-wide load covers whole 128-byte lines.  Codes are widened with
-// byte→float conversions, dotted with x in fp32, and scaled once per block:
+// GEMV (decode) mapping.  A row of IN columns is a sequence of NU "units" of
+// 32 columns (sb6: one block; sym: two blocks).  G lanes (the largest power of
+// two ≤ 64 dividing NU) cover one row; a lane owns RL consecutive rows and, of
+// each, the units g, g+G, ...  All of a lane's weight loads are issued before
+// any is used (RL·KU loads of 16–32 B in flight per lane); meanwhile the
+// workgroup stages its input rows in LDS (padded so the G lanes of a row group
+// read distinct banks) together with per-unit input sums.  A unit's 32 inputs
+// then stay in registers for the lane's RL rows ("x-stationary").  At fixed
+// (unit, row) the G lanes read G consecutive units, so each wave-wide load
+// covers whole 128-byte lines.  Codes are widened to fp32 (4-bit sb6 codes two
+// per instruction through the fp8 converter), dotted with x in fp32, and
+// scaled once per block:
 //   sb6:  Σ (q·s + m)·x = s·Σ q·x + m·Σ x      (RwkvqSb6GEMV.swift:118-144)
 //   sym6: Σ (q−32)·s·x = s·(Σ q·x − 32·Σ x)    (RwkvqSymGEMV.swift:182-194)
 // and the per-lane partial sums are reduced over the G lanes with a fixed
-// butterfly.  N input rows (batched decode) share one weight pass (in tiles
-// of NT ≤ 4 rows).  All sums have a fixed order: results are deterministic.
+// butterfly.  Up to 4 input rows (batched decode) share one weight pass; more
+// rows are processed 4 at a time.  All sums have a fixed order: results are
+// deterministic.
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "launch.h"
 
@@ -129,224 +135,356 @@ __global__ __launch_bounds__(256) void sym_dequant_kernel(
 }
 
 // ─────────────────────────────── GEMV ───────────────────────────────
-// Decode 32 codes of one unit into bytes b[0..7] (4 codes per word, word m
-// holds columns 4m..4m+3) then dot with x[0..31].
-__device__ __forceinline__ float dot32_u8(const uint32_t (&q)[8], const float* x) {
+// Byte E of w as a float (v_cvt_f32_ubyteE).  Written out: for a masked word
+// the compiler folds (w >> 8E) & 0xff into a bit-field extract + convert.
+template <int E>
+__device__ __forceinline__ float ubyte(uint32_t w) {
+    float r;
+    if constexpr (E == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+    else if constexpr (E == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+    else if constexpr (E == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
+    return r;
+}
+
+__device__ __forceinline__ void bytes4(uint32_t w, float* c) {
+    c[0] = ubyte<0>(w); c[1] = ubyte<1>(w); c[2] = ubyte<2>(w); c[3] = ubyte<3>(w);
+}
+
+// Four codes 0..15, one per byte, widened two per instruction as fp8 (E4M3)
+// values: the byte 0000nnnn decodes to n·u with u = the value of byte 0x01
+// (subnormals continue the first binade linearly), so c = code·u exactly.
+__device__ __forceinline__ void nibbles4_fp8(uint32_t w, float* c) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    c[0] = lo[0]; c[1] = lo[1]; c[2] = hi[0]; c[3] = hi[1];
+}
+
+// Σ c[i]·x[i] over 32 columns as two 16-column chains, (cols 0..15) + (16..31).
+__device__ __forceinline__ float dot32(const float (&c)[32], const float (&x)[32]) {
     float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            d0 = fmaf((float)((q[m] >> (8 * e)) & 0xffu), x[4 * m + e], d0);
-            d1 = fmaf((float)((q[m + 4] >> (8 * e)) & 0xffu), x[16 + 4 * m + e], d1);
-        }
+    for (int i = 0; i < 16; ++i) {
+        d0 = fmaf(c[i], x[i], d0);
+        d1 = fmaf(c[16 + i], x[16 + i], d1);
     }
     return d0 + d1;
 }
 
+// Formats.  A unit is 32 columns of one row; `Raw` is what a lane loads for
+// one (row, unit); `accumulate` adds the unit's contribution for NT inputs.
+// xs[nn] = (Σ x cols 0..15, Σ x cols 16..31) of the unit.
 template <int XB>
-__device__ __forceinline__ void sb6_unit_codes(const uint32_t* __restrict__ qb, uint32_t (&q)[8]) {
-    uint32_t wd[4 + XB];
+struct Sb6Fmt {
+    static constexpr int WORDS = 4 + XB;
+    static constexpr bool SUMS = true;
+    static constexpr bool WIDE = XB > 0;   // codes wider than 4 bits: more registers per unit
+    struct Ptr {
+        const uint32_t* q;
+        const uint16_t* sm;
+        const uint32_t* dd;
+    };
+    struct Raw {
+        uint32_t w[WORDS];
+        uint32_t s0, s1;   // (qs, qm) pair; (d, dm) pair
+    };
+    // 32-bit byte offsets from the (uniform) buffer bases: the packed
+    // matrix is below 4 GiB (checked by the host).
+    __device__ static void load(const Ptr& p, int NU, uint32_t row, uint32_t u, Raw& r) {
+        const uint32_t ru = row * (uint32_t)NU + u;
+        const uint32_t* qb = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(p.q) + ru * (WORDS * 4u));
 #pragma unroll
-    for (int m = 0; m < 4 + XB; ++m) wd[m] = qb[m];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        q[m] = wd[m] & 0x0F0F0F0Fu;              // columns 4m..4m+3
-        q[m + 4] = (wd[m] >> 4) & 0x0F0F0F0Fu;   // columns 16+4m..16+4m+3
+        for (int m = 0; m < WORDS; ++m) r.w[m] = qb[m];
+        r.s0 = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.sm) + ru * 2u);
+        r.s1 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(p.dd) +
+                                                  (row * (uint32_t)(NU >> 3) + (u >> 3)) * 4u);
     }
-    if constexpr (XB >= 1) {
+    // Codes of the unit; for XB == 0 they come out scaled by the fp8 unit u.
+    __device__ static void codes(const Raw& r, float (&c)[32]) {
+        if constexpr (XB == 0) {
 #pragma unroll
-        for (int m = 0; m < 8; ++m) q[m] |= spread4((wd[4] >> (4 * m)) & 0xFu) << 4;
-    }
-    if constexpr (XB >= 2) {
+            for (int m = 0; m < 4; ++m) {
+                nibbles4_fp8(r.w[m] & 0x0F0F0F0Fu, &c[4 * m]);
+                nibbles4_fp8((r.w[m] >> 4) & 0x0F0F0F0Fu, &c[16 + 4 * m]);
+            }
+        } else {
 #pragma unroll
-        for (int m = 0; m < 8; ++m) q[m] |= spread4((wd[5] >> (4 * m)) & 0xFu) << 5;
+            for (int m = 0; m < 8; ++m) {
+                uint32_t q = (m < 4) ? (r.w[m] & 0x0F0F0F0Fu) : ((r.w[m - 4] >> 4) & 0x0F0F0F0Fu);
+                q |= spread4((r.w[4] >> (4 * m)) & 0xFu) << 4;
+                if constexpr (XB >= 2) q |= spread4((r.w[5] >> (4 * m)) & 0xFu) << 5;
+                bytes4(q, &c[4 * m]);
+            }
+        }
     }
-}
-
-__device__ __forceinline__ void load_x32(const float* __restrict__ xp, float (&xv)[32]) {
-    const float4* p = reinterpret_cast<const float4*>(xp);
+    // inv = 1/u for XB == 0 (a power of two: the scaled and the plain
+    // computation round identically), 1 otherwise.
+    template <int NT>
+    __device__ static void accumulate(const Raw& r, float inv, const float (&xv)[NT][32], const float (&xs)[NT][2],
+                                      float (&acc)[NT]) {
+        float c[32];
+        codes(r, c);
+        const float s = hround((float)(r.s0 & 0xffu) * f16f(r.s1)) * inv;
+        const float m = hround((float)(int8_t)(r.s0 >> 8) * f16f(r.s1 >> 16));
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        float4 f = p[m];
-        xv[4 * m] = f.x; xv[4 * m + 1] = f.y; xv[4 * m + 2] = f.z; xv[4 * m + 3] = f.w;
+        for (int nn = 0; nn < NT; ++nn) acc[nn] = fmaf(m, xs[nn][0] + xs[nn][1], fmaf(s, dot32(c, xv[nn]), acc[nn]));
     }
-}
-
-struct GemvGeom {
-    int G;     // lanes per row
-    int R;     // row groups per wave (64 / G)
-    int KU;    // units per lane (NU / G)
-    int RL;    // consecutive rows per lane
-    int WPB;   // waves per workgroup
 };
 
-// sb6: unit = 32-column block.
-template <int XB, int RL, int NT>
-__global__ __launch_bounds__(256) void sb6_gemv_kernel(
-    const float* __restrict__ x, int N, const uint8_t* __restrict__ qblk, const uint8_t* __restrict__ qsqm,
-    const uint16_t* __restrict__ ddm, float* __restrict__ y, int OUT, int IN, GemvGeom geo) {
-    constexpr int SUW = 4 + XB;
-    const int NB = IN >> 5, NSB = NB >> 3;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int gi = lane / geo.G, g = lane - gi * geo.G;
-    const int row0 = (blockIdx.x * geo.WPB + wave) * geo.R * RL + gi * RL;
-    if (row0 >= OUT) return;   // whole lane idle (rows are assigned in RL-aligned groups)
-    const uint32_t* qw = reinterpret_cast<const uint32_t*>(qblk);
-    const uint16_t* sm2 = reinterpret_cast<const uint16_t*>(qsqm);
-    const uint32_t* dd2 = reinterpret_cast<const uint32_t*>(ddm);
-
-    for (int n0 = 0; n0 < N; n0 += NT) {
-        float acc[NT][RL];
+template <int BITS>
+struct SymFmt {
+    static constexpr int WORDS = BITS == 8 ? 8 : 6;
+    static constexpr bool SUMS = BITS == 6;
+    static constexpr bool WIDE = true;
+    struct Ptr {
+        const uint32_t* q;
+        const uint16_t* qs;   // two int8 block scales per unit
+        const uint16_t* d;
+    };
+    struct Raw {
+        uint32_t w[WORDS];
+        uint32_t s0, s1;   // two int8 block scales; super-block scale (fp16)
+    };
+    __device__ static void load(const Ptr& p, int NU, uint32_t row, uint32_t u, Raw& r) {
+        const uint32_t ru = row * (uint32_t)NU + u;
+        const uint32_t* qb = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(p.q) + ru * (WORDS * 4u));
 #pragma unroll
-        for (int nn = 0; nn < NT; ++nn)
+        for (int m = 0; m < WORDS; ++m) r.w[m] = qb[m];
+        r.s0 = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.qs) + ru * 2u);
+        r.s1 = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.d) +
+                                                  (row * (uint32_t)(NU >> 3) + (u >> 3)) * 2u);
+    }
+    template <int NT>
+    __device__ static void accumulate(const Raw& r, float, const float (&xv)[NT][32], const float (&xs)[NT][2],
+                                      float (&acc)[NT]) {
+        const float dsb = f16f(r.s1);
+        const float s0 = hround((float)(int8_t)(r.s0 & 0xffu) * dsb);
+        const float s1 = hround((float)(int8_t)(r.s0 >> 8) * dsb);
+        float c[32];
+        if constexpr (BITS == 8) {
 #pragma unroll
-            for (int rr = 0; rr < RL; ++rr) acc[nn][rr] = 0.0f;
-        for (int ku = 0; ku < geo.KU; ++ku) {
-            const int blk = ku * geo.G + g;
-            float xv[NT][32], xs[NT];
+            for (int m = 0; m < 8; ++m)
 #pragma unroll
-            for (int nn = 0; nn < NT; ++nn) {
-                const int n = min(n0 + nn, N - 1);
-                load_x32(x + (int64_t)n * IN + blk * 32, xv[nn]);
-                float s0 = 0.0f, s1 = 0.0f;
+                for (int e = 0; e < 4; ++e) c[4 * m + e] = (float)(int8_t)(r.w[m] >> (8 * e));
+        } else {
+            // register order l0,l1,h0,h1 | l2,l3,h2,h3 → columns 4m..4m+3; codes +32
 #pragma unroll
-                for (int c = 0; c < 16; ++c) { s0 += xv[nn][c]; s1 += xv[nn][16 + c]; }
-                xs[nn] = s0 + s1;
-            }
-#pragma unroll
-            for (int rr = 0; rr < RL; ++rr) {
-                const int row = row0 + rr;
-                if (row < OUT) {
-                    const int64_t rb = (int64_t)row * NB + blk;
-                    uint32_t q[8];
-                    sb6_unit_codes<XB>(qw + rb * SUW, q);
-                    const uint32_t smv = sm2[rb];
-                    const uint32_t dd = dd2[(int64_t)row * NSB + (blk >> 3)];
-                    const float s = hround((float)(smv & 0xffu) * f16f(dd));
-                    const float m = hround((float)(int8_t)(smv >> 8) * f16f(dd >> 16));
-#pragma unroll
-                    for (int nn = 0; nn < NT; ++nn) {
-                        const float dv = dot32_u8(q, xv[nn]);
-                        acc[nn][rr] = fmaf(m, xs[nn], fmaf(s, dv, acc[nn][rr]));
-                    }
-                }
+            for (int m = 0; m < 8; ++m) {
+                const uint32_t wd = r.w[(m >> 2) * 2 + (m & 1)];
+                uint32_t q = (m & 2) ? ((wd >> 4) & 0x0F0F0F0Fu) : (wd & 0x0F0F0F0Fu);
+                q |= spread4((r.w[4] >> (4 * m)) & 0xFu) << 4;
+                q |= spread4((r.w[5] >> (4 * m)) & 0xFu) << 5;
+                bytes4(q, &c[4 * m]);
             }
         }
 #pragma unroll
-        for (int nn = 0; nn < NT; ++nn)
+        for (int nn = 0; nn < NT; ++nn) {
+            float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
-            for (int rr = 0; rr < RL; ++rr) {
-                float t = acc[nn][rr];
-                for (int off = geo.G >> 1; off >= 1; off >>= 1) t += __shfl_xor(t, off, 64);
-                const int row = row0 + rr;
-                if (g == 0 && row < OUT && n0 + nn < N) y[(int64_t)(n0 + nn) * OUT + row] = t;
+            for (int i = 0; i < 16; ++i) {
+                d0 = fmaf(c[i], xv[nn][i], d0);
+                d1 = fmaf(c[16 + i], xv[nn][16 + i], d1);
             }
+            if constexpr (BITS == 8) {
+                acc[nn] = fmaf(s1, d1, fmaf(s0, d0, acc[nn]));
+            } else {
+                acc[nn] = fmaf(s1, fmaf(-32.0f, xs[nn][1], d1), fmaf(s0, fmaf(-32.0f, xs[nn][0], d0), acc[nn]));
+            }
+        }
     }
+};
+
+// Σ of v over each aligned group of G lanes (G a power of two ≤ 64), in every
+// lane of the group: DPP butterflies within 16-lane rows (quad swaps, then the
+// half-row and row mirrors pair disjoint halves), then lane swaps across rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp_pair(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float group_sum(float v, int G) {
+    if (G >= 2) v += dpp_pair<0xB1>(v);    // quad_perm [1,0,3,2]
+    if (G >= 4) v += dpp_pair<0x4E>(v);    // quad_perm [2,3,0,1]
+    if (G >= 8) v += dpp_pair<0x141>(v);   // row_half_mirror
+    if (G >= 16) v += dpp_pair<0x140>(v);  // row_mirror
+    if (G >= 32) v += __shfl_xor(v, 16, 64);
+    if (G >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
 }
 
-// sym: unit = 32 columns (two 16-blocks).  Input row of output row `row` for
-// input n is x[n·NK + row/out_per].
-template <int BITS, int RL, int NT>
-__global__ __launch_bounds__(256) void sym_gemv_kernel(
-    const float* __restrict__ x, int N, const uint8_t* __restrict__ qblk, const uint8_t* __restrict__ qs,
-    const uint16_t* __restrict__ d, float* __restrict__ y, int OUT, int IN, int out_per, GemvGeom geo) {
-    const int NB = IN >> 4, NSB = IN >> 8, NU = IN >> 5;
+struct GemvGeom {
+    int G;     // lanes per row (power of two)
+    int R;     // row groups per wave (64 / G)
+    int NP;    // passes: a lane covers units (p·KU + ku)·G + g, p < NP, ku < KU
+    int WPB;   // waves per workgroup
+};
+
+// Padded LDS row: column c at c + 4·(c / 32), so the G lanes of a row group
+// reading G different units with ds_read_b128 hit distinct banks.
+__host__ __device__ constexpr int xl_stride(int IN) { return IN + (IN >> 3); }
+
+// y[n, row] = Σ_c W[row, c] · x[n·NK + row / out_per, c].  A lane owns RL
+// consecutive rows and, for each, the units (p·KU + ku)·G + g; all RL·KU units
+// of a pass are loaded before any is used, so every lane keeps RL·KU
+// 16–32-byte loads in flight.  With `xl` the workgroup first stages its input
+// rows (and per-unit sums) in LDS while those loads are outstanding, and the
+// weights stay in registers across input tiles.
+template <class F, int RL, int KU, int NT, bool XL, bool MULTI>
+__global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float* __restrict__ x, int N, typename F::Ptr P,
+                                                   float* __restrict__ y, int OUT, int IN, int out_per, GemvGeom geo) {
+    extern __shared__ float lds[];
+    const int NU = IN >> 5;
     const int NK = OUT / out_per;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int gi = lane / geo.G, g = lane - gi * geo.G;
     const int row0 = (blockIdx.x * geo.WPB + wave) * geo.R * RL + gi * RL;
-    if (row0 >= OUT) return;
-    const int xi = row0 / out_per;   // all RL rows of this lane share it (out_per % RL == 0)
-    const uint32_t* qw = reinterpret_cast<const uint32_t*>(qblk);
-    const uint16_t* qs2 = reinterpret_cast<const uint16_t*>(qs);
+    const bool live = row0 < OUT;
+    const int xi = (live ? row0 : OUT - 1) / out_per;   // RL divides out_per
+    float inv = 1.0f;
+    if constexpr (std::is_same_v<F, Sb6Fmt<0>>) inv = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
 
-    for (int n0 = 0; n0 < N; n0 += NT) {
-        float acc[NT][RL];
+    using Raw = typename F::Raw;
+    auto load_pass = [&](int p, Raw (&W)[RL][KU]) {
+#pragma unroll
+        for (int rr = 0; rr < RL; ++rr) {
+            const uint32_t row = (uint32_t)min(row0 + rr, OUT - 1);
+#pragma unroll
+            for (int ku = 0; ku < KU; ++ku) F::load(P, NU, row, (uint32_t)((p * KU + ku) * geo.G + g), W[rr][ku]);
+        }
+    };
+    const int XS = xl_stride(IN);
+    const float* xsum = lds + NT * NK * XS;
+    auto compute_pass = [&](int p, const Raw (&W)[RL][KU], int n0, float (&acc)[NT][RL]) {
+#pragma unroll
+        for (int ku = 0; ku < KU; ++ku) {
+            // One unit's inputs live at a time (scheduling barrier).
+            if (ku) asm volatile("" ::: "memory");
+            const int u = (p * KU + ku) * geo.G + g;
+            float xv[NT][32], xs[NT][2];
+#pragma unroll
+            for (int nn = 0; nn < NT; ++nn) {
+                if constexpr (XL) {
+                    const int j = nn * NK + xi;
+                    const float4* px = reinterpret_cast<const float4*>(lds + j * XS + u * 36);
+#pragma unroll
+                    for (int m = 0; m < 8; ++m) {
+                        const float4 f = px[m];
+                        xv[nn][4 * m] = f.x; xv[nn][4 * m + 1] = f.y; xv[nn][4 * m + 2] = f.z; xv[nn][4 * m + 3] = f.w;
+                    }
+                    if constexpr (F::SUMS) {
+                        const float2 s = reinterpret_cast<const float2*>(xsum)[j * NU + u];
+                        xs[nn][0] = s.x; xs[nn][1] = s.y;
+                    }
+                } else {
+                    const int n = min(n0 + nn, N - 1);
+                    const float4* px = reinterpret_cast<const float4*>(x + ((int64_t)n * NK + xi) * IN + u * 32);
+#pragma unroll
+                    for (int m = 0; m < 8; ++m) {
+                        const float4 f = px[m];
+                        xv[nn][4 * m] = f.x; xv[nn][4 * m + 1] = f.y; xv[nn][4 * m + 2] = f.z; xv[nn][4 * m + 3] = f.w;
+                    }
+                    if constexpr (F::SUMS) {
+                        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                        for (int c = 0; c < 16; ++c) { s0 += xv[nn][c]; s1 += xv[nn][16 + c]; }
+                        xs[nn][0] = s0; xs[nn][1] = s1;
+                    }
+                }
+            }
+#pragma unroll
+            for (int rr = 0; rr < RL; ++rr) {
+                float a[NT];
+#pragma unroll
+                for (int nn = 0; nn < NT; ++nn) a[nn] = acc[nn][rr];
+                F::template accumulate<NT>(W[rr][ku], inv, xv, xs, a);
+#pragma unroll
+                for (int nn = 0; nn < NT; ++nn) acc[nn][rr] = a[nn];
+            }
+        }
+    };
+    auto store = [&](float (&acc)[NT][RL], int n0) {
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn)
+#pragma unroll
+            for (int rr = 0; rr < RL; ++rr) {
+                const float t = group_sum(acc[nn][rr], geo.G);
+                const int row = row0 + rr;
+                if (g == 0 && row < OUT && n0 + nn < N) y[(int64_t)(n0 + nn) * OUT + row] = t;
+            }
+    };
+
+    auto zero = [&](float (&acc)[NT][RL]) {
 #pragma unroll
         for (int nn = 0; nn < NT; ++nn)
 #pragma unroll
             for (int rr = 0; rr < RL; ++rr) acc[nn][rr] = 0.0f;
-        for (int ku = 0; ku < geo.KU; ++ku) {
-            const int u = ku * geo.G + g;
-            float xv[NT][32], xs0[NT], xs1[NT];
-#pragma unroll
-            for (int nn = 0; nn < NT; ++nn) {
-                const int n = min(n0 + nn, N - 1);
-                load_x32(x + ((int64_t)n * NK + xi) * IN + u * 32, xv[nn]);
-                if constexpr (BITS == 6) {
-                    float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-                    for (int c = 0; c < 16; ++c) { s0 += xv[nn][c]; s1 += xv[nn][16 + c]; }
-                    xs0[nn] = s0; xs1[nn] = s1;
-                }
+    };
+    if constexpr (XL) {
+        Raw W[RL][KU];
+        load_pass(0, W);   // in flight while the inputs are staged
+        const int rows = NT * NK;
+        auto stage = [&](int n0) {   // one tile: N <= NT
+            const int step = (int)blockDim.x * 4;
+#pragma unroll 1
+            for (int j = 0; j < rows; ++j) {   // uniform
+                const int nn = j / NK, k = j - nn * NK;
+                const float* src = x + ((int64_t)min(n0 + nn, N - 1) * NK + k) * IN;
+#pragma unroll 1
+                for (int c = (int)threadIdx.x * 4; c < IN; c += step)
+                    *reinterpret_cast<float4*>(lds + j * XS + c + (c >> 5) * 4) =
+                        *reinterpret_cast<const float4*>(src + c);
             }
+            __syncthreads();
+            if constexpr (F::SUMS) {
+                // sums[j][u][h] = x[j, 32u + 16h + 0..15], added in column order
+                float* sums = lds + NT * NK * XS;
+#pragma unroll 1
+                for (int j = 0; j < rows; ++j)
+#pragma unroll 1
+                    for (int i = threadIdx.x; i < NU * 2; i += blockDim.x) {
+                        const float4* px = reinterpret_cast<const float4*>(lds + j * XS + (i >> 1) * 36 + 16 * (i & 1));
+                        float sum = 0.0f;
 #pragma unroll
-            for (int rr = 0; rr < RL; ++rr) {
-                const int row = row0 + rr;
-                if (row < OUT) {
-                    const uint32_t sc = qs2[(int64_t)row * (NB >> 1) + u];   // two int8 block scales
-                    const float dsb = f16f(d[(int64_t)row * NSB + (u >> 3)]);
-                    const float s0 = hround((float)(int8_t)(sc & 0xffu) * dsb);
-                    const float s1 = hround((float)(int8_t)(sc >> 8) * dsb);
-                    if constexpr (BITS == 8) {
-                        const uint32_t* qb = qw + ((int64_t)row * IN + u * 32) / 4;
-                        uint32_t wd[8];
-#pragma unroll
-                        for (int m = 0; m < 8; ++m) wd[m] = qb[m];
-#pragma unroll
-                        for (int nn = 0; nn < NT; ++nn) {
-                            float d0 = 0.0f, d1 = 0.0f;
-#pragma unroll
-                            for (int m = 0; m < 4; ++m)
-#pragma unroll
-                                for (int e = 0; e < 4; ++e) {
-                                    d0 = fmaf((float)(int8_t)(wd[m] >> (8 * e)), xv[nn][4 * m + e], d0);
-                                    d1 = fmaf((float)(int8_t)(wd[m + 4] >> (8 * e)), xv[nn][16 + 4 * m + e], d1);
-                                }
-                            acc[nn][rr] = fmaf(s1, d1, fmaf(s0, d0, acc[nn][rr]));
+                        for (int m = 0; m < 4; ++m) {
+                            const float4 f = px[m];
+                            sum += f.x; sum += f.y; sum += f.z; sum += f.w;
                         }
-                    } else {
-                        const uint32_t* qb = qw + ((int64_t)row * NU + u) * 6;
-                        uint32_t wd[6];
-#pragma unroll
-                        for (int m = 0; m < 6; ++m) wd[m] = qb[m];
-                        // register order l0,l1,h0,h1 | l2,l3,h2,h3 → columns 4m..4m+3
-                        uint32_t q[8];
-                        q[0] = wd[0] & 0x0F0F0F0Fu;         q[1] = wd[1] & 0x0F0F0F0Fu;
-                        q[2] = (wd[0] >> 4) & 0x0F0F0F0Fu;  q[3] = (wd[1] >> 4) & 0x0F0F0F0Fu;
-                        q[4] = wd[2] & 0x0F0F0F0Fu;         q[5] = wd[3] & 0x0F0F0F0Fu;
-                        q[6] = (wd[2] >> 4) & 0x0F0F0F0Fu;  q[7] = (wd[3] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-                        for (int m = 0; m < 8; ++m) {
-                            q[m] |= spread4((wd[4] >> (4 * m)) & 0xFu) << 4;
-                            q[m] |= spread4((wd[5] >> (4 * m)) & 0xFu) << 5;
-                        }
-#pragma unroll
-                        for (int nn = 0; nn < NT; ++nn) {
-                            float d0 = 0.0f, d1 = 0.0f;
-#pragma unroll
-                            for (int m = 0; m < 4; ++m)
-#pragma unroll
-                                for (int e = 0; e < 4; ++e) {
-                                    d0 = fmaf((float)((q[m] >> (8 * e)) & 0xffu), xv[nn][4 * m + e], d0);
-                                    d1 = fmaf((float)((q[m + 4] >> (8 * e)) & 0xffu), xv[nn][16 + 4 * m + e], d1);
-                                }
-                            acc[nn][rr] = fmaf(s1, fmaf(-32.0f, xs1[nn], d1), fmaf(s0, fmaf(-32.0f, xs0[nn], d0), acc[nn][rr]));
-                        }
+                        sums[j * NU * 2 + i] = sum;
                     }
+                __syncthreads();
+            }
+        };
+        float acc[NT][RL];
+        stage(0);
+        zero(acc);
+        if constexpr (MULTI) {
+            for (int p = 0; p < geo.NP; ++p) {
+                if (p + 1 < geo.NP) {
+                    Raw Wn[RL][KU];
+                    load_pass(p + 1, Wn);   // next pass in flight during this one
+                    compute_pass(p, W, 0, acc);
+#pragma unroll
+                    for (int rr = 0; rr < RL; ++rr)
+#pragma unroll
+                        for (int ku = 0; ku < KU; ++ku) W[rr][ku] = Wn[rr][ku];
+                } else {
+                    compute_pass(p, W, 0, acc);
                 }
             }
+        } else {
+            compute_pass(0, W, 0, acc);   // NP == 1
         }
-#pragma unroll
-        for (int nn = 0; nn < NT; ++nn)
-#pragma unroll
-            for (int rr = 0; rr < RL; ++rr) {
-                float t = acc[nn][rr];
-                for (int off = geo.G >> 1; off >= 1; off >>= 1) t += __shfl_xor(t, off, 64);
-                const int row = row0 + rr;
-                if (g == 0 && row < OUT && n0 + nn < N) y[(int64_t)(n0 + nn) * OUT + row] = t;
+        store(acc, 0);
+    } else {
+        for (int n0 = 0; n0 < N; n0 += NT) {
+            float acc[NT][RL];
+            zero(acc);
+            for (int p = 0; p < geo.NP; ++p) {
+                Raw W[RL][KU];
+                load_pass(p, W);
+                compute_pass(p, W, n0, acc);
             }
+            store(acc, n0);
+        }
     }
 }
 
@@ -361,27 +499,141 @@ rwkv_status launch_status(const char* what) {
     return RWKV_OK;
 }
 
-// Geometry for NU units per row and OUT rows: G lanes per row, RL rows per
-// lane (dividing `rl_div`), waves per block shrunk until the grid reaches
-// ~2 workgroups per CU when the matrix allows it.
-GemvGeom pick_geom(int64_t OUT, int64_t NU, int64_t rl_div) {
-    GemvGeom g{};
-    int64_t G = NU & -NU;
+constexpr size_t kXlBudget = 64 * 1024;   // LDS bytes a workgroup may use for inputs
+
+struct GemvPlan {
+    GemvGeom geo;
+    int RL, KU, NT;
+    bool xl;   // inputs staged in LDS (requires NP == 1)
+    size_t lds;
+    unsigned blocks;
+};
+
+// Geometry for an OUT × (32·NU) matrix, N inputs, NK input rows per input
+// (fused groups), rows per lane dividing `rl_div`.  One input tile (N ≤ 1): G =
+// the smallest power of two ≤ 64 dividing NU with at most 4 units per lane
+// (fewer lanes per row: fewer reduction steps per weight), KU = the units per
+// lane, and RL·KU up to 4 so each lane keeps several unit loads in flight;
+// many small waves hide the memory latency better than few deep ones.  Four
+// inputs per tile: KU = 1, RL ≤ 2 (registers).  The inputs go through LDS when one input
+// tile covers them and they fit in 64 KB; callers split larger batches.
+GemvPlan plan_gemv(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t NK, bool sums, bool wide) {
+    GemvPlan pl{};
+    pl.NT = N >= 2 ? 4 : 1;
+    int64_t G = NU & -NU;   // largest power of two dividing NU
     if (G > 64) G = 64;
-    g.G = (int)G;
-    g.R = 64 / g.G;
-    g.KU = (int)(NU / G);
-    g.RL = (rl_div % 4 == 0) ? 4 : (rl_div % 2 == 0) ? 2 : 1;
-    g.WPB = 4;
-    auto blocks = [&](const GemvGeom& q) { return (OUT + (int64_t)q.WPB * q.R * q.RL - 1) / ((int64_t)q.WPB * q.R * q.RL); };
-    while (blocks(g) < 512 && (g.RL > 1 || g.WPB > 1)) {
-        if (g.RL > 1) g.RL >>= 1;
-        else g.WPB >>= 1;
+    if (pl.NT == 1)
+        while (G > 1 && NU / (G >> 1) <= 4) G >>= 1;
+    pl.geo.G = (int)G;
+    pl.geo.R = 64 / pl.geo.G;
+    const int64_t per_lane = NU / G;
+    // all of a lane's units in one pass (KU ≤ 4), else one unit per pass with
+    // the next pass prefetched
+    pl.KU = (pl.NT == 1 && per_lane <= 4) ? (int)per_lane : 1;
+    const int KU = pl.KU;
+    pl.geo.NP = (int)(per_lane / KU);
+    // Rows per lane (the inputs of a unit stay in registers across them),
+    // bounded by registers: RL·KU ≤ 4 (≤ 2 for wider codes), RL ≤ 2 with a
+    // prefetched pass (1 for wider codes) or four inputs per tile.
+    const int slots = pl.NT == 4 ? 2 : pl.geo.NP > 1 ? (wide ? 1 : 2) : (wide ? 2 : 4);
+    pl.RL = (rl_div % 4 == 0 && 4 * KU <= slots) ? 4 : (rl_div % 2 == 0 && 2 * KU <= slots) ? 2 : 1;
+    // Waves per workgroup share one staging of the inputs: up to 16 (one
+    // input row) while the grid keeps ≥ 256 workgroups, at least 4 (fewer
+    // lose more to the staging than they gain in spread).
+    pl.geo.WPB = pl.NT == 1 ? 16 : 4;
+    auto blocks = [&]() {
+        const int64_t per = (int64_t)pl.geo.WPB * pl.geo.R * pl.RL;
+        return (OUT + per - 1) / per;
+    };
+    while (pl.geo.WPB > 4 && blocks() < 256) pl.geo.WPB >>= 1;
+    pl.blocks = (unsigned)blocks();
+    const int64_t IN = NU * 32;
+    const int64_t lds = (int64_t)pl.NT * NK * (xl_stride((int)IN) + (sums ? NU * 2 : 0)) * 4;
+    pl.xl = N <= pl.NT && lds <= (int64_t)kXlBudget;
+    if (!pl.xl) {
+        // inputs read from global memory: one row per lane keeps registers low
+        pl.RL = 1;
+        pl.blocks = (unsigned)blocks();
     }
-    return g;
+    pl.lds = pl.xl ? (size_t)lds : 0;
+    return pl;
 }
 
-int pick_nt(int64_t N) { return N >= 4 ? 4 : N >= 2 ? 2 : 1; }
+// Returns false when the plan names a variant that is not built.
+template <class F>
+bool launch_gemv(const GemvPlan& pl, hipStream_t st, const float* x, int N, typename F::Ptr P, float* y, int OUT,
+                 int IN, int out_per) {
+    const dim3 grid(pl.blocks), block(64 * pl.geo.WPB);
+    bool launched = false;
+    auto go = [&](auto kernel) {
+        rwkv::launch_lds(kernel, grid, block, pl.lds, st, x, N, P, y, OUT, IN, out_per, pl.geo);
+        launched = true;
+    };
+    const bool multi = pl.geo.NP > 1;
+    if (!pl.xl) {
+        // inputs from global memory, one row per lane
+        if (pl.NT == 4) go(gemv_kernel<F, 1, 1, 4, false, false>);
+        else if (pl.KU == 1) go(gemv_kernel<F, 1, 1, 1, false, false>);
+        else if (pl.KU == 2) go(gemv_kernel<F, 1, 2, 1, false, false>);
+        else if (pl.KU == 3) go(gemv_kernel<F, 1, 3, 1, false, false>);
+        else if (pl.KU == 4) go(gemv_kernel<F, 1, 4, 1, false, false>);
+    } else if (pl.NT == 4) {
+        // KU == 1, RL ≤ 2
+        if (multi) {
+            if (pl.RL == 2) go(gemv_kernel<F, 2, 1, 4, true, true>);
+            else go(gemv_kernel<F, 1, 1, 4, true, true>);
+        } else {
+            if (pl.RL == 2) go(gemv_kernel<F, 2, 1, 4, true, false>);
+            else go(gemv_kernel<F, 1, 1, 4, true, false>);
+        }
+    } else if (multi) {
+        // KU == 1, RL ≤ 2 (1 for wider codes)
+        if (pl.RL == 1) go(gemv_kernel<F, 1, 1, 1, true, true>);
+        else if constexpr (!F::WIDE) {
+            if (pl.RL == 2) go(gemv_kernel<F, 2, 1, 1, true, true>);
+        }
+    } else {
+        // RL·KU ≤ 4 (≤ 2 for wider codes)
+        if (pl.KU == 1) {
+            if (pl.RL == 2) go(gemv_kernel<F, 2, 1, 1, true, false>);
+            else if (pl.RL == 1) go(gemv_kernel<F, 1, 1, 1, true, false>);
+            else if constexpr (!F::WIDE) {
+                if (pl.RL == 4) go(gemv_kernel<F, 4, 1, 1, true, false>);
+            }
+        } else if (pl.KU == 2) {
+            if (pl.RL == 1) go(gemv_kernel<F, 1, 2, 1, true, false>);
+            else if constexpr (!F::WIDE) {
+                if (pl.RL == 2) go(gemv_kernel<F, 2, 2, 1, true, false>);
+            }
+        } else if (pl.KU == 3 && pl.RL == 1) {
+            go(gemv_kernel<F, 1, 3, 1, true, false>);
+        } else if (pl.KU == 4 && pl.RL == 1) {
+            go(gemv_kernel<F, 1, 4, 1, true, false>);
+        }
+    }
+    return launched;
+}
+
+// Batches of more than 4 inputs run as launches of ≤ 4 inputs each (the
+// inputs of a launch are staged in LDS; each launch streams the weights once),
+// unless the inputs do not fit in LDS: then one launch reads them from global
+// memory.
+template <class F>
+bool run_gemv(int64_t OUT, int64_t IN, int64_t rl_div, int64_t N, int64_t NK, hipStream_t st, const float* x,
+              typename F::Ptr P, float* y, int64_t out_per) {
+    const int64_t NU = IN / 32;
+    const GemvPlan all = plan_gemv(OUT, NU, rl_div, N, NK, F::SUMS, F::WIDE);
+    if (all.xl || N <= 4) return launch_gemv<F>(all, st, x, (int)N, P, y, (int)OUT, (int)IN, (int)out_per);
+    const GemvPlan tile = plan_gemv(OUT, NU, rl_div, 4, NK, F::SUMS, F::WIDE);
+    if (!tile.xl) return launch_gemv<F>(all, st, x, (int)N, P, y, (int)OUT, (int)IN, (int)out_per);
+    for (int64_t n0 = 0; n0 < N; n0 += 4) {
+        const int64_t nn = N - n0 < 4 ? N - n0 : 4;
+        const GemvPlan pl = nn == 4 ? tile : plan_gemv(OUT, NU, rl_div, nn, NK, F::SUMS, F::WIDE);
+        if (!launch_gemv<F>(pl, st, x + n0 * NK * IN, (int)nn, P, y + n0 * OUT, (int)OUT, (int)IN, (int)out_per))
+            return false;
+    }
+    return true;
+}
 
 }  // namespace
 
@@ -462,27 +714,17 @@ rwkv_status rwkv_sb6_gemv(const float* x, int64_t N, const uint8_t* qblk, const 
     RWKV_REQUIRE(N >= 1 && N <= INT32_MAX, RWKV_E_SHAPE, "sb6_gemv: rows %lld", (long long)N);
     RWKV_REQUIRE(OUT >= 1 && OUT <= INT32_MAX && IN >= 256 && IN % 256 == 0 && IN <= (1 << 24), RWKV_E_SHAPE,
                  "sb6_gemv: shape %lldx%lld not taken (IN %% 256 == 0 required)", (long long)OUT, (long long)IN);
-    const GemvGeom geo = pick_geom(OUT, IN / 32, OUT);
-    const int64_t per_block = (int64_t)geo.WPB * geo.R * geo.RL;
-    dim3 grid((unsigned)((OUT + per_block - 1) / per_block)), block(64 * geo.WPB);
+    RWKV_REQUIRE(OUT * (IN / 32) * (16 + 4 * xbits) < (int64_t(1) << 32), RWKV_E_SHAPE,
+                 "sb6_gemv: packed matrix of %lldx%lld exceeds 4 GiB", (long long)OUT, (long long)IN);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const int nt = pick_nt(N);
-#define RWKV_GV(XB, RL, NT) \
-    rwkv::launch(sb6_gemv_kernel<XB, RL, NT>, grid, block, st, x, (int)N, qblk, qsqm, ddm, y, (int)OUT, (int)IN, geo)
-#define RWKV_GV_NT(XB, RL)                  \
-    if (nt == 4) RWKV_GV(XB, RL, 4);        \
-    else if (nt == 2) RWKV_GV(XB, RL, 2);   \
-    else RWKV_GV(XB, RL, 1);
-#define RWKV_GV_RL(XB)                                                       \
-    if (geo.RL == 4) { RWKV_GV_NT(XB, 4) } else if (geo.RL == 2) { RWKV_GV_NT(XB, 2) } else { RWKV_GV_NT(XB, 1) }
+    const Sb6Fmt<0>::Ptr P{(const uint32_t*)qblk, (const uint16_t*)qsqm, (const uint32_t*)ddm};
+    bool ok;
     switch (xbits) {
-        case 0: RWKV_GV_RL(0) break;
-        case 1: RWKV_GV_RL(1) break;
-        default: RWKV_GV_RL(2) break;
+        case 0: ok = run_gemv<Sb6Fmt<0>>(OUT, IN, OUT, N, 1, st, x, P, y, OUT); break;
+        case 1: ok = run_gemv<Sb6Fmt<1>>(OUT, IN, OUT, N, 1, st, x, {P.q, P.sm, P.dd}, y, OUT); break;
+        default: ok = run_gemv<Sb6Fmt<2>>(OUT, IN, OUT, N, 1, st, x, {P.q, P.sm, P.dd}, y, OUT); break;
     }
-#undef RWKV_GV_RL
-#undef RWKV_GV_NT
-#undef RWKV_GV
+    RWKV_REQUIRE(ok, RWKV_E_UNSUPPORTED, "sb6_gemv: no kernel variant for %lldx%lld", (long long)OUT, (long long)IN);
     rwkv_status s = launch_status("sb6_gemv launch");
     if (s == RWKV_OK) rwkv::counters().sb6_gemv++;
     return s;
@@ -502,28 +744,13 @@ rwkv_status rwkv_sym_gemv(const float* x, int64_t N, const uint8_t* qblk, const 
                  "sym_gemv: shape %lldx%lld not taken (IN %% 256 == 0 required)", (long long)OUT, (long long)IN);
     RWKV_REQUIRE(out_per >= 1 && OUT % out_per == 0, RWKV_E_SHAPE,
                  "sym_gemv: %lld rows do not split into matrices of %lld", (long long)OUT, (long long)out_per);
-    const GemvGeom geo = pick_geom(OUT, IN / 32, out_per);
-    const int64_t per_block = (int64_t)geo.WPB * geo.R * geo.RL;
-    dim3 grid((unsigned)((OUT + per_block - 1) / per_block)), block(64 * geo.WPB);
+    RWKV_REQUIRE(OUT * IN * bits / 8 < (int64_t(1) << 32), RWKV_E_SHAPE,
+                 "sym_gemv: packed matrix of %lldx%lld exceeds 4 GiB", (long long)OUT, (long long)IN);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const int nt = pick_nt(N);
-#define RWKV_GV(BITS, RL, NT)                                                                                   \
-    rwkv::launch(sym_gemv_kernel<BITS, RL, NT>, grid, block, st, x, (int)N, qblk, qs, d, y, (int)OUT, \
-                       (int)IN, (int)out_per, geo)
-#define RWKV_GV_NT(BITS, RL)                  \
-    if (nt == 4) RWKV_GV(BITS, RL, 4);        \
-    else if (nt == 2) RWKV_GV(BITS, RL, 2);   \
-    else RWKV_GV(BITS, RL, 1);
-#define RWKV_GV_RL(BITS)                                                                     \
-    if (geo.RL == 4) { RWKV_GV_NT(BITS, 4) } else if (geo.RL == 2) { RWKV_GV_NT(BITS, 2) } else { RWKV_GV_NT(BITS, 1) }
-    if (bits == 8) {
-        RWKV_GV_RL(8)
-    } else {
-        RWKV_GV_RL(6)
-    }
-#undef RWKV_GV_RL
-#undef RWKV_GV_NT
-#undef RWKV_GV
+    const int64_t NK = OUT / out_per;
+    const bool ok = bits == 8 ? run_gemv<SymFmt<8>>(OUT, IN, out_per, N, NK, st, x, {(const uint32_t*)qblk, (const uint16_t*)qs, d}, y, out_per)
+                              : run_gemv<SymFmt<6>>(OUT, IN, out_per, N, NK, st, x, {(const uint32_t*)qblk, (const uint16_t*)qs, d}, y, out_per);
+    RWKV_REQUIRE(ok, RWKV_E_UNSUPPORTED, "sym_gemv: no kernel variant for %lldx%lld", (long long)OUT, (long long)IN);
     rwkv_status s = launch_status("sym_gemv launch");
     if (s == RWKV_OK) {
         if (out_per < OUT) rwkv::counters().sym_fused++;

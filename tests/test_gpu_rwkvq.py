@@ -92,7 +92,8 @@ def test_sym_off_superblock_known_answer():
     assert np.array_equal(got.cpu().numpy().reshape(-1), np.array(kat["expected_f32"], np.float32))
 
 
-GEMV_SHAPES = [(768, 768), (3072, 768), (768, 3072), (2048, 2048), (24, 256)]
+# 32 x 7168: 224 column units per row, 7 per lane (several passes, inputs read from global memory)
+GEMV_SHAPES = [(768, 768), (3072, 768), (768, 3072), (2048, 2048), (24, 256), (32, 7168)]
 
 
 @pytest.mark.parametrize("xbits", [0, 1, 2])
@@ -140,7 +141,7 @@ def test_gemv_one_hot_is_bit_exact_dequant_column(orc):
 
 
 @pytest.mark.parametrize("bits", [8, 6])
-@pytest.mark.parametrize("OUT,IN", [(768, 768), (3072, 768), (768, 3072), (16, 256)])
+@pytest.mark.parametrize("OUT,IN", [(768, 768), (3072, 768), (768, 3072), (16, 256), (32, 7168)])
 def test_sym_gemv_matches_fp64(orc, bits, OUT, IN):
     case(f"sym gemv {OUT}x{IN} bits={bits}")
     qblk, qs, d = sym_tensor(orc, OUT, IN, bits, seed=OUT + bits)
