@@ -4,7 +4,9 @@ Headline (`value`): one-token decode of the 0.1B x070 shape (12 layers,
 n_embd 768, FFN 3072, vocab 65536), batch 1: every decode GEMV of the token
 (r/k/v/o 768x768, ffn key 3072x768, ffn value 768x3072, head 65536x768; sb6
 4-bit weights encoded from seeded N(0, 0.02)) plus the WKV-7 decode step and
-the tmix tail of each layer.  A step = one token.  The token's 97 launches are
+the tmix tail of each layer.  A step = one token: per layer one fused r/k/v
+GEMV launch, one fused step+tail launch, and the o / ffn key / ffn value
+GEMVs, then the head (61 launches).  The token's launches are
 captured once per weight copy into a HIP graph; steps rotate over
 `--copies` copies of the weights (> 256 MB in total) so they stream from HBM
 instead of the MALL.  Inputs are resident in HBM before the timed region.
@@ -91,12 +93,22 @@ class DecodeModel:
             qblk, qsqm, ddm, xb = Q.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"],
                                                     disk["gw_dm"], None, None, (OUT, IN))
             self.host[key] = (qblk, qsqm, ddm, OUT, IN)
-            base = (torch.from_numpy(qblk).to(dev), torch.from_numpy(qsqm).to(dev),
-                    torch.from_numpy(ddm.view(np.float16)).to(dev))
-            self.dev[0][key] = base
-            for c in range(1, copies):
-                self.dev[c][key] = tuple(z.clone() for z in base)
             self.bytes_per_token += qblk.nbytes + qsqm.nbytes + ddm.nbytes + 4 * (IN + OUT)
+        # device buffers; r/k/v of a layer row-concatenated (one fused launch)
+        groups = {}
+        for key in self.host:
+            if ".att.receptance." in key or ".att.key." in key or ".att.value." in key:
+                groups.setdefault(key.split(".att.")[0] + ".att.rkv", []).append(key)
+            else:
+                groups[key] = [key]
+        for gkey, members in groups.items():
+            parts = [self.host[m] for m in members]
+            base = (torch.from_numpy(np.concatenate([p[0] for p in parts])).to(dev),
+                    torch.from_numpy(np.concatenate([p[1] for p in parts])).to(dev),
+                    torch.from_numpy(np.concatenate([p[2] for p in parts]).view(np.float16)).to(dev))
+            self.dev[0][gkey] = base
+            for c in range(1, copies):
+                self.dev[c][gkey] = tuple(z.clone() for z in base)
         log(f"encoded {len(self.host)} matrices of {shape.name} in {time.time() - t0:.1f}s, "
             f"{self.bytes_per_token / 1e6:.1f} MB per token, {copies} device copies")
 
@@ -114,8 +126,9 @@ class DecodeStep:
         rng = np.random.default_rng(seed)
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
         self.xD = t(rng.standard_normal((B, self.D)))
+        self.xrkv = t(rng.standard_normal((B * 3, self.D)))   # token-shifted r/k/v inputs, per row
         self.xF = t(np.maximum(rng.standard_normal((B, self.F)), 0) ** 2 * 0.1)
-        self.y_rkv = torch.empty((3, B, self.D), device=dev)
+        self.y_rkv = torch.empty((B, 3 * self.D), device=dev)
         self.y_o = torch.empty((B, self.D), device=dev)
         self.y_k = torch.empty((B, self.F), device=dev)
         self.y_v = torch.empty((B, self.D), device=dev)
@@ -143,17 +156,15 @@ class DecodeStep:
                                        y.data_ptr(), OUT, IN, 0, stream))
 
         for l in range(self.L):
-            for j, m in enumerate(("receptance", "key", "value")):
-                gemv(self.xD, f"blocks.{l}.att.{m}.weight", self.y_rkv[j])
+            q = W[f"blocks.{l}.att.rkv"]   # r/k/v in one launch, x rows (x_r, x_k, x_v) per token
+            _lib.check(L.rwkv_sb6_gemv_fused(self.xrkv.data_ptr(), B, q[0].data_ptr(), q[1].data_ptr(),
+                                             q[2].data_ptr(), self.y_rkv.data_ptr(), 3 * D, D, 0, D, stream))
             r, w, k, v, a, b = (z[l] for z in self.rwkvab)
             st = self.state[l]
-            _lib.check(L.rwkv_wkv7_step(r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(), a.data_ptr(),
-                                        b.data_ptr(), 0, st.data_ptr(), self.wkv.data_ptr(), st.data_ptr(), B, H,
-                                        stream))
-            _lib.check(L.rwkv_wkv_tail(self.wkv.data_ptr(), r.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                       self.rk[l].data_ptr(), self.lnw[l].data_ptr(), self.lnb[l].data_ptr(),
-                                       self.g[l].data_ptr(), self.tail.data_ptr(), B, H, 64,
-                                       float(64e-5), stream))
+            _lib.check(L.rwkv_wkv7_step_tail(r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(), a.data_ptr(),
+                                             b.data_ptr(), st.data_ptr(), st.data_ptr(), self.rk[l].data_ptr(),
+                                             self.lnw[l].data_ptr(), self.lnb[l].data_ptr(), self.g[l].data_ptr(),
+                                             None, self.tail.data_ptr(), B, H, float(64e-5), stream))
             gemv(self.tail, f"blocks.{l}.att.output.weight", self.y_o)
             gemv(self.xD, f"blocks.{l}.ffn.key.weight", self.y_k)
             gemv(self.xF, f"blocks.{l}.ffn.value.weight", self.y_v)
@@ -299,9 +310,14 @@ def cpu_baseline(model, step, seconds):
     out = np.empty((1, step.H, 64), np.float32)
     ys = {}
 
+    xrkv = step.xrkv.cpu().numpy()
+    rkv_row = {"receptance": 0, "key": 1, "value": 2}
+
     def token():
         for key, (qblk, qsqm, ddm, OUT, IN) in model.host.items():
-            x = xF if IN == step.F else xD
+            part = key.split(".")
+            x = (xF if IN == step.F else
+                 xrkv[rkv_row[part[3]]] if len(part) > 3 and part[2] == "att" and part[3] in rkv_row else xD)
             ys[key] = orc.cpu_sb6_dequant_matvec(x, qblk, qsqm, ddm, OUT, IN, 0, nthreads)
         for l in range(step.L):
             r, w, k, v, a, b = (np.ascontiguousarray(z[l]) for z in vecs)
@@ -409,8 +425,9 @@ def main():
         "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "one-token decode, 0.1B x070 shape: 73 sb6 4-bit GEMVs (r/k/v/o 768x768, "
-                               "ffn 3072x768 + 768x3072, head 65536x768) + 12 WKV-7 steps + 12 tails, batch 1",
+        "config": {"workload": "one-token decode, 0.1B x070 shape: 73 sb6 4-bit GEMVs (r/k/v/o 768x768 with "
+                               "r/k/v fused per layer, ffn 3072x768 + 768x3072, head 65536x768) + 12 WKV-7 "
+                               "steps with their tails fused, batch 1, 61 launches per token",
                    "n_layer": 12, "n_embd": 768, "ffn": 3072, "vocab": 65536, "batch": 1,
                    "weights": "sb6 4-bit from seeded N(0,0.02)", "weight_copies_rotated": args.copies,
                    "hip_graph_per_token": True},

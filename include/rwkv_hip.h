@@ -122,6 +122,20 @@ rwkv_status rwkv_wkv_tail(const float* wkv, const float* r, const float* k, cons
                           const float* rk, const float* lnw, const float* lnb, const float* g,
                           float* out, int64_t N, int64_t H, int64_t S, float eps, void* stream);
 
+/* Decode step and tmix tail in one launch, fp32, head size 64: the state
+ * update of rwkv_wkv7_step followed by rwkv_wkv_tail (S = 64) on its output,
+ * bitwise equal to calling the two.  No single counterpart in the reference:
+ * it replaces the pair wkv7StepForward + wkvTail that X070Generation's tmix
+ * step launches back to back (WKV7DecodeKernels.swift:73-89, 106-178), saving
+ * one launch per layer and token.  r..b, g, out [B,H,64]; h_in/h_out
+ * [B,H,64,64] (may alias; h_in NULL = zeros); rk, lnw, lnb [H·64];
+ * wkv_out [B,H,64] receives the step output when non-NULL. */
+rwkv_status rwkv_wkv7_step_tail(const float* r, const float* w, const float* k, const float* v,
+                                const float* a, const float* b, const float* h_in, float* h_out,
+                                const float* rk, const float* lnw, const float* lnb, const float* g,
+                                float* wkv_out, float* out, int64_t B, int64_t H, float eps,
+                                void* stream);
+
 /* ───────────────────────────── RWKVQuant: dequant / GEMV ───────────────────────────── */
 
 /* sb6 K3 interleave → dense [OUT, IN] in out_dt (combine always in fp32).
@@ -148,6 +162,16 @@ int rwkv_sb6_gemv_applies(int64_t OUT, int64_t IN, int xbits, int super_block, i
 rwkv_status rwkv_sb6_gemv(const float* x, int64_t N,
                           const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
                           float* y, int64_t OUT, int64_t IN, int xbits, void* stream);
+
+/* sb6 counterpart of the sym r/k/v fusion (no counterpart in the reference,
+ * which fuses sym groups only, RwkvqSymGEMV.swift:343-358): K = OUT/out_per
+ * row-concatenated sb6 matrices in one launch; row `o` of input row n uses
+ * x[n·K + o/out_per]; x holds N·K rows.  Same arithmetic per row as
+ * rwkv_sb6_gemv. */
+rwkv_status rwkv_sb6_gemv_fused(const float* x, int64_t N,
+                                const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
+                                float* y, int64_t OUT, int64_t IN, int xbits, int64_t out_per,
+                                void* stream);
 
 /* rwkvqSymGEMVApplies (Sources/RWKVQuant/RwkvqSymGEMV.swift:213-218), same table. */
 int rwkv_sym_gemv_applies(int64_t OUT, int64_t IN, int bits, int64_t rows);
@@ -226,6 +250,8 @@ typedef struct {
     int64_t sb6_gemv;       /* rwkvqSb6GEMVCalls */
     int64_t sym_gemv;       /* rwkvqSymGEMVCalls */
     int64_t sym_fused;      /* rwkvqSymFusedCalls */
+    int64_t step_tail;      /* rwkv_wkv7_step_tail launches (no reference counter) */
+    int64_t sb6_fused;      /* rwkv_sb6_gemv_fused launches (no reference counter) */
 } rwkv_counters;
 
 void rwkv_get_counters(rwkv_counters* out);

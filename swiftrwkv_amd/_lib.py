@@ -37,7 +37,8 @@ class RwkvHipError(RuntimeError):
 
 class Counters(ctypes.Structure):
     _fields_ = [(n, L) for n in ("seq_fwd", "chunk_fwd", "train_fwd", "train_bwd", "step", "tail",
-                                 "sb6_dequant", "sym_dequant", "sb6_gemv", "sym_gemv", "sym_fused")]
+                                 "sb6_dequant", "sym_dequant", "sb6_gemv", "sym_gemv", "sym_fused",
+                                 "step_tail", "sb6_fused")]
 
 
 # name → (restype, argtypes)
@@ -52,12 +53,14 @@ _SIGS = {
     "rwkv_wkv7_train_fwd": (I, [P] * 6 + [I, P, P, P, P, P, L, L, L, P]),
     "rwkv_wkv7_train_bwd": (I, [P] * 6 + [I, P, P, P, P, P] + [P] * 6 + [I, P, L, L, L, I, P]),
     "rwkv_wkv7_step": (I, [P] * 6 + [I, P, P, P, L, L, P]),
+    "rwkv_wkv7_step_tail": (I, [P] * 14 + [L, L, F, P]),
     "rwkv_wkv_tail_applies": (I, [L]),
     "rwkv_wkv_tail": (I, [P] * 9 + [L, L, L, F, P]),
     "rwkv_sb6_dequant": (I, [P, P, P, P, I, L, L, I, P]),
     "rwkv_sym_dequant": (I, [P, P, P, P, I, L, L, I, P]),
     "rwkv_sb6_gemv_applies": (I, [L, L, I, I, L]),
     "rwkv_sb6_gemv": (I, [P, L, P, P, P, P, L, L, I, P]),
+    "rwkv_sb6_gemv_fused": (I, [P, L, P, P, P, P, L, L, I, L, P]),
     "rwkv_sym_gemv_applies": (I, [L, L, I, L]),
     "rwkv_sym_gemv": (I, [P, L, P, P, P, P, L, L, I, L, P]),
     "rwkv_unpack6x8": (I, [P, L, P]),

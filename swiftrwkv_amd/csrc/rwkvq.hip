@@ -522,8 +522,8 @@ GemvPlan plan_gemv(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t N
     pl.NT = N >= 2 ? 4 : 1;
     int64_t G = NU & -NU;   // largest power of two dividing NU
     if (G > 64) G = 64;
-    if (pl.NT == 1)
-        while (G > 1 && NU / (G >> 1) <= 4) G >>= 1;
+    // (independent of the batch, so a row's result does not depend on it)
+    while (G > 1 && NU / (G >> 1) <= 4) G >>= 1;
     pl.geo.G = (int)G;
     pl.geo.R = 64 / pl.geo.G;
     const int64_t per_lane = NU / G;
@@ -707,26 +707,49 @@ int rwkv_sb6_gemv_applies(int64_t OUT, int64_t IN, int xbits, int super_block, i
            OUT % (nsg * rs) == 0;
 }
 
-rwkv_status rwkv_sb6_gemv(const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qsqm,
-                          const uint16_t* ddm, float* y, int64_t OUT, int64_t IN, int xbits, void* stream) {
-    RWKV_REQUIRE(x && qblk && qsqm && ddm && y, RWKV_E_NULL, "sb6_gemv: null buffer");
-    RWKV_REQUIRE(xbits >= 0 && xbits <= 2, RWKV_E_SHAPE, "sb6_gemv: xbits %d outside 0...2", xbits);
-    RWKV_REQUIRE(N >= 1 && N <= INT32_MAX, RWKV_E_SHAPE, "sb6_gemv: rows %lld", (long long)N);
+}  // extern "C"
+
+namespace {
+rwkv_status sb6_gemv_impl(const char* what, const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qsqm,
+                          const uint16_t* ddm, float* y, int64_t OUT, int64_t IN, int xbits, int64_t out_per,
+                          void* stream) {
+    RWKV_REQUIRE(x && qblk && qsqm && ddm && y, RWKV_E_NULL, "%s: null buffer", what);
+    RWKV_REQUIRE(xbits >= 0 && xbits <= 2, RWKV_E_SHAPE, "%s: xbits %d outside 0...2", what, xbits);
+    RWKV_REQUIRE(N >= 1 && N <= INT32_MAX, RWKV_E_SHAPE, "%s: rows %lld", what, (long long)N);
     RWKV_REQUIRE(OUT >= 1 && OUT <= INT32_MAX && IN >= 256 && IN % 256 == 0 && IN <= (1 << 24), RWKV_E_SHAPE,
-                 "sb6_gemv: shape %lldx%lld not taken (IN %% 256 == 0 required)", (long long)OUT, (long long)IN);
+                 "%s: shape %lldx%lld not taken (IN %% 256 == 0 required)", what, (long long)OUT, (long long)IN);
+    RWKV_REQUIRE(out_per >= 1 && OUT % out_per == 0, RWKV_E_SHAPE, "%s: %lld rows do not split into matrices of %lld",
+                 what, (long long)OUT, (long long)out_per);
     RWKV_REQUIRE(OUT * (IN / 32) * (16 + 4 * xbits) < (int64_t(1) << 32), RWKV_E_SHAPE,
-                 "sb6_gemv: packed matrix of %lldx%lld exceeds 4 GiB", (long long)OUT, (long long)IN);
+                 "%s: packed matrix of %lldx%lld exceeds 4 GiB", what, (long long)OUT, (long long)IN);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const Sb6Fmt<0>::Ptr P{(const uint32_t*)qblk, (const uint16_t*)qsqm, (const uint32_t*)ddm};
+    const int64_t NK = OUT / out_per;
     bool ok;
     switch (xbits) {
-        case 0: ok = run_gemv<Sb6Fmt<0>>(OUT, IN, OUT, N, 1, st, x, P, y, OUT); break;
-        case 1: ok = run_gemv<Sb6Fmt<1>>(OUT, IN, OUT, N, 1, st, x, {P.q, P.sm, P.dd}, y, OUT); break;
-        default: ok = run_gemv<Sb6Fmt<2>>(OUT, IN, OUT, N, 1, st, x, {P.q, P.sm, P.dd}, y, OUT); break;
+        case 0: ok = run_gemv<Sb6Fmt<0>>(OUT, IN, out_per, N, NK, st, x, P, y, out_per); break;
+        case 1: ok = run_gemv<Sb6Fmt<1>>(OUT, IN, out_per, N, NK, st, x, {P.q, P.sm, P.dd}, y, out_per); break;
+        default: ok = run_gemv<Sb6Fmt<2>>(OUT, IN, out_per, N, NK, st, x, {P.q, P.sm, P.dd}, y, out_per); break;
     }
-    RWKV_REQUIRE(ok, RWKV_E_UNSUPPORTED, "sb6_gemv: no kernel variant for %lldx%lld", (long long)OUT, (long long)IN);
-    rwkv_status s = launch_status("sb6_gemv launch");
+    RWKV_REQUIRE(ok, RWKV_E_UNSUPPORTED, "%s: no kernel variant for %lldx%lld", what, (long long)OUT, (long long)IN);
+    return launch_status(what);
+}
+}  // namespace
+
+extern "C" {
+
+rwkv_status rwkv_sb6_gemv(const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qsqm,
+                          const uint16_t* ddm, float* y, int64_t OUT, int64_t IN, int xbits, void* stream) {
+    const rwkv_status s = sb6_gemv_impl("sb6_gemv", x, N, qblk, qsqm, ddm, y, OUT, IN, xbits, OUT, stream);
     if (s == RWKV_OK) rwkv::counters().sb6_gemv++;
+    return s;
+}
+
+rwkv_status rwkv_sb6_gemv_fused(const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qsqm,
+                                const uint16_t* ddm, float* y, int64_t OUT, int64_t IN, int xbits, int64_t out_per,
+                                void* stream) {
+    const rwkv_status s = sb6_gemv_impl("sb6_gemv_fused", x, N, qblk, qsqm, ddm, y, OUT, IN, xbits, out_per, stream);
+    if (s == RWKV_OK) rwkv::counters().sb6_fused++;
     return s;
 }
 

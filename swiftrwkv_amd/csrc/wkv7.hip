@@ -540,6 +540,70 @@ __global__ __launch_bounds__(64) void wkv_tail_kernel(
     }
 }
 
+// ─────────────────────────────── decode: step + tail in one launch ───────────────────────────────
+// One workgroup of four waves per (row, head).  Wave `blk` runs the T = 1
+// path of wkv7_fwd_kernel for value rows 16·blk..16·blk+15 (same device code,
+// so state and wkv are bitwise those of rwkv_wkv7_step); the head's 64 wkv
+// values meet in LDS and wave 0 applies the tail with wkv_tail_kernel's exact
+// operation sequence for S = 64.
+__global__ __launch_bounds__(256) void wkv7_step_tail_kernel(
+    const float* __restrict__ r, const float* __restrict__ w, const float* __restrict__ k,
+    const float* __restrict__ v, const float* __restrict__ a, const float* __restrict__ b,
+    const float* __restrict__ h_in, float* __restrict__ h_out, const float* __restrict__ rk,
+    const float* __restrict__ lnw, const float* __restrict__ lnb, const float* __restrict__ g,
+    float* __restrict__ wkv_out, float* __restrict__ out, int H, float eps) {
+    __shared__ float ys[D];
+    const int blk = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int ri = l & 15, gq = l >> 4;
+    const int bh = blockIdx.x;
+    const int hi = bh % H;
+    const int row = 16 * blk + ri;
+    const int vidx = 16 * gq + ri;
+    const int64_t base0 = (int64_t)bh * D;   // [B, H, 64]
+    const int64_t sbase = (int64_t)bh * D * D + (int64_t)row * D + 16 * gq;
+
+    float S[16], N[16];
+    if (h_in) {
+        const float4* src = reinterpret_cast<const float4*>(h_in + sbase);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const float4 f = src[m];
+            S[4 * m] = f.x; S[4 * m + 1] = f.y; S[4 * m + 2] = f.z; S[4 * m + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < 16; ++c) S[c] = 0.0f;
+    }
+    const float A = a[base0 + vidx], W = w[base0 + vidx], K = k[base0 + vidx], Bv = b[base0 + vidx];
+    const float R = r[base0 + vidx], V = v[base0 + row];
+    float p = 0.0f;
+    fwd_dot16(S, A, p);
+    const float sa = rowsum4(p);
+    float y = 0.0f;
+    p = 0.0f;
+    fwd_update16(S, N, K, Bv, W, R, A, V, sa, y, p);
+    y = rowsum4(y);
+    float4* dst = reinterpret_cast<float4*>(h_out + sbase);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) dst[m] = make_float4(N[4 * m], N[4 * m + 1], N[4 * m + 2], N[4 * m + 3]);
+    if (gq == 0) {
+        ys[row] = y;
+        if (wkv_out) wkv_out[base0 + row] = y;
+    }
+    __syncthreads();
+    if (blk == 0) {
+        const int64_t e = base0 + l, he = (int64_t)hi * D + l;
+        const float x = ys[l];
+        const float mean = wave_total(0.0f + x) / (float)D;
+        const float dd = x - mean;
+        const float inv = 1.0f / sqrtf(wave_total(fmaf(dd, dd, 0.0f)) / (float)D + eps);
+        const float dp = wave_total(fmaf(r[e] * k[e], rk[he], 0.0f));
+        const float nrm = (x - mean) * inv;
+        const float yo = fmaf(dp, v[e], fmaf(nrm, lnw[he], lnb[he]));
+        out[e] = yo * g[e];
+    }
+}
+
 // ─────────────────────────────── host dispatch ───────────────────────────────
 rwkv_status launch_status(const char* what) {
     hipError_t e = hipGetLastError();
@@ -674,6 +738,21 @@ rwkv_status rwkv_wkv7_train_bwd(const void* r, const void* w, const void* k, con
 #undef RWKV_BWD_LAUNCH
     s = launch_status("wkv7 backward launch");
     if (s == RWKV_OK) rwkv::counters().train_bwd++;
+    return s;
+}
+
+rwkv_status rwkv_wkv7_step_tail(const float* r, const float* w, const float* k, const float* v, const float* a,
+                                const float* b, const float* h_in, float* h_out, const float* rk, const float* lnw,
+                                const float* lnb, const float* g, float* wkv_out, float* out, int64_t B, int64_t H,
+                                float eps, void* stream) {
+    RWKV_REQUIRE(r && w && k && v && a && b && h_out && rk && lnw && lnb && g && out, RWKV_E_NULL,
+                 "wkv7_step_tail: null buffer");
+    RWKV_REQUIRE(B >= 1 && H >= 1 && B * H <= INT32_MAX, RWKV_E_SHAPE, "wkv7_step_tail: bad B (%lld) / H (%lld)",
+                 (long long)B, (long long)H);
+    rwkv::launch(wkv7_step_tail_kernel, dim3((unsigned)(B * H)), dim3(256), reinterpret_cast<hipStream_t>(stream),
+                 r, w, k, v, a, b, h_in, h_out, rk, lnw, lnb, g, wkv_out, out, (int)H, eps);
+    rwkv_status s = launch_status("wkv7_step_tail launch");
+    if (s == RWKV_OK) rwkv::counters().step_tail++;
     return s;
 }
 

@@ -338,3 +338,34 @@ def wkv_tail(wkv, r, k, v, r_k, ln_weight, ln_bias, gate, n_head: int, head_size
     _lib.call("rwkv_wkv_tail", _ptr(wkv_), _ptr(r_), _ptr(k_), _ptr(v_), _ptr(rk_), _ptr(lw_), _ptr(lb_), _ptr(g_),
               _ptr(out), rows, n_head, head_size, float(eps), _stream(wkv_))
     return out
+
+
+def wkv7_step_tail_(r, w, k, v, a, b, h, r_k, ln_weight, ln_bias, gate, eps: float = 64e-5,
+                    wkv_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode step followed by the tmix tail in one launch, fp32: h [B,H,S,S]
+    is updated in place exactly as by wkv7_step_, and the result equals
+    wkv_tail(wkv7_step_(...), r, k, v, ...) bitwise.  The pair
+    wkv7StepForward + wkvTail of the reference's tmix decode step
+    (WKV7DecodeKernels.swift:73-89, 106-178).  r..b, gate [B,H,S]; r_k,
+    ln_weight, ln_bias [H·S].  `wkv_out` [B,H,S], when given, receives the step
+    output.  Returns [B, H·S]."""
+    xs = [r, w, k, v, a, b, gate]
+    if any(x.dim() != 3 for x in xs):
+        raise ValueError("step+tail: r, w, k, v, a, b and gate must be [B,H,S]")
+    B, H, S = r.shape
+    if S != WKV7_HEAD_SIZE or any(tuple(x.shape) != (B, H, S) for x in xs):
+        raise ValueError(f"step+tail: inputs must share shape [B,H,{WKV7_HEAD_SIZE}]")
+    if h.dtype != torch.float32 or not h.is_contiguous() or tuple(h.shape) != (B, H, S, S) or h.data_ptr() % 16:
+        raise ValueError("in-place state must be a contiguous fp32 [B,H,S,S] tensor")
+    dev = r.device
+    r_, w_, k_, v_, a_, b_, g_ = (_aligned(x.to(device=dev, dtype=torch.float32)) for x in xs)
+    rk_, lw_, lb_ = (_aligned(x.reshape(H * S).to(device=dev, dtype=torch.float32)) for x in (r_k, ln_weight, ln_bias))
+    if wkv_out is not None and (wkv_out.dtype != torch.float32 or not wkv_out.is_contiguous()
+                                or tuple(wkv_out.shape) != (B, H, S)):
+        raise ValueError("wkv_out must be a contiguous fp32 [B,H,S] tensor")
+    out = torch.empty((B, H * S), dtype=torch.float32, device=dev)
+    _lib.call("rwkv_wkv7_step_tail", _ptr(r_), _ptr(w_), _ptr(k_), _ptr(v_), _ptr(a_), _ptr(b_), _ptr(h), _ptr(h),
+              _ptr(rk_), _ptr(lw_), _ptr(lb_), _ptr(g_), _ptr(wkv_out) if wkv_out is not None else None, _ptr(out),
+              B, H, float(eps), _stream(r_))
+    return out
+

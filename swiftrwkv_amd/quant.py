@@ -324,16 +324,31 @@ def rwkvq_sb6_gemv_applies(out_features: int, in_features: int, xbits: int, supe
     return bool(_lib.lib().rwkv_sb6_gemv_applies(out_features, in_features, xbits, super_block, rows))
 
 
-def rwkvq_sb6_gemv(x, qblk, qsqm, ddm, out_features: int, in_features: int, xbits: int) -> torch.Tensor:
+def rwkvq_sb6_gemv(x, qblk, qsqm, ddm, out_features: int, in_features: int, xbits: int,
+                   out_per: Optional[int] = None) -> torch.Tensor:
     """y [N, OUT] = x [N, IN] · Wᵀ straight from the K3 bytes (RwkvqSb6GEMV.swift:170-190).
-    The reference takes N = 1; here N rows share one weight pass."""
+    The reference takes N = 1; here N rows share one weight pass.  With
+    `out_per` (an extension: the reference fuses sym groups only) the K =
+    OUT/out_per row-concatenated matrices run in one launch: x holds N·K rows
+    and row o of input n reads x[n·K + o/out_per]."""
     if x.dim() != 2 or x.shape[1] != in_features:
         raise ValueError(f"sb6-GEMV: input {tuple(x.shape)}, expected [N, {in_features}]")
+    per = out_features if out_per is None else out_per
+    if per < 1 or out_features % per:
+        raise ValueError(f"sb6-GEMV: {out_features} rows do not split into matrices of {per}")
+    K = out_features // per
+    if x.shape[0] % K:
+        raise ValueError(f"sb6-GEMV: {x.shape[0]} input rows do not split over {K} fused matrices")
+    N = x.shape[0] // K
     x32 = _aligned(x.to(torch.float32))
     qblk, qsqm, ddm = _sb6_bufs(qblk, qsqm, ddm, out_features, in_features, xbits)
-    y = torch.empty((x.shape[0], out_features), dtype=torch.float32, device=x.device)
-    _lib.call("rwkv_sb6_gemv", x32.data_ptr(), x.shape[0], qblk.data_ptr(), qsqm.data_ptr(), ddm.data_ptr(),
-              y.data_ptr(), out_features, in_features, xbits, _stream(x32))
+    y = torch.empty((N, out_features), dtype=torch.float32, device=x.device)
+    if out_per is None:
+        _lib.call("rwkv_sb6_gemv", x32.data_ptr(), N, qblk.data_ptr(), qsqm.data_ptr(), ddm.data_ptr(),
+                  y.data_ptr(), out_features, in_features, xbits, _stream(x32))
+    else:
+        _lib.call("rwkv_sb6_gemv_fused", x32.data_ptr(), N, qblk.data_ptr(), qsqm.data_ptr(), ddm.data_ptr(),
+                  y.data_ptr(), out_features, in_features, xbits, per, _stream(x32))
     return y
 
 
@@ -368,6 +383,19 @@ def rwkvq_sym_gemv(x, qblk, qs, d, out_features: int, in_features: int, bits: in
 # ───────────────────────────── sidecar ─────────────────────────────
 
 @dataclass
+class RwkvqSb6FusedGroup:
+    """Row-concatenated sb6 matrices of one fusion group (the sb6 counterpart
+    of RwkvqSymFusedGroup)."""
+    keys: List[str]
+    qblk: torch.Tensor
+    qsqm: torch.Tensor
+    ddm: torch.Tensor
+    out_per: int
+    in_features: int
+    xbits: int
+
+
+@dataclass
 class RwkvqSymFusedGroup:
     """RwkvqSymGEMV.swift:282-291."""
     keys: List[str]
@@ -386,12 +414,14 @@ class RwkvqSidecar:
 
     def __init__(self, arrays: Dict[str, torch.Tensor], tensors: Dict[str, RwkvqTensorInfo], naming: str,
                  n_layer: int, n_embd: int, head_size: int, vocab_size: int,
-                 sym_fused: Optional[Dict[str, RwkvqSymFusedGroup]] = None):
+                 sym_fused: Optional[Dict[str, RwkvqSymFusedGroup]] = None,
+                 sb6_fused: Optional[Dict[str, RwkvqSb6FusedGroup]] = None):
         self.arrays = arrays
         self.tensors = tensors
         self.naming = naming
         self.n_layer, self.n_embd, self.head_size, self.vocab_size = n_layer, n_embd, head_size, vocab_size
         self.sym_fused = dict(sym_fused or {})
+        self.sb6_fused = dict(sb6_fused or {})
 
     # RwkvqFile.swift:220-228
     @classmethod
@@ -597,7 +627,8 @@ class RwkvqSidecar:
         a = {n: v for n, v in self.arrays.items() if n.split("::", 1)[0] in keep}
         return RwkvqSidecar(a, {k: v for k, v in self.tensors.items() if k in keep}, self.naming, self.n_layer,
                             self.n_embd, self.head_size, self.vocab_size,
-                            {g: v for g, v in self.sym_fused.items() if all(k in keep for k in v.keys)})
+                            {g: v for g, v in self.sym_fused.items() if all(k in keep for k in v.keys)},
+                            {g: v for g, v in self.sb6_fused.items() if all(k in keep for k in v.keys)})
 
     @property
     def packed_bytes(self) -> int:
@@ -671,7 +702,30 @@ class RwkvqSidecar:
             if g is not None:
                 fused[gid] = g
         return RwkvqSidecar(a, dict(self.tensors), self.naming, self.n_layer, self.n_embd, self.head_size,
-                            self.vocab_size, fused)
+                            self.vocab_size, fused, self.sb6_fused)
+
+    def fusing_sb6(self, groups: Dict[str, List[str]]) -> "RwkvqSidecar":
+        """fusing_sym for sb6 groups (an extension: r/k/v of an sb6 model in
+        one launch).  Member buffers become row slices of the group buffer."""
+        a = dict(self.arrays)
+        fused = dict(self.sb6_fused)
+        for gid, keys in groups.items():
+            if gid in fused:
+                continue
+            g = _fuse_sb6_group(keys, self.tensors, a)
+            if g is not None:
+                fused[gid] = g
+        return RwkvqSidecar(a, dict(self.tensors), self.naming, self.n_layer, self.n_embd, self.head_size,
+                            self.vocab_size, self.sym_fused, fused)
+
+    def sb6_gemv_fused(self, gid: str, xstack: torch.Tensor) -> Optional[torch.Tensor]:
+        """K sb6 projections in one launch: xstack [K, IN] → [K, out_per]."""
+        g = self.sb6_fused.get(gid)
+        if g is None or xstack.dim() != 2 or tuple(xstack.shape) != (len(g.keys), g.in_features):
+            return None
+        K = len(g.keys)
+        y = rwkvq_sb6_gemv(xstack, g.qblk, g.qsqm, g.ddm, g.out_per * K, g.in_features, g.xbits, out_per=g.out_per)
+        return y.reshape(K, g.out_per)
 
     def sym_gemv_fused(self, gid: str, xstack: torch.Tensor) -> Optional[torch.Tensor]:
         """K projections in one launch: xstack [K, IN] → [K, out_per] (RwkvqSymGEMV.swift:343-358)."""
@@ -681,6 +735,32 @@ class RwkvqSidecar:
         K = len(g.keys)
         y = rwkvq_sym_gemv(xstack, g.qblk, g.qs, g.d, g.out_per * K, g.in_features, g.bits, out_per=g.out_per)
         return y.reshape(K, g.out_per)
+
+
+def _fuse_sb6_group(keys: List[str], tensors: Dict[str, RwkvqTensorInfo],
+                    arrays: Dict[str, torch.Tensor]) -> Optional[RwkvqSb6FusedGroup]:
+    """sb6 counterpart of _fuse_sym_group: same shape and xbits, every member
+    taken by the sb6 GEMV.  None (arrays untouched) when the group does not
+    qualify."""
+    if len(keys) < 2:
+        return None
+    first = tensors.get(keys[0])
+    if first is None or first.kind != RwkvqKind.sb6:
+        return None
+    for k in keys:
+        t = tensors.get(k)
+        if (t is None or t.kind != RwkvqKind.sb6 or t.shape != first.shape or t.xbits != first.xbits
+                or t.super_block != first.super_block
+                or any(f"{k}::{f}" not in arrays for f in ("qblk", "qsqm", "ddm"))):
+            return None
+    if not rwkvq_sb6_gemv_applies(first.out_features, first.in_features, first.xbits, first.super_block, 1):
+        return None
+    OUT = first.out_features
+    cat = {f: torch.cat([arrays[f"{k}::{f}"] for k in keys], 0) for f in ("qblk", "qsqm", "ddm")}
+    for i, k in enumerate(keys):
+        for f in ("qblk", "qsqm", "ddm"):
+            arrays[f"{k}::{f}"] = cat[f][i * OUT:(i + 1) * OUT]
+    return RwkvqSb6FusedGroup(list(keys), cat["qblk"], cat["qsqm"], cat["ddm"], OUT, first.in_features, first.xbits)
 
 
 def _fuse_sym_group(keys: List[str], tensors: Dict[str, RwkvqTensorInfo],

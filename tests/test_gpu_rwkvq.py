@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from swiftrwkv_amd import quant as Q
+from swiftrwkv_amd import _lib, quant as Q
 from tests.test_oracle import GOLD, make_sb6, make_sym
 
 pytestmark = pytest.mark.gpu
@@ -153,6 +153,27 @@ def test_sym_gemv_matches_fp64(orc, bits, OUT, IN):
         assert rel(want, y.cpu().numpy()) < GEMV_TOL, N
 
 
+@pytest.mark.parametrize("xbits", [0, 1, 2])
+def test_fused_sb6_gemv_equals_separate_bitwise(orc, xbits):
+    case(f"fused sb6 r/k/v xbits={xbits}")
+    OUT, IN, Kn = 768, 768, 3
+    parts = [sb6_tensor(orc, OUT, IN, xbits, seed=xbits * 10 + i) for i in range(Kn)]
+    qblk, qsqm, ddm = (np.concatenate([p[j] for p in parts]) for j in range(3))
+    rng = np.random.default_rng(22)
+    for N in (1, 2):
+        x = rng.standard_normal((N * Kn, IN)).astype(np.float32)
+        _lib.reset_counters()
+        fused = Q.rwkvq_sb6_gemv(dev(x), dev(qblk), dev(qsqm), dev(ddm), OUT * Kn, IN, xbits, out_per=OUT)
+        assert _lib.counters()["sb6_fused"] == 1
+        assert fused.shape == (N, OUT * Kn)
+        for i, p in enumerate(parts):
+            xi = x.reshape(N, Kn, IN)[:, i]
+            alone = Q.rwkvq_sb6_gemv(dev(xi), *[dev(z) for z in p], OUT, IN, xbits)
+            assert torch.equal(fused[:, i * OUT:(i + 1) * OUT], alone)
+    with pytest.raises(ValueError):
+        Q.rwkvq_sb6_gemv(dev(x[:2]), dev(qblk), dev(qsqm), dev(ddm), OUT * Kn, IN, xbits, out_per=OUT)
+
+
 @pytest.mark.parametrize("bits", [8, 6])
 def test_fused_sym_gemv_equals_separate_bitwise(orc, bits):
     case(f"fused r/k/v bits={bits}")
@@ -230,6 +251,15 @@ def test_sidecar_end_to_end(tmp_path, orc, kind, bits):
     if kind == "sb6":
         assert sc.sb6_gemv(key, torch.zeros((2, 256), device=DEV)) is None
         assert not sc.sym_fused
+        sf = sc.fusing_sb6(groups)
+        assert set(sf.sb6_fused) == {"att0"}
+        xs = torch.randn((3, 256), device=DEV)
+        fused = sf.sb6_gemv_fused("att0", xs)
+        for i, k in enumerate(groups["att0"]):
+            assert torch.equal(fused[i:i + 1], sf.sb6_gemv(k, xs[i:i + 1]))
+            assert torch.equal(sf.dequantize(k), sc.dequantize(k))
+        assert sf.sb6_gemv_fused("att0", torch.zeros((2, 256), device=DEV)) is None
+        assert not sf.fusing_sb6({"x": ["blocks.0.att.key.weight", "blocks.0.ffn.key.weight"]}).sb6_fused.keys() - {"att0"}
     else:
         assert sc.sym_gemv(key, torch.zeros((5, 256), device=DEV)) is None
         assert set(sc.sym_fused) == {"att0"}

@@ -209,6 +209,41 @@ def test_tail_matches_oracle(orc):
         K.wkv_tail(dev(wkv), dev(r), dev(k), dev(v), dev(rk), dev(lnw), dev(lnb), dev(g), H, 48, rows=N)
 
 
+@pytest.mark.parametrize("B,H", [(1, 12), (4, 3), (2, 32)])
+def test_step_tail_equals_step_then_tail_bitwise(orc, B, H):
+    case(f"fused step+tail B={B} H={H}")
+    rng = np.random.default_rng(B * 100 + H)
+    xs, hs = zip(*[decode_inputs(H, 10 * B + i) for i in range(B)])
+    x = [dev(np.stack([z[j] for z in xs])) for j in range(6)]          # [B,H,64] each
+    h0 = dev(np.stack(hs))
+    D = H * 64
+    rk = dev((rng.standard_normal((H, 64)) * 0.1).astype(np.float32))
+    lnw = dev((rng.standard_normal(D) * 0.5 + 1).astype(np.float32))
+    lnb = dev((rng.standard_normal(D) * 0.1).astype(np.float32))
+    g = dev(rng.standard_normal((B, H, 64)).astype(np.float32))
+    h_sep, h_fused = h0.clone(), h0.clone()
+    wkv = K.wkv7_step_(*x, h_sep)
+    want = K.wkv_tail(wkv, x[0], x[2], x[3], rk, lnw, lnb, g, H, 64, rows=B)
+    _lib.reset_counters()
+    wkv_f = torch.empty_like(wkv)
+    got = K.wkv7_step_tail_(*x, h_fused, rk, lnw, lnb, g, wkv_out=wkv_f)
+    assert _lib.counters()["step_tail"] == 1
+    assert same(got, want) and same(h_fused, h_sep) and same(wkv_f, wkv)
+    # against the oracle: fp64 tail of the kernel's wkv
+    ref = orc.wkv_tail_f64(host(wkv), *[host(z) for z in (x[0], x[2], x[3], rk, lnw, lnb, g)], B, H, 64)
+    assert rel(ref, host(got)) < TOL
+    # NULL initial state through the C ABI = zero state
+    hz = torch.zeros_like(h0)
+    want0 = K.wkv7_step_tail_(*x, hz, rk, lnw, lnb, g)
+    h_out = torch.full_like(h0, 7.0)
+    out0 = torch.empty((B, D), device=DEV)
+    _lib.call("rwkv_wkv7_step_tail", *[z.data_ptr() for z in x], None, h_out.data_ptr(), rk.data_ptr(),
+              lnw.data_ptr(), lnb.data_ptr(), g.data_ptr(), None, out0.data_ptr(), B, H, 64e-5,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert same(out0, want0) and same(h_out, hz)
+
+
 # ───────────────────────────── backward ─────────────────────────────
 
 def train_case(B=2, T=48, H=3, seed=0):
