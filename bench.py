@@ -32,6 +32,10 @@ sys.path.insert(0, ROOT)
 
 METRIC = "WKV-7 tokens/s (fwd, fwd+bwd); .rwkvq GEMV GB/s; 1.5B decode tok/s"
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per launch of the head GEMV from two rocprofv3 counter passes
+# (FETCH_SIZE, WRITE_SIZE) over `bench.py --mode kernels`, calibrated against a
+# 256 MiB device copy; see profiles/hbm_traffic_head_gemv_and_wkv7.md.
+HEAD_GEMV_TRAFFIC_BYTES = 29449768
 VALU_PEAK_TFLOPS = 157.3
 
 
@@ -432,7 +436,7 @@ def main():
                    "weights": "sb6 4-bit from seeded N(0,0.02)", "weight_copies_rotated": args.copies,
                    "hip_graph_per_token": True},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": HEAD_GEMV_TRAFFIC_BYTES,
                      "kernel": "sb6_gemv head 65536x768 (4-bit), bytes = packed weights + x + y"},
         "cpu_baseline": cpu,
         "extra": extra,
