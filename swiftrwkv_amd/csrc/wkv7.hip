@@ -92,12 +92,21 @@ __device__ __forceinline__ float rowsum4(float x) {
 // Forward update of 8 state elements (columns c0..c0+7 of the lane's group):
 //   n = k·v ; n += b·sa ; n += w·S          (new state, one rounding per FMA)
 //   y += r·n ; p += a'·n                    (a' = next step's a)
-#define RWKV_UPD(c, S, N)                                    \
-    "v_mul_f32_dpp %[" N "], %[K], %[vv]" RWKV_BC(c)         \
-    "v_fmac_f32_dpp %[" N "], %[B], %[sa]" RWKV_BC(c)        \
-    "v_fmac_f32_dpp %[" N "], %[W], %[" S "]" RWKV_BC(c)     \
-    "v_fmac_f32_dpp %[y], %[R], %[" N "]" RWKV_BC(c)         \
-    "v_fmac_f32_dpp %[p], %[A], %[" N "]" RWKV_BC(c)
+// Issued stage by stage over the 8 elements, so neighbouring instructions are
+// independent (the y and p chains alternate).
+#define RWKV_MUL(c, N) "v_mul_f32_dpp %[" N "], %[K], %[vv]" RWKV_BC(c)
+#define RWKV_FB(c, N) "v_fmac_f32_dpp %[" N "], %[B], %[sa]" RWKV_BC(c)
+#define RWKV_FW(c, S, N) "v_fmac_f32_dpp %[" N "], %[W], %[" S "]" RWKV_BC(c)
+#define RWKV_YP(c, N) "v_fmac_f32_dpp %[y], %[R], %[" N "]" RWKV_BC(c) "v_fmac_f32_dpp %[p], %[A], %[" N "]" RWKV_BC(c)
+#define RWKV_UPD8(c0, c1, c2, c3, c4, c5, c6, c7)                                                              \
+    RWKV_MUL(c0, "n0") RWKV_MUL(c1, "n1") RWKV_MUL(c2, "n2") RWKV_MUL(c3, "n3")                                 \
+    RWKV_MUL(c4, "n4") RWKV_MUL(c5, "n5") RWKV_MUL(c6, "n6") RWKV_MUL(c7, "n7")                                 \
+    RWKV_FB(c0, "n0") RWKV_FB(c1, "n1") RWKV_FB(c2, "n2") RWKV_FB(c3, "n3")                                     \
+    RWKV_FB(c4, "n4") RWKV_FB(c5, "n5") RWKV_FB(c6, "n6") RWKV_FB(c7, "n7")                                     \
+    RWKV_FW(c0, "s0", "n0") RWKV_FW(c1, "s1", "n1") RWKV_FW(c2, "s2", "n2") RWKV_FW(c3, "s3", "n3")             \
+    RWKV_FW(c4, "s4", "n4") RWKV_FW(c5, "s5", "n5") RWKV_FW(c6, "s6", "n6") RWKV_FW(c7, "s7", "n7")             \
+    RWKV_YP(c0, "n0") RWKV_YP(c1, "n1") RWKV_YP(c2, "n2") RWKV_YP(c3, "n3")                                     \
+    RWKV_YP(c4, "n4") RWKV_YP(c5, "n5") RWKV_YP(c6, "n6") RWKV_YP(c7, "n7")
 
 #define RWKV_UPD_OPERANDS(S, N, o)                                                                              \
     : [n0] "=&v"(N[o + 0]), [n1] "=&v"(N[o + 1]), [n2] "=&v"(N[o + 2]), [n3] "=&v"(N[o + 3]),                    \
@@ -109,14 +118,8 @@ __device__ __forceinline__ float rowsum4(float x) {
 
 __device__ __forceinline__ void fwd_update16(const float (&S)[16], float (&N)[16], float K, float B, float W,
                                              float R, float A, float vv, float sa, float& y, float& p) {
-    asm("s_nop 1\n\t"
-        RWKV_UPD(0, "s0", "n0") RWKV_UPD(1, "s1", "n1") RWKV_UPD(2, "s2", "n2") RWKV_UPD(3, "s3", "n3")
-        RWKV_UPD(4, "s4", "n4") RWKV_UPD(5, "s5", "n5") RWKV_UPD(6, "s6", "n6") RWKV_UPD(7, "s7", "n7")
-        RWKV_UPD_OPERANDS(S, N, 0));
-    asm("s_nop 1\n\t"
-        RWKV_UPD(8, "s0", "n0") RWKV_UPD(9, "s1", "n1") RWKV_UPD(10, "s2", "n2") RWKV_UPD(11, "s3", "n3")
-        RWKV_UPD(12, "s4", "n4") RWKV_UPD(13, "s5", "n5") RWKV_UPD(14, "s6", "n6") RWKV_UPD(15, "s7", "n7")
-        RWKV_UPD_OPERANDS(S, N, 8));
+    asm("s_nop 1\n\t" RWKV_UPD8(0, 1, 2, 3, 4, 5, 6, 7) RWKV_UPD_OPERANDS(S, N, 0));
+    asm("s_nop 1\n\t" RWKV_UPD8(8, 9, 10, 11, 12, 13, 14, 15) RWKV_UPD_OPERANDS(S, N, 8));
 }
 
 // p += Σ_c a_c·S_c over the lane's 16 columns (the first step's sa partial).
@@ -166,7 +169,18 @@ __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
     using E = typename In::E;
     const int l = threadIdx.x;
     const int ri = l & 15, g = l >> 4;
-    const int bh = blockIdx.x >> 2, blk = blockIdx.x & 3;
+    // Workgroups are dealt round-robin to the 8 XCDs (each with its own L2):
+    // when the grid allows, the four waves of a head get ids congruent mod 8,
+    // so they share one XCD and each step vector is fetched from HBM once.
+    int bh, blk;
+    if ((gridDim.x & 31) == 0) {
+        const int id = blockIdx.x, xcd = id & 7, slot = id >> 3;
+        bh = (slot >> 2) * 8 + xcd;
+        blk = slot & 3;
+    } else {
+        bh = blockIdx.x >> 2;
+        blk = blockIdx.x & 3;
+    }
     const int bi = bh / H, hi = bh - bi * H;
     const int row = 16 * blk + ri;
     const uint32_t vidx = 16 * g + ri;   // step-vector element this lane broadcasts
@@ -195,15 +209,30 @@ __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
 
     // ring slot: a, w, k, b, r (broadcast sources), v (own row), as raw elements
     E ring[CH][6];
-    auto fetch = [&](E (&slot)[6], int t) {
-        const uint32_t o = (uint32_t)min(t, T - 1) * strideT;
-        slot[0] = in.a[o + vidx];
-        slot[1] = in.w[o + vidx];
-        slot[2] = in.k[o + vidx];
-        slot[3] = in.b[o + vidx];
-        slot[4] = in.r[o + vidx];
-        slot[5] = in.v[o + row];
+    // Buffer addressing: a descriptor per input (SGPRs), the per-lane part a
+    // fixed VGPR offset, the per-step part a scalar offset — no per-load VALU.
+    const uint32_t esz = (uint32_t)sizeof(E);
+    const uint32_t span = (uint32_t)T * strideT * esz - (uint32_t)hi * D * esz;   // bytes from this head's base
+    const uint32_t voff = vidx * esz, roff = (uint32_t)row * esz;
+    auto rsrc = [&](const void* p, uint32_t n) { return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)n, 0x00020000); };
+    const __amdgpu_buffer_rsrc_t ra = rsrc(in.a, span), rw = rsrc(in.w, span), rk_ = rsrc(in.k, span),
+                                 rb = rsrc(in.b, span), rr = rsrc(in.r, span), rv = rsrc(in.v, span);
+    auto ld = [&](__amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t so) -> E {
+        if constexpr (sizeof(E) == 2) return (E)__builtin_amdgcn_raw_buffer_load_b16(rs, vo, so, 0);
+        else return __builtin_bit_cast(E, __builtin_amdgcn_raw_buffer_load_b32(rs, vo, so, 0));
     };
+    auto fetch = [&](E (&slot)[6], int t) __attribute__((always_inline)) {
+        const uint32_t so = (uint32_t)min(t, T - 1) * strideT * esz;
+        slot[0] = ld(ra, voff, so);
+        slot[1] = ld(rw, voff, so);
+        slot[2] = ld(rk_, voff, so);
+        slot[3] = ld(rb, voff, so);
+        slot[4] = ld(rr, voff, so);
+        slot[5] = ld(rv, roff, so);
+    };
+    const uint32_t ospan = (uint32_t)T * strideT * 4u - (uint32_t)hi * D * 4u;
+    const __amdgpu_buffer_rsrc_t ro_ = rsrc(outp, ospan), rs_ = rsrc(EMIT_SA ? sap : outp, ospan);
+    const uint32_t orow = (uint32_t)row * 4u;
 #pragma unroll
     for (int s = 0; s < 8; ++s) fetch(ring[s], s);
 
@@ -211,8 +240,11 @@ __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
     fwd_dot16(S[0], In::cvt(ring[0][0]), p);
 
     // one step at chunk position s (compile-time) and time t
-    auto step = [&](auto sc, int t, int c) {
+    auto step = [&](auto sc, int t, int c) __attribute__((always_inline)) {
         constexpr int s = decltype(sc)::value;
+        // Steps stay in program order (no store sinking / load hoisting across
+        // them), so every wait for a prefetched value is a small exact count.
+        __builtin_amdgcn_sched_barrier(0);
         fetch(ring[(s + 8) & (CH - 1)], t + 8);
         const float sa = rowsum4(p);
         float y = 0.0f;
@@ -221,9 +253,10 @@ __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
         fwd_update16(S[s & 1], S[(s + 1) & 1], In::cvt(sl[2]), In::cvt(sl[3]), In::cvt(sl[1]), In::cvt(sl[4]),
                      In::cvt(ring[(s + 1) & (CH - 1)][0]), In::cvt(sl[5]), sa, y, p);
         y = rowsum4(y);
-        const uint32_t o = (uint32_t)t * strideT + row;
-        outp[o] = y;   // the four lanes of a row store the same bits
-        if constexpr (EMIT_SA) sap[o] = sa;
+        const uint32_t so = (uint32_t)t * strideT * 4u;
+        // the four lanes of a row store the same bits
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ro_, orow, so, 0);
+        if constexpr (EMIT_SA) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sa), rs_, orow, so, 0);
         if constexpr (EMIT_CK && s == CH - 1) {
             float4* dst = reinterpret_cast<float4*>(ckpt + ((int64_t)bh * NC + c) * D * D + (int64_t)row * D + 16 * g);
 #pragma unroll
@@ -231,19 +264,23 @@ __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
                 dst[m] = make_float4(S[0][4 * m], S[0][4 * m + 1], S[0][4 * m + 2], S[0][4 * m + 3]);
         }
     };
-    auto body = [&](int c, int n) {
+    auto body = [&](int c, int n) __attribute__((always_inline)) {
         const int t0 = c * CH;
         [&]<int... s>(std::integer_sequence<int, s...>) {
             ((n > s ? step(std::integral_constant<int, s>{}, t0 + s, c) : void()), ...);
         }(std::make_integer_sequence<int, CH>{});
     };
-    auto body_full = [&](int c) {
+    auto body_full = [&](int c) __attribute__((always_inline)) {
         const int t0 = c * CH;
         [&]<int... s>(std::integer_sequence<int, s...>) {
             (step(std::integral_constant<int, s>{}, t0 + s, c), ...);
         }(std::make_integer_sequence<int, CH>{});
     };
-    for (int c = 0; c < NC; ++c) body_full(c);   // branch-free: exact wait counts
+    // Branch-free chunks.  The first one is peeled so the loop is entered
+    // with the same outstanding loads and stores as its back edge: the wait
+    // counts at the loop head stay exact instead of draining everything.
+    if (NC > 0) body_full(0);
+    for (int c = 1; c < NC; ++c) body_full(c);
     const int tail = T - NC * CH;
     if (tail) body(NC, tail);
 
@@ -320,10 +357,13 @@ __device__ __forceinline__ void bwd_recompute8(const float (&S)[BJ], float (&N)[
           [u1] "v"(dR[o + 1]), [u2] "v"(dR[o + 2]), [u3] "v"(dR[o + 3]), [DS] "v"(DS), [A] "v"(A), [W] "v"(W),  \
           [dsi] "v"(dsa_i), [ai] "v"(ai))
 
+// Σ over the 8 waves' partials p[0..7] of one column (stride D floats).
 template <bool SEQ>
-__device__ __forceinline__ float sum8(const float4 lo, const float4 hi) {
-    if constexpr (SEQ) return (((((((lo.x + lo.y) + lo.z) + lo.w) + hi.x) + hi.y) + hi.z) + hi.w);
-    return ((lo.x + lo.y) + (lo.z + lo.w)) + ((hi.x + hi.y) + (hi.z + hi.w));
+__device__ __forceinline__ float sum8(const float* p) {
+    const float x0 = p[0], x1 = p[D], x2 = p[2 * D], x3 = p[3 * D];
+    const float x4 = p[4 * D], x5 = p[5 * D], x6 = p[6 * D], x7 = p[7 * D];
+    if constexpr (SEQ) return (((((((x0 + x1) + x2) + x3) + x4) + x5) + x6) + x7);
+    return ((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7));
 }
 
 // SEQ = false: variant 2 (pairwise sums).  SEQ = true: variant 1 — identical
@@ -337,8 +377,10 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
     void* __restrict__ g_dw, void* __restrict__ g_dk, void* __restrict__ g_dv, void* __restrict__ g_da,
     void* __restrict__ g_db, float* __restrict__ dh_in, int T, int H) {
     __shared__ float stage[2][NVEC][CH][D];        // step vectors of a chunk, fp32
-    __shared__ float4 dsa_part[2][D][2];           // [parity][column][waves 0-3 | 4-7]
-    __shared__ float4 ring[3][NOUT][D][2];         // output partials of the last steps
+    // Per-wave partials, column-contiguous so a wave's 64 lanes write 64
+    // consecutive words (no bank conflicts); summed over the 8 waves per column.
+    __shared__ float dsa_part[2][BQ][D];           // [parity][wave][column]
+    __shared__ float ring[3][NOUT][BQ][D];         // output partials of the last steps
 
     const int tid = threadIdx.x;
     const int i = tid & 63;                                    // key column
@@ -404,8 +446,7 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
     auto flush = [&](int uu, int tt) {   // outputs of reverse step uu (time tt)
         if (tid < NOUT * D) {
             const int o = tid >> 6, col = tid & 63;
-            const float4* pp = ring[uu % 3][o][col];
-            store1<GT>(outs[o], base0 + (int64_t)tt * strideT + col, sum8<SEQ>(pp[0], pp[1]));
+            store1<GT>(outs[o], base0 + (int64_t)tt * strideT + col, sum8<SEQ>(&ring[uu % 3][o][0][col]));
         }
     };
 
@@ -475,14 +516,14 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
                 RWKV_B2_BLOCK(0, 1, 2, 3, 0);
                 RWKV_B2_BLOCK(4, 5, 6, 7, 4);
                 const int par = u & 1, slot = u % 3;
-                reinterpret_cast<float*>(&dsa_part[par][i][0])[q] = pds;
-                reinterpret_cast<float*>(&ring[slot][0][i][0])[q] = pdr;
-                reinterpret_cast<float*>(&ring[slot][1][i][0])[q] = pdw;
-                reinterpret_cast<float*>(&ring[slot][2][i][0])[q] = pdk;
-                reinterpret_cast<float*>(&ring[slot][3][i][0])[q] = pdb;
-                reinterpret_cast<float*>(&ring[slot][4][i][0])[q] = pdv;
+                dsa_part[par][q][i] = pds;
+                ring[slot][0][q][i] = pdr;
+                ring[slot][1][q][i] = pdw;
+                ring[slot][2][q][i] = pdk;
+                ring[slot][3][q][i] = pdb;
+                ring[slot][4][q][i] = pdv;
                 __syncthreads();
-                const float dsa_i = sum8<SEQ>(dsa_part[par][i][0], dsa_part[par][i][1]);
+                const float dsa_i = sum8<SEQ>(&dsa_part[par][0][i]);
                 const float DS = __shfl(dsa_i, jl, 64);   // dsa of row 8q + (i & 7)
                 float nR[BJ], nT[BJ];
                 RWKV_B3_BLOCK(0, 1, 2, 3, 0);
@@ -492,7 +533,7 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
                     dR[jj] = nR[jj];
                     dT[jj] = fmaf(wi, dT[jj], nT[jj]);
                 }
-                reinterpret_cast<float*>(&ring[slot][5][i][0])[q] = pda;
+                ring[slot][5][q][i] = pda;
                 if (u > 0) flush(u - 1, t + 1);
             }
         }
