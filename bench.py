@@ -51,6 +51,7 @@ def parse():
     p.add_argument("--copies", type=int, default=6)
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-wkv", action="store_true")
+    p.add_argument("--skip-more", action="store_true", help="skip batched and 1.5B decode")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--mode", choices=["bench", "kernels"], default="bench",
                    help="kernels: run each dominant kernel alone (for rocprofv3 counter passes)")
@@ -175,49 +176,81 @@ class DecodeStep:
         gemv(self.xD, "head.weight", self.logits)
 
 
-def bench_decode(args, dev):
+def run_decode(model, dev, B, steps, warmup, copies, verify=True):
+    """One decode token per HIP graph replay (one graph per weight copy);
+    returns (wall seconds, GPU ms) over `steps` tokens of batch B."""
     import torch
-    from swiftrwkv_amd import synthetic as syn
 
-    model = DecodeModel(syn.X070_0B1, args.copies, dev, nthreads=min(16, os.cpu_count() or 1))
-    step = DecodeStep(model, dev)
+    step = DecodeStep(model, dev, B=B)
     stream = torch.cuda.Stream(device=dev)
-    # eager reference token from a known state, then graphs (one per weight copy)
     with torch.cuda.stream(stream):
         s0 = step.state.clone()
-        step.launch(0, stream.cuda_stream)
-        eager = step.logits.clone()
-        eager_state = step.state.clone()
-        torch.cuda.synchronize()
+        if verify:   # eager reference token from a known state
+            step.launch(0, stream.cuda_stream)
+            eager = step.logits.clone()
+            eager_state = step.state.clone()
+            torch.cuda.synchronize()
         graphs = []
-        for c in range(args.copies):
+        for c in range(copies):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
                 step.launch(c, torch.cuda.current_stream().cuda_stream)
             graphs.append(g)
         torch.cuda.synchronize()
-        for rep in range(3):   # every replay reproduces the eager token bitwise
-            step.state.copy_(s0)
-            torch.cuda.synchronize()
-            graphs[rep % args.copies].replay()
-            torch.cuda.synchronize()
-            if not (torch.equal(step.logits, eager) and torch.equal(step.state, eager_state)):
-                raise RuntimeError(f"graph replay {rep} differs from the eager decode token")
+        if verify:
+            for rep in range(3):   # every replay reproduces the eager token bitwise
+                step.state.copy_(s0)
+                torch.cuda.synchronize()
+                graphs[rep % copies].replay()
+                torch.cuda.synchronize()
+                if not (torch.equal(step.logits, eager) and torch.equal(step.state, eager_state)):
+                    raise RuntimeError(f"graph replay {rep} differs from the eager decode token")
         step.state.copy_(s0)
-        for i in range(args.warmup):
-            graphs[i % args.copies].replay()
+        for i in range(warmup):
+            graphs[i % copies].replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record(stream)
-        for i in range(args.steps):
-            graphs[i % args.copies].replay()
+        for i in range(steps):
+            graphs[i % copies].replay()
         e1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-    gpu_ms = e0.elapsed_time(e1)
+    return step, wall, e0.elapsed_time(e1)
+
+
+def bench_decode(args, dev):
+    from swiftrwkv_amd import synthetic as syn
+
+    model = DecodeModel(syn.X070_0B1, args.copies, dev, nthreads=min(16, os.cpu_count() or 1))
+    step, wall, gpu_ms = run_decode(model, dev, 1, args.steps, args.warmup, args.copies)
     log(f"decode 0.1B: {args.steps} tokens, wall {wall * 1e3:.2f} ms, gpu {gpu_ms:.2f} ms")
     return model, step, wall, gpu_ms
+
+
+def bench_decode_more(model_01, dev):
+    """Batched decode of the 0.1B shape (B = 8, 32) and one-token decode of
+    the 1.5B shape (24 layers, n_embd 2048, FFN 8192, vocab 65536; 776 MB of
+    packed weights > the MALL, so one weight copy streams from HBM)."""
+    import torch
+    from swiftrwkv_amd import synthetic as syn
+
+    res = {}
+    for B in (8, 32):
+        _, wall, gpu_ms = run_decode(model_01, dev, B, 50, 5, len(model_01.dev))
+        res[f"decode_0.1B_batch{B}"] = {"tok_s": B * 50 / wall, "ms_per_step": wall * 1e3 / 50}
+        log(f"decode 0.1B batch {B}: {wall * 1e3 / 50:.3f} ms per step")
+    model = DecodeModel(syn.X070_1B5, 1, dev, nthreads=min(16, os.cpu_count() or 1))
+    _, wall, gpu_ms = run_decode(model, dev, 1, 50, 5, 1)
+    ms = wall * 1e3 / 50
+    res["decode_1.5B_batch1"] = {"tok_s": 50 / wall, "ms_per_token": ms,
+                                 "gemv_bytes_per_token": model.bytes_per_token,
+                                 "effective_GBps": model.bytes_per_token / (ms * 1e-3) / 1e9}
+    log(f"decode 1.5B: {ms:.3f} ms per token")
+    del model
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_head_gemv(model, dev, reps=60):
@@ -419,6 +452,8 @@ def main():
     if not args.skip_wkv:
         extra.update(bench_wkv(dev))
         log("wkv done")
+    if not args.skip_more:
+        extra.update(bench_decode_more(model, dev))
     cpu = None
     if not args.skip_cpu:
         cpu = cpu_baseline(model, step, args.cpu_seconds)

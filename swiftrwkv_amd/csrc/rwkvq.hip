@@ -313,6 +313,7 @@ __device__ __forceinline__ float group_sum(float v, int G) {
 
 struct GemvGeom {
     int G;     // lanes per row (power of two)
+    int LG;    // log2(G)
     int R;     // row groups per wave (64 / G)
     int NP;    // passes: a lane covers units (p·KU + ku)·G + g, p < NP, ku < KU
     int WPB;   // waves per workgroup
@@ -335,12 +336,15 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
     const int NU = IN >> 5;
     const int NK = OUT / out_per;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int gi = lane / geo.G, g = lane - gi * geo.G;
+    const int gi = lane >> geo.LG, g = lane & (geo.G - 1);
     const int row0 = (blockIdx.x * geo.WPB + wave) * geo.R * RL + gi * RL;
     const bool live = row0 < OUT;
-    const int xi = (live ? row0 : OUT - 1) / out_per;   // RL divides out_per
+    const int xi = NK == 1 ? 0 : (live ? row0 : OUT - 1) / out_per;   // RL divides out_per
     float inv = 1.0f;
-    if constexpr (std::is_same_v<F, Sb6Fmt<0>>) inv = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
+    if constexpr (std::is_same_v<F, Sb6Fmt<0>>) {
+        // exact reciprocal of the fp8 unit (a power of two): negate the exponent
+        inv = __uint_as_float(0x7F000000u - __float_as_uint(__builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0]));
+    }
 
     using Raw = typename F::Raw;
     auto load_pass = [&](int p, Raw (&W)[RL][KU]) {
@@ -426,7 +430,7 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
             const int step = (int)blockDim.x * 4;
 #pragma unroll 1
             for (int j = 0; j < rows; ++j) {   // uniform
-                const int nn = j / NK, k = j - nn * NK;
+                const int nn = NK == 1 ? j : j / NK, k = j - nn * NK;
                 const float* src = x + ((int64_t)min(n0 + nn, N - 1) * NK + k) * IN;
 #pragma unroll 1
                 for (int c = (int)threadIdx.x * 4; c < IN; c += step)
@@ -525,6 +529,7 @@ GemvPlan plan_gemv(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t N
     // (independent of the batch, so a row's result does not depend on it)
     while (G > 1 && NU / (G >> 1) <= 4) G >>= 1;
     pl.geo.G = (int)G;
+    pl.geo.LG = __builtin_ctzll((unsigned long long)G);
     pl.geo.R = 64 / pl.geo.G;
     const int64_t per_lane = NU / G;
     // all of a lane's units in one pass (KU ≤ 4), else one unit per pass with
@@ -537,10 +542,10 @@ GemvPlan plan_gemv(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t N
     // prefetched pass (1 for wider codes) or four inputs per tile.
     const int slots = pl.NT == 4 ? 2 : pl.geo.NP > 1 ? (wide ? 1 : 2) : (wide ? 2 : 4);
     pl.RL = (rl_div % 4 == 0 && 4 * KU <= slots) ? 4 : (rl_div % 2 == 0 && 2 * KU <= slots) ? 2 : 1;
-    // Waves per workgroup share one staging of the inputs: up to 16 (one
-    // input row) while the grid keeps ≥ 256 workgroups, at least 4 (fewer
-    // lose more to the staging than they gain in spread).
-    pl.geo.WPB = pl.NT == 1 ? 16 : 4;
+    // Waves per workgroup share one staging of the inputs: 8 (one input row;
+    // measured best between 4 and 16) while the grid keeps ≥ 256 workgroups,
+    // at least 4 (fewer lose more to the staging than they gain in spread).
+    pl.geo.WPB = pl.NT == 1 ? 8 : 4;
     auto blocks = [&]() {
         const int64_t per = (int64_t)pl.geo.WPB * pl.geo.R * pl.RL;
         return (OUT + per - 1) / per;

@@ -443,11 +443,13 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
     stage_store(NC - 1);
     int u = 0;   // reverse step counter (parity of dsa_part, ring slot)
 
-    auto flush = [&](int uu, int tt) {   // outputs of reverse step uu (time tt)
-        if (tid < NOUT * D) {
-            const int o = tid >> 6, col = tid & 63;
-            store1<GT>(outs[o], base0 + (int64_t)tt * strideT + col, sum8<SEQ>(&ring[uu % 3][o][0][col]));
-        }
+    // Outputs of reverse step uu (time tt): 6 × 64 sums of 8 partials, 48 per
+    // wave so every wave carries the same share between two barriers.
+    const int fidx = q * (NOUT * D / BQ) + i;   // output index owned by this lane (i < 48)
+    const int fo = fidx >> 6, fcol = fidx & 63;
+    auto flush = [&](int uu, int tt) {
+        if (i < NOUT * D / BQ)
+            store1<GT>(outs[fo], base0 + (int64_t)tt * strideT + fcol, sum8<SEQ>(&ring[uu % 3][fo][0][fcol]));
     };
 
     for (int c = NC - 1; c >= 0; --c) {
@@ -492,15 +494,25 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
                 bwd_recompute8(hist[m], hist[m + 1], st[3][s][jl], st[7][s][jl], st[2][s][i], st[5][s][i],
                                st[1][s][i]);
             }
+            // step vectors: own column i and broadcast row jl; the next step's
+            // are read before this step's barrier so they are ready after it
+            struct StepVec {
+                float ri, wi, ai, dyi, R, W, K, V, A, B, DY, SA;
+            };
+            auto load_vec = [&](int s) __attribute__((always_inline)) {
+                return StepVec{st[0][s][i], st[1][s][i], st[4][s][i], st[6][s][i], st[0][s][jl], st[1][s][jl],
+                               st[2][s][jl], st[3][s][jl], st[4][s][jl], st[5][s][jl], st[6][s][jl], st[7][s][jl]};
+            };
+            StepVec cur = load_vec(WIN * half + WIN - 1);
 #pragma unroll
             for (int m = WIN - 1; m >= 0; --m, ++u) {
                 const int s = WIN * half + m;
                 const int t = c * CH + s;
                 const float (&Sa)[BJ] = hist[m + 1];
                 const float (&Sp)[BJ] = hist[m];
-                const float ri = st[0][s][i], wi = st[1][s][i], ai = st[4][s][i], dyi = st[6][s][i];
-                const float R = st[0][s][jl], W = st[1][s][jl], K = st[2][s][jl], V = st[3][s][jl];
-                const float A = st[4][s][jl], B = st[5][s][jl], DY = st[6][s][jl], SA = st[7][s][jl];
+                const float ri = cur.ri, wi = cur.wi, ai = cur.ai, dyi = cur.dyi;
+                const float R = cur.R, W = cur.W, K = cur.K, V = cur.V;
+                const float A = cur.A, B = cur.B, DY = cur.DY, SA = cur.SA;
                 float pdr = 0.0f, pdk = 0.0f, pdb = 0.0f, pdv = 0.0f, pds = 0.0f, pdw = 0.0f, pda = 0.0f;
                 RWKV_B1_BLOCK(0, 1, 2, 3, 0);
                 RWKV_B1_BLOCK(4, 5, 6, 7, 4);
@@ -522,6 +534,8 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
                 ring[slot][2][q][i] = pdk;
                 ring[slot][3][q][i] = pdb;
                 ring[slot][4][q][i] = pdv;
+                StepVec nxt = cur;
+                if (m > 0) nxt = load_vec(s - 1);
                 __syncthreads();
                 const float dsa_i = sum8<SEQ>(&dsa_part[par][0][i]);
                 const float DS = __shfl(dsa_i, jl, 64);   // dsa of row 8q + (i & 7)
@@ -535,6 +549,7 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
                 }
                 ring[slot][5][q][i] = pda;
                 if (u > 0) flush(u - 1, t + 1);
+                cur = nxt;
             }
         }
         if (c > 0) stage_store(c - 1);
