@@ -123,20 +123,24 @@ def test_sb6_gemv_head_shape(orc):
 def test_gemv_one_hot_is_bit_exact_dequant_column(orc):
     case("one-hot GEMV == dequant column")
     OUT, IN = 512, 768
-    qblk, qsqm, ddm = sb6_tensor(orc, OUT, IN, 2, seed=5, degenerate=True)
-    W = orc.sb6_dequant(qblk, qsqm, ddm.view(np.uint16), OUT, IN, 2)
     cols = [0, 31, 32, 400, 767]
     x = np.zeros((len(cols), IN), np.float32)
     x[np.arange(len(cols)), cols] = 1.0
-    y = Q.rwkvq_sb6_gemv(dev(x), dev(qblk), dev(qsqm), dev(ddm), OUT, IN, 2).cpu().numpy()
-    assert np.array_equal(y, W[:, cols].T)
+    for xb in (2, 0):   # 6-bit and 4-bit codes
+        qblk, qsqm, ddm = sb6_tensor(orc, OUT, IN, xb, seed=5, degenerate=True)
+        W = orc.sb6_dequant(qblk, qsqm, ddm.view(np.uint16), OUT, IN, xb)
+        y = Q.rwkvq_sb6_gemv(dev(x), dev(qblk), dev(qsqm), dev(ddm), OUT, IN, xb).cpu().numpy()
+        assert np.array_equal(y, W[:, cols].T), xb
+        # a power-of-two input scale is exact as well
+        y4 = Q.rwkvq_sb6_gemv(dev(x * 0.25), dev(qblk), dev(qsqm), dev(ddm), OUT, IN, xb).cpu().numpy()
+        assert np.array_equal(y4, (W[:, cols] * np.float32(0.25)).T), xb
     for bits in (8, 6):
         sq, qs, d = sym_tensor(orc, OUT, IN, bits, seed=bits)
         Ws = orc.sym_dequant(sq, qs, d.view(np.uint16), OUT, IN, bits)
         ys = Q.rwkvq_sym_gemv(dev(x), dev(sq), dev(qs), dev(d), OUT, IN, bits).cpu().numpy()
         assert np.array_equal(ys, Ws[:, cols].T), bits
     # zero input → exact zeros; linearity
-    z = Q.rwkvq_sb6_gemv(dev(np.zeros((1, IN), np.float32)), dev(qblk), dev(qsqm), dev(ddm), OUT, IN, 2)
+    z = Q.rwkvq_sb6_gemv(dev(np.zeros((1, IN), np.float32)), dev(qblk), dev(qsqm), dev(ddm), OUT, IN, xb)
     assert z.abs().max().item() == 0.0
 
 
