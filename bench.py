@@ -13,11 +13,17 @@ instead of the MALL.  Inputs are resident in HBM before the timed region.
 
 Also reported (`extra`): WKV-7 forward tokens/s at B1 T1024 H12 fp32, WKV-7
 forward and forward+backward tokens/s at B8 T4096 H32 bf16 (checkpointed),
-the head-GEMV HBM GB/s, and the CPU restatement of the WKV forward.
+the head-GEMV HBM GB/s, batched decode of the 0.1B and 0.4B shapes (batch
+1 / 8 / 32), one-token decode of the 1.5B shape, decode of the 7B-class shape
+(32 layers, n_embd 4096, FFN 14336) at batch 1 and 16, the WKV-7 forward of
+one 7B-class prefill layer (B1 T8192 H64 fp32), and the CPU restatement of
+the WKV forward.
 
-`roofline` is for the dominant kernel, the head sb6 GEMV; `cpu_baseline`
-times the oracle's restatement of the reference's non-kernel decode path
-(dequantise to fp32, x·Wᵀ) on the host cores.
+`roofline` is for the dominant kernel of the decode token, the sb6 GEMV (most
+of the token's kernel time): the token's algorithmic GEMV bytes per launch
+over the kernel's average in-graph duration across the token's GEMV launches.
+`cpu_baseline` times the oracle's restatement of the reference's non-kernel
+decode path (dequantise to fp32, x·Wᵀ) on the host cores.
 """
 from __future__ import annotations
 
@@ -34,8 +40,11 @@ METRIC = "WKV-7 tokens/s (fwd, fwd+bwd); .rwkvq GEMV GB/s; 1.5B decode tok/s"
 HBM_PEAK_GBPS = 8000.0
 # HBM bytes per launch of the head GEMV from two rocprofv3 counter passes
 # (FETCH_SIZE, WRITE_SIZE) over `bench.py --mode kernels`, calibrated against a
-# 256 MiB device copy; see profiles/hbm_traffic_head_gemv_and_wkv7.md.
-HEAD_GEMV_TRAFFIC_BYTES = 29449768
+# 256 MiB device copy; see profiles/hbm_traffic_decode_gemv_and_wkv7.md.
+HEAD_GEMV_TRAFFIC_BYTES = 29447562
+# The same for the average GEMV launch of one 0.1B decode token (eager tokens
+# over rotated weight copies); same profile.
+DECODE_GEMV_TRAFFIC_BYTES = 1729325
 VALU_PEAK_TFLOPS = 157.3
 
 
@@ -79,7 +88,7 @@ def kernel_ms(launch, stream=None) -> float:
 class DecodeModel:
     """Packed weights of all projections (K3 layout on the device), per copy."""
 
-    def __init__(self, shape, copies, dev, nthreads, only=None):
+    def __init__(self, shape, copies, dev, nthreads, only=None, share_layers=False):
         import numpy as np
         import torch
         from swiftrwkv_amd import quant as Q
@@ -92,13 +101,20 @@ class DecodeModel:
         for idx, (key, OUT, IN) in enumerate(shape.projections()):
             if only is not None and key not in only:
                 continue
-            rng = np.random.default_rng(1000 + idx)
-            w = (rng.standard_normal((OUT, IN), dtype=np.float32) * np.float32(0.02))
-            disk = Q.encode_sb6(w, 4, nthreads)
-            qblk, qsqm, ddm, xb = Q.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"],
-                                                    disk["gw_dm"], None, None, (OUT, IN))
-            self.host[key] = (qblk, qsqm, ddm, OUT, IN)
+            parts = key.split(".")
+            if share_layers and parts[0] == "blocks" and parts[1] != "0":
+                # same packed bytes as layer 0's matrix, in its own device buffer
+                self.host[key] = self.host[".".join(["blocks", "0"] + parts[2:])]
+            else:
+                rng = np.random.default_rng(1000 + idx)
+                w = (rng.standard_normal((OUT, IN), dtype=np.float32) * np.float32(0.02))
+                disk = Q.encode_sb6(w, 4, nthreads)
+                qblk, qsqm, ddm, xb = Q.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"],
+                                                        disk["gw_dm"], None, None, (OUT, IN))
+                self.host[key] = (qblk, qsqm, ddm, OUT, IN)
+            qblk, qsqm, ddm = self.host[key][:3]
             self.bytes_per_token += qblk.nbytes + qsqm.nbytes + ddm.nbytes + 4 * (IN + OUT)
+        self.launches_per_token = 0
         # device buffers; r/k/v of a layer row-concatenated (one fused launch)
         groups = {}
         for key in self.host:
@@ -114,6 +130,7 @@ class DecodeModel:
             self.dev[0][gkey] = base
             for c in range(1, copies):
                 self.dev[c][gkey] = tuple(z.clone() for z in base)
+        self.launches_per_token = len(groups)
         log(f"encoded {len(self.host)} matrices of {shape.name} in {time.time() - t0:.1f}s, "
             f"{self.bytes_per_token / 1e6:.1f} MB per token, {copies} device copies")
 
@@ -148,7 +165,8 @@ class DecodeStep:
         self.lnb = t(rng.standard_normal((self.L, self.D)) * 0.1)
         self.g = t(rng.standard_normal((self.L, B, self.D)))
 
-    def launch(self, copy: int, stream: int):
+    def launch(self, copy: int, stream: int, gemv_only=False):
+        """Enqueue one token (`gemv_only`: its GEMV launches alone)."""
         from swiftrwkv_amd import _lib
         L = _lib.lib()
         W = self.model.dev[copy]
@@ -164,6 +182,11 @@ class DecodeStep:
             q = W[f"blocks.{l}.att.rkv"]   # r/k/v in one launch, x rows (x_r, x_k, x_v) per token
             _lib.check(L.rwkv_sb6_gemv_fused(self.xrkv.data_ptr(), B, q[0].data_ptr(), q[1].data_ptr(),
                                              q[2].data_ptr(), self.y_rkv.data_ptr(), 3 * D, D, 0, D, stream))
+            if gemv_only:
+                gemv(self.tail, f"blocks.{l}.att.output.weight", self.y_o)
+                gemv(self.xD, f"blocks.{l}.ffn.key.weight", self.y_k)
+                gemv(self.xF, f"blocks.{l}.ffn.value.weight", self.y_v)
+                continue
             r, w, k, v, a, b = (z[l] for z in self.rwkvab)
             st = self.state[l]
             _lib.check(L.rwkv_wkv7_step_tail(r.data_ptr(), w.data_ptr(), k.data_ptr(), v.data_ptr(), a.data_ptr(),
@@ -229,6 +252,56 @@ def bench_decode(args, dev):
     return model, step, wall, gpu_ms
 
 
+def bench_decode_gemv(model, step, dev, reps=100):
+    """Average in-graph duration of the GEMV kernel over the GEMV launches of
+    a decode token: one HIP graph per weight copy holding only the token's
+    GEMV launches (back to back, as in the token's graph), replayed over the
+    rotated copies; per launch = replay time / launches.  Also returns the
+    algorithmic bytes per launch (the token's packed weights + x + y over its
+    GEMV launches)."""
+    import torch
+
+    copies = len(model.dev)
+    n_gemv = model.launches_per_token
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        graphs = []
+        for c in range(copies):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step.launch(c, torch.cuda.current_stream().cuda_stream, gemv_only=True)
+            graphs.append(g)
+        for i in range(2 * copies):
+            graphs[i % copies].replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(reps):
+            graphs[i % copies].replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    return model.bytes_per_token / n_gemv, e0.elapsed_time(e1) / (reps * n_gemv), n_gemv
+
+
+def bench_wkv_prefill_7b(dev, reps=3):
+    """WKV-7 forward of one layer of the 7B-class prefill: B1 T8192 H64 fp32."""
+    import torch
+    from swiftrwkv_amd import kernel as K, synthetic as syn
+
+    T, H, L = 8192, 64, 32
+    x = [torch.from_numpy(z).to(dev) for z in syn.wkv_inputs_config0(1, T, H, seed=4)]
+    K.wkv7_sequence_forward(*x)
+    torch.cuda.synchronize()
+    ms = sum(kernel_ms(lambda: K.wkv7_sequence_forward(*x)) for _ in range(reps)) / reps
+    nbytes = T * H * 64 * (6 * 4 + 4) + 2 * H * 64 * 64 * 4
+    flops = T * H * 9 * 64 * 64
+    roof_ms = max(nbytes / (HBM_PEAK_GBPS * 1e9), flops / (VALU_PEAK_TFLOPS * 1e12)) * 1e3
+    del x
+    torch.cuda.empty_cache()
+    return {"ms_per_layer": ms, "prefill_tok_s_32_layers": T / (L * ms * 1e-3), "bytes_per_layer": nbytes,
+            "flop_per_layer": flops, "roofline_ms": roof_ms, "roofline_frac": roof_ms / ms}
+
+
 def bench_decode_more(model_01, dev):
     """Batched decode of the 0.1B shape (B = 8, 32) and one-token decode of
     the 1.5B shape (24 layers, n_embd 2048, FFN 8192, vocab 65536; 776 MB of
@@ -241,7 +314,16 @@ def bench_decode_more(model_01, dev):
         _, wall, gpu_ms = run_decode(model_01, dev, B, 50, 5, len(model_01.dev))
         res[f"decode_0.1B_batch{B}"] = {"tok_s": B * 50 / wall, "ms_per_step": wall * 1e3 / 50}
         log(f"decode 0.1B batch {B}: {wall * 1e3 / 50:.3f} ms per step")
-    model = DecodeModel(syn.X070_1B5, 1, dev, nthreads=min(16, os.cpu_count() or 1))
+    nthreads = min(16, os.cpu_count() or 1)
+    # 0.4B (24 layers, n_embd 1024, FFN 4096): 2 weight copies (> the MALL)
+    model = DecodeModel(syn.X070_0B4, 2, dev, nthreads=nthreads)
+    for B in (1, 8, 32):
+        _, wall, gpu_ms = run_decode(model, dev, B, 30, 4, 2)
+        res[f"decode_0.4B_batch{B}"] = {"tok_s": B * 30 / wall, "ms_per_step": wall * 1e3 / 30}
+        log(f"decode 0.4B batch {B}: {wall * 1e3 / 30:.3f} ms per step")
+    del model
+    torch.cuda.empty_cache()
+    model = DecodeModel(syn.X070_1B5, 1, dev, nthreads=nthreads)
     _, wall, gpu_ms = run_decode(model, dev, 1, 50, 5, 1)
     ms = wall * 1e3 / 50
     res["decode_1.5B_batch1"] = {"tok_s": 50 / wall, "ms_per_token": ms,
@@ -250,6 +332,21 @@ def bench_decode_more(model_01, dev):
     log(f"decode 1.5B: {ms:.3f} ms per token")
     del model
     torch.cuda.empty_cache()
+    # 7B class (32 layers, n_embd 4096, FFN 14336): 3.57 GB of packed weights
+    # per token; every layer has its own device buffers holding layer 0's bytes
+    model = DecodeModel(syn.X070_7B, 1, dev, nthreads=nthreads, share_layers=True)
+    for B in (1, 16):
+        steps = 20 if B == 1 else 10
+        _, wall, gpu_ms = run_decode(model, dev, B, steps, 2, 1)
+        ms = wall * 1e3 / steps
+        res[f"decode_7B_batch{B}"] = {"tok_s": B * steps / wall, "ms_per_step": ms,
+                                      "gemv_bytes_per_token": model.bytes_per_token,
+                                      "effective_GBps": model.bytes_per_token / (ms * 1e-3) / 1e9}
+        log(f"decode 7B batch {B}: {ms:.3f} ms per step")
+    del model
+    torch.cuda.empty_cache()
+    res["wkv7_prefill_7B_B1_T8192_H64_fp32"] = bench_wkv_prefill_7b(dev)
+    log("7B prefill WKV done")
     return res
 
 
@@ -292,8 +389,10 @@ def bench_wkv(dev, reps=5):
         K.wkv7_sequence_forward(*x)
     torch.cuda.synchronize()
     ms = sum(kernel_ms(lambda: K.wkv7_sequence_forward(*x)) for _ in range(reps * 4)) / (reps * 4)
+    nbytes = 1024 * 12 * 64 * 7 * 4 + 2 * 12 * 64 * 64 * 4
     res["wkv7_fwd_B1_T1024_H12_fp32"] = {"ms": ms, "tok_s": 1024 / (ms * 1e-3),
-                                         "valu_roofline_frac": (1024 * 12 * 9 * 64 * 64 / (ms * 1e-3)) / (VALU_PEAK_TFLOPS * 1e12)}
+                                         "valu_roofline_frac": (1024 * 12 * 9 * 64 * 64 / (ms * 1e-3)) / (VALU_PEAK_TFLOPS * 1e12),
+                                         "hbm_roofline_frac": nbytes / (ms * 1e-3) / (HBM_PEAK_GBPS * 1e9)}
     del x
     # config 3: B8 T4096 H32 bf16 training forward (checkpointed) + backward
     B, T, H = 8, 4096, 32
@@ -390,9 +489,13 @@ def cpu_wkv_baseline():
             "sample": f"WKV-7 forward B1 T1024 H12 fp32 x{n}"}
 
 
-def profile_kernels(dev, reps=20):
-    """Each dominant kernel alone, plus a plain 256 MiB device copy whose
-    FETCH_SIZE / WRITE_SIZE calibrate the counters (2 × 256 MiB of traffic)."""
+def profile_kernels(dev, tokens=12):
+    """The dominant kernels alone, for rocprofv3: eager 0.1B decode tokens over
+    6 rotated weight copies (49 GEMV launches each, the head GEMV among them,
+    and 12 WKV step+tail launches), the WKV-7 forward at B1 T1024 H12 fp32
+    (20 launches), the checkpointed training forward + backward at B8 T4096
+    H32 bf16 (3 each), and a plain 256 MiB device copy whose FETCH_SIZE /
+    WRITE_SIZE calibrate the counters (2 x 256 MiB of traffic)."""
     import numpy as np
     import torch
     from swiftrwkv_amd import _lib, kernel as K, synthetic as syn
@@ -402,10 +505,15 @@ def profile_kernels(dev, reps=20):
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    model = DecodeModel(syn.X070_0B1, 6, dev, nthreads=min(16, os.cpu_count() or 1), only={"head.weight"})
-    bench_head_gemv(model, dev, reps=reps)
+    model = DecodeModel(syn.X070_0B1, 6, dev, nthreads=min(16, os.cpu_count() or 1))
+    step = DecodeStep(model, dev, B=1)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    for i in range(tokens):
+        step.launch(i % 6, stream)
+    torch.cuda.synchronize()
+    log("decode tokens done")
     x = [torch.from_numpy(z).to(dev) for z in syn.wkv_inputs_config0(1, 1024, 12, seed=0)]
-    for _ in range(reps):
+    for _ in range(20):
         K.wkv7_sequence_forward(*x)
     B, T, H = 8, 4096, 32
     xs = syn.wkv_inputs_config0(B, T, H, seed=3)
@@ -439,15 +547,23 @@ def main():
         profile_kernels(dev)
         return
     model, step, wall, gpu_ms = bench_decode(args, dev)
+    gemv_bytes, gemv_avg_ms, n_gemv = bench_decode_gemv(model, step, dev)
+    achieved = gemv_bytes / (gemv_avg_ms * 1e-3) / 1e9
+    log(f"decode GEMV: {n_gemv} launches per token, {gemv_bytes / 1e6:.3f} MB per launch, "
+        f"avg {gemv_avg_ms * 1e3:.2f} us -> {achieved:.0f} GB/s")
     nbytes, head_avg_ms, head_med_ms = bench_head_gemv(model, dev)
-    achieved = nbytes / (head_avg_ms * 1e-3) / 1e9
-    log(f"head GEMV: {nbytes / 1e6:.2f} MB, avg {head_avg_ms * 1e3:.1f} us -> {achieved:.0f} GB/s")
+    head_gbps = nbytes / (head_avg_ms * 1e-3) / 1e9
+    log(f"head GEMV: {nbytes / 1e6:.2f} MB, avg {head_avg_ms * 1e3:.1f} us -> {head_gbps:.0f} GB/s")
     extra = {
         "decode_gpu_ms_per_token": gpu_ms / args.steps,
         "decode_gemv_bytes_per_token": model.bytes_per_token,
         "decode_effective_GBps": model.bytes_per_token / (gpu_ms * 1e-3 / args.steps) / 1e9,
+        "decode_gemv_launches_per_token": n_gemv,
+        "decode_gemv_kernel_us_per_token": gemv_avg_ms * 1e3 * n_gemv,
+        "decode_gemv_share_of_token": gemv_avg_ms * n_gemv / (gpu_ms / args.steps),
         "head_gemv_65536x768": {"bytes": nbytes, "avg_us": head_avg_ms * 1e3, "median_us": head_med_ms * 1e3,
-                                "GBps": achieved},
+                                "GBps": head_gbps, "hbm_frac": head_gbps / HBM_PEAK_GBPS,
+                                "traffic": HEAD_GEMV_TRAFFIC_BYTES},
     }
     if not args.skip_wkv:
         extra.update(bench_wkv(dev))
@@ -471,8 +587,9 @@ def main():
                    "weights": "sb6 4-bit from seeded N(0,0.02)", "weight_copies_rotated": args.copies,
                    "hip_graph_per_token": True},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": HEAD_GEMV_TRAFFIC_BYTES,
-                     "kernel": "sb6_gemv head 65536x768 (4-bit), bytes = packed weights + x + y"},
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": DECODE_GEMV_TRAFFIC_BYTES,
+                     "kernel": f"gemv_kernel (sb6 4-bit), in-graph average over the {n_gemv} GEMV launches of "
+                               "one token; bytes per launch = the token's packed weights + x + y / launches"},
         "cpu_baseline": cpu,
         "extra": extra,
     }
