@@ -35,6 +35,8 @@
 
 #include <type_traits>
 
+#include <algorithm>
+
 #include "launch.h"
 
 namespace {
@@ -217,17 +219,28 @@ struct Sb6Fmt {
             }
         }
     }
+    // A unit decoded once for several inputs: codes and the two scales.
     // inv = 1/u for XB == 0 (a power of two: the scaled and the plain
     // computation round identically), 1 otherwise.
+    struct Prep {
+        float c[32];
+        float s, m;
+    };
+    __device__ static void prep(const Raw& r, float inv, Prep& q) {
+        codes(r, q.c);
+        q.s = hround((float)(r.s0 & 0xffu) * f16f(r.s1)) * inv;
+        q.m = hround((float)(int8_t)(r.s0 >> 8) * f16f(r.s1 >> 16));
+    }
+    __device__ static float apply(const Prep& q, const float (&xv)[32], const float (&xs)[2], float acc) {
+        return fmaf(q.m, xs[0] + xs[1], fmaf(q.s, dot32(q.c, xv), acc));
+    }
     template <int NT>
     __device__ static void accumulate(const Raw& r, float inv, const float (&xv)[NT][32], const float (&xs)[NT][2],
                                       float (&acc)[NT]) {
-        float c[32];
-        codes(r, c);
-        const float s = hround((float)(r.s0 & 0xffu) * f16f(r.s1)) * inv;
-        const float m = hround((float)(int8_t)(r.s0 >> 8) * f16f(r.s1 >> 16));
+        Prep q;
+        prep(r, inv, q);
 #pragma unroll
-        for (int nn = 0; nn < NT; ++nn) acc[nn] = fmaf(m, xs[nn][0] + xs[nn][1], fmaf(s, dot32(c, xv[nn]), acc[nn]));
+        for (int nn = 0; nn < NT; ++nn) acc[nn] = apply(q, xv[nn], xs[nn], acc[nn]);
     }
 };
 
@@ -254,43 +267,48 @@ struct SymFmt {
         r.s1 = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.d) +
                                                   (row * (uint32_t)(NU >> 3) + (u >> 3)) * 2u);
     }
-    template <int NT>
-    __device__ static void accumulate(const Raw& r, float, const float (&xv)[NT][32], const float (&xs)[NT][2],
-                                      float (&acc)[NT]) {
-        const float dsb = f16f(r.s1);
-        const float s0 = hround((float)(int8_t)(r.s0 & 0xffu) * dsb);
-        const float s1 = hround((float)(int8_t)(r.s0 >> 8) * dsb);
+    struct Prep {
         float c[32];
+        float s0, s1;   // block scales of columns 0..15 and 16..31
+    };
+    __device__ static void prep(const Raw& r, float, Prep& q) {
+        const float dsb = f16f(r.s1);
+        q.s0 = hround((float)(int8_t)(r.s0 & 0xffu) * dsb);
+        q.s1 = hround((float)(int8_t)(r.s0 >> 8) * dsb);
         if constexpr (BITS == 8) {
 #pragma unroll
             for (int m = 0; m < 8; ++m)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) c[4 * m + e] = (float)(int8_t)(r.w[m] >> (8 * e));
+                for (int e = 0; e < 4; ++e) q.c[4 * m + e] = (float)(int8_t)(r.w[m] >> (8 * e));
         } else {
             // register order l0,l1,h0,h1 | l2,l3,h2,h3 → columns 4m..4m+3; codes +32
 #pragma unroll
             for (int m = 0; m < 8; ++m) {
                 const uint32_t wd = r.w[(m >> 2) * 2 + (m & 1)];
-                uint32_t q = (m & 2) ? ((wd >> 4) & 0x0F0F0F0Fu) : (wd & 0x0F0F0F0Fu);
-                q |= spread4((r.w[4] >> (4 * m)) & 0xFu) << 4;
-                q |= spread4((r.w[5] >> (4 * m)) & 0xFu) << 5;
-                bytes4(q, &c[4 * m]);
+                uint32_t q4 = (m & 2) ? ((wd >> 4) & 0x0F0F0F0Fu) : (wd & 0x0F0F0F0Fu);
+                q4 |= spread4((r.w[4] >> (4 * m)) & 0xFu) << 4;
+                q4 |= spread4((r.w[5] >> (4 * m)) & 0xFu) << 5;
+                bytes4(q4, &q.c[4 * m]);
             }
         }
+    }
+    __device__ static float apply(const Prep& q, const float (&xv)[32], const float (&xs)[2], float acc) {
+        float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
-        for (int nn = 0; nn < NT; ++nn) {
-            float d0 = 0.0f, d1 = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                d0 = fmaf(c[i], xv[nn][i], d0);
-                d1 = fmaf(c[16 + i], xv[nn][16 + i], d1);
-            }
-            if constexpr (BITS == 8) {
-                acc[nn] = fmaf(s1, d1, fmaf(s0, d0, acc[nn]));
-            } else {
-                acc[nn] = fmaf(s1, fmaf(-32.0f, xs[nn][1], d1), fmaf(s0, fmaf(-32.0f, xs[nn][0], d0), acc[nn]));
-            }
+        for (int i = 0; i < 16; ++i) {
+            d0 = fmaf(q.c[i], xv[i], d0);
+            d1 = fmaf(q.c[16 + i], xv[16 + i], d1);
         }
+        if constexpr (BITS == 8) return fmaf(q.s1, d1, fmaf(q.s0, d0, acc));
+        return fmaf(q.s1, fmaf(-32.0f, xs[1], d1), fmaf(q.s0, fmaf(-32.0f, xs[0], d0), acc));
+    }
+    template <int NT>
+    __device__ static void accumulate(const Raw& r, float inv, const float (&xv)[NT][32], const float (&xs)[NT][2],
+                                      float (&acc)[NT]) {
+        Prep q;
+        prep(r, inv, q);
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn) acc[nn] = apply(q, xv[nn], xs[nn], acc[nn]);
     }
 };
 
@@ -492,6 +510,152 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
     }
 }
 
+// Batches (N ≥ 2 inputs): NT inputs share one pass over the weights.  The
+// lane → (row, unit) assignment, the per-unit arithmetic (F::prep / F::apply)
+// and the group sums are those of gemv_kernel, so every output is bitwise
+// what a single-input launch gives.  A unit's codes are decoded once for all
+// NT inputs.  blockIdx.y selects the tile of NT inputs.  The inputs are
+// staged in LDS a chunk of CP passes (CP·G units) at a time, so any IN fits
+// and a workgroup reads each input element once; the next pass's weights are
+// in flight during the current one.
+template <class F, int RL, int NT>
+__global__ __launch_bounds__(512) void gemv_batch_kernel(const float* __restrict__ x, int N, typename F::Ptr P,
+                                                         float* __restrict__ y, int OUT, int IN, int out_per,
+                                                         GemvGeom geo, int CP) {
+    extern __shared__ float lds[];
+    const int NU = IN >> 5;
+    const int NK = OUT / out_per;
+    {
+        const int n0 = (int)blockIdx.y * NT;
+        x += (int64_t)n0 * NK * IN;
+        y += (int64_t)n0 * OUT;
+        N = min(NT, N - n0);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int gi = lane >> geo.LG, g = lane & (geo.G - 1);
+    const int row0 = (blockIdx.x * geo.WPB + wave) * geo.R * RL + gi * RL;
+    const int xi = NK == 1 ? 0 : min(row0, OUT - 1) / out_per;   // RL divides out_per
+    float inv = 1.0f;
+    if constexpr (std::is_same_v<F, Sb6Fmt<0>>) {
+        inv = __uint_as_float(0x7F000000u - __float_as_uint(__builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0]));
+    }
+    const int rows = NT * NK;      // staged input rows: input nn, matrix k at nn·NK + k
+    const int CU = CP * geo.G;     // units per chunk
+    const int XS = CU * 36;        // floats per staged row: units padded to 36 floats
+    float* const sums = lds + rows * XS;   // [rows][CU][2]: Σ x of columns 0..15, 16..31
+
+    using Raw = typename F::Raw;
+    using Prep = typename F::Prep;
+    auto load_pass = [&](int p, Raw (&W)[RL]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int rr = 0; rr < RL; ++rr)
+            F::load(P, NU, (uint32_t)min(row0 + rr, OUT - 1), (uint32_t)(p * geo.G + g), W[rr]);
+    };
+    auto stage = [&](int u0, int nu) __attribute__((always_inline)) {   // units u0 .. u0 + nu - 1
+        const int q4 = nu * 8;   // float4 per staged row
+        // a thread's float4 of column c4 for 8 rows at a time: 8 loads in flight
+#pragma unroll 1
+        for (int c4 = threadIdx.x; c4 < q4; c4 += blockDim.x) {
+            const int c = c4 * 4, off = c + (c >> 5) * 4;
+#pragma unroll 1
+            for (int j0 = 0; j0 < rows; j0 += 8) {
+                // staged row j = input nn, matrix k is x row j; rows of inputs
+                // past N (their outputs are not stored) repeat the last row
+                using f4 = float __attribute__((ext_vector_type(4)));
+                f4 v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int j = min(j0 + e, N * NK - 1);
+                    v[e] = *reinterpret_cast<const f4*>(x + (int64_t)j * IN + u0 * 32 + c);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (j0 + e < rows) *reinterpret_cast<f4*>(lds + (j0 + e) * XS + off) = v[e];
+            }
+        }
+        __syncthreads();
+        if constexpr (F::SUMS) {
+#pragma unroll 1
+            for (int i = threadIdx.x; i < rows * nu * 2; i += blockDim.x) {
+                const int j = i / (nu * 2), h = i - j * (nu * 2);   // h = 2·unit + half
+                const float4* px = reinterpret_cast<const float4*>(lds + j * XS + (h >> 1) * 36 + 16 * (h & 1));
+                float sum = 0.0f;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const float4 f = px[m];
+                    sum += f.x; sum += f.y; sum += f.z; sum += f.w;
+                }
+                sums[j * CU * 2 + h] = sum;
+            }
+            __syncthreads();
+        }
+    };
+
+    float acc[NT][RL];
+#pragma unroll
+    for (int nn = 0; nn < NT; ++nn)
+#pragma unroll
+        for (int rr = 0; rr < RL; ++rr) acc[nn][rr] = 0.0f;
+    Raw W[RL];
+    load_pass(0, W);   // in flight while the first chunk is staged
+    int u0 = 0;
+#pragma unroll 1
+    for (int p = 0; p < geo.NP; ++p) {
+        if (p % CP == 0) {   // uniform across the workgroup
+            if (p) __syncthreads();   // every wave is done with the previous chunk
+            u0 = p * geo.G;
+            stage(u0, min(CP, geo.NP - p) * geo.G);
+        }
+        Raw Wn[RL];
+        if (p + 1 < geo.NP) load_pass(p + 1, Wn);
+        Prep q[RL];
+#pragma unroll
+        for (int rr = 0; rr < RL; ++rr) F::prep(W[rr], inv, q[rr]);
+        const int lu = p * geo.G + g - u0;
+        // inputs nn + 1 are read from LDS while input nn is applied; the fence
+        // (it consumes the accumulators and orders memory) keeps at most two
+        // inputs' values live
+        float xv[2][32], xs[2][2];
+        auto read_x = [&](int nn, float (&v)[32], float (&sv)[2]) __attribute__((always_inline)) {
+            const int j = nn * NK + xi;
+            const float4* px = reinterpret_cast<const float4*>(lds + j * XS + lu * 36);
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const float4 f = px[m];
+                v[4 * m] = f.x; v[4 * m + 1] = f.y; v[4 * m + 2] = f.z; v[4 * m + 3] = f.w;
+            }
+            if constexpr (F::SUMS) {
+                const float2 t = reinterpret_cast<const float2*>(sums)[j * CU + lu];
+                sv[0] = t.x; sv[1] = t.y;
+            } else {
+                sv[0] = sv[1] = 0.0f;
+            }
+        };
+        read_x(0, xv[0], xs[0]);
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn) {
+            if (nn + 1 < NT) read_x(nn + 1, xv[(nn + 1) & 1], xs[(nn + 1) & 1]);
+#pragma unroll
+            for (int rr = 0; rr < RL; ++rr) {
+                acc[nn][rr] = F::apply(q[rr], xv[nn & 1], xs[nn & 1], acc[nn][rr]);
+                asm volatile("" : "+v"(acc[nn][rr]) : : "memory");
+            }
+        }
+        if (p + 1 < geo.NP) {
+#pragma unroll
+            for (int rr = 0; rr < RL; ++rr) W[rr] = Wn[rr];
+        }
+    }
+#pragma unroll
+    for (int nn = 0; nn < NT; ++nn)
+#pragma unroll
+        for (int rr = 0; rr < RL; ++rr) {
+            const float t = group_sum(acc[nn][rr], geo.G);
+            const int row = row0 + rr;
+            if (g == 0 && row < OUT && nn < N) y[(int64_t)nn * OUT + row] = t;
+        }
+}
+
 // ─────────────────────────────── host side ───────────────────────────────
 rwkv_status launch_status(const char* what) {
     hipError_t e = hipGetLastError();
@@ -619,14 +783,78 @@ bool launch_gemv(const GemvPlan& pl, hipStream_t st, const float* x, int N, type
     return launched;
 }
 
-// Batches of more than 4 inputs run as launches of ≤ 4 inputs each (the
-// inputs of a launch are staged in LDS; each launch streams the weights once),
-// unless the inputs do not fit in LDS: then one launch reads them from global
-// memory.
+constexpr int64_t kBatchLds = 160 * 1024;   // LDS of one gfx950 workgroup (and CU)
+
+struct BatchPlan {
+    GemvGeom geo;
+    int RL, NT, CP;
+    size_t lds;
+    unsigned blocks;
+};
+
+// Batched geometry: G and the unit order are the single-input plan's (so the
+// results match it bitwise), one unit per lane and pass.  NT = 16 / 8 / 4
+// inputs per workgroup, the largest whose one pass of staged inputs fits in
+// half the LDS (two workgroups per CU; NT = 4 may take all of it), reduced
+// while the grid (row blocks × input tiles) has fewer than 256 workgroups;
+// then RL = 2 rows per lane where the rows allow and the grid stays ≥ 256
+// workgroups, and WPB = 8 waves under the same condition, else 4.  CP passes
+// per chunk fill the LDS share.
+bool plan_batch(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t NK, bool sums, BatchPlan& bp) {
+    const GemvPlan one = plan_gemv(OUT, NU, rl_div, 1, NK, sums, false);
+    bp.geo = one.geo;
+    bp.geo.NP = (int)(NU / bp.geo.G);
+    const int64_t per_row_pass = (int64_t)bp.geo.G * (36 + (sums ? 2 : 0)) * 4;   // bytes per input row, one pass
+    auto blocks = [&](int wpb, int rl) {
+        const int64_t per = (int64_t)wpb * bp.geo.R * rl;
+        return (OUT + per - 1) / per;
+    };
+    auto tiles = [&](int nt) { return (N + nt - 1) / nt; };
+    bp.NT = N > 8 ? 16 : N > 4 ? 8 : 4;
+    while (bp.NT > 4 && bp.NT * NK * per_row_pass > kBatchLds / 2) bp.NT >>= 1;
+    while (bp.NT > 4 && blocks(4, 1) * tiles(bp.NT) < 256) bp.NT >>= 1;
+    const int64_t pass_bytes = bp.NT * NK * per_row_pass;
+    if (pass_bytes > kBatchLds) return false;
+    const int64_t budget = pass_bytes <= kBatchLds / 2 ? kBatchLds / 2 : kBatchLds;
+    bp.CP = (int)std::min<int64_t>(bp.geo.NP, budget / pass_bytes);
+    bp.lds = (size_t)(pass_bytes * bp.CP);
+    bp.RL = (rl_div % 2 == 0 && blocks(4, 2) * tiles(bp.NT) >= 256) ? 2 : 1;
+    bp.geo.WPB = blocks(8, bp.RL) * tiles(bp.NT) >= 256 ? 8 : 4;
+    bp.blocks = (unsigned)blocks(bp.geo.WPB, bp.RL);
+    return true;
+}
+
+template <class F>
+bool launch_batch(const BatchPlan& bp, hipStream_t st, const float* x, int N, typename F::Ptr P, float* y, int OUT,
+                  int IN, int out_per) {
+    const dim3 grid(bp.blocks, (unsigned)((N + bp.NT - 1) / bp.NT)), block(64 * bp.geo.WPB);
+#define RWKV_GB(RLV, NTV)                                                                                    \
+    rwkv::launch_lds(gemv_batch_kernel<F, RLV, NTV>, grid, block, bp.lds, st, x, N, P, y, OUT, IN, out_per, \
+                     bp.geo, bp.CP)
+    if (bp.RL == 2) {
+        if (bp.NT == 16) RWKV_GB(2, 16);
+        else if (bp.NT == 8) RWKV_GB(2, 8);
+        else RWKV_GB(2, 4);
+    } else {
+        if (bp.NT == 16) RWKV_GB(1, 16);
+        else if (bp.NT == 8) RWKV_GB(1, 8);
+        else RWKV_GB(1, 4);
+    }
+#undef RWKV_GB
+    return true;
+}
+
+// One input: gemv_kernel.  Batches: one gemv_batch_kernel launch, a
+// workgroup per (row block, tile of NT inputs).
 template <class F>
 bool run_gemv(int64_t OUT, int64_t IN, int64_t rl_div, int64_t N, int64_t NK, hipStream_t st, const float* x,
               typename F::Ptr P, float* y, int64_t out_per) {
     const int64_t NU = IN / 32;
+    if (N >= 2) {
+        BatchPlan bp;
+        if (plan_batch(OUT, NU, rl_div, N, NK, F::SUMS, bp) && (N + bp.NT - 1) / bp.NT <= 65535)
+            return launch_batch<F>(bp, st, x, (int)N, P, y, (int)OUT, (int)IN, (int)out_per);
+    }
     const GemvPlan all = plan_gemv(OUT, NU, rl_div, N, NK, F::SUMS, F::WIDE);
     if (all.xl || N <= 4) return launch_gemv<F>(all, st, x, (int)N, P, y, (int)OUT, (int)IN, (int)out_per);
     const GemvPlan tile = plan_gemv(OUT, NU, rl_div, 4, NK, F::SUMS, F::WIDE);

@@ -196,6 +196,54 @@ def test_fused_sym_gemv_equals_separate_bitwise(orc, bits):
     assert rel(want, fused.cpu().numpy()) < GEMV_TOL
 
 
+# batches run in their own kernel (one weight pass for up to 16 inputs, the
+# inputs staged in LDS chunk by chunk); 256 x 14336 stages 7 passes of 64
+# units in chunks (a partial last chunk), N = 17 / 33 split into launches
+BATCH_NS = (2, 5, 16, 17, 33)
+
+
+@pytest.mark.parametrize("fmt", ["sb6:0", "sb6:1", "sb6:2", "sym:8", "sym:6"])
+@pytest.mark.parametrize("OUT,IN", [(768, 768), (256, 14336)])
+def test_batched_gemv_rows_equal_single_bitwise(orc, fmt, OUT, IN):
+    kind, b = fmt.split(":")
+    b = int(b)
+    case(f"batched gemv {fmt} {OUT}x{IN}")
+    rng = np.random.default_rng(OUT + b)
+    if kind == "sb6":
+        w = [dev(z) for z in sb6_tensor(orc, OUT, IN, b, seed=OUT + IN + b)]
+        run = lambda x: Q.rwkvq_sb6_gemv(x, *w, OUT, IN, b)
+        f64 = lambda x: orc.sb6_gemv_f64(x, *[z.cpu().numpy() for z in w[:2]], w[2].cpu().numpy().view(np.uint16),
+                                         OUT, IN, b)
+    else:
+        w = [dev(z) for z in sym_tensor(orc, OUT, IN, b, seed=OUT + b)]
+        run = lambda x: Q.rwkvq_sym_gemv(x, *w, OUT, IN, b)
+        f64 = lambda x: orc.sym_gemv_f64(x, *[z.cpu().numpy() for z in w[:2]], w[2].cpu().numpy().view(np.uint16),
+                                         OUT, IN, b)
+    x = rng.standard_normal((max(BATCH_NS), IN)).astype(np.float32)
+    single = torch.cat([run(dev(x[n:n + 1])) for n in range(max(BATCH_NS))])
+    assert rel(f64(x), single.cpu().numpy()) < GEMV_TOL
+    for N in BATCH_NS:
+        y = run(dev(x[:N]))
+        assert y.shape == (N, OUT)
+        assert torch.equal(y, single[:N]), N
+
+
+def test_batched_fused_gemv_equals_separate_bitwise(orc):
+    case("batched fused sb6 r/k/v 3x512x2048")
+    OUT, IN, Kn, N = 512, 2048, 3, 16
+    parts = [sb6_tensor(orc, OUT, IN, 0, seed=40 + i) for i in range(Kn)]
+    qblk, qsqm, ddm = (np.concatenate([p[j] for p in parts]) for j in range(3))
+    x = np.random.default_rng(23).standard_normal((N * Kn, IN)).astype(np.float32)
+    fused = Q.rwkvq_sb6_gemv(dev(x), dev(qblk), dev(qsqm), dev(ddm), OUT * Kn, IN, 0, out_per=OUT)
+    assert fused.shape == (N, OUT * Kn)
+    for i, p in enumerate(parts):
+        xi = np.ascontiguousarray(x.reshape(N, Kn, IN)[:, i])
+        alone = Q.rwkvq_sb6_gemv(dev(xi[:1]), *[dev(z) for z in p], OUT, IN, 0)
+        assert torch.equal(fused[:1, i * OUT:(i + 1) * OUT], alone)
+        batch = Q.rwkvq_sb6_gemv(dev(xi), *[dev(z) for z in p], OUT, IN, 0)
+        assert torch.equal(fused[:, i * OUT:(i + 1) * OUT], batch)
+
+
 def test_gemv_is_deterministic(orc):
     case("gemv determinism")
     qblk, qsqm, ddm = sb6_tensor(orc, 3072, 768, 1, seed=3)
