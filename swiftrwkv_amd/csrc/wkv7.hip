@@ -139,6 +139,53 @@ __device__ __forceinline__ void fwd_dot16(const float (&S)[16], float A, float& 
           [s6] "v"(S[14]), [s7] "v"(S[15]), [A] "v"(A));
 }
 
+// Four-row layout (small B·H): lane l holds value row 4·blk + (l & 3) and key
+// columns 4g..4g+3, g = l >> 2; the four lanes of a quad share g and hold
+// elements 4g..4g+3 of each step vector, broadcast with DPP quad_perm.
+#define RWKV_QB(c) " quad_perm:[" #c "," #c "," #c "," #c "] row_mask:0xf bank_mask:0xf\n\t"
+#define RWKV_QMUL(c, N) "v_mul_f32_dpp %[" N "], %[K], %[vv]" RWKV_QB(c)
+#define RWKV_QFB(c, N) "v_fmac_f32_dpp %[" N "], %[B], %[sa]" RWKV_QB(c)
+#define RWKV_QFW(c, S, N) "v_fmac_f32_dpp %[" N "], %[W], %[" S "]" RWKV_QB(c)
+#define RWKV_QYP(c, N) "v_fmac_f32_dpp %[y], %[R], %[" N "]" RWKV_QB(c) "v_fmac_f32_dpp %[p], %[A], %[" N "]" RWKV_QB(c)
+
+// The forward update of the lane's 4 state elements (the same FMA sequence per
+// element as fwd_update16).
+__device__ __forceinline__ void fwd_update4(const float (&S)[4], float (&N)[4], float K, float B, float W, float R,
+                                            float A, float vv, float sa, float& y, float& p) {
+    asm("s_nop 1\n\t"
+        RWKV_QMUL(0, "n0") RWKV_QMUL(1, "n1") RWKV_QMUL(2, "n2") RWKV_QMUL(3, "n3")
+        RWKV_QFB(0, "n0") RWKV_QFB(1, "n1") RWKV_QFB(2, "n2") RWKV_QFB(3, "n3")
+        RWKV_QFW(0, "s0", "n0") RWKV_QFW(1, "s1", "n1") RWKV_QFW(2, "s2", "n2") RWKV_QFW(3, "s3", "n3")
+        RWKV_QYP(0, "n0") RWKV_QYP(1, "n1") RWKV_QYP(2, "n2") RWKV_QYP(3, "n3")
+        : [n0] "=&v"(N[0]), [n1] "=&v"(N[1]), [n2] "=&v"(N[2]), [n3] "=&v"(N[3]), [y] "+v"(y), [p] "+v"(p)
+        : [s0] "v"(S[0]), [s1] "v"(S[1]), [s2] "v"(S[2]), [s3] "v"(S[3]), [K] "v"(K), [B] "v"(B), [W] "v"(W),
+          [R] "v"(R), [A] "v"(A), [vv] "v"(vv), [sa] "v"(sa));
+}
+
+// p += Σ_c a_c·S_c over the lane's 4 columns.
+__device__ __forceinline__ void fwd_dot4(const float (&S)[4], float A, float& p) {
+    asm("s_nop 1\n\t"
+        "v_fmac_f32_dpp %[p], %[A], %[s0]" RWKV_QB(0) "v_fmac_f32_dpp %[p], %[A], %[s1]" RWKV_QB(1)
+        "v_fmac_f32_dpp %[p], %[A], %[s2]" RWKV_QB(2) "v_fmac_f32_dpp %[p], %[A], %[s3]" RWKV_QB(3)
+        : [p] "+v"(p)
+        : [s0] "v"(S[0]), [s1] "v"(S[1]), [s2] "v"(S[2]), [s3] "v"(S[3]), [A] "v"(A));
+}
+
+// Sum of a value row's 16 column-group partials (lanes l & 3 + 4g): within a
+// 16-lane DPP row the lanes 8 and then 4 apart (row_ror), then across the
+// four DPP rows (rowsum4).  Every lane of the row ends with the same bits.
+__device__ __forceinline__ float rowsum16(float x) {
+    float t, u;
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0xf" : "=&v"(t) : "v"(x));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:4 row_mask:0xf bank_mask:0xf" : "=&v"(u) : "v"(t));
+    return rowsum4(u);
+}
+
+// Layout choice, a function of B·H only (so every entry point agrees bitwise
+// for a given batch and head count): four rows per wave while sixteen would
+// leave the chip with fewer waves than SIMDs (1,024).
+__host__ __device__ constexpr bool use_rows4(int64_t BH) { return BH < 256; }
+
 // ─────────────────────────────── forward ───────────────────────────────
 // Grid: 4 workgroups of one wave per (b, h); workgroup 4·(b·H + h) + blk owns
 // value rows 16·blk .. 16·blk + 15.  Offsets inside one (b, h) sequence are
@@ -292,6 +339,121 @@ __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
 #pragma unroll
         for (int m = 0; m < 4; ++m) dst[m] = make_float4(S[0][4 * m], S[0][4 * m + 1], S[0][4 * m + 2], S[0][4 * m + 3]);
     }
+}
+
+// Forward, four-row layout: 16 workgroups of one wave per (b, h); workgroup
+// 16·(b·H + h) + blk owns value rows 4·blk .. 4·blk + 3.  Each lane loads
+// element l of the step vectors (a 256-byte coalesced row per vector and
+// step) and its row's v; otherwise the step is wkv7_fwd_kernel's.
+template <int DT, bool EMIT_SA, bool EMIT_CK>
+__global__ __launch_bounds__(64) void wkv7_fwd4_kernel(
+    const void* __restrict__ r, const void* __restrict__ w, const void* __restrict__ k,
+    const void* __restrict__ v, const void* __restrict__ a, const void* __restrict__ b,
+    const float* __restrict__ h_in, float* __restrict__ out, float* __restrict__ h_out,
+    float* __restrict__ sa_out, float* __restrict__ ckpt, int T, int H) {
+    using In = FwdIn<DT>;
+    using E = typename In::E;
+    const int l = threadIdx.x;
+    const int ri = l & 3, g = l >> 2;
+    // the sixteen waves of a head on one XCD when the grid allows
+    int bh, blk;
+    if ((gridDim.x & 127) == 0) {
+        const int id = blockIdx.x, xcd = id & 7, slot = id >> 3;
+        bh = (slot >> 4) * 8 + xcd;
+        blk = slot & 15;
+    } else {
+        bh = blockIdx.x >> 4;
+        blk = blockIdx.x & 15;
+    }
+    const int bi = bh / H, hi = bh - bi * H;
+    const int row = 4 * blk + ri;
+    const uint32_t strideT = (uint32_t)H * D;
+    const int64_t base0 = ((int64_t)bi * T * H + hi) * D;
+    const int64_t sbase = (int64_t)bh * D * D + (int64_t)row * D + 4 * g;
+    const int NC = T / CH;
+    In in{reinterpret_cast<const E*>(a) + base0, reinterpret_cast<const E*>(w) + base0,
+          reinterpret_cast<const E*>(k) + base0, reinterpret_cast<const E*>(b) + base0,
+          reinterpret_cast<const E*>(r) + base0, reinterpret_cast<const E*>(v) + base0};
+    float* const outp = out + base0;
+    float* const sap = EMIT_SA ? sa_out + base0 : nullptr;
+
+    float S[2][4];
+    if (h_in) {
+        const float4 f = *reinterpret_cast<const float4*>(h_in + sbase);
+        S[0][0] = f.x; S[0][1] = f.y; S[0][2] = f.z; S[0][3] = f.w;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) S[0][c] = 0.0f;
+    }
+
+    E ring[CH][6];
+    const uint32_t esz = (uint32_t)sizeof(E);
+    const uint32_t span = (uint32_t)T * strideT * esz - (uint32_t)hi * D * esz;
+    const uint32_t voff = (uint32_t)l * esz, roff = (uint32_t)row * esz;
+    auto rsrc = [&](const void* p, uint32_t n) { return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)n, 0x00020000); };
+    const __amdgpu_buffer_rsrc_t ra = rsrc(in.a, span), rw = rsrc(in.w, span), rk_ = rsrc(in.k, span),
+                                 rb = rsrc(in.b, span), rr = rsrc(in.r, span), rv = rsrc(in.v, span);
+    auto ld = [&](__amdgpu_buffer_rsrc_t rs, uint32_t vo, uint32_t so) -> E {
+        if constexpr (sizeof(E) == 2) return (E)__builtin_amdgcn_raw_buffer_load_b16(rs, vo, so, 0);
+        else return __builtin_bit_cast(E, __builtin_amdgcn_raw_buffer_load_b32(rs, vo, so, 0));
+    };
+    auto fetch = [&](E (&slot)[6], int t) __attribute__((always_inline)) {
+        const uint32_t so = (uint32_t)min(t, T - 1) * strideT * esz;
+        slot[0] = ld(ra, voff, so);
+        slot[1] = ld(rw, voff, so);
+        slot[2] = ld(rk_, voff, so);
+        slot[3] = ld(rb, voff, so);
+        slot[4] = ld(rr, voff, so);
+        slot[5] = ld(rv, roff, so);
+    };
+    const uint32_t ospan = (uint32_t)T * strideT * 4u - (uint32_t)hi * D * 4u;
+    const __amdgpu_buffer_rsrc_t ro_ = rsrc(outp, ospan), rs_ = rsrc(EMIT_SA ? sap : outp, ospan);
+    const uint32_t orow = (uint32_t)row * 4u;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) fetch(ring[st], st);
+
+    float p = 0.0f;
+    fwd_dot4(S[0], In::cvt(ring[0][0]), p);
+
+    auto step = [&](auto sc, int t, int c) __attribute__((always_inline)) {
+        constexpr int s = decltype(sc)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(ring[(s + 8) & (CH - 1)], t + 8);
+        const float sa = rowsum16(p);
+        float y = 0.0f;
+        p = 0.0f;
+        const E* sl = ring[s];
+        fwd_update4(S[s & 1], S[(s + 1) & 1], In::cvt(sl[2]), In::cvt(sl[3]), In::cvt(sl[1]), In::cvt(sl[4]),
+                    In::cvt(ring[(s + 1) & (CH - 1)][0]), In::cvt(sl[5]), sa, y, p);
+        y = rowsum16(y);
+        const uint32_t so = (uint32_t)t * strideT * 4u;
+        // the sixteen lanes of a row store the same bits
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ro_, orow, so, 0);
+        if constexpr (EMIT_SA) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sa), rs_, orow, so, 0);
+        if constexpr (EMIT_CK && s == CH - 1) {
+            *reinterpret_cast<float4*>(ckpt + ((int64_t)bh * NC + c) * D * D + (int64_t)row * D + 4 * g) =
+                make_float4(S[0][0], S[0][1], S[0][2], S[0][3]);
+        }
+    };
+    auto body = [&](int c, int n) __attribute__((always_inline)) {
+        const int t0 = c * CH;
+        [&]<int... s>(std::integer_sequence<int, s...>) {
+            ((n > s ? step(std::integral_constant<int, s>{}, t0 + s, c) : void()), ...);
+        }(std::make_integer_sequence<int, CH>{});
+    };
+    auto body_full = [&](int c) __attribute__((always_inline)) {
+        const int t0 = c * CH;
+        [&]<int... s>(std::integer_sequence<int, s...>) {
+            (step(std::integral_constant<int, s>{}, t0 + s, c), ...);
+        }(std::make_integer_sequence<int, CH>{});
+    };
+    if (NC > 0) body_full(0);
+    for (int c = 1; c < NC; ++c) body_full(c);
+    const int tail = T - NC * CH;
+    if (tail) body(NC, tail);
+
+    const int fs = tail & 1;
+    *reinterpret_cast<float4*>(h_out + sbase) = make_float4(S[fs][0], S[fs][1], S[fs][2], S[fs][3]);
 }
 
 // ─────────────────────────────── backward ───────────────────────────────
@@ -660,6 +822,59 @@ __global__ __launch_bounds__(256) void wkv7_step_tail_kernel(
     }
 }
 
+// The same in the four-row layout: sixteen waves per (row, head), each the
+// T = 1 path of wkv7_fwd4_kernel for its four value rows.
+__global__ __launch_bounds__(1024) void wkv7_step_tail4_kernel(
+    const float* __restrict__ r, const float* __restrict__ w, const float* __restrict__ k,
+    const float* __restrict__ v, const float* __restrict__ a, const float* __restrict__ b,
+    const float* __restrict__ h_in, float* __restrict__ h_out, const float* __restrict__ rk,
+    const float* __restrict__ lnw, const float* __restrict__ lnb, const float* __restrict__ g,
+    float* __restrict__ wkv_out, float* __restrict__ out, int H, float eps) {
+    __shared__ float ys[D];
+    const int blk = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int ri = l & 3, gq = l >> 2;
+    const int bh = blockIdx.x;
+    const int hi = bh % H;
+    const int row = 4 * blk + ri;
+    const int64_t base0 = (int64_t)bh * D;   // [B, H, 64]
+    const int64_t sbase = (int64_t)bh * D * D + (int64_t)row * D + 4 * gq;
+
+    float S[4], N[4];
+    if (h_in) {
+        const float4 f = *reinterpret_cast<const float4*>(h_in + sbase);
+        S[0] = f.x; S[1] = f.y; S[2] = f.z; S[3] = f.w;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) S[c] = 0.0f;
+    }
+    const float A = a[base0 + l], W = w[base0 + l], K = k[base0 + l], Bv = b[base0 + l];
+    const float R = r[base0 + l], V = v[base0 + row];
+    float p = 0.0f;
+    fwd_dot4(S, A, p);
+    const float sa = rowsum16(p);
+    float y = 0.0f;
+    p = 0.0f;
+    fwd_update4(S, N, K, Bv, W, R, A, V, sa, y, p);
+    y = rowsum16(y);
+    *reinterpret_cast<float4*>(h_out + sbase) = make_float4(N[0], N[1], N[2], N[3]);
+    if (gq == 0) {
+        ys[row] = y;
+        if (wkv_out) wkv_out[base0 + row] = y;
+    }
+    __syncthreads();
+    if (blk == 0) {
+        const int64_t e = base0 + l, he = (int64_t)hi * D + l;
+        const float x = ys[l];
+        const float mean = wave_total(0.0f + x) / (float)D;
+        const float dd = x - mean;
+        const float inv = 1.0f / sqrtf(wave_total(fmaf(dd, dd, 0.0f)) / (float)D + eps);
+        const float dp = wave_total(fmaf(r[e] * k[e], rk[he], 0.0f));
+        const float nrm = (x - mean) * inv;
+        const float yo = fmaf(dp, v[e], fmaf(nrm, lnw[he], lnb[he]));
+        out[e] = yo * g[e];
+    }
+}
+
 // ─────────────────────────────── host dispatch ───────────────────────────────
 rwkv_status launch_status(const char* what) {
     hipError_t e = hipGetLastError();
@@ -675,19 +890,22 @@ template <bool SA, bool CK>
 rwkv_status launch_fwd(const void* r, const void* w, const void* k, const void* v, const void* a, const void* b,
                        rwkv_dtype dt, const float* h_in, float* out, float* h_out, float* sa_out, float* ck,
                        int64_t B, int64_t T, int64_t H, void* stream) {
-    dim3 grid((unsigned)(B * H * 4)), block(64);   // one wave per 16 value rows
+    const bool rows4 = use_rows4(B * H);
+    dim3 grid((unsigned)(B * H * (rows4 ? 16 : 4))), block(64);   // one wave per 4 / 16 value rows
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define RWKV_FWD(DTV)                                                                                        \
+    if (rows4)                                                                                               \
+        rwkv::launch(wkv7_fwd4_kernel<DTV, SA, CK>, grid, block, st, r, w, k, v, a, b, h_in, out, h_out, sa_out, \
+                     ck, (int)T, (int)H);                                                                    \
+    else                                                                                                     \
+        rwkv::launch(wkv7_fwd_kernel<DTV, SA, CK>, grid, block, st, r, w, k, v, a, b, h_in, out, h_out, sa_out,  \
+                     ck, (int)T, (int)H)
     switch (dt) {
-        case RWKV_F32:
-            rwkv::launch(wkv7_fwd_kernel<RWKV_F32, SA, CK>, grid, block, st, r, w, k, v, a, b, h_in, out, h_out, sa_out, ck, (int)T, (int)H);
-            break;
-        case RWKV_BF16:
-            rwkv::launch(wkv7_fwd_kernel<RWKV_BF16, SA, CK>, grid, block, st, r, w, k, v, a, b, h_in, out, h_out, sa_out, ck, (int)T, (int)H);
-            break;
-        case RWKV_F16:
-            rwkv::launch(wkv7_fwd_kernel<RWKV_F16, SA, CK>, grid, block, st, r, w, k, v, a, b, h_in, out, h_out, sa_out, ck, (int)T, (int)H);
-            break;
+        case RWKV_F32: RWKV_FWD(RWKV_F32); break;
+        case RWKV_BF16: RWKV_FWD(RWKV_BF16); break;
+        case RWKV_F16: RWKV_FWD(RWKV_F16); break;
     }
+#undef RWKV_FWD
     return launch_status("wkv7 forward launch");
 }
 
@@ -805,8 +1023,12 @@ rwkv_status rwkv_wkv7_step_tail(const float* r, const float* w, const float* k, 
                  "wkv7_step_tail: null buffer");
     RWKV_REQUIRE(B >= 1 && H >= 1 && B * H <= INT32_MAX, RWKV_E_SHAPE, "wkv7_step_tail: bad B (%lld) / H (%lld)",
                  (long long)B, (long long)H);
-    rwkv::launch(wkv7_step_tail_kernel, dim3((unsigned)(B * H)), dim3(256), reinterpret_cast<hipStream_t>(stream),
-                 r, w, k, v, a, b, h_in, h_out, rk, lnw, lnb, g, wkv_out, out, (int)H, eps);
+    if (use_rows4(B * H))
+        rwkv::launch(wkv7_step_tail4_kernel, dim3((unsigned)(B * H)), dim3(1024), reinterpret_cast<hipStream_t>(stream),
+                     r, w, k, v, a, b, h_in, h_out, rk, lnw, lnb, g, wkv_out, out, (int)H, eps);
+    else
+        rwkv::launch(wkv7_step_tail_kernel, dim3((unsigned)(B * H)), dim3(256), reinterpret_cast<hipStream_t>(stream),
+                     r, w, k, v, a, b, h_in, h_out, rk, lnw, lnb, g, wkv_out, out, (int)H, eps);
     rwkv_status s = launch_status("wkv7_step_tail launch");
     if (s == RWKV_OK) rwkv::counters().step_tail++;
     return s;

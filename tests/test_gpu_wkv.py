@@ -66,7 +66,9 @@ def test_seq_fwd_half_inputs_widened_exactly(orc, dt):
     assert rel(o64, host(out)) < TOL and rel(h64, host(h)) < TOL
 
 
-SHAPES = [(1, 1, 2), (1, 5, 3), (1, 16, 2), (1, 17, 4), (2, 53, 3), (1, 512, 12), (3, 32, 1)]
+# B·H < 256 runs four value rows per wave, B·H ≥ 256 sixteen: the last shape
+# takes the sixteen-row layout
+SHAPES = [(1, 1, 2), (1, 5, 3), (1, 16, 2), (1, 17, 4), (2, 53, 3), (1, 512, 12), (3, 32, 1), (2, 37, 128)]
 
 
 @pytest.mark.parametrize("B,T,H", SHAPES)
@@ -118,10 +120,11 @@ def test_switch_and_launch_counter():
     assert same(a, b) and same(ha, hb)
 
 
-def test_train_forward_equals_frozen_bitwise(orc):
-    case("train fwd == frozen fwd, checkpoints, sa")
-    xn = syn.wkv_inputs_train(2, 64, 4, seed=0)
-    h0n = syn.state(2, 4)
+@pytest.mark.parametrize("B,H", [(2, 4), (2, 128)])
+def test_train_forward_equals_frozen_bitwise(orc, B, H):
+    case(f"train fwd == frozen fwd, checkpoints, sa, B={B} H={H}")
+    xn = syn.wkv_inputs_train(B, 64, H, seed=0)
+    h0n = syn.state(B, H)
     x = [dev(z) for z in xn]
     h0 = dev(h0n)
     oF, hF = K.wkv7_forward_with_state(*x, h_in=h0)
@@ -160,7 +163,7 @@ def decode_inputs(H, seed):
     return [r, w, k, v, a, b], h
 
 
-@pytest.mark.parametrize("H,seed", [(12, 1), (3, 2), (32, 3)])
+@pytest.mark.parametrize("H,seed", [(12, 1), (3, 2), (32, 3), (256, 4)])
 def test_step_equals_sequence_kernel_on_one_token(H, seed):
     case(f"step == seq at T=1, H={H}")
     xn, hn = decode_inputs(H, seed)
@@ -209,7 +212,7 @@ def test_tail_matches_oracle(orc):
         K.wkv_tail(dev(wkv), dev(r), dev(k), dev(v), dev(rk), dev(lnw), dev(lnb), dev(g), H, 48, rows=N)
 
 
-@pytest.mark.parametrize("B,H", [(1, 12), (4, 3), (2, 32)])
+@pytest.mark.parametrize("B,H", [(1, 12), (4, 3), (2, 32), (2, 128)])
 def test_step_tail_equals_step_then_tail_bitwise(orc, B, H):
     case(f"fused step+tail B={B} H={H}")
     rng = np.random.default_rng(B * 100 + H)
@@ -282,6 +285,16 @@ def test_backward_matches_fp64_oracle(orc, v2):
     for n, e, g_ in zip(NAMES, errs, got):
         assert e < TOL, n
         assert g_.abs().max() > 0, n
+
+
+def test_backward_after_sixteen_row_forward_matches_fp64_oracle(orc):
+    # B·H = 256: the forward (sa, checkpoints) runs sixteen value rows per wave
+    case("backward v2 vs fp64 oracle B2 T32 H128")
+    x, h0, g, gh = train_case(B=2, T=32, H=128, seed=5)
+    got = kernel_grads(x, h0, g, gh)
+    want = orc.wkv7_bwd_f64(*x, h0, g, gh)
+    for n, w_, g_ in zip(NAMES, want, got):
+        assert rel(w_, host(g_)) < TOL, n
 
 
 def test_backward_config0_distribution(orc):
