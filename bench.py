@@ -283,6 +283,48 @@ def bench_decode_gemv(model, step, dev, reps=100):
     return model.bytes_per_token / n_gemv, e0.elapsed_time(e1) / (reps * n_gemv), n_gemv
 
 
+def bench_projection_crossover(model, dev, key="blocks.0.ffn.key.weight", reps=20):
+    """Parallel-pass projection of N input rows through one weight matrix
+    (the 0.1B ffn key, 3072x768): the GEMV kernel on the packed codes (all N
+    rows in one launch) against dequantise to fp16 + matmul (hipBLASLt), the
+    two branches of the model's baseProj.  Weights rotate over the copies."""
+    import torch
+    from swiftrwkv_amd import quant as Q
+
+    qblk, qsqm, ddm, OUT, IN = model.host[key]
+    copies = len(model.dev)
+    stream = torch.cuda.current_stream(dev)
+    res, cross = {}, None
+    for N in (1, 4, 16, 64, 256, 1024):
+        x = torch.randn((N, IN), device=dev)
+
+        def gemv(c):
+            q = model.dev[c][key]
+            return Q.rwkvq_sb6_gemv(x, q[0], q[1], q[2], OUT, IN, 0)
+
+        def deq_mm(c):
+            q = model.dev[c][key]
+            W = Q.rwkvq_dequant_dense(q[0], q[1], q[2], OUT, IN, 8, 0, torch.float16)
+            return torch.nn.functional.linear(x.to(torch.float16), W).float()
+
+        row = {}
+        for name, fn in (("gemv_us", gemv), ("dequant_matmul_us", deq_mm)):
+            for c in range(copies):
+                fn(c)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(reps):
+                fn(i % copies)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            row[name] = e0.elapsed_time(e1) * 1e3 / reps
+        res[N] = row
+        if cross is None and row["dequant_matmul_us"] < row["gemv_us"]:
+            cross = N
+    return {"shape": f"{OUT}x{IN} sb6 4-bit", "rows": res, "first_rows_where_dequant_matmul_wins": cross}
+
+
 def bench_wkv_prefill_7b(dev, reps=3):
     """WKV-7 forward of one layer of the 7B-class prefill: B1 T8192 H64 fp32."""
     import torch
@@ -309,7 +351,8 @@ def bench_decode_more(model_01, dev):
     import torch
     from swiftrwkv_amd import synthetic as syn
 
-    res = {}
+    res = {"projection_crossover_0.1B_ffn_key": bench_projection_crossover(model_01, dev)}
+    log(f"projection crossover: {res['projection_crossover_0.1B_ffn_key']}")
     for B in (8, 32):
         _, wall, gpu_ms = run_decode(model_01, dev, B, 50, 5, len(model_01.dev))
         res[f"decode_0.1B_batch{B}"] = {"tok_s": B * 50 / wall, "ms_per_step": wall * 1e3 / 50}

@@ -324,6 +324,15 @@ def rwkvq_sb6_gemv_applies(out_features: int, in_features: int, xbits: int, supe
     return bool(_lib.lib().rwkv_sb6_gemv_applies(out_features, in_features, xbits, super_block, rows))
 
 
+def default_short_pass_rows(n_embd: int, sym: bool) -> int:
+    """X070Backbone.defaultShortPassRows (X070Backbone.swift:384-389): up to
+    this many input rows (B·T) a frozen parallel pass runs on the GEMV kernels.
+    The reference's threshold reflects its one-row (sb6) / four-row (sym)
+    launches; with every row in one launch the measured crossover is higher
+    (bench.py reports it)."""
+    return max(4, n_embd // (128 if sym else 256))
+
+
 def rwkvq_sb6_gemv(x, qblk, qsqm, ddm, out_features: int, in_features: int, xbits: int,
                    out_per: Optional[int] = None) -> torch.Tensor:
     """y [N, OUT] = x [N, IN] · Wᵀ straight from the K3 bytes (RwkvqSb6GEMV.swift:170-190).
@@ -665,6 +674,39 @@ class RwkvqSidecar:
         if info.outlier_count > 0:
             raise UnsupportedKind(key, "rtn+outliers (SpQR scatter not implemented)")
         return rwkvq_dequant_rtn(codes, scale, dtype)
+
+    # ── projections (the .rwkvq branch of the model's baseProj) ──
+    def base_proj(self, key: str, x: torch.Tensor, base_dtype=torch.float16, decode: bool = False,
+                  short_rows: int = 0) -> torch.Tensor:
+        """x [..., IN] · Wᵀ → [..., OUT] in x's dtype, the .rwkvq branch of
+        X070Backbone.baseProj (X070Backbone.swift:676-746, 337-341): on the
+        recurrent step (`decode`) or a short parallel pass (B·T ≤ `short_rows`,
+        RWKVBlock.swift:418-423) the GEMV kernel on the packed codes; otherwise
+        dequantise to `base_dtype` and matmul in it.  The reference splits the
+        GEMV rows into launches of one (sb6) or four (sym); here all rows go in
+        one launch."""
+        info = self.tensors.get(key)
+        if info is None:
+            raise MissingBuffer(key, "manifest")
+        IN, OUT = info.in_features, info.out_features
+        if x.shape[-1] != IN:
+            raise ValueError(f"base_proj {key}: input {tuple(x.shape)}, expected [..., {IN}]")
+        lead = tuple(x.shape[:-1])
+        x2d = x.reshape(-1, IN)
+        rows = x2d.shape[0]
+        if decode or (short_rows > 0 and rows <= short_rows):
+            y = None
+            if info.kind == RwkvqKind.sb6 and rwkvq_sb6_gemv_applies(OUT, IN, info.xbits, info.super_block, 1):
+                y = rwkvq_sb6_gemv(x2d.float(), self._buf(key, "qblk"), self._buf(key, "qsqm"),
+                                   self._buf(key, "ddm"), OUT, IN, info.xbits)
+            elif info.kind == RwkvqKind.sym and rwkvq_sym_gemv_applies(OUT, IN, info.bits, 1):
+                y = rwkvq_sym_gemv(x2d.float(), self._buf(key, "qblk"), self._buf(key, "qs"), self._buf(key, "d"),
+                                   OUT, IN, info.bits)
+            if y is not None:
+                return y.to(x.dtype).reshape(*lead, OUT)
+        W = self.dequantize(key, base_dtype)   # the transient dense weight, [OUT, IN]
+        y = torch.nn.functional.linear(x2d.to(base_dtype), W)
+        return y.to(x.dtype).reshape(*lead, OUT)
 
     # ── GEMV (decode) ──
     def sb6_gemv(self, key: str, x: torch.Tensor) -> Optional[torch.Tensor]:

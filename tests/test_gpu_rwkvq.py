@@ -322,3 +322,43 @@ def test_sidecar_end_to_end(tmp_path, orc, kind, bits):
         assert sc.sym_gemv_fused("att0", torch.zeros((2, 256), device=DEV)) is None
         assert sc.sym_gemv_fused("none", xs) is None
     assert torch.equal(sc.dequantize("ln_out.weight"), sc.arrays["ln_out.weight::dense"].float())
+
+
+@pytest.mark.parametrize("kind,bits", [("sb6", 4), ("sym", 8)])
+def test_base_proj_paths(tmp_path, orc, kind, bits):
+    """The .rwkvq branch of baseProj: GEMV on decode / short passes, dequantise
+    + matmul in the base dtype otherwise, the result in the input's dtype."""
+    case(f"base_proj {kind}{bits}")
+    p = str(tmp_path / f"{kind}{bits}.rwkvq")
+    synth_file(p, kind, bits)
+    sc = Q.RwkvqSidecar.from_rwkvq(p)
+    key = "blocks.1.ffn.key.weight"   # 1024 x 256
+    W = sc.dequantize(key).double()
+    gen = torch.Generator(DEV).manual_seed(3)
+    x = torch.randn((2, 5, 256), device=DEV, generator=gen)
+    want = (x.double() @ W.T).cpu().numpy()
+    gemv = Q.rwkvq_sb6_gemv if kind == "sb6" else Q.rwkvq_sym_gemv
+    fields = ("qblk", "qsqm", "ddm") if kind == "sb6" else ("qblk", "qs", "d")
+    code = sc.tensors[key].xbits if kind == "sb6" else bits
+    direct = gemv(x.reshape(10, 256), *[sc.arrays[f"{key}::{f}"] for f in fields], 1024, 256, code)
+    # decode and short passes: the kernel, all ten rows in one launch
+    for kw in ({"decode": True}, {"short_rows": 10}):
+        y = sc.base_proj(key, x, **kw)
+        assert y.shape == (2, 5, 1024) and y.dtype == torch.float32
+        assert torch.equal(y.reshape(10, 1024), direct), kw
+        assert rel(want, y.cpu().numpy()) < GEMV_TOL
+    # longer than the short-pass threshold: dequantise to fp16 / bf16 + matmul
+    for base in (torch.float16, torch.bfloat16):
+        y = sc.base_proj(key, x, base_dtype=base, short_rows=9)
+        assert y.dtype == torch.float32
+        ref = torch.nn.functional.linear(x.reshape(10, 256).to(base), sc.dequantize(key, base)).float()
+        assert torch.equal(y.reshape(10, 1024), ref)
+        assert rel(want, y.cpu().numpy()) < (2e-3 if base == torch.float16 else 1e-2)
+    # the output takes the input's dtype
+    xb = x.to(torch.bfloat16)
+    assert sc.base_proj(key, xb, decode=True).dtype == torch.bfloat16
+    assert sc.base_proj(key, xb).dtype == torch.bfloat16
+    assert Q.default_short_pass_rows(768, sym=False) == 4
+    assert Q.default_short_pass_rows(2048, sym=True) == 16
+    with pytest.raises(ValueError):
+        sc.base_proj(key, torch.zeros((1, 128), device=DEV))

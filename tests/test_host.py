@@ -79,6 +79,11 @@ def test_applies_tables_are_the_reference_ones():
     assert quant.RWKVQ_SYM_GEMV_MAX_ROWS == 4
     from swiftrwkv_amd import kernel
     assert kernel.wkv_tail_applies(64) and not kernel.wkv_tail_applies(48)
+    # X070Backbone.defaultShortPassRows: max(4, D / 128) sym, max(4, D / 256) sb6
+    assert quant.default_short_pass_rows(768, sym=False) == 4
+    assert quant.default_short_pass_rows(2048, sym=False) == 8
+    assert quant.default_short_pass_rows(2048, sym=True) == 16
+    assert quant.default_short_pass_rows(4096, sym=True) == 32
 
 
 def test_unpack6_product_equals_oracle(orc):
