@@ -153,6 +153,15 @@ rwkv_status rwkv_sym_dequant(const uint8_t* qblk, const uint8_t* qs, const uint1
                              void* out, rwkv_dtype out_dt, int64_t OUT, int64_t IN, int bits,
                              void* stream);
 
+/* Rows ids[0..n) of a sym matrix, dequantised on demand (the embedding
+ * table): out [n, IN] = the rows rwkv_sym_dequant would give for those matrix
+ * rows, bitwise.  ids int32 on the device; an id outside [0, OUT) gives a row
+ * of NaN; n == 0 is a no-op (ids and out may be NULL).  Replaces RwkvqSymRowTable.rows (Sources/RWKVQuant/RwkvqSymRows.swift:43-53),
+ * which takes 8-bit tables; 6-bit ones work as well. */
+rwkv_status rwkv_sym_rows(const int32_t* ids, int64_t n, const uint8_t* qblk, const uint8_t* qs,
+                          const uint16_t* d, void* out, rwkv_dtype out_dt, int64_t OUT, int64_t IN,
+                          int bits, void* stream);
+
 /* rwkvqSb6GEMVApplies (Sources/RWKVQuant/RwkvqSb6GEMV.swift:159-164), same table. */
 int rwkv_sb6_gemv_applies(int64_t OUT, int64_t IN, int xbits, int super_block, int64_t rows);
 
@@ -252,6 +261,7 @@ typedef struct {
     int64_t sym_fused;      /* rwkvqSymFusedCalls */
     int64_t step_tail;      /* rwkv_wkv7_step_tail launches (no reference counter) */
     int64_t sb6_fused;      /* rwkv_sb6_gemv_fused launches (no reference counter) */
+    int64_t sym_rows;       /* rwkv_sym_rows launches (no reference counter) */
 } rwkv_counters;
 
 void rwkv_get_counters(rwkv_counters* out);

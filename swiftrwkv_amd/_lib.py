@@ -38,7 +38,7 @@ class RwkvHipError(RuntimeError):
 class Counters(ctypes.Structure):
     _fields_ = [(n, L) for n in ("seq_fwd", "chunk_fwd", "train_fwd", "train_bwd", "step", "tail",
                                  "sb6_dequant", "sym_dequant", "sb6_gemv", "sym_gemv", "sym_fused",
-                                 "step_tail", "sb6_fused")]
+                                 "step_tail", "sb6_fused", "sym_rows")]
 
 
 # name → (restype, argtypes)
@@ -58,6 +58,7 @@ _SIGS = {
     "rwkv_wkv_tail": (I, [P] * 9 + [L, L, L, F, P]),
     "rwkv_sb6_dequant": (I, [P, P, P, P, I, L, L, I, P]),
     "rwkv_sym_dequant": (I, [P, P, P, P, I, L, L, I, P]),
+    "rwkv_sym_rows": (I, [P, L, P, P, P, P, I, L, L, I, P]),
     "rwkv_sb6_gemv_applies": (I, [L, L, I, I, L]),
     "rwkv_sb6_gemv": (I, [P, L, P, P, P, P, L, L, I, P]),
     "rwkv_sb6_gemv_fused": (I, [P, L, P, P, P, P, L, L, I, L, P]),

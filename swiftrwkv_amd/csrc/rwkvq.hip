@@ -106,14 +106,26 @@ __global__ __launch_bounds__(256) void sb6_dequant_kernel(
 // 8-bit: one thread per 4 columns.  6-bit: one thread per (pair, part p),
 // part p = columns 4p..4p+3 of the pair in register order l0,l1,h0,h1,l2,l3,h2,h3.
 template <int BITS, int DT>
+// With `ids` (n rows): output row o is matrix row ids[o] (the embedding row
+// gather); an id outside [0, OUT) gives a row of NaN.
 __global__ __launch_bounds__(256) void sym_dequant_kernel(
     const uint8_t* __restrict__ qblk, const uint8_t* __restrict__ qs, const uint16_t* __restrict__ d,
-    void* __restrict__ out, int64_t OUT, int64_t IN) {
+    void* __restrict__ out, int64_t OUT, int64_t IN, const int32_t* __restrict__ ids, int64_t n) {
     const int64_t NB = IN >> 4, NSB = (NB + 15) >> 4;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= OUT * (IN >> 2)) return;
-    const int64_t row = gid / (IN >> 2);
-    const int64_t col = (gid - row * (IN >> 2)) * 4;
+    const int64_t rows = ids ? n : OUT;
+    if (gid >= rows * (IN >> 2)) return;
+    const int64_t orow = gid / (IN >> 2);
+    const int64_t col = (gid - orow * (IN >> 2)) * 4;
+    int64_t row = orow;
+    if (ids) {
+        row = ids[orow];
+        if (row < 0 || row >= OUT) {
+            const float nan = __int_as_float(0x7fc00000);
+            store4<DT>(out, orow * IN + col, nan, nan, nan, nan);
+            return;
+        }
+    }
     const int64_t blk = col >> 4;
     const float s = hround((float)(int8_t)qs[row * NB + blk] * f16f(d[row * NSB + (blk >> 4)]));
     float f[4];
@@ -133,7 +145,7 @@ __global__ __launch_bounds__(256) void sym_dequant_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) f[e] = (float)((int)((q4 >> (8 * e)) & 0xffu) - 32) * s;
     }
-    store4<DT>(out, row * IN + col, f[0], f[1], f[2], f[3]);
+    store4<DT>(out, orow * IN + col, f[0], f[1], f[2], f[3]);
 }
 
 // ─────────────────────────────── GEMV ───────────────────────────────
@@ -913,7 +925,8 @@ rwkv_status rwkv_sym_dequant(const uint8_t* qblk, const uint8_t* qs, const uint1
     RWKV_REQUIRE(total / 256 < INT32_MAX, RWKV_E_SHAPE, "sym_dequant: tensor too large");
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define RWKV_DQ(BITS, DT) rwkv::launch(sym_dequant_kernel<BITS, DT>, grid, block, st, qblk, qs, d, out, OUT, IN)
+#define RWKV_DQ(BITS, DT) \
+    rwkv::launch(sym_dequant_kernel<BITS, DT>, grid, block, st, qblk, qs, d, out, OUT, IN, (const int32_t*)nullptr, (int64_t)0)
 #define RWKV_DQ_DT(BITS)                                  \
     switch (out_dt) {                                     \
         case RWKV_F32: RWKV_DQ(BITS, RWKV_F32); break;    \
@@ -929,6 +942,39 @@ rwkv_status rwkv_sym_dequant(const uint8_t* qblk, const uint8_t* qs, const uint1
 #undef RWKV_DQ
     rwkv_status s = launch_status("sym_dequant launch");
     if (s == RWKV_OK) rwkv::counters().sym_dequant++;
+    return s;
+}
+
+rwkv_status rwkv_sym_rows(const int32_t* ids, int64_t n, const uint8_t* qblk, const uint8_t* qs, const uint16_t* d,
+                          void* out, rwkv_dtype out_dt, int64_t OUT, int64_t IN, int bits, void* stream) {
+    RWKV_REQUIRE((ids && out) || n == 0, RWKV_E_NULL, "sym_rows: null ids / output");
+    RWKV_REQUIRE(qblk && qs && d, RWKV_E_NULL, "sym_rows: null buffer");
+    RWKV_REQUIRE(bits == 6 || bits == 8, RWKV_E_SHAPE, "sym_rows: bits %d outside {6, 8}", bits);
+    RWKV_REQUIRE(rwkv::dtype_ok(out_dt), RWKV_E_DTYPE, "sym_rows: output dtype code %d", out_dt);
+    RWKV_REQUIRE(OUT >= 1 && IN >= 16 && IN % (bits == 8 ? 16 : 32) == 0 && n >= 0, RWKV_E_SHAPE,
+                 "sym_rows: IN (%lld) must be a positive multiple of %d, n (%lld) >= 0", (long long)IN,
+                 bits == 8 ? 16 : 32, (long long)n);
+    RWKV_REQUIRE(OUT <= INT32_MAX && n * (IN / 4) / 256 < INT32_MAX, RWKV_E_SHAPE, "sym_rows: too large");
+    if (n == 0) return RWKV_OK;
+    const int64_t total = n * (IN / 4);
+    dim3 grid((unsigned)((total + 255) / 256)), block(256);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define RWKV_DQ(BITS, DT) rwkv::launch(sym_dequant_kernel<BITS, DT>, grid, block, st, qblk, qs, d, out, OUT, IN, ids, n)
+#define RWKV_DQ_DT(BITS)                                  \
+    switch (out_dt) {                                     \
+        case RWKV_F32: RWKV_DQ(BITS, RWKV_F32); break;    \
+        case RWKV_BF16: RWKV_DQ(BITS, RWKV_BF16); break;  \
+        case RWKV_F16: RWKV_DQ(BITS, RWKV_F16); break;    \
+    }
+    if (bits == 8) {
+        RWKV_DQ_DT(8)
+    } else {
+        RWKV_DQ_DT(6)
+    }
+#undef RWKV_DQ_DT
+#undef RWKV_DQ
+    rwkv_status s = launch_status("sym_rows launch");
+    if (s == RWKV_OK) rwkv::counters().sym_rows++;
     return s;
 }
 

@@ -309,6 +309,21 @@ def rwkvq_dequant_sym(qblk, qs, d, out_features: int, in_features: int, bits: in
     return out
 
 
+def rwkvq_sym_rows(ids, qblk, qs, d, out_features: int, in_features: int, bits: int,
+                   dtype=torch.float16) -> torch.Tensor:
+    """Rows `ids` (any shape) of a sym matrix → [..., IN], dequantised on demand:
+    bitwise the rows of rwkvq_dequant_sym (RwkvqSymRows.swift:43-53).  An id
+    outside [0, OUT) gives a row of NaN."""
+    if dtype not in _OUT_DT:
+        raise ValueError(f"sym rows to {dtype} are not supported")
+    qblk, qs, d = _sym_bufs(qblk, qs, d, out_features, in_features, bits)
+    idx = ids.to(device=qblk.device, dtype=torch.int32).contiguous()
+    out = torch.empty(tuple(idx.shape) + (in_features,), dtype=dtype, device=qblk.device)
+    _lib.call("rwkv_sym_rows", idx.data_ptr(), idx.numel(), qblk.data_ptr(), qs.data_ptr(), d.data_ptr(),
+              out.data_ptr(), _OUT_DT[dtype], out_features, in_features, bits, _stream(qblk))
+    return out
+
+
 def rwkvq_sb6_gemv_config(out_features: int, in_features: int, xbits: int) -> Tuple[int, int]:
     """(NSG, RS) table of the reference kernel (RwkvqSb6GEMV.swift:39-43).
     Only the applicability rule depends on it here."""
@@ -402,6 +417,29 @@ class RwkvqSb6FusedGroup:
     out_per: int
     in_features: int
     xbits: int
+
+
+@dataclass
+class RwkvqSymRowTable:
+    """An 8-bit sym embedding table read row by row; no dense table exists
+    (RwkvqSymRows.swift:26-67)."""
+    qblk: torch.Tensor
+    qs: torch.Tensor
+    d: torch.Tensor
+    row_count: int
+    in_features: int
+
+    def rows(self, ids: torch.Tensor) -> torch.Tensor:
+        """ids of any shape → [..., IN] fp16 (RwkvqSymRows.swift:43-53)."""
+        return rwkvq_sym_rows(ids, self.qblk, self.qs, self.d, self.row_count, self.in_features, 8)
+
+    def dense(self) -> torch.Tensor:
+        """The whole table, [rows, IN] fp16 (RwkvqSymRows.swift:57-61)."""
+        return rwkvq_dequant_sym(self.qblk, self.qs, self.d, self.row_count, self.in_features, 8, torch.float16)
+
+    @property
+    def packed_bytes(self) -> int:
+        return self.qblk.numel() + self.qs.numel() + self.d.numel() * 2
 
 
 @dataclass
@@ -674,6 +712,19 @@ class RwkvqSidecar:
         if info.outlier_count > 0:
             raise UnsupportedKind(key, "rtn+outliers (SpQR scatter not implemented)")
         return rwkvq_dequant_rtn(codes, scale, dtype)
+
+    def sym_row_table(self, key: str) -> Optional[RwkvqSymRowTable]:
+        """RwkvqSymRows.swift:70-80: a row table for an 8-bit sym tensor, None
+        otherwise (the caller then takes the dense path)."""
+        info = self.tensors.get(key)
+        if (info is None or info.kind != RwkvqKind.sym or info.bits != 8 or len(info.shape) != 2
+                or info.in_features % 16):
+            return None
+        names = [f"{key}::{f}" for f in ("qblk", "qs", "d")]
+        if any(n not in self.arrays for n in names):
+            return None
+        qblk, qs, d = (self.arrays[n] for n in names)
+        return RwkvqSymRowTable(qblk, qs, d, info.out_features, info.in_features)
 
     # ── projections (the .rwkvq branch of the model's baseProj) ──
     def base_proj(self, key: str, x: torch.Tensor, base_dtype=torch.float16, decode: bool = False,

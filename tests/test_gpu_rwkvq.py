@@ -362,3 +362,43 @@ def test_base_proj_paths(tmp_path, orc, kind, bits):
     assert Q.default_short_pass_rows(2048, sym=True) == 16
     with pytest.raises(ValueError):
         sc.base_proj(key, torch.zeros((1, 128), device=DEV))
+
+
+@pytest.mark.parametrize("bits", [8, 6])
+def test_sym_rows_equal_dense_rows_bitwise(orc, bits):
+    """RwkvqSymRows: the gathered rows are the dense table's rows, bitwise."""
+    case(f"sym rows bits={bits}")
+    OUT, IN = 1000, 256 + 128 * (bits == 8)   # IN off the 256 super-block for 8 bits
+    qblk, qs, d = (dev(z) for z in sym_tensor(orc, OUT, IN, bits, seed=50 + bits))
+    ids = torch.tensor([[0, 999, 17], [17, 500, 3]], device=DEV)
+    for dt in (torch.float16, torch.bfloat16, torch.float32):
+        dense = Q.rwkvq_dequant_sym(qblk, qs, d, OUT, IN, bits, dt)
+        _lib.reset_counters()
+        rows = Q.rwkvq_sym_rows(ids, qblk, qs, d, OUT, IN, bits, dt)
+        assert _lib.counters()["sym_rows"] == 1
+        assert rows.shape == (2, 3, IN) and rows.dtype == dt
+        assert torch.equal(rows, dense[ids]), dt
+    # out-of-range ids give NaN rows; the others are unaffected
+    bad = Q.rwkvq_sym_rows(torch.tensor([5, -1, OUT], device=DEV), qblk, qs, d, OUT, IN, bits)
+    assert torch.equal(bad[0], Q.rwkvq_dequant_sym(qblk, qs, d, OUT, IN, bits, torch.float16)[5])
+    assert torch.isnan(bad[1:]).all()
+    assert Q.rwkvq_sym_rows(torch.zeros((0,), dtype=torch.int64, device=DEV), qblk, qs, d, OUT, IN, bits).shape == (0, IN)
+
+
+def test_sym_row_table_from_sidecar(tmp_path):
+    case("sym row table from a .rwkvq file")
+    p8, p6 = str(tmp_path / "s8.rwkvq"), str(tmp_path / "s6.rwkvq")
+    synth_file(p8, "sym", 8)
+    synth_file(p6, "sym", 6)
+    sc8, sc6 = Q.RwkvqSidecar.from_rwkvq(p8), Q.RwkvqSidecar.from_rwkvq(p6)
+    key = "blocks.0.ffn.key.weight"
+    t = sc8.sym_row_table(key)
+    assert t is not None and t.row_count == 1024 and t.in_features == 256
+    ids = torch.tensor([3, 1023, 3, 0], device=DEV)
+    assert torch.equal(t.rows(ids), t.dense()[ids])
+    assert torch.equal(t.dense(), sc8.dequantize(key, torch.float16))
+    assert t.packed_bytes == 1024 * 256 + 1024 * 16 + 1024 * 2
+    # the reference declines 6-bit tables and non-sym tensors (RwkvqSymRows.swift:70-80)
+    assert sc6.sym_row_table(key) is None
+    assert sc8.sym_row_table("ln_out.weight") is None
+    assert sc8.sym_row_table("missing") is None
