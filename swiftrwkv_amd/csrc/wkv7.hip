@@ -42,10 +42,11 @@
 #include <utility>
 
 #include "launch.h"
+#include "wkv7_step.h"
 
 namespace {
 
-constexpr int D = 64;   // WKV7_HEAD_SIZE
+using namespace rwkv_wkv;
 constexpr int CH = 16;  // WKV7_CHUNK
 
 template <int DT>
@@ -70,146 +71,6 @@ __device__ __forceinline__ void store1(void* __restrict__ p, int64_t off, float 
         reinterpret_cast<uint16_t*>(p)[off] = __builtin_bit_cast(uint16_t, (_Float16)x);
     }
 }
-
-// ─────────────────────────────── DPP / lane-swap helpers ───────────────────────────────
-// row_newbcast:c broadcasts lane c of every 16-lane row to the whole row.  The
-// compiler does not fold a DPP move into an FMA, so the fused forms are written
-// as inline assembly.  Every block starts with `s_nop 1`: the two wait states a
-// VALU write of a broadcast source needs before its DPP read.
-#define RWKV_BC(n) " row_newbcast:" #n " row_mask:0xf bank_mask:0xf\n\t"
-
-// Sum of the four column-group partials of a row (lanes l, l^16, l^32, l^48),
-// associated as (g0+g1)+(g2+g3) in every lane, so all four hold the same bits.
-__device__ __forceinline__ float rowsum4(float x) {
-    float a = x, b = x;
-    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    const float s = a + b;
-    float c = s, d = s;
-    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
-    return c + d;
-}
-
-// Forward update of 8 state elements (columns c0..c0+7 of the lane's group):
-//   n = k·v ; n += b·sa ; n += w·S          (new state, one rounding per FMA)
-//   y += r·n ; p += a'·n                    (a' = next step's a)
-// Issued stage by stage over the 8 elements, so neighbouring instructions are
-// independent (the y and p chains alternate).
-#define RWKV_MUL(c, N) "v_mul_f32_dpp %[" N "], %[K], %[vv]" RWKV_BC(c)
-#define RWKV_FB(c, N) "v_fmac_f32_dpp %[" N "], %[B], %[sa]" RWKV_BC(c)
-#define RWKV_FW(c, S, N) "v_fmac_f32_dpp %[" N "], %[W], %[" S "]" RWKV_BC(c)
-#define RWKV_YP(c, N) "v_fmac_f32_dpp %[y], %[R], %[" N "]" RWKV_BC(c) "v_fmac_f32_dpp %[p], %[A], %[" N "]" RWKV_BC(c)
-#define RWKV_UPD8(c0, c1, c2, c3, c4, c5, c6, c7)                                                              \
-    RWKV_MUL(c0, "n0") RWKV_MUL(c1, "n1") RWKV_MUL(c2, "n2") RWKV_MUL(c3, "n3")                                 \
-    RWKV_MUL(c4, "n4") RWKV_MUL(c5, "n5") RWKV_MUL(c6, "n6") RWKV_MUL(c7, "n7")                                 \
-    RWKV_FB(c0, "n0") RWKV_FB(c1, "n1") RWKV_FB(c2, "n2") RWKV_FB(c3, "n3")                                     \
-    RWKV_FB(c4, "n4") RWKV_FB(c5, "n5") RWKV_FB(c6, "n6") RWKV_FB(c7, "n7")                                     \
-    RWKV_FW(c0, "s0", "n0") RWKV_FW(c1, "s1", "n1") RWKV_FW(c2, "s2", "n2") RWKV_FW(c3, "s3", "n3")             \
-    RWKV_FW(c4, "s4", "n4") RWKV_FW(c5, "s5", "n5") RWKV_FW(c6, "s6", "n6") RWKV_FW(c7, "s7", "n7")             \
-    RWKV_YP(c0, "n0") RWKV_YP(c1, "n1") RWKV_YP(c2, "n2") RWKV_YP(c3, "n3")                                     \
-    RWKV_YP(c4, "n4") RWKV_YP(c5, "n5") RWKV_YP(c6, "n6") RWKV_YP(c7, "n7")
-
-#define RWKV_UPD_OPERANDS(S, N, o)                                                                              \
-    : [n0] "=&v"(N[o + 0]), [n1] "=&v"(N[o + 1]), [n2] "=&v"(N[o + 2]), [n3] "=&v"(N[o + 3]),                    \
-      [n4] "=&v"(N[o + 4]), [n5] "=&v"(N[o + 5]), [n6] "=&v"(N[o + 6]), [n7] "=&v"(N[o + 7]), [y] "+v"(y),        \
-      [p] "+v"(p)                                                                                                 \
-    : [s0] "v"(S[o + 0]), [s1] "v"(S[o + 1]), [s2] "v"(S[o + 2]), [s3] "v"(S[o + 3]), [s4] "v"(S[o + 4]),         \
-      [s5] "v"(S[o + 5]), [s6] "v"(S[o + 6]), [s7] "v"(S[o + 7]), [K] "v"(K), [B] "v"(B), [W] "v"(W), [R] "v"(R), \
-      [A] "v"(A), [vv] "v"(vv), [sa] "v"(sa)
-
-__device__ __forceinline__ void fwd_update16(const float (&S)[16], float (&N)[16], float K, float B, float W,
-                                             float R, float A, float vv, float sa, float& y, float& p) {
-    asm("s_nop 1\n\t" RWKV_UPD8(0, 1, 2, 3, 4, 5, 6, 7) RWKV_UPD_OPERANDS(S, N, 0));
-    asm("s_nop 1\n\t" RWKV_UPD8(8, 9, 10, 11, 12, 13, 14, 15) RWKV_UPD_OPERANDS(S, N, 8));
-}
-
-// p += Σ_c a_c·S_c over the lane's 16 columns (the first step's sa partial).
-#define RWKV_DOT(c, S) "v_fmac_f32_dpp %[p], %[A], %[" S "]" RWKV_BC(c)
-__device__ __forceinline__ void fwd_dot16(const float (&S)[16], float A, float& p) {
-    asm("s_nop 1\n\t"
-        RWKV_DOT(0, "s0") RWKV_DOT(1, "s1") RWKV_DOT(2, "s2") RWKV_DOT(3, "s3")
-        RWKV_DOT(4, "s4") RWKV_DOT(5, "s5") RWKV_DOT(6, "s6") RWKV_DOT(7, "s7")
-        : [p] "+v"(p)
-        : [s0] "v"(S[0]), [s1] "v"(S[1]), [s2] "v"(S[2]), [s3] "v"(S[3]), [s4] "v"(S[4]), [s5] "v"(S[5]),
-          [s6] "v"(S[6]), [s7] "v"(S[7]), [A] "v"(A));
-    asm("s_nop 1\n\t"
-        RWKV_DOT(8, "s0") RWKV_DOT(9, "s1") RWKV_DOT(10, "s2") RWKV_DOT(11, "s3")
-        RWKV_DOT(12, "s4") RWKV_DOT(13, "s5") RWKV_DOT(14, "s6") RWKV_DOT(15, "s7")
-        : [p] "+v"(p)
-        : [s0] "v"(S[8]), [s1] "v"(S[9]), [s2] "v"(S[10]), [s3] "v"(S[11]), [s4] "v"(S[12]), [s5] "v"(S[13]),
-          [s6] "v"(S[14]), [s7] "v"(S[15]), [A] "v"(A));
-}
-
-// Four-row layout (small B·H): lane l holds value row 4·blk + (l & 3) and key
-// columns 4g..4g+3, g = l >> 2; the four lanes of a quad share g and hold
-// elements 4g..4g+3 of each step vector, broadcast with DPP quad_perm.
-#define RWKV_QB(c) " quad_perm:[" #c "," #c "," #c "," #c "] row_mask:0xf bank_mask:0xf\n\t"
-#define RWKV_QMUL(c, N) "v_mul_f32_dpp %[" N "], %[K], %[vv]" RWKV_QB(c)
-#define RWKV_QFB(c, N) "v_fmac_f32_dpp %[" N "], %[B], %[sa]" RWKV_QB(c)
-#define RWKV_QFW(c, S, N) "v_fmac_f32_dpp %[" N "], %[W], %[" S "]" RWKV_QB(c)
-#define RWKV_QYP(c, N) "v_fmac_f32_dpp %[y], %[R], %[" N "]" RWKV_QB(c) "v_fmac_f32_dpp %[p], %[A], %[" N "]" RWKV_QB(c)
-
-// The forward update of the lane's 4 state elements (the same FMA sequence per
-// element as fwd_update16).
-__device__ __forceinline__ void fwd_update4(const float (&S)[4], float (&N)[4], float K, float B, float W, float R,
-                                            float A, float vv, float sa, float& y, float& p) {
-    asm("s_nop 1\n\t"
-        RWKV_QMUL(0, "n0") RWKV_QMUL(1, "n1") RWKV_QMUL(2, "n2") RWKV_QMUL(3, "n3")
-        RWKV_QFB(0, "n0") RWKV_QFB(1, "n1") RWKV_QFB(2, "n2") RWKV_QFB(3, "n3")
-        RWKV_QFW(0, "s0", "n0") RWKV_QFW(1, "s1", "n1") RWKV_QFW(2, "s2", "n2") RWKV_QFW(3, "s3", "n3")
-        RWKV_QYP(0, "n0") RWKV_QYP(1, "n1") RWKV_QYP(2, "n2") RWKV_QYP(3, "n3")
-        : [n0] "=&v"(N[0]), [n1] "=&v"(N[1]), [n2] "=&v"(N[2]), [n3] "=&v"(N[3]), [y] "+v"(y), [p] "+v"(p)
-        : [s0] "v"(S[0]), [s1] "v"(S[1]), [s2] "v"(S[2]), [s3] "v"(S[3]), [K] "v"(K), [B] "v"(B), [W] "v"(W),
-          [R] "v"(R), [A] "v"(A), [vv] "v"(vv), [sa] "v"(sa));
-}
-
-// p += Σ_c a_c·S_c over the lane's 4 columns.
-__device__ __forceinline__ void fwd_dot4(const float (&S)[4], float A, float& p) {
-    asm("s_nop 1\n\t"
-        "v_fmac_f32_dpp %[p], %[A], %[s0]" RWKV_QB(0) "v_fmac_f32_dpp %[p], %[A], %[s1]" RWKV_QB(1)
-        "v_fmac_f32_dpp %[p], %[A], %[s2]" RWKV_QB(2) "v_fmac_f32_dpp %[p], %[A], %[s3]" RWKV_QB(3)
-        : [p] "+v"(p)
-        : [s0] "v"(S[0]), [s1] "v"(S[1]), [s2] "v"(S[2]), [s3] "v"(S[3]), [A] "v"(A));
-}
-
-// Sum of a value row's 16 column-group partials (lanes l & 3 + 4g): within a
-// 16-lane DPP row the lanes 8 and then 4 apart (row_ror), then across the
-// four DPP rows (rowsum4).  Every lane of the row ends with the same bits.
-__device__ __forceinline__ float rowsum16(float x) {
-    float t, u;
-    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0xf" : "=&v"(t) : "v"(x));
-    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:4 row_mask:0xf bank_mask:0xf" : "=&v"(u) : "v"(t));
-    return rowsum4(u);
-}
-
-// rowsum16 of two independent values with their instructions interleaved
-// (the same operations per value, so the same bits): in the four-row layout
-// the next step's sa and the last step's y are reduced together, which hides
-// the latency of each chain's dependent steps (in the sixteen-row layout,
-// which issues back to back anyway, the pairing measured 5 % slower).
-#define RWKV_SWAP_PAIR(OP)                        \
-    "v_mov_b32 %[b0], %[x0]\n\t"                 \
-    "v_mov_b32 %[b1], %[x1]\n\t"                 \
-    "s_nop 1\n\t"                                \
-    OP " %[x0], %[b0]\n\t"                       \
-    OP " %[x1], %[b1]\n\t"                       \
-    "v_add_f32 %[x0], %[x0], %[b0]\n\t"          \
-    "v_add_f32 %[x1], %[x1], %[b1]\n\t"
-__device__ __forceinline__ void rowsum16_pair(float& x0, float& x1) {
-    float b0, b1;
-    asm("s_nop 1\n\t"
-        "v_add_f32_dpp %[b0], %[x0], %[x0] row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32_dpp %[b1], %[x1], %[x1] row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
-        "s_nop 1\n\t"
-        "v_add_f32_dpp %[x0], %[b0], %[b0] row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
-        "v_add_f32_dpp %[x1], %[b1], %[b1] row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
-        RWKV_SWAP_PAIR("v_permlane16_swap_b32") RWKV_SWAP_PAIR("v_permlane32_swap_b32")
-        : [x0] "+v"(x0), [x1] "+v"(x1), [b0] "=&v"(b0), [b1] "=&v"(b1));
-}
-
-// Layout choice, a function of B·H only (so every entry point agrees bitwise
-// for a given batch and head count): four rows per wave while sixteen would
-// leave the chip with fewer waves than SIMDs (1,024).
-__host__ __device__ constexpr bool use_rows4(int64_t BH) { return BH < 256; }
 
 // ─────────────────────────────── forward ───────────────────────────────
 // Grid: 4 workgroups of one wave per (b, h); workgroup 4·(b·H + h) + blk owns
@@ -754,11 +615,6 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
 }
 
 // ─────────────────────────────── tmix tail ───────────────────────────────
-__device__ __forceinline__ float wave_total(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-    return __shfl(x, 0, 64);   // one lane's association for everybody
-}
 
 __global__ __launch_bounds__(64) void wkv_tail_kernel(
     const float* __restrict__ wkv, const float* __restrict__ r, const float* __restrict__ k,
@@ -789,12 +645,14 @@ __global__ __launch_bounds__(64) void wkv_tail_kernel(
 }
 
 // ─────────────────────────────── decode: step + tail in one launch ───────────────────────────────
-// One workgroup of four waves per (row, head).  Wave `blk` runs the T = 1
-// path of wkv7_fwd_kernel for value rows 16·blk..16·blk+15 (same device code,
-// so state and wkv are bitwise those of rwkv_wkv7_step); the head's 64 wkv
-// values meet in LDS and wave 0 applies the tail with wkv_tail_kernel's exact
-// operation sequence for S = 64.
-__global__ __launch_bounds__(256) void wkv7_step_tail_kernel(
+// One workgroup per (row, head): four waves (sixteen-row layout) or sixteen
+// (four-row layout, B·H < 256), each the T = 1 path of the forward kernel for
+// its rows (head_step16 / head_step4: the same operations, so state and wkv
+// are bitwise those of rwkv_wkv7_step); the head's 64 wkv values meet in LDS
+// and wave 0 applies the tail with wkv_tail_kernel's operation sequence for
+// S = 64 (head_tail).
+template <bool R4>
+__global__ __launch_bounds__(R4 ? 1024 : 256) void wkv7_step_tail_kernel(
     const float* __restrict__ r, const float* __restrict__ w, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ a, const float* __restrict__ b,
     const float* __restrict__ h_in, float* __restrict__ h_out, const float* __restrict__ rk,
@@ -802,106 +660,24 @@ __global__ __launch_bounds__(256) void wkv7_step_tail_kernel(
     float* __restrict__ wkv_out, float* __restrict__ out, int H, float eps) {
     __shared__ float ys[D];
     const int blk = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int ri = l & 15, gq = l >> 4;
     const int bh = blockIdx.x;
     const int hi = bh % H;
-    const int row = 16 * blk + ri;
-    const int vidx = 16 * gq + ri;
     const int64_t base0 = (int64_t)bh * D;   // [B, H, 64]
-    const int64_t sbase = (int64_t)bh * D * D + (int64_t)row * D + 16 * gq;
-
-    float S[16], N[16];
-    if (h_in) {
-        const float4* src = reinterpret_cast<const float4*>(h_in + sbase);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const float4 f = src[m];
-            S[4 * m] = f.x; S[4 * m + 1] = f.y; S[4 * m + 2] = f.z; S[4 * m + 3] = f.w;
-        }
-    } else {
-#pragma unroll
-        for (int c = 0; c < 16; ++c) S[c] = 0.0f;
-    }
-    const float A = a[base0 + vidx], W = w[base0 + vidx], K = k[base0 + vidx], Bv = b[base0 + vidx];
-    const float R = r[base0 + vidx], V = v[base0 + row];
-    float p = 0.0f;
-    fwd_dot16(S, A, p);
-    const float sa = rowsum4(p);
-    float y = 0.0f;
-    p = 0.0f;
-    fwd_update16(S, N, K, Bv, W, R, A, V, sa, y, p);
-    y = rowsum4(y);
-    float4* dst = reinterpret_cast<float4*>(h_out + sbase);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) dst[m] = make_float4(N[4 * m], N[4 * m + 1], N[4 * m + 2], N[4 * m + 3]);
-    if (gq == 0) {
-        ys[row] = y;
-        if (wkv_out) wkv_out[base0 + row] = y;
-    }
-    __syncthreads();
-    if (blk == 0) {
-        const int64_t e = base0 + l, he = (int64_t)hi * D + l;
-        const float x = ys[l];
-        const float mean = wave_total(0.0f + x) / (float)D;
-        const float dd = x - mean;
-        const float inv = 1.0f / sqrtf(wave_total(fmaf(dd, dd, 0.0f)) / (float)D + eps);
-        const float dp = wave_total(fmaf(r[e] * k[e], rk[he], 0.0f));
-        const float nrm = (x - mean) * inv;
-        const float yo = fmaf(dp, v[e], fmaf(nrm, lnw[he], lnb[he]));
-        out[e] = yo * g[e];
-    }
-}
-
-// The same in the four-row layout: sixteen waves per (row, head), each the
-// T = 1 path of wkv7_fwd4_kernel for its four value rows.
-__global__ __launch_bounds__(1024) void wkv7_step_tail4_kernel(
-    const float* __restrict__ r, const float* __restrict__ w, const float* __restrict__ k,
-    const float* __restrict__ v, const float* __restrict__ a, const float* __restrict__ b,
-    const float* __restrict__ h_in, float* __restrict__ h_out, const float* __restrict__ rk,
-    const float* __restrict__ lnw, const float* __restrict__ lnb, const float* __restrict__ g,
-    float* __restrict__ wkv_out, float* __restrict__ out, int H, float eps) {
-    __shared__ float ys[D];
-    const int blk = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int ri = l & 3, gq = l >> 2;
-    const int bh = blockIdx.x;
-    const int hi = bh % H;
-    const int row = 4 * blk + ri;
-    const int64_t base0 = (int64_t)bh * D;   // [B, H, 64]
-    const int64_t sbase = (int64_t)bh * D * D + (int64_t)row * D + 4 * gq;
-
-    float S[4], N[4];
-    if (h_in) {
-        const float4 f = *reinterpret_cast<const float4*>(h_in + sbase);
-        S[0] = f.x; S[1] = f.y; S[2] = f.z; S[3] = f.w;
-    } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) S[c] = 0.0f;
-    }
+    const int64_t hb = (int64_t)bh * D * D;
+    const int row = R4 ? step4_row(blk, l) : step16_row(blk, l);
     const float A = a[base0 + l], W = w[base0 + l], K = k[base0 + l], Bv = b[base0 + l];
     const float R = r[base0 + l], V = v[base0 + row];
-    float p = 0.0f;
-    fwd_dot4(S, A, p);
-    const float sa = rowsum16(p);
-    float y = 0.0f;
-    p = 0.0f;
-    fwd_update4(S, N, K, Bv, W, R, A, V, sa, y, p);
-    y = rowsum16(y);
-    *reinterpret_cast<float4*>(h_out + sbase) = make_float4(N[0], N[1], N[2], N[3]);
-    if (gq == 0) {
+    const float* hin = h_in ? h_in + hb : nullptr;
+    const float y = R4 ? head_step4(hin, h_out + hb, blk, l, A, W, K, Bv, R, V)
+                       : head_step16(hin, h_out + hb, blk, l, A, W, K, Bv, R, V);
+    if ((R4 ? (l >> 2) : (l >> 4)) == 0) {
         ys[row] = y;
         if (wkv_out) wkv_out[base0 + row] = y;
     }
     __syncthreads();
     if (blk == 0) {
         const int64_t e = base0 + l, he = (int64_t)hi * D + l;
-        const float x = ys[l];
-        const float mean = wave_total(0.0f + x) / (float)D;
-        const float dd = x - mean;
-        const float inv = 1.0f / sqrtf(wave_total(fmaf(dd, dd, 0.0f)) / (float)D + eps);
-        const float dp = wave_total(fmaf(r[e] * k[e], rk[he], 0.0f));
-        const float nrm = (x - mean) * inv;
-        const float yo = fmaf(dp, v[e], fmaf(nrm, lnw[he], lnb[he]));
-        out[e] = yo * g[e];
+        out[e] = head_tail(ys[l], r[e], k[e], v[e], rk[he], lnw[he], lnb[he], g[e], eps);
     }
 }
 
@@ -1054,11 +830,13 @@ rwkv_status rwkv_wkv7_step_tail(const float* r, const float* w, const float* k, 
     RWKV_REQUIRE(B >= 1 && H >= 1 && B * H <= INT32_MAX, RWKV_E_SHAPE, "wkv7_step_tail: bad B (%lld) / H (%lld)",
                  (long long)B, (long long)H);
     if (use_rows4(B * H))
-        rwkv::launch(wkv7_step_tail4_kernel, dim3((unsigned)(B * H)), dim3(1024), reinterpret_cast<hipStream_t>(stream),
-                     r, w, k, v, a, b, h_in, h_out, rk, lnw, lnb, g, wkv_out, out, (int)H, eps);
+        rwkv::launch(wkv7_step_tail_kernel<true>, dim3((unsigned)(B * H)), dim3(1024),
+                     reinterpret_cast<hipStream_t>(stream), r, w, k, v, a, b, h_in, h_out, rk, lnw, lnb, g, wkv_out,
+                     out, (int)H, eps);
     else
-        rwkv::launch(wkv7_step_tail_kernel, dim3((unsigned)(B * H)), dim3(256), reinterpret_cast<hipStream_t>(stream),
-                     r, w, k, v, a, b, h_in, h_out, rk, lnw, lnb, g, wkv_out, out, (int)H, eps);
+        rwkv::launch(wkv7_step_tail_kernel<false>, dim3((unsigned)(B * H)), dim3(256),
+                     reinterpret_cast<hipStream_t>(stream), r, w, k, v, a, b, h_in, h_out, rk, lnw, lnb, g, wkv_out,
+                     out, (int)H, eps);
     rwkv_status s = launch_status("wkv7_step_tail launch");
     if (s == RWKV_OK) rwkv::counters().step_tail++;
     return s;
