@@ -171,6 +171,7 @@ __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
 
     float p = 0.0f;
     fwd_dot16(S[0], In::cvt(ring[0][0]), p);
+    float y = 0.0f;   // partial y of the previous step, reduced and stored one step late
 
     // one step at chunk position s (compile-time) and time t
     auto step = [&](auto sc, int t, int c) __attribute__((always_inline)) {
@@ -179,16 +180,18 @@ __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
         // them), so every wait for a prefetched value is a small exact count.
         __builtin_amdgcn_sched_barrier(0);
         fetch(ring[(s + 8) & (CH - 1)], t + 8);
-        const float sa = rowsum4(p);
-        float y = 0.0f;
+        float sa = p;
+        rowsum4_pair(sa, y);   // sa of step t, y of step t - 1
+        // y of step t - 1 (at t = 0 a placeholder at row 0, overwritten next
+        // step); the four lanes of a row store the same bits
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ro_, orow,
+                                              (uint32_t)max(t - 1, 0) * strideT * 4u, 0);
+        y = 0.0f;
         p = 0.0f;
         const E* sl = ring[s];
         fwd_update16(S[s & 1], S[(s + 1) & 1], In::cvt(sl[2]), In::cvt(sl[3]), In::cvt(sl[1]), In::cvt(sl[4]),
                      In::cvt(ring[(s + 1) & (CH - 1)][0]), In::cvt(sl[5]), sa, y, p);
-        y = rowsum4(y);
         const uint32_t so = (uint32_t)t * strideT * 4u;
-        // the four lanes of a row store the same bits
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ro_, orow, so, 0);
         if constexpr (EMIT_SA) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sa), rs_, orow, so, 0);
         if constexpr (EMIT_CK && s == CH - 1) {
             float4* dst = reinterpret_cast<float4*>(ckpt + ((int64_t)bh * NC + c) * D * D + (int64_t)row * D + 16 * g);
@@ -216,6 +219,8 @@ __global__ __launch_bounds__(64) void wkv7_fwd_kernel(
     for (int c = 1; c < NC; ++c) body_full(c);
     const int tail = T - NC * CH;
     if (tail) body(NC, tail);
+    y = rowsum4(y);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), ro_, orow, (uint32_t)(T - 1) * strideT * 4u, 0);
 
     float4* dst = reinterpret_cast<float4*>(h_out + sbase);
     if (tail & 1) {

@@ -122,11 +122,10 @@ __device__ __forceinline__ float rowsum16(float x) {
     return rowsum4(u);
 }
 
-// rowsum16 of two independent values with their instructions interleaved
-// (the same operations per value, so the same bits): in the four-row layout
-// the next step's sa and the last step's y are reduced together, which hides
-// the latency of each chain's dependent steps (in the sixteen-row layout,
-// which issues back to back anyway, the pairing measured 5 % slower).
+// rowsum4 / rowsum16 of two independent values with their instructions
+// interleaved (the same operations per value, so the same bits): the next
+// step's sa and the last step's y are reduced together, which hides the
+// latency of each chain's dependent steps.
 #define RWKV_SWAP_PAIR(OP)                        \
     "v_mov_b32 %[b0], %[x0]\n\t"                 \
     "v_mov_b32 %[b1], %[x1]\n\t"                 \
@@ -135,6 +134,11 @@ __device__ __forceinline__ float rowsum16(float x) {
     OP " %[x1], %[b1]\n\t"                       \
     "v_add_f32 %[x0], %[x0], %[b0]\n\t"          \
     "v_add_f32 %[x1], %[x1], %[b1]\n\t"
+__device__ __forceinline__ void rowsum4_pair(float& x0, float& x1) {
+    float b0, b1;
+    asm("s_nop 1\n\t" RWKV_SWAP_PAIR("v_permlane16_swap_b32") RWKV_SWAP_PAIR("v_permlane32_swap_b32")
+        : [x0] "+v"(x0), [x1] "+v"(x1), [b0] "=&v"(b0), [b1] "=&v"(b1));
+}
 __device__ __forceinline__ void rowsum16_pair(float& x0, float& x1) {
     float b0, b1;
     asm("s_nop 1\n\t"
