@@ -325,6 +325,45 @@ def bench_projection_crossover(model, dev, key="blocks.0.ffn.key.weight", reps=2
     return {"shape": f"{OUT}x{IN} sb6 4-bit", "rows": res, "first_rows_where_dequant_matmul_wins": cross}
 
 
+def bench_wkv_decode_step(dev, reps=30):
+    """The fused WKV-7 decode step + tail (rwkv_wkv7_step_tail) alone, against
+    its state-traffic roofline: per (row, head) the 64x64 fp32 state is read
+    and written (32 KB) plus the step vectors, the tail's inputs and the
+    output (13 · 64 · 4 B).  Rotating over 4 state buffers so the state comes
+    from HBM when it exceeds the MALL."""
+    import torch
+    from swiftrwkv_amd import _lib
+
+    res = {}
+    for name, B, H in (("0.1B_batch1", 1, 12), ("0.1B_batch32", 32, 12), ("7B_batch16", 16, 64)):
+        nb = 4
+        states = [torch.zeros((B, H, 64, 64), device=dev) for _ in range(nb)]
+        vec = [torch.randn((B, H, 64), device=dev) * 0.1 for _ in range(7)]
+        r, w, k, v, a, b, g = vec
+        w = torch.sigmoid(w) * 0.5 + 0.5
+        rk, lnw, lnb = (torch.randn(H * 64, device=dev) for _ in range(3))
+        out = torch.empty((B, H * 64), device=dev)
+        stream = torch.cuda.current_stream(dev)
+
+        def launch(i):
+            st = states[i % nb]
+            _lib.call("rwkv_wkv7_step_tail", *[z.data_ptr() for z in (r, w, k, v, a, b)], st.data_ptr(),
+                      st.data_ptr(), rk.data_ptr(), lnw.data_ptr(), lnb.data_ptr(), g.data_ptr(), None,
+                      out.data_ptr(), B, H, float(64e-5), stream.cuda_stream)
+
+        for i in range(nb):
+            launch(i)
+        torch.cuda.synchronize()
+        us = sum(kernel_ms(lambda: launch(i), stream) for i in range(reps)) / reps * 1e3
+        nbytes = B * H * (2 * 64 * 64 * 4 + 13 * 64 * 4)
+        roof_us = nbytes / (HBM_PEAK_GBPS * 1e3)
+        res[name] = {"B": B, "H": H, "us": us, "bytes": nbytes, "GBps": nbytes / (us * 1e3),
+                     "state_traffic_roofline_us": roof_us, "roofline_frac": roof_us / us}
+        del states
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_wkv_prefill_7b(dev, reps=3):
     """WKV-7 forward of one layer of the 7B-class prefill: B1 T8192 H64 fp32."""
     import torch
@@ -389,6 +428,8 @@ def bench_decode_more(model_01, dev):
     del model
     torch.cuda.empty_cache()
     res["wkv7_prefill_7B_B1_T8192_H64_fp32"] = bench_wkv_prefill_7b(dev)
+    res["wkv7_decode_step_tail"] = bench_wkv_decode_step(dev)
+    log(f"decode step+tail: {res['wkv7_decode_step_tail']}")
     log("7B prefill WKV done")
     return res
 
