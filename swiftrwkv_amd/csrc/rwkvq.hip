@@ -347,6 +347,7 @@ struct GemvGeom {
     int R;     // row groups per wave (64 / G)
     int NP;    // passes: a lane covers units (p·KU + ku)·G + g, p < NP, ku < KU
     int WPB;   // waves per workgroup
+    int one_k; // fused groups: every row of a workgroup reads the same input row, staged alone
 };
 
 // Padded LDS row: column c at c + 4·(c / 32), so the G lanes of a row group
@@ -386,7 +387,8 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
         }
     };
     const int XS = xl_stride(IN);
-    const float* xsum = lds + NT * NK * XS;
+    const int NKs = geo.one_k ? 1 : NK;   // staged input rows per input
+    const float* xsum = lds + NT * NKs * XS;
     auto compute_pass = [&](int p, const Raw (&W)[RL][KU], int n0, float (&acc)[NT][RL]) {
 #pragma unroll
         for (int ku = 0; ku < KU; ++ku) {
@@ -397,7 +399,7 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
 #pragma unroll
             for (int nn = 0; nn < NT; ++nn) {
                 if constexpr (XL) {
-                    const int j = nn * NK + xi;
+                    const int j = nn * NKs + (geo.one_k ? 0 : xi);
                     const float4* px = reinterpret_cast<const float4*>(lds + j * XS + u * 36);
 #pragma unroll
                     for (int m = 0; m < 8; ++m) {
@@ -455,12 +457,14 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
     if constexpr (XL) {
         Raw W[RL][KU];
         load_pass(0, W);   // in flight while the inputs are staged
-        const int rows = NT * NK;
+        const int rows = NT * NKs;
+        // matrix of the workgroup's rows when they all read one input row
+        const int kwg = geo.one_k ? (int)(blockIdx.x * geo.WPB * geo.R * RL) / out_per : 0;
         auto stage = [&](int n0) {   // one tile: N <= NT
             const int step = (int)blockDim.x * 4;
 #pragma unroll 1
             for (int j = 0; j < rows; ++j) {   // uniform
-                const int nn = NK == 1 ? j : j / NK, k = j - nn * NK;
+                const int nn = NKs == 1 ? j : j / NKs, k = geo.one_k ? kwg : j - nn * NK;
                 const float* src = x + ((int64_t)min(n0 + nn, N - 1) * NK + k) * IN;
 #pragma unroll 1
                 for (int c = (int)threadIdx.x * 4; c < IN; c += step)
@@ -470,7 +474,7 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
             __syncthreads();
             if constexpr (F::SUMS) {
                 // sums[j][u][h] = x[j, 32u + 16h + 0..15], added in column order
-                float* sums = lds + NT * NK * XS;
+                float* sums = lds + NT * NKs * XS;
 #pragma unroll 1
                 for (int j = 0; j < rows; ++j)
 #pragma unroll 1
@@ -733,12 +737,16 @@ GemvPlan plan_gemv(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t N
     while (pl.geo.WPB > 4 && blocks() < 256) pl.geo.WPB >>= 1;
     pl.blocks = (unsigned)blocks();
     const int64_t IN = NU * 32;
-    const int64_t lds = (int64_t)pl.NT * NK * (xl_stride((int)IN) + (sums ? NU * 2 : 0)) * 4;
+    // a fused group's workgroups stage only their own matrix's input row when
+    // their rows never straddle two matrices (out_per = rl_div)
+    pl.geo.one_k = NK > 1 && rl_div % ((int64_t)pl.geo.WPB * pl.geo.R * pl.RL) == 0;
+    const int64_t lds = (int64_t)pl.NT * (pl.geo.one_k ? 1 : NK) * (xl_stride((int)IN) + (sums ? NU * 2 : 0)) * 4;
     pl.xl = N <= pl.NT && lds <= (int64_t)kXlBudget;
     if (!pl.xl) {
         // inputs read from global memory: one row per lane keeps registers low
         pl.RL = 1;
         pl.blocks = (unsigned)blocks();
+        pl.geo.one_k = 0;
     }
     pl.lds = pl.xl ? (size_t)lds : 0;
     return pl;
