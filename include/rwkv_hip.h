@@ -193,6 +193,70 @@ rwkv_status rwkv_sym_gemv(const float* x, int64_t N,
                           float* y, int64_t OUT, int64_t IN, int bits, int64_t out_per,
                           void* stream);
 
+/* GEMV with an epilogue: epilogue 0 stores y = x·Wᵀ (rwkv_sb6_gemv /
+ * rwkv_sym_gemv with out_per = OUT), 1 adds it to y (the residual updates
+ * x = x + pj(·), X070Generation.swift:493-497), 2 stores relu(x·Wᵀ)² (cmixStep's
+ * relu(pj(xk)) squared, :308-309).  Same per-row arithmetic as the plain
+ * entry points; the epilogue is the separate operations' exact arithmetic. */
+rwkv_status rwkv_sb6_gemv_ep(const float* x, int64_t N,
+                             const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
+                             float* y, int64_t OUT, int64_t IN, int xbits, int epilogue,
+                             void* stream);
+rwkv_status rwkv_sym_gemv_ep(const float* x, int64_t N,
+                             const uint8_t* qblk, const uint8_t* qs, const uint16_t* d,
+                             float* y, int64_t OUT, int64_t IN, int bits, int epilogue,
+                             void* stream);
+
+/* ───────────────────────── x070 decode step around the hot path ───────────────────────── */
+/* fp32 activations; dense vector parameters fp32 (an fp16 file's values
+ * widen exactly); low-rank matrices f16 (the reference's `lin` narrowing,
+ * X070Generation.swift:248-253: input rounded to fp16, fp32 accumulation,
+ * product rounded to fp16) or f32 (plain fp32). */
+
+/* y[n] = LayerNorm(src_n)·w + b over D (layerNorm_, X070Generation.swift:505-515:
+ * mean, then mean squared deviation, eps).  src_n = x[n] ([N, D], f32/f16) or,
+ * with ids (int32, device), row ids[n] of the table x [rows, D] (embedForBlock
+ * + ln0, :489-490); an id outside [0, rows) gives a NaN row.  D ≤ 8192. */
+rwkv_status rwkv_layer_norm(const void* x, rwkv_dtype x_dt, const int32_t* ids, int64_t rows,
+                            const float* w, const float* b, float* y, int64_t N, int64_t D,
+                            float eps, void* stream);
+
+/* Layer norm + token shift + lerps of tmixStep (:214-239; ln1 of stepEager
+ * :492) or cmixStep (:303-308; ln2 :495-496): xl = LN(x[n]); xx = prev[n] − xl;
+ * prev[n] ← xl; m_c = xl + xx·coef[c].  nc = 6: coef [6, D] in the order
+ * r, k, v, w, a, g; out0 [N, 3, D] ← (m_r, m_k, m_v) (the fused r/k/v GEMV
+ * input), out1 [N, 3, D] ← (m_w, m_a, m_g).  nc = 1: out0 [N, D]. */
+rwkv_status rwkv_x070_shift_mix(const float* x, const float* lnw, const float* lnb, float* prev,
+                                const float* coef, int nc, float* out0, float* out1,
+                                int64_t N, int64_t D, float eps, void* stream);
+
+/* First layers of the low-rank branches (tmixStep :256-276, the inner lin of
+ * each): wcat [rw + ra + rv + rg, D] = w_lora_A ‖ a_lora_A ‖ v_lora_A ‖
+ * g_lora_A rows; la [N, rw + ra + rv + rg] = tanh(lin(xw, ·)) ‖ lin(xa, ·) ‖
+ * lin(xv, ·) ‖ sigmoid(lin(xg, ·)), xw/xa/xg = rows of xwag [N, 3, D], xv =
+ * row 2 of xrkv [N, 3, D].  with_v = 0 (layer 0) skips the v branch. */
+rwkv_status rwkv_x070_lora_in(const float* xrkv, const float* xwag, const void* wcat,
+                              rwkv_dtype w_dt, int64_t rw, int64_t ra, int64_t rv, int64_t rg,
+                              int with_v, float* la, int64_t N, int64_t D, void* stream);
+
+/* The tmix core (tmixStep :256-294): second layers of the low-rank branches
+ * for each head's rows (w2 [D, rw], a2 [D, ra], v2 [D, rv], g2 [D, rg] in
+ * w_dt; biases fp32): w = exp(−0.606531·σ(lin + w2_bias)), a = σ(lin + a2_bias),
+ * vv = σ(lin + v2_bias), gate = lin; kk = l2norm(k0·k_k) per head;
+ * k = k0·(1 + (a − 1)·k_a); v = layer0 ? v0 (v_first ← v0) : v0 + (v_first − v0)·vv;
+ * the WKV step with (r, w, k, v, −kk, kk·a) on state [N, H, 64, 64] in place
+ * (rwkv_wkv7_step's arithmetic); out [N, H·64] = the tail
+ * ((GroupNorm(y)·lnx_w + lnx_b + Σ(r·k·r_k)·v)·gate, rwkv_wkv_tail's).
+ * y_rkv [N, 3·H·64] = r | k0 | v0 (the fused r/k/v GEMV output); la from
+ * rwkv_x070_lora_in. */
+rwkv_status rwkv_x070_tmix_core(const float* y_rkv, const float* la, const void* w2, const void* a2,
+                                const void* v2, const void* g2, rwkv_dtype w_dt, int64_t rw,
+                                int64_t ra, int64_t rv, int64_t rg, const float* w2_bias,
+                                const float* a2_bias, const float* v2_bias, const float* k_k,
+                                const float* k_a, const float* r_k, const float* lnx_w,
+                                const float* lnx_b, float* v_first, int layer0, float* state,
+                                float* out, int64_t N, int64_t H, float eps, void* stream);
+
 /* ───────────────────────────── host-side format work (CPU) ───────────────────────────── */
 
 /* rwkvqUnpack6x8 (Sources/RWKVQuant/RwkvqFile.swift:171-181): n_groups × 6 bytes
@@ -262,6 +326,7 @@ typedef struct {
     int64_t step_tail;      /* rwkv_wkv7_step_tail launches (no reference counter) */
     int64_t sb6_fused;      /* rwkv_sb6_gemv_fused launches (no reference counter) */
     int64_t sym_rows;       /* rwkv_sym_rows launches (no reference counter) */
+    int64_t x070;           /* layer_norm / x070_* launches (no reference counter) */
 } rwkv_counters;
 
 void rwkv_get_counters(rwkv_counters* out);

@@ -38,7 +38,7 @@ class RwkvHipError(RuntimeError):
 class Counters(ctypes.Structure):
     _fields_ = [(n, L) for n in ("seq_fwd", "chunk_fwd", "train_fwd", "train_bwd", "step", "tail",
                                  "sb6_dequant", "sym_dequant", "sb6_gemv", "sym_gemv", "sym_fused",
-                                 "step_tail", "sb6_fused", "sym_rows")]
+                                 "step_tail", "sb6_fused", "sym_rows", "x070")]
 
 
 # name → (restype, argtypes)
@@ -64,6 +64,12 @@ _SIGS = {
     "rwkv_sb6_gemv_fused": (I, [P, L, P, P, P, P, L, L, I, L, P]),
     "rwkv_sym_gemv_applies": (I, [L, L, I, L]),
     "rwkv_sym_gemv": (I, [P, L, P, P, P, P, L, L, I, L, P]),
+    "rwkv_sb6_gemv_ep": (I, [P, L, P, P, P, P, L, L, I, I, P]),
+    "rwkv_sym_gemv_ep": (I, [P, L, P, P, P, P, L, L, I, I, P]),
+    "rwkv_layer_norm": (I, [P, I, P, L, P, P, P, L, L, F, P]),
+    "rwkv_x070_shift_mix": (I, [P, P, P, P, P, I, P, P, L, L, F, P]),
+    "rwkv_x070_lora_in": (I, [P, P, P, I, L, L, L, L, I, P, L, L, P]),
+    "rwkv_x070_tmix_core": (I, [P, P, P, P, P, P, I, L, L, L, L] + [P] * 8 + [P, I, P, P, L, L, F, P]),
     "rwkv_unpack6x8": (I, [P, L, P]),
     "rwkv_sb6_to_k3": (I, [P] * 6 + [L, L, P, P, P]),
     "rwkv_sym_interleave": (I, [P, P, P, L, L, P]),

@@ -348,7 +348,19 @@ struct GemvGeom {
     int NP;    // passes: a lane covers units (p·KU + ku)·G + g, p < NP, ku < KU
     int WPB;   // waves per workgroup
     int one_k; // fused groups: every row of a workgroup reads the same input row, staged alone
+    int ep;    // epilogue: 0 store, 1 add to y (residual stream), 2 relu² of the result
 };
+
+// y[i] ← t, y[i] + t or relu(t)², the separate operations' exact arithmetic.
+__device__ __forceinline__ void store_out(float* __restrict__ y, int64_t i, float t, int ep) {
+    if (ep == 1) {
+        t = y[i] + t;
+    } else if (ep == 2) {
+        t = fmaxf(t, 0.0f);
+        t = t * t;
+    }
+    y[i] = t;
+}
 
 // Padded LDS row: column c at c + 4·(c / 32), so the G lanes of a row group
 // reading G different units with ds_read_b128 hit distinct banks.
@@ -444,7 +456,7 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
             for (int rr = 0; rr < RL; ++rr) {
                 const float t = group_sum(acc[nn][rr], geo.G);
                 const int row = row0 + rr;
-                if (g == 0 && row < OUT && n0 + nn < N) y[(int64_t)(n0 + nn) * OUT + row] = t;
+                if (g == 0 && row < OUT && n0 + nn < N) store_out(y, (int64_t)(n0 + nn) * OUT + row, t, geo.ep);
             }
     };
 
@@ -668,7 +680,7 @@ __global__ __launch_bounds__(512) void gemv_batch_kernel(const float* __restrict
         for (int rr = 0; rr < RL; ++rr) {
             const float t = group_sum(acc[nn][rr], geo.G);
             const int row = row0 + rr;
-            if (g == 0 && row < OUT && nn < N) y[(int64_t)nn * OUT + row] = t;
+            if (g == 0 && row < OUT && nn < N) store_out(y, (int64_t)nn * OUT + row, t, geo.ep);
         }
 }
 
@@ -872,20 +884,25 @@ bool launch_batch(const BatchPlan& bp, hipStream_t st, const float* x, int N, ty
 // workgroup per (row block, tile of NT inputs).
 template <class F>
 bool run_gemv(int64_t OUT, int64_t IN, int64_t rl_div, int64_t N, int64_t NK, hipStream_t st, const float* x,
-              typename F::Ptr P, float* y, int64_t out_per) {
+              typename F::Ptr P, float* y, int64_t out_per, int ep) {
     const int64_t NU = IN / 32;
     if (N >= 2) {
         BatchPlan bp;
-        if (plan_batch(OUT, NU, rl_div, N, NK, F::SUMS, bp) && (N + bp.NT - 1) / bp.NT <= 65535)
+        if (plan_batch(OUT, NU, rl_div, N, NK, F::SUMS, bp) && (N + bp.NT - 1) / bp.NT <= 65535) {
+            bp.geo.ep = ep;
             return launch_batch<F>(bp, st, x, (int)N, P, y, (int)OUT, (int)IN, (int)out_per);
+        }
     }
-    const GemvPlan all = plan_gemv(OUT, NU, rl_div, N, NK, F::SUMS, F::WIDE);
+    GemvPlan all = plan_gemv(OUT, NU, rl_div, N, NK, F::SUMS, F::WIDE);
+    all.geo.ep = ep;
     if (all.xl || N <= 4) return launch_gemv<F>(all, st, x, (int)N, P, y, (int)OUT, (int)IN, (int)out_per);
-    const GemvPlan tile = plan_gemv(OUT, NU, rl_div, 4, NK, F::SUMS, F::WIDE);
+    GemvPlan tile = plan_gemv(OUT, NU, rl_div, 4, NK, F::SUMS, F::WIDE);
+    tile.geo.ep = ep;
     if (!tile.xl) return launch_gemv<F>(all, st, x, (int)N, P, y, (int)OUT, (int)IN, (int)out_per);
     for (int64_t n0 = 0; n0 < N; n0 += 4) {
         const int64_t nn = N - n0 < 4 ? N - n0 : 4;
-        const GemvPlan pl = nn == 4 ? tile : plan_gemv(OUT, NU, rl_div, nn, NK, F::SUMS, F::WIDE);
+        GemvPlan pl = nn == 4 ? tile : plan_gemv(OUT, NU, rl_div, nn, NK, F::SUMS, F::WIDE);
+        pl.geo.ep = ep;
         if (!launch_gemv<F>(pl, st, x + n0 * NK * IN, (int)nn, P, y + n0 * OUT, (int)OUT, (int)IN, (int)out_per))
             return false;
     }
@@ -1003,8 +1020,9 @@ int rwkv_sb6_gemv_applies(int64_t OUT, int64_t IN, int xbits, int super_block, i
 namespace {
 rwkv_status sb6_gemv_impl(const char* what, const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qsqm,
                           const uint16_t* ddm, float* y, int64_t OUT, int64_t IN, int xbits, int64_t out_per,
-                          void* stream) {
+                          void* stream, int ep = 0) {
     RWKV_REQUIRE(x && qblk && qsqm && ddm && y, RWKV_E_NULL, "%s: null buffer", what);
+    RWKV_REQUIRE(ep >= 0 && ep <= 2, RWKV_E_SHAPE, "%s: epilogue %d outside 0...2", what, ep);
     RWKV_REQUIRE(xbits >= 0 && xbits <= 2, RWKV_E_SHAPE, "%s: xbits %d outside 0...2", what, xbits);
     RWKV_REQUIRE(N >= 1 && N <= INT32_MAX, RWKV_E_SHAPE, "%s: rows %lld", what, (long long)N);
     RWKV_REQUIRE(OUT >= 1 && OUT <= INT32_MAX && IN >= 256 && IN % 256 == 0 && IN <= (1 << 24), RWKV_E_SHAPE,
@@ -1018,9 +1036,9 @@ rwkv_status sb6_gemv_impl(const char* what, const float* x, int64_t N, const uin
     const int64_t NK = OUT / out_per;
     bool ok;
     switch (xbits) {
-        case 0: ok = run_gemv<Sb6Fmt<0>>(OUT, IN, out_per, N, NK, st, x, P, y, out_per); break;
-        case 1: ok = run_gemv<Sb6Fmt<1>>(OUT, IN, out_per, N, NK, st, x, {P.q, P.sm, P.dd}, y, out_per); break;
-        default: ok = run_gemv<Sb6Fmt<2>>(OUT, IN, out_per, N, NK, st, x, {P.q, P.sm, P.dd}, y, out_per); break;
+        case 0: ok = run_gemv<Sb6Fmt<0>>(OUT, IN, out_per, N, NK, st, x, P, y, out_per, ep); break;
+        case 1: ok = run_gemv<Sb6Fmt<1>>(OUT, IN, out_per, N, NK, st, x, {P.q, P.sm, P.dd}, y, out_per, ep); break;
+        default: ok = run_gemv<Sb6Fmt<2>>(OUT, IN, out_per, N, NK, st, x, {P.q, P.sm, P.dd}, y, out_per, ep); break;
     }
     RWKV_REQUIRE(ok, RWKV_E_UNSUPPORTED, "%s: no kernel variant for %lldx%lld", what, (long long)OUT, (long long)IN);
     return launch_status(what);
@@ -1049,9 +1067,13 @@ int rwkv_sym_gemv_applies(int64_t OUT, int64_t IN, int bits, int64_t rows) {
     return (bits == 6 || bits == 8) && IN > 0 && IN % 256 == 0 && OUT > 0 && OUT % 16 == 0 && rows >= 1 && rows <= 4;
 }
 
-rwkv_status rwkv_sym_gemv(const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qs, const uint16_t* d,
-                          float* y, int64_t OUT, int64_t IN, int bits, int64_t out_per, void* stream) {
+}  // extern "C"
+
+namespace {
+rwkv_status sym_gemv_impl(const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qs, const uint16_t* d,
+                          float* y, int64_t OUT, int64_t IN, int bits, int64_t out_per, void* stream, int ep) {
     RWKV_REQUIRE(x && qblk && qs && d && y, RWKV_E_NULL, "sym_gemv: null buffer");
+    RWKV_REQUIRE(ep >= 0 && ep <= 2, RWKV_E_SHAPE, "sym_gemv: epilogue %d outside 0...2", ep);
     RWKV_REQUIRE(bits == 6 || bits == 8, RWKV_E_SHAPE, "sym_gemv: bits %d outside {6, 8}", bits);
     RWKV_REQUIRE(N >= 1 && N <= INT32_MAX, RWKV_E_SHAPE, "sym_gemv: rows %lld", (long long)N);
     RWKV_REQUIRE(OUT >= 1 && OUT <= INT32_MAX && IN >= 256 && IN % 256 == 0 && IN <= (1 << 24), RWKV_E_SHAPE,
@@ -1062,14 +1084,35 @@ rwkv_status rwkv_sym_gemv(const float* x, int64_t N, const uint8_t* qblk, const 
                  "sym_gemv: packed matrix of %lldx%lld exceeds 4 GiB", (long long)OUT, (long long)IN);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int64_t NK = OUT / out_per;
-    const bool ok = bits == 8 ? run_gemv<SymFmt<8>>(OUT, IN, out_per, N, NK, st, x, {(const uint32_t*)qblk, (const uint16_t*)qs, d}, y, out_per)
-                              : run_gemv<SymFmt<6>>(OUT, IN, out_per, N, NK, st, x, {(const uint32_t*)qblk, (const uint16_t*)qs, d}, y, out_per);
+    const bool ok = bits == 8 ? run_gemv<SymFmt<8>>(OUT, IN, out_per, N, NK, st, x, {(const uint32_t*)qblk, (const uint16_t*)qs, d}, y, out_per, ep)
+                              : run_gemv<SymFmt<6>>(OUT, IN, out_per, N, NK, st, x, {(const uint32_t*)qblk, (const uint16_t*)qs, d}, y, out_per, ep);
     RWKV_REQUIRE(ok, RWKV_E_UNSUPPORTED, "sym_gemv: no kernel variant for %lldx%lld", (long long)OUT, (long long)IN);
     rwkv_status s = launch_status("sym_gemv launch");
     if (s == RWKV_OK) {
         if (out_per < OUT) rwkv::counters().sym_fused++;
         else rwkv::counters().sym_gemv++;
     }
+    return s;
+}
+}  // namespace
+
+extern "C" {
+
+rwkv_status rwkv_sym_gemv(const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qs, const uint16_t* d,
+                          float* y, int64_t OUT, int64_t IN, int bits, int64_t out_per, void* stream) {
+    return sym_gemv_impl(x, N, qblk, qs, d, y, OUT, IN, bits, out_per, stream, 0);
+}
+
+rwkv_status rwkv_sym_gemv_ep(const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qs, const uint16_t* d,
+                             float* y, int64_t OUT, int64_t IN, int bits, int epilogue, void* stream) {
+    return sym_gemv_impl(x, N, qblk, qs, d, y, OUT, IN, bits, OUT, stream, epilogue);
+}
+
+rwkv_status rwkv_sb6_gemv_ep(const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qsqm,
+                             const uint16_t* ddm, float* y, int64_t OUT, int64_t IN, int xbits, int epilogue,
+                             void* stream) {
+    const rwkv_status s = sb6_gemv_impl("sb6_gemv_ep", x, N, qblk, qsqm, ddm, y, OUT, IN, xbits, OUT, stream, epilogue);
+    if (s == RWKV_OK) rwkv::counters().sb6_gemv++;
     return s;
 }
 

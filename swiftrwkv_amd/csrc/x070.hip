@@ -1,0 +1,400 @@
+// The x070 decode step around the WKV-7 / GEMV hot path, fp32 activations:
+// layer norms (with the embedding row gather of the first), token shift and
+// its lerps, the low-rank w / a / v / g branches, and the per-head tmix core
+// (low-rank second layers, kk / k / v mixing, the WKV step and the tail).
+//
+// Reference: X070Generation.swift stepEager (:484-500), tmixStep (:201-296),
+// cmixStep (:299-310), layerNorm_ (:505-515), l2normLast (:502-504).
+// Low-rank products follow `lin` (:248-253): with fp16 matrices the input is
+// rounded to fp16 and the product (fp32 accumulation) rounded to fp16, then
+// widened back; with fp32 matrices the product is plain fp32.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "common.h"
+#include "launch.h"
+#include "wkv7_step.h"
+
+namespace {
+using namespace rwkv_wkv;
+
+constexpr int kLnThreads = 256;
+constexpr int kLnMaxPer = 32;   // elements per thread: D ≤ 8192
+
+__device__ __forceinline__ float f16_round(float x) { return __half2float(__float2half_rn(x)); }
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Sum over the workgroup: per-wave butterfly, then the wave totals in wave
+// order; every thread gets the same value.
+__device__ __forceinline__ float block_total(float v, float* red) {
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_total(v);
+    __syncthreads();   // `red` free from the previous use
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float t = red[0];
+    for (int i = 1; i < nw; ++i) t += red[i];
+    return t;
+}
+
+// Row statistics of layerNorm_ (X070Generation.swift:511-514): mean, then the
+// mean of squared deviations; element i of the row is v[j], i = t + 256·j.
+__device__ __forceinline__ void ln_row(float (&v)[kLnMaxPer], int D, const float* __restrict__ w,
+                                       const float* __restrict__ b, float eps, float* red) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kLnMaxPer; ++j) {
+        const int i = threadIdx.x + kLnThreads * j;
+        if (i < D) s += v[j];
+    }
+    const float mean = block_total(s, red) / (float)D;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kLnMaxPer; ++j) {
+        const int i = threadIdx.x + kLnThreads * j;
+        if (i < D) {
+            const float d = v[j] - mean;
+            q += d * d;
+        }
+    }
+    const float den = sqrtf(block_total(q, red) / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < kLnMaxPer; ++j) {
+        const int i = threadIdx.x + kLnThreads * j;
+        if (i < D) v[j] = (v[j] - mean) / den * w[i] + b[i];
+    }
+}
+
+// y[n] = LN(src(n)); src(n) = x[n] or, with `ids`, row ids[n] of the table x
+// (fp32 or fp16); an id outside [0, rows) gives a NaN row.
+template <typename T>
+__global__ __launch_bounds__(kLnThreads) void layer_norm_kernel(const T* __restrict__ x, const int32_t* ids,
+                                                                int64_t rows, const float* __restrict__ w,
+                                                                const float* __restrict__ b, float* __restrict__ y,
+                                                                int D, float eps) {
+    __shared__ float red[kLnThreads / 64];
+    const int n = blockIdx.x;
+    int64_t src = n;
+    bool bad = false;
+    if (ids) {
+        const int32_t id = ids[n];
+        bad = id < 0 || (int64_t)id >= rows;
+        src = bad ? 0 : id;
+    }
+    const T* row = x + src * D;
+    float v[kLnMaxPer];
+#pragma unroll
+    for (int j = 0; j < kLnMaxPer; ++j) {
+        const int i = threadIdx.x + kLnThreads * j;
+        v[j] = i < D ? (float)row[i] : 0.0f;
+    }
+    ln_row(v, D, w, b, eps, red);
+#pragma unroll
+    for (int j = 0; j < kLnMaxPer; ++j) {
+        const int i = threadIdx.x + kLnThreads * j;
+        if (i < D) y[(int64_t)n * D + i] = bad ? __builtin_nanf("") : v[j];
+    }
+}
+
+// Token shift with its lerps (tmixStep :214-239, cmixStep :303-308) on the
+// layer-normed row: xl = LN(x[n]); xx = prev[n] − xl; prev[n] ← xl;
+// coefficient c gives xl + xx·coef[c].  Coefficients 0..2 go to out0 [N, 3, D]
+// (or [N, D] when NC == 1), 3..5 to out1 [N, 3, D].
+__global__ __launch_bounds__(kLnThreads) void shift_mix_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                               const float* __restrict__ b, float* __restrict__ prev,
+                                                               const float* __restrict__ coef, int NC,
+                                                               float* __restrict__ out0, float* __restrict__ out1, int D,
+                                                               float eps) {
+    __shared__ float red[kLnThreads / 64];
+    const int n = blockIdx.x;
+    float v[kLnMaxPer];
+#pragma unroll
+    for (int j = 0; j < kLnMaxPer; ++j) {
+        const int i = threadIdx.x + kLnThreads * j;
+        v[j] = i < D ? x[(int64_t)n * D + i] : 0.0f;
+    }
+    ln_row(v, D, w, b, eps, red);
+    const int n0 = NC < 3 ? NC : 3;
+#pragma unroll
+    for (int j = 0; j < kLnMaxPer; ++j) {
+        const int i = threadIdx.x + kLnThreads * j;
+        if (i >= D) continue;
+        const int64_t e = (int64_t)n * D + i;
+        const float xl = v[j];
+        const float xx = prev[e] - xl;
+        prev[e] = xl;
+        for (int c = 0; c < NC; ++c) {
+            const float m = xl + xx * coef[(int64_t)c * D + i];
+            if (c < n0) out0[((int64_t)n * n0 + c) * D + i] = m;
+            else out1[((int64_t)n * 3 + (c - 3)) * D + i] = m;
+        }
+    }
+}
+
+// ── low-rank first layers (tmixStep :256-276, the inner `lin` of each branch) ──
+// Rows of Wcat [rw + ra + rv + rg, D]: w, a, v, g branches; inputs xw, xa, xg
+// = xwag rows 0..2, xv = xrkv row 2.  la[n, j] = act(lin(x_branch, Wcat[j])):
+// tanh for w, sigmoid for g, none for a and v.  One wave per (row, input).
+template <bool H16>
+__global__ __launch_bounds__(256) void lora_in_kernel(const float* __restrict__ xrkv, const float* __restrict__ xwag,
+                                                      const void* __restrict__ Wcat, float* __restrict__ la, int N,
+                                                      int D, int rw, int ra, int rv, int rg, int with_v) {
+    const int lane = threadIdx.x & 63;
+    const int RT = rw + ra + rv + rg;
+    const int64_t job = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (job >= (int64_t)RT * N) return;   // uniform per wave
+    const int j = (int)(job % RT), n = (int)(job / RT);
+    const int br = j < rw ? 0 : j < rw + ra ? 1 : j < rw + ra + rv ? 2 : 3;
+    if (br == 2 && !with_v) return;
+    const float* xin = br == 2 ? xrkv + ((int64_t)n * 3 + 2) * D
+                               : xwag + ((int64_t)n * 3 + (br == 0 ? 0 : br == 1 ? 1 : 2)) * D;
+    float acc = 0.0f;
+    if constexpr (H16) {
+        const __half* wr = reinterpret_cast<const __half*>(Wcat) + (int64_t)j * D;
+        for (int c = lane * 8; c < D; c += 512) {   // D % 8 == 0
+            const uint4 raw = *reinterpret_cast<const uint4*>(wr + c);
+            const float4 x0 = *reinterpret_cast<const float4*>(xin + c);
+            const float4 x1 = *reinterpret_cast<const float4*>(xin + c + 4);
+            const __half2* h = reinterpret_cast<const __half2*>(&raw);
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float2 f = __half22float2(h[e]);
+                acc = fmaf(f16_round(xs[2 * e]), f.x, acc);
+                acc = fmaf(f16_round(xs[2 * e + 1]), f.y, acc);
+            }
+        }
+    } else {
+        const float* wr = reinterpret_cast<const float*>(Wcat) + (int64_t)j * D;
+        for (int c = lane * 4; c < D; c += 256) {   // D % 4 == 0
+            const float4 wv = *reinterpret_cast<const float4*>(wr + c);
+            const float4 xv = *reinterpret_cast<const float4*>(xin + c);
+            acc = fmaf(xv.x, wv.x, acc);
+            acc = fmaf(xv.y, wv.y, acc);
+            acc = fmaf(xv.z, wv.z, acc);
+            acc = fmaf(xv.w, wv.w, acc);
+        }
+    }
+    float t = wave_total(acc);
+    if constexpr (H16) t = f16_round(t);
+    if (br == 0) t = tanhf(t);
+    else if (br == 3) t = sigmoidf_(t);
+    if (lane == 0) la[(int64_t)n * RT + j] = t;
+}
+
+// ── the tmix core of one (input row, head) (tmixStep :256-296) ──
+// Low-rank second layers for the head's 64 rows (outer `lin` + bias + the
+// branch functions), kk = l2norm(k0·k_k), k = k0·(1 + (a − 1)·k_a), the value
+// residual v + (v_first − v)·vv (layer 0: v_first ← v), the WKV step with
+// (r, w, k, v, −kk, kk·a) on the state in place, and the tail
+// ((GroupNorm(y)·lnw + lnb + Σ(r·k·r_k)·v)·gate) into out.  The step and tail
+// are wkv7_step_tail_kernel's device code in the same layout, so this kernel's
+// step is bitwise that kernel's on the same vectors.
+struct CoreArgs {
+    const float* y_rkv;   // [N, 3D]: r | k0 | v0
+    const float* la;      // [N, RT]
+    const void* W2[4];    // w2 [D, rw], a2 [D, ra], v2 [D, rv], g2 [D, rg]
+    int rank[4];
+    const float* bias[3];   // w2, a2, v2 biases [D]
+    const float *k_k, *k_a, *r_k, *lnw, *lnb;
+    float* v_first;   // [N, D]
+    float* state;     // [N, H, 64, 64]
+    float* out;       // [N, D]
+    int H, layer0;
+    float eps;
+};
+
+template <bool R4, bool H16>
+__global__ __launch_bounds__(R4 ? 1024 : 256) void tmix_core_kernel(CoreArgs A) {
+    extern __shared__ float sm[];   // la row (RT) | w, a, vv, g (4 × 64) | y (64)
+    const int RT = A.rank[0] + A.rank[1] + A.rank[2] + A.rank[3];
+    float* lav = sm;
+    float* br = sm + RT;
+    float* ys = br + 4 * D;
+    const int nh = blockIdx.x, n = nh / A.H, h = nh % A.H;
+    const int Dm = A.H * D;
+    for (int j = threadIdx.x; j < RT; j += blockDim.x) {
+        const float t = A.la[(int64_t)n * RT + j];
+        lav[j] = H16 ? f16_round(t) : t;
+    }
+    __syncthreads();
+    if (threadIdx.x < 4 * D) {
+        const int b = threadIdx.x >> 6, i = threadIdx.x & 63;
+        const int row = h * D + i;
+        if (!(b == 2 && A.layer0)) {
+            int off = 0;
+            for (int q = 0; q < b; ++q) off += A.rank[q];
+            const int rk = A.rank[b];
+            float acc = 0.0f;
+            if constexpr (H16) {
+                const __half* wr = reinterpret_cast<const __half*>(A.W2[b]) + (int64_t)row * rk;
+                for (int c = 0; c < rk; c += 8) {   // ranks % 8 == 0
+                    const uint4 raw = *reinterpret_cast<const uint4*>(wr + c);
+                    const __half2* hh = reinterpret_cast<const __half2*>(&raw);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float2 f = __half22float2(hh[e]);
+                        acc = fmaf(lav[off + c + 2 * e], f.x, acc);
+                        acc = fmaf(lav[off + c + 2 * e + 1], f.y, acc);
+                    }
+                }
+                acc = f16_round(acc);
+            } else {
+                const float* wr = reinterpret_cast<const float*>(A.W2[b]) + (int64_t)row * rk;
+                for (int c = 0; c < rk; c += 4) {
+                    const float4 f = *reinterpret_cast<const float4*>(wr + c);
+                    acc = fmaf(lav[off + c], f.x, acc);
+                    acc = fmaf(lav[off + c + 1], f.y, acc);
+                    acc = fmaf(lav[off + c + 2], f.z, acc);
+                    acc = fmaf(lav[off + c + 3], f.w, acc);
+                }
+            }
+            float t;
+            if (b == 0) t = expf(-0.606531f * sigmoidf_(acc + A.bias[0][row]));
+            else if (b == 1) t = sigmoidf_(acc + A.bias[1][row]);
+            else if (b == 2) t = sigmoidf_(acc + A.bias[2][row]);
+            else t = acc;
+            br[b * D + i] = t;
+        }
+    }
+    __syncthreads();
+    const int blk = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int vrow = R4 ? step4_row(blk, l) : step16_row(blk, l);
+    const int64_t ye = (int64_t)n * 3 * Dm + (int64_t)h * D;   // head offset in the r block
+    const int64_t he = (int64_t)h * D + l;
+    const float r = A.y_rkv[ye + l];
+    const float k0 = A.y_rkv[ye + Dm + l];
+    const float kkr = k0 * A.k_k[he];
+    const float kk = kkr / sqrtf(wave_total(kkr * kkr) + 1e-12f);
+    const float av = br[D + l];
+    const float k = k0 * (1.0f + (av - 1.0f) * A.k_a[he]);
+    auto value = [&](int e) {
+        const float v0 = A.y_rkv[ye + 2 * Dm + e];
+        if (A.layer0) return v0;
+        const float vf = A.v_first[(int64_t)n * Dm + (int64_t)h * D + e];
+        return v0 + (vf - v0) * br[2 * D + e];
+    };
+    const float V = value(vrow);
+    const float W = br[l];
+    float* st = A.state + (int64_t)nh * D * D;
+    const float y = R4 ? head_step4(st, st, blk, l, -kk, W, k, kk * av, r, V)
+                       : head_step16(st, st, blk, l, -kk, W, k, kk * av, r, V);
+    if ((R4 ? (l >> 2) : (l >> 4)) == 0) ys[vrow] = y;
+    __syncthreads();
+    if (blk == 0) {
+        const float v = value(l);
+        if (A.layer0) A.v_first[(int64_t)n * Dm + he] = v;
+        A.out[(int64_t)n * Dm + he] =
+            head_tail(ys[l], r, k, v, A.r_k[he], A.lnw[he], A.lnb[he], br[3 * D + l], A.eps);
+    }
+}
+
+rwkv_status status_of(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        rwkv::set_error("%s: %s", what, hipGetErrorString(e));
+        return RWKV_E_HIP;
+    }
+    rwkv::clear_error();
+    rwkv::counters().x070++;
+    return RWKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+rwkv_status rwkv_layer_norm(const void* x, rwkv_dtype x_dt, const int32_t* ids, int64_t rows, const float* w,
+                            const float* b, float* y, int64_t N, int64_t D, float eps, void* stream) {
+    RWKV_REQUIRE(N == 0 || (x && w && b && y), RWKV_E_NULL, "layer_norm: null buffer");
+    RWKV_REQUIRE(x_dt == RWKV_F32 || x_dt == RWKV_F16, RWKV_E_DTYPE, "layer_norm: input dtype %d not f32/f16", (int)x_dt);
+    RWKV_REQUIRE(N >= 0 && N <= INT32_MAX && D >= 1 && D <= kLnThreads * kLnMaxPer, RWKV_E_SHAPE,
+                 "layer_norm: N=%lld D=%lld (D <= %d)", (long long)N, (long long)D, kLnThreads * kLnMaxPer);
+    RWKV_REQUIRE(!ids || rows >= 1, RWKV_E_SHAPE, "layer_norm: gather from a table of %lld rows", (long long)rows);
+    if (N == 0) return RWKV_OK;
+    if (x_dt == RWKV_F16)
+        rwkv::launch(layer_norm_kernel<__half>, dim3((unsigned)N), dim3(kLnThreads),
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const __half*>(x), ids, rows, w, b, y,
+                     (int)D, eps);
+    else
+        rwkv::launch(layer_norm_kernel<float>, dim3((unsigned)N), dim3(kLnThreads),
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const float*>(x), ids, rows, w, b, y,
+                     (int)D, eps);
+    return status_of("layer_norm launch");
+}
+
+rwkv_status rwkv_x070_shift_mix(const float* x, const float* lnw, const float* lnb, float* prev, const float* coef,
+                                int nc, float* out0, float* out1, int64_t N, int64_t D, float eps, void* stream) {
+    RWKV_REQUIRE(x && lnw && lnb && prev && coef && out0 && (nc <= 3 || out1), RWKV_E_NULL, "x070_shift_mix: null buffer");
+    RWKV_REQUIRE(nc == 1 || nc == 6, RWKV_E_SHAPE, "x070_shift_mix: %d coefficients (1 or 6)", nc);
+    RWKV_REQUIRE(N >= 1 && N <= INT32_MAX && D >= 1 && D <= kLnThreads * kLnMaxPer, RWKV_E_SHAPE,
+                 "x070_shift_mix: N=%lld D=%lld", (long long)N, (long long)D);
+    rwkv::launch(shift_mix_kernel, dim3((unsigned)N), dim3(kLnThreads), reinterpret_cast<hipStream_t>(stream), x, lnw,
+                 lnb, prev, coef, nc, out0, out1, (int)D, eps);
+    return status_of("x070_shift_mix launch");
+}
+
+rwkv_status rwkv_x070_lora_in(const float* xrkv, const float* xwag, const void* wcat, rwkv_dtype w_dt, int64_t rw,
+                              int64_t ra, int64_t rv, int64_t rg, int with_v, float* la, int64_t N, int64_t D,
+                              void* stream) {
+    RWKV_REQUIRE(xrkv && xwag && wcat && la, RWKV_E_NULL, "x070_lora_in: null buffer");
+    RWKV_REQUIRE(w_dt == RWKV_F16 || w_dt == RWKV_F32, RWKV_E_DTYPE, "x070_lora_in: matrix dtype %d not f16/f32",
+                 (int)w_dt);
+    RWKV_REQUIRE(rw >= 8 && ra >= 8 && rv >= 8 && rg >= 8 && rw % 8 == 0 && ra % 8 == 0 && rv % 8 == 0 && rg % 8 == 0 &&
+                     rw + ra + rv + rg <= 8192,
+                 RWKV_E_SHAPE, "x070_lora_in: ranks %lld/%lld/%lld/%lld (multiples of 8)", (long long)rw, (long long)ra,
+                 (long long)rv, (long long)rg);
+    RWKV_REQUIRE(N >= 1 && D >= 8 && D % 8 == 0 && D <= (1 << 20) && (rw + ra + rv + rg) * N <= INT32_MAX,
+                 RWKV_E_SHAPE, "x070_lora_in: N=%lld D=%lld", (long long)N, (long long)D);
+    const int64_t jobs = (rw + ra + rv + rg) * N;
+    const dim3 grid((unsigned)((jobs + 3) / 4)), block(256);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (w_dt == RWKV_F16)
+        rwkv::launch(lora_in_kernel<true>, grid, block, st, xrkv, xwag, wcat, la, (int)N, (int)D, (int)rw, (int)ra,
+                     (int)rv, (int)rg, with_v);
+    else
+        rwkv::launch(lora_in_kernel<false>, grid, block, st, xrkv, xwag, wcat, la, (int)N, (int)D, (int)rw, (int)ra,
+                     (int)rv, (int)rg, with_v);
+    return status_of("x070_lora_in launch");
+}
+
+rwkv_status rwkv_x070_tmix_core(const float* y_rkv, const float* la, const void* w2, const void* a2, const void* v2,
+                                const void* g2, rwkv_dtype w_dt, int64_t rw, int64_t ra, int64_t rv, int64_t rg,
+                                const float* w2_bias, const float* a2_bias, const float* v2_bias, const float* k_k,
+                                const float* k_a, const float* r_k, const float* lnx_w, const float* lnx_b,
+                                float* v_first, int layer0, float* state, float* out, int64_t N, int64_t H, float eps,
+                                void* stream) {
+    RWKV_REQUIRE(y_rkv && la && w2 && a2 && g2 && w2_bias && a2_bias && k_k && k_a && r_k && lnx_w && lnx_b &&
+                     v_first && state && out && (layer0 || (v2 && v2_bias)),
+                 RWKV_E_NULL, "x070_tmix_core: null buffer");
+    RWKV_REQUIRE(w_dt == RWKV_F16 || w_dt == RWKV_F32, RWKV_E_DTYPE, "x070_tmix_core: matrix dtype %d not f16/f32",
+                 (int)w_dt);
+    RWKV_REQUIRE(rw >= 8 && ra >= 8 && rv >= 8 && rg >= 8 && rw % 8 == 0 && ra % 8 == 0 && rv % 8 == 0 && rg % 8 == 0 &&
+                     rw + ra + rv + rg <= 8192,
+                 RWKV_E_SHAPE, "x070_tmix_core: ranks %lld/%lld/%lld/%lld (multiples of 8)", (long long)rw,
+                 (long long)ra, (long long)rv, (long long)rg);
+    RWKV_REQUIRE(N >= 1 && H >= 1 && N * H <= INT32_MAX && H * D <= (1 << 20), RWKV_E_SHAPE,
+                 "x070_tmix_core: N=%lld H=%lld", (long long)N, (long long)H);
+    CoreArgs A{};
+    A.y_rkv = y_rkv;
+    A.la = la;
+    A.W2[0] = w2; A.W2[1] = a2; A.W2[2] = v2; A.W2[3] = g2;
+    A.rank[0] = (int)rw; A.rank[1] = (int)ra; A.rank[2] = (int)rv; A.rank[3] = (int)rg;
+    A.bias[0] = w2_bias; A.bias[1] = a2_bias; A.bias[2] = v2_bias;
+    A.k_k = k_k; A.k_a = k_a; A.r_k = r_k; A.lnw = lnx_w; A.lnb = lnx_b;
+    A.v_first = v_first; A.state = state; A.out = out;
+    A.H = (int)H; A.layer0 = layer0 ? 1 : 0; A.eps = eps;
+    const size_t lds = (size_t)(rw + ra + rv + rg + 5 * D) * 4;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)(N * H));
+    const bool r4 = use_rows4(N * H), h16 = w_dt == RWKV_F16;
+    if (r4 && h16) rwkv::launch_lds(tmix_core_kernel<true, true>, grid, dim3(1024), lds, st, A);
+    else if (r4) rwkv::launch_lds(tmix_core_kernel<true, false>, grid, dim3(1024), lds, st, A);
+    else if (h16) rwkv::launch_lds(tmix_core_kernel<false, true>, grid, dim3(256), lds, st, A);
+    else rwkv::launch_lds(tmix_core_kernel<false, false>, grid, dim3(256), lds, st, A);
+    return status_of("x070_tmix_core launch");
+}
+
+}  // extern "C"

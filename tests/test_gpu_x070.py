@@ -1,0 +1,281 @@
+"""GPU parity of the x070 decode step around the hot path (layer norms, token
+shift, low-rank branches, tmix core, GEMV epilogues, whole steps) against the
+fp64 oracle (oracle/x070.py), through the C ABI.
+
+Tolerances (max|got − ref| / max|ref| unless stated): 1e-5 for the fp32
+elementwise kernels (layer norm, lerps); one fp16 ulp (2^-10 relative per
+element) for the low-rank products, whose fp16 rounding of an fp32 sum may
+land on the other side of a rounding boundary than the fp64 sum; 1e-4 for the
+tmix core and whole decode steps (the WKV bound of 1e-5 per step with those
+fp16 roundings upstream).  GEMV epilogues are bitwise the plain GEMV followed by
+the separate operations.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import x070 as X
+from swiftrwkv_amd import _lib, synthetic as syn
+from swiftrwkv_amd.x070 import X070Decoder, LN_EPS
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TINY = syn.X070Shape("tiny", 2, 256, 1024, vocab=512)
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def rel(ref, got):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(ref - np.asarray(got, np.float64)).max() / (np.abs(ref).max() + 1e-30))
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    p = syn.x070_dense_params(TINY, seed=3)
+    proj = syn.x070_projections(TINY, nthreads=4)
+    return p, proj, X.dequant_projections(proj)
+
+
+@pytest.fixture(scope="module")
+def decoder(tiny):
+    p, proj, _ = tiny
+    return X070Decoder(TINY.n_layer, TINY.n_embd, TINY.ffn, TINY.vocab, p, proj, DEV)
+
+
+@pytest.mark.parametrize("D", [256, 768, 4096])
+def test_layer_norm(D):
+    case(f"layer_norm D={D}")
+    rng = np.random.default_rng(D)
+    x = (rng.standard_normal((5, D)) * 2 + 0.5).astype(np.float32)
+    w, b = rng.standard_normal(D).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    y = torch.empty((5, D), device=DEV)
+    xd, wd, bd = dev(x), dev(w), dev(b)   # alive across the launch
+    _lib.call("rwkv_layer_norm", xd.data_ptr(), _lib.F32, None, 0, wd.data_ptr(), bd.data_ptr(),
+              y.data_ptr(), 5, D, LN_EPS, None)
+    torch.cuda.synchronize()
+    assert rel(X.layer_norm(x, w, b), y.cpu().numpy()) < 1e-5
+
+
+def test_layer_norm_gather_f16_table_and_bad_ids():
+    case("layer_norm gather")
+    rng = np.random.default_rng(1)
+    V, D = 300, 768
+    tab = (rng.standard_normal((V, D)) * 0.5).astype(np.float16)
+    w, b = rng.standard_normal(D).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    ids = np.array([5, 299, -1, 0, 300], np.int32)
+    y = torch.empty((5, D), device=DEV)
+    td, idd, wd, bd = dev(tab), dev(ids), dev(w), dev(b)
+    _lib.call("rwkv_layer_norm", td.data_ptr(), _lib.F16, idd.data_ptr(), V, wd.data_ptr(),
+              bd.data_ptr(), y.data_ptr(), 5, D, LN_EPS, None)
+    got = y.cpu().numpy()
+    good = [0, 1, 3]
+    assert rel(X.layer_norm(tab.astype(np.float64)[ids[good]], w, b), got[good]) < 1e-5
+    assert np.isnan(got[[2, 4]]).all()
+    _lib.call("rwkv_layer_norm", None, _lib.F32, None, 0, None, None, None, 0, D, LN_EPS, None)   # N = 0: no-op
+
+
+@pytest.mark.parametrize("nc", [6, 1])
+def test_shift_mix(nc):
+    case(f"shift_mix nc={nc}")
+    rng = np.random.default_rng(nc)
+    N, D = 3, 768
+    x = rng.standard_normal((N, D)).astype(np.float32)
+    w, b = rng.standard_normal(D).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    prev = rng.standard_normal((N, D)).astype(np.float32)
+    coef = rng.uniform(0, 1, (nc, D)).astype(np.float32)
+    prev_d = dev(prev)
+    out0 = torch.empty((N, min(nc, 3), D), device=DEV)
+    out1 = torch.empty((N, 3, D), device=DEV) if nc == 6 else None
+    xd, wd, bd, cd = dev(x), dev(w), dev(b), dev(coef)
+    _lib.call("rwkv_x070_shift_mix", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), prev_d.data_ptr(),
+              cd.data_ptr(), nc, out0.data_ptr(), out1.data_ptr() if out1 is not None else None, N, D, LN_EPS,
+              None)
+    xl = X.layer_norm(x, w, b)
+    mix, new_prev = X.shift_mix(xl, prev, list(coef))
+    assert rel(new_prev, prev_d.cpu().numpy()) < 1e-5
+    got = out0.cpu().numpy() if nc == 1 else np.concatenate([out0.cpu().numpy(), out1.cpu().numpy()], 1)
+    for c in range(nc):
+        assert rel(mix[c], got[:, c]) < 1e-5, c
+
+
+def _fp16_ulp_close(ref, got):
+    ref, got = np.asarray(ref, np.float64), np.asarray(got, np.float64)
+    return np.abs(ref - got) <= 2.0 ** -10 * np.abs(ref) + 1e-6
+
+
+@pytest.mark.parametrize("l", [0, 1])
+@pytest.mark.parametrize("wdt", [np.float16, np.float32])
+def test_lora_in(tiny, l, wdt):
+    case(f"lora_in layer={l} dtype={wdt.__name__}")
+    p, _, _ = tiny
+    p = dict(p)
+    t = f"blocks.{l}.tmix."
+    for nm in "wavg":
+        p[t + nm + "_lora_A.weight"] = p[t + nm + "_lora_A.weight"].astype(wdt)
+    rng = np.random.default_rng(l)
+    N, D = 2, TINY.n_embd
+    xrkv = rng.standard_normal((N, 3, D)).astype(np.float32)
+    xwag = rng.standard_normal((N, 3, D)).astype(np.float32)
+    rw, ra, rv, rg = syn.lora_ranks(D)
+    wcat = np.concatenate([p[t + nm + "_lora_A.weight"] for nm in "wavg"])
+    la = torch.full((N, rw + ra + rv + rg), 7.0, device=DEV)
+    xr_d, xw_d, wc_d = dev(xrkv), dev(xwag), dev(wcat)
+    _lib.call("rwkv_x070_lora_in", xr_d.data_ptr(), xw_d.data_ptr(), wc_d.data_ptr(),
+              _lib.F16 if wdt == np.float16 else _lib.F32, rw, ra, rv, rg, int(l > 0), la.data_ptr(), N, D, None)
+    got = la.cpu().numpy()
+    ref = X.lora_in(p, l, xwag[:, 0], xwag[:, 1], xrkv[:, 2], xwag[:, 2])
+    offs = np.cumsum([0, rw, ra, rv, rg])
+    for i, r in enumerate(ref):
+        g = got[:, offs[i]:offs[i + 1]]
+        if r is None:
+            assert (g == 7.0).all()   # layer 0: the v branch is not computed
+        elif wdt == np.float16:
+            assert _fp16_ulp_close(r, g).all(), i
+        else:
+            assert rel(r, g) < 1e-5, i
+
+
+@pytest.mark.parametrize("l", [0, 1])
+@pytest.mark.parametrize("N", [1, 5])
+def test_tmix_core(tiny, l, N):
+    case(f"tmix_core layer={l} N={N}")
+    p, _, _ = tiny
+    D, H = TINY.n_embd, TINY.n_head
+    rw, ra, rv, rg = syn.lora_ranks(D)
+    rng = np.random.default_rng(10 * l + N)
+    r, k0, v0 = (rng.standard_normal((N, D)).astype(np.float32) for _ in range(3))
+    la = [X.f16r(rng.standard_normal((N, n))).astype(np.float32) for n in (rw, ra, rv, rg)]
+    la[0] = np.tanh(la[0]).astype(np.float32)
+    v_first = rng.standard_normal((N, D)).astype(np.float32)
+    wkv = (rng.standard_normal((N, H, 64, 64)) * 0.1).astype(np.float32)
+    t = f"blocks.{l}.tmix."
+    B = [dev(p[t + nm + "_lora_B.weight"]) for nm in "wavg"]
+    bias = [dev(p[t + nm + "_lora_B.bias"].astype(np.float32)) for nm in "wav"]
+    vec = {k: dev(p[t + k].astype(np.float32)) for k in ("k_k", "k_a", "r_k", "ln_x.weight", "ln_x.bias")}
+    y_rkv = dev(np.concatenate([r, k0, v0], 1))
+    la_d = dev(np.concatenate(la, 1))
+    vf_d, st_d = dev(v_first), dev(wkv)
+    out = torch.empty((N, D), device=DEV)
+    _lib.call("rwkv_x070_tmix_core", y_rkv.data_ptr(), la_d.data_ptr(), *[b.data_ptr() for b in B], _lib.F16,
+              rw, ra, rv, rg, *[b.data_ptr() for b in bias], vec["k_k"].data_ptr(), vec["k_a"].data_ptr(),
+              vec["r_k"].data_ptr(), vec["ln_x.weight"].data_ptr(), vec["ln_x.bias"].data_ptr(), vf_d.data_ptr(),
+              int(l == 0), st_d.data_ptr(), out.data_ptr(), N, H, 64e-5, None)
+    tail, wkv_ref, vf_ref = X.core(p, l, r.astype(np.float64), k0.astype(np.float64), v0.astype(np.float64),
+                                   [z.astype(np.float64) for z in la], v_first.astype(np.float64),
+                                   wkv.astype(np.float64), H)
+    assert rel(tail, out.cpu().numpy()) < 1e-4
+    assert rel(wkv_ref, st_d.cpu().numpy()) < 1e-4
+    assert rel(vf_ref, vf_d.cpu().numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("N", [1, 3])
+def test_gemv_epilogues_bitwise(tiny, N):
+    case(f"gemv epilogues N={N}")
+    _, proj, _ = tiny
+    qb, qs, dd, OUT, IN = proj["blocks.0.ffn.key.weight"]
+    q = [dev(qb), dev(qs), dev(dd.view(np.uint16))]
+    rng = np.random.default_rng(N)
+    x = dev(rng.standard_normal((N, IN)).astype(np.float32))
+    res = dev(rng.standard_normal((N, OUT)).astype(np.float32))
+    L = _lib.lib()
+    plain = torch.empty((N, OUT), device=DEV)
+    _lib.check(L.rwkv_sb6_gemv(x.data_ptr(), N, *[t.data_ptr() for t in q], plain.data_ptr(), OUT, IN, 0, None))
+    added = res.clone()
+    _lib.check(L.rwkv_sb6_gemv_ep(x.data_ptr(), N, *[t.data_ptr() for t in q], added.data_ptr(), OUT, IN, 0, 1, None))
+    sq = torch.empty((N, OUT), device=DEV)
+    _lib.check(L.rwkv_sb6_gemv_ep(x.data_ptr(), N, *[t.data_ptr() for t in q], sq.data_ptr(), OUT, IN, 0, 2, None))
+    torch.cuda.synchronize()
+    assert torch.equal(added, res + plain)
+    h = torch.relu(plain)
+    assert torch.equal(sq, h * h)
+    with pytest.raises(_lib.RwkvHipError):
+        _lib.check(L.rwkv_sb6_gemv_ep(x.data_ptr(), N, *[t.data_ptr() for t in q], sq.data_ptr(), OUT, IN, 0, 3,
+                                      None))
+
+
+@pytest.mark.parametrize("N", [1, 3])
+def test_decode_steps_match_oracle(tiny, decoder, N):
+    case(f"decode tiny N={N}")
+    p, _, W = tiny
+    st = decoder.new_state(N)
+    ost = X.State.zeros(TINY.n_layer, N, TINY.n_head)
+    rng = np.random.default_rng(N)
+    _lib.reset_counters()
+    for t in range(4):
+        ids = rng.integers(0, TINY.vocab, N).astype(np.int32)
+        got = decoder.step(ids, st).cpu().numpy()
+        ref = X.step(p, W, ids, ost, TINY.n_layer, TINY.n_head)
+        assert rel(ref, got) < 1e-4, t
+    assert rel(ost.wkv, st.wkv.cpu().numpy()) < 1e-4
+    assert rel(ost.tmix_prev, st.tmix_prev.cpu().numpy()) < 1e-4
+    assert rel(ost.cmix_prev, st.cmix_prev.cpu().numpy()) < 1e-4
+    c = _lib.counters()
+    Lr = TINY.n_layer
+    assert c["x070"] == 4 * (2 + 4 * Lr)          # ln0 + ln_out + 4 per layer
+    assert c["sb6_gemv"] == 4 * (3 * Lr + 1)      # o_proj, ffn key, ffn value, head
+    assert c["sb6_fused"] == 4 * Lr               # r/k/v
+
+
+def test_decode_graph_replay_bitwise(tiny, decoder):
+    case("decode graph replay")
+    N = 2
+    st = decoder.new_state(N)
+    ids = torch.tensor([3, 400], dtype=torch.int32, device=DEV)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        decoder.launch(ids, st)   # one token so the state is not zero
+        s0 = st.clone()
+        eager = decoder.launch(ids, st).clone()
+        eager_st = st.clone()
+        g = torch.cuda.CUDAGraph()
+        st.copy_(s0)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            out = decoder.launch(ids, st)
+        torch.cuda.synchronize()
+        for rep in range(3):
+            st.copy_(s0)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), rep
+            assert torch.equal(st.wkv, eager_st.wkv) and torch.equal(st.cmix_prev, eager_st.cmix_prev), rep
+
+
+@pytest.fixture(scope="module")
+def proj_0b1():
+    proj = syn.x070_projections(syn.X070_0B1, nthreads=8)
+    return proj, X.dequant_projections(proj)
+
+
+# fp32 low-rank matrices: no fp16 rounding points, so the step is fp32
+# arithmetic against fp64 throughout (2e-5).  fp16 matrices (the .rwkvq norm):
+# 12 layers of low-rank outputs rounded to fp16, where an fp32 sum and the
+# fp64 sum may round to neighbouring fp16 values (one ulp = 2^-10 relative);
+# measured 1.3e-4 on these logits, bound 5e-4.
+@pytest.mark.parametrize("lora", ["f32", "f16"])
+def test_decode_0b1_shape_matches_oracle(proj_0b1, lora):
+    case(f"decode 0.1B shape, low-rank {lora}, 2 tokens")
+    shape = syn.X070_0B1
+    p = syn.x070_dense_params(shape, seed=5, lora_dtype=np.float32 if lora == "f32" else np.float16)
+    proj, W = proj_0b1
+    d = X070Decoder(shape.n_layer, shape.n_embd, shape.ffn, shape.vocab, p, proj, DEV)
+    st = d.new_state(1)
+    ost = X.State.zeros(shape.n_layer, 1, shape.n_head)
+    tol = 2e-5 if lora == "f32" else 5e-4
+    for t, i in enumerate((11, 40000)):
+        got = d.step([i], st).cpu().numpy()
+        ref = X.step(p, W, [i], ost, shape.n_layer, shape.n_head)
+        err = rel(ref, got)
+        print(f"[x070] 0.1B low-rank {lora} token {t}: rel {err:.3e}", flush=True)
+        assert err < tol, t
