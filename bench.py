@@ -243,6 +243,68 @@ def run_decode(model, dev, B, steps, warmup, copies, verify=True):
     return step, wall, e0.elapsed_time(e1)
 
 
+def run_x070(model, dev, steps, warmup, copies=1, B=1):
+    """End-to-end x070 decode token (X070Decoder: embedding + ln0, per layer
+    ln1 / shift / lerps, fused r/k/v GEMV, low-rank branches, tmix core with
+    the WKV step and tail, o_proj + residual, ln2 / shift, ffn key relu², ffn
+    value + residual; ln_out, head) over `model`'s packed projections, one
+    HIP graph per weight copy; returns (wall s, GPU ms, launches per token)
+    over `steps` tokens of B rows."""
+    import torch
+    from swiftrwkv_amd import synthetic as syn
+    from swiftrwkv_amd.x070 import X070Decoder
+
+    s = model.shape
+    dense = syn.x070_dense_params(s, seed=11)
+    decs = [X070Decoder(s.n_layer, s.n_embd, s.ffn, s.vocab, dense, model.host, dev) for _ in range(copies)]
+    st = decs[0].new_state(B)
+    ids = torch.randint(0, s.vocab, (B,), dtype=torch.int32, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        for d in decs:
+            d.launch(ids, st)   # buffers exist before capture; the state is not zero
+        torch.cuda.synchronize()
+        s0 = st.clone()
+        eager = decs[0].launch(ids, st).clone()
+        eager_wkv = st.wkv.clone()
+        graphs = []
+        for d in decs:
+            st.copy_(s0)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                out = d.launch(ids, st)
+            graphs.append((g, out))
+        torch.cuda.synchronize()
+        st.copy_(s0)
+        torch.cuda.synchronize()
+        graphs[0][0].replay()
+        torch.cuda.synchronize()
+        if not (torch.equal(graphs[0][1], eager) and torch.equal(st.wkv, eager_wkv)):
+            raise RuntimeError("x070 decode graph replay differs from the eager token")
+        for i in range(warmup):
+            graphs[i % copies][0].replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(steps):
+            graphs[i % copies][0].replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    del decs, graphs
+    torch.cuda.empty_cache()
+    return wall, e0.elapsed_time(e1), 8 * s.n_layer + 3
+
+
+def x070_line(model, dev, steps, warmup, copies=1, B=1):
+    wall, gpu_ms, launches = run_x070(model, dev, steps, warmup, copies, B)
+    ms = wall * 1e3 / steps
+    log(f"x070 decode e2e {model.shape.name} batch {B}: {ms:.3f} ms per token ({launches} launches)")
+    return {"tok_s": B * steps / wall, "ms_per_token": ms, "launches_per_token": launches,
+            "weight_copies_rotated": copies}
+
+
 def bench_decode(args, dev):
     from swiftrwkv_amd import synthetic as syn
 
@@ -392,6 +454,8 @@ def bench_decode_more(model_01, dev):
 
     res = {"projection_crossover_0.1B_ffn_key": bench_projection_crossover(model_01, dev)}
     log(f"projection crossover: {res['projection_crossover_0.1B_ffn_key']}")
+    res["x070_decode_e2e_0.1B_batch1"] = x070_line(model_01, dev, 200, 10, copies=len(model_01.dev))
+    res["x070_decode_e2e_0.1B_batch8"] = x070_line(model_01, dev, 50, 5, copies=len(model_01.dev), B=8)
     for B in (8, 32):
         _, wall, gpu_ms = run_decode(model_01, dev, B, 50, 5, len(model_01.dev))
         res[f"decode_0.1B_batch{B}"] = {"tok_s": B * 50 / wall, "ms_per_step": wall * 1e3 / 50}
@@ -412,6 +476,7 @@ def bench_decode_more(model_01, dev):
                                  "gemv_bytes_per_token": model.bytes_per_token,
                                  "effective_GBps": model.bytes_per_token / (ms * 1e-3) / 1e9}
     log(f"decode 1.5B: {ms:.3f} ms per token")
+    res["x070_decode_e2e_1.5B_batch1"] = x070_line(model, dev, 50, 5)
     del model
     torch.cuda.empty_cache()
     # 7B class (32 layers, n_embd 4096, FFN 14336): 3.57 GB of packed weights
@@ -425,6 +490,7 @@ def bench_decode_more(model_01, dev):
                                       "gemv_bytes_per_token": model.bytes_per_token,
                                       "effective_GBps": model.bytes_per_token / (ms * 1e-3) / 1e9}
         log(f"decode 7B batch {B}: {ms:.3f} ms per step")
+    res["x070_decode_e2e_7B_batch1"] = x070_line(model, dev, 20, 2)
     del model
     torch.cuda.empty_cache()
     res["wkv7_prefill_7B_B1_T8192_H64_fp32"] = bench_wkv_prefill_7b(dev)

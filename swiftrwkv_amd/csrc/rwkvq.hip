@@ -351,15 +351,19 @@ struct GemvGeom {
     int ep;    // epilogue: 0 store, 1 add to y (residual stream), 2 relu² of the result
 };
 
-// y[i] ← t, y[i] + t or relu(t)², the separate operations' exact arithmetic.
-__device__ __forceinline__ void store_out(float* __restrict__ y, int64_t i, float t, int ep) {
+// y[i] ← t, res + t (res = y[i], read before the product) or relu(t)², the
+// separate operations' exact arithmetic.
+__device__ __forceinline__ void store_out(float* __restrict__ y, int64_t i, float t, int ep, float res) {
     if (ep == 1) {
-        t = y[i] + t;
+        t = res + t;
     } else if (ep == 2) {
         t = fmaxf(t, 0.0f);
         t = t * t;
     }
     y[i] = t;
+}
+__device__ __forceinline__ void store_out(float* __restrict__ y, int64_t i, float t, int ep) {
+    store_out(y, i, t, ep, ep == 1 ? y[i] : 0.0f);
 }
 
 // Padded LDS row: column c at c + 4·(c / 32), so the G lanes of a row group
@@ -449,14 +453,26 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
             }
         }
     };
-    auto store = [&](float (&acc)[NT][RL], int n0) {
+    // the residual of the add epilogue, read while the weights stream
+    auto load_res = [&](float (&res)[NT][RL], int n0) {
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn)
+#pragma unroll
+            for (int rr = 0; rr < RL; ++rr) {
+                const int row = row0 + rr;
+                res[nn][rr] = (geo.ep == 1 && g == 0 && row < OUT && n0 + nn < N) ? y[(int64_t)(n0 + nn) * OUT + row]
+                                                                                 : 0.0f;
+            }
+    };
+    auto store = [&](float (&acc)[NT][RL], int n0, const float (&res)[NT][RL]) {
 #pragma unroll
         for (int nn = 0; nn < NT; ++nn)
 #pragma unroll
             for (int rr = 0; rr < RL; ++rr) {
                 const float t = group_sum(acc[nn][rr], geo.G);
                 const int row = row0 + rr;
-                if (g == 0 && row < OUT && n0 + nn < N) store_out(y, (int64_t)(n0 + nn) * OUT + row, t, geo.ep);
+                if (g == 0 && row < OUT && n0 + nn < N)
+                    store_out(y, (int64_t)(n0 + nn) * OUT + row, t, geo.ep, res[nn][rr]);
             }
     };
 
@@ -503,7 +519,8 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
                 __syncthreads();
             }
         };
-        float acc[NT][RL];
+        float acc[NT][RL], res[NT][RL];
+        load_res(res, 0);
         stage(0);
         zero(acc);
         if constexpr (MULTI) {
@@ -523,17 +540,18 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
         } else {
             compute_pass(0, W, 0, acc);   // NP == 1
         }
-        store(acc, 0);
+        store(acc, 0, res);
     } else {
         for (int n0 = 0; n0 < N; n0 += NT) {
-            float acc[NT][RL];
+            float acc[NT][RL], res[NT][RL];
+            load_res(res, n0);
             zero(acc);
             for (int p = 0; p < geo.NP; ++p) {
                 Raw W[RL][KU];
                 load_pass(p, W);
                 compute_pass(p, W, n0, acc);
             }
-            store(acc, n0);
+            store(acc, n0, res);
         }
     }
 }

@@ -20,8 +20,7 @@
 namespace {
 using namespace rwkv_wkv;
 
-constexpr int kLnThreads = 256;
-constexpr int kLnMaxPer = 32;   // elements per thread: D ≤ 8192
+constexpr int kRowMax = 8192;   // widest row of the row kernels
 
 __device__ __forceinline__ float f16_round(float x) { return __half2float(__float2half_rn(x)); }
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -39,43 +38,53 @@ __device__ __forceinline__ float block_total(float v, float* red) {
     return t;
 }
 
-// Row statistics of layerNorm_ (X070Generation.swift:511-514): mean, then the
-// mean of squared deviations; element i of the row is v[j], i = t + 256·j.
-__device__ __forceinline__ void ln_row(float (&v)[kLnMaxPer], int D, const float* __restrict__ w,
-                                       const float* __restrict__ b, float eps, float* red) {
+__device__ __forceinline__ float sum4(float4 a) { return (a.x + a.y) + (a.z + a.w); }
+
+// Row kernels: one workgroup per row, thread t owns the float4 chunks
+// t + T·p (p < P) of the row, T = blockDim.x = D / (4·P); every load of a
+// thread is issued before the first reduction.
+//
+// layerNorm_ (X070Generation.swift:511-514): mean, then the mean of squared
+// deviations, (x − mean)/sqrt(var + eps)·w + b.
+template <int P>
+__device__ __forceinline__ void ln_rows(float4 (&v)[P], const float4 (&w)[P], const float4 (&b)[P], int D, float eps,
+                                        float* red) {
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kLnMaxPer; ++j) {
-        const int i = threadIdx.x + kLnThreads * j;
-        if (i < D) s += v[j];
-    }
+    for (int p = 0; p < P; ++p) s += sum4(v[p]);
     const float mean = block_total(s, red) / (float)D;
     float q = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kLnMaxPer; ++j) {
-        const int i = threadIdx.x + kLnThreads * j;
-        if (i < D) {
-            const float d = v[j] - mean;
-            q += d * d;
-        }
+    for (int p = 0; p < P; ++p) {
+        const float4 d = make_float4(v[p].x - mean, v[p].y - mean, v[p].z - mean, v[p].w - mean);
+        q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
     }
     const float den = sqrtf(block_total(q, red) / (float)D + eps);
 #pragma unroll
-    for (int j = 0; j < kLnMaxPer; ++j) {
-        const int i = threadIdx.x + kLnThreads * j;
-        if (i < D) v[j] = (v[j] - mean) / den * w[i] + b[i];
+    for (int p = 0; p < P; ++p) {
+        v[p].x = (v[p].x - mean) / den * w[p].x + b[p].x;
+        v[p].y = (v[p].y - mean) / den * w[p].y + b[p].y;
+        v[p].z = (v[p].z - mean) / den * w[p].z + b[p].z;
+        v[p].w = (v[p].w - mean) / den * w[p].w + b[p].w;
     }
+}
+
+__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4(const __half* p) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(p);
+    const float2 a = __half22float2(*reinterpret_cast<const __half2*>(&raw.x));
+    const float2 c = __half22float2(*reinterpret_cast<const __half2*>(&raw.y));
+    return make_float4(a.x, a.y, c.x, c.y);
 }
 
 // y[n] = LN(src(n)); src(n) = x[n] or, with `ids`, row ids[n] of the table x
 // (fp32 or fp16); an id outside [0, rows) gives a NaN row.
-template <typename T>
-__global__ __launch_bounds__(kLnThreads) void layer_norm_kernel(const T* __restrict__ x, const int32_t* ids,
-                                                                int64_t rows, const float* __restrict__ w,
-                                                                const float* __restrict__ b, float* __restrict__ y,
-                                                                int D, float eps) {
-    __shared__ float red[kLnThreads / 64];
-    const int n = blockIdx.x;
+template <typename T, int P>
+__global__ __launch_bounds__(1024) void layer_norm_kernel(const T* __restrict__ x, const int32_t* ids, int64_t rows,
+                                                          const float* __restrict__ w, const float* __restrict__ b,
+                                                          float* __restrict__ y, int D, float eps) {
+    __shared__ float red[16];
+    const int n = blockIdx.x, T4 = blockDim.x;
     int64_t src = n;
     bool bad = false;
     if (ids) {
@@ -83,54 +92,67 @@ __global__ __launch_bounds__(kLnThreads) void layer_norm_kernel(const T* __restr
         bad = id < 0 || (int64_t)id >= rows;
         src = bad ? 0 : id;
     }
-    const T* row = x + src * D;
-    float v[kLnMaxPer];
+    float4 v[P], wv[P], bv[P];
 #pragma unroll
-    for (int j = 0; j < kLnMaxPer; ++j) {
-        const int i = threadIdx.x + kLnThreads * j;
-        v[j] = i < D ? (float)row[i] : 0.0f;
+    for (int p = 0; p < P; ++p) {
+        const int c = 4 * (threadIdx.x + T4 * p);
+        v[p] = load4(x + src * D + c);
+        wv[p] = load4(w + c);
+        bv[p] = load4(b + c);
     }
-    ln_row(v, D, w, b, eps, red);
+    ln_rows<P>(v, wv, bv, D, eps, red);
+    const float nan = __builtin_nanf("");
 #pragma unroll
-    for (int j = 0; j < kLnMaxPer; ++j) {
-        const int i = threadIdx.x + kLnThreads * j;
-        if (i < D) y[(int64_t)n * D + i] = bad ? __builtin_nanf("") : v[j];
+    for (int p = 0; p < P; ++p) {
+        const int c = 4 * (threadIdx.x + T4 * p);
+        *reinterpret_cast<float4*>(y + (int64_t)n * D + c) = bad ? make_float4(nan, nan, nan, nan) : v[p];
     }
 }
 
 // Token shift with its lerps (tmixStep :214-239, cmixStep :303-308) on the
 // layer-normed row: xl = LN(x[n]); xx = prev[n] − xl; prev[n] ← xl;
-// coefficient c gives xl + xx·coef[c].  Coefficients 0..2 go to out0 [N, 3, D]
-// (or [N, D] when NC == 1), 3..5 to out1 [N, 3, D].
-__global__ __launch_bounds__(kLnThreads) void shift_mix_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                               const float* __restrict__ b, float* __restrict__ prev,
-                                                               const float* __restrict__ coef, int NC,
-                                                               float* __restrict__ out0, float* __restrict__ out1, int D,
-                                                               float eps) {
-    __shared__ float red[kLnThreads / 64];
-    const int n = blockIdx.x;
-    float v[kLnMaxPer];
+// coefficient c gives xl + xx·coef[c].  NC = 6: coefficients 0..2 go to out0
+// [N, 3, D], 3..5 to out1 [N, 3, D]; NC = 1: out0 [N, D].
+template <int NC, int P>
+__global__ __launch_bounds__(1024) void shift_mix_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                         const float* __restrict__ b, float* __restrict__ prev,
+                                                         const float* __restrict__ coef, float* __restrict__ out0,
+                                                         float* __restrict__ out1, int D, float eps) {
+    __shared__ float red[16];
+    const int n = blockIdx.x, T4 = blockDim.x;
+    float4 v[P], wv[P], bv[P], pv[P], cv[P][NC];
 #pragma unroll
-    for (int j = 0; j < kLnMaxPer; ++j) {
-        const int i = threadIdx.x + kLnThreads * j;
-        v[j] = i < D ? x[(int64_t)n * D + i] : 0.0f;
+    for (int p = 0; p < P; ++p) {
+        const int c = 4 * (threadIdx.x + T4 * p);
+        v[p] = load4(x + (int64_t)n * D + c);
+        wv[p] = load4(w + c);
+        bv[p] = load4(b + c);
+        pv[p] = load4(prev + (int64_t)n * D + c);
+#pragma unroll
+        for (int k = 0; k < NC; ++k) cv[p][k] = load4(coef + (int64_t)k * D + c);
     }
-    ln_row(v, D, w, b, eps, red);
-    const int n0 = NC < 3 ? NC : 3;
+    ln_rows<P>(v, wv, bv, D, eps, red);
+    constexpr int N0 = NC < 3 ? NC : 3;
 #pragma unroll
-    for (int j = 0; j < kLnMaxPer; ++j) {
-        const int i = threadIdx.x + kLnThreads * j;
-        if (i >= D) continue;
-        const int64_t e = (int64_t)n * D + i;
-        const float xl = v[j];
-        const float xx = prev[e] - xl;
-        prev[e] = xl;
-        for (int c = 0; c < NC; ++c) {
-            const float m = xl + xx * coef[(int64_t)c * D + i];
-            if (c < n0) out0[((int64_t)n * n0 + c) * D + i] = m;
-            else out1[((int64_t)n * 3 + (c - 3)) * D + i] = m;
+    for (int p = 0; p < P; ++p) {
+        const int c = 4 * (threadIdx.x + T4 * p);
+        const float4 xl = v[p];
+        const float4 xx = make_float4(pv[p].x - xl.x, pv[p].y - xl.y, pv[p].z - xl.z, pv[p].w - xl.w);
+        *reinterpret_cast<float4*>(prev + (int64_t)n * D + c) = xl;
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+            const float4 q = cv[p][k];
+            const float4 m = make_float4(xl.x + xx.x * q.x, xl.y + xx.y * q.y, xl.z + xx.z * q.z, xl.w + xx.w * q.w);
+            float* dst = k < N0 ? out0 + ((int64_t)n * N0 + k) * D : out1 + ((int64_t)n * 3 + (k - 3)) * D;
+            *reinterpret_cast<float4*>(dst + c) = m;
         }
     }
+}
+
+// Threads and chunks per thread of a row kernel for width D (D % 256 == 0).
+inline void row_geometry(int64_t D, int& threads, int& P) {
+    P = D <= 4096 ? 1 : 2;
+    threads = (int)(D / (4 * P));
 }
 
 // ── low-rank first layers (tmixStep :256-276, the inner `lin` of each branch) ──
@@ -151,30 +173,41 @@ __global__ __launch_bounds__(256) void lora_in_kernel(const float* __restrict__ 
     const float* xin = br == 2 ? xrkv + ((int64_t)n * 3 + 2) * D
                                : xwag + ((int64_t)n * 3 + (br == 0 ? 0 : br == 1 ? 1 : 2)) * D;
     float acc = 0.0f;
-    if constexpr (H16) {
-        const __half* wr = reinterpret_cast<const __half*>(Wcat) + (int64_t)j * D;
-        for (int c = lane * 8; c < D; c += 512) {   // D % 8 == 0
-            const uint4 raw = *reinterpret_cast<const uint4*>(wr + c);
-            const float4 x0 = *reinterpret_cast<const float4*>(xin + c);
-            const float4 x1 = *reinterpret_cast<const float4*>(xin + c + 4);
-            const __half2* h = reinterpret_cast<const __half2*>(&raw);
-            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    constexpr int E = H16 ? 8 : 4;   // matrix elements per 16-byte load
+    constexpr int BATCH = 8;         // loads in flight per lane
+    for (int c0 = 0; c0 < D; c0 += 64 * E * BATCH) {
+        uint4 raw[BATCH];
+        float4 xa[BATCH], xb[BATCH];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float2 f = __half22float2(h[e]);
-                acc = fmaf(f16_round(xs[2 * e]), f.x, acc);
-                acc = fmaf(f16_round(xs[2 * e + 1]), f.y, acc);
+        for (int q = 0; q < BATCH; ++q) {
+            const int c = c0 + 64 * E * q + lane * E;
+            if (c < D) {   // D % 8 == 0
+                const char* base = reinterpret_cast<const char*>(Wcat) + ((int64_t)j * D + c) * (H16 ? 2 : 4);
+                raw[q] = *reinterpret_cast<const uint4*>(base);
+                xa[q] = *reinterpret_cast<const float4*>(xin + c);
+                if (H16) xb[q] = *reinterpret_cast<const float4*>(xin + c + 4);
             }
         }
-    } else {
-        const float* wr = reinterpret_cast<const float*>(Wcat) + (int64_t)j * D;
-        for (int c = lane * 4; c < D; c += 256) {   // D % 4 == 0
-            const float4 wv = *reinterpret_cast<const float4*>(wr + c);
-            const float4 xv = *reinterpret_cast<const float4*>(xin + c);
-            acc = fmaf(xv.x, wv.x, acc);
-            acc = fmaf(xv.y, wv.y, acc);
-            acc = fmaf(xv.z, wv.z, acc);
-            acc = fmaf(xv.w, wv.w, acc);
+#pragma unroll
+        for (int q = 0; q < BATCH; ++q) {
+            const int c = c0 + 64 * E * q + lane * E;
+            if (c >= D) continue;
+            if constexpr (H16) {
+                const __half2* h = reinterpret_cast<const __half2*>(&raw[q]);
+                const float xs[8] = {xa[q].x, xa[q].y, xa[q].z, xa[q].w, xb[q].x, xb[q].y, xb[q].z, xb[q].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float2 f = __half22float2(h[e]);
+                    acc = fmaf(f16_round(xs[2 * e]), f.x, acc);
+                    acc = fmaf(f16_round(xs[2 * e + 1]), f.y, acc);
+                }
+            } else {
+                const float4 wv = *reinterpret_cast<const float4*>(&raw[q]);
+                acc = fmaf(xa[q].x, wv.x, acc);
+                acc = fmaf(xa[q].y, wv.y, acc);
+                acc = fmaf(xa[q].z, wv.z, acc);
+                acc = fmaf(xa[q].w, wv.w, acc);
+            }
         }
     }
     float t = wave_total(acc);
@@ -220,43 +253,62 @@ __global__ __launch_bounds__(R4 ? 1024 : 256) void tmix_core_kernel(CoreArgs A) 
         lav[j] = H16 ? f16_round(t) : t;
     }
     __syncthreads();
-    if (threadIdx.x < 4 * D) {
-        const int b = threadIdx.x >> 6, i = threadIdx.x & 63;
-        const int row = h * D + i;
-        if (!(b == 2 && A.layer0)) {
+    {
+        // 4 branches × 8 groups of 8 rows, one group per wave at a time; a
+        // row's dot is split over 8 lanes (16-byte loads, all of a lane's
+        // loads in flight), then summed over those lanes.
+        const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        const int sub = lane & 7, i0 = lane >> 3;
+        constexpr int E = H16 ? 8 : 4;
+        for (int job = wave; job < 32; job += nw) {
+            const int b = job >> 3, i = (job & 7) * 8 + i0;
+            if (b == 2 && A.layer0) continue;   // uniform per wave
             int off = 0;
             for (int q = 0; q < b; ++q) off += A.rank[q];
             const int rk = A.rank[b];
+            const char* wr = reinterpret_cast<const char*>(A.W2[b]) + (int64_t)(h * D + i) * rk * (H16 ? 2 : 4);
             float acc = 0.0f;
-            if constexpr (H16) {
-                const __half* wr = reinterpret_cast<const __half*>(A.W2[b]) + (int64_t)row * rk;
-                for (int c = 0; c < rk; c += 8) {   // ranks % 8 == 0
-                    const uint4 raw = *reinterpret_cast<const uint4*>(wr + c);
-                    const __half2* hh = reinterpret_cast<const __half2*>(&raw);
+            for (int c0 = 0; c0 < rk; c0 += 8 * E * 8) {
+                uint4 raw[8];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float2 f = __half22float2(hh[e]);
-                        acc = fmaf(lav[off + c + 2 * e], f.x, acc);
-                        acc = fmaf(lav[off + c + 2 * e + 1], f.y, acc);
+                for (int q = 0; q < 8; ++q) {
+                    const int c = c0 + 8 * E * q + E * sub;
+                    if (c < rk) raw[q] = *reinterpret_cast<const uint4*>(wr + (int64_t)c * (H16 ? 2 : 4));
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int c = c0 + 8 * E * q + E * sub;
+                    if (c >= rk) continue;
+                    if constexpr (H16) {
+                        const __half2* hh = reinterpret_cast<const __half2*>(&raw[q]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float2 f = __half22float2(hh[e]);
+                            acc = fmaf(lav[off + c + 2 * e], f.x, acc);
+                            acc = fmaf(lav[off + c + 2 * e + 1], f.y, acc);
+                        }
+                    } else {
+                        const float4 f = *reinterpret_cast<const float4*>(&raw[q]);
+                        acc = fmaf(lav[off + c], f.x, acc);
+                        acc = fmaf(lav[off + c + 1], f.y, acc);
+                        acc = fmaf(lav[off + c + 2], f.z, acc);
+                        acc = fmaf(lav[off + c + 3], f.w, acc);
                     }
                 }
-                acc = f16_round(acc);
-            } else {
-                const float* wr = reinterpret_cast<const float*>(A.W2[b]) + (int64_t)row * rk;
-                for (int c = 0; c < rk; c += 4) {
-                    const float4 f = *reinterpret_cast<const float4*>(wr + c);
-                    acc = fmaf(lav[off + c], f.x, acc);
-                    acc = fmaf(lav[off + c + 1], f.y, acc);
-                    acc = fmaf(lav[off + c + 2], f.z, acc);
-                    acc = fmaf(lav[off + c + 3], f.w, acc);
-                }
             }
-            float t;
-            if (b == 0) t = expf(-0.606531f * sigmoidf_(acc + A.bias[0][row]));
-            else if (b == 1) t = sigmoidf_(acc + A.bias[1][row]);
-            else if (b == 2) t = sigmoidf_(acc + A.bias[2][row]);
-            else t = acc;
-            br[b * D + i] = t;
+            acc += __shfl_xor(acc, 1, 64);
+            acc += __shfl_xor(acc, 2, 64);
+            acc += __shfl_xor(acc, 4, 64);
+            if (sub == 0) {
+                if constexpr (H16) acc = f16_round(acc);
+                const int row = h * D + i;
+                float t;
+                if (b == 0) t = expf(-0.606531f * sigmoidf_(acc + A.bias[0][row]));
+                else if (b == 1) t = sigmoidf_(acc + A.bias[1][row]);
+                else if (b == 2) t = sigmoidf_(acc + A.bias[2][row]);
+                else t = acc;
+                br[b * D + i] = t;
+            }
         }
     }
     __syncthreads();
@@ -310,18 +362,24 @@ rwkv_status rwkv_layer_norm(const void* x, rwkv_dtype x_dt, const int32_t* ids, 
                             const float* b, float* y, int64_t N, int64_t D, float eps, void* stream) {
     RWKV_REQUIRE(N == 0 || (x && w && b && y), RWKV_E_NULL, "layer_norm: null buffer");
     RWKV_REQUIRE(x_dt == RWKV_F32 || x_dt == RWKV_F16, RWKV_E_DTYPE, "layer_norm: input dtype %d not f32/f16", (int)x_dt);
-    RWKV_REQUIRE(N >= 0 && N <= INT32_MAX && D >= 1 && D <= kLnThreads * kLnMaxPer, RWKV_E_SHAPE,
-                 "layer_norm: N=%lld D=%lld (D <= %d)", (long long)N, (long long)D, kLnThreads * kLnMaxPer);
+    RWKV_REQUIRE(N >= 0 && N <= INT32_MAX && D >= 256 && D % 256 == 0 && D <= kRowMax && (D <= 4096 || D % 512 == 0),
+                 RWKV_E_SHAPE, "layer_norm: N=%lld D=%lld (D %% 256 == 0, D <= %d)", (long long)N, (long long)D,
+                 kRowMax);
     RWKV_REQUIRE(!ids || rows >= 1, RWKV_E_SHAPE, "layer_norm: gather from a table of %lld rows", (long long)rows);
     if (N == 0) return RWKV_OK;
-    if (x_dt == RWKV_F16)
-        rwkv::launch(layer_norm_kernel<__half>, dim3((unsigned)N), dim3(kLnThreads),
-                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const __half*>(x), ids, rows, w, b, y,
-                     (int)D, eps);
-    else
-        rwkv::launch(layer_norm_kernel<float>, dim3((unsigned)N), dim3(kLnThreads),
-                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const float*>(x), ids, rows, w, b, y,
-                     (int)D, eps);
+    int T, P;
+    row_geometry(D, T, P);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)N), block(T);
+    if (x_dt == RWKV_F16) {
+        const __half* xh = reinterpret_cast<const __half*>(x);
+        if (P == 1) rwkv::launch(layer_norm_kernel<__half, 1>, grid, block, st, xh, ids, rows, w, b, y, (int)D, eps);
+        else rwkv::launch(layer_norm_kernel<__half, 2>, grid, block, st, xh, ids, rows, w, b, y, (int)D, eps);
+    } else {
+        const float* xf = reinterpret_cast<const float*>(x);
+        if (P == 1) rwkv::launch(layer_norm_kernel<float, 1>, grid, block, st, xf, ids, rows, w, b, y, (int)D, eps);
+        else rwkv::launch(layer_norm_kernel<float, 2>, grid, block, st, xf, ids, rows, w, b, y, (int)D, eps);
+    }
     return status_of("layer_norm launch");
 }
 
@@ -329,10 +387,23 @@ rwkv_status rwkv_x070_shift_mix(const float* x, const float* lnw, const float* l
                                 int nc, float* out0, float* out1, int64_t N, int64_t D, float eps, void* stream) {
     RWKV_REQUIRE(x && lnw && lnb && prev && coef && out0 && (nc <= 3 || out1), RWKV_E_NULL, "x070_shift_mix: null buffer");
     RWKV_REQUIRE(nc == 1 || nc == 6, RWKV_E_SHAPE, "x070_shift_mix: %d coefficients (1 or 6)", nc);
-    RWKV_REQUIRE(N >= 1 && N <= INT32_MAX && D >= 1 && D <= kLnThreads * kLnMaxPer, RWKV_E_SHAPE,
-                 "x070_shift_mix: N=%lld D=%lld", (long long)N, (long long)D);
-    rwkv::launch(shift_mix_kernel, dim3((unsigned)N), dim3(kLnThreads), reinterpret_cast<hipStream_t>(stream), x, lnw,
-                 lnb, prev, coef, nc, out0, out1, (int)D, eps);
+    RWKV_REQUIRE(N >= 1 && N <= INT32_MAX && D >= 256 && D % 256 == 0 && D <= kRowMax && (D <= 4096 || D % 512 == 0),
+                 RWKV_E_SHAPE, "x070_shift_mix: N=%lld D=%lld (D %% 256 == 0, D <= %d)", (long long)N, (long long)D,
+                 kRowMax);
+    int T, P;
+    row_geometry(D, T, P);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)N), block(T);
+#define RWKV_SM(NCV, PV) \
+    rwkv::launch(shift_mix_kernel<NCV, PV>, grid, block, st, x, lnw, lnb, prev, coef, out0, out1, (int)D, eps)
+    if (nc == 6) {
+        if (P == 1) RWKV_SM(6, 1);
+        else RWKV_SM(6, 2);
+    } else {
+        if (P == 1) RWKV_SM(1, 1);
+        else RWKV_SM(1, 2);
+    }
+#undef RWKV_SM
     return status_of("x070_shift_mix launch");
 }
 
