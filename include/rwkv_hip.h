@@ -216,7 +216,8 @@ rwkv_status rwkv_sym_gemv_ep(const float* x, int64_t N,
 /* y[n] = LayerNorm(src_n)·w + b over D (layerNorm_, X070Generation.swift:505-515:
  * mean, then mean squared deviation, eps).  src_n = x[n] ([N, D], f32/f16) or,
  * with ids (int32, device), row ids[n] of the table x [rows, D] (embedForBlock
- * + ln0, :489-490); an id outside [0, rows) gives a NaN row.  D ≤ 8192. */
+ * + ln0, :489-490); an id outside [0, rows) gives a NaN row.  D % 256 == 0 and
+ * D ≤ 4096, or D ∈ {2048, 4096, 8192}; y must not alias x.  N ≤ 65535. */
 rwkv_status rwkv_layer_norm(const void* x, rwkv_dtype x_dt, const int32_t* ids, int64_t rows,
                             const float* w, const float* b, float* y, int64_t N, int64_t D,
                             float eps, void* stream);
@@ -225,7 +226,8 @@ rwkv_status rwkv_layer_norm(const void* x, rwkv_dtype x_dt, const int32_t* ids, 
  * :492) or cmixStep (:303-308; ln2 :495-496): xl = LN(x[n]); xx = prev[n] − xl;
  * prev[n] ← xl; m_c = xl + xx·coef[c].  nc = 6: coef [6, D] in the order
  * r, k, v, w, a, g; out0 [N, 3, D] ← (m_r, m_k, m_v) (the fused r/k/v GEMV
- * input), out1 [N, 3, D] ← (m_w, m_a, m_g).  nc = 1: out0 [N, D]. */
+ * input), out1 [N, 3, D] ← (m_w, m_a, m_g).  nc = 1: out0 [N, D].  Widths as
+ * rwkv_layer_norm; the outputs must not alias x. */
 rwkv_status rwkv_x070_shift_mix(const float* x, const float* lnw, const float* lnb, float* prev,
                                 const float* coef, int nc, float* out0, float* out1,
                                 int64_t N, int64_t D, float eps, void* stream);

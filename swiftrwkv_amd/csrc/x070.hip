@@ -40,33 +40,32 @@ __device__ __forceinline__ float block_total(float v, float* red) {
 
 __device__ __forceinline__ float sum4(float4 a) { return (a.x + a.y) + (a.z + a.w); }
 
-// Row kernels: one workgroup per row, thread t owns the float4 chunks
-// t + T·p (p < P) of the row, T = blockDim.x = D / (4·P); every load of a
-// thread is issued before the first reduction.
+// Row kernels: a row of D is split over S workgroups of T threads (S = D/1024
+// with T = 256 when 1024 divides D, else S = 1 with T = D/4); thread t of
+// slice s writes the float4 chunk s·T + t.  Every workgroup forms the row's
+// statistics itself from the whole row (PS = D/(4T) chunks per thread, the
+// same order in every slice), with all of a thread's loads issued first.
 //
 // layerNorm_ (X070Generation.swift:511-514): mean, then the mean of squared
-// deviations, (x − mean)/sqrt(var + eps)·w + b.
-template <int P>
-__device__ __forceinline__ void ln_rows(float4 (&v)[P], const float4 (&w)[P], const float4 (&b)[P], int D, float eps,
-                                        float* red) {
+// deviations; the row's (mean, sqrt(var + eps)).
+template <int PS>
+__device__ __forceinline__ float2 row_stats(const float4 (&v)[PS], int D, float eps, float* red) {
     float s = 0.0f;
 #pragma unroll
-    for (int p = 0; p < P; ++p) s += sum4(v[p]);
+    for (int p = 0; p < PS; ++p) s += sum4(v[p]);
     const float mean = block_total(s, red) / (float)D;
     float q = 0.0f;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
+    for (int p = 0; p < PS; ++p) {
         const float4 d = make_float4(v[p].x - mean, v[p].y - mean, v[p].z - mean, v[p].w - mean);
         q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
     }
-    const float den = sqrtf(block_total(q, red) / (float)D + eps);
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        v[p].x = (v[p].x - mean) / den * w[p].x + b[p].x;
-        v[p].y = (v[p].y - mean) / den * w[p].y + b[p].y;
-        v[p].z = (v[p].z - mean) / den * w[p].z + b[p].z;
-        v[p].w = (v[p].w - mean) / den * w[p].w + b[p].w;
-    }
+    return make_float2(mean, sqrtf(block_total(q, red) / (float)D + eps));
+}
+
+__device__ __forceinline__ float4 ln_apply(float4 x, float2 md, float4 w, float4 b) {
+    return make_float4((x.x - md.x) / md.y * w.x + b.x, (x.y - md.x) / md.y * w.y + b.y,
+                       (x.z - md.x) / md.y * w.z + b.z, (x.w - md.x) / md.y * w.w + b.w);
 }
 
 __device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -78,13 +77,13 @@ __device__ __forceinline__ float4 load4(const __half* p) {
 }
 
 // y[n] = LN(src(n)); src(n) = x[n] or, with `ids`, row ids[n] of the table x
-// (fp32 or fp16); an id outside [0, rows) gives a NaN row.
-template <typename T, int P>
+// (fp32 or fp16); an id outside [0, rows) gives a NaN row.  Grid (S, N).
+template <typename T, int PS>
 __global__ __launch_bounds__(1024) void layer_norm_kernel(const T* __restrict__ x, const int32_t* ids, int64_t rows,
                                                           const float* __restrict__ w, const float* __restrict__ b,
                                                           float* __restrict__ y, int D, float eps) {
     __shared__ float red[16];
-    const int n = blockIdx.x, T4 = blockDim.x;
+    const int n = blockIdx.y, T4 = blockDim.x;
     int64_t src = n;
     bool bad = false;
     if (ids) {
@@ -92,68 +91,63 @@ __global__ __launch_bounds__(1024) void layer_norm_kernel(const T* __restrict__ 
         bad = id < 0 || (int64_t)id >= rows;
         src = bad ? 0 : id;
     }
-    float4 v[P], wv[P], bv[P];
+    const T* row = x + src * D;
+    const int c = 4 * ((int)blockIdx.x * T4 + (int)threadIdx.x);
+    float4 v[PS];
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const int c = 4 * (threadIdx.x + T4 * p);
-        v[p] = load4(x + src * D + c);
-        wv[p] = load4(w + c);
-        bv[p] = load4(b + c);
-    }
-    ln_rows<P>(v, wv, bv, D, eps, red);
+    for (int p = 0; p < PS; ++p) v[p] = load4(row + 4 * (threadIdx.x + T4 * p));
+    const float4 xo = load4(row + c), wv = load4(w + c), bv = load4(b + c);
+    const float2 md = row_stats<PS>(v, D, eps, red);
     const float nan = __builtin_nanf("");
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const int c = 4 * (threadIdx.x + T4 * p);
-        *reinterpret_cast<float4*>(y + (int64_t)n * D + c) = bad ? make_float4(nan, nan, nan, nan) : v[p];
-    }
+    *reinterpret_cast<float4*>(y + (int64_t)n * D + c) = bad ? make_float4(nan, nan, nan, nan) : ln_apply(xo, md, wv, bv);
 }
 
 // Token shift with its lerps (tmixStep :214-239, cmixStep :303-308) on the
 // layer-normed row: xl = LN(x[n]); xx = prev[n] − xl; prev[n] ← xl;
 // coefficient c gives xl + xx·coef[c].  NC = 6: coefficients 0..2 go to out0
-// [N, 3, D], 3..5 to out1 [N, 3, D]; NC = 1: out0 [N, D].
-template <int NC, int P>
+// [N, 3, D], 3..5 to out1 [N, 3, D]; NC = 1: out0 [N, D].  Grid (S, N).
+template <int NC, int PS>
 __global__ __launch_bounds__(1024) void shift_mix_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                          const float* __restrict__ b, float* __restrict__ prev,
                                                          const float* __restrict__ coef, float* __restrict__ out0,
                                                          float* __restrict__ out1, int D, float eps) {
     __shared__ float red[16];
-    const int n = blockIdx.x, T4 = blockDim.x;
-    float4 v[P], wv[P], bv[P], pv[P], cv[P][NC];
+    const int n = blockIdx.y, T4 = blockDim.x;
+    const float* row = x + (int64_t)n * D;
+    const int c = 4 * ((int)blockIdx.x * T4 + (int)threadIdx.x);
+    float4 v[PS], cv[NC];
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const int c = 4 * (threadIdx.x + T4 * p);
-        v[p] = load4(x + (int64_t)n * D + c);
-        wv[p] = load4(w + c);
-        bv[p] = load4(b + c);
-        pv[p] = load4(prev + (int64_t)n * D + c);
+    for (int p = 0; p < PS; ++p) v[p] = load4(row + 4 * (threadIdx.x + T4 * p));
+    const float4 xo = load4(row + c), wv = load4(w + c), bv = load4(b + c);
+    const float4 pv = load4(prev + (int64_t)n * D + c);
 #pragma unroll
-        for (int k = 0; k < NC; ++k) cv[p][k] = load4(coef + (int64_t)k * D + c);
-    }
-    ln_rows<P>(v, wv, bv, D, eps, red);
+    for (int k = 0; k < NC; ++k) cv[k] = load4(coef + (int64_t)k * D + c);
+    const float2 md = row_stats<PS>(v, D, eps, red);
+    const float4 xl = ln_apply(xo, md, wv, bv);
+    const float4 xx = make_float4(pv.x - xl.x, pv.y - xl.y, pv.z - xl.z, pv.w - xl.w);
+    *reinterpret_cast<float4*>(prev + (int64_t)n * D + c) = xl;
     constexpr int N0 = NC < 3 ? NC : 3;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const int c = 4 * (threadIdx.x + T4 * p);
-        const float4 xl = v[p];
-        const float4 xx = make_float4(pv[p].x - xl.x, pv[p].y - xl.y, pv[p].z - xl.z, pv[p].w - xl.w);
-        *reinterpret_cast<float4*>(prev + (int64_t)n * D + c) = xl;
-#pragma unroll
-        for (int k = 0; k < NC; ++k) {
-            const float4 q = cv[p][k];
-            const float4 m = make_float4(xl.x + xx.x * q.x, xl.y + xx.y * q.y, xl.z + xx.z * q.z, xl.w + xx.w * q.w);
-            float* dst = k < N0 ? out0 + ((int64_t)n * N0 + k) * D : out1 + ((int64_t)n * 3 + (k - 3)) * D;
-            *reinterpret_cast<float4*>(dst + c) = m;
-        }
+    for (int k = 0; k < NC; ++k) {
+        const float4 q = cv[k];
+        const float4 m = make_float4(xl.x + xx.x * q.x, xl.y + xx.y * q.y, xl.z + xx.z * q.z, xl.w + xx.w * q.w);
+        float* dst = k < N0 ? out0 + ((int64_t)n * N0 + k) * D : out1 + ((int64_t)n * 3 + (k - 3)) * D;
+        *reinterpret_cast<float4*>(dst + c) = m;
     }
 }
 
-// Threads and chunks per thread of a row kernel for width D (D % 256 == 0).
-inline void row_geometry(int64_t D, int& threads, int& P) {
-    P = D <= 4096 ? 1 : 2;
-    threads = (int)(D / (4 * P));
+// Slices S, threads T and statistics chunks PS of a row kernel for width D
+// (D % 256 == 0; D ≤ 4096 or 1024 | D ≤ 8192).
+inline void row_geometry(int64_t D, int& S, int& T, int& PS) {
+    if (D % 1024 == 0) {
+        T = 256;
+        S = PS = (int)(D / 1024);
+    } else {
+        T = (int)(D / 4);
+        S = PS = 1;
+    }
 }
+inline bool row_width_ok(int64_t D) { return D >= 256 && D % 256 == 0 && D <= kRowMax && (D <= 4096 || D % 1024 == 0); }
 
 // ── low-rank first layers (tmixStep :256-276, the inner `lin` of each branch) ──
 // Rows of Wcat [rw + ra + rv + rg, D]: w, a, v, g branches; inputs xw, xa, xg
@@ -223,8 +217,7 @@ __global__ __launch_bounds__(256) void lora_in_kernel(const float* __restrict__ 
 // residual v + (v_first − v)·vv (layer 0: v_first ← v), the WKV step with
 // (r, w, k, v, −kk, kk·a) on the state in place, and the tail
 // ((GroupNorm(y)·lnw + lnb + Σ(r·k·r_k)·v)·gate) into out.  The step and tail
-// are wkv7_step_tail_kernel's device code in the same layout, so this kernel's
-// step is bitwise that kernel's on the same vectors.
+// are wkv7_step_tail_kernel's device code (same layout for the same N·H).
 struct CoreArgs {
     const float* y_rkv;   // [N, 3D]: r | k0 | v0
     const float* la;      // [N, RT]
@@ -248,98 +241,143 @@ __global__ __launch_bounds__(R4 ? 1024 : 256) void tmix_core_kernel(CoreArgs A) 
     float* ys = br + 4 * D;
     const int nh = blockIdx.x, n = nh / A.H, h = nh % A.H;
     const int Dm = A.H * D;
+    const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sub = lane & 7, i0 = lane >> 3;
+    constexpr int E = H16 ? 8 : 4;      // matrix elements per 16-byte load
+    constexpr int CH = 8 * 8 * E;       // a chunk: 8 loads of each of a row's 8 lanes
+
+    // ── loads that depend on nothing computed here, issued first ──
+    const int blk = wave, l = lane;
+    const int vrow = R4 ? step4_row(blk, l) : step16_row(blk, l);
+    const int64_t ye = (int64_t)n * 3 * Dm + (int64_t)h * D;   // the head in the r block
+    const int64_t he = (int64_t)h * D + l, vf0 = (int64_t)n * Dm + (int64_t)h * D;
+    const float r = A.y_rkv[ye + l], k0 = A.y_rkv[ye + Dm + l];
+    const float v0l = A.y_rkv[ye + 2 * Dm + l], v0r = A.y_rkv[ye + 2 * Dm + vrow];
+    const float vfl = A.layer0 ? 0.0f : A.v_first[vf0 + l], vfr = A.layer0 ? 0.0f : A.v_first[vf0 + vrow];
+    const float kkc = A.k_k[he], kac = A.k_a[he], rkc = A.r_k[he], lnwc = A.lnw[he], lnbc = A.lnb[he];
+    float* st = A.state + (int64_t)nh * D * D;
+    float S[R4 ? 4 : 16];
+    if constexpr (R4) load_state4(st, blk, l, S);
+    else load_state16(st, blk, l, S);
+
+    // Low-rank second layers: 4 branches × 8 groups of 8 rows; a row's dot is
+    // split over 8 lanes, then summed over them.  Job = branch·8 + group.
+    struct Job {
+        int b, i, off, rk;
+        const char* wr;
+        bool on;
+    };
+    auto job_of = [&](int job) {
+        Job j;
+        j.b = job >> 3;
+        j.i = (job & 7) * 8 + i0;
+        j.on = !(j.b == 2 && A.layer0);
+        j.off = 0;
+        for (int q = 0; q < j.b; ++q) j.off += A.rank[q];
+        j.rk = A.rank[j.b];
+        j.wr = reinterpret_cast<const char*>(A.W2[j.b]) + (int64_t)(h * D + j.i) * j.rk * (H16 ? 2 : 4);
+        return j;
+    };
+    auto load_chunk = [&](const Job& j, int c0, uint4 (&raw)[8]) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int c = c0 + 8 * E * q + E * sub;
+            if (c < j.rk) raw[q] = *reinterpret_cast<const uint4*>(j.wr + (int64_t)c * (H16 ? 2 : 4));
+        }
+    };
+    auto fma_chunk = [&](const Job& j, int c0, const uint4 (&raw)[8], float& acc) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int c = c0 + 8 * E * q + E * sub;
+            if (c >= j.rk) continue;
+            if constexpr (H16) {
+                const __half2* hh = reinterpret_cast<const __half2*>(&raw[q]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float2 f = __half22float2(hh[e]);
+                    acc = fmaf(lav[j.off + c + 2 * e], f.x, acc);
+                    acc = fmaf(lav[j.off + c + 2 * e + 1], f.y, acc);
+                }
+            } else {
+                const float4 f = *reinterpret_cast<const float4*>(&raw[q]);
+                acc = fmaf(lav[j.off + c], f.x, acc);
+                acc = fmaf(lav[j.off + c + 1], f.y, acc);
+                acc = fmaf(lav[j.off + c + 2], f.z, acc);
+                acc = fmaf(lav[j.off + c + 3], f.w, acc);
+            }
+        }
+    };
+    auto finish = [&](const Job& j, float acc) {
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        acc += __shfl_xor(acc, 4, 64);
+        if (sub == 0) {
+            if constexpr (H16) acc = f16_round(acc);
+            const int row = h * D + j.i;
+            float t;
+            if (j.b == 0) t = expf(-0.606531f * sigmoidf_(acc + A.bias[0][row]));
+            else if (j.b == 1) t = sigmoidf_(acc + A.bias[1][row]);
+            else if (j.b == 2) t = sigmoidf_(acc + A.bias[2][row]);
+            else t = acc;
+            br[j.b * D + j.i] = t;
+        }
+    };
+    auto run_job = [&](const Job& j, const uint4 (&first)[8]) {
+        float acc = 0.0f;
+        fma_chunk(j, 0, first, acc);
+        for (int c0 = CH; c0 < j.rk; c0 += CH) {
+            uint4 raw[8];
+            load_chunk(j, c0, raw);
+            fma_chunk(j, c0, raw, acc);
+        }
+        finish(j, acc);
+    };
+
+    // sixteen waves: two jobs per wave, their first chunks in flight now
+    Job jobs[R4 ? 2 : 1];
+    uint4 pre[R4 ? 2 : 1][8];
+    if constexpr (R4) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            jobs[u] = job_of(wave + 16 * u);
+            if (jobs[u].on) load_chunk(jobs[u], 0, pre[u]);
+        }
+    }
     for (int j = threadIdx.x; j < RT; j += blockDim.x) {
         const float t = A.la[(int64_t)n * RT + j];
         lav[j] = H16 ? f16_round(t) : t;
     }
     __syncthreads();
-    {
-        // 4 branches × 8 groups of 8 rows, one group per wave at a time; a
-        // row's dot is split over 8 lanes (16-byte loads, all of a lane's
-        // loads in flight), then summed over those lanes.
-        const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-        const int sub = lane & 7, i0 = lane >> 3;
-        constexpr int E = H16 ? 8 : 4;
+    if constexpr (R4) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            if (jobs[u].on) run_job(jobs[u], pre[u]);   // uniform per wave
+    } else {
         for (int job = wave; job < 32; job += nw) {
-            const int b = job >> 3, i = (job & 7) * 8 + i0;
-            if (b == 2 && A.layer0) continue;   // uniform per wave
-            int off = 0;
-            for (int q = 0; q < b; ++q) off += A.rank[q];
-            const int rk = A.rank[b];
-            const char* wr = reinterpret_cast<const char*>(A.W2[b]) + (int64_t)(h * D + i) * rk * (H16 ? 2 : 4);
-            float acc = 0.0f;
-            for (int c0 = 0; c0 < rk; c0 += 8 * E * 8) {
-                uint4 raw[8];
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const int c = c0 + 8 * E * q + E * sub;
-                    if (c < rk) raw[q] = *reinterpret_cast<const uint4*>(wr + (int64_t)c * (H16 ? 2 : 4));
-                }
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const int c = c0 + 8 * E * q + E * sub;
-                    if (c >= rk) continue;
-                    if constexpr (H16) {
-                        const __half2* hh = reinterpret_cast<const __half2*>(&raw[q]);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const float2 f = __half22float2(hh[e]);
-                            acc = fmaf(lav[off + c + 2 * e], f.x, acc);
-                            acc = fmaf(lav[off + c + 2 * e + 1], f.y, acc);
-                        }
-                    } else {
-                        const float4 f = *reinterpret_cast<const float4*>(&raw[q]);
-                        acc = fmaf(lav[off + c], f.x, acc);
-                        acc = fmaf(lav[off + c + 1], f.y, acc);
-                        acc = fmaf(lav[off + c + 2], f.z, acc);
-                        acc = fmaf(lav[off + c + 3], f.w, acc);
-                    }
-                }
-            }
-            acc += __shfl_xor(acc, 1, 64);
-            acc += __shfl_xor(acc, 2, 64);
-            acc += __shfl_xor(acc, 4, 64);
-            if (sub == 0) {
-                if constexpr (H16) acc = f16_round(acc);
-                const int row = h * D + i;
-                float t;
-                if (b == 0) t = expf(-0.606531f * sigmoidf_(acc + A.bias[0][row]));
-                else if (b == 1) t = sigmoidf_(acc + A.bias[1][row]);
-                else if (b == 2) t = sigmoidf_(acc + A.bias[2][row]);
-                else t = acc;
-                br[b * D + i] = t;
-            }
+            const Job j = job_of(job);
+            if (!j.on) continue;   // uniform per wave
+            load_chunk(j, 0, pre[0]);
+            run_job(j, pre[0]);
         }
     }
     __syncthreads();
-    const int blk = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int vrow = R4 ? step4_row(blk, l) : step16_row(blk, l);
-    const int64_t ye = (int64_t)n * 3 * Dm + (int64_t)h * D;   // head offset in the r block
-    const int64_t he = (int64_t)h * D + l;
-    const float r = A.y_rkv[ye + l];
-    const float k0 = A.y_rkv[ye + Dm + l];
-    const float kkr = k0 * A.k_k[he];
+
+    // ── kk, k, v, the WKV step and the tail ──
+    const float kkr = k0 * kkc;
     const float kk = kkr / sqrtf(wave_total(kkr * kkr) + 1e-12f);
     const float av = br[D + l];
-    const float k = k0 * (1.0f + (av - 1.0f) * A.k_a[he]);
-    auto value = [&](int e) {
-        const float v0 = A.y_rkv[ye + 2 * Dm + e];
-        if (A.layer0) return v0;
-        const float vf = A.v_first[(int64_t)n * Dm + (int64_t)h * D + e];
-        return v0 + (vf - v0) * br[2 * D + e];
-    };
-    const float V = value(vrow);
+    const float k = k0 * (1.0f + (av - 1.0f) * kac);
+    const float V = A.layer0 ? v0r : v0r + (vfr - v0r) * br[2 * D + vrow];
     const float W = br[l];
-    float* st = A.state + (int64_t)nh * D * D;
-    const float y = R4 ? head_step4(st, st, blk, l, -kk, W, k, kk * av, r, V)
-                       : head_step16(st, st, blk, l, -kk, W, k, kk * av, r, V);
+    float y;
+    if constexpr (R4) y = head_step4_regs(S, st, blk, l, -kk, W, k, kk * av, r, V);
+    else y = head_step16_regs(S, st, blk, l, -kk, W, k, kk * av, r, V);
     if ((R4 ? (l >> 2) : (l >> 4)) == 0) ys[vrow] = y;
     __syncthreads();
     if (blk == 0) {
-        const float v = value(l);
-        if (A.layer0) A.v_first[(int64_t)n * Dm + he] = v;
-        A.out[(int64_t)n * Dm + he] =
-            head_tail(ys[l], r, k, v, A.r_k[he], A.lnw[he], A.lnb[he], br[3 * D + l], A.eps);
+        const float v = A.layer0 ? v0l : v0l + (vfl - v0l) * br[2 * D + l];
+        if (A.layer0) A.v_first[vf0 + l] = v;
+        A.out[(int64_t)n * Dm + he] = head_tail(ys[l], r, k, v, rkc, lnwc, lnbc, br[3 * D + l], A.eps);
     }
 }
 
@@ -362,24 +400,33 @@ rwkv_status rwkv_layer_norm(const void* x, rwkv_dtype x_dt, const int32_t* ids, 
                             const float* b, float* y, int64_t N, int64_t D, float eps, void* stream) {
     RWKV_REQUIRE(N == 0 || (x && w && b && y), RWKV_E_NULL, "layer_norm: null buffer");
     RWKV_REQUIRE(x_dt == RWKV_F32 || x_dt == RWKV_F16, RWKV_E_DTYPE, "layer_norm: input dtype %d not f32/f16", (int)x_dt);
-    RWKV_REQUIRE(N >= 0 && N <= INT32_MAX && D >= 256 && D % 256 == 0 && D <= kRowMax && (D <= 4096 || D % 512 == 0),
-                 RWKV_E_SHAPE, "layer_norm: N=%lld D=%lld (D %% 256 == 0, D <= %d)", (long long)N, (long long)D,
-                 kRowMax);
+    RWKV_REQUIRE(N >= 0 && N <= 65535 && row_width_ok(D), RWKV_E_SHAPE,
+                 "layer_norm: N=%lld D=%lld (D %% 256 == 0, D <= 4096 or a multiple of 1024 <= %d)", (long long)N,
+                 (long long)D, kRowMax);
     RWKV_REQUIRE(!ids || rows >= 1, RWKV_E_SHAPE, "layer_norm: gather from a table of %lld rows", (long long)rows);
     if (N == 0) return RWKV_OK;
-    int T, P;
-    row_geometry(D, T, P);
+    int S, T, PS;
+    row_geometry(D, S, T, PS);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)N), block(T);
-    if (x_dt == RWKV_F16) {
-        const __half* xh = reinterpret_cast<const __half*>(x);
-        if (P == 1) rwkv::launch(layer_norm_kernel<__half, 1>, grid, block, st, xh, ids, rows, w, b, y, (int)D, eps);
-        else rwkv::launch(layer_norm_kernel<__half, 2>, grid, block, st, xh, ids, rows, w, b, y, (int)D, eps);
-    } else {
-        const float* xf = reinterpret_cast<const float*>(x);
-        if (P == 1) rwkv::launch(layer_norm_kernel<float, 1>, grid, block, st, xf, ids, rows, w, b, y, (int)D, eps);
-        else rwkv::launch(layer_norm_kernel<float, 2>, grid, block, st, xf, ids, rows, w, b, y, (int)D, eps);
+    const dim3 grid((unsigned)S, (unsigned)N), block(T);
+#define RWKV_LN(TY, PV) \
+    rwkv::launch(layer_norm_kernel<TY, PV>, grid, block, st, reinterpret_cast<const TY*>(x), ids, rows, w, b, y, (int)D, eps)
+#define RWKV_LN_P(TY)                    \
+    switch (PS) {                        \
+        case 1: RWKV_LN(TY, 1); break;   \
+        case 2: RWKV_LN(TY, 2); break;   \
+        case 4: RWKV_LN(TY, 4); break;   \
+        default: RWKV_LN(TY, 8); break;  \
     }
+    RWKV_REQUIRE(PS == 1 || PS == 2 || PS == 4 || PS == 8, RWKV_E_SHAPE,
+                 "layer_norm: D=%lld not taken (D/1024 must be 1, 2, 4 or 8)", (long long)D);
+    if (x_dt == RWKV_F16) {
+        RWKV_LN_P(__half)
+    } else {
+        RWKV_LN_P(float)
+    }
+#undef RWKV_LN_P
+#undef RWKV_LN
     return status_of("layer_norm launch");
 }
 
@@ -387,22 +434,30 @@ rwkv_status rwkv_x070_shift_mix(const float* x, const float* lnw, const float* l
                                 int nc, float* out0, float* out1, int64_t N, int64_t D, float eps, void* stream) {
     RWKV_REQUIRE(x && lnw && lnb && prev && coef && out0 && (nc <= 3 || out1), RWKV_E_NULL, "x070_shift_mix: null buffer");
     RWKV_REQUIRE(nc == 1 || nc == 6, RWKV_E_SHAPE, "x070_shift_mix: %d coefficients (1 or 6)", nc);
-    RWKV_REQUIRE(N >= 1 && N <= INT32_MAX && D >= 256 && D % 256 == 0 && D <= kRowMax && (D <= 4096 || D % 512 == 0),
-                 RWKV_E_SHAPE, "x070_shift_mix: N=%lld D=%lld (D %% 256 == 0, D <= %d)", (long long)N, (long long)D,
-                 kRowMax);
-    int T, P;
-    row_geometry(D, T, P);
+    RWKV_REQUIRE(N >= 1 && N <= 65535 && row_width_ok(D), RWKV_E_SHAPE,
+                 "x070_shift_mix: N=%lld D=%lld (D %% 256 == 0, D <= 4096 or a multiple of 1024 <= %d)", (long long)N,
+                 (long long)D, kRowMax);
+    int S, T, PS;
+    row_geometry(D, S, T, PS);
+    RWKV_REQUIRE(PS == 1 || PS == 2 || PS == 4 || PS == 8, RWKV_E_SHAPE,
+                 "x070_shift_mix: D=%lld not taken (D/1024 must be 1, 2, 4 or 8)", (long long)D);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)N), block(T);
+    const dim3 grid((unsigned)S, (unsigned)N), block(T);
 #define RWKV_SM(NCV, PV) \
     rwkv::launch(shift_mix_kernel<NCV, PV>, grid, block, st, x, lnw, lnb, prev, coef, out0, out1, (int)D, eps)
-    if (nc == 6) {
-        if (P == 1) RWKV_SM(6, 1);
-        else RWKV_SM(6, 2);
-    } else {
-        if (P == 1) RWKV_SM(1, 1);
-        else RWKV_SM(1, 2);
+#define RWKV_SM_P(NCV)                    \
+    switch (PS) {                         \
+        case 1: RWKV_SM(NCV, 1); break;   \
+        case 2: RWKV_SM(NCV, 2); break;   \
+        case 4: RWKV_SM(NCV, 4); break;   \
+        default: RWKV_SM(NCV, 8); break;  \
     }
+    if (nc == 6) {
+        RWKV_SM_P(6)
+    } else {
+        RWKV_SM_P(1)
+    }
+#undef RWKV_SM_P
 #undef RWKV_SM
     return status_of("x070_shift_mix launch");
 }
