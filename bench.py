@@ -292,9 +292,10 @@ def run_x070(model, dev, steps, warmup, copies=1, B=1):
         e1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+    launches = decs[0].launches_per_token(B)
     del decs, graphs
     torch.cuda.empty_cache()
-    return wall, e0.elapsed_time(e1), 8 * s.n_layer + 3
+    return wall, e0.elapsed_time(e1), launches
 
 
 def x070_line(model, dev, steps, warmup, copies=1, B=1):

@@ -226,8 +226,9 @@ rwkv_status rwkv_layer_norm(const void* x, rwkv_dtype x_dt, const int32_t* ids, 
  * :492) or cmixStep (:303-308; ln2 :495-496): xl = LN(x[n]); xx = prev[n] − xl;
  * prev[n] ← xl; m_c = xl + xx·coef[c].  nc = 6: coef [6, D] in the order
  * r, k, v, w, a, g; out0 [N, 3, D] ← (m_r, m_k, m_v) (the fused r/k/v GEMV
- * input), out1 [N, 3, D] ← (m_w, m_a, m_g).  nc = 1: out0 [N, D].  Widths as
- * rwkv_layer_norm; the outputs must not alias x. */
+ * input), out1 [N, 4, D] ← (m_w, m_a, m_v, m_g) (the low-rank inputs).
+ * nc = 1: out0 [N, D].  Widths as rwkv_layer_norm; the outputs must not
+ * alias x. */
 rwkv_status rwkv_x070_shift_mix(const float* x, const float* lnw, const float* lnb, float* prev,
                                 const float* coef, int nc, float* out0, float* out1,
                                 int64_t N, int64_t D, float eps, void* stream);
@@ -235,11 +236,11 @@ rwkv_status rwkv_x070_shift_mix(const float* x, const float* lnw, const float* l
 /* First layers of the low-rank branches (tmixStep :256-276, the inner lin of
  * each): wcat [rw + ra + rv + rg, D] = w_lora_A ‖ a_lora_A ‖ v_lora_A ‖
  * g_lora_A rows; la [N, rw + ra + rv + rg] = tanh(lin(xw, ·)) ‖ lin(xa, ·) ‖
- * lin(xv, ·) ‖ sigmoid(lin(xg, ·)), xw/xa/xg = rows of xwag [N, 3, D], xv =
- * row 2 of xrkv [N, 3, D].  with_v = 0 (layer 0) skips the v branch. */
-rwkv_status rwkv_x070_lora_in(const float* xrkv, const float* xwag, const void* wcat,
-                              rwkv_dtype w_dt, int64_t rw, int64_t ra, int64_t rv, int64_t rg,
-                              int with_v, float* la, int64_t N, int64_t D, void* stream);
+ * lin(xv, ·) ‖ sigmoid(lin(xg, ·)), xw, xa, xv, xg = rows of xmix [N, 4, D].
+ * with_v = 0 (layer 0) skips the v branch. */
+rwkv_status rwkv_x070_lora_in(const float* xmix, const void* wcat, rwkv_dtype w_dt, int64_t rw,
+                              int64_t ra, int64_t rv, int64_t rg, int with_v, float* la, int64_t N,
+                              int64_t D, void* stream);
 
 /* The tmix core (tmixStep :256-294): second layers of the low-rank branches
  * for each head's rows (w2 [D, rw], a2 [D, ra], v2 [D, rv], g2 [D, rg] in

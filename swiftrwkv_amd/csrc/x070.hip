@@ -104,8 +104,9 @@ __global__ __launch_bounds__(1024) void layer_norm_kernel(const T* __restrict__ 
 
 // Token shift with its lerps (tmixStep :214-239, cmixStep :303-308) on the
 // layer-normed row: xl = LN(x[n]); xx = prev[n] − xl; prev[n] ← xl;
-// coefficient c gives xl + xx·coef[c].  NC = 6: coefficients 0..2 go to out0
-// [N, 3, D], 3..5 to out1 [N, 3, D]; NC = 1: out0 [N, D].  Grid (S, N).
+// coefficient c gives xl + xx·coef[c].  NC = 6 (coefficients r, k, v, w, a, g):
+// out0 [N, 3, D] ← (r, k, v), out1 [N, 4, D] ← (w, a, v, g), the low-rank
+// branches' inputs; NC = 1: out0 [N, D].  Grid (S, N).
 template <int NC, int PS>
 __global__ __launch_bounds__(1024) void shift_mix_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                          const float* __restrict__ b, float* __restrict__ prev,
@@ -131,8 +132,10 @@ __global__ __launch_bounds__(1024) void shift_mix_kernel(const float* __restrict
     for (int k = 0; k < NC; ++k) {
         const float4 q = cv[k];
         const float4 m = make_float4(xl.x + xx.x * q.x, xl.y + xx.y * q.y, xl.z + xx.z * q.z, xl.w + xx.w * q.w);
-        float* dst = k < N0 ? out0 + ((int64_t)n * N0 + k) * D : out1 + ((int64_t)n * 3 + (k - 3)) * D;
-        *reinterpret_cast<float4*>(dst + c) = m;
+        if (k < N0) *reinterpret_cast<float4*>(out0 + ((int64_t)n * N0 + k) * D + c) = m;
+        // low-rank inputs: w, a, v, g ← coefficients 3, 4, 2, 5
+        const int slot = k == 3 ? 0 : k == 4 ? 1 : k == 2 ? 2 : k == 5 ? 3 : -1;
+        if (NC == 6 && slot >= 0) *reinterpret_cast<float4*>(out1 + ((int64_t)n * 4 + slot) * D + c) = m;
     }
 }
 
@@ -150,13 +153,13 @@ inline void row_geometry(int64_t D, int& S, int& T, int& PS) {
 inline bool row_width_ok(int64_t D) { return D >= 256 && D % 256 == 0 && D <= kRowMax && (D <= 4096 || D % 1024 == 0); }
 
 // ── low-rank first layers (tmixStep :256-276, the inner `lin` of each branch) ──
-// Rows of Wcat [rw + ra + rv + rg, D]: w, a, v, g branches; inputs xw, xa, xg
-// = xwag rows 0..2, xv = xrkv row 2.  la[n, j] = act(lin(x_branch, Wcat[j])):
+// Rows of Wcat [rw + ra + rv + rg, D]: w, a, v, g branches; inputs xmix [N, 4, D]
+// rows w, a, v, g.  la[n, j] = act(lin(x_branch, Wcat[j])):
 // tanh for w, sigmoid for g, none for a and v.  One wave per (row, input).
 template <bool H16>
-__global__ __launch_bounds__(256) void lora_in_kernel(const float* __restrict__ xrkv, const float* __restrict__ xwag,
-                                                      const void* __restrict__ Wcat, float* __restrict__ la, int N,
-                                                      int D, int rw, int ra, int rv, int rg, int with_v) {
+__global__ __launch_bounds__(256) void lora_in_kernel(const float* __restrict__ xmix, const void* __restrict__ Wcat,
+                                                      float* __restrict__ la, int N, int D, int rw, int ra, int rv,
+                                                      int rg, int with_v) {
     const int lane = threadIdx.x & 63;
     const int RT = rw + ra + rv + rg;
     const int64_t job = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -164,8 +167,7 @@ __global__ __launch_bounds__(256) void lora_in_kernel(const float* __restrict__ 
     const int j = (int)(job % RT), n = (int)(job / RT);
     const int br = j < rw ? 0 : j < rw + ra ? 1 : j < rw + ra + rv ? 2 : 3;
     if (br == 2 && !with_v) return;
-    const float* xin = br == 2 ? xrkv + ((int64_t)n * 3 + 2) * D
-                               : xwag + ((int64_t)n * 3 + (br == 0 ? 0 : br == 1 ? 1 : 2)) * D;
+    const float* xin = xmix + ((int64_t)n * 4 + br) * D;
     float acc = 0.0f;
     constexpr int E = H16 ? 8 : 4;   // matrix elements per 16-byte load
     constexpr int BATCH = 8;         // loads in flight per lane
@@ -462,10 +464,9 @@ rwkv_status rwkv_x070_shift_mix(const float* x, const float* lnw, const float* l
     return status_of("x070_shift_mix launch");
 }
 
-rwkv_status rwkv_x070_lora_in(const float* xrkv, const float* xwag, const void* wcat, rwkv_dtype w_dt, int64_t rw,
-                              int64_t ra, int64_t rv, int64_t rg, int with_v, float* la, int64_t N, int64_t D,
-                              void* stream) {
-    RWKV_REQUIRE(xrkv && xwag && wcat && la, RWKV_E_NULL, "x070_lora_in: null buffer");
+rwkv_status rwkv_x070_lora_in(const float* xmix, const void* wcat, rwkv_dtype w_dt, int64_t rw, int64_t ra,
+                              int64_t rv, int64_t rg, int with_v, float* la, int64_t N, int64_t D, void* stream) {
+    RWKV_REQUIRE(xmix && wcat && la, RWKV_E_NULL, "x070_lora_in: null buffer");
     RWKV_REQUIRE(w_dt == RWKV_F16 || w_dt == RWKV_F32, RWKV_E_DTYPE, "x070_lora_in: matrix dtype %d not f16/f32",
                  (int)w_dt);
     RWKV_REQUIRE(rw >= 8 && ra >= 8 && rv >= 8 && rg >= 8 && rw % 8 == 0 && ra % 8 == 0 && rv % 8 == 0 && rg % 8 == 0 &&
@@ -478,10 +479,10 @@ rwkv_status rwkv_x070_lora_in(const float* xrkv, const float* xwag, const void* 
     const dim3 grid((unsigned)((jobs + 3) / 4)), block(256);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (w_dt == RWKV_F16)
-        rwkv::launch(lora_in_kernel<true>, grid, block, st, xrkv, xwag, wcat, la, (int)N, (int)D, (int)rw, (int)ra,
+        rwkv::launch(lora_in_kernel<true>, grid, block, st, xmix, wcat, la, (int)N, (int)D, (int)rw, (int)ra,
                      (int)rv, (int)rg, with_v);
     else
-        rwkv::launch(lora_in_kernel<false>, grid, block, st, xrkv, xwag, wcat, la, (int)N, (int)D, (int)rw, (int)ra,
+        rwkv::launch(lora_in_kernel<false>, grid, block, st, xmix, wcat, la, (int)N, (int)D, (int)rw, (int)ra,
                      (int)rv, (int)rg, with_v);
     return status_of("x070_lora_in launch");
 }

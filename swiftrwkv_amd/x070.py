@@ -139,9 +139,9 @@ class X070Decoder:
         if self._bufs is None or self._bufs["N"] != N:
             dev, D = self.device, self.D
             z = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)
-            self._bufs = {"N": N, "x": z(N, D), "xrkv": z(N, 3, D), "xwag": z(N, 3, D), "y_rkv": z(N, 3 * D),
+            self._bufs = {"N": N, "x": z(N, D), "xrkv": z(N, 3, D), "xmix": z(N, 4, D), "y_rkv": z(N, 3 * D),
                           "la": z(N, sum(self.ranks)), "tout": z(N, D), "xk": z(N, D), "hk": z(N, self.F),
-                          "xo": z(N, D), "logits": z(N, self.V)}
+                          "xo": z(N, D), "xl": z(D), "logits": z(N, self.V)}
         return self._bufs
 
     def launch(self, ids: torch.Tensor, state: RWKVState, stream: Optional[int] = None) -> torch.Tensor:
@@ -156,28 +156,19 @@ class X070Decoder:
             raise ValueError(f"state holds {state.n_rows} rows, ids {N}")
         s = torch.cuda.current_stream(self.device).cuda_stream if stream is None else stream
         bf = self._buffers(N)
-        L, D, H, F = _lib.lib(), self.D, self.H, self.F
+        L, D = _lib.lib(), self.D
         p = lambda t: t.data_ptr()
-        rw, ra, rv, rg = self.ranks
         x = bf["x"]
         emb_dt = _lib.F16 if self.emb.dtype == torch.float16 else _lib.F32
         _lib.check(L.rwkv_layer_norm(p(self.emb), emb_dt, p(ids), self.V, p(self.ln0[0]), p(self.ln0[1]), p(x),
                                      N, D, LN_EPS, s))
         for l, lay in enumerate(self.layers):
             _lib.check(L.rwkv_x070_shift_mix(p(x), p(lay["ln1"][0]), p(lay["ln1"][1]), p(state.tmix_prev[l]),
-                                             p(lay["coef6"]), 6, p(bf["xrkv"]), p(bf["xwag"]), N, D, LN_EPS, s))
+                                             p(lay["coef6"]), 6, p(bf["xrkv"]), p(bf["xmix"]), N, D, LN_EPS, s))
             q = self.proj[f"blocks.{l}.att.rkv"]
             _lib.check(L.rwkv_sb6_gemv_fused(p(bf["xrkv"]), N, p(q[0]), p(q[1]), p(q[2]), p(bf["y_rkv"]), q[3], q[4],
                                              self.xbits, D, s))
-            wdt = _dt(lay["wcat"])
-            _lib.check(L.rwkv_x070_lora_in(p(bf["xrkv"]), p(bf["xwag"]), p(lay["wcat"]), wdt, rw, ra, rv, rg,
-                                           int(l > 0), p(bf["la"]), N, D, s))
-            Bm = lay["B"]
-            _lib.check(L.rwkv_x070_tmix_core(p(bf["y_rkv"]), p(bf["la"]), p(Bm[0]), p(Bm[1]), p(Bm[2]), p(Bm[3]), wdt,
-                                             rw, ra, rv, rg, p(lay["bias"][0]), p(lay["bias"][1]), p(lay["bias"][2]),
-                                             p(lay["k_k"]), p(lay["k_a"]), p(lay["r_k"]), p(lay["lnx"][0]),
-                                             p(lay["lnx"][1]), p(state.v_first), int(l == 0), p(state.wkv[l]),
-                                             p(bf["tout"]), N, H, LNX_EPS, s))
+            self._tmix_core(l, lay, state, bf, N, s)
             self._gemv(f"blocks.{l}.att.output.weight", bf["tout"], x, 1, N, s)
             _lib.check(L.rwkv_x070_shift_mix(p(x), p(lay["ln2"][0]), p(lay["ln2"][1]), p(state.cmix_prev[l]),
                                              p(lay["ck"]), 1, p(bf["xk"]), None, N, D, LN_EPS, s))
@@ -187,6 +178,22 @@ class X070Decoder:
                                      N, D, LN_EPS, s))
         self._gemv("head.weight", bf["xo"], bf["logits"], 0, N, s)
         return bf["logits"]
+
+    def launches_per_token(self, N: int = 1) -> int:
+        return 8 * self.L + 3
+
+    def _tmix_core(self, l, lay, state, bf, N, s):
+        L, p = _lib.lib(), (lambda t: t.data_ptr())
+        rw, ra, rv, rg = self.ranks
+        wdt = _dt(lay["wcat"])
+        _lib.check(L.rwkv_x070_lora_in(p(bf["xmix"]), p(lay["wcat"]), wdt, rw, ra, rv, rg, int(l > 0), p(bf["la"]),
+                                       N, self.D, s))
+        Bm = lay["B"]
+        _lib.check(L.rwkv_x070_tmix_core(p(bf["y_rkv"]), p(bf["la"]), p(Bm[0]), p(Bm[1]), p(Bm[2]), p(Bm[3]), wdt,
+                                         rw, ra, rv, rg, p(lay["bias"][0]), p(lay["bias"][1]), p(lay["bias"][2]),
+                                         p(lay["k_k"]), p(lay["k_a"]), p(lay["r_k"]), p(lay["lnx"][0]),
+                                         p(lay["lnx"][1]), p(state.v_first), int(l == 0), p(state.wkv[l]),
+                                         p(bf["tout"]), N, self.H, LNX_EPS, s))
 
     def _gemv(self, key, x, y, ep, N, s):
         q = self.proj[key]
@@ -201,4 +208,3 @@ class X070Decoder:
             ids = torch.tensor(np.asarray(ids, np.int32).reshape(-1), device=self.device)
         return self.launch(ids.to(device=self.device, dtype=torch.int32).reshape(-1), state).clone()
 
-    launches_per_layer = 8

@@ -95,7 +95,7 @@ def test_shift_mix(nc):
     coef = rng.uniform(0, 1, (nc, D)).astype(np.float32)
     prev_d = dev(prev)
     out0 = torch.empty((N, min(nc, 3), D), device=DEV)
-    out1 = torch.empty((N, 3, D), device=DEV) if nc == 6 else None
+    out1 = torch.empty((N, 4, D), device=DEV) if nc == 6 else None
     xd, wd, bd, cd = dev(x), dev(w), dev(b), dev(coef)
     _lib.call("rwkv_x070_shift_mix", xd.data_ptr(), wd.data_ptr(), bd.data_ptr(), prev_d.data_ptr(),
               cd.data_ptr(), nc, out0.data_ptr(), out1.data_ptr() if out1 is not None else None, N, D, LN_EPS,
@@ -103,9 +103,14 @@ def test_shift_mix(nc):
     xl = X.layer_norm(x, w, b)
     mix, new_prev = X.shift_mix(xl, prev, list(coef))
     assert rel(new_prev, prev_d.cpu().numpy()) < 1e-5
-    got = out0.cpu().numpy() if nc == 1 else np.concatenate([out0.cpu().numpy(), out1.cpu().numpy()], 1)
-    for c in range(nc):
+    # coefficients r, k, v, w, a, g: out0 ← (r, k, v), out1 ← (w, a, v, g)
+    got = out0.cpu().numpy()
+    for c in range(min(nc, 3)):
         assert rel(mix[c], got[:, c]) < 1e-5, c
+    if nc == 6:
+        g1 = out1.cpu().numpy()
+        for slot, c in enumerate((3, 4, 2, 5)):
+            assert rel(mix[c], g1[:, slot]) < 1e-5, (slot, c)
 
 
 def _fp16_ulp_close(ref, got):
@@ -124,16 +129,15 @@ def test_lora_in(tiny, l, wdt):
         p[t + nm + "_lora_A.weight"] = p[t + nm + "_lora_A.weight"].astype(wdt)
     rng = np.random.default_rng(l)
     N, D = 2, TINY.n_embd
-    xrkv = rng.standard_normal((N, 3, D)).astype(np.float32)
-    xwag = rng.standard_normal((N, 3, D)).astype(np.float32)
+    xmix = rng.standard_normal((N, 4, D)).astype(np.float32)   # w, a, v, g inputs
     rw, ra, rv, rg = syn.lora_ranks(D)
     wcat = np.concatenate([p[t + nm + "_lora_A.weight"] for nm in "wavg"])
     la = torch.full((N, rw + ra + rv + rg), 7.0, device=DEV)
-    xr_d, xw_d, wc_d = dev(xrkv), dev(xwag), dev(wcat)
-    _lib.call("rwkv_x070_lora_in", xr_d.data_ptr(), xw_d.data_ptr(), wc_d.data_ptr(),
-              _lib.F16 if wdt == np.float16 else _lib.F32, rw, ra, rv, rg, int(l > 0), la.data_ptr(), N, D, None)
+    xm_d, wc_d = dev(xmix), dev(wcat)
+    _lib.call("rwkv_x070_lora_in", xm_d.data_ptr(), wc_d.data_ptr(), _lib.F16 if wdt == np.float16 else _lib.F32,
+              rw, ra, rv, rg, int(l > 0), la.data_ptr(), N, D, None)
     got = la.cpu().numpy()
-    ref = X.lora_in(p, l, xwag[:, 0], xwag[:, 1], xrkv[:, 2], xwag[:, 2])
+    ref = X.lora_in(p, l, xmix[:, 0], xmix[:, 1], xmix[:, 2], xmix[:, 3])
     offs = np.cumsum([0, rw, ra, rv, rg])
     for i, r in enumerate(ref):
         g = got[:, offs[i]:offs[i + 1]]
@@ -224,13 +228,14 @@ def test_decode_steps_match_oracle(tiny, decoder, N):
     assert c["x070"] == 4 * (2 + 4 * Lr)          # ln0 + ln_out + 4 per layer
     assert c["sb6_gemv"] == 4 * (3 * Lr + 1)      # o_proj, ffn key, ffn value, head
     assert c["sb6_fused"] == 4 * Lr               # r/k/v
+    assert decoder.launches_per_token(N) == 8 * Lr + 3
 
 
-def test_decode_graph_replay_bitwise(tiny, decoder):
-    case("decode graph replay")
-    N = 2
+@pytest.mark.parametrize("N", [1, 2])
+def test_decode_graph_replay_bitwise(tiny, decoder, N):
+    case(f"decode graph replay N={N}")
     st = decoder.new_state(N)
-    ids = torch.tensor([3, 400], dtype=torch.int32, device=DEV)
+    ids = torch.tensor([3, 400][:N], dtype=torch.int32, device=DEV)
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         decoder.launch(ids, st)   # one token so the state is not zero
