@@ -41,10 +41,10 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per launch of the head GEMV from two rocprofv3 counter passes
 # (FETCH_SIZE, WRITE_SIZE) over `bench.py --mode kernels`, calibrated against a
 # 256 MiB device copy; see profiles/hbm_traffic_decode_gemv_and_wkv7.md.
-HEAD_GEMV_TRAFFIC_BYTES = 29447562
+HEAD_GEMV_TRAFFIC_BYTES = 29440395
 # The same for the average GEMV launch of one 0.1B decode token (eager tokens
 # over rotated weight copies); same profile.
-DECODE_GEMV_TRAFFIC_BYTES = 1729325
+DECODE_GEMV_TRAFFIC_BYTES = 1721907
 VALU_PEAK_TFLOPS = 157.3
 
 
@@ -62,7 +62,7 @@ def parse():
     p.add_argument("--skip-wkv", action="store_true")
     p.add_argument("--skip-more", action="store_true", help="skip batched and 1.5B decode")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--mode", choices=["bench", "kernels"], default="bench",
+    p.add_argument("--mode", choices=["bench", "kernels", "e2e"], default="bench",
                    help="kernels: run each dominant kernel alone (for rocprofv3 counter passes)")
     return p.parse_args()
 
@@ -682,6 +682,21 @@ def profile_kernels(dev, tokens=12):
     log("kernels done")
 
 
+def profile_x070(dev, tokens=20):
+    """End-to-end x070 decode tokens (HIP graph replays) of the 0.1B and
+    7B-class shapes, batch 1, for kernel traces."""
+    import torch
+    from swiftrwkv_amd import synthetic as syn
+
+    nthreads = min(16, os.cpu_count() or 1)
+    for shape in (syn.X070_0B1, syn.X070_7B):
+        model = DecodeModel(shape, 1, dev, nthreads=nthreads, share_layers=shape is syn.X070_7B)
+        wall, _, launches = run_x070(model, dev, tokens, 2)
+        log(f"x070 decode {shape.name}: {wall * 1e3 / tokens:.3f} ms per token, {launches} launches")
+        del model
+        torch.cuda.empty_cache()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -696,6 +711,9 @@ def main():
     log(f"device {torch.cuda.get_device_name(0)}")
     if args.mode == "kernels":
         profile_kernels(dev)
+        return
+    if args.mode == "e2e":
+        profile_x070(dev)
         return
     model, step, wall, gpu_ms = bench_decode(args, dev)
     gemv_bytes, gemv_avg_ms, n_gemv = bench_decode_gemv(model, step, dev)
