@@ -58,6 +58,19 @@ class UnsupportedKind(RwkvqError):
         super().__init__(f"{tensor}: {kind}")
 
 
+class PartialExport(RwkvqError):
+    """RwkvqError.partialExport: the file holds only compressed projections,
+    no dense model body (X070Backbone load(fromSidecar:))."""
+
+    def __init__(self, tensors: int):
+        self.tensors = tensors
+        super().__init__(f"partial export: {tensors} tensors, none of them dense")
+
+
+class IncompleteManifest(RwkvqError):
+    """RwkvqFullConvertError.incompleteManifest (RwkvqFullConvert.swift:31-39)."""
+
+
 class RwkvqKind(str, enum.Enum):
     """RwkvqKind (RwkvqSidecar.swift:60-67)."""
     sb6 = "sb6"
@@ -712,6 +725,59 @@ class RwkvqSidecar:
         if info.outlier_count > 0:
             raise UnsupportedKind(key, "rtn+outliers (SpQR scatter not implemented)")
         return rwkvq_dequant_rtn(codes, scale, dtype)
+
+    def build_dense_weights(self, dtype=torch.float16) -> Dict[str, torch.Tensor]:
+        """The x070 dictionary of everything but the quantised projections
+        (RwkvqSidecar.buildDenseWeights, RwkvqFullConvert.swift:49-140): layer
+        norms, token-shift coefficients, k_k / k_a / r_k as [H, S], the
+        low-rank branches in the Linear convention (A [rank, D], B [D, rank];
+        a tensor whose manifest says `transposed` is turned, and the shape is
+        checked), w0 / a0 / v0 flattened into the B biases, the v branch only
+        for layers > 0, ln_x and the cmix coefficient; plus `emb.weight`
+        dequantised once (load(fromSidecar:), X070Backbone.swift)."""
+        if not (self.n_layer > 0 and self.n_embd > 0 and self.head_size > 0):
+            raise IncompleteManifest("n_layer / n_embd / head_size missing or zero: the manifest does not describe "
+                                     "the model")
+        if not any(t.kind == RwkvqKind.dense for t in self.tensors.values()):
+            raise PartialExport(len(self.tensors))
+        D, S = self.n_embd, self.head_size
+        H = D // S
+        dq = lambda k: self.dequantize(k, dtype)
+
+        def low_rank(k: str, is_a: bool) -> torch.Tensor:
+            info = self.tensors.get(k)
+            if info is None:
+                raise MissingBuffer(k, "manifest")
+            v = dq(k)
+            if info.transposed:
+                v = v.t().contiguous()
+            if v.dim() != 2 or v.shape[1 if is_a else 0] != D:
+                raise ShapeMismatch(k, [-1, D] if is_a else [D, -1], list(v.shape))
+            return v
+
+        out = {"ln0.weight": dq("blocks.0.ln0.weight"), "ln0.bias": dq("blocks.0.ln0.bias"),
+               "ln_out.weight": dq("ln_out.weight"), "ln_out.bias": dq("ln_out.bias")}
+        for i in range(self.n_layer):
+            b = f"blocks.{i}."
+            att, ffn, P = b + "att.", b + "ffn.", b + "tmix."
+            for n in ("ln1", "ln2"):
+                out[b + n + ".weight"] = dq(b + n + ".weight")
+                out[b + n + ".bias"] = dq(b + n + ".bias")
+            for x in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g"):
+                out[P + x] = dq(att + x)
+            for x in ("k_k", "k_a", "r_k"):
+                out[P + x] = dq(att + x).reshape(H, S)
+            branches = [("w", True), ("a", True), ("g", False)] + ([("v", True)] if i > 0 else [])
+            for n, bias in branches:
+                out[P + n + "_lora_A.weight"] = low_rank(att + n + "1", True)
+                out[P + n + "_lora_B.weight"] = low_rank(att + n + "2", False)
+                if bias:
+                    out[P + n + "_lora_B.bias"] = dq(att + n + "0").reshape(D)
+            out[P + "ln_x.weight"] = dq(att + "ln_x.weight")
+            out[P + "ln_x.bias"] = dq(att + "ln_x.bias")
+            out[b + "cmix.x_k"] = dq(ffn + "x_k")
+        out["emb.weight"] = dq("emb.weight")
+        return out
 
     def sym_row_table(self, key: str) -> Optional[RwkvqSymRowTable]:
         """RwkvqSymRows.swift:70-80: a row table for an 8-bit sym tensor, None

@@ -18,6 +18,7 @@ narrowing of :248-253).  There is no CPU fallback: a missing library raises.
 """
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import Dict, Optional, Tuple
 
 import numpy as np
@@ -69,68 +70,155 @@ def _dt(t: torch.Tensor) -> int:
     raise TypeError(f"low-rank matrices must be fp16 or fp32, got {t.dtype}")
 
 
+@dataclass
+class Proj:
+    """A projection on the device: kind "sb6" (K3 qblk, qsqm, ddm; xbits),
+    "sym" (qblk, qs, d; bits) or "dense" (w [OUT, IN] fp32).  out_per < OUT:
+    a row-concatenated group whose row o uses input row o // out_per."""
+    kind: str
+    bufs: Tuple[torch.Tensor, ...]
+    OUT: int
+    IN: int
+    bits: int = 4
+    xbits: int = 0
+    out_per: int = 0
+
+    def __post_init__(self):
+        if self.out_per == 0:
+            self.out_per = self.OUT
+
+
 class X070Decoder:
-    """Device-resident x070 model (sb6 projections in K3 layout + dense
-    parameters) and its one-token step.
+    """Device-resident x070 model (quantised projections + dense parameters)
+    and its one-token step.
 
-    dense: the `gg` parameters by name (numpy; see synthetic.x070_dense_params
-    for the names); proj: key → (qblk, qsqm, ddm, OUT, IN) K3 buffers of every
-    projection (X070Shape.projections names, sb6 4-bit)."""
+    dense: the `gg` parameters by the reference's x070 names
+    (RwkvqSidecar.buildDenseWeights' dictionary; numpy arrays or tensors);
+    proj: world key (X070Shape.projections names) → Proj, or an sb6
+    (qblk, qsqm, ddm, OUT, IN) tuple of K3 buffers (xbits from `xbits`).
+    The r/k/v projections of a layer run as one fused GEMV when they share
+    kind and format."""
 
-    def __init__(self, n_layer: int, n_embd: int, ffn: int, vocab: int, dense: Dict[str, np.ndarray],
-                 proj: Dict[str, Tuple], device, xbits: int = 0):
+    def __init__(self, n_layer: int, n_embd: int, ffn: int, vocab: int, dense: Dict[str, object],
+                 proj: Dict[str, object], device, xbits: int = 0):
         self.L, self.D, self.F, self.V = n_layer, n_embd, ffn, vocab
         self.H = n_embd // HEAD
-        self.xbits = xbits
         self.device = torch.empty(0, device=device).device   # concrete index (cuda → cuda:N)
         dev = self.device
-        f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
-        keep = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-        self.emb = keep(dense["emb.weight"])
-        if self.emb.dtype not in (torch.float16, torch.float32):
-            raise TypeError("emb.weight must be fp16 or fp32")
+
+        def tens(a) -> torch.Tensor:
+            return a if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a))
+
+        f32 = lambda a: tens(a).to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+
+        def lowrank(a) -> torch.Tensor:
+            t = tens(a).to(dev).contiguous()
+            if t.dtype not in (torch.float16, torch.float32):
+                raise TypeError(f"low-rank matrices must be fp16 or fp32, got {t.dtype}")
+            return t
+
+        emb = tens(dense["emb.weight"]).to(dev)
+        self.emb = emb.contiguous() if emb.dtype in (torch.float16, torch.float32) else emb.float().contiguous()
         self.ln0 = (f32(dense["ln0.weight"]), f32(dense["ln0.bias"]))
         self.ln_out = (f32(dense["ln_out.weight"]), f32(dense["ln_out.bias"]))
+        def rank_of(l, nm):
+            k = f"blocks.{l}.tmix.{nm}_lora_A.weight"
+            return int(tens(dense[k]).shape[0]) if k in dense else None
+
+        # layer 0 has no value-residual branch (RwkvqFullConvert.swift:20-25); its
+        # slot in the low-rank buffers keeps the model's v rank, never read
+        rv = next((r for r in (rank_of(l, "v") for l in range(n_layer)) if r), 8)
+        ranks = (rank_of(0, "w"), rank_of(0, "a"), rv, rank_of(0, "g"))
         self.layers = []
-        ranks = None
         for l in range(n_layer):
             b, t = f"blocks.{l}.", f"blocks.{l}.tmix."
-            A = [dense[t + nm + "_lora_A.weight"] for nm in "wavg"]
-            r = tuple(int(a.shape[0]) for a in A)
-            ranks = ranks or r
-            if r != ranks:
-                raise ValueError("low-rank sizes differ between layers")
+            has_v = t + "v_lora_A.weight" in dense
+            if l > 0 and not has_v:
+                raise KeyError(f"{t}v_lora_A.weight: layers above 0 need the value-residual branch")
+            A = [lowrank(dense[t + nm + "_lora_A.weight"]) for nm in "wag"]
+            dt = A[0].dtype
+            A.insert(2, lowrank(dense[t + "v_lora_A.weight"]) if has_v else
+                     torch.zeros((rv, n_embd), dtype=dt, device=dev))
+            B = [lowrank(dense[t + nm + "_lora_B.weight"]) for nm in "wag"]
+            B.insert(2, lowrank(dense[t + "v_lora_B.weight"]) if has_v else
+                     torch.zeros((n_embd, rv), dtype=dt, device=dev))
+            if tuple(int(x.shape[0]) for x in A) != ranks or any(int(m.shape[1]) != r for m, r in zip(B, ranks)):
+                raise ValueError(f"layer {l}: low-rank sizes differ from layer 0's {ranks}")
             lay = {
                 "ln1": (f32(dense[b + "ln1.weight"]), f32(dense[b + "ln1.bias"])),
                 "ln2": (f32(dense[b + "ln2.weight"]), f32(dense[b + "ln2.bias"])),
-                "coef6": f32(np.stack([dense[t + "x_" + c] for c in _COEF_ORDER])),
+                "coef6": torch.stack([f32(dense[t + "x_" + c]) for c in _COEF_ORDER]).contiguous(),
                 "ck": f32(dense[b + "cmix.x_k"]),
-                "wcat": keep(np.concatenate(A, 0)),
-                "B": [keep(dense[t + nm + "_lora_B.weight"]) for nm in "wavg"],
-                "bias": [f32(dense[t + nm + "_lora_B.bias"]) for nm in "wav"],
+                "wcat": torch.cat(A, 0).contiguous(),
+                "B": B,
+                "bias": [f32(dense[t + "w_lora_B.bias"]), f32(dense[t + "a_lora_B.bias"]),
+                         f32(dense[t + "v_lora_B.bias"]) if has_v else torch.zeros(n_embd, device=dev)],
                 "k_k": f32(dense[t + "k_k"]), "k_a": f32(dense[t + "k_a"]), "r_k": f32(dense[t + "r_k"]),
                 "lnx": (f32(dense[t + "ln_x.weight"]), f32(dense[t + "ln_x.bias"])),
             }
-            dts = {lay["wcat"].dtype} | {m.dtype for m in lay["B"]}
-            if len(dts) != 1:
+            if len({lay["wcat"].dtype} | {m.dtype for m in B}) != 1:
                 raise TypeError("low-rank matrices of a layer must share one dtype")
             self.layers.append(lay)
         self.ranks = ranks
-        self.proj = {}
+        self.proj: Dict[str, object] = {}
+        as_proj = lambda v: v if isinstance(v, Proj) else self._sb6(v, xbits)
         for l in range(n_layer):
             keys = [f"blocks.{l}.att.{m}.weight" for m in ("receptance", "key", "value")]
-            self.proj[f"blocks.{l}.att.rkv"] = self._k3([proj[k] for k in keys])
+            self.proj[f"blocks.{l}.att.rkv"] = self._group([as_proj(proj[k]) for k in keys])
             for k in (f"blocks.{l}.att.output.weight", f"blocks.{l}.ffn.key.weight", f"blocks.{l}.ffn.value.weight"):
-                self.proj[k] = self._k3([proj[k]])
-        self.proj["head.weight"] = self._k3([proj["head.weight"]])
+                self.proj[k] = as_proj(proj[k])
+        self.proj["head.weight"] = as_proj(proj["head.weight"])
         self._bufs: Optional[dict] = None
+        self._tmp: Dict[tuple, torch.Tensor] = {}
 
-    def _k3(self, parts):
+    @classmethod
+    def from_sidecar(cls, sc, device=None, param_dtype=torch.float16) -> "X070Decoder":
+        """X070Backbone.load(fromSidecar:) (RwkvqStandaloneLoad.swift:164-194)
+        for decoding: the dense body from RwkvqSidecar.build_dense_weights and
+        every projection kept in its file layout (sb6 K3 / sym on the GEMV;
+        other kinds dequantised once to fp32)."""
+        from .quant import RwkvqKind
+
+        device = device or next(iter(sc.arrays.values())).device
+        dense = sc.build_dense_weights(param_dtype)
+        keys = [f"blocks.{l}.att.{m}.weight" for l in range(sc.n_layer)
+                for m in ("receptance", "key", "value", "output")]
+        keys += [f"blocks.{l}.ffn.{m}.weight" for l in range(sc.n_layer) for m in ("key", "value")]
+        keys.append("head.weight")
+        proj = {}
+        for k in keys:
+            info = sc.tensors.get(k)
+            if info is None:
+                from .quant import MissingBuffer
+                raise MissingBuffer(k, "manifest")
+            OUT, IN = info.out_features, info.in_features
+            if info.kind == RwkvqKind.sb6:
+                proj[k] = Proj("sb6", tuple(sc.arrays[f"{k}::{f}"] for f in ("qblk", "qsqm", "ddm")), OUT, IN,
+                               bits=info.bits, xbits=info.xbits)
+            elif info.kind == RwkvqKind.sym:
+                proj[k] = Proj("sym", tuple(sc.arrays[f"{k}::{f}"] for f in ("qblk", "qs", "d")), OUT, IN,
+                               bits=info.bits)
+            else:
+                proj[k] = Proj("dense", (sc.dequantize(k, torch.float32).contiguous(),), OUT, IN)
+        ffn = sc.tensors["blocks.0.ffn.key.weight"].out_features
+        return cls(sc.n_layer, sc.n_embd, ffn, sc.vocab_size, dense, proj, device)
+
+    def _sb6(self, t, xbits) -> Proj:
         dev = self.device
-        return (torch.from_numpy(np.concatenate([p[0] for p in parts])).to(dev),
-                torch.from_numpy(np.concatenate([p[1] for p in parts])).to(dev),
-                torch.from_numpy(np.concatenate([p[2] for p in parts]).view(np.uint16)).to(dev),
-                sum(p[3] for p in parts), parts[0][4])
+        tt = lambda a: (a if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a))).to(dev)
+        ddm = t[2] if isinstance(t[2], torch.Tensor) else np.ascontiguousarray(t[2]).view(np.uint16)
+        return Proj("sb6", (tt(t[0]), tt(t[1]), tt(ddm)), int(t[3]), int(t[4]), bits=4 + xbits, xbits=xbits)
+
+    @staticmethod
+    def _group(parts):
+        """One fused Proj when the members share kind and format, else the list."""
+        p0 = parts[0]
+        same = all(p.kind == p0.kind and p.bits == p0.bits and p.xbits == p0.xbits and p.OUT == p0.OUT
+                   and p.IN == p0.IN for p in parts)
+        if same and p0.kind in ("sb6", "sym"):
+            bufs = tuple(torch.cat([p.bufs[i] for p in parts], 0).contiguous() for i in range(3))
+            return Proj(p0.kind, bufs, p0.OUT * len(parts), p0.IN, bits=p0.bits, xbits=p0.xbits, out_per=p0.OUT)
+        return list(parts)
 
     def new_state(self, n_rows: int) -> RWKVState:
         return RWKVState(self.L, n_rows, self.D, self.device)
@@ -165,9 +253,7 @@ class X070Decoder:
         for l, lay in enumerate(self.layers):
             _lib.check(L.rwkv_x070_shift_mix(p(x), p(lay["ln1"][0]), p(lay["ln1"][1]), p(state.tmix_prev[l]),
                                              p(lay["coef6"]), 6, p(bf["xrkv"]), p(bf["xmix"]), N, D, LN_EPS, s))
-            q = self.proj[f"blocks.{l}.att.rkv"]
-            _lib.check(L.rwkv_sb6_gemv_fused(p(bf["xrkv"]), N, p(q[0]), p(q[1]), p(q[2]), p(bf["y_rkv"]), q[3], q[4],
-                                             self.xbits, D, s))
+            self._rkv(l, bf, N, s)
             self._tmix_core(l, lay, state, bf, N, s)
             self._gemv(f"blocks.{l}.att.output.weight", bf["tout"], x, 1, N, s)
             _lib.check(L.rwkv_x070_shift_mix(p(x), p(lay["ln2"][0]), p(lay["ln2"][1]), p(state.cmix_prev[l]),
@@ -196,9 +282,63 @@ class X070Decoder:
                                          p(bf["tout"]), N, self.H, LNX_EPS, s))
 
     def _gemv(self, key, x, y, ep, N, s):
-        q = self.proj[key]
-        _lib.check(_lib.lib().rwkv_sb6_gemv_ep(x.data_ptr(), N, q[0].data_ptr(), q[1].data_ptr(), q[2].data_ptr(),
-                                               y.data_ptr(), q[3], q[4], self.xbits, ep, s))
+        self._run(self.proj[key], x, y, ep, N, s)
+
+    def _run(self, q: Proj, x: torch.Tensor, y: torch.Tensor, ep: int, N: int, s) -> None:
+        """y = ep(x · Wᵀ): ep 0 store, 1 add into y, 2 relu² (rwkv_*_gemv_ep)."""
+        L = _lib.lib()
+        if q.kind == "sb6":
+            if q.out_per < q.OUT:
+                if ep != 0:
+                    raise ValueError("a fused group stores its result (epilogue 0)")
+                _lib.check(L.rwkv_sb6_gemv_fused(x.data_ptr(), N, *[b.data_ptr() for b in q.bufs], y.data_ptr(),
+                                                 q.OUT, q.IN, q.xbits, q.out_per, s))
+            else:
+                _lib.check(L.rwkv_sb6_gemv_ep(x.data_ptr(), N, *[b.data_ptr() for b in q.bufs], y.data_ptr(),
+                                              q.OUT, q.IN, q.xbits, ep, s))
+        elif q.kind == "sym":
+            if q.out_per < q.OUT:
+                if ep != 0:
+                    raise ValueError("a fused group stores its result (epilogue 0)")
+                _lib.check(L.rwkv_sym_gemv(x.data_ptr(), N, *[b.data_ptr() for b in q.bufs], y.data_ptr(),
+                                           q.OUT, q.IN, q.bits, q.out_per, s))
+            else:
+                _lib.check(L.rwkv_sym_gemv_ep(x.data_ptr(), N, *[b.data_ptr() for b in q.bufs], y.data_ptr(),
+                                              q.OUT, q.IN, q.bits, ep, s))
+        else:   # dense: the library GEMM on torch's current stream
+            if s != torch.cuda.current_stream(self.device).cuda_stream:
+                raise ValueError("dense projections run on the current stream only")
+            tmp = self._tmp.get((id(q), N))
+            if tmp is None:
+                tmp = self._tmp[(id(q), N)] = torch.empty((N, q.OUT), dtype=torch.float32, device=self.device)
+            torch.mm(x.reshape(N, q.IN), q.bufs[0].t(), out=tmp)
+            yv = y.reshape(N, q.OUT)
+            if ep == 1:
+                yv.add_(tmp)
+            elif ep == 2:
+                torch.relu_(tmp)
+                yv.copy_(tmp.square_())
+            else:
+                yv.copy_(tmp)
+
+    def _rkv(self, l, bf, N, s):
+        """r / k / v projections of layer l into y_rkv [N, 3D]: one fused GEMV,
+        or the three matrices one by one (through contiguous staging rows
+        when N > 1)."""
+        q = self.proj[f"blocks.{l}.att.rkv"]
+        if isinstance(q, Proj):
+            self._run(q, bf["xrkv"], bf["y_rkv"], 0, N, s)
+            return
+        D = self.D
+        for k, qk in enumerate(q):
+            if N == 1:
+                self._run(qk, bf["xrkv"][0, k], bf["y_rkv"][0, k * D:(k + 1) * D], 0, 1, s)
+            else:
+                xi = self._tmp.setdefault(("rkv_x", N), torch.empty((N, D), device=self.device))
+                yi = self._tmp.setdefault(("rkv_y", N), torch.empty((N, D), device=self.device))
+                xi.copy_(bf["xrkv"][:, k])
+                self._run(qk, xi, yi, 0, N, s)
+                bf["y_rkv"][:, k * D:(k + 1) * D].copy_(yi)
 
     def step(self, ids, state: RWKVState) -> torch.Tensor:
         """X070Backbone.step (X070Generation.swift:437-474): token ids [N]

@@ -284,3 +284,36 @@ def test_decode_0b1_shape_matches_oracle(proj_0b1, lora):
         err = rel(ref, got)
         print(f"[x070] 0.1B low-rank {lora} token {t}: rel {err:.3e}", flush=True)
         assert err < tol, t
+
+
+def test_decoder_from_rwkvq_file(tmp_path, orc):
+    """A full .rwkvq export (world naming, dense body) with mixed projection
+    kinds: layer 0 r/k/v sb6 (one fused sb6 GEMV), o_proj dense (as current
+    presets store it), layer 1 r/k/v sym 8-bit (one fused sym GEMV), sym
+    ffn, sym head; decoded through X070Decoder.from_sidecar against the oracle
+    on the matrices dequantised from the disk buffers."""
+    from swiftrwkv_amd import quant as Q
+    from tests.test_x070_oracle import file_projections, world_file
+    case("decoder from .rwkvq file, mixed kinds")
+    p = syn.x070_dense_params(TINY, seed=9)
+    kinds = {"blocks.0.att.output.weight": "dense", "head.weight": "sym8"}
+    kinds.update({f"blocks.1.att.{m}.weight": "sym8" for m in ("receptance", "key", "value")})
+    kinds.update({f"blocks.1.ffn.{m}.weight": "sym8" for m in ("key", "value")})
+    path = str(tmp_path / "tiny.rwkvq")
+    T = world_file(path, TINY, p, kinds)
+    sc = Q.RwkvqSidecar.from_rwkvq(path)
+    dec = X070Decoder.from_sidecar(sc)
+    from swiftrwkv_amd.x070 import Proj
+    assert isinstance(dec.proj["blocks.0.att.rkv"], Proj) and dec.proj["blocks.0.att.rkv"].kind == "sb6"
+    assert isinstance(dec.proj["blocks.1.att.rkv"], Proj) and dec.proj["blocks.1.att.rkv"].kind == "sym"
+    assert dec.proj["blocks.0.att.output.weight"].kind == "dense"
+    W = file_projections(orc, T, TINY)
+    for N in (1, 2):
+        st = dec.new_state(N)
+        ost = X.State.zeros(TINY.n_layer, N, TINY.n_head)
+        rng = np.random.default_rng(N)
+        for t in range(3):
+            ids = rng.integers(0, TINY.vocab, N).astype(np.int32)
+            got = dec.step(ids, st).cpu().numpy()
+            ref = X.step(p, W, ids, ost, TINY.n_layer, TINY.n_head)
+            assert rel(ref, got) < 1e-4, (N, t)

@@ -93,3 +93,109 @@ def test_rows_are_independent(tiny):
         for t, ids in enumerate(([1, 2], [3, 4])):
             one = X.step(p, W, [ids[row]], st1, TINY.n_layer, TINY.n_head)
             np.testing.assert_allclose(one[0], two[t][row], rtol=0, atol=1e-12 * np.abs(one).max())
+
+
+# ───────────── a full .rwkvq export (world naming) and its dense body ─────────────
+
+def world_file(path, shape, p, kinds, nthreads=4):
+    """Write x070 parameters `p` (x070 names, flat vectors) as a full .rwkvq
+    export in world naming: dense body as the reference's converter reads it
+    (token-shift and k_k / k_a / r_k vectors [1, 1, D], w0 / a0 / v0 [1, 1, D],
+    low-rank matrices raw [in, out] with `transposed` on layer 0 and Linear
+    [out, in] on the others), projections encoded per `kinds` (world key →
+    "sb6" / "sym8" / "dense"), the embedding dense fp16."""
+    from swiftrwkv_amd import quant as Q
+    D = shape.n_embd
+    T = {}
+    dense = lambda a, **m: ({"kind": "dense", "shape": list(np.shape(a)), **m},
+                            {"dense": np.ascontiguousarray(a, np.float16)})
+    vec = lambda a: dense(np.asarray(a).reshape(1, 1, D))
+    T["blocks.0.ln0.weight"], T["blocks.0.ln0.bias"] = dense(p["ln0.weight"]), dense(p["ln0.bias"])
+    T["ln_out.weight"], T["ln_out.bias"] = dense(p["ln_out.weight"]), dense(p["ln_out.bias"])
+    T["emb.weight"] = dense(p["emb.weight"])
+    for l in range(shape.n_layer):
+        b, t = f"blocks.{l}.", f"blocks.{l}.tmix."
+        att = b + "att."
+        for n in ("ln1", "ln2"):
+            T[b + n + ".weight"], T[b + n + ".bias"] = dense(p[b + n + ".weight"]), dense(p[b + n + ".bias"])
+        for c in "rwkvag":
+            T[att + "x_" + c] = vec(p[t + "x_" + c])
+        for c in ("k_k", "k_a", "r_k"):
+            T[att + c] = vec(p[t + c])
+        for nm in "wavg":
+            A, B = p[t + nm + "_lora_A.weight"], p[t + nm + "_lora_B.weight"]
+            if l == 0:   # raw world orientation, [in, out]
+                T[att + nm + "1"] = dense(A.T, transposed=True)
+                T[att + nm + "2"] = dense(B.T, transposed=True)
+            else:
+                T[att + nm + "1"] = dense(A, transposed=False)
+                T[att + nm + "2"] = dense(B, transposed=False)
+            if nm != "g":
+                T[att + nm + "0"] = vec(p[t + nm + "_lora_B.bias"])
+        T[att + "ln_x.weight"], T[att + "ln_x.bias"] = dense(p[t + "ln_x.weight"]), dense(p[t + "ln_x.bias"])
+        T[b + "ffn.x_k"] = vec(p[b + "cmix.x_k"])
+    for idx, (key, OUT, IN) in enumerate(shape.projections()):
+        w = (np.random.default_rng(500 + idx).standard_normal((OUT, IN)) * 0.02).astype(np.float32)
+        k = kinds.get(key, "sb6")
+        if k == "sb6":
+            T[key] = Q.sb6_entry(w, 4, nthreads)
+        elif k == "sym8":
+            T[key] = Q.sym_entry(w, 8, nthreads)
+        else:
+            T[key] = dense(w)
+    Q.write_rwkvq(path, T, n_layer=shape.n_layer, n_embd=D, vocab_size=shape.vocab)
+    return T
+
+
+def test_build_dense_weights_round_trip(tmp_path):
+    from swiftrwkv_amd import quant as Q
+    p = syn.x070_dense_params(TINY, seed=9)
+    path = str(tmp_path / "tiny.rwkvq")
+    world_file(path, TINY, p, {})
+    sc = Q.RwkvqSidecar.from_rwkvq(path, device="cpu")
+    got = sc.build_dense_weights(torch.float16)
+    H = TINY.n_head
+    for k, v in p.items():
+        if ".v_lora_" in k and k.startswith("blocks.0."):
+            assert k not in got, k   # layer 0 has no value-residual branch
+            continue
+        g = got[k].numpy()
+        want = np.asarray(v).astype(np.float16)
+        if k.endswith(("k_k", "k_a", "r_k")):
+            want = want.reshape(H, 64)
+        elif k.split(".")[-1].startswith("x_"):
+            want = want.reshape(1, 1, -1)
+        assert g.shape == want.shape, k
+        np.testing.assert_array_equal(g, want, err_msg=k)
+    assert set(got) == {k for k in p if not (".v_lora_" in k and k.startswith("blocks.0."))}
+
+
+def test_build_dense_weights_refusals(tmp_path):
+    from swiftrwkv_amd import quant as Q
+    path = str(tmp_path / "partial.rwkvq")
+    w = (np.random.default_rng(0).standard_normal((256, 256)) * 0.02).astype(np.float32)
+    Q.write_rwkvq(path, {"blocks.0.att.key.weight": Q.sb6_entry(w, 4, 4)}, n_layer=1, n_embd=256, vocab_size=512)
+    with pytest.raises(Q.PartialExport):
+        Q.RwkvqSidecar.from_rwkvq(path, device="cpu").build_dense_weights()
+    path2 = str(tmp_path / "nolayers.rwkvq")
+    Q.write_rwkvq(path2, {"ln_out.weight": ({"kind": "dense", "shape": [256]}, {"dense": np.ones(256, np.float16)})})
+    with pytest.raises(Q.IncompleteManifest):
+        Q.RwkvqSidecar.from_rwkvq(path2, device="cpu").build_dense_weights()
+
+
+def file_projections(orc, T, shape):
+    """fp64 dense matrices of the file's projections, dequantised by the
+    oracle from the disk buffers."""
+    W = {}
+    for key, OUT, IN in shape.projections():
+        m, f = T[key]
+        if m["kind"] == "sb6":
+            qblk, qsqm, ddm, xb = orc.sb6_to_k3(f["codes_packed"], f.get("gw_qh"), f.get("gw_qh2"), f["gw_qsqm"],
+                                                f["gw_d"].view(np.uint16), f["gw_dm"].view(np.uint16), OUT, IN)
+            W[key] = orc.sb6_dequant(qblk, qsqm, ddm, OUT, IN, xb).astype(np.float64)
+        elif m["kind"] == "sym":
+            W[key] = orc.sym_dequant(f["codes"].view(np.uint8), f["gw_qs"].view(np.uint8),
+                                     f["gw_d"].view(np.uint16), OUT, IN, 8).astype(np.float64)
+        else:
+            W[key] = f["dense"].astype(np.float64)
+    return W
