@@ -58,6 +58,30 @@ def test_status_strings_and_errors():
     assert st == 1
 
 
+def test_x070_step_entry_validation():
+    """The x070 decode-step entries reject bad arguments before any device work."""
+    lib, d = _lib.lib(), 8
+    F32, F16 = _lib.F32, _lib.F16
+    # layer norm: width not a multiple of 256, or a multiple of 1024 only above 4096; dtype f32/f16
+    assert lib.rwkv_layer_norm(d, F32, None, 0, d, d, d, 1, 300, 1e-5, None) == 1
+    assert lib.rwkv_layer_norm(d, F32, None, 0, d, d, d, 1, 4608, 1e-5, None) == 1
+    assert lib.rwkv_layer_norm(d, _lib.BF16, None, 0, d, d, d, 1, 768, 1e-5, None) == 2
+    assert lib.rwkv_layer_norm(d, F32, d, 0, d, d, d, 1, 768, 1e-5, None) == 1      # gather from no rows
+    assert lib.rwkv_layer_norm(None, F32, None, 0, None, None, None, 0, 768, 1e-5, None) == 0   # N = 0
+    # shift + lerps: 1 or 6 coefficients, out1 needed for 6
+    assert lib.rwkv_x070_shift_mix(d, d, d, d, d, 3, d, d, 1, 768, 1e-5, None) == 1
+    assert lib.rwkv_x070_shift_mix(d, d, d, d, d, 6, d, None, 1, 768, 1e-5, None) == 6
+    # low-rank: ranks multiples of 8, matrices f16/f32
+    assert lib.rwkv_x070_lora_in(d, d, F16, 60, 64, 32, 128, 1, d, 1, 768, None) == 1
+    assert lib.rwkv_x070_lora_in(d, d, _lib.BF16, 64, 64, 32, 128, 1, d, 1, 768, None) == 2
+    # tmix core: v branch buffers needed above layer 0
+    args = [d] * 6 + [F16, 64, 64, 32, 128] + [d, d, None] + [d] * 5 + [d, 0, d, d, 1, 12, 64e-5, None]
+    assert lib.rwkv_x070_tmix_core(*args) == 6
+    # GEMV epilogue code
+    assert lib.rwkv_sb6_gemv_ep(d, 1, d, d, d, d, 256, 256, 0, 3, None) == 1
+    assert lib.rwkv_sym_gemv_ep(d, 1, d, d, d, d, 256, 256, 8, -1, None) == 1
+
+
 def test_applies_tables_are_the_reference_ones():
     # RwkvqSb6GEMVTests.swift:80-100
     assert quant.rwkvq_sb6_gemv_config(65536, 2048, 0) == (4, 4)
