@@ -156,11 +156,17 @@ __device__ __forceinline__ void rowsum16_pair(float& x0, float& x1) {
 // leave the chip with fewer waves than SIMDs (1,024).
 __host__ __device__ constexpr bool use_rows4(int64_t BH) { return BH < 256; }
 
-// Sum over the wave, the same association in every lane.
+// Sum over the 64 lanes of a full wave, the same bits in every lane: within
+// each 16-lane DPP row the lanes 8, 4, 2 and 1 apart (row_ror; each lane's
+// partner pairs the same values, so the row's lanes agree), then across the
+// four rows (rowsum4).  DPP and lane swaps only — no LDS round trips.
 __device__ __forceinline__ float wave_total(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-    return __shfl(x, 0, 64);   // one lane's association for everybody
+    float t, u;
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0xf" : "=&v"(t) : "v"(x));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:4 row_mask:0xf bank_mask:0xf" : "=&v"(u) : "v"(t));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:2 row_mask:0xf bank_mask:0xf" : "=&v"(t) : "v"(u));
+    asm("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:1 row_mask:0xf bank_mask:0xf" : "=&v"(u) : "v"(t));
+    return rowsum4(u);
 }
 
 // ── decode: the T = 1 step of one head and the tmix tail ──
