@@ -331,13 +331,25 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_pair(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
+// v_l + v_(l^16) (v_l + v_(l^32)) from a lane swap across DPP rows (halves):
+// each lane adds the same two values, so the sum is the xor-partner add's.
+__device__ __forceinline__ float swap16_add(float v) {
+    float a = v, b = v;
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+__device__ __forceinline__ float swap32_add(float v) {
+    float a = v, b = v;
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
+}
 __device__ __forceinline__ float group_sum(float v, int G) {
     if (G >= 2) v += dpp_pair<0xB1>(v);    // quad_perm [1,0,3,2]
     if (G >= 4) v += dpp_pair<0x4E>(v);    // quad_perm [2,3,0,1]
     if (G >= 8) v += dpp_pair<0x141>(v);   // row_half_mirror
     if (G >= 16) v += dpp_pair<0x140>(v);  // row_mirror
-    if (G >= 32) v += __shfl_xor(v, 16, 64);
-    if (G >= 64) v += __shfl_xor(v, 32, 64);
+    if (G >= 32) v = swap16_add(v);        // lanes l, l ^ 16
+    if (G >= 64) v = swap32_add(v);        // lanes l, l ^ 32
     return v;
 }
 
