@@ -40,6 +40,20 @@ __device__ __forceinline__ float block_total(float v, float* red) {
 
 __device__ __forceinline__ float sum4(float4 a) { return (a.x + a.y) + (a.z + a.w); }
 
+// v + (v of the DPP partner lane); CTRL quad_perm / row_half_mirror.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf,
+                                                                       false));
+}
+// Sum over the 8 lanes 8j .. 8j+7 (lanes 1, 2 apart, then the other quad),
+// the same bits in each of them.
+__device__ __forceinline__ float sum8_lanes(float v) {
+    v = dpp_add<0xB1>(v);    // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E>(v);    // quad_perm [2,3,0,1]
+    return dpp_add<0x141>(v);   // row_half_mirror
+}
+
 // Row kernels: a row of D is split over S workgroups of T threads (S = D/1024
 // with T = 256 when 1024 divides D, else S = 1 with T = D/4); thread t of
 // slice s writes the float4 chunk s·T + t.  Every workgroup forms the row's
@@ -310,9 +324,7 @@ __global__ __launch_bounds__(R4 ? 1024 : 256) void tmix_core_kernel(CoreArgs A) 
         }
     };
     auto finish = [&](const Job& j, float acc) {
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
-        acc += __shfl_xor(acc, 4, 64);
+        acc = sum8_lanes(acc);
         if (sub == 0) {
             if constexpr (H16) acc = f16_round(acc);
             const int row = h * D + j.i;
