@@ -597,7 +597,11 @@ __global__ __launch_bounds__(512) void gemv_batch_kernel(const float* __restrict
     if constexpr (std::is_same_v<F, Sb6Fmt<0>>) {
         inv = __uint_as_float(0x7F000000u - __float_as_uint(__builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0]));
     }
-    const int rows = NT * NK;      // staged input rows: input nn, matrix k at nn·NK + k
+    // staged input rows: input nn, matrix k at nn·NK + k, or only the
+    // workgroup's own matrix kwg (one_k) at nn
+    const int NKs = geo.one_k ? 1 : NK;
+    const int kwg = geo.one_k ? (int)(blockIdx.x * geo.WPB * geo.R * RL) / out_per : 0;
+    const int rows = NT * NKs;
     const int CU = CP * geo.G;     // units per chunk
     const int XS = CU * 36;        // floats per staged row: units padded to 36 floats
     float* const sums = lds + rows * XS;   // [rows][CU][2]: Σ x of columns 0..15, 16..31
@@ -623,7 +627,7 @@ __global__ __launch_bounds__(512) void gemv_batch_kernel(const float* __restrict
                 f4 v[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const int j = min(j0 + e, N * NK - 1);
+                    const int j = NKs == 1 && NK > 1 ? min(j0 + e, N - 1) * NK + kwg : min(j0 + e, N * NK - 1);
                     v[e] = *reinterpret_cast<const f4*>(x + (int64_t)j * IN + u0 * 32 + c);
                 }
 #pragma unroll
@@ -675,7 +679,7 @@ __global__ __launch_bounds__(512) void gemv_batch_kernel(const float* __restrict
         // inputs' values live
         float xv[2][32], xs[2][2];
         auto read_x = [&](int nn, float (&v)[32], float (&sv)[2]) __attribute__((always_inline)) {
-            const int j = nn * NK + xi;
+            const int j = nn * NKs + (geo.one_k ? 0 : xi);
             const float4* px = reinterpret_cast<const float4*>(lds + j * XS + lu * 36);
 #pragma unroll
             for (int m = 0; m < 8; ++m) {
@@ -876,10 +880,15 @@ bool plan_batch(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t NK, 
         return (OUT + per - 1) / per;
     };
     auto tiles = [&](int nt) { return (N + nt - 1) / nt; };
+    // A fused group's workgroups stage only their own matrix's input rows when
+    // no workgroup straddles two matrices: workgroup rows (WPB·R·RL, powers
+    // of two up to 8·R·2) divide rl_div (= out_per) whenever the largest does.
+    bp.geo.one_k = NK > 1 && rl_div % (8 * (int64_t)bp.geo.R * 2) == 0;
+    const int64_t NKs = bp.geo.one_k ? 1 : NK;
     bp.NT = N > 8 ? 16 : N > 4 ? 8 : 4;
-    while (bp.NT > 4 && bp.NT * NK * per_row_pass > kBatchLds / 2) bp.NT >>= 1;
+    while (bp.NT > 4 && bp.NT * NKs * per_row_pass > kBatchLds / 2) bp.NT >>= 1;
     while (bp.NT > 4 && blocks(4, 1) * tiles(bp.NT) < 256) bp.NT >>= 1;
-    const int64_t pass_bytes = bp.NT * NK * per_row_pass;
+    const int64_t pass_bytes = bp.NT * NKs * per_row_pass;
     if (pass_bytes > kBatchLds) return false;
     const int64_t budget = pass_bytes <= kBatchLds / 2 ? kBatchLds / 2 : kBatchLds;
     bp.CP = (int)std::min<int64_t>(bp.geo.NP, budget / pass_bytes);
