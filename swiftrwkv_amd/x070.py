@@ -248,8 +248,8 @@ class X070Decoder:
         p = lambda t: t.data_ptr()
         x = bf["x"]
         emb_dt = _lib.F16 if self.emb.dtype == torch.float16 else _lib.F32
-        _lib.check(L.rwkv_layer_norm(p(self.emb), emb_dt, p(ids), self.V, p(self.ln0[0]), p(self.ln0[1]), p(x),
-                                     N, D, LN_EPS, s))
+        _lib.check(L.rwkv_layer_norm(p(self.emb), emb_dt, p(ids), int(self.emb.shape[0]), p(self.ln0[0]),
+                                     p(self.ln0[1]), p(x), N, D, LN_EPS, s))
         for l, lay in enumerate(self.layers):
             _lib.check(L.rwkv_x070_shift_mix(p(x), p(lay["ln1"][0]), p(lay["ln1"][1]), p(state.tmix_prev[l]),
                                              p(lay["coef6"]), 6, p(bf["xrkv"]), p(bf["xmix"]), N, D, LN_EPS, s))
@@ -266,7 +266,21 @@ class X070Decoder:
         return bf["logits"]
 
     def launches_per_token(self, N: int = 1) -> int:
-        return 8 * self.L + 3
+        """Kernel launches of one step of N rows: per layer 2 shift_mix +
+        lora_in + tmix_core and the projections (one per sb6 / sym GEMV or
+        fused group; a dense one is the library GEMM plus its epilogue's
+        elementwise kernels; r / k / v taken one by one at N > 1 add two
+        staging copies each), plus emb/ln0, ln_out and the head."""
+        def n(q, ep=0, staged=False):
+            if isinstance(q, list):
+                return sum(n(m, ep, N > 1) for m in q)
+            k = 1 + (1 + 2 * (ep == 2) if q.kind == "dense" else 0)
+            return k + 2 * staged
+        per_layer = sum(4 + n(self.proj[f"blocks.{l}.att.rkv"]) + sum(
+            n(self.proj[f"blocks.{l}.{k}.weight"], ep) for k, ep in (("att.output", 1), ("ffn.key", 2),
+                                                                       ("ffn.value", 1)))
+            for l in range(self.L))
+        return per_layer + 2 + n(self.proj["head.weight"])
 
     def _tmix_core(self, l, lay, state, bf, N, s):
         L, p = _lib.lib(), (lambda t: t.data_ptr())

@@ -279,3 +279,26 @@ def test_lora_orientation_naming_rule():
     assert not quant.is_raw_lora_world("blocks.0.att.w0")
     assert not quant.is_raw_lora_world("blocks.0.att.key.weight")
     assert not quant.is_raw_lora_world("blocks.0.ffn.w1")
+
+
+def test_x070_launch_count():
+    """launches_per_token over mixed projection kinds: a fused sb6 / sym GEMV
+    is one launch, a dense projection its GEMM plus epilogue kernels (store or
+    residual add: 1; relu²: 3), unfused r / k / v at N > 1 two staging copies
+    per matrix."""
+    from swiftrwkv_amd.x070 import Proj, X070Decoder
+    d = X070Decoder.__new__(X070Decoder)
+    d.L = 2
+    P = lambda kind: Proj(kind, (), 64, 64)
+    d.proj = {"blocks.0.att.rkv": P("sb6"), "blocks.1.att.rkv": [P("sym"), P("sb6"), P("dense")],
+              "head.weight": P("dense")}
+    for l in range(2):
+        for k in ("att.output", "ffn.key", "ffn.value"):
+            d.proj[f"blocks.{l}.{k}.weight"] = P("sb6")
+    d.proj["blocks.0.ffn.key.weight"] = P("dense")
+    # layer 0: 4 + 1 + (1 + 4 + 1); layer 1: 4 + (1 + 1 + 2) + 3; ln / head: 2 + 2
+    assert d.launches_per_token(1) == 11 + 11 + 4
+    assert d.launches_per_token(2) == 11 + 11 + 6 + 4
+    for k in list(d.proj):
+        d.proj[k] = P("sb6")
+    assert d.launches_per_token(1) == 8 * 2 + 3
