@@ -361,6 +361,7 @@ struct GemvGeom {
     int WPB;   // waves per workgroup
     int one_k; // fused groups: every row of a workgroup reads the same input row, staged alone
     int ep;    // epilogue: 0 store, 1 add to y (residual stream), 2 relu² of the result
+    int xfirst;   // single input: inputs loaded before the weights (gemv_kernel<..., XF = true>)
 };
 
 // y[i] ← t, res + t (res = y[i], read before the product) or relu(t)², the
@@ -388,7 +389,7 @@ __host__ __device__ constexpr int xl_stride(int IN) { return IN + (IN >> 3); }
 // 16–32-byte loads in flight.  With `xl` the workgroup first stages its input
 // rows (and per-unit sums) in LDS while those loads are outstanding, and the
 // weights stay in registers across input tiles.
-template <class F, int RL, int KU, int NT, bool XL, bool MULTI>
+template <class F, int RL, int KU, int NT, bool XL, bool MULTI, bool XF = false>
 __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float* __restrict__ x, int N, typename F::Ptr P,
                                                    float* __restrict__ y, int OUT, int IN, int out_per, GemvGeom geo) {
     extern __shared__ float lds[];
@@ -496,22 +497,15 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
     };
     if constexpr (XL) {
         Raw W[RL][KU];
-        load_pass(0, W);   // in flight while the inputs are staged
-        const int rows = NT * NKs;
+        float acc[NT][RL], res[NT][RL];
+        const int rows = NT * NKs;   // one tile: N <= NT
         // matrix of the workgroup's rows when they all read one input row
         const int kwg = geo.one_k ? (int)(blockIdx.x * geo.WPB * geo.R * RL) / out_per : 0;
-        auto stage = [&](int n0) {   // one tile: N <= NT
-            const int step = (int)blockDim.x * 4;
-#pragma unroll 1
-            for (int j = 0; j < rows; ++j) {   // uniform
-                const int nn = NKs == 1 ? j : j / NKs, k = geo.one_k ? kwg : j - nn * NK;
-                const float* src = x + ((int64_t)min(n0 + nn, N - 1) * NK + k) * IN;
-#pragma unroll 1
-                for (int c = (int)threadIdx.x * 4; c < IN; c += step)
-                    *reinterpret_cast<float4*>(lds + j * XS + c + (c >> 5) * 4) =
-                        *reinterpret_cast<const float4*>(src + c);
-            }
-            __syncthreads();
+        auto row_src = [&](int j) {   // staged row j
+            const int nn = NKs == 1 ? j : j / NKs, k = geo.one_k ? kwg : j - nn * NK;
+            return x + ((int64_t)min(nn, N - 1) * NK + k) * IN;
+        };
+        auto row_sums = [&]() {
             if constexpr (F::SUMS) {
                 // sums[j][u][h] = x[j, 32u + 16h + 0..15], added in column order
                 float* sums = lds + NT * NKs * XS;
@@ -531,9 +525,71 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
                 __syncthreads();
             }
         };
-        float acc[NT][RL], res[NT][RL];
-        load_res(res, 0);
-        stage(0);
+        if constexpr (XF) {
+            // Inputs first: the first XPRE float4 of each thread's share of
+            // the staged rows are loaded before the weights.  Loads complete
+            // in issue order, so the LDS stores then wait for these inputs,
+            // not for the weights, and staging and sums run while the weights
+            // stream (a bandwidth-bound launch's workgroups otherwise hold
+            // their staging until their weights arrive).
+            using v4 = float __attribute__((ext_vector_type(4)));
+            const int IN4 = IN >> 2, total4 = rows * IN4;
+            auto split = [&](int e, int& j, int& q) {   // float4 e → (row j, float4 q)
+                if (rows == 1) {
+                    j = 0; q = e;
+                } else {
+                    j = e / IN4; q = e - j * IN4;
+                }
+            };
+            auto src4 = [&](int j, int q) { return reinterpret_cast<const v4*>(row_src(j)) + q; };
+            auto dst4 = [&](int j, int q) { return reinterpret_cast<v4*>(lds + j * XS + q * 4 + (q >> 3) * 4); };
+            constexpr int XPRE = 4;
+            v4 xp[XPRE];
+#pragma unroll
+            for (int i = 0; i < XPRE; ++i) {
+                const int e = (int)threadIdx.x + i * (int)blockDim.x;
+                int j, q;
+                split(e, j, q);
+                v4 t = {};
+                if (e < total4) t = *src4(j, q);
+                xp[i] = t;
+            }
+            load_pass(0, W);
+            load_res(res, 0);
+#pragma unroll
+            for (int i = 0; i < XPRE; ++i) {
+                const int e = (int)threadIdx.x + i * (int)blockDim.x;
+                if (e < total4) {
+                    int j, q;
+                    split(e, j, q);
+                    *dst4(j, q) = xp[i];
+                }
+            }
+#pragma unroll 1
+            for (int e = (int)threadIdx.x + XPRE * (int)blockDim.x; e < total4; e += (int)blockDim.x) {
+                int j, q;
+                split(e, j, q);
+                *dst4(j, q) = *src4(j, q);
+            }
+            __syncthreads();
+            row_sums();
+            // the weights' decode stays after the barriers
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            load_pass(0, W);   // in flight while the inputs are staged
+            load_res(res, 0);
+            const int step = (int)blockDim.x * 4;
+#pragma unroll 1
+            for (int j = 0; j < rows; ++j) {   // uniform
+                const float* src = row_src(j);
+#pragma unroll 1
+                for (int c = (int)threadIdx.x * 4; c < IN; c += step)
+                    *reinterpret_cast<float4*>(lds + j * XS + c + (c >> 5) * 4) =
+                        *reinterpret_cast<const float4*>(src + c);
+            }
+            __syncthreads();
+            row_sums();
+        }
         zero(acc);
         if constexpr (MULTI) {
             for (int p = 0; p < geo.NP; ++p) {
@@ -795,6 +851,11 @@ GemvPlan plan_gemv(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t N
         pl.geo.one_k = 0;
     }
     pl.lds = pl.xl ? (size_t)lds : 0;
+    // inputs loaded before the weights where the launch streams enough for
+    // the staging latency to matter (a full grid or input rows of 2048 and
+    // more: measured faster from 2 MB of weights on); a few workgroups of
+    // short rows, bound by one memory round trip, issue their weights first
+    pl.geo.xfirst = pl.xl && pl.NT == 1 && (pl.blocks >= 256 || IN >= 2048);
     return pl;
 }
 
@@ -807,6 +868,11 @@ bool launch_gemv(const GemvPlan& pl, hipStream_t st, const float* x, int N, type
     auto go = [&](auto kernel) {
         rwkv::launch_lds(kernel, grid, block, pl.lds, st, x, N, P, y, OUT, IN, out_per, pl.geo);
         launched = true;
+    };
+    // single input: the inputs-first variant where the plan asks for it
+    auto go2 = [&](auto kernel, auto kernel_xfirst) {
+        if (pl.geo.xfirst) go(kernel_xfirst);
+        else go(kernel);
     };
     const bool multi = pl.geo.NP > 1;
     if (!pl.xl) {
@@ -827,27 +893,27 @@ bool launch_gemv(const GemvPlan& pl, hipStream_t st, const float* x, int N, type
         }
     } else if (multi) {
         // KU == 1, RL ≤ 2 (1 for wider codes)
-        if (pl.RL == 1) go(gemv_kernel<F, 1, 1, 1, true, true>);
+        if (pl.RL == 1) go2(gemv_kernel<F, 1, 1, 1, true, true>, gemv_kernel<F, 1, 1, 1, true, true, true>);
         else if constexpr (!F::WIDE) {
-            if (pl.RL == 2) go(gemv_kernel<F, 2, 1, 1, true, true>);
+            if (pl.RL == 2) go2(gemv_kernel<F, 2, 1, 1, true, true>, gemv_kernel<F, 2, 1, 1, true, true, true>);
         }
     } else {
         // RL·KU ≤ 4 (≤ 2 for wider codes)
         if (pl.KU == 1) {
-            if (pl.RL == 2) go(gemv_kernel<F, 2, 1, 1, true, false>);
-            else if (pl.RL == 1) go(gemv_kernel<F, 1, 1, 1, true, false>);
+            if (pl.RL == 2) go2(gemv_kernel<F, 2, 1, 1, true, false>, gemv_kernel<F, 2, 1, 1, true, false, true>);
+            else if (pl.RL == 1) go2(gemv_kernel<F, 1, 1, 1, true, false>, gemv_kernel<F, 1, 1, 1, true, false, true>);
             else if constexpr (!F::WIDE) {
-                if (pl.RL == 4) go(gemv_kernel<F, 4, 1, 1, true, false>);
+                if (pl.RL == 4) go2(gemv_kernel<F, 4, 1, 1, true, false>, gemv_kernel<F, 4, 1, 1, true, false, true>);
             }
         } else if (pl.KU == 2) {
-            if (pl.RL == 1) go(gemv_kernel<F, 1, 2, 1, true, false>);
+            if (pl.RL == 1) go2(gemv_kernel<F, 1, 2, 1, true, false>, gemv_kernel<F, 1, 2, 1, true, false, true>);
             else if constexpr (!F::WIDE) {
-                if (pl.RL == 2) go(gemv_kernel<F, 2, 2, 1, true, false>);
+                if (pl.RL == 2) go2(gemv_kernel<F, 2, 2, 1, true, false>, gemv_kernel<F, 2, 2, 1, true, false, true>);
             }
         } else if (pl.KU == 3 && pl.RL == 1) {
-            go(gemv_kernel<F, 1, 3, 1, true, false>);
+            go2(gemv_kernel<F, 1, 3, 1, true, false>, gemv_kernel<F, 1, 3, 1, true, false, true>);
         } else if (pl.KU == 4 && pl.RL == 1) {
-            go(gemv_kernel<F, 1, 4, 1, true, false>);
+            go2(gemv_kernel<F, 1, 4, 1, true, false>, gemv_kernel<F, 1, 4, 1, true, false, true>);
         }
     }
     return launched;
