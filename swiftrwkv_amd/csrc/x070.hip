@@ -24,6 +24,12 @@ constexpr int kRowMax = 8192;   // widest row of the row kernels
 
 __device__ __forceinline__ float f16_round(float x) { return __half2float(__float2half_rn(x)); }
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// The low-rank branch functions on a tmix core's critical path: exp2 of the
+// scaled argument and the hardware reciprocal (each ~1 ulp; relative error of
+// the result ~1e-6 over the branch outputs' range, against the IEEE
+// sequences' ~30 dependent instructions).
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_fast(-x)); }
 
 // Sum over the workgroup: per-wave butterfly, then the wave totals in wave
 // order; every thread gets the same value.
@@ -323,20 +329,20 @@ __global__ __launch_bounds__(R4 ? 1024 : 256) void tmix_core_kernel(CoreArgs A) 
             }
         }
     };
-    auto finish = [&](const Job& j, float acc) {
+    // the row's bias (w, a, v branches), loaded with the job's first chunk
+    auto bias_of = [&](const Job& j) { return j.b < 3 ? A.bias[j.b][h * D + j.i] : 0.0f; };
+    auto finish = [&](const Job& j, float acc, float bias) {
         acc = sum8_lanes(acc);
         if (sub == 0) {
             if constexpr (H16) acc = f16_round(acc);
-            const int row = h * D + j.i;
             float t;
-            if (j.b == 0) t = expf(-0.606531f * sigmoidf_(acc + A.bias[0][row]));
-            else if (j.b == 1) t = sigmoidf_(acc + A.bias[1][row]);
-            else if (j.b == 2) t = sigmoidf_(acc + A.bias[2][row]);
-            else t = acc;
+            if (j.b == 0) t = exp_fast(-0.606531f * sigmoid_fast(acc + bias));
+            else if (j.b == 3) t = acc;
+            else t = sigmoid_fast(acc + bias);
             br[j.b * D + j.i] = t;
         }
     };
-    auto run_job = [&](const Job& j, const uint4 (&first)[8]) {
+    auto run_job = [&](const Job& j, const uint4 (&first)[8], float bias) {
         float acc = 0.0f;
         fma_chunk(j, 0, first, acc);
         for (int c0 = CH; c0 < j.rk; c0 += CH) {
@@ -344,17 +350,22 @@ __global__ __launch_bounds__(R4 ? 1024 : 256) void tmix_core_kernel(CoreArgs A) 
             load_chunk(j, c0, raw);
             fma_chunk(j, c0, raw, acc);
         }
-        finish(j, acc);
+        finish(j, acc, bias);
     };
 
     // sixteen waves: two jobs per wave, their first chunks in flight now
     Job jobs[R4 ? 2 : 1];
     uint4 pre[R4 ? 2 : 1][8];
+    float bpre[R4 ? 2 : 1];
     if constexpr (R4) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             jobs[u] = job_of(wave + 16 * u);
-            if (jobs[u].on) load_chunk(jobs[u], 0, pre[u]);
+            bpre[u] = 0.0f;
+            if (jobs[u].on) {
+                load_chunk(jobs[u], 0, pre[u]);
+                bpre[u] = bias_of(jobs[u]);
+            }
         }
     }
     for (int j = threadIdx.x; j < RT; j += blockDim.x) {
@@ -363,15 +374,38 @@ __global__ __launch_bounds__(R4 ? 1024 : 256) void tmix_core_kernel(CoreArgs A) 
     }
     __syncthreads();
     if constexpr (R4) {
+        // both jobs' products, then both branch functions in one straight
+        // line, so the two dependent chains interleave
+        float acc[2] = {0.0f, 0.0f};
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-            if (jobs[u].on) run_job(jobs[u], pre[u]);   // uniform per wave
+        for (int u = 0; u < 2; ++u) {
+            if (!jobs[u].on) continue;   // uniform per wave
+            fma_chunk(jobs[u], 0, pre[u], acc[u]);
+            for (int c0 = CH; c0 < jobs[u].rk; c0 += CH) {
+                uint4 raw[8];
+                load_chunk(jobs[u], c0, raw);
+                fma_chunk(jobs[u], c0, raw, acc[u]);
+            }
+        }
+        float t[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            float a = sum8_lanes(acc[u]);
+            if constexpr (H16) a = f16_round(a);
+            const float sg = sigmoid_fast(a + bpre[u]);
+            t[u] = jobs[u].b == 0 ? exp_fast(-0.606531f * sg) : jobs[u].b == 3 ? a : sg;
+        }
+        if (sub == 0) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+                if (jobs[u].on) br[jobs[u].b * D + jobs[u].i] = t[u];
+        }
     } else {
         for (int job = wave; job < 32; job += nw) {
             const Job j = job_of(job);
             if (!j.on) continue;   // uniform per wave
             load_chunk(j, 0, pre[0]);
-            run_job(j, pre[0]);
+            run_job(j, pre[0], bias_of(j));
         }
     }
     __syncthreads();
