@@ -242,6 +242,20 @@ rwkv_status rwkv_x070_lora_in(const float* xmix, const void* wcat, rwkv_dtype w_
                               int64_t ra, int64_t rv, int64_t rg, int with_v, float* la, int64_t N,
                               int64_t D, void* stream);
 
+/* One input row (batch 1): the layer's fused r/k/v GEMV (rwkv_sb6_gemv_fused
+ * with N = 1: x_rkv [OUT / out_per, IN] → y_rkv [OUT]) and its low-rank first
+ * layers (rwkv_x070_lora_in with N = 1, D = IN) in one launch — tmixStep
+ * computes them one after the other (:237-239, :256-276); both depend only on
+ * the shift mixes.  The results are bitwise those of the two entries.  4-bit sb6 with
+ * fp16 low-rank matrices and the GEMV plans of the x070 shapes take the single
+ * launch; other inputs run the two entries.  Counts one sb6_fused and one
+ * x070 launch. */
+rwkv_status rwkv_x070_rkv_lora(const float* x_rkv, const uint8_t* qblk, const uint8_t* qsqm,
+                               const uint16_t* ddm, float* y_rkv, int64_t OUT, int64_t IN, int xbits,
+                               int64_t out_per, const float* xmix, const void* wcat, rwkv_dtype w_dt,
+                               int64_t rw, int64_t ra, int64_t rv, int64_t rg, int with_v, float* la,
+                               void* stream);
+
 /* The tmix core (tmixStep :256-294): second layers of the low-rank branches
  * for each head's rows (w2 [D, rw], a2 [D, ra], v2 [D, rv], g2 [D, rg] in
  * w_dt; biases fp32): w = exp(−0.606531·σ(lin + w2_bias)), a = σ(lin + a2_bias),

@@ -69,6 +69,7 @@ _SIGS = {
     "rwkv_layer_norm": (I, [P, I, P, L, P, P, P, L, L, F, P]),
     "rwkv_x070_shift_mix": (I, [P, P, P, P, P, I, P, P, L, L, F, P]),
     "rwkv_x070_lora_in": (I, [P, P, I, L, L, L, L, I, P, L, L, P]),
+    "rwkv_x070_rkv_lora": (I, [P, P, P, P, P, L, L, I, L, P, P, I, L, L, L, L, I, P, P]),
     "rwkv_x070_tmix_core": (I, [P, P, P, P, P, P, I, L, L, L, L] + [P] * 8 + [P, I, P, P, L, L, F, P]),
     "rwkv_unpack6x8": (I, [P, L, P]),
     "rwkv_sb6_to_k3": (I, [P] * 6 + [L, L, P, P, P]),

@@ -38,6 +38,7 @@
 #include <algorithm>
 
 #include "launch.h"
+#include "lora_in.h"
 
 namespace {
 
@@ -389,15 +390,17 @@ __host__ __device__ constexpr int xl_stride(int IN) { return IN + (IN >> 3); }
 // 16–32-byte loads in flight.  With `xl` the workgroup first stages its input
 // rows (and per-unit sums) in LDS while those loads are outstanding, and the
 // weights stay in registers across input tiles.
-template <class F, int RL, int KU, int NT, bool XL, bool MULTI, bool XF = false>
-__global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float* __restrict__ x, int N, typename F::Ptr P,
-                                                   float* __restrict__ y, int OUT, int IN, int out_per, GemvGeom geo) {
+// The body of workgroup `bx` (gemv_kernel runs workgroup blockIdx.x; a fused
+// launch may run it beside other work).
+template <class F, int RL, int KU, int NT, bool XL, bool MULTI, bool XF>
+__device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, int N, typename F::Ptr P,
+                                          float* __restrict__ y, int OUT, int IN, int out_per, GemvGeom geo) {
     extern __shared__ float lds[];
     const int NU = IN >> 5;
     const int NK = OUT / out_per;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int gi = lane >> geo.LG, g = lane & (geo.G - 1);
-    const int row0 = (blockIdx.x * geo.WPB + wave) * geo.R * RL + gi * RL;
+    const int row0 = (bx * geo.WPB + wave) * geo.R * RL + gi * RL;
     const bool live = row0 < OUT;
     const int xi = NK == 1 ? 0 : (live ? row0 : OUT - 1) / out_per;   // RL divides out_per
     float inv = 1.0f;
@@ -500,7 +503,7 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
         float acc[NT][RL], res[NT][RL];
         const int rows = NT * NKs;   // one tile: N <= NT
         // matrix of the workgroup's rows when they all read one input row
-        const int kwg = geo.one_k ? (int)(blockIdx.x * geo.WPB * geo.R * RL) / out_per : 0;
+        const int kwg = geo.one_k ? (int)(bx * geo.WPB * geo.R * RL) / out_per : 0;
         auto row_src = [&](int j) {   // staged row j
             const int nn = NKs == 1 ? j : j / NKs, k = geo.one_k ? kwg : j - nn * NK;
             return x + ((int64_t)min(nn, N - 1) * NK + k) * IN;
@@ -621,6 +624,34 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float*
             }
             store(acc, n0, res);
         }
+    }
+}
+
+template <class F, int RL, int KU, int NT, bool XL, bool MULTI, bool XF = false>
+__global__ __launch_bounds__(NT == 1 ? 1024 : 256) void gemv_kernel(const float* __restrict__ x, int N, typename F::Ptr P,
+                                                   float* __restrict__ y, int OUT, int IN, int out_per, GemvGeom geo) {
+    gemv_body<F, RL, KU, NT, XL, MULTI, XF>((int)blockIdx.x, x, N, P, y, OUT, IN, out_per, geo);
+}
+
+// The fused r/k/v GEMV of an x070 layer (one input row, sb6 4-bit) and the
+// layer's low-rank first layers (fp16 matrices) in one launch: both read only
+// the token-shift mixes, and each alone leaves most of the GPU idle at small
+// widths.  The first `lb` workgroups run one lora_in job per wave (the same
+// arithmetic as lora_in_kernel), dispatched first so they overlap the GEMV
+// when its workgroups fill the GPU; the rest are gemv_kernel's workgroups
+// (the same code, so y is bitwise the separate launch's).
+template <int RL, int KU, bool XF>
+__global__ __launch_bounds__(1024) void rkv_lora_kernel(const float* __restrict__ x, typename Sb6Fmt<0>::Ptr P,
+                                                        float* __restrict__ y, int OUT, int IN, int out_per,
+                                                        GemvGeom geo, int lb, const float* __restrict__ xmix,
+                                                        const void* __restrict__ wcat, float* __restrict__ la, int rw,
+                                                        int ra, int rv, int rg, int with_v) {
+    if ((int)blockIdx.x >= lb) {   // uniform per workgroup
+        gemv_body<Sb6Fmt<0>, RL, KU, 1, true, false, XF>((int)blockIdx.x - lb, x, 1, P, y, OUT, IN, out_per, geo);
+    } else {
+        const int64_t job = (int64_t)blockIdx.x * geo.WPB + (threadIdx.x >> 6);
+        if (job >= rw + ra + rv + rg) return;   // uniform per wave
+        rwkv_x070::lora_in_job<true, 4>(job, threadIdx.x & 63, xmix, wcat, la, IN, rw, ra, rv, rg, with_v);
     }
 }
 
@@ -1123,9 +1154,9 @@ int rwkv_sb6_gemv_applies(int64_t OUT, int64_t IN, int xbits, int super_block, i
 }  // extern "C"
 
 namespace {
-rwkv_status sb6_gemv_impl(const char* what, const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qsqm,
-                          const uint16_t* ddm, float* y, int64_t OUT, int64_t IN, int xbits, int64_t out_per,
-                          void* stream, int ep = 0) {
+rwkv_status sb6_gemv_args(const char* what, const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qsqm,
+                          const uint16_t* ddm, const float* y, int64_t OUT, int64_t IN, int xbits, int64_t out_per,
+                          int ep) {
     RWKV_REQUIRE(x && qblk && qsqm && ddm && y, RWKV_E_NULL, "%s: null buffer", what);
     RWKV_REQUIRE(ep >= 0 && ep <= 2, RWKV_E_SHAPE, "%s: epilogue %d outside 0...2", what, ep);
     RWKV_REQUIRE(xbits >= 0 && xbits <= 2, RWKV_E_SHAPE, "%s: xbits %d outside 0...2", what, xbits);
@@ -1136,6 +1167,14 @@ rwkv_status sb6_gemv_impl(const char* what, const float* x, int64_t N, const uin
                  what, (long long)OUT, (long long)out_per);
     RWKV_REQUIRE(OUT * (IN / 32) * (16 + 4 * xbits) < (int64_t(1) << 32), RWKV_E_SHAPE,
                  "%s: packed matrix of %lldx%lld exceeds 4 GiB", what, (long long)OUT, (long long)IN);
+    return RWKV_OK;
+}
+
+rwkv_status sb6_gemv_impl(const char* what, const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qsqm,
+                          const uint16_t* ddm, float* y, int64_t OUT, int64_t IN, int xbits, int64_t out_per,
+                          void* stream, int ep = 0) {
+    const rwkv_status a = sb6_gemv_args(what, x, N, qblk, qsqm, ddm, y, OUT, IN, xbits, out_per, ep);
+    if (a != RWKV_OK) return a;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const Sb6Fmt<0>::Ptr P{(const uint32_t*)qblk, (const uint16_t*)qsqm, (const uint32_t*)ddm};
     const int64_t NK = OUT / out_per;
@@ -1165,6 +1204,68 @@ rwkv_status rwkv_sb6_gemv_fused(const float* x, int64_t N, const uint8_t* qblk, 
     const rwkv_status s = sb6_gemv_impl("sb6_gemv_fused", x, N, qblk, qsqm, ddm, y, OUT, IN, xbits, out_per, stream);
     if (s == RWKV_OK) rwkv::counters().sb6_fused++;
     return s;
+}
+
+}  // extern "C"
+
+namespace {
+// rkv_lora_kernel for a single-pass plan of 3 or 4 units per lane (every
+// r/k/v shape of the x070 presets); false where the plan is another.
+bool launch_rkv_lora(const GemvPlan& pl, hipStream_t st, const float* x, Sb6Fmt<0>::Ptr P, float* y, int OUT, int IN,
+                     int out_per, const float* xmix, const void* wcat, float* la, int rw, int ra, int rv, int rg,
+                     int with_v) {
+    if (pl.NT != 1 || !pl.xl || pl.geo.NP != 1 || pl.RL != 1 || (pl.KU != 3 && pl.KU != 4)) return false;
+    const int RT = rw + ra + rv + rg;
+    const int lb = (RT + pl.geo.WPB - 1) / pl.geo.WPB;   // lora_in workgroups
+    const dim3 grid(pl.blocks + (unsigned)lb), block(64 * pl.geo.WPB);
+#define RWKV_RL(KUV, XFV)                                                                                        \
+    rwkv::launch_lds(rkv_lora_kernel<1, KUV, XFV>, grid, block, pl.lds, st, x, P, y, OUT, IN, out_per, pl.geo, \
+                     lb, xmix, wcat, la, rw, ra, rv, rg, with_v)
+    if (pl.KU == 4) {
+        if (pl.geo.xfirst) RWKV_RL(4, true);
+        else RWKV_RL(4, false);
+    } else {
+        if (pl.geo.xfirst) RWKV_RL(3, true);
+        else RWKV_RL(3, false);
+    }
+#undef RWKV_RL
+    return true;
+}
+}  // namespace
+
+extern "C" {
+
+rwkv_status rwkv_x070_rkv_lora(const float* x_rkv, const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
+                               float* y_rkv, int64_t OUT, int64_t IN, int xbits, int64_t out_per, const float* xmix,
+                               const void* wcat, rwkv_dtype w_dt, int64_t rw, int64_t ra, int64_t rv, int64_t rg,
+                               int with_v, float* la, void* stream) {
+    RWKV_REQUIRE(xmix && wcat && la, RWKV_E_NULL, "x070_rkv_lora: null low-rank buffer");
+    RWKV_REQUIRE(w_dt == RWKV_F16 || w_dt == RWKV_F32, RWKV_E_DTYPE, "x070_rkv_lora: matrix dtype %d not f16/f32",
+                 (int)w_dt);
+    RWKV_REQUIRE(rw >= 8 && ra >= 8 && rv >= 8 && rg >= 8 && rw % 8 == 0 && ra % 8 == 0 && rv % 8 == 0 && rg % 8 == 0 &&
+                     rw + ra + rv + rg <= 8192,
+                 RWKV_E_SHAPE, "x070_rkv_lora: ranks %lld/%lld/%lld/%lld (multiples of 8)", (long long)rw,
+                 (long long)ra, (long long)rv, (long long)rg);
+    const rwkv_status a = sb6_gemv_args("x070_rkv_lora", x_rkv, 1, qblk, qsqm, ddm, y_rkv, OUT, IN, xbits, out_per, 0);
+    if (a != RWKV_OK) return a;
+    if (xbits == 0 && w_dt == RWKV_F16) {
+        GemvPlan pl = plan_gemv(OUT, IN / 32, out_per, 1, OUT / out_per, true, false);
+        pl.geo.ep = 0;
+        const Sb6Fmt<0>::Ptr P{(const uint32_t*)qblk, (const uint16_t*)qsqm, (const uint32_t*)ddm};
+        if (launch_rkv_lora(pl, reinterpret_cast<hipStream_t>(stream), x_rkv, P, y_rkv, (int)OUT, (int)IN,
+                            (int)out_per, xmix, wcat, la, (int)rw, (int)ra, (int)rv, (int)rg, with_v)) {
+            const rwkv_status s = launch_status("x070_rkv_lora");
+            if (s == RWKV_OK) {
+                rwkv::counters().sb6_fused++;
+                rwkv::counters().x070++;
+            }
+            return s;
+        }
+    }
+    // other formats and plans: the two launches
+    const rwkv_status s = rwkv_sb6_gemv_fused(x_rkv, 1, qblk, qsqm, ddm, y_rkv, OUT, IN, xbits, out_per, stream);
+    if (s != RWKV_OK) return s;
+    return rwkv_x070_lora_in(xmix, wcat, w_dt, rw, ra, rv, rg, with_v, la, 1, IN, stream);
 }
 
 int rwkv_sym_gemv_applies(int64_t OUT, int64_t IN, int bits, int64_t rows) {

@@ -15,15 +15,15 @@
 
 #include "common.h"
 #include "launch.h"
+#include "lora_in.h"
 #include "wkv7_step.h"
 
 namespace {
 using namespace rwkv_wkv;
+using namespace rwkv_x070;
 
 constexpr int kRowMax = 8192;   // widest row of the row kernels
 
-__device__ __forceinline__ float f16_round(float x) { return __half2float(__float2half_rn(x)); }
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 // The low-rank branch functions on a tmix core's critical path: exp2 of the
 // scaled argument and the hardware reciprocal (each ~1 ulp; relative error of
 // the result ~1e-6 over the branch outputs' range, against the IEEE
@@ -173,64 +173,14 @@ inline void row_geometry(int64_t D, int& S, int& T, int& PS) {
 inline bool row_width_ok(int64_t D) { return D >= 256 && D % 256 == 0 && D <= kRowMax && (D <= 4096 || D % 1024 == 0); }
 
 // ── low-rank first layers (tmixStep :256-276, the inner `lin` of each branch) ──
-// Rows of Wcat [rw + ra + rv + rg, D]: w, a, v, g branches; inputs xmix [N, 4, D]
-// rows w, a, v, g.  la[n, j] = act(lin(x_branch, Wcat[j])):
-// tanh for w, sigmoid for g, none for a and v.  One wave per (row, input).
+// One wave per (input row, matrix row): lora_in_job (lora_in.h).
 template <bool H16>
 __global__ __launch_bounds__(256) void lora_in_kernel(const float* __restrict__ xmix, const void* __restrict__ Wcat,
                                                       float* __restrict__ la, int N, int D, int rw, int ra, int rv,
                                                       int rg, int with_v) {
-    const int lane = threadIdx.x & 63;
-    const int RT = rw + ra + rv + rg;
     const int64_t job = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (job >= (int64_t)RT * N) return;   // uniform per wave
-    const int j = (int)(job % RT), n = (int)(job / RT);
-    const int br = j < rw ? 0 : j < rw + ra ? 1 : j < rw + ra + rv ? 2 : 3;
-    if (br == 2 && !with_v) return;
-    const float* xin = xmix + ((int64_t)n * 4 + br) * D;
-    float acc = 0.0f;
-    constexpr int E = H16 ? 8 : 4;   // matrix elements per 16-byte load
-    constexpr int BATCH = 8;         // loads in flight per lane
-    for (int c0 = 0; c0 < D; c0 += 64 * E * BATCH) {
-        uint4 raw[BATCH];
-        float4 xa[BATCH], xb[BATCH];
-#pragma unroll
-        for (int q = 0; q < BATCH; ++q) {
-            const int c = c0 + 64 * E * q + lane * E;
-            if (c < D) {   // D % 8 == 0
-                const char* base = reinterpret_cast<const char*>(Wcat) + ((int64_t)j * D + c) * (H16 ? 2 : 4);
-                raw[q] = *reinterpret_cast<const uint4*>(base);
-                xa[q] = *reinterpret_cast<const float4*>(xin + c);
-                if (H16) xb[q] = *reinterpret_cast<const float4*>(xin + c + 4);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < BATCH; ++q) {
-            const int c = c0 + 64 * E * q + lane * E;
-            if (c >= D) continue;
-            if constexpr (H16) {
-                const __half2* h = reinterpret_cast<const __half2*>(&raw[q]);
-                const float xs[8] = {xa[q].x, xa[q].y, xa[q].z, xa[q].w, xb[q].x, xb[q].y, xb[q].z, xb[q].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float2 f = __half22float2(h[e]);
-                    acc = fmaf(f16_round(xs[2 * e]), f.x, acc);
-                    acc = fmaf(f16_round(xs[2 * e + 1]), f.y, acc);
-                }
-            } else {
-                const float4 wv = *reinterpret_cast<const float4*>(&raw[q]);
-                acc = fmaf(xa[q].x, wv.x, acc);
-                acc = fmaf(xa[q].y, wv.y, acc);
-                acc = fmaf(xa[q].z, wv.z, acc);
-                acc = fmaf(xa[q].w, wv.w, acc);
-            }
-        }
-    }
-    float t = wave_total(acc);
-    if constexpr (H16) t = f16_round(t);
-    if (br == 0) t = tanhf(t);
-    else if (br == 3) t = sigmoidf_(t);
-    if (lane == 0) la[(int64_t)n * RT + j] = t;
+    if (job >= (int64_t)(rw + ra + rv + rg) * N) return;   // uniform per wave
+    lora_in_job<H16, 8>(job, threadIdx.x & 63, xmix, Wcat, la, D, rw, ra, rv, rg, with_v);
 }
 
 // ── the tmix core of one (input row, head) (tmixStep :256-296) ──

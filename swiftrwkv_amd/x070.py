@@ -13,6 +13,8 @@ Per layer and token, eight launches through the C ABI:
   rwkv_sb6_gemv_ep     (ffn key, relu², :308-309)
   rwkv_sb6_gemv_ep     (ffn value + residual add, :309 / :496)
 plus rwkv_layer_norm for emb + ln0 (:489-490) and ln_out, and the head GEMV.
+At batch 1 (4-bit sb6 r/k/v, fp16 low-rank matrices) the r/k/v GEMV and
+lora_in are one launch, rwkv_x070_rkv_lora (seven per layer).
 Activations are fp32; low-rank matrices keep their dtype (fp16: the `lin`
 narrowing of :248-253).  There is no CPU fallback: a missing library raises.
 """
@@ -104,6 +106,9 @@ class X070Decoder:
         self.L, self.D, self.F, self.V = n_layer, n_embd, ffn, vocab
         self.H = n_embd // HEAD
         self.device = torch.empty(0, device=device).device   # concrete index (cuda → cuda:N)
+        # one launch for a layer's r/k/v GEMV and low-rank first layers where
+        # _fused_rkv_lora allows (bitwise equal to the two launches)
+        self.fuse_rkv_lora = True
         dev = self.device
 
         def tens(a) -> torch.Tensor:
@@ -253,7 +258,9 @@ class X070Decoder:
         for l, lay in enumerate(self.layers):
             _lib.check(L.rwkv_x070_shift_mix(p(x), p(lay["ln1"][0]), p(lay["ln1"][1]), p(state.tmix_prev[l]),
                                              p(lay["coef6"]), 6, p(bf["xrkv"]), p(bf["xmix"]), N, D, LN_EPS, s))
-            self._rkv(l, bf, N, s)
+            if not self._rkv_lora(l, lay, bf, N, s):
+                self._rkv(l, bf, N, s)
+                self._lora_in(l, lay, bf, N, s)
             self._tmix_core(l, lay, state, bf, N, s)
             self._gemv(f"blocks.{l}.att.output.weight", bf["tout"], x, 1, N, s)
             _lib.check(L.rwkv_x070_shift_mix(p(x), p(lay["ln2"][0]), p(lay["ln2"][1]), p(state.cmix_prev[l]),
@@ -270,24 +277,50 @@ class X070Decoder:
         lora_in + tmix_core and the projections (one per sb6 / sym GEMV or
         fused group; a dense one is the library GEMM plus its epilogue's
         elementwise kernels; r / k / v taken one by one at N > 1 add two
-        staging copies each), plus emb/ln0, ln_out and the head."""
+        staging copies each; the r/k/v group and lora_in as one launch where
+        _fused_rkv_lora holds), plus emb/ln0, ln_out and the head."""
         def n(q, ep=0, staged=False):
             if isinstance(q, list):
                 return sum(n(m, ep, N > 1) for m in q)
             k = 1 + (1 + 2 * (ep == 2) if q.kind == "dense" else 0)
             return k + 2 * staged
-        per_layer = sum(4 + n(self.proj[f"blocks.{l}.att.rkv"]) + sum(
+        # 2 shift_mix + tmix_core + (lora_in and the r/k/v projections, or
+        # their one fused launch) + o / ffn key / ffn value
+        per_layer = sum((4 if self._fused_rkv_lora(l, N) else 4 + n(self.proj[f"blocks.{l}.att.rkv"])) + sum(
             n(self.proj[f"blocks.{l}.{k}.weight"], ep) for k, ep in (("att.output", 1), ("ffn.key", 2),
                                                                        ("ffn.value", 1)))
             for l in range(self.L))
         return per_layer + 2 + n(self.proj["head.weight"])
 
+    def _fused_rkv_lora(self, l, N) -> bool:
+        """The layer's r/k/v GEMV and low-rank first layers run as one launch
+        (rwkv_x070_rkv_lora): batch 1, one 4-bit sb6 r/k/v group, fp16
+        low-rank matrices."""
+        q = self.proj[f"blocks.{l}.att.rkv"]
+        return (self.fuse_rkv_lora and N == 1 and isinstance(q, Proj) and q.kind == "sb6" and q.xbits == 0
+                and q.out_per < q.OUT and self.layers[l]["wcat"].dtype == torch.float16)
+
+    def _rkv_lora(self, l, lay, bf, N, s) -> bool:
+        if not self._fused_rkv_lora(l, N):
+            return False
+        L, p = _lib.lib(), (lambda t: t.data_ptr())
+        q = self.proj[f"blocks.{l}.att.rkv"]
+        rw, ra, rv, rg = self.ranks
+        _lib.check(L.rwkv_x070_rkv_lora(p(bf["xrkv"]), p(q.bufs[0]), p(q.bufs[1]), p(q.bufs[2]), p(bf["y_rkv"]),
+                                        q.OUT, q.IN, q.xbits, q.out_per, p(bf["xmix"]), p(lay["wcat"]), _lib.F16,
+                                        rw, ra, rv, rg, int(l > 0), p(bf["la"]), s))
+        return True
+
+    def _lora_in(self, l, lay, bf, N, s):
+        L, p = _lib.lib(), (lambda t: t.data_ptr())
+        rw, ra, rv, rg = self.ranks
+        _lib.check(L.rwkv_x070_lora_in(p(bf["xmix"]), p(lay["wcat"]), _dt(lay["wcat"]), rw, ra, rv, rg, int(l > 0),
+                                       p(bf["la"]), N, self.D, s))
+
     def _tmix_core(self, l, lay, state, bf, N, s):
         L, p = _lib.lib(), (lambda t: t.data_ptr())
         rw, ra, rv, rg = self.ranks
         wdt = _dt(lay["wcat"])
-        _lib.check(L.rwkv_x070_lora_in(p(bf["xmix"]), p(lay["wcat"]), wdt, rw, ra, rv, rg, int(l > 0), p(bf["la"]),
-                                       N, self.D, s))
         Bm = lay["B"]
         _lib.check(L.rwkv_x070_tmix_core(p(bf["y_rkv"]), p(bf["la"]), p(Bm[0]), p(Bm[1]), p(Bm[2]), p(Bm[3]), wdt,
                                          rw, ra, rv, rg, p(lay["bias"][0]), p(lay["bias"][1]), p(lay["bias"][2]),

@@ -228,7 +228,60 @@ def test_decode_steps_match_oracle(tiny, decoder, N):
     assert c["x070"] == 4 * (2 + 4 * Lr)          # ln0 + ln_out + 4 per layer
     assert c["sb6_gemv"] == 4 * (3 * Lr + 1)      # o_proj, ffn key, ffn value, head
     assert c["sb6_fused"] == 4 * Lr               # r/k/v
-    assert decoder.launches_per_token(N) == 8 * Lr + 3
+    # batch 1: each layer's r/k/v GEMV and lora_in share one launch
+    assert decoder.launches_per_token(N) == (7 if N == 1 else 8) * Lr + 3
+
+
+@pytest.mark.parametrize("D", [768, 2048, 4096])
+@pytest.mark.parametrize("l", [0, 1])
+def test_rkv_lora_matches_separate(D, l):
+    """rwkv_x070_rkv_lora (one launch) against rwkv_sb6_gemv_fused +
+    rwkv_x070_lora_in, bitwise, at the r/k/v widths of the 0.1B, 1.5B and
+    7B-class shapes (weights-first and inputs-first GEMV plans)."""
+    from swiftrwkv_amd import quant as Q
+    case(f"rkv_lora D={D} layer={l}")
+    rng = np.random.default_rng(D + l)
+    w = (rng.standard_normal((3 * D, D), dtype=np.float32) * np.float32(0.02))
+    disk = Q.encode_sb6(w, 4, 8)
+    qb, qs, dd, _ = Q.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"], disk["gw_dm"], None, None,
+                                      (3 * D, D))
+    q = [dev(qb), dev(qs), dev(np.ascontiguousarray(dd).view(np.float16))]
+    rw, ra, rv, rg = syn.lora_ranks(D)
+    RT = rw + ra + rv + rg
+    wcat = dev((rng.standard_normal((RT, D)) * 0.05).astype(np.float16))
+    xrkv = dev(rng.standard_normal((1, 3, D)).astype(np.float32))
+    xmix = dev(rng.standard_normal((1, 4, D)).astype(np.float32))
+    y1, y2 = torch.full((1, 3 * D), 5.0, device=DEV), torch.full((1, 3 * D), 5.0, device=DEV)
+    la1, la2 = torch.full((1, RT), 7.0, device=DEV), torch.full((1, RT), 7.0, device=DEV)
+    _lib.reset_counters()
+    _lib.call("rwkv_x070_rkv_lora", xrkv.data_ptr(), *[t.data_ptr() for t in q], y1.data_ptr(), 3 * D, D, 0, D,
+              xmix.data_ptr(), wcat.data_ptr(), _lib.F16, rw, ra, rv, rg, int(l > 0), la1.data_ptr(), None)
+    c = _lib.counters()
+    assert c["sb6_fused"] == 1 and c["x070"] == 1
+    _lib.call("rwkv_sb6_gemv_fused", xrkv.data_ptr(), 1, *[t.data_ptr() for t in q], y2.data_ptr(), 3 * D, D, 0, D,
+              None)
+    _lib.call("rwkv_x070_lora_in", xmix.data_ptr(), wcat.data_ptr(), _lib.F16, rw, ra, rv, rg, int(l > 0),
+              la2.data_ptr(), 1, D, None)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert torch.equal(la1, la2)
+    if l == 0:   # the v branch is left as it was
+        assert (la1[:, rw + ra:rw + ra + rv] == 7.0).all()
+
+
+def test_decode_fused_rkv_lora_bitwise(tiny, decoder):
+    """The decoder's batch-1 step with the r/k/v GEMV and lora_in fused is
+    bitwise the step with the two launches."""
+    case("decode fused rkv+lora vs separate")
+    ids = [5, 300, 17]
+    outs = []
+    for fuse in (True, False):
+        decoder.fuse_rkv_lora = fuse
+        st = decoder.new_state(1)
+        outs.append([decoder.step([i], st) for i in ids] + [st.wkv.clone(), st.v_first.clone()])
+    decoder.fuse_rkv_lora = True
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("N", [1, 2])

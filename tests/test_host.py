@@ -77,6 +77,13 @@ def test_x070_step_entry_validation():
     # tmix core: v branch buffers needed above layer 0
     args = [d] * 6 + [F16, 64, 64, 32, 128] + [d, d, None] + [d] * 5 + [d, 0, d, d, 1, 12, 64e-5, None]
     assert lib.rwkv_x070_tmix_core(*args) == 6
+    # r/k/v GEMV + low-rank first layers in one launch: the checks of both entries
+    rkl = lambda *a: lib.rwkv_x070_rkv_lora(d, d, d, d, d, *a)
+    assert rkl(3 * 768, 768, 0, 768, None, d, F16, 64, 64, 32, 128, 1, d, None) == 6            # no xmix
+    assert rkl(3 * 768, 768, 0, 768, d, d, _lib.BF16, 64, 64, 32, 128, 1, d, None) == 2         # matrix dtype
+    assert rkl(3 * 768, 768, 0, 768, d, d, F16, 60, 64, 32, 128, 1, d, None) == 1               # ranks
+    assert rkl(3 * 768, 768, 0, 700, d, d, F16, 64, 64, 32, 128, 1, d, None) == 1               # out_per
+    assert rkl(3 * 768, 768, 3, 768, d, d, F16, 64, 64, 32, 128, 1, d, None) == 1               # xbits
     # GEMV epilogue code
     assert lib.rwkv_sb6_gemv_ep(d, 1, d, d, d, d, 256, 256, 0, 3, None) == 1
     assert lib.rwkv_sym_gemv_ep(d, 1, d, d, d, d, 256, 256, 8, -1, None) == 1
@@ -289,6 +296,7 @@ def test_x070_launch_count():
     from swiftrwkv_amd.x070 import Proj, X070Decoder
     d = X070Decoder.__new__(X070Decoder)
     d.L = 2
+    d.fuse_rkv_lora = False
     P = lambda kind: Proj(kind, (), 64, 64)
     d.proj = {"blocks.0.att.rkv": P("sb6"), "blocks.1.att.rkv": [P("sym"), P("sb6"), P("dense")],
               "head.weight": P("dense")}
@@ -301,4 +309,14 @@ def test_x070_launch_count():
     assert d.launches_per_token(2) == 11 + 11 + 6 + 4
     for k in list(d.proj):
         d.proj[k] = P("sb6")
+    assert d.launches_per_token(1) == 8 * 2 + 3
+    # batch 1, a fused 4-bit sb6 r/k/v group and fp16 low-rank matrices: the
+    # group and lora_in share one launch
+    d.fuse_rkv_lora = True
+    d.layers = [{"wcat": torch.empty(0, dtype=torch.float16)}] * 2
+    for l in range(2):
+        d.proj[f"blocks.{l}.att.rkv"] = Proj("sb6", (), 192, 64, out_per=64)
+    assert d.launches_per_token(1) == 7 * 2 + 3
+    assert d.launches_per_token(2) == 8 * 2 + 3
+    d.layers = [{"wcat": torch.empty(0, dtype=torch.float32)}] * 2
     assert d.launches_per_token(1) == 8 * 2 + 3
