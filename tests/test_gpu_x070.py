@@ -232,35 +232,39 @@ def test_decode_steps_match_oracle(tiny, decoder, N):
     assert decoder.launches_per_token(N) == (7 if N == 1 else 8) * Lr + 3
 
 
-@pytest.mark.parametrize("D", [768, 2048, 4096])
+@pytest.mark.parametrize("D,xbits,wdt", [(768, 0, np.float16), (2048, 0, np.float16), (4096, 0, np.float16),
+                                          (768, 1, np.float16), (768, 0, np.float32)])
 @pytest.mark.parametrize("l", [0, 1])
-def test_rkv_lora_matches_separate(D, l):
-    """rwkv_x070_rkv_lora (one launch) against rwkv_sb6_gemv_fused +
-    rwkv_x070_lora_in, bitwise, at the r/k/v widths of the 0.1B, 1.5B and
-    7B-class shapes (weights-first and inputs-first GEMV plans)."""
+def test_rkv_lora_matches_separate(D, xbits, wdt, l):
+    """rwkv_x070_rkv_lora against rwkv_sb6_gemv_fused + rwkv_x070_lora_in,
+    bitwise: one launch at the r/k/v widths of the 0.1B, 1.5B and 7B-class
+    shapes (weights-first and inputs-first GEMV plans), the two launches for
+    5-bit sb6 or fp32 low-rank matrices."""
     from swiftrwkv_amd import quant as Q
-    case(f"rkv_lora D={D} layer={l}")
+    case(f"rkv_lora D={D} xbits={xbits} {wdt.__name__} layer={l}")
     rng = np.random.default_rng(D + l)
     w = (rng.standard_normal((3 * D, D), dtype=np.float32) * np.float32(0.02))
-    disk = Q.encode_sb6(w, 4, 8)
-    qb, qs, dd, _ = Q.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"], disk["gw_dm"], None, None,
-                                      (3 * D, D))
+    disk = Q.encode_sb6(w, 4 + xbits, 8)
+    qb, qs, dd, xb = Q.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"], disk["gw_dm"],
+                                       disk.get("gw_qh"), disk.get("gw_qh2"), (3 * D, D))
+    assert xb == xbits
     q = [dev(qb), dev(qs), dev(np.ascontiguousarray(dd).view(np.float16))]
     rw, ra, rv, rg = syn.lora_ranks(D)
     RT = rw + ra + rv + rg
-    wcat = dev((rng.standard_normal((RT, D)) * 0.05).astype(np.float16))
+    wcat = dev((rng.standard_normal((RT, D)) * 0.05).astype(wdt))
+    wcode = _lib.F16 if wdt == np.float16 else _lib.F32
     xrkv = dev(rng.standard_normal((1, 3, D)).astype(np.float32))
     xmix = dev(rng.standard_normal((1, 4, D)).astype(np.float32))
     y1, y2 = torch.full((1, 3 * D), 5.0, device=DEV), torch.full((1, 3 * D), 5.0, device=DEV)
     la1, la2 = torch.full((1, RT), 7.0, device=DEV), torch.full((1, RT), 7.0, device=DEV)
     _lib.reset_counters()
-    _lib.call("rwkv_x070_rkv_lora", xrkv.data_ptr(), *[t.data_ptr() for t in q], y1.data_ptr(), 3 * D, D, 0, D,
-              xmix.data_ptr(), wcat.data_ptr(), _lib.F16, rw, ra, rv, rg, int(l > 0), la1.data_ptr(), None)
+    _lib.call("rwkv_x070_rkv_lora", xrkv.data_ptr(), *[t.data_ptr() for t in q], y1.data_ptr(), 3 * D, D, xbits, D,
+              xmix.data_ptr(), wcat.data_ptr(), wcode, rw, ra, rv, rg, int(l > 0), la1.data_ptr(), None)
     c = _lib.counters()
     assert c["sb6_fused"] == 1 and c["x070"] == 1
-    _lib.call("rwkv_sb6_gemv_fused", xrkv.data_ptr(), 1, *[t.data_ptr() for t in q], y2.data_ptr(), 3 * D, D, 0, D,
-              None)
-    _lib.call("rwkv_x070_lora_in", xmix.data_ptr(), wcat.data_ptr(), _lib.F16, rw, ra, rv, rg, int(l > 0),
+    _lib.call("rwkv_sb6_gemv_fused", xrkv.data_ptr(), 1, *[t.data_ptr() for t in q], y2.data_ptr(), 3 * D, D, xbits,
+              D, None)
+    _lib.call("rwkv_x070_lora_in", xmix.data_ptr(), wcat.data_ptr(), wcode, rw, ra, rv, rg, int(l > 0),
               la2.data_ptr(), 1, D, None)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
