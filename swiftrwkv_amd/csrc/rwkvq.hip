@@ -399,6 +399,10 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
     const int NU = IN >> 5;
     const int NK = OUT / out_per;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // every launch of this body has 64·WPB threads; a constant instead of
+    // blockDim.x, whose code-object-v5 read is a vector load that would queue
+    // behind the weight loads
+    const int nthr = 64 * geo.WPB;
     const int gi = lane >> geo.LG, g = lane & (geo.G - 1);
     const int row0 = (bx * geo.WPB + wave) * geo.R * RL + gi * RL;
     const bool live = row0 < OUT;
@@ -515,7 +519,7 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
 #pragma unroll 1
                 for (int j = 0; j < rows; ++j)
 #pragma unroll 1
-                    for (int i = threadIdx.x; i < NU * 2; i += blockDim.x) {
+                    for (int i = threadIdx.x; i < NU * 2; i += nthr) {
                         const float4* px = reinterpret_cast<const float4*>(lds + j * XS + (i >> 1) * 36 + 16 * (i & 1));
                         float sum = 0.0f;
 #pragma unroll
@@ -550,7 +554,7 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
             v4 xp[XPRE];
 #pragma unroll
             for (int i = 0; i < XPRE; ++i) {
-                const int e = (int)threadIdx.x + i * (int)blockDim.x;
+                const int e = (int)threadIdx.x + i * nthr;
                 int j, q;
                 split(e, j, q);
                 v4 t = {};
@@ -561,7 +565,7 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
             load_res(res, 0);
 #pragma unroll
             for (int i = 0; i < XPRE; ++i) {
-                const int e = (int)threadIdx.x + i * (int)blockDim.x;
+                const int e = (int)threadIdx.x + i * nthr;
                 if (e < total4) {
                     int j, q;
                     split(e, j, q);
@@ -569,7 +573,7 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
                 }
             }
 #pragma unroll 1
-            for (int e = (int)threadIdx.x + XPRE * (int)blockDim.x; e < total4; e += (int)blockDim.x) {
+            for (int e = (int)threadIdx.x + XPRE * nthr; e < total4; e += nthr) {
                 int j, q;
                 split(e, j, q);
                 *dst4(j, q) = *src4(j, q);
@@ -581,7 +585,7 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
         } else {
             load_pass(0, W);   // in flight while the inputs are staged
             load_res(res, 0);
-            const int step = (int)blockDim.x * 4;
+            const int step = nthr * 4;
 #pragma unroll 1
             for (int j = 0; j < rows; ++j) {   // uniform
                 const float* src = row_src(j);
