@@ -964,13 +964,17 @@ struct BatchPlan {
 };
 
 // Batched geometry: G and the unit order are the single-input plan's (so the
-// results match it bitwise), one unit per lane and pass.  NT = 16 / 8 / 4
-// inputs per workgroup, the largest whose one pass of staged inputs fits in
-// half the LDS (two workgroups per CU; NT = 4 may take all of it), reduced
-// while the grid (row blocks × input tiles) has fewer than 256 workgroups;
-// then RL = 2 rows per lane where the rows allow and the grid stays ≥ 256
-// workgroups, and WPB = 8 waves under the same condition, else 4.  CP passes
-// per chunk fill the LDS share.
+// results match it bitwise), one unit per lane and pass.  NT = 8 / 4 inputs
+// per workgroup: 8 where one pass of staged inputs fits in half the LDS (two
+// workgroups per CU; NT = 4 may take all of it) and the grid (row blocks ×
+// input tiles, at 4 waves per workgroup) keeps ≥ 1024 workgroups, else 4.
+// A batch is bound by the FMAs, 32 per unit and input, and a grid of fewer
+// workgroups leaves SIMDs idle; measured per projection at N = 8…32, this
+// beats tiles of 16 inputs (0.4B FFN value × 32: 22.3 → 11.9 µs; 7B-class
+// output projection × 16: 31.3 → 18.6 µs) and, at the 7B-class shapes with
+// ≥ 1024 workgroups of 8 inputs, also tiles of 4.  Then RL = 2 rows per lane
+// where the rows allow and the grid stays ≥ 256 workgroups, and WPB = 8 waves
+// under the same condition, else 4.  CP passes per chunk fill the LDS share.
 bool plan_batch(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t NK, bool sums, BatchPlan& bp) {
     const GemvPlan one = plan_gemv(OUT, NU, rl_div, 1, NK, sums, false);
     bp.geo = one.geo;
@@ -986,9 +990,8 @@ bool plan_batch(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t NK, 
     // of two up to 8·R·2) divide rl_div (= out_per) whenever the largest does.
     bp.geo.one_k = NK > 1 && rl_div % (8 * (int64_t)bp.geo.R * 2) == 0;
     const int64_t NKs = bp.geo.one_k ? 1 : NK;
-    bp.NT = N > 8 ? 16 : N > 4 ? 8 : 4;
-    while (bp.NT > 4 && bp.NT * NKs * per_row_pass > kBatchLds / 2) bp.NT >>= 1;
-    while (bp.NT > 4 && blocks(4, 1) * tiles(bp.NT) < 256) bp.NT >>= 1;
+    bp.NT = N > 4 ? 8 : 4;
+    if (bp.NT > 4 && (bp.NT * NKs * per_row_pass > kBatchLds / 2 || blocks(4, 1) * tiles(bp.NT) < 1024)) bp.NT = 4;
     const int64_t pass_bytes = bp.NT * NKs * per_row_pass;
     if (pass_bytes > kBatchLds) return false;
     const int64_t budget = pass_bytes <= kBatchLds / 2 ? kBatchLds / 2 : kBatchLds;
@@ -1008,12 +1011,10 @@ bool launch_batch(const BatchPlan& bp, hipStream_t st, const float* x, int N, ty
     rwkv::launch_lds(gemv_batch_kernel<F, RLV, NTV>, grid, block, bp.lds, st, x, N, P, y, OUT, IN, out_per, \
                      bp.geo, bp.CP)
     if (bp.RL == 2) {
-        if (bp.NT == 16) RWKV_GB(2, 16);
-        else if (bp.NT == 8) RWKV_GB(2, 8);
+        if (bp.NT == 8) RWKV_GB(2, 8);
         else RWKV_GB(2, 4);
     } else {
-        if (bp.NT == 16) RWKV_GB(1, 16);
-        else if (bp.NT == 8) RWKV_GB(1, 8);
+        if (bp.NT == 8) RWKV_GB(1, 8);
         else RWKV_GB(1, 4);
     }
 #undef RWKV_GB

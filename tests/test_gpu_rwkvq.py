@@ -196,14 +196,15 @@ def test_fused_sym_gemv_equals_separate_bitwise(orc, bits):
     assert rel(want, fused.cpu().numpy()) < GEMV_TOL
 
 
-# batches run in their own kernel (one weight pass for up to 16 inputs, the
+# batches run in their own kernel (one weight pass for 4 or 8 inputs, the
 # inputs staged in LDS chunk by chunk); 256 x 14336 stages 7 passes of 64
-# units in chunks (a partial last chunk), N = 17 / 33 split into launches
+# units in chunks (a partial last chunk); 3072 x 4096 takes tiles of 8 inputs
+# at N = 17 / 33 (a grid of >= 1024 workgroups) and of 4 below
 BATCH_NS = (2, 5, 16, 17, 33)
 
 
 @pytest.mark.parametrize("fmt", ["sb6:0", "sb6:1", "sb6:2", "sym:8", "sym:6"])
-@pytest.mark.parametrize("OUT,IN", [(768, 768), (256, 14336)])
+@pytest.mark.parametrize("OUT,IN", [(768, 768), (256, 14336), (3072, 4096)])
 def test_batched_gemv_rows_equal_single_bitwise(orc, fmt, OUT, IN):
     kind, b = fmt.split(":")
     b = int(b)
