@@ -964,15 +964,19 @@ struct BatchPlan {
 };
 
 // Batched geometry: G and the unit order are the single-input plan's (so the
-// results match it bitwise), one unit per lane and pass.  NT = 8 / 4 inputs
-// per workgroup: 8 where one pass of staged inputs fits in half the LDS (two
-// workgroups per CU; NT = 4 may take all of it) and the grid (row blocks ×
-// input tiles, at 4 waves per workgroup) keeps ≥ 1024 workgroups, else 4.
+// results match it bitwise), one unit per lane and pass.  NT = 8 / 4 / 2
+// inputs per workgroup: 8 where one pass of staged inputs fits in half the
+// LDS (two workgroups per CU; NT = 4 may take all of it) and the grid (row
+// blocks × input tiles, at 4 waves per workgroup) keeps ≥ 1024 workgroups;
+// else 4, or 2 for N ≤ 2 and for N ≤ 8 on a grid of < 1024 workgroups.
 // A batch is bound by the FMAs, 32 per unit and input, and a grid of fewer
 // workgroups leaves SIMDs idle; measured per projection at N = 8…32, this
 // beats tiles of 16 inputs (0.4B FFN value × 32: 22.3 → 11.9 µs; 7B-class
 // output projection × 16: 31.3 → 18.6 µs) and, at the 7B-class shapes with
-// ≥ 1024 workgroups of 8 inputs, also tiles of 4.  Then RL = 2 rows per lane
+// ≥ 1024 workgroups of 8 inputs, also tiles of 4; tiles of 2 win at N = 8
+// (0.1B / 0.4B projections 5–20 % faster) but lose at N = 32 on the small
+// grids (0.1B r/k/v × 32: 8.9 → 11.3 µs), where the decode of each unit is
+// repeated per tile.  Then RL = 2 rows per lane
 // where the rows allow and the grid stays ≥ 256 workgroups, and WPB = 8 waves
 // under the same condition, else 4.  CP passes per chunk fill the LDS share.
 bool plan_batch(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t NK, bool sums, BatchPlan& bp) {
@@ -992,6 +996,7 @@ bool plan_batch(int64_t OUT, int64_t NU, int64_t rl_div, int64_t N, int64_t NK, 
     const int64_t NKs = bp.geo.one_k ? 1 : NK;
     bp.NT = N > 4 ? 8 : 4;
     if (bp.NT > 4 && (bp.NT * NKs * per_row_pass > kBatchLds / 2 || blocks(4, 1) * tiles(bp.NT) < 1024)) bp.NT = 4;
+    if (bp.NT == 4 && (N <= 2 || (N <= 8 && blocks(4, 1) * tiles(4) < 1024))) bp.NT = 2;
     const int64_t pass_bytes = bp.NT * NKs * per_row_pass;
     if (pass_bytes > kBatchLds) return false;
     const int64_t budget = pass_bytes <= kBatchLds / 2 ? kBatchLds / 2 : kBatchLds;
@@ -1012,10 +1017,12 @@ bool launch_batch(const BatchPlan& bp, hipStream_t st, const float* x, int N, ty
                      bp.geo, bp.CP)
     if (bp.RL == 2) {
         if (bp.NT == 8) RWKV_GB(2, 8);
-        else RWKV_GB(2, 4);
+        else if (bp.NT == 4) RWKV_GB(2, 4);
+        else RWKV_GB(2, 2);
     } else {
         if (bp.NT == 8) RWKV_GB(1, 8);
-        else RWKV_GB(1, 4);
+        else if (bp.NT == 4) RWKV_GB(1, 4);
+        else RWKV_GB(1, 2);
     }
 #undef RWKV_GB
     return true;

@@ -196,10 +196,11 @@ def test_fused_sym_gemv_equals_separate_bitwise(orc, bits):
     assert rel(want, fused.cpu().numpy()) < GEMV_TOL
 
 
-# batches run in their own kernel (one weight pass for 4 or 8 inputs, the
+# batches run in their own kernel (one weight pass for 2, 4 or 8 inputs, the
 # inputs staged in LDS chunk by chunk); 256 x 14336 stages 7 passes of 64
 # units in chunks (a partial last chunk); 3072 x 4096 takes tiles of 8 inputs
-# at N = 17 / 33 (a grid of >= 1024 workgroups) and of 4 below
+# at N = 17 / 33 (a grid of >= 1024 workgroups) and of 4 at N = 16; N = 2 and
+# N = 5 take tiles of 2
 BATCH_NS = (2, 5, 16, 17, 33)
 
 
