@@ -21,7 +21,7 @@ narrowing of :248-253).  There is no CPU fallback: a missing library raises.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Dict, Optional, Tuple
+from typing import Dict, List, Optional, Tuple
 
 import numpy as np
 import torch
@@ -61,6 +61,23 @@ class RWKVState:
         for a, b in zip((self.wkv, self.tmix_prev, self.cmix_prev, self.v_first),
                         (other.wkv, other.tmix_prev, other.cmix_prev, other.v_first)):
             a.copy_(b)
+        return self
+
+    def gather(self, rows) -> "RWKVState":
+        """RWKVBatchState.gather: a new state of the listed rows, in that order
+        (BatchGenerate.swift:105-108 drops the rows that stopped)."""
+        idx = torch.as_tensor(list(rows), dtype=torch.long, device=self.wkv.device)
+        c = RWKVState.__new__(RWKVState)
+        c.wkv, c.tmix_prev, c.cmix_prev = (t.index_select(1, idx) for t in (self.wkv, self.tmix_prev, self.cmix_prev))
+        c.v_first = self.v_first.index_select(0, idx)
+        return c
+
+    def scatter_(self, rows, sub: "RWKVState") -> "RWKVState":
+        """Writes the rows of `sub` back to the listed rows of this state."""
+        idx = torch.as_tensor(list(rows), dtype=torch.long, device=self.wkv.device)
+        for a, b in zip((self.wkv, self.tmix_prev, self.cmix_prev), (sub.wkv, sub.tmix_prev, sub.cmix_prev)):
+            a.index_copy_(1, idx, b)
+        self.v_first.index_copy_(0, idx, sub.v_first)
         return self
 
 
@@ -394,4 +411,73 @@ class X070Decoder:
         if not isinstance(ids, torch.Tensor):
             ids = torch.tensor(np.asarray(ids, np.int32).reshape(-1), device=self.device)
         return self.launch(ids.to(device=self.device, dtype=torch.int32).reshape(-1), state).clone()
+
+    def step_batch(self, ids, state: RWKVState) -> torch.Tensor:
+        """stepBatch (BatchGenerate.swift:56-63): one token per row of `state`."""
+        if len(ids) != state.n_rows:
+            raise ValueError(f"step_batch: {len(ids)} tokens for a batch of {state.n_rows}")
+        return self.step(ids, state)
+
+    def prefill_batch(self, prompts) -> Tuple[torch.Tensor, RWKVState]:
+        """prefillBatch (BatchGenerate.swift:37-53): logits [B, vocab] of each
+        prompt's last token and the batch state.  The rows step together
+        through the decode step, a row leaving the stepped set once its prompt
+        is consumed, so each row ends in the state of its prompt alone (the
+        reference runs its parallel pass with right padding and a mask; the
+        parallel prefill block is not part of this path)."""
+        if len(prompts) == 0:
+            raise ValueError("prefill_batch: no prompts")
+        if any(len(p) == 0 for p in prompts):
+            raise ValueError("prefill_batch: empty prompt")
+        B, T = len(prompts), max(len(p) for p in prompts)
+        state = self.new_state(B)
+        logits = torch.empty((B, self.V), dtype=torch.float32, device=self.device)
+        for t in range(T):
+            rows = [i for i, p in enumerate(prompts) if len(p) > t]
+            ids = [int(prompts[i][t]) for i in rows]
+            if len(rows) == B:
+                out = self.step(ids, state)
+            else:
+                sub = state.gather(rows)
+                out = self.step(ids, sub)
+                state.scatter_(rows, sub)
+            for j, i in enumerate(rows):
+                if len(prompts[i]) == t + 1:
+                    logits[i] = out[j]
+        return logits, state
+
+    def generate_batch(self, prompts, max_tokens: int, stop_tokens=()) -> List[List[int]]:
+        """generateBatch (BatchGenerate.swift:71-116) with the greedy choice
+        (the first largest logit; greedy does not depend on the per-row seed):
+        the continuations of several prompts in one batch.  A row that emits a
+        stop token keeps it as its last token and leaves the batch (its state
+        rows are gathered out); every row stops at `max_tokens`.  Stop strings
+        need a tokenizer and are not part of this path."""
+        if max_tokens < 0:
+            raise ValueError("generate_batch: max_tokens < 0")
+        B = len(prompts)
+        produced: List[List[int]] = [[] for _ in range(B)]
+        if B == 0 or max_tokens == 0:
+            return produced
+        stops = {int(t) for t in stop_tokens}
+        logits, state = self.prefill_batch(prompts)
+        alive = list(range(B))
+        for _ in range(max_tokens):
+            ids = torch.argmax(logits, dim=1).cpu().tolist()
+            nxt, keep = [], []
+            for row, i in enumerate(alive):
+                produced[i].append(int(ids[row]))
+                if ids[row] in stops:
+                    continue
+                nxt.append(int(ids[row]))
+                keep.append(row)
+            if not keep:
+                break
+            if len(keep) < len(alive):
+                state = state.gather(keep)
+                alive = [alive[r] for r in keep]
+            if len(produced[alive[0]]) >= max_tokens:
+                break
+            logits = self.step(nxt, state)
+        return produced
 

@@ -314,6 +314,39 @@ def test_decode_graph_replay_bitwise(tiny, decoder, N):
             assert torch.equal(st.wkv, eager_st.wkv) and torch.equal(st.cmix_prev, eager_st.cmix_prev), rep
 
 
+def test_generate_batch_rows_equal_prompts_alone(decoder):
+    # prefillBatch / generateBatch (BatchGenerate.swift:37-116) with the
+    # greedy choice: every row of the batch is bitwise its prompt alone (the
+    # batched GEMVs and row kernels are row-invariant; 4 heads keep the
+    # four-rows-per-wave WKV layout at every batch here)
+    case("generate_batch tiny")
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, TINY.vocab, n).tolist() for n in (3, 5, 1)]
+    logits, st = decoder.prefill_batch(prompts)
+    assert logits.shape == (3, TINY.vocab)
+    for i, p in enumerate(prompts):
+        li, si = decoder.prefill_batch([p])
+        assert torch.equal(logits[i], li[0]), i
+        for a, b in ((st.wkv, si.wkv), (st.tmix_prev, si.tmix_prev), (st.cmix_prev, si.cmix_prev)):
+            assert torch.equal(a[:, i], b[:, 0]), i
+    out = decoder.generate_batch(prompts, 6)
+    assert [len(o) for o in out] == [6, 6, 6]
+    assert out == [decoder.generate_batch([p], 6)[0] for p in prompts]
+    # the first token is the greedy choice of the prefill logits
+    assert [o[0] for o in out] == torch.argmax(logits, dim=1).cpu().tolist()
+    # a stop token ends its row (kept as the row's last token); the other
+    # rows go on after it leaves the batch
+    stop = out[0][2]
+    out2 = decoder.generate_batch(prompts, 6, stop_tokens=[stop])
+    assert out2[0] == out[0][:out[0].index(stop) + 1]
+    assert out2 == [decoder.generate_batch([p], 6, stop_tokens=[stop])[0] for p in prompts]
+    assert decoder.generate_batch(prompts, 0) == [[], [], []]
+    with pytest.raises(ValueError):
+        decoder.prefill_batch([[1, 2], []])
+    with pytest.raises(ValueError):
+        decoder.step_batch([1, 2], decoder.new_state(3))
+
+
 @pytest.fixture(scope="module")
 def proj_0b1():
     proj = syn.x070_projections(syn.X070_0B1, nthreads=8)
