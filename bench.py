@@ -701,7 +701,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU runs are not part of this build", file=sys.stderr)
+              "the path runs on one GPU; how it would shard is described, not built", file=sys.stderr)
         sys.exit(1)
     import torch
     from swiftrwkv_amd import _lib

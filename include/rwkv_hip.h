@@ -36,7 +36,7 @@ typedef enum {
     RWKV_OK = 0,
     RWKV_E_SHAPE = 1,        /* shape precondition violated (T, D, OUT, IN, rows ...) */
     RWKV_E_DTYPE = 2,        /* unsupported dtype code */
-    RWKV_E_UNSUPPORTED = 3,  /* valid request this build does not implement */
+    RWKV_E_UNSUPPORTED = 3,  /* valid request this library does not implement */
     RWKV_E_FORMAT = 4,       /* malformed .rwkvq / safetensors container or manifest */
     RWKV_E_HIP = 5,          /* HIP runtime error (launch, device) */
     RWKV_E_NULL = 6,         /* required pointer is NULL */

@@ -2,8 +2,9 @@
  * oracle.c — CPU restatement of the SwiftRWKV WKV-7 + .rwkvq hot path.
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the checker
- * (or, for cpu_baseline, as the timed CPU restatement).  The product path in
+ * cpu_baseline leg of bench.py may load this library, and only as the reference
+ * results are compared with (or, for cpu_baseline, as the timed CPU
+ * restatement).  The product path in
  * swiftrwkv_amd/ never calls it.
  *
  * Every function names the reference lines (Sources/... in RafaelUI/SwiftRWKV)

@@ -1,8 +1,9 @@
 """numpy front end of the C oracle (oracle/oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and by
-the cpu_baseline leg of bench.py, always as the checker (or the timed CPU
-restatement), never by the product package swiftrwkv_amd/.
+the cpu_baseline leg of bench.py, always as the reference results are
+compared with (or the timed CPU restatement), never by the product package
+swiftrwkv_amd/.
 
 Each wrapper names the reference lines its C function restates.
 """

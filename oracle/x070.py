@@ -1,8 +1,8 @@
 """fp64 restatement of the x070 decode step around the hot path.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and by
-the cpu_baseline leg of bench.py, always as the checker, never by the product
-package swiftrwkv_amd/.
+the cpu_baseline leg of bench.py, always as the reference results are
+compared with, never by the product package swiftrwkv_amd/.
 
 Follows Sources/RWKVGen/X070Generation.swift for an .rwkvq base with the step
 kernels on (the `fused` branch of tmixStep, :278-294), with fp32 activations:
