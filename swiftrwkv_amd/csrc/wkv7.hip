@@ -673,17 +673,29 @@ __global__ __launch_bounds__(R4 ? 1024 : 256) void wkv7_step_tail_kernel(
     const float A = a[base0 + l], W = w[base0 + l], K = k[base0 + l], Bv = b[base0 + l];
     const float R = r[base0 + l], V = v[base0 + row];
     const float* hin = h_in ? h_in + hb : nullptr;
-    const float y = R4 ? head_step4(hin, h_out + hb, blk, l, A, W, K, Bv, R, V)
-                       : head_step16(hin, h_out + hb, blk, l, A, W, K, Bv, R, V);
+    float S[R4 ? 4 : 16];
+    if constexpr (R4) load_state4(hin, blk, l, S);
+    else load_state16(hin, blk, l, S);
+    // the tail's other inputs (wave 0; r and k of column l are R and K) do not
+    // depend on the step: loaded with the state, not after the barrier
+    const int64_t e = base0 + l, he = (int64_t)hi * D + l;
+    float tv = 0.0f, trk = 0.0f, tlnw = 0.0f, tlnb = 0.0f, tg = 0.0f;
+    if (blk == 0) {   // uniform per wave
+        tv = v[e];
+        trk = rk[he];
+        tlnw = lnw[he];
+        tlnb = lnb[he];
+        tg = g[e];
+    }
+    float y;
+    if constexpr (R4) y = head_step4_regs(S, h_out + hb, blk, l, A, W, K, Bv, R, V);
+    else y = head_step16_regs(S, h_out + hb, blk, l, A, W, K, Bv, R, V);
     if ((R4 ? (l >> 2) : (l >> 4)) == 0) {
         ys[row] = y;
         if (wkv_out) wkv_out[base0 + row] = y;
     }
     __syncthreads();
-    if (blk == 0) {
-        const int64_t e = base0 + l, he = (int64_t)hi * D + l;
-        out[e] = head_tail(ys[l], r[e], k[e], v[e], rk[he], lnw[he], lnb[he], g[e], eps);
-    }
+    if (blk == 0) out[e] = head_tail(ys[l], R, K, tv, trk, tlnw, tlnb, tg, eps);
 }
 
 // ─────────────────────────────── host dispatch ───────────────────────────────
