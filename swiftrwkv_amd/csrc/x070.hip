@@ -32,11 +32,11 @@ __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp
 __device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_fast(-x)); }
 
 // Sum over the workgroup: per-wave butterfly, then the wave totals in wave
-// order; every thread gets the same value.
+// order; every thread gets the same value.  `red` (16 floats) is used once
+// per kernel, so no barrier is needed before it is written.
 __device__ __forceinline__ float block_total(float v, float* red) {
     const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     v = wave_total(v);
-    __syncthreads();   // `red` free from the previous use
     if ((threadIdx.x & 63) == 0) red[wave] = v;
     __syncthreads();
     float t = red[0];
@@ -73,14 +73,14 @@ __device__ __forceinline__ float2 row_stats(const float4 (&v)[PS], int D, float 
     float s = 0.0f;
 #pragma unroll
     for (int p = 0; p < PS; ++p) s += sum4(v[p]);
-    const float mean = block_total(s, red) / (float)D;
+    const float mean = block_total(s, red) / (float)D;   // red[0..15], then red[16..31]
     float q = 0.0f;
 #pragma unroll
     for (int p = 0; p < PS; ++p) {
         const float4 d = make_float4(v[p].x - mean, v[p].y - mean, v[p].z - mean, v[p].w - mean);
         q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
     }
-    return make_float2(mean, sqrtf(block_total(q, red) / (float)D + eps));
+    return make_float2(mean, sqrtf(block_total(q, red + 16) / (float)D + eps));
 }
 
 __device__ __forceinline__ float4 ln_apply(float4 x, float2 md, float4 w, float4 b) {
@@ -102,7 +102,7 @@ template <typename T, int PS>
 __global__ __launch_bounds__(1024) void layer_norm_kernel(const T* __restrict__ x, const int32_t* ids, int64_t rows,
                                                           const float* __restrict__ w, const float* __restrict__ b,
                                                           float* __restrict__ y, int D, float eps) {
-    __shared__ float red[16];
+    __shared__ float red[32];
     const int n = blockIdx.y, T4 = blockDim.x;
     int64_t src = n;
     bool bad = false;
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(1024) void shift_mix_kernel(const float* __restrict
                                                          const float* __restrict__ b, float* __restrict__ prev,
                                                          const float* __restrict__ coef, float* __restrict__ out0,
                                                          float* __restrict__ out1, int D, float eps) {
-    __shared__ float red[16];
+    __shared__ float red[32];
     const int n = blockIdx.y, T4 = blockDim.x;
     const float* row = x + (int64_t)n * D;
     const int c = 4 * ((int)blockIdx.x * T4 + (int)threadIdx.x);
