@@ -150,7 +150,7 @@ def test_lora_in(tiny, l, wdt):
 
 
 @pytest.mark.parametrize("l", [0, 1])
-@pytest.mark.parametrize("N", [1, 5])
+@pytest.mark.parametrize("N", [1, 5, 64])   # 64 rows x 4 heads: the sixteen-rows-per-wave layout
 def test_tmix_core(tiny, l, N):
     case(f"tmix_core layer={l} N={N}")
     p, _, _ = tiny
@@ -177,8 +177,11 @@ def test_tmix_core(tiny, l, N):
     tail, wkv_ref, vf_ref = X.core(p, l, r.astype(np.float64), k0.astype(np.float64), v0.astype(np.float64),
                                    [z.astype(np.float64) for z in la], v_first.astype(np.float64),
                                    wkv.astype(np.float64), H)
-    assert rel(tail, out.cpu().numpy()) < 1e-4
-    assert rel(wkv_ref, st_d.cpu().numpy()) < 1e-4
+    # an fp16 low-rank output may round to the other fp16 neighbour of the
+    # fp64 sum (one fp16 ulp); 64 rows meet such flips more often than 5
+    tol = 1e-4 if N < 64 else 5e-4
+    assert rel(tail, out.cpu().numpy()) < tol
+    assert rel(wkv_ref, st_d.cpu().numpy()) < tol
     assert rel(vf_ref, vf_d.cpu().numpy()) < 1e-6
 
 
@@ -207,22 +210,23 @@ def test_gemv_epilogues_bitwise(tiny, N):
                                       None))
 
 
-@pytest.mark.parametrize("N", [1, 3])
+@pytest.mark.parametrize("N", [1, 3, 64])   # 64 rows x 4 heads: the sixteen-rows-per-wave layout
 def test_decode_steps_match_oracle(tiny, decoder, N):
     case(f"decode tiny N={N}")
     p, _, W = tiny
     st = decoder.new_state(N)
     ost = X.State.zeros(TINY.n_layer, N, TINY.n_head)
     rng = np.random.default_rng(N)
+    tol = 1e-4 if N < 64 else 5e-4   # fp16 low-rank rounding flips, as in test_tmix_core
     _lib.reset_counters()
     for t in range(4):
         ids = rng.integers(0, TINY.vocab, N).astype(np.int32)
         got = decoder.step(ids, st).cpu().numpy()
         ref = X.step(p, W, ids, ost, TINY.n_layer, TINY.n_head)
-        assert rel(ref, got) < 1e-4, t
-    assert rel(ost.wkv, st.wkv.cpu().numpy()) < 1e-4
-    assert rel(ost.tmix_prev, st.tmix_prev.cpu().numpy()) < 1e-4
-    assert rel(ost.cmix_prev, st.cmix_prev.cpu().numpy()) < 1e-4
+        assert rel(ref, got) < tol, t
+    assert rel(ost.wkv, st.wkv.cpu().numpy()) < tol
+    assert rel(ost.tmix_prev, st.tmix_prev.cpu().numpy()) < tol
+    assert rel(ost.cmix_prev, st.cmix_prev.cpu().numpy()) < tol
     c = _lib.counters()
     Lr = TINY.n_layer
     assert c["x070"] == 4 * (2 + 4 * Lr)          # ln0 + ln_out + 4 per layer
