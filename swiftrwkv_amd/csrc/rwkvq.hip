@@ -425,6 +425,10 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
     const int XS = xl_stride(IN);
     const int NKs = geo.one_k ? 1 : NK;   // staged input rows per input
     const float* xsum = lds + NT * NKs * XS;
+    // A single input staged weights-first (a launch of few workgroups, bound by
+    // its round trips): each lane forms its units' Σx from the 32 inputs it
+    // reads, instead of a sums pass and a barrier after the staging.
+    constexpr bool LANE_SUMS = NT == 1 && !XF;
     auto compute_pass = [&](int p, const Raw (&W)[RL][KU], int n0, float (&acc)[NT][RL]) {
 #pragma unroll
         for (int ku = 0; ku < KU; ++ku) {
@@ -443,8 +447,15 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
                         xv[nn][4 * m] = f.x; xv[nn][4 * m + 1] = f.y; xv[nn][4 * m + 2] = f.z; xv[nn][4 * m + 3] = f.w;
                     }
                     if constexpr (F::SUMS) {
-                        const float2 s = reinterpret_cast<const float2*>(xsum)[j * NU + u];
-                        xs[nn][0] = s.x; xs[nn][1] = s.y;
+                        if constexpr (LANE_SUMS) {   // the staged sums' order: bitwise the same
+                            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                            for (int c = 0; c < 16; ++c) { s0 += xv[nn][c]; s1 += xv[nn][16 + c]; }
+                            xs[nn][0] = s0; xs[nn][1] = s1;
+                        } else {
+                            const float2 s = reinterpret_cast<const float2*>(xsum)[j * NU + u];
+                            xs[nn][0] = s.x; xs[nn][1] = s.y;
+                        }
                     }
                 } else {
                     const int n = min(n0 + nn, N - 1);
@@ -595,7 +606,7 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
                         *reinterpret_cast<const float4*>(src + c);
             }
             __syncthreads();
-            row_sums();
+            if constexpr (!LANE_SUMS) row_sums();
         }
         zero(acc);
         if constexpr (MULTI) {
