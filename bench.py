@@ -41,10 +41,10 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per launch of the head GEMV from two rocprofv3 counter passes
 # (FETCH_SIZE, WRITE_SIZE) over `bench.py --mode kernels`, calibrated against a
 # 256 MiB device copy; see profiles/hbm_traffic_decode_gemv_and_wkv7.md.
-HEAD_GEMV_TRAFFIC_BYTES = 29489569
+HEAD_GEMV_TRAFFIC_BYTES = 29494797
 # The same for the average GEMV launch of one 0.1B decode token (eager tokens
 # over rotated weight copies); same profile.
-DECODE_GEMV_TRAFFIC_BYTES = 1743217
+DECODE_GEMV_TRAFFIC_BYTES = 1744043
 VALU_PEAK_TFLOPS = 157.3
 
 
