@@ -317,6 +317,72 @@ rwkv_status rwkvq_entry(const rwkvq_file* f, int64_t i, const char** name, const
 /* "__metadata__" string value for `key`, or NULL. */
 const char* rwkvq_metadata(const rwkvq_file* f, const char* key);
 
+/* The .rwkvq manifest (the "rwkvq" JSON string of __metadata__), validated as
+ * a whole against the container's buffers: replaces the checks of
+ * RwkvqSidecar.init(rwkvq:only:fusingSym:) (Sources/RWKVQuant/RwkvqFile.swift:254-492)
+ * with the tensor kinds of RwkvqKind / RwkvqTensorInfo (RwkvqSidecar.swift:60-99).
+ * Beyond the reference's checks, every buffer an sb6 / sym / asym decode reads
+ * must hold exactly the element count its (OUT, IN) needs, so no repack or
+ * kernel can read past a buffer of an accepted file. */
+typedef enum { RWKVQ_DENSE = 0, RWKVQ_SB6 = 1, RWKVQ_SYM = 2, RWKVQ_ASYM = 3, RWKVQ_RTN = 4 } rwkvq_kind;
+
+/* What a rejected manifest was rejected for (the RwkvqError cases
+ * malformedManifest / missingBuffer / shapeMismatch, RwkvqSidecar.swift:25-56). */
+typedef enum {
+    RWKVQ_FINDING_NONE = 0,
+    RWKVQ_FINDING_MALFORMED = 1,
+    RWKVQ_FINDING_MISSING_BUFFER = 2,
+    RWKVQ_FINDING_SHAPE = 3
+} rwkvq_finding_kind;
+
+typedef struct {
+    int kind;              /* rwkvq_finding_kind */
+    char tensor[192];      /* manifest key ("" for file-level problems) */
+    char buffer[32];       /* field name ("gw_qsqm" ...) for MISSING_BUFFER / SHAPE */
+    int n_expected, n_got; /* SHAPE: the dims the layout needs / the file holds */
+    int64_t expected[4], got[4];
+} rwkvq_finding;
+
+typedef struct {
+    const char* key;       /* valid while the manifest lives */
+    int kind;              /* rwkvq_kind */
+    int ndim;
+    int64_t shape[8];      /* manifest shape; [OUT, IN] for matrices */
+    int bits, xbits;       /* code width; sb6 high-bit planes (0..2) */
+    int group_size, super_block;
+    int transposed;        /* stored [in, out]: the Linear convention needs a turn */
+    int packed;            /* rtn: codes_packed present */
+    int64_t outliers;      /* rtn: outlier count */
+} rwkvq_tensor;
+
+typedef struct {
+    int format_version;
+    const char* naming;    /* "world" when absent */
+    int64_t n_layer, n_embd, head_size, vocab_size;
+} rwkvq_model;
+
+typedef struct rwkvq_manifest rwkvq_manifest;
+/* Reads and checks the manifest of `f` (which must stay open while the
+ * manifest is used).  On RWKV_E_FORMAT, `finding` (may be NULL) says what was
+ * wrong and rwkv_last_error() says it in words. */
+rwkv_status rwkvq_manifest_read(const rwkvq_file* f, int max_format_version, rwkvq_manifest** out,
+                                rwkvq_finding* finding);
+void rwkvq_manifest_free(rwkvq_manifest* m);
+int64_t rwkvq_manifest_count(const rwkvq_manifest* m);
+/* Entry `i` in key order. */
+rwkv_status rwkvq_manifest_tensor(const rwkvq_manifest* m, int64_t i, rwkvq_tensor* out);
+rwkv_status rwkvq_manifest_model(const rwkvq_manifest* m, rwkvq_model* out);
+/* Entry `i` of an sb6 / sym matrix in the loader layouts (rwkv_sb6_to_k3 /
+ * rwkv_sym_interleave of its disk buffers), written to caller host buffers:
+ * qblk [OUT, IN/32·(16+4·xbits)], qsqm [OUT, IN/32·2], ddm [OUT, IN/256·2];
+ * sym: qblk [OUT, IN] (8-bit) or [OUT, IN/32·24] (6-bit), qs [OUT, IN/16],
+ * d [OUT, IN/256].  Rows are packed densely, so pointing into row i·OUT of a
+ * larger buffer places a matrix inside a row-concatenated group. */
+rwkv_status rwkvq_read_sb6(const rwkvq_file* f, const rwkvq_manifest* m, int64_t i, uint8_t* qblk,
+                           uint8_t* qsqm, uint16_t* ddm);
+rwkv_status rwkvq_read_sym(const rwkvq_file* f, const rwkvq_manifest* m, int64_t i, uint8_t* qblk,
+                           uint8_t* qs, uint16_t* d);
+
 /* ───────────────────────────── measurement ───────────────────────────── */
 
 /* Measurement hook, no counterpart in the reference (its benches time whole

@@ -41,6 +41,24 @@ class Counters(ctypes.Structure):
                                  "step_tail", "sb6_fused", "sym_rows", "x070")]
 
 
+class Finding(ctypes.Structure):
+    """rwkvq_finding: why a manifest was rejected."""
+    _fields_ = [("kind", I), ("tensor", ctypes.c_char * 192), ("buffer", ctypes.c_char * 32),
+                ("n_expected", I), ("n_got", I), ("expected", L * 4), ("got", L * 4)]
+
+
+class TensorDesc(ctypes.Structure):
+    """rwkvq_tensor: one validated manifest entry."""
+    _fields_ = [("key", ctypes.c_char_p), ("kind", I), ("ndim", I), ("shape", L * 8), ("bits", I), ("xbits", I),
+                ("group_size", I), ("super_block", I), ("transposed", I), ("packed", I), ("outliers", L)]
+
+
+class ModelDesc(ctypes.Structure):
+    """rwkvq_model: the manifest's model-level fields."""
+    _fields_ = [("format_version", I), ("naming", ctypes.c_char_p), ("n_layer", L), ("n_embd", L),
+                ("head_size", L), ("vocab_size", L)]
+
+
 # name → (restype, argtypes)
 _SIGS = {
     "rwkv_abi_version": (I, []),
@@ -83,6 +101,13 @@ _SIGS = {
                         ctypes.POINTER(I), ctypes.POINTER(ctypes.POINTER(L)), ctypes.POINTER(P),
                         ctypes.POINTER(L)]),
     "rwkvq_metadata": (ctypes.c_char_p, [P, ctypes.c_char_p]),
+    "rwkvq_manifest_read": (I, [P, I, ctypes.POINTER(P), ctypes.POINTER(Finding)]),
+    "rwkvq_manifest_free": (None, [P]),
+    "rwkvq_manifest_count": (L, [P]),
+    "rwkvq_manifest_tensor": (I, [P, L, ctypes.POINTER(TensorDesc)]),
+    "rwkvq_manifest_model": (I, [P, ctypes.POINTER(ModelDesc)]),
+    "rwkvq_read_sb6": (I, [P, P, L, P, P, P]),
+    "rwkvq_read_sym": (I, [P, P, L, P, P, P]),
     "rwkv_time_next_launch": (I, [P, P]),
     "rwkv_get_counters": (None, [ctypes.POINTER(Counters)]),
     "rwkv_reset_counters": (None, []),

@@ -18,7 +18,7 @@ LIB = os.path.join(PKG, "libswiftrwkv_hip.so")
 ARCH = os.environ.get("SWIFTRWKV_ARCH", "gfx950")
 
 HIP_SOURCES = ["wkv7.hip", "rwkvq.hip", "x070.hip"]
-HOST_SOURCES = ["host.cpp"]
+HOST_SOURCES = ["host.cpp", "manifest.cpp"]
 
 # Packed-FP32 VALU ops are disabled for every device compile.
 HIP_FLAGS = [

@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "common.h"
+#include "container.h"
 
 namespace rwkv {
 
@@ -376,178 +377,10 @@ rwkv_status rwkvq_encode_sym(const float* w, int64_t OUT, int64_t IN, int bits, 
 }  // extern "C"
 
 // ─────────────────────────────── safetensors container ───────────────────────────────
-namespace {
-
-// Minimal JSON reader for safetensors headers: objects, arrays, strings,
-// integers / numbers, true / false / null.
-struct JVal {
-    enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
-    bool b = false;
-    double num = 0;
-    bool is_int = false;
-    int64_t i = 0;
-    std::string s;
-    std::vector<JVal> arr;
-    std::vector<std::pair<std::string, JVal>> obj;
-};
-
-struct JParser {
-    const char* p;
-    const char* end;
-    std::string err;
-
-    void ws() {
-        while (p < end && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) ++p;
-    }
-    bool fail(const char* m) {
-        if (err.empty()) err = m;
-        return false;
-    }
-    static void put_utf8(std::string& out, uint32_t cp) {
-        if (cp < 0x80) out += (char)cp;
-        else if (cp < 0x800) { out += (char)(0xc0 | (cp >> 6)); out += (char)(0x80 | (cp & 0x3f)); }
-        else if (cp < 0x10000) {
-            out += (char)(0xe0 | (cp >> 12)); out += (char)(0x80 | ((cp >> 6) & 0x3f)); out += (char)(0x80 | (cp & 0x3f));
-        } else {
-            out += (char)(0xf0 | (cp >> 18)); out += (char)(0x80 | ((cp >> 12) & 0x3f));
-            out += (char)(0x80 | ((cp >> 6) & 0x3f)); out += (char)(0x80 | (cp & 0x3f));
-        }
-    }
-    bool hex4(uint32_t& v) {
-        if (end - p < 4) return fail("short \\u escape");
-        v = 0;
-        for (int e = 0; e < 4; ++e) {
-            char c = *p++;
-            v <<= 4;
-            if (c >= '0' && c <= '9') v |= (uint32_t)(c - '0');
-            else if (c >= 'a' && c <= 'f') v |= (uint32_t)(c - 'a' + 10);
-            else if (c >= 'A' && c <= 'F') v |= (uint32_t)(c - 'A' + 10);
-            else return fail("bad \\u escape");
-        }
-        return true;
-    }
-    bool str(std::string& out) {
-        if (p >= end || *p != '"') return fail("expected string");
-        ++p;
-        while (p < end && *p != '"') {
-            char c = *p++;
-            if (c != '\\') { out += c; continue; }
-            if (p >= end) return fail("bad escape");
-            char e = *p++;
-            switch (e) {
-                case '"': out += '"'; break;
-                case '\\': out += '\\'; break;
-                case '/': out += '/'; break;
-                case 'b': out += '\b'; break;
-                case 'f': out += '\f'; break;
-                case 'n': out += '\n'; break;
-                case 'r': out += '\r'; break;
-                case 't': out += '\t'; break;
-                case 'u': {
-                    uint32_t cp;
-                    if (!hex4(cp)) return false;
-                    if (cp >= 0xd800 && cp < 0xdc00 && end - p >= 6 && p[0] == '\\' && p[1] == 'u') {
-                        p += 2;
-                        uint32_t lo;
-                        if (!hex4(lo)) return false;
-                        cp = 0x10000 + ((cp - 0xd800) << 10) + (lo - 0xdc00);
-                    }
-                    put_utf8(out, cp);
-                    break;
-                }
-                default: return fail("bad escape");
-            }
-        }
-        if (p >= end) return fail("unterminated string");
-        ++p;
-        return true;
-    }
-    bool value(JVal& v, int depth) {
-        if (depth > 64) return fail("nesting too deep");
-        ws();
-        if (p >= end) return fail("unexpected end");
-        char c = *p;
-        if (c == '{') {
-            v.kind = JVal::Obj;
-            ++p;
-            ws();
-            if (p < end && *p == '}') { ++p; return true; }
-            for (;;) {
-                ws();
-                std::string key;
-                if (!str(key)) return false;
-                ws();
-                if (p >= end || *p != ':') return fail("expected ':'");
-                ++p;
-                JVal child;
-                if (!value(child, depth + 1)) return false;
-                v.obj.emplace_back(std::move(key), std::move(child));
-                ws();
-                if (p < end && *p == ',') { ++p; continue; }
-                if (p < end && *p == '}') { ++p; return true; }
-                return fail("expected ',' or '}'");
-            }
-        }
-        if (c == '[') {
-            v.kind = JVal::Arr;
-            ++p;
-            ws();
-            if (p < end && *p == ']') { ++p; return true; }
-            for (;;) {
-                JVal child;
-                if (!value(child, depth + 1)) return false;
-                v.arr.push_back(std::move(child));
-                ws();
-                if (p < end && *p == ',') { ++p; continue; }
-                if (p < end && *p == ']') { ++p; return true; }
-                return fail("expected ',' or ']'");
-            }
-        }
-        if (c == '"') { v.kind = JVal::Str; return str(v.s); }
-        if (end - p >= 4 && !std::strncmp(p, "true", 4)) { v.kind = JVal::Bool; v.b = true; p += 4; return true; }
-        if (end - p >= 5 && !std::strncmp(p, "false", 5)) { v.kind = JVal::Bool; p += 5; return true; }
-        if (end - p >= 4 && !std::strncmp(p, "null", 4)) { v.kind = JVal::Null; p += 4; return true; }
-        if (c == '-' || (c >= '0' && c <= '9')) {
-            const char* s0 = p;
-            if (*p == '-') ++p;
-            bool integral = true;
-            while (p < end && ((*p >= '0' && *p <= '9') || *p == '.' || *p == 'e' || *p == 'E' || *p == '+' || *p == '-')) {
-                if (*p == '.' || *p == 'e' || *p == 'E') integral = false;
-                ++p;
-            }
-            std::string tok(s0, p);
-            v.kind = JVal::Num;
-            v.num = std::strtod(tok.c_str(), nullptr);
-            v.is_int = integral;
-            if (integral) v.i = std::strtoll(tok.c_str(), nullptr, 10);
-            return true;
-        }
-        return fail("unexpected character");
-    }
-};
-
-struct Entry {
-    std::string name, dtype;
-    std::vector<int64_t> shape;
-    int64_t begin = 0, end = 0;
-};
-
-int64_t dtype_bytes(const std::string& t) {
-    static const std::map<std::string, int64_t> m = {{"BOOL", 1}, {"U8", 1},  {"I8", 1},  {"I16", 2}, {"U16", 2},
-                                                     {"F16", 2},  {"BF16", 2}, {"I32", 4}, {"U32", 4}, {"F32", 4},
-                                                     {"F64", 8},  {"I64", 8},  {"U64", 8}};
-    auto it = m.find(t);
-    return it == m.end() ? -1 : it->second;
-}
-
-}  // namespace
-
-struct rwkvq_file {
-    void* map = nullptr;
-    size_t size = 0;
-    std::vector<Entry> entries;   // sorted by name
-    std::map<std::string, std::string> metadata;
-};
+using rwkv::Entry;
+using rwkv::JParser;
+using rwkv::JVal;
+using rwkv::dtype_bytes;
 
 extern "C" {
 
@@ -614,19 +447,26 @@ rwkv_status rwkvq_open(const char* path, rwkvq_file** out) {
         const int64_t esz = dtype_bytes(e.dtype);
         RWKV_REQUIRE(esz > 0, RWKV_E_FORMAT, "%s: dtype %s of buffer %s is not supported", path, e.dtype.c_str(),
                      e.name.c_str());
+        // Every product and sum below is checked: a header is untrusted input,
+        // and a wrapped size would let an entry point past the mapping.
         int64_t count = 1;
+        bool wrapped = false;
         for (auto& s : shape->arr) {
             RWKV_REQUIRE(s.kind == JVal::Num && s.is_int && s.i >= 0, RWKV_E_FORMAT, "%s: bad shape of %s", path,
                          e.name.c_str());
             e.shape.push_back(s.i);
-            count *= s.i;
+            wrapped = wrapped || __builtin_mul_overflow(count, s.i, &count);
         }
+        int64_t nbytes = 0;
+        wrapped = wrapped || __builtin_mul_overflow(count, esz, &nbytes);
+        RWKV_REQUIRE(!wrapped, RWKV_E_FORMAT, "%s: the shape of %s overflows 64-bit sizes", path, e.name.c_str());
         RWKV_REQUIRE(off->arr[0].kind == JVal::Num && off->arr[0].is_int && off->arr[1].kind == JVal::Num &&
                          off->arr[1].is_int,
                      RWKV_E_FORMAT, "%s: bad data_offsets of %s", path, e.name.c_str());
         e.begin = off->arr[0].i;
         e.end = off->arr[1].i;
-        RWKV_REQUIRE(e.begin >= 0 && e.end >= e.begin && base + e.end <= (int64_t)size && e.end - e.begin == count * esz,
+        const int64_t payload = (int64_t)size - base;   // > 0: base <= size was checked above
+        RWKV_REQUIRE(e.begin >= 0 && e.end >= e.begin && e.end <= payload && e.end - e.begin == nbytes,
                      RWKV_E_FORMAT, "%s: buffer %s offsets [%lld, %lld] disagree with its shape and dtype %s", path,
                      e.name.c_str(), (long long)e.begin, (long long)e.end, e.dtype.c_str());
         e.begin += base;

@@ -255,15 +255,27 @@ def wkv7_step_forward(r, w, k, v, a, b, h) -> Tuple[torch.Tensor, torch.Tensor]:
     return out, h_new
 
 
+def _check_inplace(t: torch.Tensor, shape, device, what: str) -> None:
+    """A caller buffer the kernel writes: fp32, contiguous, 16-byte aligned,
+    of exactly `shape`, on the inputs' device."""
+    if (t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != tuple(shape) or t.data_ptr() % 16
+            or t.device != device):
+        raise ValueError(f"{what} must be a contiguous, 16-byte aligned fp32 tensor of shape {list(shape)} on "
+                         f"{device}, got {tuple(t.shape)} {t.dtype} on {t.device}")
+
+
 def wkv7_step_(r, w, k, v, a, b, h, out=None) -> torch.Tensor:
     """In-place decode step for B rows: h [B,H,S,S] fp32 is updated in place
     (the C ABI allows h_in == h_out).  Returns out [B,H,S]."""
     (r, w, k, v, a, b), dt = _prep([r, w, k, v, a, b], ndim_ok=(3,))
     B, H, S = r.shape
-    if h.dtype != torch.float32 or not h.is_contiguous() or tuple(h.shape) != (B, H, S, S) or h.data_ptr() % 16:
-        raise ValueError("in-place state must be a contiguous fp32 [B,H,S,S] tensor")
+    if S != WKV7_HEAD_SIZE:
+        raise ValueError(f"S ({S}) must equal HEAD_SIZE {WKV7_HEAD_SIZE}")
+    _check_inplace(h, (B, H, S, S), r.device, "in-place state")
     if out is None:
         out = torch.empty((B, H, S), dtype=torch.float32, device=r.device)
+    else:
+        _check_inplace(out, (B, H, S), r.device, "out")
     _lib.call("rwkv_wkv7_step", _ptr(r), _ptr(w), _ptr(k), _ptr(v), _ptr(a), _ptr(b), dt, _ptr(h), _ptr(out),
               _ptr(h), B, H, _stream(r))
     return out
@@ -355,14 +367,14 @@ def wkv7_step_tail_(r, w, k, v, a, b, h, r_k, ln_weight, ln_bias, gate, eps: flo
     B, H, S = r.shape
     if S != WKV7_HEAD_SIZE or any(tuple(x.shape) != (B, H, S) for x in xs):
         raise ValueError(f"step+tail: inputs must share shape [B,H,{WKV7_HEAD_SIZE}]")
-    if h.dtype != torch.float32 or not h.is_contiguous() or tuple(h.shape) != (B, H, S, S) or h.data_ptr() % 16:
-        raise ValueError("in-place state must be a contiguous fp32 [B,H,S,S] tensor")
     dev = r.device
+    if dev.type != "cuda":
+        raise ValueError(f"step+tail inputs must live on a ROCm device, got {dev}")
+    _check_inplace(h, (B, H, S, S), dev, "in-place state")
     r_, w_, k_, v_, a_, b_, g_ = (_aligned(x.to(device=dev, dtype=torch.float32)) for x in xs)
     rk_, lw_, lb_ = (_aligned(x.reshape(H * S).to(device=dev, dtype=torch.float32)) for x in (r_k, ln_weight, ln_bias))
-    if wkv_out is not None and (wkv_out.dtype != torch.float32 or not wkv_out.is_contiguous()
-                                or tuple(wkv_out.shape) != (B, H, S)):
-        raise ValueError("wkv_out must be a contiguous fp32 [B,H,S] tensor")
+    if wkv_out is not None:
+        _check_inplace(wkv_out, (B, H, S), dev, "wkv_out")
     out = torch.empty((B, H * S), dtype=torch.float32, device=dev)
     _lib.call("rwkv_wkv7_step_tail", _ptr(r_), _ptr(w_), _ptr(k_), _ptr(v_), _ptr(a_), _ptr(b_), _ptr(h), _ptr(h),
               _ptr(rk_), _ptr(lw_), _ptr(lb_), _ptr(g_), _ptr(wkv_out) if wkv_out is not None else None, _ptr(out),

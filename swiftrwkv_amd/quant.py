@@ -41,15 +41,15 @@ class MalformedManifest(RwkvqError):
 
 
 class MissingBuffer(RwkvqError):
-    def __init__(self, tensor: str, buffer: str):
+    def __init__(self, tensor: str, buffer: str, message: Optional[str] = None):
         self.tensor, self.buffer = tensor, buffer
-        super().__init__(f"no buffer {buffer} for tensor {tensor}")
+        super().__init__(message or f"no buffer {buffer} for tensor {tensor}")
 
 
 class ShapeMismatch(RwkvqError):
-    def __init__(self, tensor: str, expected, got):
+    def __init__(self, tensor: str, expected, got, message: Optional[str] = None):
         self.tensor, self.expected, self.got = tensor, list(expected), list(got)
-        super().__init__(f"{tensor}: expected shape {self.expected}, file has {self.got}")
+        super().__init__(message or f"{tensor}: expected shape {self.expected}, file has {self.got}")
 
 
 class UnsupportedKind(RwkvqError):
@@ -194,6 +194,154 @@ class RwkvqContainer:
         return np.frombuffer(raw, dtype=np.uint8).copy().view(npdt).reshape(shape)
 
 
+# ───────────────────────────── manifest ─────────────────────────────
+
+_KINDS = (RwkvqKind.dense, RwkvqKind.sb6, RwkvqKind.sym, RwkvqKind.asym, RwkvqKind.rtn)   # rwkvq_kind order
+
+
+class RwkvqManifest:
+    """The .rwkvq manifest of an open container, checked by the C reader
+    (rwkvq_manifest_read) as a whole before anything is loaded: the tensor
+    table (key → RwkvqTensorInfo) and the model fields.  Lives as long as
+    the container it was read from."""
+
+    def __init__(self, box: RwkvqContainer, max_format_version: int):
+        lib = _lib.lib()
+        h, finding = ctypes.c_void_p(), _lib.Finding()
+        st = lib.rwkvq_manifest_read(box._h, max_format_version, ctypes.byref(h), ctypes.byref(finding))
+        if st != _lib.RWKV_OK:
+            raise _finding_error(finding, lib.rwkv_last_error().decode())
+        self._box, self._h = box, h
+        model = _lib.ModelDesc()
+        _lib.check(lib.rwkvq_manifest_model(h, ctypes.byref(model)))
+        self.format_version = model.format_version
+        self.naming = model.naming.decode()
+        self.n_layer, self.n_embd = model.n_layer, model.n_embd
+        self.head_size, self.vocab_size = model.head_size, model.vocab_size
+        self.infos: Dict[str, RwkvqTensorInfo] = {}
+        self._index: Dict[str, int] = {}
+        d = _lib.TensorDesc()
+        for i in range(lib.rwkvq_manifest_count(h)):
+            _lib.check(lib.rwkvq_manifest_tensor(h, i, ctypes.byref(d)))
+            key = d.key.decode()
+            self._index[key] = i
+            self.infos[key] = RwkvqTensorInfo(
+                kind=_KINDS[d.kind], shape=tuple(d.shape[j] for j in range(d.ndim)), bits=d.bits, xbits=d.xbits,
+                group_size=d.group_size, super_block=d.super_block, packed=bool(d.packed),
+                outlier_count=d.outliers, transposed=bool(d.transposed))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            _lib.lib().rwkvq_manifest_free(self._h)
+            self._h = None
+
+    @property
+    def keys(self) -> List[str]:
+        return list(self.infos)
+
+    def buffer(self, key: str, field: str, as_dtype=None) -> np.ndarray:
+        """A buffer of an entry, as stored (the dense / asym / rtn op-chain inputs)."""
+        return self._box.array(f"{key}::{field}", as_dtype)
+
+    def read_into(self, key: str, bufs: Tuple[np.ndarray, ...]) -> None:
+        """The loader layout of an sb6 / sym matrix into (qblk, qsqm|qs, ddm|d):
+        contiguous host arrays, or row slices of a group's arrays."""
+        info = self.infos[key]
+        fn = "rwkvq_read_sb6" if info.kind == RwkvqKind.sb6 else "rwkvq_read_sym"
+        _lib.call(fn, self._box._h, self._h, self._index[key], *[_np_ptr(b) for b in bufs])
+
+
+def _finding_error(f: "_lib.Finding", message: str) -> RwkvqError:
+    tensor, buffer = f.tensor.decode(), f.buffer.decode()
+    if f.kind == 2:
+        return MissingBuffer(tensor, buffer, message)
+    if f.kind == 3:
+        return ShapeMismatch(tensor, f.expected[:f.n_expected], f.got[:f.n_got], message)
+    return MalformedManifest(message)
+
+
+def _loader_arrays(info: RwkvqTensorInfo, rows: int) -> Tuple[np.ndarray, ...]:
+    """Host arrays for `rows` rows of an sb6 / sym matrix in the loader layouts."""
+    IN = info.in_features
+    if info.kind == RwkvqKind.sb6:
+        return (np.empty((rows, IN // 32 * (16 + 4 * info.xbits)), np.uint8), np.empty((rows, IN // 16), np.uint8),
+                np.empty((rows, IN // 128), np.uint16))
+    width = IN if info.bits == 8 else IN // 32 * 24
+    return np.empty((rows, width), np.uint8), np.empty((rows, IN // 16), np.uint8), np.empty((rows, IN // 256), np.uint16)
+
+
+def _loader_fields(kind: RwkvqKind) -> Tuple[str, str, str]:
+    return ("qblk", "qsqm", "ddm") if kind == RwkvqKind.sb6 else ("qblk", "qs", "d")
+
+
+def _to_device(a: np.ndarray, device, as_torch=None) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if as_torch is not None:
+        t = t.view(as_torch)
+    return t.to(device)
+
+
+def _read_tensor(man: RwkvqManifest, key: str, device) -> Dict[str, torch.Tensor]:
+    """The device buffers one entry is kept in (names "<key>::<field>")."""
+    info = man.infos[key]
+    if info.is_quantized_base:
+        host = _loader_arrays(info, info.out_features)
+        man.read_into(key, host)
+        fields = _loader_fields(info.kind)
+        return {f"{key}::{f}": _to_device(a, device, torch.float16 if a.dtype == np.uint16 else None)
+                for f, a in zip(fields, host)}
+    if info.kind == RwkvqKind.dense:
+        raw = man.buffer(key, "dense")
+        bf16 = man._box.dtype(f"{key}::dense") == "BF16"
+        return {f"{key}::dense": _to_device(raw, device, torch.bfloat16 if bf16 else None)}
+    fields = ("codes", "gw_scale", "gw_min") if info.kind == RwkvqKind.asym else (
+        ("codes_packed" if info.packed else "codes"), "scale")
+    return {f"{key}::{f}": _to_device(man.buffer(key, f), device) for f in fields}
+
+
+def _sym_fusable(members: List[RwkvqTensorInfo]) -> bool:
+    """The sym fusion condition (RwkvqSymGEMV.swift:314-339): ≥ 2 sym matrices
+    of one shape and code width whose row-concatenation the sym GEMV takes,
+    with a whole number of its 4-row groups per matrix."""
+    if len(members) < 2 or any(m is None or m.kind != RwkvqKind.sym for m in members):
+        return False
+    m0 = members[0]
+    if any(m.shape != m0.shape or m.bits != m0.bits for m in members):
+        return False
+    return rwkvq_sym_gemv_applies(m0.out_features * len(members), m0.in_features, m0.bits, 1) and \
+        m0.out_features % 4 == 0
+
+
+def _plan_fused_reads(groups: Dict[str, List[str]], infos: Dict[str, RwkvqTensorInfo],
+                      admitted: set) -> Dict[str, List[str]]:
+    """The groups to read as one buffer: every member admitted and the
+    group fusable; a key joins at most one group (the first that claims it)."""
+    plan, claimed = {}, set()
+    for gid, keys in groups.items():
+        if any(k not in admitted or k in claimed for k in keys):
+            continue
+        if _sym_fusable([infos.get(k) for k in keys]):
+            plan[gid] = list(keys)
+            claimed.update(keys)
+    return plan
+
+
+def _read_sym_group(man: RwkvqManifest, keys: List[str], arrays: Dict[str, torch.Tensor],
+                    device) -> "RwkvqSymFusedGroup":
+    """Reads the members into row ranges of one set of host arrays, moves it
+    to the device once, and files each member as a row view."""
+    info = man.infos[keys[0]]
+    OUT = info.out_features
+    host = _loader_arrays(info, OUT * len(keys))
+    for i, k in enumerate(keys):
+        man.read_into(k, tuple(a[i * OUT:(i + 1) * OUT] for a in host))
+    dev = [_to_device(a, device, torch.float16 if a.dtype == np.uint16 else None) for a in host]
+    for i, k in enumerate(keys):
+        for f, t in zip(_loader_fields(info.kind), dev):
+            arrays[f"{k}::{f}"] = t[i * OUT:(i + 1) * OUT]
+    return RwkvqSymFusedGroup(list(keys), dev[0], dev[1], dev[2], OUT, info.in_features, info.bits)
+
+
 # ───────────────────────────── host repack ─────────────────────────────
 
 def _np_ptr(a: Optional[np.ndarray]):
@@ -228,6 +376,10 @@ def rwkvq_sb6_to_k3(codes_packed, qsqm, d, dm, qh, qh2, shape, group_size=32, su
 
     c = [np.ascontiguousarray(x, dtype=np.uint8) if x is not None else None
          for x in (codes_packed, qh, qh2, qsqm)] + [bits16(d), bits16(dm)]
+    need = (OUT * IN // 2, OUT * IN // 8, OUT * IN // 8, OUT * (IN // 256) * 12, OUT * (IN // 256), OUT * (IN // 256))
+    for name, x, n in zip(("codes_packed", "qh", "qh2", "qsqm", "d", "dm"), c, need):
+        if x is not None and x.size != n:
+            raise ValueError(f"sb6 repack: {name} holds {x.size} elements, [{OUT}, {IN}] needs {n}")
     qblk = np.empty((OUT, NB * (16 + 4 * xbits)), np.uint8)
     k3 = np.empty((OUT, NB * 2), np.uint8)
     ddm = np.empty((OUT, (NB // 8) * 2), np.uint16)
@@ -240,6 +392,9 @@ def rwkvq_sym_interleave(codes_packed, qh, qh2, shape) -> np.ndarray:
     OUT, IN = shape
     qblk = np.empty((OUT, IN // 32 * 24), np.uint8)
     c = [np.ascontiguousarray(x, dtype=np.uint8) for x in (codes_packed, qh, qh2)]
+    for name, x, n in zip(("codes_packed", "qh", "qh2"), c, (OUT * IN // 2, OUT * IN // 8, OUT * IN // 8)):
+        if x.size != n:
+            raise ValueError(f"sym interleave: {name} holds {x.size} bytes, [{OUT}, {IN}] needs {n}")
     _lib.call("rwkv_sym_interleave", *[_np_ptr(x) for x in c], OUT, IN, _np_ptr(qblk))
     return qblk
 
@@ -491,187 +646,29 @@ class RwkvqSidecar:
     @classmethod
     def from_rwkvq(cls, path: str, only: Optional[Callable[[str], bool]] = None,
                    fusing_sym: Optional[Dict[str, List[str]]] = None, device="cuda") -> "RwkvqSidecar":
-        """Read a .rwkvq directly (RwkvqFile.swift:254-492): validate the whole
-        manifest, load (and repack) the buffers of the tensors `only` admits."""
-        p = os.path.expanduser(path)
-        box = RwkvqContainer(p)
-        text = box.metadata.get("rwkvq")
+        """Read a .rwkvq directly (the reference's RwkvqSidecar.init(rwkvq:only:fusingSym:),
+        RwkvqFile.swift:254-492).  The C reader checks the whole manifest
+        against the file first (rwkvq_manifest_read); then the buffers of the
+        tensors `only` admits are repacked from the mapped file and moved to
+        `device`.  A `fusing_sym` group whose members all qualify is read
+        straight into one row-concatenated buffer, the members becoming row
+        views of it."""
+        box = RwkvqContainer(os.path.expanduser(path))
         try:
-            root = json.loads(text) if text is not None else None
-        except json.JSONDecodeError:
-            root = None
-        if not isinstance(root, dict):
-            raise MalformedManifest(f"{p}: not .rwkvq — no rwkvq key in __metadata__")
-        if root.get("format") != "rwkvq":
-            raise MalformedManifest(f"{p}: format {root.get('format')}")
-        version = root.get("format_version", 0)
-        if not isinstance(version, int) or version > cls.max_format_version:
-            raise MalformedManifest(f"{p}: format_version {version} newer than {cls.max_format_version}")
-        tensor_dict = root.get("tensors")
-        if not isinstance(tensor_dict, dict):
-            raise MalformedManifest(f'{p}: no "tensors" section')
-        naming = root.get("naming", "world")
-        groups = dict(fusing_sym or {})
-        arrays: Dict[str, torch.Tensor] = {}
-        infos: Dict[str, RwkvqTensorInfo] = {}
-
-        def to_dev(a: np.ndarray, as_t=None) -> torch.Tensor:
-            t = torch.from_numpy(np.ascontiguousarray(a))
-            if as_t is not None:
-                t = t.view(as_t)
-            return t.to(device)
-
-        def process(key: str):
-            m = tensor_dict.get(key)
-            if not isinstance(m, dict) or not isinstance(m.get("shape"), list) or not isinstance(m.get("kind"), str):
-                raise MalformedManifest(f"{p}: no shape or layout for {key}")
-            try:
-                kind = RwkvqKind(m["kind"])
-            except ValueError:
-                raise MalformedManifest(f"unknown layout {m['kind']} of {key}") from None
-            shape = tuple(m["shape"])
-            load = only(key) if only else True
-            bits = m.get("bits", 16)
-            gs = m.get("gw_gs", 0)
-            sb = m.get("gw_sb", 0)
-            transposed = m.get("transposed")
-            if not isinstance(transposed, bool):
-                transposed = naming == "world" and is_raw_lora_world(key)
-
-            def need(field, as_dtype=None) -> np.ndarray:
-                a = box.array(f"{key}::{field}", as_dtype)
-                if a is None:
-                    raise MissingBuffer(key, field)
-                return a
-
-            def dims(field) -> Tuple[int, ...]:
-                s = box.shape(f"{key}::{field}")
-                if s is None:
-                    raise MissingBuffer(key, field)
-                return s
-
-            def n_blocks_check(got: int, what: str):
-                nb = m.get("n_blocks")
-                if isinstance(nb, int) and nb > 0 and nb != got:
-                    raise MalformedManifest(f"{key}: {what} covers {got} blocks, the manifest says {nb}")
-
-            xbits, packed, outliers = 0, False, 0
-            if kind == RwkvqKind.dense:
-                dims("dense")
-                if load:
-                    a = need("dense")
-                    arrays[f"{key}::dense"] = (to_dev(a, torch.bfloat16) if box.dtype(f"{key}::dense") == "BF16"
-                                               else to_dev(a))
-            elif kind == RwkvqKind.asym:
-                if len(shape) != 2 or gs <= 0:
-                    raise MalformedManifest(f"incomplete asym entry for {key}")
-                scale_shape = dims("gw_scale")
-                nb = (shape[1] + gs - 1) // gs
-                if not scale_shape or scale_shape[-1] != nb:
-                    raise ShapeMismatch(key, [shape[0], nb], scale_shape)
-                n_blocks_check(nb, "gw_scale")
-                dims("codes")
-                dims("gw_min")
-                if load:
-                    for f in ("codes", "gw_scale", "gw_min"):
-                        arrays[f"{key}::{f}"] = to_dev(need(f))
-            elif kind == RwkvqKind.rtn:
-                packed = box.contains(f"{key}::codes_packed")
-                if not packed:
-                    dims("codes")
-                dims("scale")
-                if load:
-                    f = "codes_packed" if packed else "codes"
-                    arrays[f"{key}::{f}"] = to_dev(need(f))
-                    arrays[f"{key}::scale"] = to_dev(need("scale"))
-                os_ = box.shape(f"{key}::outlier_indices")
-                outliers = os_[0] if os_ else 0
-            elif kind == RwkvqKind.sb6:
-                if not (len(shape) == 2 and gs == 32 and sb == 8 and shape[1] % (gs * sb) == 0):
-                    raise MalformedManifest(
-                        f"{key}: sb6 is read with block 32 and super-block 8 (file: gw_gs={gs}, gw_sb={sb}, shape {list(shape)})")
-                n_blocks_check(shape[1] // gs, "sb6")
-                want = (shape[0], shape[1] // (gs * sb), 12)
-                got = dims("gw_qsqm")
-                if tuple(got) != want:
-                    raise ShapeMismatch(key, want, got)
-                dims("codes_packed")
-                dims("gw_d")
-                dims("gw_dm")
-                xbits = int(box.contains(f"{key}::gw_qh")) + int(box.contains(f"{key}::gw_qh2"))
-                if bits != 4 + xbits:
-                    raise MalformedManifest(f"{key}: bits={bits}, but the file has {xbits} bit planes")
-                if load:
-                    qblk, k3, ddm, xb = rwkvq_sb6_to_k3(
-                        need("codes_packed"), need("gw_qsqm"), need("gw_d", np.uint16), need("gw_dm", np.uint16),
-                        box.array(f"{key}::gw_qh"), box.array(f"{key}::gw_qh2"), shape, gs, sb)
-                    assert xb == xbits
-                    arrays[f"{key}::qblk"] = to_dev(qblk)
-                    arrays[f"{key}::qsqm"] = to_dev(k3)
-                    arrays[f"{key}::ddm"] = to_dev(ddm, torch.float16)
-            elif kind == RwkvqKind.sym:
-                if not (len(shape) == 2 and gs == 16 and sb == 16):
-                    raise MalformedManifest(f"{key}: sym is read with block 16 and super-block 16 (file: gw_gs={gs}, gw_sb={sb})")
-                OUT, IN = shape
-                if IN % gs:
-                    raise MalformedManifest(f"{key}: sym, IN={IN} is not a multiple of block 16")
-                qs_shape, d_shape = dims("gw_qs"), dims("gw_d")
-                n_blocks_check(qs_shape[-1] if qs_shape else 0, "gw_qs")
-                if tuple(qs_shape) != (OUT, IN // gs) or len(d_shape) != 2 or d_shape[1] * sb != IN // gs:
-                    raise ShapeMismatch(key, [OUT, IN // gs], qs_shape)
-                eight = box.contains(f"{key}::codes")
-                if eight:
-                    if bits != 8:
-                        raise MalformedManifest(f"{key}: sym with a codes buffer at bits={bits}")
-                else:
-                    if bits != 6 or IN % 32:
-                        raise MalformedManifest(f"{key}: sym with codes_packed at bits={bits}, IN={IN}")
-                    dims("codes_packed")
-                    dims("gw_qh")
-                    dims("gw_qh2")
-                if load:
-                    if eight:
-                        qblk = need("codes", np.uint8)
-                    else:
-                        qblk = rwkvq_sym_interleave(need("codes_packed"), need("gw_qh"), need("gw_qh2"), shape)
-                    arrays[f"{key}::qblk"] = to_dev(qblk)
-                    arrays[f"{key}::qs"] = to_dev(need("gw_qs", np.uint8))
-                    arrays[f"{key}::d"] = to_dev(need("gw_d", np.uint16), torch.float16)
-            infos[key] = RwkvqTensorInfo(kind=kind, shape=shape, bits=bits, xbits=xbits, group_size=gs,
-                                         super_block=sb, packed=packed, outlier_count=outliers,
-                                         transposed=transposed)
-
-        def elements(key):
-            m = tensor_dict.get(key)
-            s = m.get("shape", []) if isinstance(m, dict) else []
-            n = 1
-            for v in s:
-                n *= v
-            return n
-
-        group_of = {k: gid for gid, keys in groups.items() for k in keys}
-        fused: Dict[str, RwkvqSymFusedGroup] = {}
-        done = set()
-        ordered = sorted(tensor_dict.keys(), key=lambda k: (-elements(k), k))
-        for key in ordered:
-            if key in done:
-                continue
-            gid = group_of.get(key)
-            members = groups.get(gid) if gid is not None else None
-            if members is None or not all(k in tensor_dict and (only(k) if only else True) for k in members):
-                process(key)
-                done.add(key)
-                continue
-            for k in members:
-                if k not in done:
-                    process(k)
-                    done.add(k)
-            g = _fuse_sym_group(members, infos, arrays)
-            if g is not None:
-                fused[gid] = g
-        box.close()
-        return cls(arrays, infos, naming, root.get("n_layer", 0), root.get("n_embd", 0),
-                   root.get("head_size", 64), root.get("vocab_size", 0), fused)
+            man = RwkvqManifest(box, cls.max_format_version)
+            admitted = [k for k in man.keys if only is None or only(k)]
+            plan = _plan_fused_reads(fusing_sym or {}, man.infos, set(admitted))
+            arrays: Dict[str, torch.Tensor] = {}
+            fused: Dict[str, RwkvqSymFusedGroup] = {}
+            for gid, members in plan.items():
+                fused[gid] = _read_sym_group(man, members, arrays, device)
+            grouped = {k for members in plan.values() for k in members}
+            for key in admitted:
+                if key not in grouped:
+                    arrays.update(_read_tensor(man, key, device))
+            return cls(arrays, man.infos, man.naming, man.n_layer, man.n_embd, man.head_size, man.vocab_size, fused)
+        finally:
+            box.close()
 
     # ── queries ──
     @property
@@ -728,55 +725,26 @@ class RwkvqSidecar:
 
     def build_dense_weights(self, dtype=torch.float16) -> Dict[str, torch.Tensor]:
         """The x070 dictionary of everything but the quantised projections
-        (RwkvqSidecar.buildDenseWeights, RwkvqFullConvert.swift:49-140): layer
-        norms, token-shift coefficients, k_k / k_a / r_k as [H, S], the
-        low-rank branches in the Linear convention (A [rank, D], B [D, rank];
-        a tensor whose manifest says `transposed` is turned, and the shape is
-        checked), w0 / a0 / v0 flattened into the B biases, the v branch only
-        for layers > 0, ln_x and the cmix coefficient; plus `emb.weight`
-        dequantised once (load(fromSidecar:), X070Backbone.swift)."""
+        (the reference's RwkvqSidecar.buildDenseWeights, RwkvqFullConvert.swift:49-140,
+        plus `emb.weight` dequantised once as its load(fromSidecar:) does),
+        produced by interpreting the name table _X070_BODY: each row maps one
+        world key to one x070 key through a shape rule."""
         if not (self.n_layer > 0 and self.n_embd > 0 and self.head_size > 0):
             raise IncompleteManifest("n_layer / n_embd / head_size missing or zero: the manifest does not describe "
                                      "the model")
         if not any(t.kind == RwkvqKind.dense for t in self.tensors.values()):
             raise PartialExport(len(self.tensors))
         D, S = self.n_embd, self.head_size
-        H = D // S
-        dq = lambda k: self.dequantize(k, dtype)
-
-        def low_rank(k: str, is_a: bool) -> torch.Tensor:
-            info = self.tensors.get(k)
-            if info is None:
-                raise MissingBuffer(k, "manifest")
-            v = dq(k)
-            if info.transposed:
-                v = v.t().contiguous()
-            if v.dim() != 2 or v.shape[1 if is_a else 0] != D:
-                raise ShapeMismatch(k, [-1, D] if is_a else [D, -1], list(v.shape))
-            return v
-
-        out = {"ln0.weight": dq("blocks.0.ln0.weight"), "ln0.bias": dq("blocks.0.ln0.bias"),
-               "ln_out.weight": dq("ln_out.weight"), "ln_out.bias": dq("ln_out.bias")}
-        for i in range(self.n_layer):
-            b = f"blocks.{i}."
-            att, ffn, P = b + "att.", b + "ffn.", b + "tmix."
-            for n in ("ln1", "ln2"):
-                out[b + n + ".weight"] = dq(b + n + ".weight")
-                out[b + n + ".bias"] = dq(b + n + ".bias")
-            for x in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g"):
-                out[P + x] = dq(att + x)
-            for x in ("k_k", "k_a", "r_k"):
-                out[P + x] = dq(att + x).reshape(H, S)
-            branches = [("w", True), ("a", True), ("g", False)] + ([("v", True)] if i > 0 else [])
-            for n, bias in branches:
-                out[P + n + "_lora_A.weight"] = low_rank(att + n + "1", True)
-                out[P + n + "_lora_B.weight"] = low_rank(att + n + "2", False)
-                if bias:
-                    out[P + n + "_lora_B.bias"] = dq(att + n + "0").reshape(D)
-            out[P + "ln_x.weight"] = dq(att + "ln_x.weight")
-            out[P + "ln_x.bias"] = dq(att + "ln_x.bias")
-            out[b + "cmix.x_k"] = dq(ffn + "x_k")
-        out["emb.weight"] = dq("emb.weight")
+        out: Dict[str, torch.Tensor] = {}
+        for layer in [None] + list(range(self.n_layer)):
+            for x070, world, rule in (_X070_GLOBAL if layer is None else _X070_LAYER):
+                if layer == 0 and ".tmix.v_" in x070:
+                    continue   # layer 0 has no value-residual branch to mix with
+                src = world.format(i=layer)
+                if src not in self.tensors:
+                    raise MissingBuffer(src, "manifest")
+                out[x070.format(i=layer)] = _x070_shape(rule, self.dequantize(src, dtype), self.tensors[src], src,
+                                                        D, S)
         return out
 
     def sym_row_table(self, key: str) -> Optional[RwkvqSymRowTable]:
@@ -850,32 +818,39 @@ class RwkvqSidecar:
         return rwkvq_sym_gemv(x, *[self.arrays[n] for n in names], info.out_features, info.in_features, info.bits)
 
     def fusing_sym(self, groups: Dict[str, List[str]]) -> "RwkvqSidecar":
-        """Concatenate the rows of each sym group into one buffer; the member
-        buffers become row slices of it (RwkvqSymGEMV.swift:298-310)."""
-        a = dict(self.arrays)
-        fused = dict(self.sym_fused)
-        for gid, keys in groups.items():
-            if gid in fused:
-                continue
-            g = _fuse_sym_group(keys, self.tensors, a)
-            if g is not None:
-                fused[gid] = g
-        return RwkvqSidecar(a, dict(self.tensors), self.naming, self.n_layer, self.n_embd, self.head_size,
-                            self.vocab_size, fused, self.sb6_fused)
+        """RwkvqSymGEMV.swift:298-310 on a loaded sidecar: each qualifying sym
+        group becomes one row-concatenated buffer, its members row views of it;
+        a group that does not qualify is left as separate matrices."""
+        return self._fusing(groups, "sym")
 
     def fusing_sb6(self, groups: Dict[str, List[str]]) -> "RwkvqSidecar":
-        """fusing_sym for sb6 groups (an extension: r/k/v of an sb6 model in
-        one launch).  Member buffers become row slices of the group buffer."""
-        a = dict(self.arrays)
-        fused = dict(self.sb6_fused)
+        """fusing_sym for sb6 groups (an extension: the r/k/v matrices of an
+        sb6 model in one launch)."""
+        return self._fusing(groups, "sb6")
+
+    def _fusing(self, groups: Dict[str, List[str]], kind: str) -> "RwkvqSidecar":
+        arrays = dict(self.arrays)
+        made = dict(self.sym_fused if kind == "sym" else self.sb6_fused)
         for gid, keys in groups.items():
-            if gid in fused:
+            if gid in made:
+                continue   # already one buffer: concatenating its views again would copy
+            infos = [self.tensors.get(k) for k in keys]
+            fields = _loader_fields(RwkvqKind(kind))
+            loaded = all(f"{k}::{f}" in arrays for k in keys for f in fields)
+            if not loaded or not (_sym_fusable(infos) if kind == "sym" else _sb6_fusable(infos)):
                 continue
-            g = _fuse_sb6_group(keys, self.tensors, a)
-            if g is not None:
-                fused[gid] = g
-        return RwkvqSidecar(a, dict(self.tensors), self.naming, self.n_layer, self.n_embd, self.head_size,
-                            self.vocab_size, self.sym_fused, fused)
+            OUT = infos[0].out_features
+            cat = [torch.cat([arrays[f"{k}::{f}"] for k in keys], 0) for f in fields]
+            for i, k in enumerate(keys):
+                for f, t in zip(fields, cat):
+                    arrays[f"{k}::{f}"] = t[i * OUT:(i + 1) * OUT]
+            if kind == "sym":
+                made[gid] = RwkvqSymFusedGroup(list(keys), *cat, OUT, infos[0].in_features, infos[0].bits)
+            else:
+                made[gid] = RwkvqSb6FusedGroup(list(keys), *cat, OUT, infos[0].in_features, infos[0].xbits)
+        sym, sb6 = (made, self.sb6_fused) if kind == "sym" else (self.sym_fused, made)
+        return RwkvqSidecar(arrays, dict(self.tensors), self.naming, self.n_layer, self.n_embd, self.head_size,
+                            self.vocab_size, sym, sb6)
 
     def sb6_gemv_fused(self, gid: str, xstack: torch.Tensor) -> Optional[torch.Tensor]:
         """K sb6 projections in one launch: xstack [K, IN] → [K, out_per]."""
@@ -896,58 +871,49 @@ class RwkvqSidecar:
         return y.reshape(K, g.out_per)
 
 
-def _fuse_sb6_group(keys: List[str], tensors: Dict[str, RwkvqTensorInfo],
-                    arrays: Dict[str, torch.Tensor]) -> Optional[RwkvqSb6FusedGroup]:
-    """sb6 counterpart of _fuse_sym_group: same shape and xbits, every member
-    taken by the sb6 GEMV.  None (arrays untouched) when the group does not
-    qualify."""
-    if len(keys) < 2:
-        return None
-    first = tensors.get(keys[0])
-    if first is None or first.kind != RwkvqKind.sb6:
-        return None
-    for k in keys:
-        t = tensors.get(k)
-        if (t is None or t.kind != RwkvqKind.sb6 or t.shape != first.shape or t.xbits != first.xbits
-                or t.super_block != first.super_block
-                or any(f"{k}::{f}" not in arrays for f in ("qblk", "qsqm", "ddm"))):
-            return None
-    if not rwkvq_sb6_gemv_applies(first.out_features, first.in_features, first.xbits, first.super_block, 1):
-        return None
-    OUT = first.out_features
-    cat = {f: torch.cat([arrays[f"{k}::{f}"] for k in keys], 0) for f in ("qblk", "qsqm", "ddm")}
-    for i, k in enumerate(keys):
-        for f in ("qblk", "qsqm", "ddm"):
-            arrays[f"{k}::{f}"] = cat[f][i * OUT:(i + 1) * OUT]
-    return RwkvqSb6FusedGroup(list(keys), cat["qblk"], cat["qsqm"], cat["ddm"], OUT, first.in_features, first.xbits)
+def _sb6_fusable(members: List[RwkvqTensorInfo]) -> bool:
+    """≥ 2 sb6 matrices of one shape and format that the sb6 GEMV takes."""
+    if len(members) < 2 or any(m is None or m.kind != RwkvqKind.sb6 for m in members):
+        return False
+    m0 = members[0]
+    if any(m.shape != m0.shape or m.xbits != m0.xbits or m.super_block != m0.super_block for m in members):
+        return False
+    return rwkvq_sb6_gemv_applies(m0.out_features, m0.in_features, m0.xbits, m0.super_block, 1)
 
 
-def _fuse_sym_group(keys: List[str], tensors: Dict[str, RwkvqTensorInfo],
-                    arrays: Dict[str, torch.Tensor]) -> Optional[RwkvqSymFusedGroup]:
-    """RwkvqSymGEMV.swift:314-339.  Returns None (arrays untouched) when the
-    group does not qualify."""
-    if len(keys) < 2:
-        return None
-    first = tensors.get(keys[0])
-    if first is None or first.kind != RwkvqKind.sym:
-        return None
-    for k in keys:
-        t = tensors.get(k)
-        if (t is None or t.kind != RwkvqKind.sym or t.shape != first.shape or t.bits != first.bits
-                or any(f"{k}::{f}" not in arrays for f in ("qblk", "qs", "d"))):
-            return None
-    if not rwkvq_sym_gemv_applies(first.out_features * len(keys), first.in_features, first.bits, 1) \
-            or first.out_features % 4:
-        return None
-    OUT = first.out_features
-    qblk = torch.cat([arrays[f"{k}::qblk"] for k in keys], 0)
-    qs = torch.cat([arrays[f"{k}::qs"] for k in keys], 0)
-    d = torch.cat([arrays[f"{k}::d"] for k in keys], 0)
-    for i, k in enumerate(keys):
-        arrays[f"{k}::qblk"] = qblk[i * OUT:(i + 1) * OUT]
-        arrays[f"{k}::qs"] = qs[i * OUT:(i + 1) * OUT]
-        arrays[f"{k}::d"] = d[i * OUT:(i + 1) * OUT]
-    return RwkvqSymFusedGroup(list(keys), qblk, qs, d, OUT, first.in_features, first.bits)
+# x070 names of the dense model body from the world names of a full export
+# (the mapping of RwkvqFullConvert.swift:49-140): (x070 key, world key, rule),
+# {i} = layer.  Rules: "as_is"; "heads" → [H, S]; "bias" → [D];
+# "rank_in" / "rank_out" → the Linear convention A [rank, D] / B [D, rank],
+# turned when the manifest marks the tensor `transposed`.
+_X070_GLOBAL = (("ln0.weight", "blocks.0.ln0.weight", "as_is"), ("ln0.bias", "blocks.0.ln0.bias", "as_is"),
+                ("ln_out.weight", "ln_out.weight", "as_is"), ("ln_out.bias", "ln_out.bias", "as_is"),
+                ("emb.weight", "emb.weight", "as_is"))
+_X070_LAYER = (
+    tuple((f"blocks.{{i}}.{n}.{p}", f"blocks.{{i}}.{n}.{p}", "as_is") for n in ("ln1", "ln2") for p in ("weight", "bias"))
+    + tuple((f"blocks.{{i}}.tmix.x_{c}", f"blocks.{{i}}.att.x_{c}", "as_is") for c in "rwkvag")
+    + tuple((f"blocks.{{i}}.tmix.{c}", f"blocks.{{i}}.att.{c}", "heads") for c in ("k_k", "k_a", "r_k"))
+    + tuple((f"blocks.{{i}}.tmix.{b}_lora_A.weight", f"blocks.{{i}}.att.{b}1", "rank_in") for b in "wagv")
+    + tuple((f"blocks.{{i}}.tmix.{b}_lora_B.weight", f"blocks.{{i}}.att.{b}2", "rank_out") for b in "wagv")
+    + tuple((f"blocks.{{i}}.tmix.{b}_lora_B.bias", f"blocks.{{i}}.att.{b}0", "bias") for b in "wav")
+    + (("blocks.{i}.tmix.ln_x.weight", "blocks.{i}.att.ln_x.weight", "as_is"),
+       ("blocks.{i}.tmix.ln_x.bias", "blocks.{i}.att.ln_x.bias", "as_is"),
+       ("blocks.{i}.cmix.x_k", "blocks.{i}.ffn.x_k", "as_is")))
+
+
+def _x070_shape(rule: str, v: torch.Tensor, info: RwkvqTensorInfo, key: str, D: int, S: int) -> torch.Tensor:
+    if rule == "as_is":
+        return v
+    if rule == "heads":
+        return v.reshape(D // S, S)
+    if rule == "bias":
+        return v.reshape(D)
+    if info.transposed:
+        v = v.t().contiguous()
+    side = 1 if rule == "rank_in" else 0
+    if v.dim() != 2 or v.shape[side] != D:
+        raise ShapeMismatch(key, [-1, D] if side else [D, -1], list(v.shape))
+    return v
 
 
 # ───────────────────────────── asym / rtn (op chains, as in the reference) ─────────────────────────────

@@ -223,7 +223,7 @@ def test_container_rejects_foreign_files(tmp_path):
         quant.RwkvqSidecar.from_rwkvq(str(zipf), device="cpu")
     plain = tmp_path / "plain.safetensors"
     quant.write_safetensors(str(plain), {"x": np.float32([1, 2, 3])})
-    with pytest.raises(quant.MalformedManifest, match="not .rwkvq"):
+    with pytest.raises(quant.MalformedManifest, match="not an .rwkvq file"):
         quant.RwkvqSidecar.from_rwkvq(str(plain), device="cpu")
     good = tmp_path / "good.rwkvq"
     _small_file(str(good))
@@ -242,8 +242,15 @@ def test_container_rejects_foreign_files(tmp_path):
     bad.write_bytes((10 ** 6).to_bytes(8, "little") + b"{}")
     with pytest.raises(quant.MalformedManifest, match="outside the file"):
         quant.RwkvqContainer(str(bad))
+    big = 2 ** 63
     for hdr in (b'{"x":{"dtype":"Q7","shape":[1],"data_offsets":[0,1]}}',
-                b'{"x":{"dtype":"F32","shape":[2],"data_offsets":[0,4]}}'):
+                b'{"x":{"dtype":"F32","shape":[2],"data_offsets":[0,4]}}',
+                # offsets whose sum with the header end wraps past 2^63
+                b'{"x":{"dtype":"U8","shape":[8],"data_offsets":[%d,%d]}}' % (big - 11, big - 3),
+                # a shape whose byte size wraps int64
+                b'{"x":{"dtype":"F32","shape":[%d,4],"data_offsets":[0,0]}}' % (2 ** 62),
+                # an integer beyond int64
+                b'{"x":{"dtype":"U8","shape":[8],"data_offsets":[0,%d]}}' % (2 ** 70)):
         f = tmp_path / "hdr.rwkvq"
         f.write_bytes(len(hdr).to_bytes(8, "little") + hdr + bytes(8))
         with pytest.raises(quant.MalformedManifest):
@@ -260,7 +267,7 @@ def test_manifest_validation_errors(tmp_path):
         quant.write_rwkvq(p, {"k.weight": (entry, buffers)}, **kw)
         return p
 
-    with pytest.raises(quant.MalformedManifest, match="block 32"):
+    with pytest.raises(quant.MalformedManifest, match="blocks of 32 columns"):
         quant.RwkvqSidecar.from_rwkvq(write(dict(m, gw_gs=64), bufs), device="cpu")
     with pytest.raises(quant.MalformedManifest, match="bit planes"):
         quant.RwkvqSidecar.from_rwkvq(write(dict(m, bits=5), bufs), device="cpu")
@@ -268,7 +275,7 @@ def test_manifest_validation_errors(tmp_path):
         quant.RwkvqSidecar.from_rwkvq(write(m, dict(bufs, gw_qsqm=bufs["gw_qsqm"].reshape(16, 24))), device="cpu")
     with pytest.raises(quant.MissingBuffer):
         quant.RwkvqSidecar.from_rwkvq(write(m, {k: v for k, v in bufs.items() if k != "gw_dm"}), device="cpu")
-    with pytest.raises(quant.MalformedManifest, match="blocks"):
+    with pytest.raises(quant.MalformedManifest, match="n_blocks"):
         quant.RwkvqSidecar.from_rwkvq(write(dict(m, n_blocks=3), bufs), device="cpu")
     with pytest.raises(quant.MalformedManifest, match="format_version"):
         quant.RwkvqSidecar.from_rwkvq(write(m, bufs, format_version=3), device="cpu")
@@ -277,6 +284,99 @@ def test_manifest_validation_errors(tmp_path):
     sm, sbufs = quant.sym_entry(w, 8)
     with pytest.raises(quant.MalformedManifest, match="codes buffer"):
         quant.RwkvqSidecar.from_rwkvq(write(dict(sm, bits=6), sbufs), device="cpu")
+
+
+@pytest.mark.parametrize("bits", [4, 5, 6])
+def test_short_sb6_buffers_are_rejected(tmp_path, bits):
+    """Every buffer an sb6 decode reads must be complete: a truncated one is a
+    ShapeMismatch naming it, before any repack could read past it."""
+    w = (np.random.default_rng(2).standard_normal((16, 512)) * 0.02).astype(np.float32)
+    m, bufs = quant.sb6_entry(w, bits)
+    p = str(tmp_path / "s.rwkvq")
+    for field in bufs:
+        short = dict(bufs, **{field: bufs[field].reshape(-1)[:-1]})
+        quant.write_rwkvq(p, {"k.weight": (m, short)})
+        with pytest.raises(quant.ShapeMismatch) as e:
+            quant.RwkvqSidecar.from_rwkvq(p, device="cpu")
+        assert e.value.tensor == "k.weight" and field in str(e.value), field
+    if bits == 6:   # a second high-bit plane without the first
+        quant.write_rwkvq(p, {"k.weight": (dict(m, bits=5), {f: v for f, v in bufs.items() if f != "gw_qh"})})
+        with pytest.raises(quant.MalformedManifest, match="gw_qh2"):
+            quant.RwkvqSidecar.from_rwkvq(p, device="cpu")
+
+
+@pytest.mark.parametrize("bits", [8, 6])
+def test_short_sym_buffers_are_rejected(tmp_path, bits):
+    w = (np.random.default_rng(3).standard_normal((16, 512)) * 0.02).astype(np.float32)
+    m, bufs = quant.sym_entry(w, bits)
+    p = str(tmp_path / "s.rwkvq")
+    for field in bufs:
+        short = dict(bufs, **{field: bufs[field].reshape(-1)[:-1]})
+        quant.write_rwkvq(p, {"k.weight": (m, short)})
+        with pytest.raises(quant.ShapeMismatch) as e:
+            quant.RwkvqSidecar.from_rwkvq(p, device="cpu")
+        assert field in str(e.value), field
+    # a scale table that is the right size but not [OUT, IN/256]
+    quant.write_rwkvq(p, {"k.weight": (m, dict(bufs, gw_d=bufs["gw_d"].reshape(32, 1)))})
+    with pytest.raises(quant.ShapeMismatch, match="gw_d"):
+        quant.RwkvqSidecar.from_rwkvq(p, device="cpu")
+
+
+def test_repack_wrappers_check_buffer_sizes():
+    w = (np.random.default_rng(5).standard_normal((8, 256)) * 0.02).astype(np.float32)
+    d = quant.encode_sb6(w, 5)
+    args = [d["codes_packed"], d["gw_qsqm"], d["gw_d"], d["gw_dm"], d["gw_qh"], None]
+    quant.rwkvq_sb6_to_k3(*args, (8, 256))
+    for i in range(5):
+        bad = list(args)
+        bad[i] = bad[i].reshape(-1)[:-1]
+        with pytest.raises(ValueError):
+            quant.rwkvq_sb6_to_k3(*bad, (8, 256))
+    s6 = quant.encode_sym(w, 6)
+    quant.rwkvq_sym_interleave(s6["codes_packed"], s6["gw_qh"], s6["gw_qh2"], (8, 256))
+    with pytest.raises(ValueError):
+        quant.rwkvq_sym_interleave(s6["codes_packed"][:-1], s6["gw_qh"], s6["gw_qh2"], (8, 256))
+
+
+def test_manifest_transposed_default_follows_world_naming(tmp_path):
+    """The reader's default for `transposed` is the world naming rule
+    (RwkvqFileTests.swift:123-127) unless the manifest says otherwise."""
+    keys = ["blocks.1.att.w1", "blocks.1.att.g2", "blocks.1.att.w0", "blocks.1.ffn.key.weight", "x.att.a1"]
+    ent = lambda: ({"kind": "dense", "shape": [4]}, {"dense": np.ones(4, np.float16)})
+    p = str(tmp_path / "n.rwkvq")
+    quant.write_rwkvq(p, {k: ent() for k in keys} | {"blocks.2.att.v1": ({"kind": "dense", "shape": [4],
+                                                                           "transposed": False},
+                                                                          {"dense": np.ones(4, np.float16)})})
+    sc = quant.RwkvqSidecar.from_rwkvq(p, device="cpu")
+    for k in keys:
+        assert sc.tensors[k].transposed == quant.is_raw_lora_world(k), k
+    assert not sc.tensors["blocks.2.att.v1"].transposed
+    quant.write_rwkvq(p, {k: ent() for k in keys}, naming="x070")
+    assert not any(t.transposed for t in quant.RwkvqSidecar.from_rwkvq(p, device="cpu").tensors.values())
+
+
+def test_sym_group_read_at_load_equals_fusing_after(tmp_path):
+    """A fusing_sym group read straight into one buffer holds the same bytes
+    as the members loaded alone and concatenated afterwards; members are row
+    views of it; a group with a non-sym member is not fused."""
+    rng = np.random.default_rng(4)
+    T = {f"blocks.0.att.{m}.weight": quant.sym_entry((rng.standard_normal((32, 256)) * 0.02).astype(np.float32), 6)
+         for m in ("receptance", "key", "value")}
+    T["blocks.0.att.output.weight"] = quant.sb6_entry((rng.standard_normal((32, 256)) * 0.02).astype(np.float32), 4)
+    p = str(tmp_path / "g.rwkvq")
+    quant.write_rwkvq(p, T)
+    rkv = [f"blocks.0.att.{m}.weight" for m in ("receptance", "key", "value")]
+    groups = {"att0": rkv, "mixed": ["blocks.0.att.output.weight", rkv[0]]}
+    at_load = quant.RwkvqSidecar.from_rwkvq(p, fusing_sym=groups, device="cpu")
+    after = quant.RwkvqSidecar.from_rwkvq(p, device="cpu").fusing_sym(groups)
+    assert set(at_load.sym_fused) == set(after.sym_fused) == {"att0"}
+    for f in ("qblk", "qs", "d"):
+        a, b = getattr(at_load.sym_fused["att0"], f), getattr(after.sym_fused["att0"], f)
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), f
+        for i, k in enumerate(rkv):
+            v = at_load.arrays[f"{k}::{f}"]
+            assert v.untyped_storage().data_ptr() == a.untyped_storage().data_ptr(), (k, f)
+            assert torch.equal(v.view(torch.uint8), a[i * 32:(i + 1) * 32].view(torch.uint8)), (k, f)
 
 
 def test_lora_orientation_naming_rule():
