@@ -380,3 +380,39 @@ def test_tail_formula_and_closed_form(orc):
         got = orc.wkv_tail_f64(c, r, k, v, rk, lnw, lnb, g, N, H, S)
         want = (lnb + ((r.astype(np.float64) * k * rk).sum(-1, keepdims=True) * v).reshape(N, D)) * g
         assert np.allclose(got, want, rtol=1e-13, atol=1e-13)
+
+
+@pytest.mark.parametrize("xbits", [0, 1])
+def test_cpu_baseline_matvec_matches_fp64(orc, xbits):
+    """The timed CPU restatement of the non-kernel projection path (dequantise
+    to fp32, fp32 x·Wᵀ) agrees with the fp64 anchor, on any thread count."""
+    OUT, IN = 96, 1024
+    t = make_sb6(OUT, IN, xbits, np.random.default_rng(30 + xbits))
+    qblk, qsqm, ddm, xb = orc.sb6_to_k3(t["cp"], t["qh"], t["qh2"], t["qsqm_disk"], t["d"].view(np.uint16),
+                                        t["dm"].view(np.uint16), OUT, IN)
+    x = np.random.default_rng(31).standard_normal(IN).astype(np.float32)
+    want = orc.sb6_gemv_f64(x[None], qblk, qsqm, ddm, OUT, IN, xb)[0]
+    y1 = orc.cpu_sb6_dequant_matvec(x, qblk, qsqm, ddm, OUT, IN, xb, 1)
+    y4 = orc.cpu_sb6_dequant_matvec(x, qblk, qsqm, ddm, OUT, IN, xb, 4)
+    assert np.array_equal(y1, y4)
+    assert np.abs(y1 - want).max() / np.abs(want).max() < 2e-5
+
+
+def test_cpu_baseline_wkv_step_matches_fp64(orc):
+    """The timed CPU decode step (B rows, in place) against the fp64 forward
+    at T = 1 from the same state."""
+    from swiftrwkv_amd import synthetic as syn
+    B, H = 2, 3
+    x = syn.wkv_inputs_config0(B, 1, H, seed=32)
+    h0 = syn.state(B, H, scale=0.5, seed=33)
+    o64, h64 = orc.wkv7_fwd_f64(*x, h0)
+    vec = [np.ascontiguousarray(z[:, 0]) for z in x]
+    outs = []
+    for nt in (1, 4):
+        h = h0.copy()
+        out = np.empty((B, H, 64), np.float32)
+        orc.cpu_wkv7_step(*vec, h, out, B, H, nt)
+        outs.append((out, h))
+        assert np.abs(out - o64[:, 0]).max() / np.abs(o64).max() < 1e-5
+        assert np.abs(h - h64).max() / np.abs(h64).max() < 1e-5
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
