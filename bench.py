@@ -1,29 +1,29 @@
 """Benchmark of the MI355X WKV-7 + .rwkvq hot path (one GPU).
 
-Headline (`value`): one-token decode of the 0.1B x070 shape (12 layers,
-n_embd 768, FFN 3072, vocab 65536), batch 1: every decode GEMV of the token
-(r/k/v/o 768x768, ffn key 3072x768, ffn value 768x3072, head 65536x768; sb6
-4-bit weights encoded from seeded N(0, 0.02)) plus the WKV-7 decode step and
-the tmix tail of each layer.  A step = one token: per layer one fused r/k/v
-GEMV launch, one fused step+tail launch, and the o / ffn key / ffn value
-GEMVs, then the head (61 launches).  The token's launches are
-captured once per weight copy into a HIP graph; steps rotate over
-`--copies` copies of the weights (> 256 MB in total) so they stream from HBM
-instead of the MALL.  Inputs are resident in HBM before the timed region.
+Headline (`value`): "1.5B decode tok/s" — one-token decode of the 1.5B x070
+shape (24 layers, n_embd 2048, FFN 8192, vocab 65536), batch 1, through the
+whole step (X070Decoder.launch: embedding row + ln0; per layer ln1 / token
+shift / lerps, the fused r/k/v GEMV with the low-rank first layers, the tmix
+core with the WKV-7 step and tail, o_proj + residual, ln2 / shift, ffn key
+relu², ffn value + residual; ln_out, head) captured in one HIP graph.  Weights
+are sb6 4-bit encoded from seeded N(0, 0.02): 776 MB of packed projections
+per token (> the 256 MB MALL), resident in HBM before the timed region.
 
-Also reported (`extra`): WKV-7 forward tokens/s at B1 T1024 H12 fp32, WKV-7
-forward and forward+backward tokens/s at B8 T4096 H32 bf16 (checkpointed),
-the head-GEMV HBM GB/s, batched decode of the 0.1B and 0.4B shapes (batch
-1 / 8 / 32), one-token decode of the 1.5B shape, decode of the 7B-class shape
-(32 layers, n_embd 4096, FFN 14336) at batch 1 and 16, the WKV-7 forward of
-one 7B-class prefill layer (B1 T8192 H64 fp32), and the CPU restatement of
-the WKV forward.
+`roofline` is for the dominant kernel of that token, the sb6 GEMV: the
+token's algorithmic GEMV bytes per launch (packed weights + x + y, over the
+token's GEMV launches) over the kernel's average in-graph duration, measured
+live on a graph holding only those GEMV launches.  `cpu_baseline` times the
+oracle's restatement of the reference's non-kernel decode path (dequantise
+to fp32, x·Wᵀ per projection; MLX-op WKV step) on a bounded sample of 1.5B
+tokens, checked against the GPU head GEMV first.
 
-`roofline` is for the dominant kernel of the decode token, the sb6 GEMV (most
-of the token's kernel time): the token's algorithmic GEMV bytes per launch
-over the kernel's average in-graph duration across the token's GEMV launches.
-`cpu_baseline` times the oracle's restatement of the reference's non-kernel
-decode path (dequantise to fp32, x·Wᵀ) on the host cores.
+Also reported (`extra`): the 0.1B decode (GEMV + WKV chain of one token, and
+the whole step), WKV-7 forward tokens/s at B1 T1024 H12 fp32, forward and
+forward+backward at B8 T4096 H32 bf16 (checkpointed), the head-GEMV HBM GB/s,
+batched decode of the 0.1B and 0.4B shapes (batch 1 / 8 / 32), decode of the
+7B-class shape (32 layers, n_embd 4096, FFN 14336) at batch 1 and 16, the
+WKV-7 forward of one 7B-class prefill layer (B1 T8192 H64 fp32), and the CPU
+restatements.
 """
 from __future__ import annotations
 
@@ -45,6 +45,8 @@ HEAD_GEMV_TRAFFIC_BYTES = 29494797
 # The same for the average GEMV launch of one 0.1B decode token (eager tokens
 # over rotated weight copies); same profile.
 DECODE_GEMV_TRAFFIC_BYTES = 1744043
+# The same for the average GEMV launch of one 1.5B decode token; null until measured.
+DECODE_1B5_GEMV_TRAFFIC_BYTES = None
 VALU_PEAK_TFLOPS = 157.3
 
 
@@ -455,7 +457,6 @@ def bench_decode_more(model_01, dev):
 
     res = {"projection_crossover_0.1B_ffn_key": bench_projection_crossover(model_01, dev)}
     log(f"projection crossover: {res['projection_crossover_0.1B_ffn_key']}")
-    res["x070_decode_e2e_0.1B_batch1"] = x070_line(model_01, dev, 200, 10, copies=len(model_01.dev))
     res["x070_decode_e2e_0.1B_batch8"] = x070_line(model_01, dev, 50, 5, copies=len(model_01.dev), B=8)
     for B in (8, 32):
         _, wall, gpu_ms = run_decode(model_01, dev, B, 50, 5, len(model_01.dev))
@@ -468,16 +469,6 @@ def bench_decode_more(model_01, dev):
         _, wall, gpu_ms = run_decode(model, dev, B, 30, 4, 2)
         res[f"decode_0.4B_batch{B}"] = {"tok_s": B * 30 / wall, "ms_per_step": wall * 1e3 / 30}
         log(f"decode 0.4B batch {B}: {wall * 1e3 / 30:.3f} ms per step")
-    del model
-    torch.cuda.empty_cache()
-    model = DecodeModel(syn.X070_1B5, 1, dev, nthreads=nthreads)
-    _, wall, gpu_ms = run_decode(model, dev, 1, 50, 5, 1)
-    ms = wall * 1e3 / 50
-    res["decode_1.5B_batch1"] = {"tok_s": 50 / wall, "ms_per_token": ms,
-                                 "gemv_bytes_per_token": model.bytes_per_token,
-                                 "effective_GBps": model.bytes_per_token / (ms * 1e-3) / 1e9}
-    log(f"decode 1.5B: {ms:.3f} ms per token")
-    res["x070_decode_e2e_1.5B_batch1"] = x070_line(model, dev, 50, 5)
     del model
     torch.cuda.empty_cache()
     # 7B class (32 layers, n_embd 4096, FFN 14336): 3.57 GB of packed weights
@@ -584,21 +575,34 @@ def bench_wkv(dev, reps=5):
     return res
 
 
-def cpu_baseline(model, step, seconds):
-    """The oracle's restatement of the non-kernel decode path on the host."""
-    import numpy as np
+def cpu_threads() -> int:
+    """Threads for the CPU restatement: the host cores this process may run
+    on, capped at the CPU share of one GPU (16) on an 8-GPU host."""
     from oracle import oracle as orc
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return max(1, min(16, avail, orc.max_threads()))
 
-    nthreads = min(16, orc.max_threads())
+
+def cpu_baseline(model, step, seconds, dev):
+    """The oracle's restatement of the non-kernel decode path on the host:
+    every projection of one token dequantised to fp32 and multiplied in fp32
+    (OpenMP over output rows), plus the MLX-op WKV step of every layer.  The
+    CPU head output is first checked against the GPU head GEMV on the same
+    packed bytes and input."""
+    import numpy as np
+    import torch
+    from oracle import oracle as orc
+    from swiftrwkv_amd import quant as Q
+
+    nthreads = cpu_threads()
     xD = step.xD.cpu().numpy()[0]
     xF = step.xF.cpu().numpy()[0]
+    xrkv = step.xrkv.cpu().numpy()
     vecs = [z.cpu().numpy() for z in step.rwkvab]
     state = np.zeros((step.L, 1, step.H, 64, 64), np.float32)
     out = np.empty((1, step.H, 64), np.float32)
-    ys = {}
-
-    xrkv = step.xrkv.cpu().numpy()
     rkv_row = {"receptance": 0, "key": 1, "value": 2}
+    ys = {}
 
     def token():
         for key, (qblk, qsqm, ddm, OUT, IN) in model.host.items():
@@ -610,16 +614,26 @@ def cpu_baseline(model, step, seconds):
             r, w, k, v, a, b = (np.ascontiguousarray(z[l]) for z in vecs)
             orc.cpu_wkv7_step(r, w, k, v, a, b, state[l], out, 1, step.H, nthreads)
 
+    t0 = time.perf_counter()
     token()
+    first = time.perf_counter() - t0
+    # the CPU head equals the GPU head GEMV (same bytes, same x) within the GEMV tolerance
+    q = model.dev[0]["head.weight"]
+    OUT, IN = model.host["head.weight"][3:5]
+    gpu = Q.rwkvq_sb6_gemv(step.xD, q[0], q[1], q[2], OUT, IN, 0)[0].cpu().numpy().astype(np.float64)
+    err = float(np.abs(gpu - ys["head.weight"]).max() / np.abs(gpu).max())
+    if not err < 1e-5:
+        raise RuntimeError(f"CPU head differs from the GPU head GEMV: rel {err:.3e}")
     n, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds and n < 2000:
         token()
         n += 1
     el = time.perf_counter() - t0
-    # check the CPU head against the GPU head GEMV of copy 0 (same bytes, same x)
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     return {"value": n / el, "unit": "tok/s", "cores": nthreads, "kind": "port",
-            "sample": f"{n} decode tokens of the 0.1B shape (73 sb6 dequant+fp32 matvecs + 12 WKV steps), "
-                      f"{el:.1f} s, OpenMP over output rows"}
+            "sample": f"{n} decode tokens of the {model.shape.name} shape ({len(model.host)} sb6 dequant+fp32 "
+                      f"matvecs + {step.L} WKV steps each; first token {first:.2f} s), {el:.1f} s on {nthreads} "
+                      f"OpenMP threads ({avail} cores visible); CPU head vs GPU head GEMV rel {err:.1e}"}
 
 
 def cpu_wkv_baseline():
@@ -628,7 +642,7 @@ def cpu_wkv_baseline():
     from swiftrwkv_amd import synthetic as syn
 
     x = syn.wkv_inputs_config0(1, 1024, 12, seed=0)
-    nthreads = min(16, orc.max_threads())
+    nthreads = cpu_threads()
     orc.wkv7_fwd_f32(*x, nthreads=nthreads)
     t0 = time.perf_counter()
     n = 0
@@ -697,6 +711,65 @@ def profile_x070(dev, tokens=20):
         torch.cuda.empty_cache()
 
 
+def headline_1b5(args, dev):
+    """The 1.5B decode: the whole x070 step per token (the headline), the
+    GEMV + WKV chain of the same token, the GEMV roofline and the CPU baseline."""
+    from swiftrwkv_amd import synthetic as syn
+
+    model = DecodeModel(syn.X070_1B5, 1, dev, nthreads=min(16, os.cpu_count() or 1))
+    wall, gpu_ms, launches = run_x070(model, dev, args.steps, args.warmup)
+    log(f"x070 decode 1.5B: {args.steps} tokens, wall {wall * 1e3:.2f} ms, gpu {gpu_ms:.2f} ms, {launches} launches")
+    step, cwall, cgpu = run_decode(model, dev, 1, 100, 10, 1)
+    gemv_bytes, gemv_avg_ms, n_gemv = bench_decode_gemv(model, step, dev)
+    achieved = gemv_bytes / (gemv_avg_ms * 1e-3) / 1e9
+    log(f"1.5B decode GEMV: {n_gemv} launches per token, {gemv_bytes / 1e6:.3f} MB per launch, "
+        f"avg {gemv_avg_ms * 1e3:.2f} us -> {achieved:.0f} GB/s")
+    chain = {"tok_s": 100 / cwall, "ms_per_token": cwall * 10, "gemv_bytes_per_token": model.bytes_per_token,
+             "effective_GBps": model.bytes_per_token / (cwall * 1e-2) / 1e9,
+             "gemv_launches_per_token": n_gemv, "gemv_avg_us": gemv_avg_ms * 1e3,
+             "gemv_kernel_us_per_token": gemv_avg_ms * 1e3 * n_gemv}
+    cpu = None if args.skip_cpu else cpu_baseline(model, step, args.cpu_seconds, dev)
+    res = {"wall": wall, "gpu_ms": gpu_ms, "launches": launches, "achieved": achieved, "n_gemv": n_gemv,
+           "gemv_bytes": gemv_bytes, "chain": chain, "cpu": cpu, "bytes_per_token": model.bytes_per_token}
+    del model, step
+    import torch
+    torch.cuda.empty_cache()
+    return res
+
+
+def config1_0b1(args, dev):
+    """One-token decode of the 0.1B shape: the GEMV + WKV chain (73 GEMVs as
+    49 launches and 12 step+tail launches, rotated weight copies), its GEMV
+    roofline, the head GEMV alone, the whole step, and the CPU baseline."""
+    model, step, wall, gpu_ms = bench_decode(args, dev)
+    gemv_bytes, gemv_avg_ms, n_gemv = bench_decode_gemv(model, step, dev)
+    achieved = gemv_bytes / (gemv_avg_ms * 1e-3) / 1e9
+    log(f"0.1B decode GEMV: {n_gemv} launches per token, {gemv_bytes / 1e6:.3f} MB per launch, "
+        f"avg {gemv_avg_ms * 1e3:.2f} us -> {achieved:.0f} GB/s")
+    nbytes, head_avg_ms, head_med_ms = bench_head_gemv(model, dev)
+    head_gbps = nbytes / (head_avg_ms * 1e-3) / 1e9
+    log(f"head GEMV: {nbytes / 1e6:.2f} MB, avg {head_avg_ms * 1e3:.1f} us -> {head_gbps:.0f} GB/s")
+    steps = args.steps
+    res = {
+        "decode_0.1B_gemv_wkv_chain_batch1": {
+            "tok_s": steps / wall, "ms_per_token": wall * 1e3 / steps, "gpu_ms_per_token": gpu_ms / steps,
+            "gemv_bytes_per_token": model.bytes_per_token,
+            "effective_GBps": model.bytes_per_token / (gpu_ms * 1e-3 / steps) / 1e9,
+            "launches_per_token": n_gemv + 12, "weight_copies_rotated": args.copies,
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBPS, "traffic": DECODE_GEMV_TRAFFIC_BYTES,
+                         "kernel": f"gemv_kernel, in-graph average over the {n_gemv} GEMV launches of one token"}},
+        "head_gemv_65536x768": {"bytes": nbytes, "avg_us": head_avg_ms * 1e3, "median_us": head_med_ms * 1e3,
+                                "GBps": head_gbps, "hbm_frac": head_gbps / HBM_PEAK_GBPS,
+                                "traffic": HEAD_GEMV_TRAFFIC_BYTES},
+        "x070_decode_e2e_0.1B_batch1": x070_line(model, dev, 200, 10, copies=len(model.dev)),
+    }
+    if not args.skip_cpu:
+        res["decode_0.1B_gemv_wkv_chain_batch1"]["cpu_baseline"] = cpu_baseline(model, step, min(5.0, args.cpu_seconds),
+                                                                                 dev)
+    return model, res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -715,51 +788,38 @@ def main():
     if args.mode == "e2e":
         profile_x070(dev)
         return
-    model, step, wall, gpu_ms = bench_decode(args, dev)
-    gemv_bytes, gemv_avg_ms, n_gemv = bench_decode_gemv(model, step, dev)
-    achieved = gemv_bytes / (gemv_avg_ms * 1e-3) / 1e9
-    log(f"decode GEMV: {n_gemv} launches per token, {gemv_bytes / 1e6:.3f} MB per launch, "
-        f"avg {gemv_avg_ms * 1e3:.2f} us -> {achieved:.0f} GB/s")
-    nbytes, head_avg_ms, head_med_ms = bench_head_gemv(model, dev)
-    head_gbps = nbytes / (head_avg_ms * 1e-3) / 1e9
-    log(f"head GEMV: {nbytes / 1e6:.2f} MB, avg {head_avg_ms * 1e3:.1f} us -> {head_gbps:.0f} GB/s")
-    extra = {
-        "decode_gpu_ms_per_token": gpu_ms / args.steps,
-        "decode_gemv_bytes_per_token": model.bytes_per_token,
-        "decode_effective_GBps": model.bytes_per_token / (gpu_ms * 1e-3 / args.steps) / 1e9,
-        "decode_gemv_launches_per_token": n_gemv,
-        "decode_gemv_kernel_us_per_token": gemv_avg_ms * 1e3 * n_gemv,
-        "decode_gemv_share_of_token": gemv_avg_ms * n_gemv / (gpu_ms / args.steps),
-        "head_gemv_65536x768": {"bytes": nbytes, "avg_us": head_avg_ms * 1e3, "median_us": head_med_ms * 1e3,
-                                "GBps": head_gbps, "hbm_frac": head_gbps / HBM_PEAK_GBPS,
-                                "traffic": HEAD_GEMV_TRAFFIC_BYTES},
-    }
+    head = headline_1b5(args, dev)
+    extra = {"decode_1.5B_gemv_wkv_chain_batch1": head["chain"]}
+    model01, more01 = config1_0b1(args, dev)
+    extra.update(more01)
     if not args.skip_wkv:
         extra.update(bench_wkv(dev))
         log("wkv done")
     if not args.skip_more:
-        extra.update(bench_decode_more(model, dev))
-    cpu = None
+        extra.update(bench_decode_more(model01, dev))
     if not args.skip_cpu:
-        cpu = cpu_baseline(model, step, args.cpu_seconds)
         extra["cpu_wkv7_fwd_B1_T1024_H12"] = cpu_wkv_baseline()
         log("cpu baseline done")
-    value = args.steps / wall
+    wall = head["wall"]
     line = {
-        "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC, "value": args.steps / wall, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "one-token decode, 0.1B x070 shape: 73 sb6 4-bit GEMVs (r/k/v/o 768x768 with "
-                               "r/k/v fused per layer, ffn 3072x768 + 768x3072, head 65536x768) + 12 WKV-7 "
-                               "steps with their tails fused, batch 1, 61 launches per token",
-                   "n_layer": 12, "n_embd": 768, "ffn": 3072, "vocab": 65536, "batch": 1,
-                   "weights": "sb6 4-bit from seeded N(0,0.02)", "weight_copies_rotated": args.copies,
-                   "hip_graph_per_token": True},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": DECODE_GEMV_TRAFFIC_BYTES,
-                     "kernel": f"gemv_kernel (sb6 4-bit), in-graph average over the {n_gemv} GEMV launches of "
-                               "one token; bytes per launch = the token's packed weights + x + y / launches"},
-        "cpu_baseline": cpu,
+        "config": {"workload": "1.5B decode: one-token x070 decode step of the 1.5B shape, batch 1, end to end "
+                               "(embedding row to logits) in one HIP graph: per layer ln1 + token shift + 6 "
+                               "lerps, fused r/k/v sb6 GEMV with the low-rank first layers, tmix core (low-rank "
+                               "second layers, WKV-7 step, group-norm tail, gate), o_proj + residual, ln2 + "
+                               "shift, ffn key relu², ffn value + residual; ln_out, head",
+                   "n_layer": 24, "n_embd": 2048, "n_head": 32, "ffn": 8192, "vocab": 65536, "batch": 1,
+                   "weights": "sb6 4-bit from seeded N(0,0.02), 776 MB packed per token; dense parameters "
+                              "seeded, low-rank matrices fp16",
+                   "launches_per_token": head["launches"], "hip_graph_per_token": True},
+        "roofline": {"bound": "hbm", "achieved": head["achieved"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": head["achieved"] / HBM_PEAK_GBPS, "traffic": DECODE_1B5_GEMV_TRAFFIC_BYTES,
+                     "kernel": f"gemv_kernel (sb6 4-bit), in-graph average over the {head['n_gemv']} GEMV "
+                               f"launches of one 1.5B token; bytes per launch = the token's packed weights + "
+                               f"x + y / launches = {head['gemv_bytes']:.0f}"},
+        "cpu_baseline": head["cpu"],
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
