@@ -207,6 +207,23 @@ rwkv_status rwkv_sym_gemv_ep(const float* x, int64_t N,
                              float* y, int64_t OUT, int64_t IN, int bits, int epilogue,
                              void* stream);
 
+/* Parallel-pass projection (many input rows) on the matrix cores: the long
+ * pass of X070Backbone.baseMatmul with an fp16 base (Sources/RWKVGen/X070Backbone.swift:337-356,
+ * 733-739): y = fp16(fp16(x)·fp16(W)ᵀ) where fp16(W) is exactly the dequant
+ * rwkv_sb6_dequant(out_dt = f16) stores, products summed in fp32, the sum
+ * rounded to fp16 (the fp16 matmul's output) — computed from the K3 bytes
+ * without writing the dense weight.  4-bit sb6 only; OUT and out_per
+ * multiples of 256, IN of 256 (rwkv_sb6_gemm_applies).
+ * x [groups][M][lda] in x_dt (f32 or f16; groups = OUT / out_per, matrix g
+ * at x + g·x_group_stride elements): output feature o reads group o / out_per,
+ * so r/k/v with their own inputs run as one launch.  y [M][ldy]:
+ * epilogue 0 stores, 1 adds into y (fp32; the residual update), 2 stores
+ * relu(·)² as fp16 (y is then an fp16 buffer; cmix's key, exact in fp16). */
+int rwkv_sb6_gemm_applies(int64_t OUT, int64_t IN, int xbits, int64_t out_per);
+rwkv_status rwkv_sb6_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda, int64_t x_group_stride,
+                          const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, void* y, int64_t ldy,
+                          int64_t OUT, int64_t IN, int xbits, int64_t out_per, int epilogue, void* stream);
+
 /* ───────────────────────── x070 decode step around the hot path ───────────────────────── */
 /* fp32 activations; dense vector parameters fp32 (an fp16 file's values
  * widen exactly); low-rank matrices f16 (the reference's `lin` narrowing,
@@ -273,6 +290,37 @@ rwkv_status rwkv_x070_tmix_core(const float* y_rkv, const float* la, const void*
                                 const float* k_a, const float* r_k, const float* lnx_w,
                                 const float* lnx_b, float* v_first, int layer0, float* state,
                                 float* out, int64_t N, int64_t H, float eps, void* stream);
+
+/* ───────────────────────── x070 parallel (prefill) pass ───────────────────────── */
+/* B rows of T tokens flattened as n = b·T + t; lengths (int32, device) [B]
+ * gives each row's real tokens (right padding; NULL = all T). */
+
+/* Token shift over a sequence with its lerps (rwkvTokenShift and the x_c
+ * lerps of rwkvTmixForward / rwkvCmixForward, Sources/RWKVGen/RWKVBlock.swift:145-183,
+ * 300-307): for layer-normed rows xl [B·T, D], prev_t = xl[n − 1] (t > 0) or
+ * prev_in[b] (the carried shift state; NULL = zeros); m_c = xl + (prev_t − xl)·coef[c].
+ * Coefficients [0, n0) → y0 (f32 or f16; element (n, c) at n·y0_row + c·y0_coef);
+ * y1 (f32, may be NULL) receives every coefficient at n·y1_row + c·y1_coef; prev_out [B, D] ← xl of
+ * each row's last real token (gatherLast, :320-335).  nc = 6 (r, k, v, w, a, g)
+ * or 1.  prev_out must not alias prev_in. */
+rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float* prev_out, const int32_t* lengths,
+                                    const float* coef, int nc, int n0, void* y0, rwkv_dtype y0_dt, int64_t y0_row,
+                                    int64_t y0_coef, float* y1, int64_t y1_row, int64_t y1_coef, int64_t B, int64_t T,
+                                    int64_t D, void* stream);
+
+/* The time-mix arithmetic between the projections and the recurrence
+ * (rwkvTmixForward, RWKVBlock.swift:185-237): y_rkv [B·T, 3D] = r | k0 | v0,
+ * low-rank second layers ww, aa, vv [B·T, D] before their biases (vv NULL at
+ * layer 0) → the WKV-7 inputs r, w, k, v, a, b [B·T, D] (w = exp(−0.606531·σ(ww + w_bias)),
+ * a = −kk, b = kk·σ(aa + a_bias), kk = l2norm(k0·k_k) per head,
+ * k = k0·(1 + (σ(aa + a_bias) − 1)·k_a), v mixed with v_first [B·T, D] or, at
+ * layer 0, written to it), pad steps neutral (w = 1, k = 0, b = 0,
+ * :232-237), and k_bonus = k unmasked for the tail. */
+rwkv_status rwkv_x070_seq_tmix_pre(const float* y_rkv, const float* ww, const float* aa, const float* vv,
+                                   const float* w_bias, const float* a_bias, const float* v_bias, const float* k_k,
+                                   const float* k_a, float* v_first, int layer0, const int32_t* lengths, float* r,
+                                   float* w, float* k, float* v, float* a, float* b, float* k_bonus, int64_t B,
+                                   int64_t T, int64_t H, void* stream);
 
 /* ───────────────────────────── host-side format work (CPU) ───────────────────────────── */
 
@@ -410,6 +458,7 @@ typedef struct {
     int64_t sb6_fused;      /* rwkv_sb6_gemv_fused launches (no reference counter) */
     int64_t sym_rows;       /* rwkv_sym_rows launches (no reference counter) */
     int64_t x070;           /* layer_norm / x070_* launches (no reference counter) */
+    int64_t sb6_gemm;       /* rwkv_sb6_gemm launches (no reference counter) */
 } rwkv_counters;
 
 void rwkv_get_counters(rwkv_counters* out);

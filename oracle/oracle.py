@@ -247,6 +247,19 @@ def sym_gemv_f64(x, qblk, qs, d, OUT, IN, bits, out_per=None):
     return y
 
 
+def sb6_matmul_f16_base(x, qblk, qsqm, ddm, OUT, IN, xbits=0):
+    """The long pass of X070Backbone.baseMatmul with an fp16 base
+    (X070Backbone.swift:337-356): W16 = the fp16 dequant (RwkvqDequant.swift:116-140
+    stored as fp16), x rounded to fp16, and their product summed exactly
+    (fp64: the fp16·fp16 products and their sums over these sizes are exact
+    to 2^-52) — the value the fp16 matmul's output rounds.  Returns
+    (exact [N, OUT], magnitude Σ|x16·w16| [N, OUT]); the magnitude scales the
+    accumulation error an fp32 sum of the same products may carry."""
+    W16 = sb6_dequant(qblk, qsqm, ddm, OUT, IN, xbits, "f16").view(np.float16).astype(np.float64)
+    x16 = np.asarray(x, np.float32).reshape(-1, IN).astype(np.float16).astype(np.float64)
+    return x16 @ W16.T, np.abs(x16) @ np.abs(W16).T
+
+
 # ───────────────────────────── CPU baseline ─────────────────────────────
 
 def cpu_sb6_dequant_matvec(x, qblk, qsqm, ddm, OUT, IN, xbits, nthreads):

@@ -206,3 +206,69 @@ def sequence(p, W, ids, n_layer, H):
         h = np.maximum(xk @ W[b + "ffn.key.weight"].T, 0.0)
         x = x + (h * h) @ W[b + "ffn.value.weight"].T
     return layer_norm(x, p["ln_out.weight"], p["ln_out.bias"]) @ W["head.weight"].T
+
+
+def prefill(p, W, ids, n_layer, H, f16_base=False):
+    """The parallel pass over one prompt from the zero state, as the
+    reference's prefill runs it for an .rwkvq base (rwkvTmixForward /
+    rwkvCmixForward, RWKVBlock.swift:163-307; bodyWithState + the head of
+    prefillBatch, BatchGenerate.swift:37-53): token shift as a shifted copy
+    of the sequence, one WKV-7 pass over all T steps, the low-rank branches
+    as plain products (fp32 activations times the fp16 matrices' exact
+    values: no `lin` narrowing on this path), projections through baseProj:
+      * f16_base (the long pass of baseMatmul, X070Backbone.swift:337-356):
+        y = fp16(fp16(x) · fp16(W)ᵀ), fp16(W) the fp16 dequant; cmix's
+        relu(·)² rounded to fp16 (it is the next product's fp16 input);
+      * else the fp32 GEMV (short pass): y = x·Wᵀ, relu² unrounded;
+    the head always the GEMV (decode: true).  Returns (logits of the last
+    token [vocab], State with the WKV states, and the shift states taken at
+    the last token)."""
+    T, D = len(ids), H * HEAD
+    W16 = {}
+
+    def proj(y, key):
+        if not f16_base:
+            return y @ W[key].T
+        if key not in W16:
+            W16[key] = f16r(W[key])
+        return f16r(f16r(y) @ W16[key].T)
+
+    wide = lambda y, m: np.asarray(y, np.float64) @ np.asarray(m, np.float64).T
+    st = State.zeros(n_layer, 1, H)
+    x = layer_norm(p["emb.weight"].astype(np.float64)[np.asarray(ids)], p["ln0.weight"], p["ln0.bias"])
+    v_first = None
+    for l in range(n_layer):
+        b = f"blocks.{l}."
+        t = b + "tmix."
+        a_ = b + "att."
+        xl = layer_norm(x, p[b + "ln1.weight"], p[b + "ln1.bias"])
+        st.tmix_prev[l, 0] = xl[-1]
+        xx = np.concatenate([np.zeros((1, D)), xl[:-1]], 0) - xl
+        m = {c: xl + xx * p[t + "x_" + c].astype(np.float64) for c in "rwkvag"}
+        r = proj(m["r"], a_ + "receptance.weight")
+        k0 = proj(m["k"], a_ + "key.weight")
+        v = proj(m["v"], a_ + "value.weight")
+        gate = wide(sigmoid(wide(m["g"], p[t + "g_lora_A.weight"])), p[t + "g_lora_B.weight"])
+        if l == 0:
+            v_first = v.copy()
+        else:
+            vv = sigmoid(wide(wide(m["v"], p[t + "v_lora_A.weight"]), p[t + "v_lora_B.weight"]) + p[t + "v_lora_B.bias"])
+            v = v + (v_first - v) * vv
+        a = sigmoid(wide(wide(m["a"], p[t + "a_lora_A.weight"]), p[t + "a_lora_B.weight"]) + p[t + "a_lora_B.bias"])
+        ww = wide(np.tanh(wide(m["w"], p[t + "w_lora_A.weight"])), p[t + "w_lora_B.weight"]) + p[t + "w_lora_B.bias"]
+        w = np.exp(-0.606531 * sigmoid(ww))
+        kk = l2norm_heads(k0 * p[t + "k_k"], H)
+        k = k0 * (1.0 + (a - 1.0) * p[t + "k_a"])
+        sh = lambda z: np.asarray(z, np.float64).reshape(1, T, H, HEAD)
+        out, st.wkv[l] = O.wkv7_fwd_f64(sh(r), sh(w), sh(k), sh(v), sh(-kk), sh(kk * a), None)
+        tail = O.wkv_tail_f64(out.reshape(T, D), r, k, v, p[t + "r_k"], p[t + "ln_x.weight"], p[t + "ln_x.bias"],
+                              gate, T, H, HEAD, 64e-5)
+        x = x + proj(tail, a_ + "output.weight")
+        xl = layer_norm(x, p[b + "ln2.weight"], p[b + "ln2.bias"])
+        st.cmix_prev[l, 0] = xl[-1]
+        xk = xl + (np.concatenate([np.zeros((1, D)), xl[:-1]], 0) - xl) * p[b + "cmix.x_k"].astype(np.float64)
+        h = np.maximum(proj(xk, b + "ffn.key.weight"), 0.0)
+        h = f16r(h * h) if f16_base else h * h
+        x = x + proj(h, b + "ffn.value.weight")
+    logits = layer_norm(x[-1:], p["ln_out.weight"], p["ln_out.bias"]) @ W["head.weight"].T
+    return logits[0], st

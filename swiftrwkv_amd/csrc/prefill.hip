@@ -1,0 +1,183 @@
+// The parallel (prefill) pass of the x070 block around its matrix products:
+// the token shift over a whole sequence and the time-mix arithmetic between
+// the projections / low-rank branches and the WKV-7 recurrence, for B rows of
+// T tokens with right padding (Sources/RWKVGen/RWKVBlock.swift:145-264,
+// rwkvTokenShift and rwkvTmixForward; BatchGenerate.swift:37-53).
+//
+// Rows are [B, T] flattened (n = b·T + t); row b holds lengths[b] real
+// tokens, the rest is padding.  The padding is made neutral for the
+// recurrence exactly as the reference does (w ← 1, k ← 0, b ← 0 at pad steps,
+// RWKVBlock.swift:232-237): the state of a row stops at its last real token,
+// whatever its neighbours or the amount of padding.  Outputs at pad positions
+// are computed and left unused.
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "launch.h"
+#include "lora_in.h"
+#include "wkv7_step.h"
+
+namespace {
+
+using rwkv_wkv::wave_total;
+using rwkv_x070::exp_fast;
+using rwkv_x070::sigmoid_fast;
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+// Token shift over the sequence with its lerps (rwkvTokenShift + the x_c
+// lerps of rwkvTmixForward / rwkvCmixForward): for the layer-normed rows xl,
+// prev_t = xl[t − 1] (t > 0) or the carried shift state prev_in[b] (zeros when
+// NULL); m_c = xl + (prev_t − xl)·coef[c].  Coefficients [0, n0) go to y0
+// (fp16 or fp32, element (n, c) at n·y0_row + c·y0_coef); with y1, every
+// coefficient also goes to y1 (fp32).  prev_out[b] ← xl[b, lengths[b] − 1] (the shift state of the row's
+// last real token, gatherLast).  One thread per 4 columns of one row.
+template <int NC, bool F16>
+__global__ __launch_bounds__(256) void seq_shift_kernel(const float* __restrict__ xl, const float* __restrict__ prev_in,
+                                                        float* __restrict__ prev_out, const int32_t* __restrict__ lengths,
+                                                        const float* __restrict__ coef, int n0, void* __restrict__ y0,
+                                                        int64_t y0_row, int64_t y0_coef, float* __restrict__ y1,
+                                                        int64_t y1_row, int64_t y1_coef, int T, int D, int64_t total) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
+    const int D4 = D >> 2;
+    const int64_t n = gid / D4;
+    const int c = (int)(gid - n * D4) * 4;
+    const int b = (int)(n / T), t = (int)(n - (int64_t)b * T);
+    const float4 x = ld4(xl + n * D + c);
+    float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t > 0) p = ld4(xl + (n - 1) * D + c);
+    else if (prev_in) p = ld4(prev_in + (int64_t)b * D + c);
+    const int len = lengths ? lengths[b] : T;
+    if (t == len - 1) *reinterpret_cast<float4*>(prev_out + (int64_t)b * D + c) = x;
+    const float4 xx = make_float4(p.x - x.x, p.y - x.y, p.z - x.z, p.w - x.w);
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+        const float4 q = ld4(coef + (int64_t)k * D + c);
+        const float4 m = make_float4(x.x + xx.x * q.x, x.y + xx.y * q.y, x.z + xx.z * q.z, x.w + xx.w * q.w);
+        if (k < n0) {
+            const int64_t o = n * y0_row + k * y0_coef + c;
+            if constexpr (F16) {
+                __half2 h[2] = {__floats2half2_rn(m.x, m.y), __floats2half2_rn(m.z, m.w)};
+                *reinterpret_cast<uint2*>(reinterpret_cast<__half*>(y0) + o) = *reinterpret_cast<uint2*>(h);
+            } else {
+                *reinterpret_cast<float4*>(reinterpret_cast<float*>(y0) + o) = m;
+            }
+        }
+        if (y1) *reinterpret_cast<float4*>(y1 + n * y1_row + k * y1_coef + c) = m;
+    }
+}
+
+// The time-mix arithmetic between the projections and the WKV recurrence
+// (rwkvTmixForward, RWKVBlock.swift:185-237), one wave per (row, head), lane
+// = channel of the head.  Inputs: y_rkv [M, 3D] = r | k0 | v0 (the r/k/v
+// projections), the low-rank second layers ww, aa, vv (pre-bias) [M, D]
+// (vv NULL at layer 0).  Computes
+//   w = exp(−0.606531·σ(ww + w_bias)), a = σ(aa + a_bias),
+//   kk = l2norm(k0·k_k) over the head, k = k0·(1 + (a − 1)·k_a),
+//   v = layer 0 ? v0 (v_first ← v0) : v0 + (v_first − v0)·σ(vv + v_bias),
+// and writes the recurrence inputs r, w, k, v, a_w = −kk, b_w = kk·a [M, D]
+// with pad steps neutral (w ← 1, k ← 0, b_w ← 0), plus k_bonus = k unmasked
+// (the tail's bonus term uses it, RWKVBlock.swift:287-289).  The branch
+// functions are the decode core's (exp2 / reciprocal based, ~1e-6).
+__global__ __launch_bounds__(256) void seq_tmix_pre_kernel(
+    const float* __restrict__ y_rkv, const float* __restrict__ ww, const float* __restrict__ aa,
+    const float* __restrict__ vv, const float* __restrict__ w_bias, const float* __restrict__ a_bias,
+    const float* __restrict__ v_bias, const float* __restrict__ k_k, const float* __restrict__ k_a,
+    float* __restrict__ v_first, int layer0, const int32_t* __restrict__ lengths, float* __restrict__ r_o,
+    float* __restrict__ w_o, float* __restrict__ k_o, float* __restrict__ v_o, float* __restrict__ a_o,
+    float* __restrict__ b_o, float* __restrict__ kb_o, int T, int H, int64_t units) {
+    const int64_t unit = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (unit >= units) return;   // uniform per wave
+    const int lane = threadIdx.x & 63;
+    const int D = H * 64;
+    const int64_t n = unit / H;
+    const int h = (int)(unit - n * H);
+    const int ch = h * 64 + lane;
+    const int b = (int)(n / T), t = (int)(n - (int64_t)b * T);
+    const bool real = t < (lengths ? lengths[b] : T);
+    const int64_t e = n * D + ch;
+    const float* yr = y_rkv + n * 3 * D;
+    const float r = yr[ch], k0 = yr[D + ch], v0 = yr[2 * D + ch];
+    const float w = exp_fast(-0.606531f * sigmoid_fast(ww[e] + w_bias[ch]));
+    const float a = sigmoid_fast(aa[e] + a_bias[ch]);
+    float v = v0;
+    if (layer0) {
+        v_first[e] = v0;
+    } else {
+        const float vf = v_first[e];
+        v = v0 + (vf - v0) * sigmoid_fast(vv[e] + v_bias[ch]);
+    }
+    const float kkr = k0 * k_k[ch];
+    const float kk = kkr / sqrtf(wave_total(kkr * kkr) + 1e-12f);
+    const float k = k0 * (1.0f + (a - 1.0f) * k_a[ch]);
+    r_o[e] = r;
+    v_o[e] = v;
+    a_o[e] = -kk;
+    kb_o[e] = k;
+    w_o[e] = real ? w : 1.0f;
+    k_o[e] = real ? k : 0.0f;
+    b_o[e] = real ? kk * a : 0.0f;
+}
+
+}  // namespace
+
+extern "C" {
+
+rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float* prev_out, const int32_t* lengths,
+                                    const float* coef, int nc, int n0, void* y0, rwkv_dtype y0_dt, int64_t y0_row,
+                                    int64_t y0_coef, float* y1, int64_t y1_row, int64_t y1_coef, int64_t B, int64_t T,
+                                    int64_t D, void* stream) {
+    RWKV_REQUIRE(xl && prev_out && coef && y0, RWKV_E_NULL, "x070_seq_shift_mix: null buffer");
+    RWKV_REQUIRE(nc == 1 || nc == 6, RWKV_E_SHAPE, "x070_seq_shift_mix: %d coefficients (1 or 6)", nc);
+    RWKV_REQUIRE(n0 >= 1 && n0 <= nc, RWKV_E_SHAPE, "x070_seq_shift_mix: n0 = %d", n0);
+    RWKV_REQUIRE(y0_dt == RWKV_F32 || y0_dt == RWKV_F16, RWKV_E_DTYPE, "x070_seq_shift_mix: y0 must be f32 or f16");
+    RWKV_REQUIRE(B >= 1 && T >= 1 && D >= 4 && D % 4 == 0 && B * T <= ((int64_t)1 << 26), RWKV_E_SHAPE,
+                 "x070_seq_shift_mix: B=%lld T=%lld D=%lld", (long long)B, (long long)T, (long long)D);
+    RWKV_REQUIRE(y0_row % 4 == 0 && y0_coef % 4 == 0 && (!y1 || (y1_row % 4 == 0 && y1_coef % 4 == 0)),
+                 RWKV_E_SHAPE, "x070_seq_shift_mix: output strides must be multiples of 4");
+    RWKV_REQUIRE(prev_out != prev_in, RWKV_E_SHAPE, "x070_seq_shift_mix: prev_out must not alias prev_in");
+    const int64_t total = B * T * (D / 4);
+    const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const bool f16 = y0_dt == RWKV_F16;
+#define RWKV_SHIFT(NCV, F)                                                                                          \
+    rwkv::launch(seq_shift_kernel<NCV, F>, grid, block, s, xl, prev_in, prev_out, lengths, coef, n0, y0, y0_row,   \
+                 y0_coef, y1, y1_row, y1_coef, (int)T, (int)D, total)
+    if (nc == 6) {
+        if (f16) RWKV_SHIFT(6, true);
+        else RWKV_SHIFT(6, false);
+    } else {
+        if (f16) RWKV_SHIFT(1, true);
+        else RWKV_SHIFT(1, false);
+    }
+#undef RWKV_SHIFT
+    RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "x070_seq_shift_mix: launch failed");
+    rwkv::counters().x070.fetch_add(1);
+    rwkv::clear_error();
+    return RWKV_OK;
+}
+
+rwkv_status rwkv_x070_seq_tmix_pre(const float* y_rkv, const float* ww, const float* aa, const float* vv,
+                                   const float* w_bias, const float* a_bias, const float* v_bias, const float* k_k,
+                                   const float* k_a, float* v_first, int layer0, const int32_t* lengths, float* r,
+                                   float* w, float* k, float* v, float* a, float* b, float* k_bonus, int64_t B,
+                                   int64_t T, int64_t H, void* stream) {
+    RWKV_REQUIRE(y_rkv && ww && aa && w_bias && a_bias && k_k && k_a && v_first && r && w && k && v && a && b &&
+                     k_bonus && (layer0 || (vv && v_bias)),
+                 RWKV_E_NULL, "x070_seq_tmix_pre: null buffer");
+    RWKV_REQUIRE(B >= 1 && T >= 1 && H >= 1 && B * T * H <= ((int64_t)1 << 30), RWKV_E_SHAPE,
+                 "x070_seq_tmix_pre: B=%lld T=%lld H=%lld", (long long)B, (long long)T, (long long)H);
+    const int64_t units = B * T * H;
+    const dim3 grid((unsigned)((units + 3) / 4)), block(256);
+    rwkv::launch(seq_tmix_pre_kernel, grid, block, reinterpret_cast<hipStream_t>(stream), y_rkv, ww, aa, vv, w_bias,
+                 a_bias, v_bias, k_k, k_a, v_first, layer0, lengths, r, w, k, v, a, b, k_bonus, (int)T, (int)H, units);
+    RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "x070_seq_tmix_pre: launch failed");
+    rwkv::counters().x070.fetch_add(1);
+    rwkv::clear_error();
+    return RWKV_OK;
+}
+
+}  // extern "C"

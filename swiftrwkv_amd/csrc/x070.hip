@@ -24,12 +24,6 @@ using namespace rwkv_x070;
 
 constexpr int kRowMax = 8192;   // widest row of the row kernels
 
-// The low-rank branch functions on a tmix core's critical path: exp2 of the
-// scaled argument and the hardware reciprocal (each ~1 ulp; relative error of
-// the result ~1e-6 over the branch outputs' range, against the IEEE
-// sequences' ~30 dependent instructions).
-__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
-__device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_fast(-x)); }
 
 // Sum over the workgroup: per-wave butterfly, then the wave totals in wave
 // order; every thread gets the same value.  `red` (16 floats) is used once

@@ -544,6 +544,52 @@ def rwkvq_sb6_gemv(x, qblk, qsqm, ddm, out_features: int, in_features: int, xbit
     return y
 
 
+def rwkvq_sb6_gemm_applies(out_features: int, in_features: int, xbits: int, out_per: Optional[int] = None) -> bool:
+    """Whether the matrix-core long pass takes this sb6 matrix (group)."""
+    per = out_features if out_per is None else out_per
+    return bool(_lib.lib().rwkv_sb6_gemm_applies(out_features, in_features, xbits, per))
+
+
+_GEMM_EP = {"store": 0, "add": 1, "relu2_f16": 2}
+
+
+def rwkvq_sb6_gemm(x, qblk, qsqm, ddm, out_features: int, in_features: int, xbits: int = 0,
+                   out_per: Optional[int] = None, epilogue: str = "store",
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The fp16-base long pass of baseMatmul (X070Backbone.swift:337-356) on
+    the matrix cores, straight from the K3 bytes: y [M, OUT] =
+    fp16(fp16(x)·fp16(W)ᵀ) with fp32 sums.  x [M, IN] (one matrix) or
+    [G, M, IN] (G = OUT / out_per row-concatenated matrices, matrix g reading
+    x[g]), fp32 or fp16.  epilogue "store" / "add" (fp32 `out`, added into) /
+    "relu2_f16" (relu(·)² in an fp16 `out`)."""
+    per = out_features if out_per is None else out_per
+    if not rwkvq_sb6_gemm_applies(out_features, in_features, xbits, per):
+        raise ValueError(f"sb6 GEMM: [{out_features}, {in_features}] xbits={xbits} out_per={per} not taken")
+    G = out_features // per
+    if x.dim() == 2:
+        x = x.unsqueeze(0)
+    if x.dim() != 3 or x.shape[0] != G or x.shape[2] != in_features:
+        raise ValueError(f"sb6 GEMM: input {tuple(x.shape)}, expected [{G}, M, {in_features}]")
+    if x.dtype not in (torch.float32, torch.float16):
+        x = x.float()
+    x = _aligned(x)
+    M = x.shape[1]
+    qblk, qsqm, ddm = _sb6_bufs(qblk, qsqm, ddm, out_features, in_features, xbits)
+    ep = _GEMM_EP[epilogue]
+    ydt = torch.float16 if ep == 2 else torch.float32
+    if out is None:
+        if ep == 1:
+            raise ValueError("sb6 GEMM: the add epilogue needs `out`")
+        out = torch.empty((M, out_features), dtype=ydt, device=x.device)
+    elif out.dtype != ydt or tuple(out.shape) != (M, out_features) or not out.is_contiguous() or \
+            out.device != x.device:
+        raise ValueError(f"sb6 GEMM: out must be a contiguous {ydt} [{M}, {out_features}] tensor on {x.device}")
+    _lib.call("rwkv_sb6_gemm", x.data_ptr(), _OUT_DT[x.dtype], M, in_features, M * in_features, qblk.data_ptr(),
+              qsqm.data_ptr(), ddm.data_ptr(), out.data_ptr(), out_features, out_features, in_features, xbits, per,
+              ep, _stream(x))
+    return out
+
+
 RWKVQ_SYM_GEMV_MAX_ROWS = 4   # RwkvqSymGEMV.swift:40
 
 

@@ -418,33 +418,193 @@ class X070Decoder:
             raise ValueError(f"step_batch: {len(ids)} tokens for a batch of {state.n_rows}")
         return self.step(ids, state)
 
-    def prefill_batch(self, prompts) -> Tuple[torch.Tensor, RWKVState]:
-        """prefillBatch (BatchGenerate.swift:37-53): logits [B, vocab] of each
-        prompt's last token and the batch state.  The rows step together
-        through the decode step, a row leaving the stepped set once its prompt
-        is consumed, so each row ends in the state of its prompt alone (the
-        reference runs its parallel pass with right padding and a mask; the
-        parallel prefill block is not part of this path)."""
+    def prefill_batch(self, prompts, base_dtype=torch.float16, short_rows: int = 0) -> Tuple[torch.Tensor, RWKVState]:
+        """prefillBatch (BatchGenerate.swift:37-53): every prompt in one
+        parallel pass — right padding to the longest prompt, a mask that makes
+        the pad steps neutral for the recurrence, each row's shift state taken
+        at its last real token — returning the logits [B, vocab] of each
+        prompt's last token and the batch state.  Per layer (rwkvTmixForward /
+        rwkvCmixForward, RWKVBlock.swift:163-307): ln1 + token shift + lerps
+        over the sequence, the r/k/v projections, the low-rank branches, the
+        time-mix arithmetic with the pad mask, one WKV-7 launch for the whole
+        sequence from the row's state, the tail, o_proj + residual, ln2 +
+        shift, the FFN.  Projections (baseProj, X070Backbone.swift:676-746):
+        with `base_dtype` fp16, B·T rows above `short_rows` take the fp16 long
+        pass on the matrix cores (rwkv_sb6_gemm for 4-bit sb6; dequantise +
+        library GEMM otherwise), the others the fp32 GEMV; with fp32 every
+        projection is the fp32 GEMV.  The head is the GEMV (decode: true)."""
         if len(prompts) == 0:
             raise ValueError("prefill_batch: no prompts")
         if any(len(p) == 0 for p in prompts):
             raise ValueError("prefill_batch: empty prompt")
+        if base_dtype not in (torch.float16, torch.float32):
+            raise ValueError(f"prefill_batch: base dtype {base_dtype} (float16 or float32)")
         B, T = len(prompts), max(len(p) for p in prompts)
+        M = B * T
+        if M > 65535:
+            raise ValueError(f"prefill_batch: {M} rows in one pass (at most 65535)")
+        dev, D = self.device, self.D
+        ids = np.zeros((B, T), np.int32)
+        for i, p in enumerate(prompts):
+            ids[i, :len(p)] = np.asarray(p, np.int32)
+        lens = [len(p) for p in prompts]
+        ids_t = torch.from_numpy(ids.reshape(-1)).to(dev)
+        len_t = torch.tensor(lens, dtype=torch.int32, device=dev)
+        last_t = torch.tensor([i * T + n - 1 for i, n in enumerate(lens)], dtype=torch.int32, device=dev)
         state = self.new_state(B)
-        logits = torch.empty((B, self.V), dtype=torch.float32, device=self.device)
-        for t in range(T):
-            rows = [i for i, p in enumerate(prompts) if len(p) > t]
-            ids = [int(prompts[i][t]) for i in rows]
-            if len(rows) == B:
-                out = self.step(ids, state)
-            else:
-                sub = state.gather(rows)
-                out = self.step(ids, sub)
-                state.scatter_(rows, sub)
-            for j, i in enumerate(rows):
-                if len(prompts[i]) == t + 1:
-                    logits[i] = out[j]
+        s = torch.cuda.current_stream(dev).cuda_stream
+        long = base_dtype == torch.float16 and M > short_rows
+        bf = self._prefill_buffers(M, long)
+        L, p = _lib.lib(), (lambda t: t.data_ptr())
+        x = bf["x"]
+        emb_dt = _lib.F16 if self.emb.dtype == torch.float16 else _lib.F32
+        _lib.check(L.rwkv_layer_norm(p(self.emb), emb_dt, p(ids_t), int(self.emb.shape[0]), p(self.ln0[0]),
+                                     p(self.ln0[1]), p(x), M, D, LN_EPS, s))
+        for l in range(self.L):
+            self._prefill_layer(l, state, bf, len_t, B, T, long, s)
+        xo = torch.empty((B, D), dtype=torch.float32, device=dev)
+        _lib.check(L.rwkv_layer_norm(p(x), _lib.F32, p(last_t), M, p(self.ln_out[0]), p(self.ln_out[1]), p(xo),
+                                     B, D, LN_EPS, s))
+        logits = torch.empty((B, self.V), dtype=torch.float32, device=dev)
+        self._gemv("head.weight", xo, logits, 0, B, s)
         return logits, state
+
+    def _prefill_buffers(self, M: int, long: bool) -> dict:
+        key = ("prefill", M, long)
+        bf = self._tmp.get(key)
+        if bf is None:
+            dev, D, F = self.device, self.D, self.F
+            z = lambda *sh, dt=torch.float32: torch.empty(sh, dtype=dt, device=dev)
+            bf = {"x": z(M, D), "xl": z(M, D), "mix": z(6, M, D), "y_rkv": z(M, 3 * D), "v_first": z(M, D),
+                  "ww": z(M, D), "aa": z(M, D), "vv": z(M, D), "gate": z(M, D), "wkv": z(M, D), "tout": z(M, D),
+                  "prev": z(max(1, M), D)}
+            for n in ("r", "w", "k", "v", "a", "b", "kb"):
+                bf[n] = z(M, D)
+            bf["rkv_in"] = z(3, M, D, dt=torch.float16) if long else z(M, 3, D)
+            bf["xk"] = z(M, D, dt=torch.float16) if long else z(M, D)
+            bf["hk"] = z(M, F, dt=torch.float16) if long else z(M, F)
+            self._tmp = {k: v for k, v in self._tmp.items() if not (isinstance(k, tuple) and k[0] == "prefill")}
+            self._tmp[key] = bf
+        return bf
+
+    def _lowrank_f32(self, l: int) -> list:
+        """The layer's low-rank matrices in fp32 (the file's fp16 values widen
+        exactly): the parallel pass multiplies fp32 activations by them
+        without narrowing (MLX promotes the fp16 weight, RWKVBlock.swift:185-226)."""
+        key = ("lowrank32", l)
+        m = self._tmp.get(key)
+        if m is None:
+            lay = self.layers[l]
+            rw, ra, rv, rg = self.ranks
+            A = lay["wcat"].float()
+            m = [A[:rw], A[rw:rw + ra], A[rw + ra:rw + ra + rv], A[rw + ra + rv:]] + [t.float() for t in lay["B"]]
+            self._tmp[key] = m
+        return m
+
+    def _prefill_layer(self, l, state, bf, len_t, B, T, long, s):
+        L, p = _lib.lib(), (lambda t: t.data_ptr())
+        D, H, F, M = self.D, self.H, self.F, B * T
+        lay = self.layers[l]
+        x, xl, mix = bf["x"], bf["xl"], bf["mix"]
+        # ── time mix ──
+        _lib.check(L.rwkv_layer_norm(p(x), _lib.F32, None, 0, p(lay["ln1"][0]), p(lay["ln1"][1]), p(xl), M, D,
+                                     LN_EPS, s))
+        prev = bf["prev"][:B]
+        rkv_in = bf["rkv_in"]
+        if long:   # r/k/v inputs fp16 [3, M, D] for the GEMM
+            y0 = (rkv_in, _lib.F16, D, M * D)
+        else:      # fp32 [M, 3, D] for the fused GEMV
+            y0 = (rkv_in, _lib.F32, 3 * D, D)
+        _lib.check(L.rwkv_x070_seq_shift_mix(p(xl), p(state.tmix_prev[l]), p(prev), p(len_t), p(lay["coef6"]), 6, 3,
+                                             p(y0[0]), y0[1], y0[2], y0[3], p(mix), D, M * D, B, T, D, s))
+        state.tmix_prev[l].copy_(prev)
+        self._prefill_proj(self.proj[f"blocks.{l}.att.rkv"], rkv_in, bf["y_rkv"], 0, M, long, s)
+        Aw, Aa, Av, Ag, Bw, Ba, Bv, Bg = self._lowrank_f32(l)
+        # mix rows: r, k, v, w, a, g
+        torch.mm(torch.tanh(torch.mm(mix[3], Aw.t())), Bw.t(), out=bf["ww"])
+        torch.mm(torch.mm(mix[4], Aa.t()), Ba.t(), out=bf["aa"])
+        if l > 0:
+            torch.mm(torch.mm(mix[2], Av.t()), Bv.t(), out=bf["vv"])
+        torch.mm(torch.sigmoid(torch.mm(mix[5], Ag.t())), Bg.t(), out=bf["gate"])
+        bias = lay["bias"]
+        _lib.check(L.rwkv_x070_seq_tmix_pre(p(bf["y_rkv"]), p(bf["ww"]), p(bf["aa"]), p(bf["vv"]) if l > 0 else None,
+                                            p(bias[0]), p(bias[1]), p(bias[2]) if l > 0 else None, p(lay["k_k"]),
+                                            p(lay["k_a"]), p(bf["v_first"]), int(l == 0), p(len_t), p(bf["r"]),
+                                            p(bf["w"]), p(bf["k"]), p(bf["v"]), p(bf["a"]), p(bf["b"]), p(bf["kb"]),
+                                            B, T, H, s))
+        st = state.wkv[l]
+        _lib.check(L.rwkv_wkv7_seq_fwd(p(bf["r"]), p(bf["w"]), p(bf["k"]), p(bf["v"]), p(bf["a"]), p(bf["b"]),
+                                       _lib.F32, p(st), p(bf["wkv"]), p(st), B, T, H, s))
+        _lib.check(L.rwkv_wkv_tail(p(bf["wkv"]), p(bf["r"]), p(bf["kb"]), p(bf["v"]), p(lay["r_k"]), p(lay["lnx"][0]),
+                                   p(lay["lnx"][1]), p(bf["gate"]), p(bf["tout"]), M, H, HEAD, LNX_EPS, s))
+        self._prefill_proj(self.proj[f"blocks.{l}.att.output.weight"], bf["tout"], x, 1, M, long, s)
+        # ── channel mix ──
+        _lib.check(L.rwkv_layer_norm(p(x), _lib.F32, None, 0, p(lay["ln2"][0]), p(lay["ln2"][1]), p(xl), M, D,
+                                     LN_EPS, s))
+        xk, hk = bf["xk"], bf["hk"]
+        _lib.check(L.rwkv_x070_seq_shift_mix(p(xl), p(state.cmix_prev[l]), p(prev), p(len_t), p(lay["ck"]), 1, 1,
+                                             p(xk), _lib.F16 if long else _lib.F32, D, M * D, None, 0, 0, B, T, D, s))
+        state.cmix_prev[l].copy_(prev)
+        self._prefill_proj(self.proj[f"blocks.{l}.ffn.key.weight"], xk, hk, 2, M, long, s)
+        self._prefill_proj(self.proj[f"blocks.{l}.ffn.value.weight"], hk, x, 1, M, long, s)
+
+    def _prefill_proj(self, q, x, y, ep, M, long, s):
+        """A projection of the parallel pass: ep 0 store, 1 add into y, 2
+        relu²; long passes through the fp16 base (fp16 inputs / relu² output
+        where the buffers are fp16), short ones through the fp32 GEMV."""
+        if not long:
+            if isinstance(q, list):   # r / k / v one by one: x [M, 3, D] → y [M, 3D]
+                for k, qk in enumerate(q):
+                    xi = x[:, k].contiguous()
+                    yi = torch.empty((M, qk.OUT), dtype=torch.float32, device=self.device)
+                    self._run(qk, xi, yi, 0, M, s)
+                    y[:, k * qk.OUT:(k + 1) * qk.OUT].copy_(yi)
+                return
+            self._run(q, x, y, ep, M, s)
+            return
+        parts = q if isinstance(q, list) else [q]
+        G = len(parts) if isinstance(q, list) else (q.OUT // q.out_per)
+        if (not isinstance(q, list) and q.kind == "sb6" and q.xbits == 0
+                and _lib.lib().rwkv_sb6_gemm_applies(q.OUT, q.IN, 0, q.out_per)):
+            xdt = _lib.F16 if x.dtype == torch.float16 else _lib.F32
+            _lib.check(_lib.lib().rwkv_sb6_gemm(x.data_ptr(), xdt, M, q.IN, M * q.IN, q.bufs[0].data_ptr(),
+                                                q.bufs[1].data_ptr(), q.bufs[2].data_ptr(), y.data_ptr(), q.OUT, q.OUT,
+                                                q.IN, 0, q.out_per, ep, s))
+            return
+        # other layouts: the reference's long pass — dequantise to fp16, library GEMM in fp16
+        from .quant import rwkvq_dequant_dense, rwkvq_dequant_sym
+        xs = x.reshape(G, M, -1) if G > 1 else x.reshape(1, M, -1)
+        col = 0
+        for g, qq in enumerate(self._split_group(q)):
+            if qq.kind == "sb6":
+                W = rwkvq_dequant_dense(*qq.bufs, qq.OUT, qq.IN, 8, qq.xbits, torch.float16)
+            elif qq.kind == "sym":
+                W = rwkvq_dequant_sym(*qq.bufs, qq.OUT, qq.IN, qq.bits, torch.float16)
+            else:
+                W = qq.bufs[0].to(torch.float16)
+            prod = torch.mm(xs[g].to(torch.float16), W.t()).float()
+            dst = y[:, col:col + qq.OUT] if y.dim() == 2 else y
+            if ep == 0:
+                dst.copy_(prod)
+            elif ep == 1:
+                dst.add_(prod)
+            else:
+                dst.copy_(torch.relu(prod).square_().to(dst.dtype))
+            col += qq.OUT
+
+    @staticmethod
+    def _split_group(q):
+        """The member matrices of a projection (a fused group's row views)."""
+        if isinstance(q, list):
+            return q
+        if q.out_per == q.OUT:
+            return [q]
+        K = q.OUT // q.out_per
+        out = []
+        for g in range(K):
+            rows = slice(g * q.out_per, (g + 1) * q.out_per)
+            out.append(Proj(q.kind, tuple(b[rows] for b in q.bufs), q.out_per, q.IN, bits=q.bits, xbits=q.xbits))
+        return out
 
     def generate_batch(self, prompts, max_tokens: int, stop_tokens=()) -> List[List[int]]:
         """generateBatch (BatchGenerate.swift:71-116) with the greedy choice

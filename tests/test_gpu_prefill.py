@@ -1,0 +1,202 @@
+"""GPU parity of the parallel-pass (prefill) path.
+
+The sb6 matrix-core GEMM against the fp16-base long pass of the reference
+(X070Backbone.baseMatmul, X070Backbone.swift:337-356): every output is the
+fp16 rounding of an fp32-accurate sum of the exact products of the fp16
+inputs and fp16 dequantised weights: within ½ fp16 ulp plus 2^-16·Σ|x·w| of
+the exact value, and equal to its fp16 rounding for all but a small fraction
+of outputs.  Epilogues and
+fused groups are bitwise the plain launch and the separate operations; rows
+are independent of the other rows of the launch (bitwise).
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from swiftrwkv_amd import quant as Q
+from tests.test_gpu_model_shapes import random_k3
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def check_f16_rounding(got, exact, mag):
+    """got = fp16(acc) with |acc − exact| ≤ 2^-16·Σ|x·w| (an fp32 sum of the
+    same products): |got − exact| ≤ ½ ulp16 + 2^-16·mag everywhere.  Returns
+    the fraction of outputs that differ from fp16(exact)."""
+    got = np.asarray(got, np.float64)
+    assert np.all(np.isfinite(got))
+    ulp = np.maximum(np.spacing(np.abs(got).astype(np.float16)).astype(np.float64),
+                     np.spacing(np.abs(exact).astype(np.float16)).astype(np.float64))
+    excess = np.abs(got - exact) - (0.5 * ulp + 2.0 ** -16 * mag)
+    assert excess.max() <= 0, f"worst excess {excess.max():.3e} at {np.unravel_index(excess.argmax(), excess.shape)}"
+    return float((got != exact.astype(np.float16).astype(np.float64)).mean())
+
+
+@pytest.mark.parametrize("M,OUT,IN", [(1, 256, 256), (37, 768, 768), (300, 3072, 768), (128, 768, 3072),
+                                      (257, 4096, 1024), (130, 1024, 4096)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
+def test_sb6_gemm_matches_f16_base_pass(orc, M, OUT, IN, xdt):
+    case(f"sb6 gemm M={M} {OUT}x{IN} x {xdt}")
+    rng = np.random.default_rng(M + OUT + IN)
+    qblk, qsqm, ddm = random_k3(OUT, IN, rng)
+    x = rng.standard_normal((M, IN)).astype(np.float32)
+    if xdt == torch.float16:
+        x = x.astype(np.float16).astype(np.float32)
+    y = Q.rwkvq_sb6_gemm(dev(x).to(xdt), dev(qblk), dev(qsqm), dev(ddm), OUT, IN)
+    exact, mag = orc.sb6_matmul_f16_base(x, qblk, qsqm, ddm.view(np.uint16), OUT, IN)
+    frac = check_f16_rounding(y.cpu().numpy(), exact, mag)
+    print(f"[gemm] M={M} {OUT}x{IN}: {frac:.2e} of outputs on the other side of an fp16 boundary", flush=True)
+    assert frac < 5e-2
+
+
+def test_sb6_gemm_epilogues_groups_and_row_independence(orc):
+    case("sb6 gemm epilogues, r/k/v group, rows")
+    D, M = 1024, 200
+    rng = np.random.default_rng(7)
+    qblk, qsqm, ddm = (dev(z) for z in random_k3(3 * D, D, rng))
+    x = dev(rng.standard_normal((3, M, D)).astype(np.float32))
+    fused = Q.rwkvq_sb6_gemm(x, qblk, qsqm, ddm, 3 * D, D, out_per=D)
+    for g in range(3):
+        rows = slice(g * D, (g + 1) * D)
+        sep = Q.rwkvq_sb6_gemm(x[g], qblk[rows], qsqm[rows], ddm[rows], D, D)
+        assert torch.equal(fused[:, rows], sep), g
+        for m in (0, 63, 199):   # a row alone gives the same bits as inside the launch
+            assert torch.equal(Q.rwkvq_sb6_gemm(x[g, m:m + 1], qblk[rows], qsqm[rows], ddm[rows], D, D)[0], sep[m])
+    base = dev(rng.standard_normal((M, D)).astype(np.float32))
+    y0 = Q.rwkvq_sb6_gemm(x[1], qblk[:D], qsqm[:D], ddm[:D], D, D)
+    y1 = base.clone()
+    Q.rwkvq_sb6_gemm(x[1], qblk[:D], qsqm[:D], ddm[:D], D, D, epilogue="add", out=y1)
+    assert torch.equal(y1, base + y0)
+    h = Q.rwkvq_sb6_gemm(x[1], qblk[:D], qsqm[:D], ddm[:D], D, D, epilogue="relu2_f16")
+    assert h.dtype == torch.float16
+    assert torch.equal(h, (torch.relu(y0) * torch.relu(y0)).to(torch.float16))
+    # fp16 inputs equal fp32 inputs holding the same fp16 values
+    x16 = x[1].to(torch.float16)
+    assert torch.equal(Q.rwkvq_sb6_gemm(x16, qblk[:D], qsqm[:D], ddm[:D], D, D),
+                       Q.rwkvq_sb6_gemm(x16.float(), qblk[:D], qsqm[:D], ddm[:D], D, D))
+    with pytest.raises(ValueError):
+        Q.rwkvq_sb6_gemm(x[0], qblk[:D], qsqm[:D], ddm[:D], D + 64, D)
+
+
+# ───────────────────────── the parallel (prefill) pass of the model ─────────────────────────
+
+from oracle import x070 as X                      # noqa: E402
+from swiftrwkv_amd import synthetic as syn        # noqa: E402
+from swiftrwkv_amd.x070 import X070Decoder        # noqa: E402
+
+TINY = syn.X070Shape("tiny", 2, 256, 1024, vocab=512)
+# lengths around the 16-token chunk of the reference kernels (BatchGenerateTests.swift:29-30)
+PROMPTS = [[1, 2, 3, 4, 5], [7, 8, 9, 10, 11, 12, 13, 14, 15], [42], [(i * 5) % 512 for i in range(16)],
+           [(i * 3 + 1) % 512 for i in range(17)]]
+
+
+def rel(ref, got):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(ref - np.asarray(got, np.float64)).max() / (np.abs(ref).max() + 1e-30))
+
+
+@pytest.fixture(scope="module")
+def tiny_model():
+    proj = syn.x070_projections(TINY, nthreads=4)
+    return proj, X.dequant_projections(proj)
+
+
+@pytest.mark.parametrize("lora", ["f32", "f16"])
+def test_prefill_fp32_base_matches_oracle_and_rows_are_independent(tiny_model, lora):
+    """fp32 base (every projection on the fp32 GEMV): each row's last logits
+    and states against the oracle's parallel pass of that prompt alone
+    (1e-4), and each row against the same prompt prefilled alone (1e-5): the
+    pad steps are neutral and rows do not see each other."""
+    case(f"prefill fp32 base, low-rank {lora}")
+    proj, W = tiny_model
+    p = syn.x070_dense_params(TINY, seed=31, lora_dtype=np.float32 if lora == "f32" else np.float16)
+    dec = X070Decoder(TINY.n_layer, TINY.n_embd, TINY.ffn, TINY.vocab, p, proj, DEV)
+    logits, st = dec.prefill_batch(PROMPTS, base_dtype=torch.float32)
+    assert logits.shape == (len(PROMPTS), TINY.vocab)
+    for i, pr in enumerate(PROMPTS):
+        ref, ost = X.prefill(p, W, pr, TINY.n_layer, TINY.n_head)
+        e = rel(ref, logits[i].cpu().numpy())
+        ew = rel(ost.wkv[:, 0], st.wkv[:, i].cpu().numpy())
+        es = max(rel(ost.tmix_prev[:, 0], st.tmix_prev[:, i].cpu().numpy()),
+                 rel(ost.cmix_prev[:, 0], st.cmix_prev[:, i].cpu().numpy()))
+        print(f"[prefill] fp32 base row {i} (T={len(pr)}): logits {e:.2e}, wkv {ew:.2e}, shift {es:.2e}", flush=True)
+        assert e < 1e-4 and ew < 1e-4 and es < 1e-4, i
+        alone, _ = dec.prefill_batch([pr], base_dtype=torch.float32)
+        assert rel(alone[0].cpu().numpy(), logits[i].cpu().numpy()) < 1e-5, i
+
+
+def test_prefill_fp16_base_long_pass_matches_oracle(tiny_model):
+    """fp16 base, every projection on the matrix-core long pass: the oracle
+    with the same fp16 rounding points (inputs, dequantised weights, product
+    outputs, relu²), within the flips an fp32 sum may take at those points."""
+    case("prefill fp16 base (matrix-core long pass)")
+    proj, W = tiny_model
+    p = syn.x070_dense_params(TINY, seed=32, lora_dtype=np.float16)
+    dec = X070Decoder(TINY.n_layer, TINY.n_embd, TINY.ffn, TINY.vocab, p, proj, DEV)
+    from swiftrwkv_amd import _lib
+    n0 = _lib.counters()["sb6_gemm"]
+    logits, st = dec.prefill_batch(PROMPTS, base_dtype=torch.float16, short_rows=0)
+    assert _lib.counters()["sb6_gemm"] - n0 == TINY.n_layer * 4   # r/k/v, o, ffn key, ffn value
+    for i, pr in enumerate(PROMPTS):
+        ref, ost = X.prefill(p, W, pr, TINY.n_layer, TINY.n_head, f16_base=True)
+        e = rel(ref, logits[i].cpu().numpy())
+        ew = rel(ost.wkv[:, 0], st.wkv[:, i].cpu().numpy())
+        print(f"[prefill] fp16 base row {i} (T={len(pr)}): logits {e:.2e}, wkv {ew:.2e}", flush=True)
+        assert e < 2e-3 and ew < 2e-3, i
+
+
+def test_prefill_then_decode_continues_the_prompt(tiny_model):
+    """The state a parallel prefill leaves continues by decode steps exactly
+    as decoding the prompt token by token does (fp32 base, 1e-4)."""
+    case("prefill then decode")
+    proj, W = tiny_model
+    p = syn.x070_dense_params(TINY, seed=33, lora_dtype=np.float32)
+    dec = X070Decoder(TINY.n_layer, TINY.n_embd, TINY.ffn, TINY.vocab, p, proj, DEV)
+    logits, st = dec.prefill_batch(PROMPTS[:2], base_dtype=torch.float32)
+    osts = []
+    for pr in PROMPTS[:2]:
+        o = X.State.zeros(TINY.n_layer, 1, TINY.n_head)
+        for tok in pr:
+            X.step(p, W, [tok], o, TINY.n_layer, TINY.n_head)
+        osts.append(o)
+    for step_ids in ([3, 4], [100, 200], [7, 7]):
+        got = dec.step_batch(step_ids, st).cpu().numpy()
+        for i, o in enumerate(osts):
+            ref = X.step(p, W, [step_ids[i]], o, TINY.n_layer, TINY.n_head)
+            assert rel(ref, got[i]) < 1e-4, (step_ids, i)
+
+
+def test_prefill_0b4_width_fp16_base(orc):
+    """The 0.4B width (n_embd 1024, FFN 4096, H 16; four layers sharing
+    packed bytes, the 65536-row head), four prompts of 7..64 tokens on the
+    fp16 long pass, against the oracle with its rounding points."""
+    case("prefill 0.4B width, fp16 base")
+    shape = syn.X070Shape("0.4B width, 4 layers", 4, 1024, 4096)
+    proj = syn.x070_projections(shape, nthreads=16, share_layers=True)
+    memo, W = {}, {}
+    for k, q in proj.items():
+        if id(q[0]) not in memo:
+            memo[id(q[0])] = X.dequant_projections({k: q})[k]
+        W[k] = memo[id(q[0])]
+    p = syn.x070_dense_params(shape, seed=34, lora_dtype=np.float16)
+    dec = X070Decoder(shape.n_layer, shape.n_embd, shape.ffn, shape.vocab, p, proj, DEV)
+    rng = np.random.default_rng(34)
+    prompts = [list(rng.integers(0, shape.vocab, n)) for n in (64, 7, 33, 50)]
+    logits, _ = dec.prefill_batch(prompts, base_dtype=torch.float16, short_rows=0)
+    for i, pr in enumerate(prompts):
+        ref, _ = X.prefill(p, W, pr, shape.n_layer, shape.n_head, f16_base=True)
+        e = rel(ref, logits[i].cpu().numpy())
+        print(f"[prefill] 0.4B width fp16 base row {i} (T={len(pr)}): logits {e:.2e}", flush=True)
+        assert e < 2e-3, i

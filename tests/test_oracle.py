@@ -416,3 +416,25 @@ def test_cpu_baseline_wkv_step_matches_fp64(orc):
         assert np.abs(out - o64[:, 0]).max() / np.abs(o64).max() < 1e-5
         assert np.abs(h - h64).max() / np.abs(h64).max() < 1e-5
     assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+
+
+def test_f16_base_matmul_oracle(orc):
+    """The fp16-base long-pass anchor: one-hot inputs give the fp16 dequant
+    column exactly (a value exact in fp16 passes unrounded); an input that is
+    not an fp16 value is rounded (RNE) before the product; the magnitude is
+    Σ|x·w|."""
+    OUT, IN = 64, 512
+    t = make_sb6(OUT, IN, 0, np.random.default_rng(40))
+    qblk, qsqm, ddm, _ = orc.sb6_to_k3(t["cp"], None, None, t["qsqm_disk"], t["d"].view(np.uint16),
+                                       t["dm"].view(np.uint16), OUT, IN)
+    w16 = sb6_expected(t).astype(np.float16).astype(np.float64)   # one rounding of the fp32 dequant
+    for j in (0, 77, 511):
+        x = np.zeros((1, IN), np.float32)
+        x[0, j] = 1.0
+        exact, mag = orc.sb6_matmul_f16_base(x, qblk, qsqm, ddm, OUT, IN)
+        assert np.array_equal(exact[0], w16[:, j]) and np.array_equal(mag[0], np.abs(w16[:, j]))
+    x = np.zeros((1, IN), np.float32)
+    x[0, 5] = np.float32(1.0 + 2.0 ** -12)        # between fp16 neighbours 1 and 1 + 2^-10: rounds to 1
+    x[0, 9] = np.float32(1.0 + 3 * 2.0 ** -11)    # a tie: rounds to even, 1 + 2^-9
+    exact, _ = orc.sb6_matmul_f16_base(x, qblk, qsqm, ddm, OUT, IN)
+    assert np.allclose(exact[0], w16[:, 5] + (1.0 + 2.0 ** -9) * w16[:, 9], rtol=0, atol=1e-15)

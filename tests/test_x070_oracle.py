@@ -199,3 +199,26 @@ def file_projections(orc, T, shape):
         else:
             W[key] = f["dense"].astype(np.float64)
     return W
+
+
+def test_prefill_equals_sequence_and_steps():
+    """The oracle's parallel pass (fp32 base, fp32 low-rank matrices, where
+    `lin` has no narrowing either) equals the whole-sequence formulation's
+    last logits and the token-by-token decode, states included; the fp16 base
+    moves the logits by its roundings only (~1e-4)."""
+    p = syn.x070_dense_params(TINY, seed=12, lora_dtype=np.float32)
+    proj = syn.x070_projections(TINY, nthreads=4)
+    W = X.dequant_projections(proj)
+    ids = [5, 9, 300, 7, 100, 42]
+    lg, st = X.prefill(p, W, ids, TINY.n_layer, TINY.n_head)
+    seq = X.sequence(p, W, ids, TINY.n_layer, TINY.n_head)
+    assert np.abs(lg - seq[-1]).max() <= 1e-12 * np.abs(seq).max()
+    ost = X.State.zeros(TINY.n_layer, 1, TINY.n_head)
+    for i in ids:
+        step = X.step(p, W, [i], ost, TINY.n_layer, TINY.n_head)
+    assert np.abs(lg - step[0]).max() <= 1e-12 * np.abs(step).max()
+    for a, b in ((st.wkv, ost.wkv), (st.tmix_prev, ost.tmix_prev), (st.cmix_prev, ost.cmix_prev)):
+        assert np.abs(a - b).max() <= 1e-12 * (np.abs(b).max() + 1)
+    lg16, _ = X.prefill(p, W, ids, TINY.n_layer, TINY.n_head, f16_base=True)
+    d = np.abs(lg16 - lg).max() / np.abs(lg).max()
+    assert 1e-6 < d < 1e-2
