@@ -62,7 +62,7 @@ def parse():
     p.add_argument("--copies", type=int, default=6)
     p.add_argument("--skip-cpu", action="store_true")
     p.add_argument("--skip-wkv", action="store_true")
-    p.add_argument("--skip-more", action="store_true", help="skip batched and 1.5B decode")
+    p.add_argument("--skip-more", action="store_true", help="skip batched / 7B-class decode and the prefill pass")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--mode", choices=["bench", "kernels", "e2e"], default="bench",
                    help="kernels: run each dominant kernel alone (for rocprofv3 counter passes)")
@@ -492,6 +492,77 @@ def bench_decode_more(model_01, dev):
     return res
 
 
+def bench_prefill(dev, seconds_cap=60.0):
+    """The parallel prefill pass (X070Decoder.prefill_batch, fp16 base: the
+    sb6 projections on the matrix-core GEMM) of 128-token prompts of uniform
+    random ids at the 0.1B and 0.4B shapes, batch 1 / 8 / 32, and the whole
+    generate_batch workload at batch 8 (128-token prefill, then 256 greedy
+    steps); the 7B-class T = 8192 prefill; and the GEMM alone at the largest
+    projection of each (its MFMA roofline)."""
+    import numpy as np
+    import torch
+    from swiftrwkv_amd import quant as Q, synthetic as syn
+    from swiftrwkv_amd.x070 import X070Decoder
+
+    res = {}
+    rng = np.random.default_rng(5)
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    def gemm_line(model, key, M):
+        qblk, qsqm, ddm, OUT, IN = model.host[key]
+        q = model.dev[0][key] if key in model.dev[0] else None
+        if q is None:
+            return None
+        x = torch.randn((M, IN), device=dev).to(torch.float16)
+        ms = timed(lambda: Q.rwkvq_sb6_gemm(x, q[0], q[1], q[2], OUT, IN), 10) * 1e3
+        tf = 2 * M * OUT * IN / (ms * 1e-3) / 1e12
+        return {"shape": f"{M}x{OUT}x{IN}", "ms": ms, "TFLOPs": tf, "mfma_fp16_peak_frac": tf / 2500.0}
+
+    nthreads = min(16, os.cpu_count() or 1)
+    for shape in (syn.X070_0B1, syn.X070_0B4):
+        model = DecodeModel(shape, 1, dev, nthreads=nthreads, share_layers=shape is syn.X070_0B4)
+        dense = syn.x070_dense_params(shape, seed=11)
+        dec = X070Decoder(shape.n_layer, shape.n_embd, shape.ffn, shape.vocab, dense, model.host, dev)
+        for B in (1, 8, 32):
+            prompts = [list(rng.integers(0, shape.vocab, 128)) for _ in range(B)]
+            sec = timed(lambda: dec.prefill_batch(prompts, base_dtype=torch.float16), 3)
+            res[f"prefill_{shape.name}_B{B}_T128_fp16base"] = {"ms": sec * 1e3, "tok_s": B * 128 / sec}
+            log(f"prefill {shape.name} B{B} T128: {sec * 1e3:.2f} ms ({B * 128 / sec:.0f} tok/s)")
+        prompts = [list(rng.integers(0, shape.vocab, 128)) for _ in range(8)]
+        t0 = time.perf_counter()
+        out = dec.generate_batch(prompts, 256)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        res[f"generate_batch_{shape.name}_B8_prefill128_new256"] = {
+            "s": el, "new_tok_s": sum(len(o) for o in out) / el,
+            "note": "eager decode steps (no HIP graph), greedy choice on the host after each step"}
+        log(f"generate_batch {shape.name} B8: {el:.2f} s")
+        res[f"gemm_{shape.name}_ffn_key_M4096"] = gemm_line(model, "blocks.0.ffn.key.weight", 4096)
+        del dec, model
+        torch.cuda.empty_cache()
+    # 7B class: one pass over a T = 8192 prompt, 32 layers sharing packed bytes
+    shape = syn.X070_7B
+    model = DecodeModel(shape, 1, dev, nthreads=nthreads, share_layers=True)
+    dense = syn.x070_dense_params(shape, seed=11)
+    dec = X070Decoder(shape.n_layer, shape.n_embd, shape.ffn, shape.vocab, dense, model.host, dev)
+    prompt = [list(rng.integers(0, shape.vocab, 8192))]
+    sec = timed(lambda: dec.prefill_batch(prompt, base_dtype=torch.float16), 1)
+    res["prefill_7B_B1_T8192_fp16base"] = {"ms": sec * 1e3, "tok_s": 8192 / sec}
+    log(f"prefill 7B T8192: {sec * 1e3:.1f} ms")
+    res["gemm_7B_ffn_key_M8192"] = gemm_line(model, "blocks.0.ffn.key.weight", 8192)
+    del dec, model
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_head_gemv(model, dev, reps=60):
     """Average duration of the head GEMV over rotated weight copies (HBM)."""
     import torch
@@ -797,6 +868,7 @@ def main():
         log("wkv done")
     if not args.skip_more:
         extra.update(bench_decode_more(model01, dev))
+        extra.update(bench_prefill(dev))
     if not args.skip_cpu:
         extra["cpu_wkv7_fwd_B1_T1024_H12"] = cpu_wkv_baseline()
         log("cpu baseline done")
