@@ -66,6 +66,22 @@ rwkv_status rwkv_wkv7_seq_fwd(const void* r, const void* w, const void* k, const
                               const float* h_in, float* out, float* h_out,
                               int64_t B, int64_t T, int64_t H, void* stream);
 
+/* Whole-sequence frozen forward computed in 32-token time chunks, in
+ * parallel over the chunks (the same recurrence as rwkv_wkv7_seq_fwd,
+ * WKV7.swift:213-220, in its chunked matrix form): for sequences with few
+ * (batch, head) rows, where one workgroup per row walking T steps leaves the
+ * GPU idle.  Same arguments and layouts as rwkv_wkv7_seq_fwd, plus a device
+ * workspace of at least rwkv_wkv7_chunked_workspace(B, T, H) bytes, 16-byte
+ * aligned (48 KiB per 32 tokens per head).  Agrees with rwkv_wkv7_seq_fwd to
+ * fp32 rounding, not bitwise.  h_out may alias h_in.  Prefill counterpart of
+ * wkv7SequenceForward (WKV7.swift:242-264); no separate reference entry. */
+int64_t rwkv_wkv7_chunked_workspace(int64_t B, int64_t T, int64_t H);
+rwkv_status rwkv_wkv7_seq_fwd_chunked(const void* r, const void* w, const void* k, const void* v,
+                                      const void* a, const void* b, rwkv_dtype in_dt,
+                                      const float* h_in, float* out, float* h_out,
+                                      int64_t B, int64_t T, int64_t H,
+                                      void* workspace, int64_t workspace_bytes, void* stream);
+
 /* One 16-token chunk, also emitting sa = S·a per step.
  * Replaces wkv7ChunkForward (WKV7.swift:64-82).  T must equal 16.
  * h_in is required (the reference passes an explicit state). */
@@ -459,6 +475,7 @@ typedef struct {
     int64_t sym_rows;       /* rwkv_sym_rows launches (no reference counter) */
     int64_t x070;           /* layer_norm / x070_* launches (no reference counter) */
     int64_t sb6_gemm;       /* rwkv_sb6_gemm launches (no reference counter) */
+    int64_t seq_chunked;    /* rwkv_wkv7_seq_fwd_chunked launches (no reference counter) */
 } rwkv_counters;
 
 void rwkv_get_counters(rwkv_counters* out);

@@ -38,7 +38,7 @@ class RwkvHipError(RuntimeError):
 class Counters(ctypes.Structure):
     _fields_ = [(n, L) for n in ("seq_fwd", "chunk_fwd", "train_fwd", "train_bwd", "step", "tail",
                                  "sb6_dequant", "sym_dequant", "sb6_gemv", "sym_gemv", "sym_fused",
-                                 "step_tail", "sb6_fused", "sym_rows", "x070", "sb6_gemm")]
+                                 "step_tail", "sb6_fused", "sym_rows", "x070", "sb6_gemm", "seq_chunked")]
 
 
 class Finding(ctypes.Structure):
@@ -68,6 +68,8 @@ _SIGS = {
     "rwkv_wkv7_chunk": (I, []),
     "rwkv_wkv7_seq_fwd": (I, [P] * 6 + [I, P, P, P, L, L, L, P]),
     "rwkv_wkv7_chunk_fwd": (I, [P] * 6 + [I, P, P, P, P, L, L, L, P]),
+    "rwkv_wkv7_chunked_workspace": (L, [L, L, L]),
+    "rwkv_wkv7_seq_fwd_chunked": (I, [P] * 6 + [I, P, P, P, L, L, L, P, L, P]),
     "rwkv_wkv7_train_fwd": (I, [P] * 6 + [I, P, P, P, P, P, L, L, L, P]),
     "rwkv_wkv7_train_bwd": (I, [P] * 6 + [I, P, P, P, P, P] + [P] * 6 + [I, P, L, L, L, I, P]),
     "rwkv_wkv7_step": (I, [P] * 6 + [I, P, P, P, L, L, P]),

@@ -89,6 +89,40 @@ def wkv7_sequence_forward(r, w, k, v, a, b, h_in=None) -> Tuple[torch.Tensor, to
     return out, h_out
 
 
+def wkv7_chunked_workspace_bytes(B: int, T: int, H: int) -> int:
+    """Device workspace the time-chunked forward needs (48 KiB per 32 tokens
+    per head)."""
+    return int(_lib.lib().rwkv_wkv7_chunked_workspace(B, T, H))
+
+
+def wkv7_sequence_forward_chunked(r, w, k, v, a, b, h_in=None,
+                                  workspace: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The whole-sequence forward of wkv7_sequence_forward (WKV7.swift:242-264)
+    computed in 32-token chunks, in parallel over the chunks: for prefill with
+    few (batch, head) rows.  Same inputs and outputs; agrees with the
+    step-by-step kernel to fp32 rounding (not bitwise).  `workspace` is an
+    optional uint8 device buffer of at least wkv7_chunked_workspace_bytes."""
+    (r, w, k, v, a, b), dt = _prep([r, w, k, v, a, b])
+    B, T, H, D = r.shape
+    if T < 1:
+        raise ValueError(f"T ({T}) must be >= 1")
+    if D != WKV7_HEAD_SIZE:
+        raise ValueError(f"D ({D}) must equal HEAD_SIZE {WKV7_HEAD_SIZE}")
+    h = _state(h_in, (B, H, D, D), r.device)
+    need = wkv7_chunked_workspace_bytes(B, T, H)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=r.device)
+    elif workspace.device != r.device or workspace.numel() * workspace.element_size() < need \
+            or not workspace.is_contiguous() or workspace.data_ptr() % 16:
+        raise ValueError(f"workspace must be a contiguous, 16-byte aligned buffer of >= {need} bytes on {r.device}")
+    out = torch.empty((B, T, H, D), dtype=torch.float32, device=r.device)
+    h_out = torch.empty((B, H, D, D), dtype=torch.float32, device=r.device)
+    _lib.call("rwkv_wkv7_seq_fwd_chunked", _ptr(r), _ptr(w), _ptr(k), _ptr(v), _ptr(a), _ptr(b), dt, _ptr(h),
+              _ptr(out), _ptr(h_out), B, T, H, _ptr(workspace), workspace.numel() * workspace.element_size(),
+              _stream(r))
+    return out, h_out
+
+
 def wkv7_chunk_forward(r, w, k, v, a, b, h_in) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """One 16-token chunk (WKV7.swift:64-82): (out, h_out, sa_out)."""
     (r, w, k, v, a, b), dt = _prep([r, w, k, v, a, b])
@@ -143,7 +177,8 @@ def wkv7_forward(r, w, k, v, a, b) -> torch.Tensor:
 
 
 def wkv7_sequence_launches() -> int:
-    return _lib.counters()["seq_fwd"]
+    c = _lib.counters()
+    return c["seq_fwd"] + c["seq_chunked"]
 
 
 # ───────────────────────────── training (autograd) ─────────────────────────────

@@ -107,6 +107,16 @@ class Proj:
             self.out_per = self.OUT
 
 
+def wkv_chunked_prefers(B: int, T: int, H: int) -> bool:
+    """Whether the time-chunked WKV-7 forward beats the step-by-step kernel
+    for a [B, T, H] pass on MI355X: the step kernel runs B·H·4 workgroups
+    for T steps each, the chunked one B·H·⌈T/32⌉ workgroups and then a scan
+    of ⌈T/32⌉ steps, so it wins where B·H is small and T long (measured: B1
+    T1024 H12 48 vs 139 µs, B1 T8192 H64 0.77 vs 1.2 ms; B32 T128 H16 loses,
+    114 vs 63 µs)."""
+    return B * H <= 128 and T >= 512
+
+
 class X070Decoder:
     """Device-resident x070 model (quantised projections + dense parameters)
     and its one-token step.
@@ -418,7 +428,8 @@ class X070Decoder:
             raise ValueError(f"step_batch: {len(ids)} tokens for a batch of {state.n_rows}")
         return self.step(ids, state)
 
-    def prefill_batch(self, prompts, base_dtype=torch.float16, short_rows: int = 0) -> Tuple[torch.Tensor, RWKVState]:
+    def prefill_batch(self, prompts, base_dtype=torch.float16, short_rows: int = 0,
+                      wkv_chunked: Optional[bool] = None) -> Tuple[torch.Tensor, RWKVState]:
         """prefillBatch (BatchGenerate.swift:37-53): every prompt in one
         parallel pass — right padding to the longest prompt, a mask that makes
         the pad steps neutral for the recurrence, each row's shift state taken
@@ -432,7 +443,11 @@ class X070Decoder:
         with `base_dtype` fp16, B·T rows above `short_rows` take the fp16 long
         pass on the matrix cores (rwkv_sb6_gemm for 4-bit sb6; dequantise +
         library GEMM otherwise), the others the fp32 GEMV; with fp32 every
-        projection is the fp32 GEMV.  The head is the GEMV (decode: true)."""
+        projection is the fp32 GEMV.  The head is the GEMV (decode: true).
+        The WKV-7 pass runs in 32-token chunks in parallel over time
+        (rwkv_wkv7_seq_fwd_chunked) when `wkv_chunked` is True, or when it is
+        None and the pass has few (batch, head) rows and a long T
+        (wkv_chunked_prefers); otherwise step by step (rwkv_wkv7_seq_fwd)."""
         if len(prompts) == 0:
             raise ValueError("prefill_batch: no prompts")
         if any(len(p) == 0 for p in prompts):
@@ -455,6 +470,12 @@ class X070Decoder:
         s = torch.cuda.current_stream(dev).cuda_stream
         long = base_dtype == torch.float16 and M > short_rows
         bf = self._prefill_buffers(M, long)
+        chunked = wkv_chunked_prefers(B, T, self.H) if wkv_chunked is None else bool(wkv_chunked)
+        if chunked:
+            need = int(_lib.lib().rwkv_wkv7_chunked_workspace(B, T, self.H))
+            if bf.get("wkv_ws") is None or bf["wkv_ws"].numel() < need:
+                bf["wkv_ws"] = torch.empty(need, dtype=torch.uint8, device=dev)
+        bf["chunked"] = chunked
         L, p = _lib.lib(), (lambda t: t.data_ptr())
         x = bf["x"]
         emb_dt = _lib.F16 if self.emb.dtype == torch.float16 else _lib.F32
@@ -533,8 +554,14 @@ class X070Decoder:
                                             p(bf["w"]), p(bf["k"]), p(bf["v"]), p(bf["a"]), p(bf["b"]), p(bf["kb"]),
                                             B, T, H, s))
         st = state.wkv[l]
-        _lib.check(L.rwkv_wkv7_seq_fwd(p(bf["r"]), p(bf["w"]), p(bf["k"]), p(bf["v"]), p(bf["a"]), p(bf["b"]),
-                                       _lib.F32, p(st), p(bf["wkv"]), p(st), B, T, H, s))
+        if bf["chunked"]:
+            ws = bf["wkv_ws"]
+            _lib.check(L.rwkv_wkv7_seq_fwd_chunked(p(bf["r"]), p(bf["w"]), p(bf["k"]), p(bf["v"]), p(bf["a"]),
+                                                   p(bf["b"]), _lib.F32, p(st), p(bf["wkv"]), p(st), B, T, H,
+                                                   p(ws), ws.numel(), s))
+        else:
+            _lib.check(L.rwkv_wkv7_seq_fwd(p(bf["r"]), p(bf["w"]), p(bf["k"]), p(bf["v"]), p(bf["a"]), p(bf["b"]),
+                                           _lib.F32, p(st), p(bf["wkv"]), p(st), B, T, H, s))
         _lib.check(L.rwkv_wkv_tail(p(bf["wkv"]), p(bf["r"]), p(bf["kb"]), p(bf["v"]), p(lay["r_k"]), p(lay["lnx"][0]),
                                    p(lay["lnx"][1]), p(bf["gate"]), p(bf["tout"]), M, H, HEAD, LNX_EPS, s))
         self._prefill_proj(self.proj[f"blocks.{l}.att.output.weight"], bf["tout"], x, 1, M, long, s)

@@ -157,6 +157,38 @@ def test_prefill_fp16_base_long_pass_matches_oracle(tiny_model):
         assert e < 2e-3 and ew < 2e-3, i
 
 
+def test_prefill_time_chunked_wkv_matches_oracle(tiny_model):
+    """The prefill with its WKV-7 pass in 32-token chunks (forced for the
+    short prompts, chosen by itself for a 600-token one): the oracle at the
+    fp32 bar (1e-4), and the step-by-step pass within fp32 rounding (1e-5)."""
+    case("prefill fp32 base, time-chunked WKV")
+    from swiftrwkv_amd import _lib
+    from swiftrwkv_amd.x070 import wkv_chunked_prefers
+    proj, W = tiny_model
+    p = syn.x070_dense_params(TINY, seed=35, lora_dtype=np.float32)
+    dec = X070Decoder(TINY.n_layer, TINY.n_embd, TINY.ffn, TINY.vocab, p, proj, DEV)
+    n0 = _lib.counters()["seq_chunked"]
+    logits, st = dec.prefill_batch(PROMPTS, base_dtype=torch.float32, wkv_chunked=True)
+    assert _lib.counters()["seq_chunked"] - n0 == TINY.n_layer
+    step_logits, step_st = dec.prefill_batch(PROMPTS, base_dtype=torch.float32, wkv_chunked=False)
+    for i, pr in enumerate(PROMPTS):
+        ref, ost = X.prefill(p, W, pr, TINY.n_layer, TINY.n_head)
+        e, ew = rel(ref, logits[i].cpu().numpy()), rel(ost.wkv[:, 0], st.wkv[:, i].cpu().numpy())
+        print(f"[prefill] chunked WKV row {i} (T={len(pr)}): logits {e:.2e}, wkv {ew:.2e}", flush=True)
+        assert e < 1e-4 and ew < 1e-4, i
+        assert rel(step_logits[i].cpu().numpy(), logits[i].cpu().numpy()) < 1e-5, i
+    rng = np.random.default_rng(35)
+    long_prompt = [int(t) for t in rng.integers(0, TINY.vocab, 600)]
+    assert wkv_chunked_prefers(1, 600, TINY.n_head)
+    n0 = _lib.counters()["seq_chunked"]
+    logits, st = dec.prefill_batch([long_prompt], base_dtype=torch.float32)
+    assert _lib.counters()["seq_chunked"] - n0 == TINY.n_layer
+    ref, ost = X.prefill(p, W, long_prompt, TINY.n_layer, TINY.n_head)
+    e, ew = rel(ref, logits[0].cpu().numpy()), rel(ost.wkv[:, 0], st.wkv[:, 0].cpu().numpy())
+    print(f"[prefill] chunked WKV T=600: logits {e:.2e}, wkv {ew:.2e}", flush=True)
+    assert e < 1e-4 and ew < 1e-4
+
+
 def test_prefill_then_decode_continues_the_prompt(tiny_model):
     """The state a parallel prefill leaves continues by decode steps exactly
     as decoding the prompt token by token does (fp32 base, 1e-4)."""
