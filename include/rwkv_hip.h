@@ -82,6 +82,19 @@ rwkv_status rwkv_wkv7_seq_fwd_chunked(const void* r, const void* w, const void* 
                                       int64_t B, int64_t T, int64_t H,
                                       void* workspace, int64_t workspace_bytes, void* stream);
 
+/* rwkv_wkv7_seq_fwd_chunked with no workspace argument and no allocation:
+ * the chunk transforms live in a static 64 MiB device array of the library
+ * (one per GPU it runs on, held until the process ends), so at most
+ * B·H·ceil(T/32) <= 1365; larger passes return RWKV_E_SHAPE.  No counterpart
+ * in the reference: for callers that cannot allocate device memory (code
+ * under stream capture, serving loops, hosts that forbid hipMalloc).  Calls
+ * on one GPU share the array: calls that overlap on one GPU race.  Nothing
+ * in it needs clearing between calls. */
+rwkv_status rwkv_wkv7_seq_fwd_chunked_static(const void* r, const void* w, const void* k, const void* v,
+                                             const void* a, const void* b, rwkv_dtype in_dt,
+                                             const float* h_in, float* out, float* h_out,
+                                             int64_t B, int64_t T, int64_t H, void* stream);
+
 /* One 16-token chunk, also emitting sa = S·a per step.
  * Replaces wkv7ChunkForward (WKV7.swift:64-82).  T must equal 16.
  * h_in is required (the reference passes an explicit state). */

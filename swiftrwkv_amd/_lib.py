@@ -70,6 +70,7 @@ _SIGS = {
     "rwkv_wkv7_chunk_fwd": (I, [P] * 6 + [I, P, P, P, P, L, L, L, P]),
     "rwkv_wkv7_chunked_workspace": (L, [L, L, L]),
     "rwkv_wkv7_seq_fwd_chunked": (I, [P] * 6 + [I, P, P, P, L, L, L, P, L, P]),
+    "rwkv_wkv7_seq_fwd_chunked_static": (I, [P] * 6 + [I, P, P, P, L, L, L, P]),
     "rwkv_wkv7_train_fwd": (I, [P] * 6 + [I, P, P, P, P, P, L, L, L, P]),
     "rwkv_wkv7_train_bwd": (I, [P] * 6 + [I, P, P, P, P, P] + [P] * 6 + [I, P, L, L, L, I, P]),
     "rwkv_wkv7_step": (I, [P] * 6 + [I, P, P, P, L, L, P]),

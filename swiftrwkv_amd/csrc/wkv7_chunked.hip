@@ -39,6 +39,8 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "launch.h"
 
@@ -478,6 +480,68 @@ rwkv_status run_chunked(const void* r, const void* w, const void* k, const void*
 
 }  // namespace
 
+// Device scratch of the entry point that allocates nothing
+// (rwkv_wkv7_seq_fwd_chunked_static): 64 MiB, the workspace of at most 1365
+// (batch row, head, 32-token chunk) triples.  Every GPU the library runs on
+// holds its own copy until the process ends.  Host code never names the array
+// as an address: it uses the pointer hipGetSymbolAddress returns for the
+// current device.
+constexpr int64_t kScratchBytes = (int64_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch`, looked up once per device.
+rwkv_status scratch_on_current_device(void** out) {
+    int dev = -1;
+    RWKV_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices, RWKV_E_HIP,
+                 "wkv7_seq_fwd_chunked_static: no current HIP device (or device index %d >= %d)", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        RWKV_REQUIRE(e == hipSuccess && p, RWKV_E_HIP, "wkv7_seq_fwd_chunked_static: hipGetSymbolAddress: %s",
+                     hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return RWKV_OK;
+}
+
+rwkv_status seq_fwd_chunked(const char* who, const void* r, const void* w, const void* k, const void* v,
+                            const void* a, const void* b, rwkv_dtype in_dt, const float* h_in, float* out,
+                            float* h_out, int64_t B, int64_t T, int64_t H, void* workspace, int64_t workspace_bytes,
+                            void* stream) {
+    RWKV_REQUIRE(r && w && k && v && a && b && out && h_out && workspace, RWKV_E_NULL, "%s: null buffer", who);
+    RWKV_REQUIRE(rwkv::dtype_ok(in_dt), RWKV_E_DTYPE, "%s: dtype %d", who, (int)in_dt);
+    RWKV_REQUIRE(B >= 1 && T >= 1 && H >= 1 && B * H * ((T + CH - 1) / CH) <= INT32_MAX && B * H * 4 <= INT32_MAX &&
+                     B * T <= INT32_MAX && B * T * H * 64 < ((int64_t)1 << 40),
+                 RWKV_E_SHAPE, "%s: B=%lld T=%lld H=%lld", who, (long long)B, (long long)T, (long long)H);
+    const uintptr_t al = (uintptr_t)r | (uintptr_t)w | (uintptr_t)k | (uintptr_t)v | (uintptr_t)a | (uintptr_t)b |
+                         (uintptr_t)h_in | (uintptr_t)out | (uintptr_t)h_out | (uintptr_t)workspace;
+    RWKV_REQUIRE(al % 16 == 0, RWKV_E_SHAPE, "%s: every buffer must be 16-byte aligned", who);
+    const int64_t need = B * H * ((T + CH - 1) / CH) * (int64_t)WS_CHUNK * 4;
+    RWKV_REQUIRE(workspace_bytes >= need, RWKV_E_SHAPE, "%s: workspace %lld bytes, needs %lld", who,
+                 (long long)workspace_bytes, (long long)need);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    float* ws = reinterpret_cast<float*>(workspace);
+    rwkv_status st;
+    if (in_dt == RWKV_F32) st = run_chunked<float>(r, w, k, v, a, b, h_in, out, h_out, ws, (int)B, (int)T, (int)H, s);
+    else if (in_dt == RWKV_BF16)
+        st = run_chunked<__hip_bfloat16>(r, w, k, v, a, b, h_in, out, h_out, ws, (int)B, (int)T, (int)H, s);
+    else st = run_chunked<__half>(r, w, k, v, a, b, h_in, out, h_out, ws, (int)B, (int)T, (int)H, s);
+    RWKV_REQUIRE(st == RWKV_OK, st, "%s: launch failed", who);
+    rwkv::counters().seq_chunked.fetch_add(1);
+    rwkv::clear_error();
+    return RWKV_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int64_t rwkv_wkv7_chunked_workspace(int64_t B, int64_t T, int64_t H) {
@@ -489,29 +553,27 @@ rwkv_status rwkv_wkv7_seq_fwd_chunked(const void* r, const void* w, const void* 
                                       const void* b, rwkv_dtype in_dt, const float* h_in, float* out, float* h_out,
                                       int64_t B, int64_t T, int64_t H, void* workspace, int64_t workspace_bytes,
                                       void* stream) {
-    RWKV_REQUIRE(r && w && k && v && a && b && out && h_out && workspace, RWKV_E_NULL,
-                 "wkv7_seq_fwd_chunked: null buffer");
-    RWKV_REQUIRE(rwkv::dtype_ok(in_dt), RWKV_E_DTYPE, "wkv7_seq_fwd_chunked: dtype %d", (int)in_dt);
-    RWKV_REQUIRE(B >= 1 && T >= 1 && H >= 1 && B * H * ((T + CH - 1) / CH) <= INT32_MAX && B * H * 4 <= INT32_MAX &&
-                     B * T <= INT32_MAX && B * T * H * 64 < ((int64_t)1 << 40),
-                 RWKV_E_SHAPE, "wkv7_seq_fwd_chunked: B=%lld T=%lld H=%lld", (long long)B, (long long)T, (long long)H);
-    const uintptr_t al = (uintptr_t)r | (uintptr_t)w | (uintptr_t)k | (uintptr_t)v | (uintptr_t)a | (uintptr_t)b |
-                         (uintptr_t)h_in | (uintptr_t)out | (uintptr_t)h_out | (uintptr_t)workspace;
-    RWKV_REQUIRE(al % 16 == 0, RWKV_E_SHAPE, "wkv7_seq_fwd_chunked: every buffer must be 16-byte aligned");
-    const int64_t need = rwkv_wkv7_chunked_workspace(B, T, H);
-    RWKV_REQUIRE(workspace_bytes >= need, RWKV_E_SHAPE, "wkv7_seq_fwd_chunked: workspace %lld bytes, needs %lld",
-                 (long long)workspace_bytes, (long long)need);
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    float* ws = reinterpret_cast<float*>(workspace);
-    rwkv_status st;
-    if (in_dt == RWKV_F32) st = run_chunked<float>(r, w, k, v, a, b, h_in, out, h_out, ws, (int)B, (int)T, (int)H, s);
-    else if (in_dt == RWKV_BF16)
-        st = run_chunked<__hip_bfloat16>(r, w, k, v, a, b, h_in, out, h_out, ws, (int)B, (int)T, (int)H, s);
-    else st = run_chunked<__half>(r, w, k, v, a, b, h_in, out, h_out, ws, (int)B, (int)T, (int)H, s);
-    RWKV_REQUIRE(st == RWKV_OK, st, "wkv7_seq_fwd_chunked: launch failed");
-    rwkv::counters().seq_chunked.fetch_add(1);
-    rwkv::clear_error();
-    return RWKV_OK;
+    return seq_fwd_chunked("wkv7_seq_fwd_chunked", r, w, k, v, a, b, in_dt, h_in, out, h_out, B, T, H, workspace,
+                           workspace_bytes, stream);
+}
+
+rwkv_status rwkv_wkv7_seq_fwd_chunked_static(const void* r, const void* w, const void* k, const void* v,
+                                             const void* a, const void* b, rwkv_dtype in_dt, const float* h_in,
+                                             float* out, float* h_out, int64_t B, int64_t T, int64_t H,
+                                             void* stream) {
+    const char* who = "wkv7_seq_fwd_chunked_static";
+    RWKV_REQUIRE(B >= 1 && T >= 1 && H >= 1, RWKV_E_SHAPE, "%s: B=%lld T=%lld H=%lld", who, (long long)B,
+                 (long long)T, (long long)H);
+    RWKV_REQUIRE(B <= kScratchBytes && H <= kScratchBytes && B * H * ((T + CH - 1) / CH) * (int64_t)WS_CHUNK * 4 <=
+                                                                 kScratchBytes,
+                 RWKV_E_SHAPE,
+                 "%s: B·H·ceil(T/32) = %lld exceeds the static scratch (%lld chunks of 48 KiB, 64 MiB); use "
+                 "rwkv_wkv7_seq_fwd_chunked with a workspace",
+                 who, (long long)(B * H * ((T + CH - 1) / CH)), (long long)(kScratchBytes / (WS_CHUNK * 4)));
+    void* ptr = nullptr;
+    const rwkv_status st = scratch_on_current_device(&ptr);
+    if (st != RWKV_OK) return st;
+    return seq_fwd_chunked(who, r, w, k, v, a, b, in_dt, h_in, out, h_out, B, T, H, ptr, kScratchBytes, stream);
 }
 
 }  // extern "C"
