@@ -85,6 +85,73 @@ def kernel_ms(launch, stream=None) -> float:
     return e0.elapsed_time(e1)
 
 
+# MFMA issues of the chunk-transform kernel per 32-token chunk of one head:
+# 216 per wave × 4 waves + 8 for T21 (wkv7_chunk_prep_kernel), each
+# v_mfma_f32_16x16x4_f32 = 2048 flops.
+CHUNK_PREP_MFMA_FLOPS = (216 * 4 + 8) * 2048
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def graph_ms(launch, reps=20) -> float:
+    """Average replay time of a HIP graph holding `launch()`'s kernels (no
+    host overhead between them)."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        launch()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def bench_wkv_chunked(dev, B, T, H, gen, reps=10):
+    """The time-chunked WKV-7 forward (rwkv_wkv7_seq_fwd_chunked) next to the
+    step-by-step one on the same inputs: the call's two launches replayed from
+    a HIP graph, the chunk-transform kernel alone (its own timestamps) with
+    its matrix-core roofline, and the step kernel alone."""
+    import torch
+    from swiftrwkv_amd import _lib, kernel as K
+
+    x = [torch.from_numpy(z).to(dev) for z in gen(B, T, H, seed=0)]
+    ws = torch.empty(K.wkv7_chunked_workspace_bytes(B, T, H), dtype=torch.uint8, device=dev)
+    out = torch.empty((B, T, H, 64), device=dev)
+    h = torch.empty((B, H, 64, 64), device=dev)
+    ptrs = [z.data_ptr() for z in x]
+
+    def chunked():
+        _lib.call("rwkv_wkv7_seq_fwd_chunked", *ptrs, _lib.F32, None, out.data_ptr(), h.data_ptr(), B, T, H,
+                  ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+
+    def step():
+        _lib.call("rwkv_wkv7_seq_fwd", *ptrs, _lib.F32, None, out.data_ptr(), h.data_ptr(), B, T, H,
+                  torch.cuda.current_stream().cuda_stream)
+
+    ms = graph_ms(chunked, reps)
+    prep_ms = sum(kernel_ms(chunked) for _ in range(reps)) / reps
+    step_ms = sum(kernel_ms(step) for _ in range(reps)) / reps
+    n_chunks = B * H * ((T + 31) // 32)
+    flops = n_chunks * CHUNK_PREP_MFMA_FLOPS
+    del x, ws, out, h
+    torch.cuda.empty_cache()
+    return {"ms": ms, "tok_s": B * T / (ms * 1e-3), "step_kernel_ms": step_ms, "speedup_vs_step": step_ms / ms,
+            "chunk_prep_ms": prep_ms, "scan_ms": ms - prep_ms,
+            "chunk_prep_mfma_tflops": flops / (prep_ms * 1e-3) / 1e12,
+            "chunk_prep_mfma_frac": flops / (prep_ms * 1e-3) / (FP32_MFMA_PEAK_TFLOPS * 1e12)}
+
+
 # ───────────────────────────── decode model ─────────────────────────────
 
 class DecodeModel:
@@ -486,6 +553,9 @@ def bench_decode_more(model_01, dev):
     del model
     torch.cuda.empty_cache()
     res["wkv7_prefill_7B_B1_T8192_H64_fp32"] = bench_wkv_prefill_7b(dev)
+    from swiftrwkv_amd import synthetic as syn
+    res["wkv7_prefill_7B_B1_T8192_H64_fp32_chunked"] = bench_wkv_chunked(dev, 1, 8192, 64, syn.wkv_inputs_train,
+                                                                         reps=3)
     res["wkv7_decode_step_tail"] = bench_wkv_decode_step(dev)
     log(f"decode step+tail: {res['wkv7_decode_step_tail']}")
     log("7B prefill WKV done")
@@ -607,6 +677,7 @@ def bench_wkv(dev, reps=5):
                                          "valu_roofline_frac": (1024 * 12 * 9 * 64 * 64 / (ms * 1e-3)) / (VALU_PEAK_TFLOPS * 1e12),
                                          "hbm_roofline_frac": nbytes / (ms * 1e-3) / (HBM_PEAK_GBPS * 1e9)}
     del x
+    res["wkv7_fwd_B1_T1024_H12_fp32_chunked"] = bench_wkv_chunked(dev, 1, 1024, 12, syn.wkv_inputs_config0)
     # config 3: B8 T4096 H32 bf16 training forward (checkpointed) + backward
     B, T, H = 8, 4096, 32
     rng = np.random.default_rng(3)
