@@ -45,8 +45,9 @@ HEAD_GEMV_TRAFFIC_BYTES = 29494797
 # The same for the average GEMV launch of one 0.1B decode token (eager tokens
 # over rotated weight copies); same profile.
 DECODE_GEMV_TRAFFIC_BYTES = 1744043
-# The same for the average GEMV launch of one 1.5B decode token; null until measured.
-DECODE_1B5_GEMV_TRAFFIC_BYTES = None
+# The same for the average GEMV launch of one 1.5B decode token (582 launches
+# of 6 eager tokens; profiles/hbm_traffic_decode_1.5B_gemv_and_wkv7_chunked.md).
+DECODE_1B5_GEMV_TRAFFIC_BYTES = 8291062
 VALU_PEAK_TFLOPS = 157.3
 
 
@@ -799,10 +800,12 @@ def cpu_wkv_baseline():
 def profile_kernels(dev, tokens=12):
     """The dominant kernels alone, for rocprofv3: eager 0.1B decode tokens over
     6 rotated weight copies (49 GEMV launches each, the head GEMV among them,
-    and 12 WKV step+tail launches), the WKV-7 forward at B1 T1024 H12 fp32
-    (20 launches), the checkpointed training forward + backward at B8 T4096
-    H32 bf16 (3 each), and a plain 256 MiB device copy whose FETCH_SIZE /
-    WRITE_SIZE calibrate the counters (2 x 256 MiB of traffic)."""
+    and 12 WKV step+tail launches), 6 eager 1.5B decode tokens (97 GEMV
+    launches each), the WKV-7 forward at B1 T1024 H12 fp32 (20 launches), the
+    time-chunked forward at B1 T1024 H12 (5) and B1 T8192 H64 (2), the
+    checkpointed training forward + backward at B8 T4096 H32 bf16 (3 each),
+    and a plain 256 MiB device copy whose FETCH_SIZE / WRITE_SIZE calibrate
+    the counters (2 x 256 MiB of traffic)."""
     import numpy as np
     import torch
     from swiftrwkv_amd import _lib, kernel as K, synthetic as syn
@@ -819,9 +822,24 @@ def profile_kernels(dev, tokens=12):
         step.launch(i % 6, stream)
     torch.cuda.synchronize()
     log("decode tokens done")
+    del model, step
+    model = DecodeModel(syn.X070_1B5, 1, dev, nthreads=min(16, os.cpu_count() or 1))
+    step = DecodeStep(model, dev, B=1)
+    for _ in range(6):
+        step.launch(0, stream)
+    torch.cuda.synchronize()
+    del model, step
+    torch.cuda.empty_cache()
+    log("1.5B decode tokens done")
     x = [torch.from_numpy(z).to(dev) for z in syn.wkv_inputs_config0(1, 1024, 12, seed=0)]
     for _ in range(20):
         K.wkv7_sequence_forward(*x)
+    for _ in range(5):
+        K.wkv7_sequence_forward_chunked(*x)
+    x7 = [torch.from_numpy(z).to(dev) for z in syn.wkv_inputs_train(1, 8192, 64, seed=0)]
+    for _ in range(2):
+        K.wkv7_sequence_forward_chunked(*x7)
+    del x7
     B, T, H = 8, 4096, 32
     xs = syn.wkv_inputs_config0(B, T, H, seed=3)
     ins = [torch.from_numpy(z).to(dev).to(torch.bfloat16) for z in xs]

@@ -388,12 +388,18 @@ __device__ __forceinline__ void scan_load(ScanOps& o, const float* base, int c, 
 // separates every write from its readers.
 __global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const float* __restrict__ ws,
                                                               const float* __restrict__ h_in, float* __restrict__ out,
-                                                              float* __restrict__ h_out, int T, int H, int NC) {
+                                                              float* __restrict__ h_out, int T, int H, int NC, int BH) {
     __shared__ __attribute__((aligned(16))) float S[2][16 * RS];
     __shared__ __attribute__((aligned(16))) float Yp[2][4 * CH * 17];   // partial outputs [wave][token][row]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, li = lane & 15;
-    const int slice = blockIdx.x & 3, bh = blockIdx.x >> 2;
+    // workgroups are dealt to the 8 XCDs round-robin (id mod 8); the four
+    // row slices of a head get ids congruent mod 8, so they share one L2 and
+    // each chunk's P and G come from HBM once.  The grid is padded to whole
+    // groups of 8 heads.
+    const int xcd = blockIdx.x & 7, loc = blockIdx.x >> 3;
+    const int slice = loc & 3, bh = (loc >> 2) * 8 + xcd;
+    if (bh >= BH) return;
     const int h = bh % H, bb = bh / H;
     const int i0 = slice * 16;
     const int64_t hoff = (int64_t)bh * 4096;
@@ -473,8 +479,8 @@ rwkv_status run_chunked(const void* r, const void* w, const void* k, const void*
     const int NC = (T + CH - 1) / CH;
     rwkv::launch(wkv7_chunk_prep_kernel<TI>, dim3((unsigned)(B * H * NC)), dim3(256), s, (const TI*)r, (const TI*)w,
                  (const TI*)k, (const TI*)v, (const TI*)a, (const TI*)b, ws, T, H, NC);
-    rwkv::launch(wkv7_chunk_scan_kernel, dim3((unsigned)(B * H * 4)), dim3(256), s, (const float*)ws, h_in, out, h_out,
-                 T, H, NC);
+    rwkv::launch(wkv7_chunk_scan_kernel, dim3((unsigned)((B * H + 7) / 8 * 32)), dim3(256), s, (const float*)ws, h_in,
+                 out, h_out, T, H, NC, B * H);
     return hipGetLastError() == hipSuccess ? RWKV_OK : RWKV_E_HIP;
 }
 
@@ -518,7 +524,7 @@ rwkv_status seq_fwd_chunked(const char* who, const void* r, const void* w, const
                             void* stream) {
     RWKV_REQUIRE(r && w && k && v && a && b && out && h_out && workspace, RWKV_E_NULL, "%s: null buffer", who);
     RWKV_REQUIRE(rwkv::dtype_ok(in_dt), RWKV_E_DTYPE, "%s: dtype %d", who, (int)in_dt);
-    RWKV_REQUIRE(B >= 1 && T >= 1 && H >= 1 && B * H * ((T + CH - 1) / CH) <= INT32_MAX && B * H * 4 <= INT32_MAX &&
+    RWKV_REQUIRE(B >= 1 && T >= 1 && H >= 1 && B * H * ((T + CH - 1) / CH) <= INT32_MAX && (B * H + 7) / 8 * 32 <= INT32_MAX &&
                      B * T <= INT32_MAX && B * T * H * 64 < ((int64_t)1 << 40),
                  RWKV_E_SHAPE, "%s: B=%lld T=%lld H=%lld", who, (long long)B, (long long)T, (long long)H);
     const uintptr_t al = (uintptr_t)r | (uintptr_t)w | (uintptr_t)k | (uintptr_t)v | (uintptr_t)a | (uintptr_t)b |
