@@ -46,7 +46,7 @@ HEAD_GEMV_TRAFFIC_BYTES = 29494797
 # over rotated weight copies); same profile.
 DECODE_GEMV_TRAFFIC_BYTES = 1744043
 # The same for the average GEMV launch of one 1.5B decode token (582 launches
-# of 6 eager tokens; profiles/hbm_traffic_decode_1.5B_gemv_and_wkv7_chunked.md).
+# of 6 eager tokens; profiles/hbm_traffic_decode_1.5B_gemv.md).
 DECODE_1B5_GEMV_TRAFFIC_BYTES = 8291062
 VALU_PEAK_TFLOPS = 157.3
 
