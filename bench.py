@@ -234,6 +234,31 @@ class DecodeStep:
         self.lnw = t(rng.standard_normal((self.L, self.D)) * 0.5 + 1)
         self.lnb = t(rng.standard_normal((self.L, self.D)) * 0.1)
         self.g = t(rng.standard_normal((self.L, B, self.D)))
+        # batches of 8-32 rows take the matrix-core batched GEMV (one
+        # workspace for all projections: the launches run in stream order)
+        from swiftrwkv_amd import _lib, quant as Q
+        L = _lib.lib()
+        self.mfma, need = set(), 0
+        D, F = self.D, self.F
+        for OUT, IN, per in ((3 * D, D, D), (D, D, D), (F, D, F), (D, F, D), (s.vocab, D, s.vocab)):
+            if B <= 32 and Q.rwkvq_sb6_gemv_batch_prefers(B, OUT, IN) and \
+                    L.rwkv_sb6_gemv_batch_applies(B, OUT, IN, 0, per):
+                self.mfma.add((OUT, IN, per))
+                need = max(need, int(L.rwkv_sb6_gemv_batch_workspace(B, OUT, IN, per)))
+        self.ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+
+    def _gemv(self, L, x, q, y, OUT, IN, per, stream, fused=False):
+        from swiftrwkv_amd import _lib
+        if (OUT, IN, per) in self.mfma:
+            _lib.check(L.rwkv_sb6_gemv_batch(x.data_ptr(), self.B, q[0].data_ptr(), q[1].data_ptr(), q[2].data_ptr(),
+                                             y.data_ptr(), OUT, IN, 0, per, 0, self.ws.data_ptr(), self.ws.numel(),
+                                             stream))
+        elif fused:
+            _lib.check(L.rwkv_sb6_gemv_fused(x.data_ptr(), self.B, q[0].data_ptr(), q[1].data_ptr(), q[2].data_ptr(),
+                                             y.data_ptr(), OUT, IN, 0, per, stream))
+        else:
+            _lib.check(L.rwkv_sb6_gemv(x.data_ptr(), self.B, q[0].data_ptr(), q[1].data_ptr(), q[2].data_ptr(),
+                                       y.data_ptr(), OUT, IN, 0, stream))
 
     def launch(self, copy: int, stream: int, gemv_only=False):
         """Enqueue one token (`gemv_only`: its GEMV launches alone)."""
@@ -243,15 +268,12 @@ class DecodeStep:
         B, D, F, H = self.B, self.D, self.F, self.H
 
         def gemv(x, key, y):
-            q = W[key]
             OUT, IN = self.model.host[key][3], self.model.host[key][4]
-            _lib.check(L.rwkv_sb6_gemv(x.data_ptr(), B, q[0].data_ptr(), q[1].data_ptr(), q[2].data_ptr(),
-                                       y.data_ptr(), OUT, IN, 0, stream))
+            self._gemv(L, x, W[key], y, OUT, IN, OUT, stream)
 
         for l in range(self.L):
-            q = W[f"blocks.{l}.att.rkv"]   # r/k/v in one launch, x rows (x_r, x_k, x_v) per token
-            _lib.check(L.rwkv_sb6_gemv_fused(self.xrkv.data_ptr(), B, q[0].data_ptr(), q[1].data_ptr(),
-                                             q[2].data_ptr(), self.y_rkv.data_ptr(), 3 * D, D, 0, D, stream))
+            # r/k/v in one launch, x rows (x_r, x_k, x_v) per token
+            self._gemv(L, self.xrkv, W[f"blocks.{l}.att.rkv"], self.y_rkv, 3 * D, D, D, stream, fused=True)
             if gemv_only:
                 gemv(self.tail, f"blocks.{l}.att.output.weight", self.y_o)
                 gemv(self.xD, f"blocks.{l}.ffn.key.weight", self.y_k)

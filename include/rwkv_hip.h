@@ -201,6 +201,24 @@ rwkv_status rwkv_sb6_gemv(const float* x, int64_t N,
                           const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
                           float* y, int64_t OUT, int64_t IN, int xbits, void* stream);
 
+/* Batched sb6 4-bit GEMV on the matrix cores: y[n] = W·x[n] for 2 <= N <= 32
+ * input rows with the weights streamed once (bf16 MFMA; the inputs split
+ * exactly into three bf16 parts, the block scales folded in fp32 per
+ * 32-column unit).  Per row within fp32 rounding of rwkv_sb6_gemv on that
+ * row alone (not bitwise).  out_per: rows per input row (OUT for one matrix,
+ * D for a row-concatenated fused group reading x [N, OUT/out_per, IN]);
+ * multiple of 64.  epilogue as rwkv_sb6_gemv_ep (0 store, 1 add to y,
+ * 2 relu²).  workspace: >= rwkv_sb6_gemv_batch_workspace(N, OUT, IN, out_per)
+ * bytes, 16-byte aligned (fp32 partial sums of the K slices).  The batched
+ * counterpart of rwkvqSb6GEMV (RwkvqSb6GEMV.swift:159-190), which the
+ * reference launches once per row (BatchGenerate.swift:58-90). */
+int rwkv_sb6_gemv_batch_applies(int64_t N, int64_t OUT, int64_t IN, int xbits, int64_t out_per);
+int64_t rwkv_sb6_gemv_batch_workspace(int64_t N, int64_t OUT, int64_t IN, int64_t out_per);
+rwkv_status rwkv_sb6_gemv_batch(const float* x, int64_t N, const uint8_t* qblk, const uint8_t* qsqm,
+                                const uint16_t* ddm, float* y, int64_t OUT, int64_t IN, int xbits,
+                                int64_t out_per, int epilogue, void* workspace, int64_t workspace_bytes,
+                                void* stream);
+
 /* sb6 counterpart of the sym r/k/v fusion (no counterpart in the reference,
  * which fuses sym groups only, RwkvqSymGEMV.swift:343-358): K = OUT/out_per
  * row-concatenated sb6 matrices in one launch; row `o` of input row n uses
@@ -489,6 +507,7 @@ typedef struct {
     int64_t x070;           /* layer_norm / x070_* launches (no reference counter) */
     int64_t sb6_gemm;       /* rwkv_sb6_gemm launches (no reference counter) */
     int64_t seq_chunked;    /* rwkv_wkv7_seq_fwd_chunked launches (no reference counter) */
+    int64_t sb6_batch;      /* rwkv_sb6_gemv_batch calls (no reference counter) */
 } rwkv_counters;
 
 void rwkv_get_counters(rwkv_counters* out);

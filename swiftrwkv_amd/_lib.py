@@ -38,7 +38,8 @@ class RwkvHipError(RuntimeError):
 class Counters(ctypes.Structure):
     _fields_ = [(n, L) for n in ("seq_fwd", "chunk_fwd", "train_fwd", "train_bwd", "step", "tail",
                                  "sb6_dequant", "sym_dequant", "sb6_gemv", "sym_gemv", "sym_fused",
-                                 "step_tail", "sb6_fused", "sym_rows", "x070", "sb6_gemm", "seq_chunked")]
+                                 "step_tail", "sb6_fused", "sym_rows", "x070", "sb6_gemm", "seq_chunked",
+                                 "sb6_batch")]
 
 
 class Finding(ctypes.Structure):
@@ -69,6 +70,9 @@ _SIGS = {
     "rwkv_wkv7_seq_fwd": (I, [P] * 6 + [I, P, P, P, L, L, L, P]),
     "rwkv_wkv7_chunk_fwd": (I, [P] * 6 + [I, P, P, P, P, L, L, L, P]),
     "rwkv_wkv7_chunked_workspace": (L, [L, L, L]),
+    "rwkv_sb6_gemv_batch_applies": (I, [L, L, L, I, L]),
+    "rwkv_sb6_gemv_batch_workspace": (L, [L, L, L, L]),
+    "rwkv_sb6_gemv_batch": (I, [P, L, P, P, P, P, L, L, I, L, I, P, L, P]),
     "rwkv_wkv7_seq_fwd_chunked": (I, [P] * 6 + [I, P, P, P, L, L, L, P, L, P]),
     "rwkv_wkv7_seq_fwd_chunked_static": (I, [P] * 6 + [I, P, P, P, L, L, L, P]),
     "rwkv_wkv7_train_fwd": (I, [P] * 6 + [I, P, P, P, P, P, L, L, L, P]),

@@ -17,7 +17,7 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libswiftrwkv_hip.so")
 ARCH = os.environ.get("SWIFTRWKV_ARCH", "gfx950")
 
-HIP_SOURCES = ["wkv7.hip", "wkv7_chunked.hip", "rwkvq.hip", "x070.hip", "gemm.hip", "prefill.hip"]
+HIP_SOURCES = ["wkv7.hip", "wkv7_chunked.hip", "rwkvq.hip", "x070.hip", "gemm.hip", "gemv_mfma.hip", "prefill.hip"]
 HOST_SOURCES = ["host.cpp", "manifest.cpp"]
 
 # Packed-FP32 VALU ops are disabled for every device compile.

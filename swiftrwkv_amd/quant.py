@@ -590,6 +590,66 @@ def rwkvq_sb6_gemm(x, qblk, qsqm, ddm, out_features: int, in_features: int, xbit
     return out
 
 
+def rwkvq_sb6_gemv_batch_applies(rows: int, out_features: int, in_features: int, xbits: int,
+                                 out_per: Optional[int] = None) -> bool:
+    """Whether the matrix-core batched GEMV takes `rows` input rows of this
+    sb6 matrix (group): 4-bit codes, 2..32 rows, matrices of a multiple of 64
+    rows."""
+    per = out_features if out_per is None else out_per
+    return bool(_lib.lib().rwkv_sb6_gemv_batch_applies(rows, out_features, in_features, xbits, per))
+
+
+def rwkvq_sb6_gemv_batch_prefers(rows: int, out_features: int, in_features: int) -> bool:
+    """Where the batched matrix-core GEMV beats the one-input kernel run over
+    the rows (MI355X, measured per launch): 8+ rows of matrices of 2^24+
+    weights (7B-class layers, the heads: 4096x4096 x16 17 vs 20 µs,
+    14336x4096 x16 27 vs 72 µs, 65536x1024 x32 46 vs 112 µs); smaller ones
+    are bound by the launch pair it needs (1024x1024 x32 8.1 vs 7.6 µs)."""
+    return rows >= 8 and out_features * in_features >= (1 << 24)
+
+
+_GEMV_EP = {"store": 0, "add": 1, "relu2": 2}
+
+
+def rwkvq_sb6_gemv_batch(x, qblk, qsqm, ddm, out_features: int, in_features: int, xbits: int = 0,
+                         out_per: Optional[int] = None, epilogue: str = "store",
+                         out: Optional[torch.Tensor] = None,
+                         workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y [N, OUT] = x · Wᵀ for N = 2..32 input rows on the matrix cores, the
+    weights streamed once (the batched counterpart of rwkvq_sb6_gemv, within
+    fp32 rounding of it per row).  x [N, IN], or [N·K, IN] for K = OUT/out_per
+    fused matrices (row o of input n reads x[n·K + o/out_per]).  epilogue
+    "store" / "add" (into `out`, the residual stream) / "relu2".  `workspace`:
+    an optional uint8 device buffer of rwkv_sb6_gemv_batch_workspace bytes."""
+    per = out_features if out_per is None else out_per
+    if x.dim() != 2 or x.shape[1] != in_features:
+        raise ValueError(f"sb6 batched GEMV: input {tuple(x.shape)}, expected [N, {in_features}]")
+    K = out_features // per if per and out_features % per == 0 else 0
+    if K == 0 or x.shape[0] % K:
+        raise ValueError(f"sb6 batched GEMV: {x.shape[0]} input rows for {out_features} rows of matrices of {per}")
+    N = x.shape[0] // K
+    if not rwkvq_sb6_gemv_batch_applies(N, out_features, in_features, xbits, per):
+        raise ValueError(f"sb6 batched GEMV: N={N} [{out_features}, {in_features}] xbits={xbits} out_per={per} "
+                         "not taken")
+    x32 = _aligned(x.to(torch.float32))
+    qblk, qsqm, ddm = _sb6_bufs(qblk, qsqm, ddm, out_features, in_features, xbits)
+    ep = _GEMV_EP[epilogue]
+    if out is None:
+        if ep == 1:
+            raise ValueError("sb6 batched GEMV: the add epilogue needs `out`")
+        out = torch.empty((N, out_features), dtype=torch.float32, device=x.device)
+    elif out.dtype != torch.float32 or tuple(out.shape) != (N, out_features) or not out.is_contiguous() or \
+            out.device != x.device:
+        raise ValueError(f"sb6 batched GEMV: out must be a contiguous float32 [{N}, {out_features}] tensor")
+    need = int(_lib.lib().rwkv_sb6_gemv_batch_workspace(N, out_features, in_features, per))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _lib.call("rwkv_sb6_gemv_batch", x32.data_ptr(), N, qblk.data_ptr(), qsqm.data_ptr(), ddm.data_ptr(),
+              out.data_ptr(), out_features, in_features, xbits, per, ep, workspace.data_ptr(),
+              workspace.numel() * workspace.element_size(), _stream(x32))
+    return out
+
+
 RWKVQ_SYM_GEMV_MAX_ROWS = 4   # RwkvqSymGEMV.swift:40
 
 

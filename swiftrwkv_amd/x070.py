@@ -27,6 +27,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from . import quant as Q
 
 HEAD = 64
 LN_EPS = 1e-5
@@ -302,13 +303,17 @@ class X070Decoder:
     def launches_per_token(self, N: int = 1) -> int:
         """Kernel launches of one step of N rows: per layer 2 shift_mix +
         lora_in + tmix_core and the projections (one per sb6 / sym GEMV or
-        fused group; a dense one is the library GEMM plus its epilogue's
+        fused group, two per chunk of the batched matrix-core GEMV; a dense
+        one is the library GEMM plus its epilogue's
         elementwise kernels; r / k / v taken one by one at N > 1 add two
         staging copies each; the r/k/v group and lora_in as one launch where
         _fused_rkv_lora holds), plus emb/ln0, ln_out and the head."""
         def n(q, ep=0, staged=False):
             if isinstance(q, list):
                 return sum(n(m, ep, N > 1) for m in q)
+            chunks = self._batch_chunks(q, N)
+            if chunks is not None:   # partial sums + their reduction per chunk
+                return 2 * len(chunks) + 2 * staged
             k = 1 + (1 + 2 * (ep == 2) if q.kind == "dense" else 0)
             return k + 2 * staged
         # 2 shift_mix + tmix_core + (lora_in and the r/k/v projections, or
@@ -358,9 +363,57 @@ class X070Decoder:
     def _gemv(self, key, x, y, ep, N, s):
         self._run(self.proj[key], x, y, ep, N, s)
 
+    # Which sb6 projections of a batch take the matrix-core batched GEMV
+    # (within fp32 rounding of each row alone) instead of the one-input
+    # arithmetic run over the rows (bitwise each row alone): None = where it
+    # is faster (quant.rwkvq_sb6_gemv_batch_prefers: 8+ rows, 2^24+ weights),
+    # True = wherever it applies (2+ rows), False = never.
+    batch_mfma: Optional[bool] = None
+
+    def _batch_ws(self, nbytes: int) -> torch.Tensor:
+        ws = self._tmp.get("batch_ws")
+        if ws is None or ws.numel() < nbytes:
+            ws = self._tmp["batch_ws"] = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self.device)
+        return ws
+
+    def _batch_chunks(self, q, N: int) -> Optional[List[int]]:
+        """Row counts of the rwkv_sb6_gemv_batch launches a projection of N
+        rows takes (chunks of at most 32), or None where it keeps the
+        one-input kernels."""
+        if not isinstance(q, Proj) or q.kind != "sb6" or q.xbits != 0 or N < 2 or self.batch_mfma is False:
+            return None
+        if self.batch_mfma is None and not Q.rwkvq_sb6_gemv_batch_prefers(N, q.OUT, q.IN):
+            return None
+        nch = (N + 31) // 32
+        sizes = [N // nch + (1 if c < N % nch else 0) for c in range(nch)]
+        L = _lib.lib()
+        if not all(L.rwkv_sb6_gemv_batch_applies(n, q.OUT, q.IN, 0, q.out_per) for n in set(sizes)):
+            return None
+        return sizes
+
+    def _run_batch(self, q: Proj, x: torch.Tensor, y: torch.Tensor, ep: int, N: int, s) -> bool:
+        """rwkv_sb6_gemv_batch over chunks of at most 32 rows; False where it
+        does not apply."""
+        sizes = self._batch_chunks(q, N)
+        if sizes is None:
+            return False
+        L = _lib.lib()
+        K = q.OUT // q.out_per
+        ws = self._batch_ws(max(int(L.rwkv_sb6_gemv_batch_workspace(n, q.OUT, q.IN, q.out_per)) for n in set(sizes)))
+        x2, y2 = x.reshape(N * K, q.IN), y.reshape(N, q.OUT)
+        n0 = 0
+        for n in sizes:
+            _lib.check(L.rwkv_sb6_gemv_batch(x2[n0 * K].data_ptr(), n, *[b.data_ptr() for b in q.bufs],
+                                             y2[n0].data_ptr(), q.OUT, q.IN, 0, q.out_per, ep, ws.data_ptr(),
+                                             ws.numel(), s))
+            n0 += n
+        return True
+
     def _run(self, q: Proj, x: torch.Tensor, y: torch.Tensor, ep: int, N: int, s) -> None:
         """y = ep(x · Wᵀ): ep 0 store, 1 add into y, 2 relu² (rwkv_*_gemv_ep)."""
         L = _lib.lib()
+        if self._run_batch(q, x, y, ep, N, s):
+            return
         if q.kind == "sb6":
             if q.out_per < q.OUT:
                 if ep != 0:

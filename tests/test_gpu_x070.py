@@ -230,10 +230,19 @@ def test_decode_steps_match_oracle(tiny, decoder, N):
     c = _lib.counters()
     Lr = TINY.n_layer
     assert c["x070"] == 4 * (2 + 4 * Lr)          # ln0 + ln_out + 4 per layer
-    assert c["sb6_gemv"] == 4 * (3 * Lr + 1)      # o_proj, ffn key, ffn value, head
-    assert c["sb6_fused"] == 4 * Lr               # r/k/v
-    # batch 1: each layer's r/k/v GEMV and lora_in share one launch
-    assert decoder.launches_per_token(N) == (7 if N == 1 else 8) * Lr + 3
+    if decoder._batch_chunks(decoder.proj["head.weight"], N):   # batched matrix-core GEMV, chunks <= 32 rows
+        assert c["sb6_batch"] == 4 * ((N + 31) // 32) * (4 * Lr + 1)
+        assert c["sb6_gemv"] == 0 and c["sb6_fused"] == 0
+    else:
+        assert c["sb6_gemv"] == 4 * (3 * Lr + 1)      # o_proj, ffn key, ffn value, head
+        assert c["sb6_fused"] == 4 * Lr               # r/k/v
+    # batch 1: each layer's r/k/v GEMV and lora_in share one launch; the
+    # batched matrix-core GEMV is two launches per chunk of <= 32 rows
+    if decoder._batch_chunks(decoder.proj["head.weight"], N):
+        ch = (N + 31) // 32
+        assert decoder.launches_per_token(N) == (4 + 4 * 2 * ch) * Lr + 2 + 2 * ch
+    else:
+        assert decoder.launches_per_token(N) == (7 if N == 1 else 8) * Lr + 3
 
 
 @pytest.mark.parametrize("D,xbits,wdt", [(768, 0, np.float16), (2048, 0, np.float16), (4096, 0, np.float16),
