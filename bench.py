@@ -825,7 +825,9 @@ def profile_kernels(dev, tokens=12):
     and 12 WKV step+tail launches), 6 eager 1.5B decode tokens (97 GEMV
     launches each), the WKV-7 forward at B1 T1024 H12 fp32 (20 launches), the
     time-chunked forward at B1 T1024 H12 (5) and B1 T8192 H64 (2), the
-    checkpointed training forward + backward at B8 T4096 H32 bf16 (3 each),
+    batched GEMV of a 14336x4096 matrix x 16 rows on the matrix cores and
+    on the VALU kernel (3 each), the checkpointed training forward +
+    backward at B8 T4096 H32 bf16 (3 each),
     and a plain 256 MiB device copy whose FETCH_SIZE / WRITE_SIZE calibrate
     the counters (2 x 256 MiB of traffic)."""
     import numpy as np
@@ -862,6 +864,20 @@ def profile_kernels(dev, tokens=12):
     for _ in range(2):
         K.wkv7_sequence_forward_chunked(*x7)
     del x7
+    # batched decode GEMV, 7B-class FFN key 14336x4096 x 16 rows: matrix cores, then the VALU kernel
+    from swiftrwkv_amd import quant as Q
+    OUT, IN, N = 14336, 4096, 16
+    w = np.random.default_rng(3).standard_normal((OUT, IN), dtype=np.float32) * np.float32(0.02)
+    disk = Q.encode_sb6(w, 4, min(16, os.cpu_count() or 1))
+    qb, qs, dd, _ = Q.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"], disk["gw_dm"], None,
+                                      None, (OUT, IN))
+    qb, qs, dd = (torch.from_numpy(z).to(dev) for z in (qb, qs, dd.view(np.float16)))
+    xb = torch.randn((N, IN), device=dev)
+    for _ in range(3):
+        Q.rwkvq_sb6_gemv_batch(xb, qb, qs, dd, OUT, IN)
+    for _ in range(3):
+        Q.rwkvq_sb6_gemv(xb, qb, qs, dd, OUT, IN, 0)
+    del qb, qs, dd, xb
     B, T, H = 8, 4096, 32
     xs = syn.wkv_inputs_config0(B, T, H, seed=3)
     ins = [torch.from_numpy(z).to(dev).to(torch.bfloat16) for z in xs]
