@@ -329,14 +329,50 @@ rwkv_status rwkv_x070_rkv_lora(const float* x_rkv, const uint8_t* qblk, const ui
  * (rwkv_wkv7_step's arithmetic); out [N, H·64] = the tail
  * ((GroupNorm(y)·lnx_w + lnx_b + Σ(r·k·r_k)·v)·gate, rwkv_wkv_tail's).
  * y_rkv [N, 3·H·64] = r | k0 | v0 (the fused r/k/v GEMV output); la from
- * rwkv_x070_lora_in. */
+ * rwkv_x070_lora_in.  shift_src / shift_dst (both or neither): copies the
+ * row shift_src [N, H·64] to shift_dst, the token-shift state that
+ * rwkv_x070_rkv_lora_ln read (its LN row, for the next token). */
 rwkv_status rwkv_x070_tmix_core(const float* y_rkv, const float* la, const void* w2, const void* a2,
                                 const void* v2, const void* g2, rwkv_dtype w_dt, int64_t rw,
                                 int64_t ra, int64_t rv, int64_t rg, const float* w2_bias,
                                 const float* a2_bias, const float* v2_bias, const float* k_k,
                                 const float* k_a, const float* r_k, const float* lnx_w,
                                 const float* lnx_b, float* v_first, int layer0, float* state,
-                                float* out, int64_t N, int64_t H, float eps, void* stream);
+                                float* out, int64_t N, int64_t H, float eps, const float* shift_src,
+                                float* shift_dst, void* stream);
+
+/* ─────── one-row decode launches that form their GEMV inputs themselves ───────
+ * (no counterpart in the reference, whose step runs the layer norm, the token
+ * shift and the lerps as separate ops, X070Generation.swift :214-239,
+ * :303-308): each GEMV workgroup forms its input row — LN(x) with (ln_w,
+ * ln_b), then the lerp LN(x) + (prev − LN(x))·coef — in rwkv_x070_shift_mix's
+ * exact arithmetic, so a step built from them is bitwise the one built from
+ * shift_mix + the GEMV entries, with two launches per layer fewer.  `prev`
+ * (the token-shift state) is read, not written: LN(x) goes to `xln`, and a
+ * later launch of the same layer (rwkv_x070_tmix_core / rwkv_x070_ffn_value
+ * with shift_src = xln) stores it as the next `prev`, after every reader of
+ * the old one has run.  Batch 1, 4-bit sb6, the x070 plans (D ≤ 4096):
+ * rwkv_x070_ln_fused_applies(D, F, xbits). */
+int rwkv_x070_ln_fused_applies(int64_t D, int64_t F, int xbits);
+/* rwkv_x070_rkv_lora with its inputs formed from x [D]: coef6 [6, D] in the
+ * order r, k, v, w, a, g (rwkv_x070_shift_mix's); fp16 low-rank matrices. */
+rwkv_status rwkv_x070_rkv_lora_ln(const float* x, const float* ln_w, const float* ln_b, const float* prev,
+                                  const float* coef6, float eps, float* xln, const uint8_t* qblk,
+                                  const uint8_t* qsqm, const uint16_t* ddm, float* y_rkv, int64_t D,
+                                  int xbits, const void* wcat, rwkv_dtype w_dt, int64_t rw, int64_t ra,
+                                  int64_t rv, int64_t rg, int with_v, float* la, void* stream);
+/* The ffn key GEMV with the relu² epilogue (cmixStep :308-309): hk [F] =
+ * relu(W_key · (LN2(x) + (prev − LN2(x))·coef))², coef [D]. */
+rwkv_status rwkv_x070_ffn_key_ln(const float* x, const float* ln_w, const float* ln_b, const float* prev,
+                                 const float* coef, float eps, float* xln, const uint8_t* qblk,
+                                 const uint8_t* qsqm, const uint16_t* ddm, float* hk, int64_t F, int64_t D,
+                                 int xbits, void* stream);
+/* The ffn value GEMV with the residual add (x [D] += W_value · hk [F],
+ * :309 / :496), and with shift_src / shift_dst (both or neither) the copy
+ * shift_dst [D] ← shift_src [D]. */
+rwkv_status rwkv_x070_ffn_value(const float* hk, const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
+                                float* x, int64_t D, int64_t F, int xbits, const float* shift_src,
+                                float* shift_dst, void* stream);
 
 /* ───────────────────────── x070 parallel (prefill) pass ───────────────────────── */
 /* B rows of T tokens flattened as n = b·T + t; lengths (int32, device) [B]

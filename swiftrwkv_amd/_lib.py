@@ -99,7 +99,11 @@ _SIGS = {
     "rwkv_x070_shift_mix": (I, [P, P, P, P, P, I, P, P, L, L, F, P]),
     "rwkv_x070_lora_in": (I, [P, P, I, L, L, L, L, I, P, L, L, P]),
     "rwkv_x070_rkv_lora": (I, [P, P, P, P, P, L, L, I, L, P, P, I, L, L, L, L, I, P, P]),
-    "rwkv_x070_tmix_core": (I, [P, P, P, P, P, P, I, L, L, L, L] + [P] * 8 + [P, I, P, P, L, L, F, P]),
+    "rwkv_x070_tmix_core": (I, [P, P, P, P, P, P, I, L, L, L, L] + [P] * 8 + [P, I, P, P, L, L, F, P, P, P]),
+    "rwkv_x070_ln_fused_applies": (I, [L, L, I]),
+    "rwkv_x070_rkv_lora_ln": (I, [P] * 5 + [F, P, P, P, P, P, L, I, P, I, L, L, L, L, I, P, P]),
+    "rwkv_x070_ffn_key_ln": (I, [P] * 5 + [F, P, P, P, P, P, L, L, I, P]),
+    "rwkv_x070_ffn_value": (I, [P, P, P, P, P, L, L, I, P, P, P]),
     "rwkv_unpack6x8": (I, [P, L, P]),
     "rwkv_sb6_to_k3": (I, [P] * 6 + [L, L, P, P, P]),
     "rwkv_sym_interleave": (I, [P, P, P, L, L, P]),

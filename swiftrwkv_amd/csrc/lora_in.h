@@ -29,15 +29,16 @@ __device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn
 // `with_v` (layer 0).  A lane takes 16-byte matrix slices lane·E + 64·E·q
 // (E elements each) in ascending column order, BATCH loads in flight; the
 // result does not depend on BATCH.  The caller guards job < RT·N.
+
+// The branch of matrix row j.
+__device__ __forceinline__ int lora_branch(int j, int rw, int ra, int rv) {
+    return j < rw ? 0 : j < rw + ra ? 1 : j < rw + ra + rv ? 2 : 3;
+}
+
+// One job given its branch's input row xin (global memory or LDS).
 template <bool H16, int BATCH>
-__device__ __forceinline__ void lora_in_job(int64_t job, int lane, const float* __restrict__ xmix,
-                                            const void* __restrict__ Wcat, float* __restrict__ la, int D, int rw,
-                                            int ra, int rv, int rg, int with_v) {
-    const int RT = rw + ra + rv + rg;
-    const int j = (int)(job % RT), n = (int)(job / RT);
-    const int br = j < rw ? 0 : j < rw + ra ? 1 : j < rw + ra + rv ? 2 : 3;
-    if (br == 2 && !with_v) return;
-    const float* xin = xmix + ((int64_t)n * 4 + br) * D;
+__device__ __forceinline__ void lora_in_row(int j, int n, int lane, const float* xin, const void* __restrict__ Wcat,
+                                            float* __restrict__ la, int D, int RT, int br) {
     float acc = 0.0f;
     constexpr int E = H16 ? 8 : 4;   // matrix elements per 16-byte load
     for (int c0 = 0; c0 < D; c0 += 64 * E * BATCH) {
@@ -80,6 +81,17 @@ __device__ __forceinline__ void lora_in_job(int64_t job, int lane, const float* 
     if (br == 0) t = tanhf(t);
     else if (br == 3) t = sigmoidf_(t);
     if (lane == 0) la[(int64_t)n * RT + j] = t;
+}
+
+template <bool H16, int BATCH>
+__device__ __forceinline__ void lora_in_job(int64_t job, int lane, const float* __restrict__ xmix,
+                                            const void* __restrict__ Wcat, float* __restrict__ la, int D, int rw,
+                                            int ra, int rv, int rg, int with_v) {
+    const int RT = rw + ra + rv + rg;
+    const int j = (int)(job % RT), n = (int)(job / RT);
+    const int br = lora_branch(j, rw, ra, rv);
+    if (br == 2 && !with_v) return;
+    lora_in_row<H16, BATCH>(j, n, lane, xmix + ((int64_t)n * 4 + br) * D, Wcat, la, D, RT, br);
 }
 
 }  // namespace rwkv_x070

@@ -39,6 +39,7 @@
 
 #include "launch.h"
 #include "lora_in.h"
+#include "x070_row.h"
 
 namespace {
 
@@ -363,6 +364,26 @@ struct GemvGeom {
     int one_k; // fused groups: every row of a workgroup reads the same input row, staged alone
     int ep;    // epilogue: 0 store, 1 add to y (residual stream), 2 relu² of the result
     int xfirst;   // single input: inputs loaded before the weights (gemv_kernel<..., XF = true>)
+    // with the store of output row `row` (one input, OUT = the copied width):
+    // cp_dst[row] ← cp_src[row] (a state row handed on after every reader of
+    // the old one has run); null: none
+    const float* cp_src;
+    float* cp_dst;
+};
+
+// A GEMV input row formed in the launch: LN(x) with (w, b), then the token
+// shift lerp with the previous row `prev` and coefficient row `coef`
+// (X070Generation.swift tmixStep :214-239 / cmixStep :303-308), in the row
+// kernels' exact arithmetic (x070_row.h).  `xln` (nullable) receives LN(x)
+// from one workgroup, for a later launch to store as the next `prev`.
+struct LnMix {
+    const float* x;
+    const float* w;
+    const float* b;
+    const float* prev;
+    const float* coef;   // coefficient rows; a fused group's matrix k uses row k
+    float* xln;
+    float eps;
 };
 
 // y[i] ← t, res + t (res = y[i], read before the product) or relu(t)², the
@@ -392,9 +413,10 @@ __host__ __device__ constexpr int xl_stride(int IN) { return IN + (IN >> 3); }
 // weights stay in registers across input tiles.
 // The body of workgroup `bx` (gemv_kernel runs workgroup blockIdx.x; a fused
 // launch may run it beside other work).
-template <class F, int RL, int KU, int NT, bool XL, bool MULTI, bool XF>
+template <class F, int RL, int KU, int NT, bool XL, bool MULTI, bool XF, int LNC = 0>
 __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, int N, typename F::Ptr P,
-                                          float* __restrict__ y, int OUT, int IN, int out_per, GemvGeom geo) {
+                                          float* __restrict__ y, int OUT, int IN, int out_per, GemvGeom geo,
+                                          const LnMix& lm = LnMix{}) {
     extern __shared__ float lds[];
     const int NU = IN >> 5;
     const int NK = OUT / out_per;
@@ -502,8 +524,10 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
             for (int rr = 0; rr < RL; ++rr) {
                 const float t = group_sum(acc[nn][rr], geo.G);
                 const int row = row0 + rr;
-                if (g == 0 && row < OUT && n0 + nn < N)
+                if (g == 0 && row < OUT && n0 + nn < N) {
                     store_out(y, (int64_t)(n0 + nn) * OUT + row, t, geo.ep, res[nn][rr]);
+                    if (geo.cp_dst) geo.cp_dst[row] = geo.cp_src[row];
+                }
             }
     };
 
@@ -543,7 +567,48 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
                 __syncthreads();
             }
         };
-        if constexpr (XF) {
+        if constexpr (LNC > 0) {
+            // The input row formed here: LN(x) and its token-shift lerp.  All
+            // the row loads first (the statistics chunks of threads < T as
+            // the row kernel assigns them, then this thread's LNC staging
+            // chunks e = tid + i·nthr), then the weights; one input row
+            // (rows == 1), IN ≤ 4·LNC·nthr and IN ≤ 4096 (checked by the host).
+            using namespace rwkv_x070;
+            __shared__ float red[32];
+            const int IN4 = IN >> 2;
+            int S_, T, PS;
+            row_geometry(IN, S_, T, PS);
+            const bool on = (int)threadIdx.x < T;
+            float4 sv[4], xo[LNC], pv[LNC], cv[LNC], wv[LNC], bv[LNC];
+            const float* coef = lm.coef + (int64_t)kwg * IN;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) sv[p] = *reinterpret_cast<const float4*>(lm.x + 4 * min((int)threadIdx.x + T * p, IN4 - 1));
+#pragma unroll
+            for (int i = 0; i < LNC; ++i) {
+                const int e = min((int)threadIdx.x + i * nthr, IN4 - 1);
+                xo[i] = *reinterpret_cast<const float4*>(lm.x + 4 * e);
+                pv[i] = *reinterpret_cast<const float4*>(lm.prev + 4 * e);
+                cv[i] = *reinterpret_cast<const float4*>(coef + 4 * e);
+                wv[i] = *reinterpret_cast<const float4*>(lm.w + 4 * e);
+                bv[i] = *reinterpret_cast<const float4*>(lm.b + 4 * e);
+            }
+            load_pass(0, W);
+            load_res(res, 0);
+            const float2 md = row_stats<4>(sv, PS, on, IN, lm.eps, red);
+            // chunks past the row repeat the last one (the same values to the
+            // same addresses): no branch, so the row loads stay ahead of the
+            // weight loads instead of being sunk behind them
+#pragma unroll
+            for (int i = 0; i < LNC; ++i) {
+                const int e = min((int)threadIdx.x + i * nthr, IN4 - 1);
+                const float4 xl = ln_apply(xo[i], md, wv[i], bv[i]);
+                *reinterpret_cast<float4*>(lds + e * 4 + (e >> 3) * 4) = shift_lerp(xl, shift_delta(pv[i], xl), cv[i]);
+                if (bx == 0 && lm.xln) *reinterpret_cast<float4*>(lm.xln + 4 * e) = xl;
+            }
+            __syncthreads();
+            row_sums();
+            __builtin_amdgcn_sched_barrier(0);
+        } else if constexpr (XF) {
             // Inputs first: the first XPRE float4 of each thread's share of
             // the staged rows are loaded before the weights.  Loads complete
             // in issue order, so the LDS stores then wait for these inputs,
@@ -668,6 +733,63 @@ __global__ __launch_bounds__(1024) void rkv_lora_kernel(const float* __restrict_
         if (job >= rw + ra + rv + rg) return;   // uniform per wave
         rwkv_x070::lora_in_job<true, 4>(job, threadIdx.x & 63, xmix, wcat, la, IN, rw, ra, rv, rg, with_v);
     }
+}
+
+// rkv_lora_kernel forming its inputs itself (LnMix: ln1, the token shift
+// and its lerps) instead of reading the shift_mix launch's rows: a GEMV
+// workgroup forms the r, k or v row of its matrix, a low-rank workgroup (its
+// jobs are rows of one branch: ranks are multiples of 8, WPB divides 8) the
+// w, a, v or g row in LDS.  Bitwise the shift_mix + rkv_lora pair.
+template <int KU, int LNC>
+__global__ __launch_bounds__(1024) void rkv_lora_ln_kernel(typename Sb6Fmt<0>::Ptr P, float* __restrict__ y, int OUT,
+                                                           int IN, int out_per, GemvGeom geo, int lb, LnMix lm,
+                                                           const void* __restrict__ wcat, float* __restrict__ la,
+                                                           int rw, int ra, int rv, int rg, int with_v) {
+    if ((int)blockIdx.x >= lb) {   // uniform per workgroup
+        gemv_body<Sb6Fmt<0>, 1, KU, 1, true, false, true, LNC>((int)blockIdx.x - lb, lm.x, 1, P, y, OUT, IN, out_per,
+                                                               geo, lm);
+        return;
+    }
+    using namespace rwkv_x070;
+    extern __shared__ float lds[];
+    __shared__ float red[32];
+    const int RT = rw + ra + rv + rg, nthr = 64 * geo.WPB, IN4 = IN >> 2;
+    const int job = (int)blockIdx.x * geo.WPB + (threadIdx.x >> 6);
+    const int br = lora_branch(min((int)blockIdx.x * geo.WPB, RT - 1), rw, ra, rv);   // uniform
+    const float* coef = lm.coef + (int64_t)(br == 0 ? 3 : br == 1 ? 4 : br == 2 ? 2 : 5) * IN;
+    int S_, T, PS;
+    row_geometry(IN, S_, T, PS);
+    const bool on = (int)threadIdx.x < T;
+    float4 sv[4], xo[LNC], pv[LNC], cv[LNC], wv[LNC], bv[LNC];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) sv[p] = *reinterpret_cast<const float4*>(lm.x + 4 * min((int)threadIdx.x + T * p, IN4 - 1));
+#pragma unroll
+    for (int i = 0; i < LNC; ++i) {
+        const int e = min((int)threadIdx.x + i * nthr, IN4 - 1);
+        xo[i] = *reinterpret_cast<const float4*>(lm.x + 4 * e);
+        pv[i] = *reinterpret_cast<const float4*>(lm.prev + 4 * e);
+        cv[i] = *reinterpret_cast<const float4*>(coef + 4 * e);
+        wv[i] = *reinterpret_cast<const float4*>(lm.w + 4 * e);
+        bv[i] = *reinterpret_cast<const float4*>(lm.b + 4 * e);
+    }
+    const float2 md = row_stats<4>(sv, PS, on, IN, lm.eps, red);
+#pragma unroll
+    for (int i = 0; i < LNC; ++i) {   // past the row: the last chunk again, no branch
+        const int e = min((int)threadIdx.x + i * nthr, IN4 - 1);
+        const float4 xl = ln_apply(xo[i], md, wv[i], bv[i]);
+        reinterpret_cast<float4*>(lds)[e] = shift_lerp(xl, shift_delta(pv[i], xl), cv[i]);
+    }
+    __syncthreads();
+    if (job >= RT || (br == 2 && !with_v)) return;   // uniform per wave
+    lora_in_row<true, 4>(job, 0, threadIdx.x & 63, lds, wcat, la, IN, RT, br);
+}
+
+// The ffn key GEMV (relu² epilogue) forming its input itself (LnMix: ln2,
+// the token shift and its lerp); bitwise the shift_mix + GEMV pair.
+template <int KU, int LNC>
+__global__ __launch_bounds__(1024) void gemv_ln_kernel(typename Sb6Fmt<0>::Ptr P, float* __restrict__ y, int OUT,
+                                                       int IN, GemvGeom geo, LnMix lm) {
+    gemv_body<Sb6Fmt<0>, 1, KU, 1, true, false, true, LNC>((int)blockIdx.x, lm.x, 1, P, y, OUT, IN, OUT, geo, lm);
 }
 
 // Batches (N ≥ 2 inputs): NT inputs share one pass over the weights.  The
@@ -1289,6 +1411,139 @@ rwkv_status rwkv_x070_rkv_lora(const float* x_rkv, const uint8_t* qblk, const ui
     const rwkv_status s = rwkv_sb6_gemv_fused(x_rkv, 1, qblk, qsqm, ddm, y_rkv, OUT, IN, xbits, out_per, stream);
     if (s != RWKV_OK) return s;
     return rwkv_x070_lora_in(xmix, wcat, w_dt, rw, ra, rv, rg, with_v, la, 1, IN, stream);
+}
+
+}  // extern "C"
+
+namespace {
+// The plan of a GEMV that forms its input row in the launch: one input, one
+// pass of 3 or 4 units per lane, one input row per workgroup, and the row
+// (IN ≤ 4096, IN % 256 == 0) within four float4 per thread.
+bool ln_plan(int64_t OUT, int64_t IN, int64_t out_per, GemvPlan& pl) {
+    if (IN < 256 || IN % 256 || IN > 4096 || out_per < 1 || OUT % out_per) return false;
+    pl = plan_gemv(OUT, IN / 32, out_per, 1, OUT / out_per, true, false);
+    return pl.NT == 1 && pl.xl && pl.geo.NP == 1 && pl.RL == 1 && (pl.KU == 3 || pl.KU == 4) &&
+           (OUT == out_per || pl.geo.one_k) && IN <= 16 * 64 * pl.geo.WPB;
+}
+// float4 chunks of the row per thread (1, 2 or 4)
+int ln_chunks(int64_t IN, const GemvPlan& pl) {
+    const int64_t c = (IN / 4 + 64 * pl.geo.WPB - 1) / (64 * pl.geo.WPB);
+    return c <= 1 ? 1 : c <= 2 ? 2 : 4;
+}
+// the value GEMV with the residual add and the state copy
+bool value_plan(int64_t OUT, int64_t IN, GemvPlan& pl) {
+    if (IN < 256 || IN % 256) return false;
+    pl = plan_gemv(OUT, IN / 32, OUT, 1, 1, true, false);
+    return pl.NT == 1;
+}
+}  // namespace
+
+extern "C" {
+
+int rwkv_x070_ln_fused_applies(int64_t D, int64_t F, int xbits) {
+    GemvPlan a, b, c;
+    return xbits == 0 && ln_plan(3 * D, D, D, a) && ln_plan(F, D, F, b) && value_plan(D, F, c) ? 1 : 0;
+}
+
+rwkv_status rwkv_x070_rkv_lora_ln(const float* x, const float* ln_w, const float* ln_b, const float* prev,
+                                  const float* coef6, float eps, float* xln, const uint8_t* qblk, const uint8_t* qsqm,
+                                  const uint16_t* ddm, float* y_rkv, int64_t D, int xbits, const void* wcat,
+                                  rwkv_dtype w_dt, int64_t rw, int64_t ra, int64_t rv, int64_t rg, int with_v,
+                                  float* la, void* stream) {
+    RWKV_REQUIRE(x && ln_w && ln_b && prev && coef6 && xln && wcat && la, RWKV_E_NULL, "x070_rkv_lora_ln: null buffer");
+    RWKV_REQUIRE(w_dt == RWKV_F16, RWKV_E_DTYPE, "x070_rkv_lora_ln: low-rank matrices must be f16 (dtype %d)",
+                 (int)w_dt);
+    RWKV_REQUIRE(rw >= 8 && ra >= 8 && rv >= 8 && rg >= 8 && rw % 8 == 0 && ra % 8 == 0 && rv % 8 == 0 && rg % 8 == 0 &&
+                     rw + ra + rv + rg <= 8192,
+                 RWKV_E_SHAPE, "x070_rkv_lora_ln: ranks %lld/%lld/%lld/%lld (multiples of 8)", (long long)rw,
+                 (long long)ra, (long long)rv, (long long)rg);
+    const rwkv_status a = sb6_gemv_args("x070_rkv_lora_ln", x, 1, qblk, qsqm, ddm, y_rkv, 3 * D, D, xbits, D, 0);
+    if (a != RWKV_OK) return a;
+    GemvPlan pl;
+    RWKV_REQUIRE(xbits == 0 && ln_plan(3 * D, D, D, pl), RWKV_E_UNSUPPORTED,
+                 "x070_rkv_lora_ln: D=%lld xbits=%d not taken (rwkv_x070_ln_fused_applies)", (long long)D, xbits);
+    pl.geo.ep = 0;
+    const Sb6Fmt<0>::Ptr P{(const uint32_t*)qblk, (const uint16_t*)qsqm, (const uint32_t*)ddm};
+    const LnMix lm{x, ln_w, ln_b, prev, coef6, xln, eps};
+    const int RT = (int)(rw + ra + rv + rg);
+    const int lb = (RT + pl.geo.WPB - 1) / pl.geo.WPB;
+    const dim3 grid(pl.blocks + (unsigned)lb), block(64 * pl.geo.WPB);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int ch = ln_chunks(D, pl);
+#define RWKV_RLL(KUV, CHV)                                                                                         \
+    if (pl.KU == KUV && ch == CHV)                                                                                 \
+    rwkv::launch_lds(rkv_lora_ln_kernel<KUV, CHV>, grid, block, pl.lds, st, P, y_rkv, (int)(3 * D), (int)D, (int)D, \
+                     pl.geo, lb, lm, wcat, la, (int)rw, (int)ra, (int)rv, (int)rg, with_v)
+    RWKV_RLL(4, 1);
+    RWKV_RLL(4, 2);
+    RWKV_RLL(4, 4);
+    RWKV_RLL(3, 1);
+    RWKV_RLL(3, 2);
+    RWKV_RLL(3, 4);
+#undef RWKV_RLL
+    const rwkv_status s = launch_status("x070_rkv_lora_ln");
+    if (s == RWKV_OK) {
+        rwkv::counters().sb6_fused++;
+        rwkv::counters().x070++;
+    }
+    return s;
+}
+
+rwkv_status rwkv_x070_ffn_key_ln(const float* x, const float* ln_w, const float* ln_b, const float* prev,
+                                 const float* coef, float eps, float* xln, const uint8_t* qblk, const uint8_t* qsqm,
+                                 const uint16_t* ddm, float* hk, int64_t F, int64_t D, int xbits, void* stream) {
+    RWKV_REQUIRE(x && ln_w && ln_b && prev && coef && xln, RWKV_E_NULL, "x070_ffn_key_ln: null buffer");
+    const rwkv_status a = sb6_gemv_args("x070_ffn_key_ln", x, 1, qblk, qsqm, ddm, hk, F, D, xbits, F, 2);
+    if (a != RWKV_OK) return a;
+    GemvPlan pl;
+    RWKV_REQUIRE(xbits == 0 && ln_plan(F, D, F, pl), RWKV_E_UNSUPPORTED,
+                 "x070_ffn_key_ln: %lldx%lld xbits=%d not taken (rwkv_x070_ln_fused_applies)", (long long)F,
+                 (long long)D, xbits);
+    pl.geo.ep = 2;
+    const Sb6Fmt<0>::Ptr P{(const uint32_t*)qblk, (const uint16_t*)qsqm, (const uint32_t*)ddm};
+    const LnMix lm{x, ln_w, ln_b, prev, coef, xln, eps};
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid(pl.blocks), block(64 * pl.geo.WPB);
+    const int ch = ln_chunks(D, pl);
+#define RWKV_KL(KUV, CHV) \
+    if (pl.KU == KUV && ch == CHV) rwkv::launch_lds(gemv_ln_kernel<KUV, CHV>, grid, block, pl.lds, st, P, hk, (int)F, (int)D, pl.geo, lm)
+    RWKV_KL(4, 1);
+    RWKV_KL(4, 2);
+    RWKV_KL(4, 4);
+    RWKV_KL(3, 1);
+    RWKV_KL(3, 2);
+    RWKV_KL(3, 4);
+#undef RWKV_KL
+    const rwkv_status s = launch_status("x070_ffn_key_ln");
+    if (s == RWKV_OK) {
+        rwkv::counters().sb6_gemv++;
+        rwkv::counters().x070++;
+    }
+    return s;
+}
+
+rwkv_status rwkv_x070_ffn_value(const float* hk, const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm,
+                                float* x, int64_t D, int64_t F, int xbits, const float* shift_src, float* shift_dst,
+                                void* stream) {
+    RWKV_REQUIRE((shift_src == nullptr) == (shift_dst == nullptr), RWKV_E_NULL,
+                 "x070_ffn_value: shift_src and shift_dst are both set or both null");
+    const rwkv_status a = sb6_gemv_args("x070_ffn_value", hk, 1, qblk, qsqm, ddm, x, D, F, xbits, D, 1);
+    if (a != RWKV_OK) return a;
+    GemvPlan pl;
+    RWKV_REQUIRE(xbits == 0 && value_plan(D, F, pl), RWKV_E_UNSUPPORTED, "x070_ffn_value: %lldx%lld xbits=%d not taken",
+                 (long long)D, (long long)F, xbits);
+    pl.geo.ep = 1;
+    pl.geo.cp_src = shift_src;
+    pl.geo.cp_dst = shift_dst;
+    const Sb6Fmt<0>::Ptr P{(const uint32_t*)qblk, (const uint16_t*)qsqm, (const uint32_t*)ddm};
+    RWKV_REQUIRE(launch_gemv<Sb6Fmt<0>>(pl, reinterpret_cast<hipStream_t>(stream), hk, 1, P, x, (int)D, (int)F, (int)D),
+                 RWKV_E_UNSUPPORTED, "x070_ffn_value: no kernel variant for %lldx%lld", (long long)D, (long long)F);
+    const rwkv_status s = launch_status("x070_ffn_value");
+    if (s == RWKV_OK) {
+        rwkv::counters().sb6_gemv++;
+        rwkv::counters().x070++;
+    }
+    return s;
 }
 
 int rwkv_sym_gemv_applies(int64_t OUT, int64_t IN, int bits, int64_t rows) {

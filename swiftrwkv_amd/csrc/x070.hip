@@ -17,6 +17,7 @@
 #include "launch.h"
 #include "lora_in.h"
 #include "wkv7_step.h"
+#include "x070_row.h"
 
 namespace {
 using namespace rwkv_wkv;
@@ -24,21 +25,6 @@ using namespace rwkv_x070;
 
 constexpr int kRowMax = 8192;   // widest row of the row kernels
 
-
-// Sum over the workgroup: per-wave butterfly, then the wave totals in wave
-// order; every thread gets the same value.  `red` (16 floats) is used once
-// per kernel, so no barrier is needed before it is written.
-__device__ __forceinline__ float block_total(float v, float* red) {
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    v = wave_total(v);
-    if ((threadIdx.x & 63) == 0) red[wave] = v;
-    __syncthreads();
-    float t = red[0];
-    for (int i = 1; i < nw; ++i) t += red[i];
-    return t;
-}
-
-__device__ __forceinline__ float sum4(float4 a) { return (a.x + a.y) + (a.z + a.w); }
 
 // v + (v of the DPP partner lane); CTRL quad_perm / row_half_mirror.
 template <int CTRL>
@@ -54,33 +40,7 @@ __device__ __forceinline__ float sum8_lanes(float v) {
     return dpp_add<0x141>(v);   // row_half_mirror
 }
 
-// Row kernels: a row of D is split over S workgroups of T threads (S = D/1024
-// with T = 256 when 1024 divides D, else S = 1 with T = D/4); thread t of
-// slice s writes the float4 chunk s·T + t.  Every workgroup forms the row's
-// statistics itself from the whole row (PS = D/(4T) chunks per thread, the
-// same order in every slice), with all of a thread's loads issued first.
-//
-// layerNorm_ (X070Generation.swift:511-514): mean, then the mean of squared
-// deviations; the row's (mean, sqrt(var + eps)).
-template <int PS>
-__device__ __forceinline__ float2 row_stats(const float4 (&v)[PS], int D, float eps, float* red) {
-    float s = 0.0f;
-#pragma unroll
-    for (int p = 0; p < PS; ++p) s += sum4(v[p]);
-    const float mean = block_total(s, red) / (float)D;   // red[0..15], then red[16..31]
-    float q = 0.0f;
-#pragma unroll
-    for (int p = 0; p < PS; ++p) {
-        const float4 d = make_float4(v[p].x - mean, v[p].y - mean, v[p].z - mean, v[p].w - mean);
-        q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
-    }
-    return make_float2(mean, sqrtf(block_total(q, red + 16) / (float)D + eps));
-}
-
-__device__ __forceinline__ float4 ln_apply(float4 x, float2 md, float4 w, float4 b) {
-    return make_float4((x.x - md.x) / md.y * w.x + b.x, (x.y - md.x) / md.y * w.y + b.y,
-                       (x.z - md.x) / md.y * w.z + b.z, (x.w - md.x) / md.y * w.w + b.w);
-}
+// Row kernels (row_geometry): all of a thread's loads are issued first.
 
 __device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ float4 load4(const __half* p) {
@@ -111,7 +71,7 @@ __global__ __launch_bounds__(1024) void layer_norm_kernel(const T* __restrict__ 
 #pragma unroll
     for (int p = 0; p < PS; ++p) v[p] = load4(row + 4 * (threadIdx.x + T4 * p));
     const float4 xo = load4(row + c), wv = load4(w + c), bv = load4(b + c);
-    const float2 md = row_stats<PS>(v, D, eps, red);
+    const float2 md = row_stats<PS>(v, PS, true, D, eps, red);
     const float nan = __builtin_nanf("");
     *reinterpret_cast<float4*>(y + (int64_t)n * D + c) = bad ? make_float4(nan, nan, nan, nan) : ln_apply(xo, md, wv, bv);
 }
@@ -137,15 +97,14 @@ __global__ __launch_bounds__(1024) void shift_mix_kernel(const float* __restrict
     const float4 pv = load4(prev + (int64_t)n * D + c);
 #pragma unroll
     for (int k = 0; k < NC; ++k) cv[k] = load4(coef + (int64_t)k * D + c);
-    const float2 md = row_stats<PS>(v, D, eps, red);
+    const float2 md = row_stats<PS>(v, PS, true, D, eps, red);
     const float4 xl = ln_apply(xo, md, wv, bv);
-    const float4 xx = make_float4(pv.x - xl.x, pv.y - xl.y, pv.z - xl.z, pv.w - xl.w);
+    const float4 xx = shift_delta(pv, xl);
     *reinterpret_cast<float4*>(prev + (int64_t)n * D + c) = xl;
     constexpr int N0 = NC < 3 ? NC : 3;
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
-        const float4 q = cv[k];
-        const float4 m = make_float4(xl.x + xx.x * q.x, xl.y + xx.y * q.y, xl.z + xx.z * q.z, xl.w + xx.w * q.w);
+        const float4 m = shift_lerp(xl, xx, cv[k]);
         if (k < N0) *reinterpret_cast<float4*>(out0 + ((int64_t)n * N0 + k) * D + c) = m;
         // low-rank inputs: w, a, v, g ← coefficients 3, 4, 2, 5
         const int slot = k == 3 ? 0 : k == 4 ? 1 : k == 2 ? 2 : k == 5 ? 3 : -1;
@@ -153,17 +112,7 @@ __global__ __launch_bounds__(1024) void shift_mix_kernel(const float* __restrict
     }
 }
 
-// Slices S, threads T and statistics chunks PS of a row kernel for width D
-// (D % 256 == 0; D ≤ 4096 or 1024 | D ≤ 8192).
-inline void row_geometry(int64_t D, int& S, int& T, int& PS) {
-    if (D % 1024 == 0) {
-        T = 256;
-        S = PS = (int)(D / 1024);
-    } else {
-        T = (int)(D / 4);
-        S = PS = 1;
-    }
-}
+// Widths the row kernels take (D % 256 == 0; D ≤ 4096 or 1024 | D ≤ 8192).
 inline bool row_width_ok(int64_t D) { return D >= 256 && D % 256 == 0 && D <= kRowMax && (D <= 4096 || D % 1024 == 0); }
 
 // ── low-rank first layers (tmixStep :256-276, the inner `lin` of each branch) ──
@@ -194,6 +143,8 @@ struct CoreArgs {
     float* v_first;   // [N, D]
     float* state;     // [N, H, 64, 64]
     float* out;       // [N, D]
+    const float* shift_src;   // nullable: shift_dst[n, :] ← shift_src[n, :] (the next token-shift row)
+    float* shift_dst;
     int H, layer0;
     float eps;
 };
@@ -370,6 +321,7 @@ __global__ __launch_bounds__(R4 ? 1024 : 256) void tmix_core_kernel(CoreArgs A) 
         const float v = A.layer0 ? v0l : v0l + (vfl - v0l) * br[2 * D + l];
         if (A.layer0) A.v_first[vf0 + l] = v;
         A.out[(int64_t)n * Dm + he] = head_tail(ys[l], r, k, v, rkc, lnwc, lnbc, br[3 * D + l], A.eps);
+        if (A.shift_dst) A.shift_dst[vf0 + l] = A.shift_src[vf0 + l];
     }
 }
 
@@ -482,10 +434,12 @@ rwkv_status rwkv_x070_tmix_core(const float* y_rkv, const float* la, const void*
                                 const float* w2_bias, const float* a2_bias, const float* v2_bias, const float* k_k,
                                 const float* k_a, const float* r_k, const float* lnx_w, const float* lnx_b,
                                 float* v_first, int layer0, float* state, float* out, int64_t N, int64_t H, float eps,
-                                void* stream) {
+                                const float* shift_src, float* shift_dst, void* stream) {
     RWKV_REQUIRE(y_rkv && la && w2 && a2 && g2 && w2_bias && a2_bias && k_k && k_a && r_k && lnx_w && lnx_b &&
                      v_first && state && out && (layer0 || (v2 && v2_bias)),
                  RWKV_E_NULL, "x070_tmix_core: null buffer");
+    RWKV_REQUIRE((shift_src == nullptr) == (shift_dst == nullptr), RWKV_E_NULL,
+                 "x070_tmix_core: shift_src and shift_dst are both set or both null");
     RWKV_REQUIRE(w_dt == RWKV_F16 || w_dt == RWKV_F32, RWKV_E_DTYPE, "x070_tmix_core: matrix dtype %d not f16/f32",
                  (int)w_dt);
     RWKV_REQUIRE(rw >= 8 && ra >= 8 && rv >= 8 && rg >= 8 && rw % 8 == 0 && ra % 8 == 0 && rv % 8 == 0 && rg % 8 == 0 &&
@@ -502,6 +456,7 @@ rwkv_status rwkv_x070_tmix_core(const float* y_rkv, const float* la, const void*
     A.bias[0] = w2_bias; A.bias[1] = a2_bias; A.bias[2] = v2_bias;
     A.k_k = k_k; A.k_a = k_a; A.r_k = r_k; A.lnw = lnx_w; A.lnb = lnx_b;
     A.v_first = v_first; A.state = state; A.out = out;
+    A.shift_src = shift_src; A.shift_dst = shift_dst;
     A.H = (int)H; A.layer0 = layer0 ? 1 : 0; A.eps = eps;
     const size_t lds = (size_t)(rw + ra + rv + rg + 5 * D) * 4;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);

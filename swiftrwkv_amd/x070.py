@@ -14,7 +14,11 @@ Per layer and token, eight launches through the C ABI:
   rwkv_sb6_gemv_ep     (ffn value + residual add, :309 / :496)
 plus rwkv_layer_norm for emb + ln0 (:489-490) and ln_out, and the head GEMV.
 At batch 1 (4-bit sb6 r/k/v, fp16 low-rank matrices) the r/k/v GEMV and
-lora_in are one launch, rwkv_x070_rkv_lora (seven per layer).
+lora_in are one launch, rwkv_x070_rkv_lora (seven per layer); with 4-bit
+ffn key / value too, the r/k/v + low-rank and the ffn key launches form
+their input rows themselves (rwkv_x070_rkv_lora_ln, rwkv_x070_ffn_key_ln;
+the tmix core and rwkv_x070_ffn_value store the next token-shift rows):
+five per layer, bitwise the same step.
 Activations are fp32; low-rank matrices keep their dtype (fp16: the `lin`
 narrowing of :248-253).  There is no CPU fallback: a missing library raises.
 """
@@ -137,6 +141,10 @@ class X070Decoder:
         # one launch for a layer's r/k/v GEMV and low-rank first layers where
         # _fused_rkv_lora allows (bitwise equal to the two launches)
         self.fuse_rkv_lora = True
+        # batch 1: the r/k/v + low-rank and ffn key launches form their input
+        # rows (layer norm, token shift, lerps) themselves, two launches per
+        # layer fewer (bitwise the shift_mix path), where _ln_fused allows
+        self.fuse_ln = True
         dev = self.device
 
         def tens(a) -> torch.Tensor:
@@ -262,7 +270,7 @@ class X070Decoder:
             z = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)
             self._bufs = {"N": N, "x": z(N, D), "xrkv": z(N, 3, D), "xmix": z(N, 4, D), "y_rkv": z(N, 3 * D),
                           "la": z(N, sum(self.ranks)), "tout": z(N, D), "xk": z(N, D), "hk": z(N, self.F),
-                          "xo": z(N, D), "xl": z(D), "logits": z(N, self.V)}
+                          "xo": z(N, D), "xl": z(D), "xl1": z(D), "xl2": z(D), "logits": z(N, self.V)}
         return self._bufs
 
     def launch(self, ids: torch.Tensor, state: RWKVState, stream: Optional[int] = None) -> torch.Tensor:
@@ -283,6 +291,10 @@ class X070Decoder:
         emb_dt = _lib.F16 if self.emb.dtype == torch.float16 else _lib.F32
         _lib.check(L.rwkv_layer_norm(p(self.emb), emb_dt, p(ids), int(self.emb.shape[0]), p(self.ln0[0]),
                                      p(self.ln0[1]), p(x), N, D, LN_EPS, s))
+        if self._ln_fused(N):
+            for l, lay in enumerate(self.layers):
+                self._layer_ln_fused(l, lay, state, bf, s)
+            return self._head(bf, N, s)
         for l, lay in enumerate(self.layers):
             _lib.check(L.rwkv_x070_shift_mix(p(x), p(lay["ln1"][0]), p(lay["ln1"][1]), p(state.tmix_prev[l]),
                                              p(lay["coef6"]), 6, p(bf["xrkv"]), p(bf["xmix"]), N, D, LN_EPS, s))
@@ -295,10 +307,51 @@ class X070Decoder:
                                              p(lay["ck"]), 1, p(bf["xk"]), None, N, D, LN_EPS, s))
             self._gemv(f"blocks.{l}.ffn.key.weight", bf["xk"], bf["hk"], 2, N, s)
             self._gemv(f"blocks.{l}.ffn.value.weight", bf["hk"], x, 1, N, s)
-        _lib.check(L.rwkv_layer_norm(p(x), _lib.F32, None, 0, p(self.ln_out[0]), p(self.ln_out[1]), p(bf["xo"]),
-                                     N, D, LN_EPS, s))
+        return self._head(bf, N, s)
+
+    def _head(self, bf, N, s) -> torch.Tensor:
+        L, p = _lib.lib(), (lambda t: t.data_ptr())
+        _lib.check(L.rwkv_layer_norm(p(bf["x"]), _lib.F32, None, 0, p(self.ln_out[0]), p(self.ln_out[1]),
+                                     p(bf["xo"]), N, self.D, LN_EPS, s))
         self._gemv("head.weight", bf["xo"], bf["logits"], 0, N, s)
         return bf["logits"]
+
+    def _ln_fused(self, N) -> bool:
+        """Batch 1 with every layer's r/k/v group and low-rank first layers
+        fused, 4-bit sb6 ffn key / value, and the x070 plans
+        (rwkv_x070_ln_fused_applies)."""
+        if not (self.fuse_ln and N == 1):
+            return False
+        for l in range(self.L):
+            kv = [self.proj[f"blocks.{l}.ffn.{k}.weight"] for k in ("key", "value")]
+            if not (self._fused_rkv_lora(l, N) and all(isinstance(q, Proj) and q.kind == "sb6" and q.xbits == 0
+                                                       for q in kv)):
+                return False
+        return bool(_lib.lib().rwkv_x070_ln_fused_applies(self.D, self.F, 0))
+
+    def _layer_ln_fused(self, l, lay, state, bf, s):
+        """One layer of the batch-1 step in five launches: r/k/v + low-rank
+        (forming the ln1 / shift rows; ln1 row → xl1), the tmix core (which
+        stores xl1 as the next tmix shift row), o_proj + residual, ffn key
+        (forming the ln2 / shift row; ln2 row → xl2), ffn value + residual
+        (which stores xl2 as the next cmix shift row)."""
+        L, p = _lib.lib(), (lambda t: t.data_ptr())
+        q = self.proj[f"blocks.{l}.att.rkv"]
+        rw, ra, rv, rg = self.ranks
+        x = bf["x"]
+        _lib.check(L.rwkv_x070_rkv_lora_ln(p(x), p(lay["ln1"][0]), p(lay["ln1"][1]), p(state.tmix_prev[l]),
+                                           p(lay["coef6"]), LN_EPS, p(bf["xl1"]), p(q.bufs[0]), p(q.bufs[1]),
+                                           p(q.bufs[2]), p(bf["y_rkv"]), self.D, 0, p(lay["wcat"]), _lib.F16,
+                                           rw, ra, rv, rg, int(l > 0), p(bf["la"]), s))
+        self._tmix_core(l, lay, state, bf, 1, s, shift=(bf["xl1"], state.tmix_prev[l]))
+        self._gemv(f"blocks.{l}.att.output.weight", bf["tout"], x, 1, 1, s)
+        k = self.proj[f"blocks.{l}.ffn.key.weight"]
+        _lib.check(L.rwkv_x070_ffn_key_ln(p(x), p(lay["ln2"][0]), p(lay["ln2"][1]), p(state.cmix_prev[l]),
+                                          p(lay["ck"]), LN_EPS, p(bf["xl2"]), p(k.bufs[0]), p(k.bufs[1]),
+                                          p(k.bufs[2]), p(bf["hk"]), self.F, self.D, 0, s))
+        v = self.proj[f"blocks.{l}.ffn.value.weight"]
+        _lib.check(L.rwkv_x070_ffn_value(p(bf["hk"]), p(v.bufs[0]), p(v.bufs[1]), p(v.bufs[2]), p(x), self.D, self.F,
+                                         0, p(bf["xl2"]), p(state.cmix_prev[l]), s))
 
     def launches_per_token(self, N: int = 1) -> int:
         """Kernel launches of one step of N rows: per layer 2 shift_mix +
@@ -316,6 +369,9 @@ class X070Decoder:
                 return 2 * len(chunks) + 2 * staged
             k = 1 + (1 + 2 * (ep == 2) if q.kind == "dense" else 0)
             return k + 2 * staged
+        if self._ln_fused(N):   # r/k/v + low-rank, tmix core, o, ffn key, ffn value
+            return sum(4 + n(self.proj[f"blocks.{l}.att.output.weight"], 1) for l in range(self.L)) + 2 + n(
+                self.proj["head.weight"])
         # 2 shift_mix + tmix_core + (lora_in and the r/k/v projections, or
         # their one fused launch) + o / ffn key / ffn value
         per_layer = sum((4 if self._fused_rkv_lora(l, N) else 4 + n(self.proj[f"blocks.{l}.att.rkv"])) + sum(
@@ -349,7 +405,7 @@ class X070Decoder:
         _lib.check(L.rwkv_x070_lora_in(p(bf["xmix"]), p(lay["wcat"]), _dt(lay["wcat"]), rw, ra, rv, rg, int(l > 0),
                                        p(bf["la"]), N, self.D, s))
 
-    def _tmix_core(self, l, lay, state, bf, N, s):
+    def _tmix_core(self, l, lay, state, bf, N, s, shift=None):
         L, p = _lib.lib(), (lambda t: t.data_ptr())
         rw, ra, rv, rg = self.ranks
         wdt = _dt(lay["wcat"])
@@ -358,7 +414,8 @@ class X070Decoder:
                                          rw, ra, rv, rg, p(lay["bias"][0]), p(lay["bias"][1]), p(lay["bias"][2]),
                                          p(lay["k_k"]), p(lay["k_a"]), p(lay["r_k"]), p(lay["lnx"][0]),
                                          p(lay["lnx"][1]), p(state.v_first), int(l == 0), p(state.wkv[l]),
-                                         p(bf["tout"]), N, self.H, LNX_EPS, s))
+                                         p(bf["tout"]), N, self.H, LNX_EPS, None if shift is None else p(shift[0]),
+                                         None if shift is None else p(shift[1]), s))
 
     def _gemv(self, key, x, y, ep, N, s):
         self._run(self.proj[key], x, y, ep, N, s)

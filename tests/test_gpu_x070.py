@@ -173,7 +173,7 @@ def test_tmix_core(tiny, l, N):
     _lib.call("rwkv_x070_tmix_core", y_rkv.data_ptr(), la_d.data_ptr(), *[b.data_ptr() for b in B], _lib.F16,
               rw, ra, rv, rg, *[b.data_ptr() for b in bias], vec["k_k"].data_ptr(), vec["k_a"].data_ptr(),
               vec["r_k"].data_ptr(), vec["ln_x.weight"].data_ptr(), vec["ln_x.bias"].data_ptr(), vf_d.data_ptr(),
-              int(l == 0), st_d.data_ptr(), out.data_ptr(), N, H, 64e-5, None)
+              int(l == 0), st_d.data_ptr(), out.data_ptr(), N, H, 64e-5, None, None, None)
     tail, wkv_ref, vf_ref = X.core(p, l, r.astype(np.float64), k0.astype(np.float64), v0.astype(np.float64),
                                    [z.astype(np.float64) for z in la], v_first.astype(np.float64),
                                    wkv.astype(np.float64), H)
@@ -242,7 +242,7 @@ def test_decode_steps_match_oracle(tiny, decoder, N):
         ch = (N + 31) // 32
         assert decoder.launches_per_token(N) == (4 + 4 * 2 * ch) * Lr + 2 + 2 * ch
     else:
-        assert decoder.launches_per_token(N) == (7 if N == 1 else 8) * Lr + 3
+        assert decoder.launches_per_token(N) == (5 if N == 1 else 8) * Lr + 3
 
 
 @pytest.mark.parametrize("D,xbits,wdt", [(768, 0, np.float16), (2048, 0, np.float16), (4096, 0, np.float16),
@@ -287,18 +287,76 @@ def test_rkv_lora_matches_separate(D, xbits, wdt, l):
 
 
 def test_decode_fused_rkv_lora_bitwise(tiny, decoder):
-    """The decoder's batch-1 step with the r/k/v GEMV and lora_in fused is
-    bitwise the step with the two launches."""
-    case("decode fused rkv+lora vs separate")
+    """The decoder's batch-1 step with the r/k/v GEMV and lora_in fused, and
+    with the GEMV launches forming their ln / token-shift rows themselves, is
+    bitwise the step with the separate launches (logits and every state row)."""
+    case("decode fused rkv+lora / rows formed in the GEMVs vs separate")
     ids = [5, 300, 17]
     outs = []
-    for fuse in (True, False):
-        decoder.fuse_rkv_lora = fuse
+    for fuse, ln in ((True, True), (True, False), (False, False)):
+        decoder.fuse_rkv_lora, decoder.fuse_ln = fuse, ln
+        assert decoder._ln_fused(1) == ln
         st = decoder.new_state(1)
-        outs.append([decoder.step([i], st) for i in ids] + [st.wkv.clone(), st.v_first.clone()])
-    decoder.fuse_rkv_lora = True
-    for a, b in zip(*outs):
-        assert torch.equal(a, b)
+        outs.append([decoder.step([i], st) for i in ids] + [st.wkv.clone(), st.v_first.clone(),
+                                                             st.tmix_prev.clone(), st.cmix_prev.clone()])
+    decoder.fuse_rkv_lora = decoder.fuse_ln = True
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("D", [768, 2048, 4096])
+def test_rows_formed_in_gemv_launches_bitwise(D):
+    """rwkv_x070_rkv_lora_ln / ffn_key_ln / ffn_value against rwkv_x070_shift_mix
+    + rwkv_x070_rkv_lora / rwkv_sb6_gemv_ep at the 0.1B, 1.5B and 7B-class
+    widths: outputs, the LN rows handed on and the shift-state copy, bitwise."""
+    from swiftrwkv_amd import quant as Q
+    case(f"rows formed in the GEMV launches D={D}")
+    rng = np.random.default_rng(D)
+    F = 4 * D if D < 4096 else 14336
+    L = _lib.lib()
+
+    def sb6(OUT, IN):
+        w = (rng.standard_normal((OUT, IN), dtype=np.float32) * np.float32(0.02))
+        disk = Q.encode_sb6(w, 4, 8)
+        qb, qs, dd, _ = Q.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"], disk["gw_dm"], None,
+                                          None, (OUT, IN))
+        return [dev(qb), dev(qs), dev(np.ascontiguousarray(dd).view(np.float16))]
+
+    qr, qk, qv = sb6(3 * D, D), sb6(F, D), sb6(D, F)
+    rw, ra, rv, rg = syn.lora_ranks(D)
+    RT = rw + ra + rv + rg
+    wcat = dev((rng.standard_normal((RT, D)) * 0.05).astype(np.float16))
+    f = lambda *s, scale=1.0: dev((rng.standard_normal(s) * scale).astype(np.float32))
+    x, lnw, lnb, prev, coef6 = f(D, scale=2.0), f(D, scale=0.3) + 1, f(D, scale=0.1), f(D), f(6, D, scale=0.5)
+    p = lambda t: t.data_ptr()
+    # reference: shift_mix (6 coefficients) + rkv_lora
+    prev_a, xrkv, xmix = prev.clone(), torch.empty(3, D, device=DEV), torch.empty(4, D, device=DEV)
+    y_a, la_a = torch.empty(3 * D, device=DEV), torch.empty(RT, device=DEV)
+    _lib.check(L.rwkv_x070_shift_mix(p(x), p(lnw), p(lnb), p(prev_a), p(coef6), 6, p(xrkv), p(xmix), 1, D, 1e-5, None))
+    _lib.check(L.rwkv_x070_rkv_lora(p(xrkv), *[p(t) for t in qr], p(y_a), 3 * D, D, 0, D, p(xmix), p(wcat), _lib.F16,
+                                    rw, ra, rv, rg, 1, p(la_a), None))
+    y_b, la_b, xl = torch.empty(3 * D, device=DEV), torch.empty(RT, device=DEV), torch.empty(D, device=DEV)
+    _lib.check(L.rwkv_x070_rkv_lora_ln(p(x), p(lnw), p(lnb), p(prev), p(coef6), 1e-5, p(xl), *[p(t) for t in qr],
+                                       p(y_b), D, 0, p(wcat), _lib.F16, rw, ra, rv, rg, 1, p(la_b), None))
+    torch.cuda.synchronize()
+    assert torch.equal(y_a, y_b) and torch.equal(la_a, la_b)
+    assert torch.equal(xl, prev_a)          # the LN row shift_mix stored as the next prev
+    # ffn: shift_mix (1 coefficient) + key GEMV relu², then value + residual
+    ck = coef6[1].contiguous()
+    prev_c, xk, hk_a = prev.clone(), torch.empty(D, device=DEV), torch.empty(F, device=DEV)
+    _lib.check(L.rwkv_x070_shift_mix(p(x), p(lnw), p(lnb), p(prev_c), p(ck), 1, p(xk), None, 1, D, 1e-5, None))
+    _lib.check(L.rwkv_sb6_gemv_ep(p(xk), 1, *[p(t) for t in qk], p(hk_a), F, D, 0, 2, None))
+    hk_b, xl2 = torch.empty(F, device=DEV), torch.empty(D, device=DEV)
+    _lib.check(L.rwkv_x070_ffn_key_ln(p(x), p(lnw), p(lnb), p(prev), p(ck), 1e-5, p(xl2), *[p(t) for t in qk],
+                                      p(hk_b), F, D, 0, None))
+    torch.cuda.synchronize()
+    assert torch.equal(hk_a, hk_b) and torch.equal(xl2, prev_c)
+    xa, xb, dst = x.clone(), x.clone(), prev.clone()
+    _lib.check(L.rwkv_sb6_gemv_ep(p(hk_a), 1, *[p(t) for t in qv], p(xa), D, F, 0, 1, None))
+    _lib.check(L.rwkv_x070_ffn_value(p(hk_b), *[p(t) for t in qv], p(xb), D, F, 0, p(xl2), p(dst), None))
+    torch.cuda.synchronize()
+    assert torch.equal(xa, xb) and torch.equal(dst, prev_c)
 
 
 @pytest.mark.parametrize("N", [1, 2])

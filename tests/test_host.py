@@ -75,8 +75,19 @@ def test_x070_step_entry_validation():
     assert lib.rwkv_x070_lora_in(d, d, F16, 60, 64, 32, 128, 1, d, 1, 768, None) == 1
     assert lib.rwkv_x070_lora_in(d, d, _lib.BF16, 64, 64, 32, 128, 1, d, 1, 768, None) == 2
     # tmix core: v branch buffers needed above layer 0
-    args = [d] * 6 + [F16, 64, 64, 32, 128] + [d, d, None] + [d] * 5 + [d, 0, d, d, 1, 12, 64e-5, None]
+    args = [d] * 6 + [F16, 64, 64, 32, 128] + [d, d, None] + [d] * 5 + [d, 0, d, d, 1, 12, 64e-5, None, None, None]
     assert lib.rwkv_x070_tmix_core(*args) == 6
+    args = [d] * 6 + [F16, 64, 64, 32, 128] + [d, d, d] + [d] * 5 + [d, 0, d, d, 1, 12, 64e-5, d, None, None]
+    assert lib.rwkv_x070_tmix_core(*args) == 6                                                    # shift copy: both
+    # launches forming their GEMV inputs: the x070 plans, batch 1, 4-bit
+    assert lib.rwkv_x070_ln_fused_applies(768, 3072, 0) == 1
+    assert lib.rwkv_x070_ln_fused_applies(4096, 14336, 0) == 1
+    assert lib.rwkv_x070_ln_fused_applies(768, 3072, 1) == 0
+    assert lib.rwkv_x070_ln_fused_applies(8192, 32768, 0) == 0                                     # D > 4096
+    assert lib.rwkv_x070_ffn_value(d, d, d, d, d, 768, 3072, 0, d, None, None) == 6              # copy: both
+    assert lib.rwkv_x070_ffn_key_ln(d, d, d, None, d, 1e-5, d, d, d, d, d, 3072, 768, 0, None) == 6
+    assert lib.rwkv_x070_rkv_lora_ln(*([d] * 5), 1e-5, d, d, d, d, d, 768, 0, d, _lib.BF16, 64, 64, 32, 128, 1, d,
+                                     None) == 2                                                    # fp16 matrices
     # r/k/v GEMV + low-rank first layers in one launch: the checks of both entries
     rkl = lambda *a: lib.rwkv_x070_rkv_lora(d, d, d, d, d, *a)
     assert rkl(3 * 768, 768, 0, 768, None, d, F16, 64, 64, 32, 128, 1, d, None) == 6            # no xmix
@@ -397,6 +408,7 @@ def test_x070_launch_count():
     d = X070Decoder.__new__(X070Decoder)
     d.L = 2
     d.fuse_rkv_lora = False
+    d.fuse_ln = False
     P = lambda kind: Proj(kind, (), 64, 64)
     d.proj = {"blocks.0.att.rkv": P("sb6"), "blocks.1.att.rkv": [P("sym"), P("sb6"), P("dense")],
               "head.weight": P("dense")}
@@ -417,6 +429,10 @@ def test_x070_launch_count():
     for l in range(2):
         d.proj[f"blocks.{l}.att.rkv"] = Proj("sb6", (), 192, 64, out_per=64)
     assert d.launches_per_token(1) == 7 * 2 + 3
+    # and forming the rows: r/k/v + low-rank, tmix core, o, ffn key, ffn value
+    d.fuse_ln, d.D, d.F = True, 768, 3072
+    assert d.launches_per_token(1) == 5 * 2 + 3
+    assert d.launches_per_token(2) == 8 * 2 + 3   # batches keep the shift_mix launches
     assert d.launches_per_token(2) == 8 * 2 + 3
     d.layers = [{"wcat": torch.empty(0, dtype=torch.float32)}] * 2
     assert d.launches_per_token(1) == 8 * 2 + 3
