@@ -184,15 +184,20 @@ __global__ __launch_bounds__(R4 ? 1024 : 256) void tmix_core_kernel(CoreArgs A) 
         const char* wr;
         bool on;
     };
+    // The branch is uniform per wave (read from the first lane) and the
+    // job's matrix, rank and offset are selected among the kernel arguments,
+    // not indexed: an indexed argument is a vector load whose result every
+    // address below would have to wait for.
     auto job_of = [&](int job) {
         Job j;
-        j.b = job >> 3;
+        j.b = __builtin_amdgcn_readfirstlane(job >> 3);
         j.i = (job & 7) * 8 + i0;
         j.on = !(j.b == 2 && A.layer0);
-        j.off = 0;
-        for (int q = 0; q < j.b; ++q) j.off += A.rank[q];
-        j.rk = A.rank[j.b];
-        j.wr = reinterpret_cast<const char*>(A.W2[j.b]) + (int64_t)(h * D + j.i) * j.rk * (H16 ? 2 : 4);
+        const int r0 = A.rank[0], r1 = A.rank[1], r2 = A.rank[2], r3 = A.rank[3];
+        j.off = j.b == 0 ? 0 : j.b == 1 ? r0 : j.b == 2 ? r0 + r1 : r0 + r1 + r2;
+        j.rk = j.b == 0 ? r0 : j.b == 1 ? r1 : j.b == 2 ? r2 : r3;
+        const void* w = j.b == 0 ? A.W2[0] : j.b == 1 ? A.W2[1] : j.b == 2 ? A.W2[2] : A.W2[3];
+        j.wr = reinterpret_cast<const char*>(w) + (int64_t)(h * D + j.i) * j.rk * (H16 ? 2 : 4);
         return j;
     };
     auto load_chunk = [&](const Job& j, int c0, uint4 (&raw)[8]) {
@@ -202,30 +207,49 @@ __global__ __launch_bounds__(R4 ? 1024 : 256) void tmix_core_kernel(CoreArgs A) 
             if (c < j.rk) raw[q] = *reinterpret_cast<const uint4*>(j.wr + (int64_t)c * (H16 ? 2 : 4));
         }
     };
+    // The low-rank inputs of two slices are read from LDS before their
+    // products (16-byte reads; a row's last slices may read up to 127 floats
+    // past its rank, inside the RT + 5·64 floats of LDS, values that are not
+    // used); the products stay in column order.
     auto fma_chunk = [&](const Job& j, int c0, const uint4 (&raw)[8], float& acc) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int c = c0 + 8 * E * q + E * sub;
-            if (c >= j.rk) continue;
-            if constexpr (H16) {
-                const __half2* hh = reinterpret_cast<const __half2*>(&raw[q]);
+        for (int q0 = 0; q0 < 8; q0 += 2) {   // two slices' reads in flight at a time
+            if (c0 + 8 * E * q0 >= j.rk) break;   // uniform: no slice from q0 on is taken
+            float4 xa[2], xb[2];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float2 f = __half22float2(hh[e]);
-                    acc = fmaf(lav[j.off + c + 2 * e], f.x, acc);
-                    acc = fmaf(lav[j.off + c + 2 * e + 1], f.y, acc);
+            for (int u = 0; u < 2; ++u) {
+                const int c = c0 + 8 * E * (q0 + u) + E * sub;
+                xa[u] = *reinterpret_cast<const float4*>(lav + j.off + c);
+                if constexpr (H16) xb[u] = *reinterpret_cast<const float4*>(lav + j.off + c + 4);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int q = q0 + u, c = c0 + 8 * E * q + E * sub;
+                if (c >= j.rk) continue;
+                if constexpr (H16) {
+                    const __half2* hh = reinterpret_cast<const __half2*>(&raw[q]);
+                    const float xs[8] = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float2 f = __half22float2(hh[e]);
+                        acc = fmaf(xs[2 * e], f.x, acc);
+                        acc = fmaf(xs[2 * e + 1], f.y, acc);
+                    }
+                } else {
+                    const float4 f = *reinterpret_cast<const float4*>(&raw[q]);
+                    acc = fmaf(xa[u].x, f.x, acc);
+                    acc = fmaf(xa[u].y, f.y, acc);
+                    acc = fmaf(xa[u].z, f.z, acc);
+                    acc = fmaf(xa[u].w, f.w, acc);
                 }
-            } else {
-                const float4 f = *reinterpret_cast<const float4*>(&raw[q]);
-                acc = fmaf(lav[j.off + c], f.x, acc);
-                acc = fmaf(lav[j.off + c + 1], f.y, acc);
-                acc = fmaf(lav[j.off + c + 2], f.z, acc);
-                acc = fmaf(lav[j.off + c + 3], f.w, acc);
             }
         }
     };
     // the row's bias (w, a, v branches), loaded with the job's first chunk
-    auto bias_of = [&](const Job& j) { return j.b < 3 ? A.bias[j.b][h * D + j.i] : 0.0f; };
+    auto bias_of = [&](const Job& j) {
+        const float* bp = j.b == 0 ? A.bias[0] : j.b == 1 ? A.bias[1] : A.bias[2];
+        return j.b < 3 ? bp[h * D + j.i] : 0.0f;
+    };
     auto finish = [&](const Job& j, float acc, float bias) {
         acc = sum8_lanes(acc);
         if (sub == 0) {
