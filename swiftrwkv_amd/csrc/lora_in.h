@@ -35,10 +35,26 @@ __device__ __forceinline__ int lora_branch(int j, int rw, int ra, int rv) {
     return j < rw ? 0 : j < rw + ra ? 1 : j < rw + ra + rv ? 2 : 3;
 }
 
-// One job given its branch's input row xin (global memory or LDS).
+// The matrix slices of a job's first chunk (columns lane·E + 64·E·q), for a
+// caller that issues them before it forms the input row.
+template <bool H16, int BATCH>
+__device__ __forceinline__ void lora_in_first(int j, int lane, const void* __restrict__ Wcat, int D,
+                                              uint4 (&first)[BATCH]) {
+    constexpr int E = H16 ? 8 : 4;
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q) {
+        const int c = min(64 * E * q + lane * E, D - E);   // past the row: a valid slice, not used
+        first[q] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(Wcat) +
+                                                   ((int64_t)j * D + c) * (H16 ? 2 : 4));
+    }
+}
+
+// One job given its branch's input row xin (global memory or LDS); with
+// `first`, the first chunk's matrix slices are already loaded.
 template <bool H16, int BATCH>
 __device__ __forceinline__ void lora_in_row(int j, int n, int lane, const float* xin, const void* __restrict__ Wcat,
-                                            float* __restrict__ la, int D, int RT, int br) {
+                                            float* __restrict__ la, int D, int RT, int br,
+                                            const uint4 (*first)[BATCH] = nullptr) {
     float acc = 0.0f;
     constexpr int E = H16 ? 8 : 4;   // matrix elements per 16-byte load
     for (int c0 = 0; c0 < D; c0 += 64 * E * BATCH) {
@@ -49,7 +65,7 @@ __device__ __forceinline__ void lora_in_row(int j, int n, int lane, const float*
             const int c = c0 + 64 * E * q + lane * E;
             if (c < D) {   // D % 8 == 0
                 const char* base = reinterpret_cast<const char*>(Wcat) + ((int64_t)j * D + c) * (H16 ? 2 : 4);
-                raw[q] = *reinterpret_cast<const uint4*>(base);
+                raw[q] = (first && c0 == 0) ? (*first)[q] : *reinterpret_cast<const uint4*>(base);
                 xa[q] = *reinterpret_cast<const float4*>(xin + c);
                 if (H16) xb[q] = *reinterpret_cast<const float4*>(xin + c + 4);
             }

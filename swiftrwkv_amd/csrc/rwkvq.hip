@@ -507,6 +507,9 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
         }
     };
     // the residual of the add epilogue, read while the weights stream
+    // (and the state row a copy epilogue hands on: read here, with the
+    // weights in flight, not after the products)
+    float cpv[RL];
     auto load_res = [&](float (&res)[NT][RL], int n0) {
 #pragma unroll
         for (int nn = 0; nn < NT; ++nn)
@@ -516,6 +519,11 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
                 res[nn][rr] = (geo.ep == 1 && g == 0 && row < OUT && n0 + nn < N) ? y[(int64_t)(n0 + nn) * OUT + row]
                                                                                  : 0.0f;
             }
+#pragma unroll
+        for (int rr = 0; rr < RL; ++rr) {
+            const int row = row0 + rr;
+            cpv[rr] = (geo.cp_dst && g == 0 && row < OUT) ? geo.cp_src[row] : 0.0f;
+        }
     };
     auto store = [&](float (&acc)[NT][RL], int n0, const float (&res)[NT][RL]) {
 #pragma unroll
@@ -526,7 +534,7 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
                 const int row = row0 + rr;
                 if (g == 0 && row < OUT && n0 + nn < N) {
                     store_out(y, (int64_t)(n0 + nn) * OUT + row, t, geo.ep, res[nn][rr]);
-                    if (geo.cp_dst) geo.cp_dst[row] = geo.cp_src[row];
+                    if (geo.cp_dst && n0 + nn == 0) geo.cp_dst[row] = cpv[rr];
                 }
             }
     };
@@ -756,6 +764,10 @@ __global__ __launch_bounds__(1024) void rkv_lora_ln_kernel(typename Sb6Fmt<0>::P
     const int RT = rw + ra + rv + rg, nthr = 64 * geo.WPB, IN4 = IN >> 2;
     const int job = (int)blockIdx.x * geo.WPB + (threadIdx.x >> 6);
     const int br = lora_branch(min((int)blockIdx.x * geo.WPB, RT - 1), rw, ra, rv);   // uniform
+    // the job's matrix row first (its first chunk; a wave past the jobs
+    // reads row RT − 1), then the input row's loads
+    uint4 first[4];
+    lora_in_first<true, 4>(min(job, RT - 1), threadIdx.x & 63, wcat, IN, first);
     const float* coef = lm.coef + (int64_t)(br == 0 ? 3 : br == 1 ? 4 : br == 2 ? 2 : 5) * IN;
     int S_, T, PS;
     row_geometry(IN, S_, T, PS);
@@ -781,7 +793,7 @@ __global__ __launch_bounds__(1024) void rkv_lora_ln_kernel(typename Sb6Fmt<0>::P
     }
     __syncthreads();
     if (job >= RT || (br == 2 && !with_v)) return;   // uniform per wave
-    lora_in_row<true, 4>(job, 0, threadIdx.x & 63, lds, wcat, la, IN, RT, br);
+    lora_in_row<true, 4>(job, 0, threadIdx.x & 63, lds, wcat, la, IN, RT, br, &first);
 }
 
 // The ffn key GEMV (relu² epilogue) forming its input itself (LnMix: ln2,
