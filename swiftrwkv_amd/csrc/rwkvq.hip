@@ -1430,12 +1430,18 @@ rwkv_status rwkv_x070_rkv_lora(const float* x_rkv, const uint8_t* qblk, const ui
 namespace {
 // The plan of a GEMV that forms its input row in the launch: one input, one
 // pass of 3 or 4 units per lane, one input row per workgroup, and the row
-// (IN ≤ 4096, IN % 256 == 0) within four float4 per thread.
+// (IN ≤ 4096, IN % 256 == 0) within four float4 per thread.  Forming the row
+// costs registers (~90-104 VGPRs against 58: 4-5 waves per SIMD against 8),
+// so only grids that still run in one round take it: at most 4096 waves, four
+// per SIMD of the 256 CUs of a gfx950 (the 0.1B ... 1.5B shapes; at 7B-class
+// widths the separate row launch is faster: 1.78 against 1.93 ms per token).
+constexpr int64_t kLnWavesMax = 4 * 4 * 256;
 bool ln_plan(int64_t OUT, int64_t IN, int64_t out_per, GemvPlan& pl) {
     if (IN < 256 || IN % 256 || IN > 4096 || out_per < 1 || OUT % out_per) return false;
     pl = plan_gemv(OUT, IN / 32, out_per, 1, OUT / out_per, true, false);
     return pl.NT == 1 && pl.xl && pl.geo.NP == 1 && pl.RL == 1 && (pl.KU == 3 || pl.KU == 4) &&
-           (OUT == out_per || pl.geo.one_k) && IN <= 16 * 64 * pl.geo.WPB;
+           (OUT == out_per || pl.geo.one_k) && IN <= 16 * 64 * pl.geo.WPB &&
+           (int64_t)pl.blocks * pl.geo.WPB <= kLnWavesMax;
 }
 // float4 chunks of the row per thread (1, 2 or 4)
 int ln_chunks(int64_t IN, const GemvPlan& pl) {

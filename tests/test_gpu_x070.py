@@ -305,16 +305,18 @@ def test_decode_fused_rkv_lora_bitwise(tiny, decoder):
             assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("D", [768, 2048, 4096])
+@pytest.mark.parametrize("D", [768, 1024, 2048])
 def test_rows_formed_in_gemv_launches_bitwise(D):
     """rwkv_x070_rkv_lora_ln / ffn_key_ln / ffn_value against rwkv_x070_shift_mix
-    + rwkv_x070_rkv_lora / rwkv_sb6_gemv_ep at the 0.1B, 1.5B and 7B-class
-    widths: outputs, the LN rows handed on and the shift-state copy, bitwise."""
+    + rwkv_x070_rkv_lora / rwkv_sb6_gemv_ep at the 0.1B, 0.4B and 1.5B widths
+    (the shapes rwkv_x070_ln_fused_applies takes): outputs, the LN rows handed
+    on and the shift-state copy, bitwise."""
     from swiftrwkv_amd import quant as Q
     case(f"rows formed in the GEMV launches D={D}")
     rng = np.random.default_rng(D)
-    F = 4 * D if D < 4096 else 14336
+    F = 4 * D
     L = _lib.lib()
+    assert L.rwkv_x070_ln_fused_applies(D, F, 0) == 1
 
     def sb6(OUT, IN):
         w = (rng.standard_normal((OUT, IN), dtype=np.float32) * np.float32(0.02))

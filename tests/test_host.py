@@ -81,7 +81,8 @@ def test_x070_step_entry_validation():
     assert lib.rwkv_x070_tmix_core(*args) == 6                                                    # shift copy: both
     # launches forming their GEMV inputs: the x070 plans, batch 1, 4-bit
     assert lib.rwkv_x070_ln_fused_applies(768, 3072, 0) == 1
-    assert lib.rwkv_x070_ln_fused_applies(4096, 14336, 0) == 1
+    assert lib.rwkv_x070_ln_fused_applies(2048, 8192, 0) == 1
+    assert lib.rwkv_x070_ln_fused_applies(4096, 14336, 0) == 0                                    # grids > one round
     assert lib.rwkv_x070_ln_fused_applies(768, 3072, 1) == 0
     assert lib.rwkv_x070_ln_fused_applies(8192, 32768, 0) == 0                                     # D > 4096
     assert lib.rwkv_x070_ffn_value(d, d, d, d, d, 768, 3072, 0, d, None, None) == 6              # copy: both
