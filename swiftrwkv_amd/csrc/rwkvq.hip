@@ -580,7 +580,8 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
             // the row loads first (the statistics chunks of threads < T as
             // the row kernel assigns them, then this thread's LNC staging
             // chunks e = tid + i·nthr), then the weights; one input row
-            // (rows == 1), IN ≤ 4·LNC·nthr and IN ≤ 4096 (checked by the host).
+            // (rows == 1), IN ≤ 4·LNC·nthr, LNC ≤ 2 and IN ≤ 4096 (checked by
+            // the host).
             using namespace rwkv_x070;
             __shared__ float red[32];
             const int IN4 = IN >> 2;
@@ -1440,13 +1441,12 @@ bool ln_plan(int64_t OUT, int64_t IN, int64_t out_per, GemvPlan& pl) {
     if (IN < 256 || IN % 256 || IN > 4096 || out_per < 1 || OUT % out_per) return false;
     pl = plan_gemv(OUT, IN / 32, out_per, 1, OUT / out_per, true, false);
     return pl.NT == 1 && pl.xl && pl.geo.NP == 1 && pl.RL == 1 && (pl.KU == 3 || pl.KU == 4) &&
-           (OUT == out_per || pl.geo.one_k) && IN <= 16 * 64 * pl.geo.WPB &&
+           (OUT == out_per || pl.geo.one_k) && IN <= 8 * 64 * pl.geo.WPB &&
            (int64_t)pl.blocks * pl.geo.WPB <= kLnWavesMax;
 }
-// float4 chunks of the row per thread (1, 2 or 4)
+// float4 chunks of the row per thread (1 or 2; more would spill)
 int ln_chunks(int64_t IN, const GemvPlan& pl) {
-    const int64_t c = (IN / 4 + 64 * pl.geo.WPB - 1) / (64 * pl.geo.WPB);
-    return c <= 1 ? 1 : c <= 2 ? 2 : 4;
+    return IN / 4 <= 64 * pl.geo.WPB ? 1 : 2;
 }
 // the value GEMV with the residual add and the state copy
 bool value_plan(int64_t OUT, int64_t IN, GemvPlan& pl) {
@@ -1494,10 +1494,8 @@ rwkv_status rwkv_x070_rkv_lora_ln(const float* x, const float* ln_w, const float
                      pl.geo, lb, lm, wcat, la, (int)rw, (int)ra, (int)rv, (int)rg, with_v)
     RWKV_RLL(4, 1);
     RWKV_RLL(4, 2);
-    RWKV_RLL(4, 4);
     RWKV_RLL(3, 1);
     RWKV_RLL(3, 2);
-    RWKV_RLL(3, 4);
 #undef RWKV_RLL
     const rwkv_status s = launch_status("x070_rkv_lora_ln");
     if (s == RWKV_OK) {
@@ -1527,10 +1525,8 @@ rwkv_status rwkv_x070_ffn_key_ln(const float* x, const float* ln_w, const float*
     if (pl.KU == KUV && ch == CHV) rwkv::launch_lds(gemv_ln_kernel<KUV, CHV>, grid, block, pl.lds, st, P, hk, (int)F, (int)D, pl.geo, lm)
     RWKV_KL(4, 1);
     RWKV_KL(4, 2);
-    RWKV_KL(4, 4);
     RWKV_KL(3, 1);
     RWKV_KL(3, 2);
-    RWKV_KL(3, 4);
 #undef RWKV_KL
     const rwkv_status s = launch_status("x070_ffn_key_ln");
     if (s == RWKV_OK) {
