@@ -600,12 +600,15 @@ def rwkvq_sb6_gemv_batch_applies(rows: int, out_features: int, in_features: int,
 
 
 def rwkvq_sb6_gemv_batch_prefers(rows: int, out_features: int, in_features: int) -> bool:
-    """Where the batched matrix-core GEMV beats the one-input kernel run over
-    the rows (MI355X, measured per launch): 8+ rows of matrices of 2^24+
-    weights (7B-class layers, the heads: 4096x4096 x16 17 vs 20 µs,
-    14336x4096 x16 27 vs 72 µs, 65536x1024 x32 46 vs 112 µs); smaller ones
-    are bound by the launch pair it needs (1024x1024 x32 8.1 vs 7.6 µs)."""
-    return rows >= 8 and out_features * in_features >= (1 << 24)
+    """Where the batched matrix-core GEMV (its launch pair included) beats the
+    VALU batch kernel (MI355X, graph-timed per launch): 16+ rows of matrices
+    of 2^20+ weights (1024x1024 x16 5.5 vs 6.9 µs, 3072x768 x32 7.8 vs
+    9.1 µs, 2048x8192 x32 19.1 vs 44.0 µs), 8+ rows of 2^22+ weights
+    (4096x1024 x8 6.8 vs 7.3 µs, 6144x2048 x8 10.8 vs 14.8 µs); below that
+    the two are within a few percent (768x768 x32 6.0 vs 5.6 µs) and the
+    VALU kernel keeps its bitwise one-row results."""
+    n = out_features * in_features
+    return (rows >= 16 and n >= (1 << 20)) or (rows >= 8 and n >= (1 << 22))
 
 
 _GEMV_EP = {"store": 0, "add": 1, "relu2": 2}

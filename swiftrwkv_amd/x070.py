@@ -423,7 +423,8 @@ class X070Decoder:
     # Which sb6 projections of a batch take the matrix-core batched GEMV
     # (within fp32 rounding of each row alone) instead of the one-input
     # arithmetic run over the rows (bitwise each row alone): None = where it
-    # is faster (quant.rwkvq_sb6_gemv_batch_prefers: 8+ rows, 2^24+ weights),
+    # is faster (quant.rwkvq_sb6_gemv_batch_prefers: 16+ rows of 2^20+ weights,
+    # 8+ rows of 2^22+),
     # True = wherever it applies (2+ rows), False = never.
     batch_mfma: Optional[bool] = None
 
