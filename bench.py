@@ -246,13 +246,23 @@ class DecodeStep:
                 self.mfma.add((OUT, IN, per))
                 need = max(need, int(L.rwkv_sb6_gemv_batch_workspace(B, OUT, IN, per)))
         self.ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        # their weights in the matrix cores' T16 order, one copy per device copy
+        self.t16 = [{} for _ in model.dev]
+        if self.mfma:
+            for c, W in enumerate(model.dev):
+                for key, q in W.items():
+                    OUT, IN = q[0].shape[0], q[0].shape[1] * 2   # qblk [OUT, IN/2]
+                    per = D if key.endswith("att.rkv") else OUT
+                    if (OUT, IN, per) in self.mfma:
+                        self.t16[c][id(q)] = Q.rwkvq_sb6_t16(q[0], q[1], q[2], OUT, IN)
 
-    def _gemv(self, L, x, q, y, OUT, IN, per, stream, fused=False):
+    def _gemv(self, L, x, q, y, OUT, IN, per, stream, fused=False, copy=0):
         from swiftrwkv_amd import _lib
         if (OUT, IN, per) in self.mfma:
-            _lib.check(L.rwkv_sb6_gemv_batch(x.data_ptr(), self.B, q[0].data_ptr(), q[1].data_ptr(), q[2].data_ptr(),
-                                             y.data_ptr(), OUT, IN, 0, per, 0, self.ws.data_ptr(), self.ws.numel(),
-                                             stream))
+            t = self.t16[copy][id(q)]
+            _lib.check(L.rwkv_sb6_gemv_batch_t16(x.data_ptr(), self.B, t[0].data_ptr(), t[1].data_ptr(),
+                                                 t[2].data_ptr(), y.data_ptr(), OUT, IN, per, 0, self.ws.data_ptr(),
+                                                 self.ws.numel(), stream))
         elif fused:
             _lib.check(L.rwkv_sb6_gemv_fused(x.data_ptr(), self.B, q[0].data_ptr(), q[1].data_ptr(), q[2].data_ptr(),
                                              y.data_ptr(), OUT, IN, 0, per, stream))
@@ -269,11 +279,12 @@ class DecodeStep:
 
         def gemv(x, key, y):
             OUT, IN = self.model.host[key][3], self.model.host[key][4]
-            self._gemv(L, x, W[key], y, OUT, IN, OUT, stream)
+            self._gemv(L, x, W[key], y, OUT, IN, OUT, stream, copy=copy)
 
         for l in range(self.L):
             # r/k/v in one launch, x rows (x_r, x_k, x_v) per token
-            self._gemv(L, self.xrkv, W[f"blocks.{l}.att.rkv"], self.y_rkv, 3 * D, D, D, stream, fused=True)
+            self._gemv(L, self.xrkv, W[f"blocks.{l}.att.rkv"], self.y_rkv, 3 * D, D, D, stream, fused=True,
+                       copy=copy)
             if gemv_only:
                 gemv(self.tail, f"blocks.{l}.att.output.weight", self.y_o)
                 gemv(self.xD, f"blocks.{l}.ffn.key.weight", self.y_k)

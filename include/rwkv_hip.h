@@ -219,6 +219,26 @@ rwkv_status rwkv_sb6_gemv_batch(const float* x, int64_t N, const uint8_t* qblk, 
                                 int64_t out_per, int epilogue, void* workspace, int64_t workspace_bytes,
                                 void* stream);
 
+/* The sb6 4-bit weights of rwkv_sb6_gemv_batch in the matrix cores' own
+ * order ("T16"; no counterpart in the reference, whose weights stay in K3):
+ * per 16-row tile and group of 4 32-column units, the codes as one 1 KiB
+ * block (lane-ordered for 16-byte loads) and the unit scales precomputed,
+ * s = half(qs·d) and m = half(qm·dm) fp16 [16 rows][4 units].  Sizes as K3:
+ * tq OUT·IN/2 bytes (16-byte aligned), ts and tm OUT·IN/32 fp16 each.
+ * OUT % 16 == 0, IN % 256 == 0.  A permutation and the kernels' own rounding
+ * of s and m: exact. */
+rwkv_status rwkv_sb6_t16_pack(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, int64_t OUT,
+                              int64_t IN, uint8_t* tq, uint16_t* ts, uint16_t* tm, void* stream);
+
+/* rwkv_sb6_gemv_batch over T16 weights (rwkv_sb6_t16_pack): the same shapes,
+ * epilogues, workspace and applies rule (xbits 0); the m·Σx term of every
+ * unit on the matrix cores as well.  Within fp32 rounding of the K3 batch
+ * kernel and of rwkv_sb6_gemv per row (not bitwise).  The batched
+ * counterpart of rwkvqSb6GEMV (RwkvqSb6GEMV.swift:159-190). */
+rwkv_status rwkv_sb6_gemv_batch_t16(const float* x, int64_t N, const uint8_t* tq, const uint16_t* ts,
+                                    const uint16_t* tm, float* y, int64_t OUT, int64_t IN, int64_t out_per,
+                                    int epilogue, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* sb6 counterpart of the sym r/k/v fusion (no counterpart in the reference,
  * which fuses sym groups only, RwkvqSymGEMV.swift:343-358): K = OUT/out_per
  * row-concatenated sb6 matrices in one launch; row `o` of input row n uses

@@ -29,6 +29,10 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
+# The batched matrix-core GEMV reads every MFMA result with VALU ops: results
+# in VGPRs (not AGPRs) save a v_accvgpr_read per result dword.
+FILE_FLAGS = {"gemv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def _hipcc() -> str:
     for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
@@ -52,7 +56,8 @@ def build(verbose: bool = False, extra_hip_flags=()) -> str:
     for src in HIP_SOURCES:
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
         objs.append(obj)
-        jobs.append([hipcc, *HIP_FLAGS, *extra_hip_flags, "-c", os.path.join(CSRC, src), "-o", obj])
+        jobs.append([hipcc, *HIP_FLAGS, *FILE_FLAGS.get(src, ()), *extra_hip_flags, "-c", os.path.join(CSRC, src),
+                     "-o", obj])
     for src in HOST_SOURCES:
         obj = os.path.join(BUILD, src.replace(".cpp", ".o"))
         objs.append(obj)

@@ -653,6 +653,62 @@ def rwkvq_sb6_gemv_batch(x, qblk, qsqm, ddm, out_features: int, in_features: int
     return out
 
 
+def rwkvq_sb6_t16(qblk, qsqm, ddm, out_features: int, in_features: int):
+    """The 4-bit sb6 weights in the matrix cores' T16 order (rwkv_sb6_t16_pack):
+    (tq uint8 [OUT·IN/2], ts fp16 [OUT·IN/32], tm fp16 [OUT·IN/32]) on the
+    device of qblk, for rwkvq_sb6_gemv_batch_t16."""
+    if out_features % 16 or in_features % 256:
+        raise ValueError(f"sb6 T16: [{out_features}, {in_features}] (OUT % 16 == 0, IN % 256 == 0)")
+    if ddm.dtype in (torch.uint16, torch.int16):   # fp16 bit patterns
+        ddm = ddm.view(torch.float16)
+    qblk, qsqm, ddm = _sb6_bufs(qblk, qsqm, ddm, out_features, in_features, 0)
+    dev = qblk.device
+    tq = torch.empty(out_features * in_features // 2, dtype=torch.uint8, device=dev)
+    ts = torch.empty(out_features * in_features // 32, dtype=torch.float16, device=dev)
+    tm = torch.empty_like(ts)
+    _lib.call("rwkv_sb6_t16_pack", qblk.data_ptr(), qsqm.data_ptr(), ddm.data_ptr(), out_features, in_features,
+              tq.data_ptr(), ts.data_ptr(), tm.data_ptr(), _stream(qblk))
+    return tq, ts, tm
+
+
+def rwkvq_sb6_gemv_batch_t16(x, tq, ts, tm, out_features: int, in_features: int, out_per: Optional[int] = None,
+                             epilogue: str = "store", out: Optional[torch.Tensor] = None,
+                             workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """rwkvq_sb6_gemv_batch over T16 weights (rwkvq_sb6_t16): the same inputs,
+    epilogues and workspace."""
+    per = out_features if out_per is None else out_per
+    if x.dim() != 2 or x.shape[1] != in_features:
+        raise ValueError(f"sb6 batched GEMV: input {tuple(x.shape)}, expected [N, {in_features}]")
+    K = out_features // per if per and out_features % per == 0 else 0
+    if K == 0 or x.shape[0] % K:
+        raise ValueError(f"sb6 batched GEMV: {x.shape[0]} input rows for {out_features} rows of matrices of {per}")
+    N = x.shape[0] // K
+    if not rwkvq_sb6_gemv_batch_applies(N, out_features, in_features, 0, per):
+        raise ValueError(f"sb6 batched GEMV: N={N} [{out_features}, {in_features}] out_per={per} not taken")
+    for t, n, dt in ((tq, out_features * in_features // 2, torch.uint8), (ts, out_features * in_features // 32,
+                                                                        torch.float16), (tm, None, torch.float16)):
+        if not t.is_cuda or t.dtype != dt or not t.is_contiguous() or (n is not None and t.numel() != n):
+            raise ValueError("sb6 batched GEMV: T16 buffers from rwkvq_sb6_t16 expected")
+    if tm.numel() != ts.numel():
+        raise ValueError("sb6 batched GEMV: T16 buffers from rwkvq_sb6_t16 expected")
+    x32 = _aligned(x.to(torch.float32))
+    ep = _GEMV_EP[epilogue]
+    if out is None:
+        if ep == 1:
+            raise ValueError("sb6 batched GEMV: the add epilogue needs `out`")
+        out = torch.empty((N, out_features), dtype=torch.float32, device=x.device)
+    elif out.dtype != torch.float32 or tuple(out.shape) != (N, out_features) or not out.is_contiguous() or \
+            out.device != x.device:
+        raise ValueError(f"sb6 batched GEMV: out must be a contiguous float32 [{N}, {out_features}] tensor")
+    need = int(_lib.lib().rwkv_sb6_gemv_batch_workspace(N, out_features, in_features, per))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _lib.call("rwkv_sb6_gemv_batch_t16", x32.data_ptr(), N, tq.data_ptr(), ts.data_ptr(), tm.data_ptr(),
+              out.data_ptr(), out_features, in_features, per, ep, workspace.data_ptr(),
+              workspace.numel() * workspace.element_size(), _stream(x32))
+    return out
+
+
 RWKVQ_SYM_GEMV_MAX_ROWS = 4   # RwkvqSymGEMV.swift:40
 
 

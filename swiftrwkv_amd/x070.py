@@ -211,6 +211,9 @@ class X070Decoder:
         self.proj["head.weight"] = as_proj(proj["head.weight"])
         self._bufs: Optional[dict] = None
         self._tmp: Dict[tuple, torch.Tensor] = {}
+        # T16 copies (quant.rwkvq_sb6_t16) of the sb6 projections that take
+        # the batched matrix-core GEMV, made with the buffers of a batch size
+        self._t16: Dict[int, tuple] = {}
 
     @classmethod
     def from_sidecar(cls, sc, device=None, param_dtype=torch.float16) -> "X070Decoder":
@@ -266,6 +269,9 @@ class X070Decoder:
 
     def _buffers(self, N: int) -> dict:
         if self._bufs is None or self._bufs["N"] != N:
+            for q in self.proj.values():
+                if self._batch_chunks(q, N) is not None and id(q) not in self._t16:
+                    self._t16[id(q)] = Q.rwkvq_sb6_t16(*q.bufs, q.OUT, q.IN)
             dev, D = self.device, self.D
             z = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)
             self._bufs = {"N": N, "x": z(N, D), "xrkv": z(N, 3, D), "xmix": z(N, 4, D), "y_rkv": z(N, 3 * D),
@@ -450,20 +456,23 @@ class X070Decoder:
         return sizes
 
     def _run_batch(self, q: Proj, x: torch.Tensor, y: torch.Tensor, ep: int, N: int, s) -> bool:
-        """rwkv_sb6_gemv_batch over chunks of at most 32 rows; False where it
-        does not apply."""
+        """rwkv_sb6_gemv_batch_t16 over chunks of at most 32 rows, on the
+        projection's T16 copy; False where it does not apply."""
         sizes = self._batch_chunks(q, N)
         if sizes is None:
             return False
+        t16 = self._t16.get(id(q))
+        if t16 is None:   # (launch makes them with its buffers, before any capture)
+            t16 = self._t16[id(q)] = Q.rwkvq_sb6_t16(*q.bufs, q.OUT, q.IN)
         L = _lib.lib()
         K = q.OUT // q.out_per
         ws = self._batch_ws(max(int(L.rwkv_sb6_gemv_batch_workspace(n, q.OUT, q.IN, q.out_per)) for n in set(sizes)))
         x2, y2 = x.reshape(N * K, q.IN), y.reshape(N, q.OUT)
         n0 = 0
         for n in sizes:
-            _lib.check(L.rwkv_sb6_gemv_batch(x2[n0 * K].data_ptr(), n, *[b.data_ptr() for b in q.bufs],
-                                             y2[n0].data_ptr(), q.OUT, q.IN, 0, q.out_per, ep, ws.data_ptr(),
-                                             ws.numel(), s))
+            _lib.check(L.rwkv_sb6_gemv_batch_t16(x2[n0 * K].data_ptr(), n, *[b.data_ptr() for b in t16],
+                                                 y2[n0].data_ptr(), q.OUT, q.IN, q.out_per, ep, ws.data_ptr(),
+                                                 ws.numel(), s))
             n0 += n
         return True
 

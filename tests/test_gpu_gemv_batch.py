@@ -89,6 +89,83 @@ def test_fused_group_and_epilogues(orc, D, N):
     assert rel(host(torch.relu(single) ** 2), host(y_r2)) < 2e-5
 
 
+def t16_unpack(tq, ts, tm, OUT, IN):
+    """T16 → (K3 code bytes [OUT, NU·16], s [OUT, NU] fp16, m [OUT, NU] fp16),
+    the inverse of the layout rwkv_sb6_t16_pack documents: per (16-row tile,
+    4-unit group) 1 KiB of codes, byte offset (g·16 + i)·16 = unit 4G + g of
+    row 16r + i; s, m [16 rows][4 units]."""
+    NU, NG = IN // 32, IN // 128
+    q = tq.reshape(OUT // 16, NG, 4, 16, 16).transpose(0, 3, 1, 2, 4).reshape(OUT, NU * 16)
+    sc = ts.reshape(OUT // 16, NG, 16, 4).transpose(0, 2, 1, 3).reshape(OUT, NU)
+    mc = tm.reshape(OUT // 16, NG, 16, 4).transpose(0, 2, 1, 3).reshape(OUT, NU)
+    return q, sc, mc
+
+
+@pytest.mark.parametrize("OUT,IN", [(768, 768), (192, 2048), (4096, 1024)])
+def test_t16_pack_is_the_k3_weights(orc, OUT, IN):
+    """rwkv_sb6_t16_pack: the codes are the K3 bytes permuted, and code·s + m
+    from its scales is bitwise the oracle's dequantised weight (w = code·s + m,
+    s = half(qs·d), m = half(qm·dm), RwkvqDequant.swift:116-140) everywhere."""
+    case(f"sb6 T16 pack {OUT}x{IN}")
+    rng = np.random.default_rng(OUT + IN)
+    qblk, qsqm, ddm = random_k3(OUT, IN, rng)
+    tq, ts, tm = Q.rwkvq_sb6_t16(dev(qblk), dev(qsqm), dev(ddm), OUT, IN)
+    q, sc, mc = t16_unpack(tq.cpu().numpy(), ts.cpu().numpy(), tm.cpu().numpy(), OUT, IN)
+    assert np.array_equal(q, qblk)
+    codes = np.empty((OUT, IN), np.float32)
+    qb = qblk.reshape(OUT, IN // 32, 16)
+    codes.reshape(OUT, IN // 32, 32)[..., :16] = qb & 0xF
+    codes.reshape(OUT, IN // 32, 32)[..., 16:] = qb >> 4
+    w = codes * np.repeat(sc.astype(np.float32), 32, axis=1) + np.repeat(mc.astype(np.float32), 32, axis=1)
+    want = orc.sb6_dequant(qblk, qsqm, ddm.view(np.uint16), OUT, IN, 0)
+    assert np.array_equal(w.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("OUT,IN", [(768, 768), (3072, 768), (768, 3072), (4096, 4096), (14336, 4096),
+                                    (4096, 14336), (65536, 768)])
+@pytest.mark.parametrize("N", [2, 16, 17, 32])
+def test_t16_batch_matches_k3_batch_and_oracle(orc, OUT, IN, N):
+    case(f"sb6 batched gemv T16 {OUT}x{IN} N={N}")
+    rng = np.random.default_rng(7 * OUT + IN + N)
+    qblk, qsqm, ddm = random_k3(OUT, IN, rng)
+    w = (dev(qblk), dev(qsqm), dev(ddm))
+    t = Q.rwkvq_sb6_t16(*w, OUT, IN)
+    x = rng.standard_normal((N, IN)).astype(np.float32)
+    xd = dev(x)
+    y16 = host(Q.rwkvq_sb6_gemv_batch_t16(xd, *t, OUT, IN))
+    yk3 = host(Q.rwkvq_sb6_gemv_batch(xd, *w, OUT, IN))
+    worst = max(rel(yk3[n], y16[n]) for n in range(N))
+    print(f"[gemv batch t16] {OUT}x{IN} N={N}: rel to the K3 batch kernel {worst:.2e}", flush=True)
+    assert worst < 1e-5
+    if OUT * IN <= 4096 * 4096 or N == 2:
+        want = orc.sb6_gemv_f64(x, qblk, qsqm, ddm.view(np.uint16), OUT, IN, 0)
+        assert rel(want, y16) < 2e-5
+
+
+@pytest.mark.parametrize("D,N", [(768, 8), (4096, 16)])
+def test_t16_fused_group_and_epilogues(D, N):
+    case(f"sb6 batched gemv T16 fused 3x{D}x{D} N={N}, epilogues")
+    rng = np.random.default_rng(3 * D + N)
+    qblk, qsqm, ddm = random_k3(3 * D, D, rng)
+    w = (dev(qblk), dev(qsqm), dev(ddm))
+    t = Q.rwkvq_sb6_t16(*w, 3 * D, D)
+    x = dev(rng.standard_normal((3 * N, D)).astype(np.float32))
+    y = Q.rwkvq_sb6_gemv_batch_t16(x, *t, 3 * D, D, out_per=D)
+    ys = singles(x, w, 3 * D, D, out_per=D)
+    assert rel(host(ys), host(y)) < 1e-5
+    t1 = Q.rwkvq_sb6_t16(w[0][:D], w[1][:D], w[2][:D], D, D)
+    xm = dev(rng.standard_normal((N, D)).astype(np.float32))
+    base = dev(rng.standard_normal((N, D)).astype(np.float32))
+    single = singles(xm, (w[0][:D], w[1][:D], w[2][:D]), D, D)
+    y_add = Q.rwkvq_sb6_gemv_batch_t16(xm, *t1, D, D, epilogue="add", out=base.clone())
+    assert rel(host(base + single), host(y_add)) < 1e-5
+    y_r2 = Q.rwkvq_sb6_gemv_batch_t16(xm, *t1, D, D, epilogue="relu2")
+    assert rel(host(torch.relu(single) ** 2), host(y_r2)) < 2e-5
+    a = Q.rwkvq_sb6_gemv_batch_t16(xm, *t1, D, D)
+    b = Q.rwkvq_sb6_gemv_batch_t16(xm, *t1, D, D)
+    assert torch.equal(a, b)
+
+
 def test_contract_and_declines():
     case("sb6 batched gemv: applicability, workspace, counters")
     L = _lib.lib()
