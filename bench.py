@@ -836,8 +836,9 @@ def profile_kernels(dev, tokens=12):
     and 12 WKV step+tail launches), 6 eager 1.5B decode tokens (97 GEMV
     launches each), the WKV-7 forward at B1 T1024 H12 fp32 (20 launches), the
     time-chunked forward at B1 T1024 H12 (5) and B1 T8192 H64 (2), the
-    batched GEMV of a 14336x4096 matrix x 16 rows on the matrix cores and
-    on the VALU kernel (3 each), the checkpointed training forward +
+    batched GEMV of a 14336x4096 matrix x 16 rows on the matrix cores over
+    K3 weights, over T16 weights and on the VALU kernel (3 each), the
+    checkpointed training forward +
     backward at B8 T4096 H32 bf16 (3 each),
     and a plain 256 MiB device copy whose FETCH_SIZE / WRITE_SIZE calibrate
     the counters (2 x 256 MiB of traffic)."""
@@ -886,9 +887,12 @@ def profile_kernels(dev, tokens=12):
     xb = torch.randn((N, IN), device=dev)
     for _ in range(3):
         Q.rwkvq_sb6_gemv_batch(xb, qb, qs, dd, OUT, IN)
+    t16 = Q.rwkvq_sb6_t16(qb, qs, dd, OUT, IN)
+    for _ in range(3):
+        Q.rwkvq_sb6_gemv_batch_t16(xb, *t16, OUT, IN)
     for _ in range(3):
         Q.rwkvq_sb6_gemv(xb, qb, qs, dd, OUT, IN, 0)
-    del qb, qs, dd, xb
+    del qb, qs, dd, xb, t16
     B, T, H = 8, 4096, 32
     xs = syn.wkv_inputs_config0(B, T, H, seed=3)
     ins = [torch.from_numpy(z).to(dev).to(torch.bfloat16) for z in xs]
