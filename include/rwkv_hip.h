@@ -222,11 +222,12 @@ rwkv_status rwkv_sb6_gemv_batch(const float* x, int64_t N, const uint8_t* qblk, 
 /* The sb6 4-bit weights of rwkv_sb6_gemv_batch in the matrix cores' own
  * order ("T16"; no counterpart in the reference, whose weights stay in K3):
  * per 16-row tile and group of 4 32-column units, the codes as one 1 KiB
- * block (lane-ordered for 16-byte loads) and the unit scales precomputed,
- * s = half(qs·d) and m = half(qm·dm) fp16 [16 rows][4 units].  Sizes as K3:
- * tq OUT·IN/2 bytes (16-byte aligned), ts and tm OUT·IN/32 fp16 each.
- * OUT % 16 == 0, IN % 256 == 0.  A permutation and the kernels' own rounding
- * of s and m: exact. */
+ * block (lane-ordered for 16-byte loads, each lane's dwords of the four
+ * units together) and the unit scales precomputed: s = half(qs·d) fp16
+ * [16 rows][4 units], m = half(qm·dm) as two exact bf16 parts [16 rows]
+ * [4 high, 4 low].  tq OUT·IN/2 bytes (16-byte aligned), ts OUT·IN/32 fp16,
+ * tm OUT·IN/16 bf16.  OUT % 16 == 0, IN % 256 == 0.  A permutation and the
+ * kernels' own rounding of s and m: exact. */
 rwkv_status rwkv_sb6_t16_pack(const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, int64_t OUT,
                               int64_t IN, uint8_t* tq, uint16_t* ts, uint16_t* tm, void* stream);
 

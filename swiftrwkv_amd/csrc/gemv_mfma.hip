@@ -364,24 +364,27 @@ __global__ __launch_bounds__(256) void sb6_gemv_mfma_kernel(BatchArgs A) {
 // T16 layout: the same weights permuted for this kernel's loads, and the unit
 // scales precomputed (rwkv_sb6_t16_pack).  Per 16-row tile (rows 16r..16r+15)
 // and group of 4 units (4G..4G+3), in tile order [r][G]:
-//   codes  1 KiB: byte offset (g·16 + i)·16 holds unit 4G + g of row 16r + i
-//          (the K3 unit's 16 bytes), so lane i + 16g of one 16-byte load per
-//          lane gets exactly what the K3 kernel loads;
-//   s, m   [16 rows][4 units] fp16 each: s = half(qs·d), m = half(qm·dm), the
-//          values the K3 kernels round per unit.
+//   codes  1 KiB: the 16 bytes at offset (g·16 + i)·16 are dword g of units
+//          4G..4G+3 of row 16r + i (a K3 unit's dword g: columns 4g..4g+3 in
+//          the low nibbles, 16+4g.. in the high ones), so lane i + 16g of one
+//          16-byte load per lane holds its B-operand slots of all four units;
+//   s      [16 rows][4 units] fp16: s = half(qs·d), the value the K3 kernels
+//          round per unit;
+//   m      [16 rows][8] bf16: m = half(qm·dm) as two exact bf16 parts, the
+//          four units' high parts, then their low parts (m = hi + lo).
 // One step's codes are 1 KiB contiguous per row tile (8 whole cache lines,
 // where a K3 load touches 16 rows' half lines), its scales 128 bytes.
 //
 // The m·Σx term of every unit runs on the matrix cores once per row group:
 // A = the slice's unit sums Σx [16 inputs × 16 units] in three bf16 parts,
-// B = m [16 units × 16 rows] in two (an fp16 value splits exactly into two
-// bf16 parts), six v_mfma_f32_16x16x16_bf16 into the row group's
-// accumulator; per unit only acc += s·(Σ c·x) stays on the VALU.
+// B = m [16 units × 16 rows] in its two bf16 parts, six
+// v_mfma_f32_16x16x16_bf16 into the row group's accumulator; per unit only
+// acc += s·(Σ c·x) stays on the VALU.
 template <int RT>
 struct T16Buf {
-    uint32_t cw[RT][4];   // codes: unit g (before the transpose), dword g of units 0..3 (after)
+    uint32_t cw[RT][4];   // codes: dword g of the group's units 0..3, row i
     uint2 sv[RT];         // s of the group's 4 units, row i
-    uint2 mv[RT];         // m of the slice's unit group g, row i (first step of a row group)
+    uint4 mv[RT];         // m (bf16 hi ×4, lo ×4) of the slice's unit group g, row i (first step of a row group)
 };
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -417,7 +420,7 @@ __global__ __launch_bounds__(256) void sb6_t16_gemv_mfma_kernel(BatchArgs A) {
         const uint32_t tt = (uint32_t)(wave * RT + rt);
         oc[rt] = tt * NG * 1024 + lane * 16;
         os[rt] = tt * NG * 128 + i * 8;
-        om[rt] = tt * NG * 128 + gs * 128 + i * 8;
+        om[rt] = tt * NG * 256 + gs * 256 + i * 16;
     }
     auto load = [&](T16Buf<RT>& b, int s, auto slot) {
         constexpr int SLOT = decltype(slot)::value;
@@ -433,9 +436,9 @@ __global__ __launch_bounds__(256) void sb6_t16_gemv_mfma_kernel(BatchArgs A) {
             b.sv[rt] = *reinterpret_cast<const uint2*>(sb + os[rt]);
         }
         if constexpr (SLOT % QPR == 0) {
-            const char* mb = reinterpret_cast<const char*>(A.tm) + (rtile * NG + (u0 >> 2)) * 128;
+            const char* mb = reinterpret_cast<const char*>(A.tm) + (rtile * NG + (u0 >> 2)) * 256;
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) b.mv[rt] = *reinterpret_cast<const uint2*>(mb + om[rt]);
+            for (int rt = 0; rt < RT; ++rt) b.mv[rt] = *reinterpret_cast<const uint4*>(mb + om[rt]);
         }
     };
     using S0 = std::integral_constant<int, 0>;
@@ -475,15 +478,8 @@ __global__ __launch_bounds__(256) void sb6_t16_gemv_mfma_kernel(BatchArgs A) {
             // the row group's m·Σx over the whole slice (units past KW have A = 0)
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
-                bf16x4 bh, bl;
-                const uint32_t mw[2] = {b.mv[rt].x, b.mv[rt].y};
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk) {
-                    const float m = f16f(mw[kk >> 1] >> (16 * (kk & 1)));
-                    const __bf16 h = (__bf16)m;
-                    bh[kk] = h;
-                    bl[kk] = (__bf16)(m - (float)h);
-                }
+                const bf16x4 bh = __builtin_bit_cast(bf16x4, make_uint2(b.mv[rt].x, b.mv[rt].y));
+                const bf16x4 bl = __builtin_bit_cast(bf16x4, make_uint2(b.mv[rt].z, b.mv[rt].w));
 #pragma unroll
                 for (int t = 0; t < NTL; ++t) {
                     f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -496,8 +492,6 @@ __global__ __launch_bounds__(256) void sb6_t16_gemv_mfma_kernel(BatchArgs A) {
                 }
             }
         }
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) transpose4(b.cw[rt][0], b.cw[rt][1], b.cw[rt][2], b.cw[rt][3]);
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             bf16x8 ap[2][NTL][3];
@@ -575,12 +569,18 @@ __global__ __launch_bounds__(256) void sb6_t16_pack_kernel(const uint4* __restri
     const int u = (int)(e - row * NU), NG = NU >> 2, NSB = NU >> 3;
     const int64_t tile = (row >> 4) * NG + (u >> 2);
     const int ri = (int)(row & 15), g = u & 3;
-    tq[tile * 64 + g * 16 + ri] = qblk[e];
+    const uint4 q = qblk[e];
+    const uint32_t qd[4] = {q.x, q.y, q.z, q.w};
+    uint32_t* tqw = reinterpret_cast<uint32_t*>(tq) + tile * 256;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) tqw[(d * 16 + ri) * 4 + g] = qd[d];   // dword d of unit g → lane (ri, d), slot g
     const uint32_t sm = qsqm[e], dd = ddm[row * NSB + (u >> 3)];
     const _Float16 sv = (_Float16)((float)(sm & 0xffu) * f16f(dd));
-    const _Float16 mv = (_Float16)((float)(int8_t)(sm >> 8) * f16f(dd >> 16));
+    const float mv = (float)(_Float16)((float)(int8_t)(sm >> 8) * f16f(dd >> 16));
+    const __bf16 mh = (__bf16)mv, ml = (__bf16)(mv - (float)mh);   // exact: 11 significant bits
     ts[tile * 64 + ri * 4 + g] = __builtin_bit_cast(uint16_t, sv);
-    tm[tile * 64 + ri * 4 + g] = __builtin_bit_cast(uint16_t, mv);
+    tm[tile * 128 + ri * 8 + g] = __builtin_bit_cast(uint16_t, mh);
+    tm[tile * 128 + ri * 8 + 4 + g] = __builtin_bit_cast(uint16_t, ml);
 }
 
 // y[n, row] = epilogue(Σ_ks part[ks, n, row]), slices in order; V
@@ -766,8 +766,8 @@ rwkv_status rwkv_sb6_gemv_batch_t16(const float* x, int64_t N, const uint8_t* tq
                                     const uint16_t* tm, float* y, int64_t OUT, int64_t IN, int64_t out_per,
                                     int epilogue, void* workspace, int64_t workspace_bytes, void* stream) {
     RWKV_REQUIRE(x && tq && ts && tm && y && workspace, RWKV_E_NULL, "sb6_gemv_batch_t16: null buffer");
-    RWKV_REQUIRE((uintptr_t)tq % 16 == 0 && (uintptr_t)ts % 8 == 0 && (uintptr_t)tm % 8 == 0, RWKV_E_SHAPE,
-                 "sb6_gemv_batch_t16: tq must be 16-byte aligned, ts and tm 8-byte");
+    RWKV_REQUIRE((uintptr_t)tq % 16 == 0 && (uintptr_t)ts % 8 == 0 && (uintptr_t)tm % 16 == 0, RWKV_E_SHAPE,
+                 "sb6_gemv_batch_t16: tq and tm must be 16-byte aligned, ts 8-byte");
     BatchArgs a{x, (const uint32_t*)tq, nullptr, nullptr, ts, tm};
     return launch_batch(a, true, N, y, OUT, IN, out_per, epilogue, workspace, workspace_bytes, stream,
                         "sb6_gemv_batch_t16");

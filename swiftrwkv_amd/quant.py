@@ -655,7 +655,7 @@ def rwkvq_sb6_gemv_batch(x, qblk, qsqm, ddm, out_features: int, in_features: int
 
 def rwkvq_sb6_t16(qblk, qsqm, ddm, out_features: int, in_features: int):
     """The 4-bit sb6 weights in the matrix cores' T16 order (rwkv_sb6_t16_pack):
-    (tq uint8 [OUT·IN/2], ts fp16 [OUT·IN/32], tm fp16 [OUT·IN/32]) on the
+    (tq uint8 [OUT·IN/2], ts fp16 [OUT·IN/32], tm bf16 [OUT·IN/16]) on the
     device of qblk, for rwkvq_sb6_gemv_batch_t16."""
     if out_features % 16 or in_features % 256:
         raise ValueError(f"sb6 T16: [{out_features}, {in_features}] (OUT % 16 == 0, IN % 256 == 0)")
@@ -665,7 +665,7 @@ def rwkvq_sb6_t16(qblk, qsqm, ddm, out_features: int, in_features: int):
     dev = qblk.device
     tq = torch.empty(out_features * in_features // 2, dtype=torch.uint8, device=dev)
     ts = torch.empty(out_features * in_features // 32, dtype=torch.float16, device=dev)
-    tm = torch.empty_like(ts)
+    tm = torch.empty(out_features * in_features // 16, dtype=torch.bfloat16, device=dev)
     _lib.call("rwkv_sb6_t16_pack", qblk.data_ptr(), qsqm.data_ptr(), ddm.data_ptr(), out_features, in_features,
               tq.data_ptr(), ts.data_ptr(), tm.data_ptr(), _stream(qblk))
     return tq, ts, tm
@@ -685,12 +685,10 @@ def rwkvq_sb6_gemv_batch_t16(x, tq, ts, tm, out_features: int, in_features: int,
     N = x.shape[0] // K
     if not rwkvq_sb6_gemv_batch_applies(N, out_features, in_features, 0, per):
         raise ValueError(f"sb6 batched GEMV: N={N} [{out_features}, {in_features}] out_per={per} not taken")
-    for t, n, dt in ((tq, out_features * in_features // 2, torch.uint8), (ts, out_features * in_features // 32,
-                                                                        torch.float16), (tm, None, torch.float16)):
-        if not t.is_cuda or t.dtype != dt or not t.is_contiguous() or (n is not None and t.numel() != n):
+    nw = out_features * in_features
+    for t, n, dt in ((tq, nw // 2, torch.uint8), (ts, nw // 32, torch.float16), (tm, nw // 16, torch.bfloat16)):
+        if not t.is_cuda or t.dtype != dt or not t.is_contiguous() or t.numel() != n:
             raise ValueError("sb6 batched GEMV: T16 buffers from rwkvq_sb6_t16 expected")
-    if tm.numel() != ts.numel():
-        raise ValueError("sb6 batched GEMV: T16 buffers from rwkvq_sb6_t16 expected")
     x32 = _aligned(x.to(torch.float32))
     ep = _GEMV_EP[epilogue]
     if out is None:

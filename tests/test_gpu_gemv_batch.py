@@ -90,14 +90,17 @@ def test_fused_group_and_epilogues(orc, D, N):
 
 
 def t16_unpack(tq, ts, tm, OUT, IN):
-    """T16 → (K3 code bytes [OUT, NU·16], s [OUT, NU] fp16, m [OUT, NU] fp16),
+    """T16 → (K3 code bytes [OUT, NU·16], s [OUT, NU] fp16, m [OUT, NU] fp32),
     the inverse of the layout rwkv_sb6_t16_pack documents: per (16-row tile,
-    4-unit group) 1 KiB of codes, byte offset (g·16 + i)·16 = unit 4G + g of
-    row 16r + i; s, m [16 rows][4 units]."""
+    4-unit group) 1 KiB of codes whose 16 bytes at (g·16 + i)·16 are dword g
+    of units 4G..4G+3 of row 16r + i; s [16 rows][4 units]; m [16 rows]
+    [4 high, 4 low] bf16 parts."""
     NU, NG = IN // 32, IN // 128
-    q = tq.reshape(OUT // 16, NG, 4, 16, 16).transpose(0, 3, 1, 2, 4).reshape(OUT, NU * 16)
+    d = tq.view(np.uint32).reshape(OUT // 16, NG, 4, 16, 4)           # [r][G][dword g][row i][unit k]
+    q = d.transpose(0, 3, 1, 4, 2).reshape(OUT, NU, 4).view(np.uint8).reshape(OUT, NU * 16)
     sc = ts.reshape(OUT // 16, NG, 16, 4).transpose(0, 2, 1, 3).reshape(OUT, NU)
-    mc = tm.reshape(OUT // 16, NG, 16, 4).transpose(0, 2, 1, 3).reshape(OUT, NU)
+    mb = tm.reshape(OUT // 16, NG, 16, 2, 4).astype(np.float32)       # [r][G][row][hi/lo][unit]
+    mc = (mb[:, :, :, 0, :] + mb[:, :, :, 1, :]).transpose(0, 2, 1, 3).reshape(OUT, NU)
     return q, sc, mc
 
 
@@ -110,13 +113,13 @@ def test_t16_pack_is_the_k3_weights(orc, OUT, IN):
     rng = np.random.default_rng(OUT + IN)
     qblk, qsqm, ddm = random_k3(OUT, IN, rng)
     tq, ts, tm = Q.rwkvq_sb6_t16(dev(qblk), dev(qsqm), dev(ddm), OUT, IN)
-    q, sc, mc = t16_unpack(tq.cpu().numpy(), ts.cpu().numpy(), tm.cpu().numpy(), OUT, IN)
+    q, sc, mc = t16_unpack(tq.cpu().numpy(), ts.cpu().numpy(), tm.float().cpu().numpy(), OUT, IN)
     assert np.array_equal(q, qblk)
     codes = np.empty((OUT, IN), np.float32)
     qb = qblk.reshape(OUT, IN // 32, 16)
     codes.reshape(OUT, IN // 32, 32)[..., :16] = qb & 0xF
     codes.reshape(OUT, IN // 32, 32)[..., 16:] = qb >> 4
-    w = codes * np.repeat(sc.astype(np.float32), 32, axis=1) + np.repeat(mc.astype(np.float32), 32, axis=1)
+    w = codes * np.repeat(sc.astype(np.float32), 32, axis=1) + np.repeat(mc, 32, axis=1)
     want = orc.sb6_dequant(qblk, qsqm, ddm.view(np.uint16), OUT, IN, 0)
     assert np.array_equal(w.view(np.uint32), want.view(np.uint32))
 
