@@ -75,6 +75,8 @@ _SIGS = {
     "rwkv_sb6_gemv_batch": (I, [P, L, P, P, P, P, L, L, I, L, I, P, L, P]),
     "rwkv_sb6_t16_pack": (I, [P, P, P, L, L, P, P, P, P]),
     "rwkv_sb6_gemv_batch_t16": (I, [P, L, P, P, P, P, L, L, L, I, P, L, P]),
+    "rwkv_sb6_gemv_batch_t16_rows": (I, [P, L, P, P, P, P, L, L, L, I, P]),
+    "rwkv_sb6_gemv_batch_t16_launches": (I, [L, L, L, L]),
     "rwkv_wkv7_seq_fwd_chunked": (I, [P] * 6 + [I, P, P, P, L, L, L, P, L, P]),
     "rwkv_wkv7_seq_fwd_chunked_static": (I, [P] * 6 + [I, P, P, P, L, L, L, P]),
     "rwkv_wkv7_train_fwd": (I, [P] * 6 + [I, P, P, P, P, P, L, L, L, P]),

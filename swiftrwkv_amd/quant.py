@@ -600,15 +600,21 @@ def rwkvq_sb6_gemv_batch_applies(rows: int, out_features: int, in_features: int,
 
 
 def rwkvq_sb6_gemv_batch_prefers(rows: int, out_features: int, in_features: int) -> bool:
-    """Where the batched matrix-core GEMV (its launch pair included) beats the
-    VALU batch kernel (MI355X, graph-timed per launch): 16+ rows of matrices
-    of 2^20+ weights (1024x1024 x16 5.5 vs 6.9 µs, 3072x768 x32 7.8 vs
-    9.1 µs, 2048x8192 x32 19.1 vs 44.0 µs), 8+ rows of 2^22+ weights
-    (4096x1024 x8 6.8 vs 7.3 µs, 6144x2048 x8 10.8 vs 14.8 µs); below that
-    the two are within a few percent (768x768 x32 6.0 vs 5.6 µs) and the
-    VALU kernel keeps its bitwise one-row results."""
+    """Where the batched matrix-core GEMV over T16 weights
+    (rwkv_sb6_gemv_batch_t16, which picks its own kernel) beats the VALU
+    batch kernel (MI355X, graph-timed per call): every batch of 2+ rows for
+    K <= 1024 and <= 8192 rows (the row-owned kernel: 768x768 x2 3.3 vs
+    4.6 µs, 4096x1024 x32 6.4 vs 10.6), matrices of 2^24+ weights at any
+    batch (4096x4096 x2 8.5 vs 10.0), of 2^22+ from 8 rows (2048x2048 x8 7.6
+    vs 7.8) and of any size from 16 rows (768x3072 x16 8.1 vs 8.5); below
+    that the VALU kernel is faster (1024x4096 x4 7.9 vs 8.3 µs) and keeps its
+    bitwise one-row results."""
     n = out_features * in_features
-    return (rows >= 16 and n >= (1 << 20)) or (rows >= 8 and n >= (1 << 22))
+    if rows < 2:
+        return False
+    if in_features <= 1024 and out_features <= 8192:
+        return True
+    return rows >= 16 or (rows >= 8 and n >= (1 << 22)) or n >= (1 << 24)
 
 
 _GEMV_EP = {"store": 0, "add": 1, "relu2": 2}
@@ -673,9 +679,11 @@ def rwkvq_sb6_t16(qblk, qsqm, ddm, out_features: int, in_features: int):
 
 def rwkvq_sb6_gemv_batch_t16(x, tq, ts, tm, out_features: int, in_features: int, out_per: Optional[int] = None,
                              epilogue: str = "store", out: Optional[torch.Tensor] = None,
-                             workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                             workspace: Optional[torch.Tensor] = None, rows_kernel: bool = False) -> torch.Tensor:
     """rwkvq_sb6_gemv_batch over T16 weights (rwkvq_sb6_t16): the same inputs,
-    epilogues and workspace."""
+    epilogues and workspace.  `rows_kernel`: the row-owned kernel alone
+    (rwkv_sb6_gemv_batch_t16_rows: one launch, no workspace), which the
+    default call also picks by itself for matrices of a few thousand rows."""
     per = out_features if out_per is None else out_per
     if x.dim() != 2 or x.shape[1] != in_features:
         raise ValueError(f"sb6 batched GEMV: input {tuple(x.shape)}, expected [N, {in_features}]")
@@ -698,6 +706,10 @@ def rwkvq_sb6_gemv_batch_t16(x, tq, ts, tm, out_features: int, in_features: int,
     elif out.dtype != torch.float32 or tuple(out.shape) != (N, out_features) or not out.is_contiguous() or \
             out.device != x.device:
         raise ValueError(f"sb6 batched GEMV: out must be a contiguous float32 [{N}, {out_features}] tensor")
+    if rows_kernel:
+        _lib.call("rwkv_sb6_gemv_batch_t16_rows", x32.data_ptr(), N, tq.data_ptr(), ts.data_ptr(), tm.data_ptr(),
+                  out.data_ptr(), out_features, in_features, per, ep, _stream(x32))
+        return out
     need = int(_lib.lib().rwkv_sb6_gemv_batch_workspace(N, out_features, in_features, per))
     if workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)

@@ -362,7 +362,8 @@ class X070Decoder:
     def launches_per_token(self, N: int = 1) -> int:
         """Kernel launches of one step of N rows: per layer 2 shift_mix +
         lora_in + tmix_core and the projections (one per sb6 / sym GEMV or
-        fused group, two per chunk of the batched matrix-core GEMV; a dense
+        fused group, one or two per chunk of the batched matrix-core GEMV
+        (rwkv_sb6_gemv_batch_t16_launches); a dense
         one is the library GEMM plus its epilogue's
         elementwise kernels; r / k / v taken one by one at N > 1 add two
         staging copies each; the r/k/v group and lora_in as one launch where
@@ -371,8 +372,10 @@ class X070Decoder:
             if isinstance(q, list):
                 return sum(n(m, ep, N > 1) for m in q)
             chunks = self._batch_chunks(q, N)
-            if chunks is not None:   # partial sums + their reduction per chunk
-                return 2 * len(chunks) + 2 * staged
+            if chunks is not None:   # one (row-owned) or two (K slices + reduction) per chunk
+                L = _lib.lib()
+                return sum(int(L.rwkv_sb6_gemv_batch_t16_launches(n, q.OUT, q.IN, q.out_per)) for n in chunks) + \
+                    2 * staged
             k = 1 + (1 + 2 * (ep == 2) if q.kind == "dense" else 0)
             return k + 2 * staged
         if self._ln_fused(N):   # r/k/v + low-rank, tmix core, o, ffn key, ffn value
@@ -429,8 +432,8 @@ class X070Decoder:
     # Which sb6 projections of a batch take the matrix-core batched GEMV
     # (within fp32 rounding of each row alone) instead of the one-input
     # arithmetic run over the rows (bitwise each row alone): None = where it
-    # is faster (quant.rwkvq_sb6_gemv_batch_prefers: 16+ rows of 2^20+ weights,
-    # 8+ rows of 2^22+),
+    # is faster (quant.rwkvq_sb6_gemv_batch_prefers: 2+ rows for K <= 1024,
+    # 16+ rows of any matrix, 8+ of 2^22+ weights, 2+ of 2^24+),
     # True = wherever it applies (2+ rows), False = never.
     batch_mfma: Optional[bool] = None
 

@@ -169,6 +169,55 @@ def test_t16_fused_group_and_epilogues(D, N):
     assert torch.equal(a, b)
 
 
+# K of 2 unit groups (two of four waves idle), 6 (waves with 2 and 1), 8, 16,
+# 24 (3: an odd count) and 32 per 16-row tile
+@pytest.mark.parametrize("OUT,IN", [(64, 256), (768, 768), (3072, 768), (768, 3072), (1024, 1024), (4096, 1024),
+                                    (1024, 4096), (192, 2048)])
+@pytest.mark.parametrize("N", [2, 8, 16, 17, 32])
+def test_t16_rows_kernel_matches_single_rows_and_oracle(orc, OUT, IN, N):
+    case(f"sb6 batched gemv T16 row-owned {OUT}x{IN} N={N}")
+    rng = np.random.default_rng(11 * OUT + IN + N)
+    qblk, qsqm, ddm = random_k3(OUT, IN, rng)
+    w = (dev(qblk), dev(qsqm), dev(ddm))
+    t = Q.rwkvq_sb6_t16(*w, OUT, IN)
+    x = rng.standard_normal((N, IN)).astype(np.float32)
+    xd = dev(x)
+    yr = host(Q.rwkvq_sb6_gemv_batch_t16(xd, *t, OUT, IN, rows_kernel=True))
+    one = host(singles(xd, w, OUT, IN))
+    worst = max(rel(one[n], yr[n]) for n in range(N))
+    print(f"[gemv batch t16 rows] {OUT}x{IN} N={N}: rel to the one-input kernel {worst:.2e}", flush=True)
+    assert worst < 1e-5
+    want = orc.sb6_gemv_f64(x, qblk, qsqm, ddm.view(np.uint16), OUT, IN, 0)
+    assert rel(want, yr) < 2e-5
+
+
+@pytest.mark.parametrize("D,N", [(768, 8), (1024, 32)])
+def test_t16_rows_kernel_fused_group_and_epilogues(D, N):
+    case(f"sb6 batched gemv T16 row-owned fused 3x{D}x{D} N={N}, epilogues")
+    rng = np.random.default_rng(5 * D + N)
+    qblk, qsqm, ddm = random_k3(3 * D, D, rng)
+    w = (dev(qblk), dev(qsqm), dev(ddm))
+    t = Q.rwkvq_sb6_t16(*w, 3 * D, D)
+    x = dev(rng.standard_normal((3 * N, D)).astype(np.float32))
+    y = Q.rwkvq_sb6_gemv_batch_t16(x, *t, 3 * D, D, out_per=D, rows_kernel=True)
+    assert rel(host(singles(x, w, 3 * D, D, out_per=D)), host(y)) < 1e-5
+    t1 = Q.rwkvq_sb6_t16(w[0][:D], w[1][:D], w[2][:D], D, D)
+    xm = dev(rng.standard_normal((N, D)).astype(np.float32))
+    base = dev(rng.standard_normal((N, D)).astype(np.float32))
+    single = singles(xm, (w[0][:D], w[1][:D], w[2][:D]), D, D)
+    y_add = Q.rwkvq_sb6_gemv_batch_t16(xm, *t1, D, D, epilogue="add", out=base.clone(), rows_kernel=True)
+    assert rel(host(base + single), host(y_add)) < 1e-5
+    y_r2 = Q.rwkvq_sb6_gemv_batch_t16(xm, *t1, D, D, epilogue="relu2", rows_kernel=True)
+    assert rel(host(torch.relu(single) ** 2), host(y_r2)) < 2e-5
+    a = Q.rwkvq_sb6_gemv_batch_t16(xm, *t1, D, D, rows_kernel=True)
+    b = Q.rwkvq_sb6_gemv_batch_t16(xm, *t1, D, D, rows_kernel=True)
+    assert torch.equal(a, b)
+    # rows of other inputs untouched: the kernel stores inputs < N only
+    out = torch.full((N, D), 7.0, device=DEV)
+    Q.rwkvq_sb6_gemv_batch_t16(xm[:N - 1].contiguous(), *t1, D, D, out=out[:N - 1], rows_kernel=True)
+    assert torch.all(out[N - 1] == 7.0)
+
+
 def test_contract_and_declines():
     case("sb6 batched gemv: applicability, workspace, counters")
     L = _lib.lib()
@@ -208,7 +257,7 @@ def test_decoder_batch_rows_match_each_row_alone():
     p = syn.x070_dense_params(tiny, seed=13, lora_dtype=np.float32)
     proj = syn.x070_projections(tiny, nthreads=4)
     dec = X070Decoder(tiny.n_layer, tiny.n_embd, tiny.ffn, tiny.vocab, p, proj, DEV)
-    dec.batch_mfma = True   # the tiny matrices are below the size where it is faster
+    dec.batch_mfma = True   # the matrix-core path for every projection, whatever the size rule
     rng = np.random.default_rng(13)
     assert dec._batch_chunks(dec.proj["head.weight"], 40) == [20, 20]
     for N in (9, 24):

@@ -237,10 +237,11 @@ def test_decode_steps_match_oracle(tiny, decoder, N):
         assert c["sb6_gemv"] == 4 * (3 * Lr + 1)      # o_proj, ffn key, ffn value, head
         assert c["sb6_fused"] == 4 * Lr               # r/k/v
     # batch 1: each layer's r/k/v GEMV and lora_in share one launch; the
-    # batched matrix-core GEMV is two launches per chunk of <= 32 rows
+    # batched matrix-core GEMV is one launch per chunk of <= 32 rows here
+    # (the row-owned kernel: every K of this shape is <= 1024)
     if decoder._batch_chunks(decoder.proj["head.weight"], N):
         ch = (N + 31) // 32
-        assert decoder.launches_per_token(N) == (4 + 4 * 2 * ch) * Lr + 2 + 2 * ch
+        assert decoder.launches_per_token(N) == (4 + 4 * ch) * Lr + 2 + ch
     else:
         assert decoder.launches_per_token(N) == (5 if N == 1 else 8) * Lr + 3
 
@@ -389,9 +390,10 @@ def test_decode_graph_replay_bitwise(tiny, decoder, N):
 
 def test_generate_batch_rows_equal_prompts_alone(decoder):
     # prefillBatch / generateBatch (BatchGenerate.swift:37-116) with the
-    # greedy choice: every row of the batch is bitwise its prompt alone (the
-    # batched GEMVs and row kernels are row-invariant; 4 heads keep the
-    # four-rows-per-wave WKV layout at every batch here)
+    # greedy choice: every row of the batch within 1e-5 of its prompt alone
+    # (BatchGenerateTests.swift:56-61; a batch's projections run on the
+    # matrix cores, one row alone on the one-input kernel, so not bitwise)
+    # and the same greedy tokens (BatchGenerateTests.swift:69-88)
     case("generate_batch tiny")
     rng = np.random.default_rng(5)
     prompts = [rng.integers(0, TINY.vocab, n).tolist() for n in (3, 5, 1)]
@@ -399,9 +401,9 @@ def test_generate_batch_rows_equal_prompts_alone(decoder):
     assert logits.shape == (3, TINY.vocab)
     for i, p in enumerate(prompts):
         li, si = decoder.prefill_batch([p])
-        assert torch.equal(logits[i], li[0]), i
+        assert rel(li[0].cpu().numpy(), logits[i].cpu().numpy()) < 1e-5, i
         for a, b in ((st.wkv, si.wkv), (st.tmix_prev, si.tmix_prev), (st.cmix_prev, si.cmix_prev)):
-            assert torch.equal(a[:, i], b[:, 0]), i
+            assert rel(b[:, 0].cpu().numpy(), a[:, i].cpu().numpy()) < 1e-5, i
     out = decoder.generate_batch(prompts, 6)
     assert [len(o) for o in out] == [6, 6, 6]
     assert out == [decoder.generate_batch([p], 6)[0] for p in prompts]
