@@ -601,16 +601,17 @@ def rwkvq_sb6_gemv_batch_applies(rows: int, out_features: int, in_features: int,
 
 def rwkvq_sb6_gemv_batch_prefers(rows: int, out_features: int, in_features: int) -> bool:
     """Where the batched matrix-core GEMV over T16 weights
-    (rwkv_sb6_gemv_batch_t16, which picks its own kernel) beats the VALU
-    batch kernel (MI355X, graph-timed per call): every batch of 2+ rows for
-    K <= 1024 and <= 8192 rows (the row-owned kernel: 768x768 x2 3.3 vs
-    4.6 µs, 4096x1024 x32 6.4 vs 10.6), matrices of 2^24+ weights at any
-    batch (4096x4096 x2 8.5 vs 10.0), of 2^22+ from 8 rows (2048x2048 x8 7.6
-    vs 7.8) and of any size from 16 rows (768x3072 x16 8.1 vs 8.5); below
-    that the VALU kernel is faster (1024x4096 x4 7.9 vs 8.3 µs) and keeps its
-    bitwise one-row results."""
+    (rwkv_sb6_gemv_batch_t16, which picks its own kernel) takes a batch
+    instead of the VALU batch kernel.  Up to 4 rows the VALU kernel stays:
+    each of its rows is bitwise that row alone (the matrix cores agree to
+    fp32 rounding only), at a cost of at most ~1.3 µs per call.  From 5
+    rows, where the matrix cores are faster (MI355X, graph-timed per call):
+    K <= 1024 and <= 8192 rows (the row-owned kernel: 768x768 x8 3.5 vs
+    4.6 µs, 4096x1024 x32 6.4 vs 10.6), 2^24+ weights (4096x4096 x8 8.5 vs
+    12.7), 2^22+ from 8 rows (2048x2048 x8 7.6 vs 7.8) and any size from 16
+    rows (768x3072 x16 8.1 vs 8.5)."""
     n = out_features * in_features
-    if rows < 2:
+    if rows <= 4:
         return False
     if in_features <= 1024 and out_features <= 8192:
         return True

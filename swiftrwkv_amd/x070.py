@@ -432,8 +432,8 @@ class X070Decoder:
     # Which sb6 projections of a batch take the matrix-core batched GEMV
     # (within fp32 rounding of each row alone) instead of the one-input
     # arithmetic run over the rows (bitwise each row alone): None = where it
-    # is faster (quant.rwkvq_sb6_gemv_batch_prefers: 2+ rows for K <= 1024,
-    # 16+ rows of any matrix, 8+ of 2^22+ weights, 2+ of 2^24+),
+    # is faster and the batch has 5+ rows (quant.rwkvq_sb6_gemv_batch_prefers:
+    # K <= 1024, or 16+ rows of any matrix, 8+ of 2^22+ weights, 2^24+),
     # True = wherever it applies (2+ rows), False = never.
     batch_mfma: Optional[bool] = None
 

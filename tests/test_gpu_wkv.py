@@ -212,7 +212,8 @@ def test_tail_matches_oracle(orc):
         K.wkv_tail(dev(wkv), dev(r), dev(k), dev(v), dev(rk), dev(lnw), dev(lnb), dev(g), H, 48, rows=N)
 
 
-@pytest.mark.parametrize("B,H", [(1, 12), (4, 3), (2, 32), (2, 128)])
+# B·H < 256: the four-row layout; from 256 the sixteen-row one
+@pytest.mark.parametrize("B,H", [(1, 12), (4, 3), (2, 32), (2, 128), (3, 129), (32, 12), (16, 64)])
 def test_step_tail_equals_step_then_tail_bitwise(orc, B, H):
     case(f"fused step+tail B={B} H={H}")
     rng = np.random.default_rng(B * 100 + H)

@@ -390,10 +390,10 @@ def test_decode_graph_replay_bitwise(tiny, decoder, N):
 
 def test_generate_batch_rows_equal_prompts_alone(decoder):
     # prefillBatch / generateBatch (BatchGenerate.swift:37-116) with the
-    # greedy choice: every row of the batch within 1e-5 of its prompt alone
-    # (BatchGenerateTests.swift:56-61; a batch's projections run on the
-    # matrix cores, one row alone on the one-input kernel, so not bitwise)
-    # and the same greedy tokens (BatchGenerateTests.swift:69-88)
+    # greedy choice: every row of the batch is bitwise its prompt alone (the
+    # reference bounds it at 1e-5, BatchGenerateTests.swift:56-61; batches of
+    # up to 4 rows keep the row-invariant VALU GEMVs and row kernels; 4 heads
+    # keep the four-rows-per-wave WKV layout at every batch here)
     case("generate_batch tiny")
     rng = np.random.default_rng(5)
     prompts = [rng.integers(0, TINY.vocab, n).tolist() for n in (3, 5, 1)]
@@ -401,9 +401,9 @@ def test_generate_batch_rows_equal_prompts_alone(decoder):
     assert logits.shape == (3, TINY.vocab)
     for i, p in enumerate(prompts):
         li, si = decoder.prefill_batch([p])
-        assert rel(li[0].cpu().numpy(), logits[i].cpu().numpy()) < 1e-5, i
+        assert torch.equal(logits[i], li[0]), i
         for a, b in ((st.wkv, si.wkv), (st.tmix_prev, si.tmix_prev), (st.cmix_prev, si.cmix_prev)):
-            assert rel(b[:, 0].cpu().numpy(), a[:, i].cpu().numpy()) < 1e-5, i
+            assert torch.equal(a[:, i], b[:, 0]), i
     out = decoder.generate_batch(prompts, 6)
     assert [len(o) for o in out] == [6, 6, 6]
     assert out == [decoder.generate_batch([p], 6)[0] for p in prompts]
