@@ -241,16 +241,17 @@ rwkv_status rwkv_sb6_gemv_batch_t16(const float* x, int64_t N, const uint8_t* tq
                                     int epilogue, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Kernel launches one rwkv_sb6_gemv_batch_t16 call makes: 1 where it takes
- * the row-owned kernel (K <= 1024 and OUT <= 8192), 2 (K slices and their
- * reduction) otherwise, 0 where it does not apply.  For launch accounting of
+ * the row-owned kernel (OUT·K <= 2^23 for K <= 2048; OUT·K·ceil(N/16) < 2^23
+ * for K <= 4096), 2 (K slices and their reduction) otherwise, 0 where it
+ * does not apply.  For launch accounting of
  * captured graphs; no counterpart in the reference. */
 int rwkv_sb6_gemv_batch_t16_launches(int64_t N, int64_t OUT, int64_t IN, int64_t out_per);
 
 /* rwkv_sb6_gemv_batch_t16 by the row-owned kernel alone: one workgroup per
  * 16-row tile whose waves split K and sum their partial products in LDS, so
  * one launch and no workspace.  Same shapes, epilogues and accuracy; for
- * matrices of a few thousand rows, where K slices leave each workgroup a few
- * units of work (rwkv_sb6_gemv_batch_t16 chooses it there itself).  The
+ * matrices of a few million weights, where K slices leave each workgroup a
+ * few units of work (rwkv_sb6_gemv_batch_t16 chooses it there itself).  The
  * batched counterpart of rwkvqSb6GEMV (RwkvqSb6GEMV.swift:159-190). */
 rwkv_status rwkv_sb6_gemv_batch_t16_rows(const float* x, int64_t N, const uint8_t* tq, const uint16_t* ts,
                                          const uint16_t* tm, float* y, int64_t OUT, int64_t IN, int64_t out_per,

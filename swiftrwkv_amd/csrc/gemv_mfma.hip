@@ -574,10 +574,11 @@ struct RowBuf {
     float4 xa[4], xb[4];   // input i of the tile, unit uu: columns 4g..4g+3 and 16+4g..16+4g+3
 };
 
-// ONE: every wave has at most one unit group (K ≤ W groups): no loop, and
-// few enough registers for two workgroups per CU.
-template <int W, bool ONE>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(ONE ? 4 : 1)))
+// SG > 0: every wave has at most SG unit groups (K ≤ SG·W groups), all
+// loaded up front, no loop (SG = 1 leaves few enough registers for several
+// workgroups per CU); SG = 0: any K, two groups in flight.
+template <int W, int SG>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SG == 1 ? 4 : 1)))
 void sb6_t16_gemv_rows_kernel(BatchArgs A, float* __restrict__ y, int ep) {
     __shared__ f32x4 red[W][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, i = lane & 15;
@@ -640,12 +641,28 @@ void sb6_t16_gemv_rows_kernel(BatchArgs A, float* __restrict__ y, int ep) {
             for (int e = 0; e < 4; ++e) acc[e] = fmaf(mu, sx[e], fmaf(sv, d[e], acc[e]));
         }
     };
-    if (ONE || S == 1) {
+    if constexpr (SG == 1) {
         if (S == 1) {
             RowBuf b0;
             load(b0, 0);
             step(b0);
         }
+    } else if constexpr (SG == 2) {
+        if (S == 2) {
+            RowBuf b0, b1;
+            load(b0, 0);
+            load(b1, 1);
+            step(b0);
+            step(b1);
+        } else if (S == 1) {
+            RowBuf b0;
+            load(b0, 0);
+            step(b0);
+        }
+    } else if (S == 1) {
+        RowBuf b0;
+        load(b0, 0);
+        step(b0);
     } else if (S > 1) {
         // two buffers, the next group's loads in flight while one is
         // multiplied; loads past the last group reload it (clamped, unused),
@@ -785,13 +802,20 @@ bool plan_batch(int64_t N, int64_t OUT, int64_t IN, int64_t out_per, BatchPlan& 
     return p.KS <= KS_MAX && p.grid() <= INT32_MAX;
 }
 
-// The row-owned kernel: 8 waves per (16-row, 16-input) tile (4 where K has
-// at most 4 unit groups).  Taken by the T16 entry for K ≤ 1024 and ≤ 8192
-// rows, where it measured 1.5-3 µs faster per call than K slices plus their
-// reduction (1024x1024 x32 4.3 vs 6.5 µs, 8192x1024 x32 10.4 vs 12.2); with
-// more rows the workgroups' own input splits (every one converts its whole
-// K) outweigh the saved launch (16384x768 x32 14.9 vs 14.4 µs).
-bool rows_kernel_taken(int64_t OUT, int64_t IN) { return IN <= 1024 && OUT <= 8192; }
+// The row-owned kernel: 4, 8 or 16 waves per (16-row, 16-input) tile with
+// at most two unit groups each up to K = 4096; beyond, 8 waves that loop.
+// Taken by the T16 entry up to 2^23 weights for K ≤ 2048, and up to 2^23
+// per 16-input tile for K ≤ 4096, where it measured faster per call than K
+// slices plus their reduction (graph-timed: 1024x1024 x32 4.3 vs 6.5 µs,
+// 2048x2048 x32 6.5 vs 8.7, 768x3072 x32 8.2 vs 9.9, 1024x4096 x8 8.1 vs 8.9);
+// past it every workgroup's conversion of its whole K into bf16 parts
+// outweighs the saved launch (1024x4096 x32 10.2 vs 9.4, 4096x4096 x16 10.7
+// vs 9.3, 8192x2048 x16 10.9 vs 9.6).
+bool rows_kernel_taken(int64_t N, int64_t OUT, int64_t IN) {
+    const int64_t w = OUT * IN;
+    if (IN <= 2048) return w <= ((int64_t)1 << 23);
+    return IN <= 4096 && w * ((N + 15) / 16) < ((int64_t)1 << 23);
+}
 
 rwkv_status launch_rows(BatchArgs a, int64_t N, float* y, int64_t OUT, int64_t IN, int64_t out_per, int epilogue,
                         void* stream, const char* who) {
@@ -814,11 +838,15 @@ rwkv_status launch_rows(BatchArgs a, int64_t N, float* y, int64_t OUT, int64_t I
     const dim3 grid((unsigned)(OUT / 16), (unsigned)((N + 15) / 16));
     const int64_t NG = IN / 128;
     if (NG <= 4)
-        rwkv::launch(sb6_t16_gemv_rows_kernel<4, true>, grid, dim3(256), st, a, y, epilogue);
+        rwkv::launch(sb6_t16_gemv_rows_kernel<4, 1>, grid, dim3(256), st, a, y, epilogue);
     else if (NG <= 8)
-        rwkv::launch(sb6_t16_gemv_rows_kernel<8, true>, grid, dim3(512), st, a, y, epilogue);
+        rwkv::launch(sb6_t16_gemv_rows_kernel<8, 1>, grid, dim3(512), st, a, y, epilogue);
+    else if (NG <= 16)
+        rwkv::launch(sb6_t16_gemv_rows_kernel<16, 1>, grid, dim3(1024), st, a, y, epilogue);
+    else if (NG <= 32)
+        rwkv::launch(sb6_t16_gemv_rows_kernel<16, 2>, grid, dim3(1024), st, a, y, epilogue);
     else
-        rwkv::launch(sb6_t16_gemv_rows_kernel<8, false>, grid, dim3(512), st, a, y, epilogue);
+        rwkv::launch(sb6_t16_gemv_rows_kernel<8, 0>, grid, dim3(512), st, a, y, epilogue);
     RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "%s: launch failed", who);
     rwkv::counters().sb6_batch.fetch_add(1);
     rwkv::clear_error();
@@ -838,7 +866,7 @@ rwkv_status launch_batch(BatchArgs a, bool t16, int64_t N, float* y, int64_t OUT
                  "%s: x and the workspace must be 16-byte aligned", who);
     RWKV_REQUIRE(workspace_bytes >= p.ws_bytes, RWKV_E_SHAPE, "%s: workspace %lld bytes, needs %lld", who,
                  (long long)workspace_bytes, (long long)p.ws_bytes);
-    if (t16 && rows_kernel_taken(OUT, IN))
+    if (t16 && rows_kernel_taken(N, OUT, IN))
         return launch_rows(a, N, y, OUT, IN, out_per, epilogue, stream, who);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     a.part = (float*)workspace;
@@ -898,7 +926,7 @@ int rwkv_sb6_gemv_batch_applies(int64_t N, int64_t OUT, int64_t IN, int xbits, i
 int rwkv_sb6_gemv_batch_t16_launches(int64_t N, int64_t OUT, int64_t IN, int64_t out_per) {
     BatchPlan p;
     if (!plan_batch(N, OUT, IN, out_per, p)) return 0;
-    return rows_kernel_taken(OUT, IN) ? 1 : 2;
+    return rows_kernel_taken(N, OUT, IN) ? 1 : 2;
 }
 
 int64_t rwkv_sb6_gemv_batch_workspace(int64_t N, int64_t OUT, int64_t IN, int64_t out_per) {

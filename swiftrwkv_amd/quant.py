@@ -606,14 +606,15 @@ def rwkvq_sb6_gemv_batch_prefers(rows: int, out_features: int, in_features: int)
     each of its rows is bitwise that row alone (the matrix cores agree to
     fp32 rounding only), at a cost of at most ~1.3 µs per call.  From 5
     rows, where the matrix cores are faster (MI355X, graph-timed per call):
-    K <= 1024 and <= 8192 rows (the row-owned kernel: 768x768 x8 3.5 vs
-    4.6 µs, 4096x1024 x32 6.4 vs 10.6), 2^24+ weights (4096x4096 x8 8.5 vs
-    12.7), 2^22+ from 8 rows (2048x2048 x8 7.6 vs 7.8) and any size from 16
-    rows (768x3072 x16 8.1 vs 8.5)."""
+    wherever the entry takes its one-launch row-owned kernel
+    (rwkv_sb6_gemv_batch_t16_launches == 1; 768x768 x8 3.5 vs 4.6 µs,
+    768x3072 x8 6.5 vs 6.9, 4096x1024 x32 6.4 vs 10.6), 2^24+ weights
+    (4096x4096 x8 8.5 vs 12.7), 2^22+ from 8 rows (2048x8192 x8 9.3 vs 15.2)
+    and any size from 16 rows (768x3072 x16 8.1 vs 8.5)."""
     n = out_features * in_features
     if rows <= 4:
         return False
-    if in_features <= 1024 and out_features <= 8192:
+    if _lib.lib().rwkv_sb6_gemv_batch_t16_launches(min(rows, 32), out_features, in_features, out_features) == 1:
         return True
     return rows >= 16 or (rows >= 8 and n >= (1 << 22)) or n >= (1 << 24)
 
