@@ -65,8 +65,9 @@ def parse():
     p.add_argument("--skip-wkv", action="store_true")
     p.add_argument("--skip-more", action="store_true", help="skip batched / 7B-class decode and the prefill pass")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--mode", choices=["bench", "kernels", "e2e"], default="bench",
-                   help="kernels: run each dominant kernel alone (for rocprofv3 counter passes)")
+    p.add_argument("--mode", choices=["bench", "kernels", "e2e", "batch"], default="bench",
+                   help="kernels: run each dominant kernel alone (for rocprofv3 counter passes); "
+                        "e2e / batch: x070 decode tokens / batched GEMV + WKV decode steps only (for kernel traces)")
     return p.parse_args()
 
 
@@ -924,6 +925,23 @@ def profile_x070(dev, tokens=20):
         torch.cuda.empty_cache()
 
 
+def profile_batch(dev, steps=20):
+    """Batched decode steps (GEMV + WKV chain, HIP graph replays) of the 0.1B
+    (batch 8, 32), 0.4B (8, 32) and 7B-class (16) shapes, for kernel traces;
+    the shapes run in that order."""
+    import torch
+    from swiftrwkv_amd import synthetic as syn
+
+    nthreads = min(16, os.cpu_count() or 1)
+    for shape, copies, batches in ((syn.X070_0B1, 6, (8, 32)), (syn.X070_0B4, 2, (8, 32)), (syn.X070_7B, 1, (16,))):
+        model = DecodeModel(shape, copies, dev, nthreads=nthreads, share_layers=shape is syn.X070_7B)
+        for B in batches:
+            _, wall, _ = run_decode(model, dev, B, steps, 2, copies)
+            log(f"batched decode {shape.name} batch {B}: {wall * 1e3 / steps:.3f} ms per step")
+        del model
+        torch.cuda.empty_cache()
+
+
 def headline_1b5(args, dev):
     """The 1.5B decode: the whole x070 step per token (the headline), the
     GEMV + WKV chain of the same token, the GEMV roofline and the CPU baseline."""
@@ -1000,6 +1018,9 @@ def main():
         return
     if args.mode == "e2e":
         profile_x070(dev)
+        return
+    if args.mode == "batch":
+        profile_batch(dev)
         return
     head = headline_1b5(args, dev)
     extra = {"decode_1.5B_gemv_wkv_chain_batch1": head["chain"]}
