@@ -214,6 +214,10 @@ class X070Decoder:
         # T16 copies (quant.rwkvq_sb6_t16) of the sb6 projections that take
         # the batched matrix-core GEMV, made with the buffers of a batch size
         self._t16: Dict[int, tuple] = {}
+        # (projection, rows, batch_mfma) → (chunk sizes, workspace bytes) or None:
+        # the batched-GEMV decision, made once (eager steps pay per ctypes call)
+        self._plans: Dict[tuple, Optional[tuple]] = {}
+        self._t16p: Dict[int, tuple] = {}   # device addresses of the T16 copies
 
     @classmethod
     def from_sidecar(cls, sc, device=None, param_dtype=torch.float16) -> "X070Decoder":
@@ -458,24 +462,43 @@ class X070Decoder:
             return None
         return sizes
 
+    def _batch_plan(self, q, N: int) -> Optional[tuple]:
+        """(_batch_chunks, the workspace bytes they need), or None; memoised."""
+        key = (id(q), N, self.batch_mfma)
+        if key not in self._plans:
+            sizes = self._batch_chunks(q, N)
+            plan = None
+            if sizes is not None:
+                L = _lib.lib()
+                plan = (sizes, max(int(L.rwkv_sb6_gemv_batch_workspace(n, q.OUT, q.IN, q.out_per)) for n in set(sizes)))
+            self._plans[key] = plan
+        return self._plans[key]
+
     def _run_batch(self, q: Proj, x: torch.Tensor, y: torch.Tensor, ep: int, N: int, s) -> bool:
         """rwkv_sb6_gemv_batch_t16 over chunks of at most 32 rows, on the
         projection's T16 copy; False where it does not apply."""
-        sizes = self._batch_chunks(q, N)
-        if sizes is None:
+        plan = self._batch_plan(q, N)
+        if plan is None:
             return False
+        sizes, need = plan
         t16 = self._t16.get(id(q))
         if t16 is None:   # (launch makes them with its buffers, before any capture)
             t16 = self._t16[id(q)] = Q.rwkvq_sb6_t16(*q.bufs, q.OUT, q.IN)
+        tp = self._t16p.get(id(q))
+        if tp is None:
+            tp = self._t16p[id(q)] = tuple(b.data_ptr() for b in t16)
         L = _lib.lib()
         K = q.OUT // q.out_per
-        ws = self._batch_ws(max(int(L.rwkv_sb6_gemv_batch_workspace(n, q.OUT, q.IN, q.out_per)) for n in set(sizes)))
-        x2, y2 = x.reshape(N * K, q.IN), y.reshape(N, q.OUT)
+        ws = self._batch_ws(need)
+        if not x.is_contiguous():
+            x = x.contiguous()
+        # chunk n0 starts at input row n0: plain pointer offsets (x [N, K, IN],
+        # y [N, OUT] fp32, contiguous), no views per call
+        xp, yp, wp, wn = x.data_ptr(), y.data_ptr(), ws.data_ptr(), ws.numel()
         n0 = 0
         for n in sizes:
-            _lib.check(L.rwkv_sb6_gemv_batch_t16(x2[n0 * K].data_ptr(), n, *[b.data_ptr() for b in t16],
-                                                 y2[n0].data_ptr(), q.OUT, q.IN, q.out_per, ep, ws.data_ptr(),
-                                                 ws.numel(), s))
+            _lib.check(L.rwkv_sb6_gemv_batch_t16(xp + 4 * n0 * K * q.IN, n, *tp, yp + 4 * n0 * q.OUT, q.OUT, q.IN,
+                                                 q.out_per, ep, wp, wn, s))
             n0 += n
         return True
 
