@@ -400,6 +400,31 @@ def test_lora_orientation_naming_rule():
     assert not quant.is_raw_lora_world("blocks.0.ffn.w1")
 
 
+def test_batched_gemv_kernel_choice_rules():
+    """The T16 batched GEMV's one-launch row-owned kernel: up to 2^23 weights for
+    K <= 2048, up to 2^23 per 16-input tile for K <= 4096; K slices plus their
+    reduction (two launches) elsewhere; 0 where the batched GEMV does not apply.
+    The decoder's preference for it keeps batches of up to 4 rows on the VALU
+    kernel (bitwise each row alone)."""
+    from swiftrwkv_amd import _lib
+    L = _lib.lib()
+    launches = lambda N, OUT, IN, per=None: int(L.rwkv_sb6_gemv_batch_t16_launches(N, OUT, IN, per or OUT))
+    assert launches(32, 1024, 1024) == 1
+    assert launches(32, 8192, 1024) == 1            # 2^23 weights
+    assert launches(32, 16384, 768) == 2
+    assert launches(16, 2048, 2048) == 1 and launches(32, 4096, 2048) == 1
+    assert launches(16, 8192, 2048) == 2
+    assert launches(8, 1024, 4096) == 1 and launches(16, 1024, 4096) == 1
+    assert launches(17, 1024, 4096) == 2            # two input tiles: 2^23, not below
+    assert launches(16, 4096, 4096) == 2 and launches(16, 2048, 8192) == 2
+    assert launches(8, 3 * 768, 768, 768) == 1      # fused r/k/v group
+    assert launches(1, 768, 768) == 0 and launches(33, 768, 768) == 0 and launches(8, 768, 800) == 0
+    pref = quant.rwkvq_sb6_gemv_batch_prefers
+    assert not pref(4, 768, 768) and pref(5, 768, 768)
+    assert not pref(4, 4096, 4096) and pref(8, 4096, 4096)
+    assert not pref(8, 256, 8192) and pref(16, 256, 8192)   # 2^21 weights, K past the row-owned kernel
+
+
 def test_x070_launch_count():
     """launches_per_token over mixed projection kinds: a fused sb6 / sym GEMV
     is one launch, a dense projection its GEMM plus epilogue kernels (store or
