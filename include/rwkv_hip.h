@@ -241,9 +241,9 @@ rwkv_status rwkv_sb6_gemv_batch_t16(const float* x, int64_t N, const uint8_t* tq
                                     int epilogue, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Kernel launches one rwkv_sb6_gemv_batch_t16 call makes: 1 where it takes
- * the row-owned kernel (OUT·K <= 2^23 for K <= 2048; OUT·K·ceil(N/16) < 2^23
- * for K <= 4096), 2 (K slices and their reduction) otherwise, 0 where it
- * does not apply.  For launch accounting of
+ * the row-owned kernel (OUT·K <= 2^24 and K <= 3072; or K <= 4096 with
+ * (OUT/16)·ceil(N/16) <= 64 or > 256), 2 (K slices and their reduction)
+ * otherwise, 0 where it does not apply.  For launch accounting of
  * captured graphs; no counterpart in the reference. */
 int rwkv_sb6_gemv_batch_t16_launches(int64_t N, int64_t OUT, int64_t IN, int64_t out_per);
 

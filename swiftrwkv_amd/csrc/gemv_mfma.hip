@@ -567,36 +567,41 @@ __global__ __launch_bounds__(256) void sb6_t16_gemv_mfma_kernel(BatchArgs A) {
 // workspace.  Per unit the same MFMAs give Σ c·x (B = the codes) and Σ x
 // (B = ones) of the lane's four inputs, so acc += s·Σ c·x + m·Σ x is four
 // fmas each.
+template <int RT>
 struct RowBuf {
-    uint4 cw;          // codes: dword g of the group's units 0..3, row i
-    uint2 sv;          // s of the 4 units, row i
-    uint4 mv;          // m of the 4 units (bf16 high ×4, low ×4), row i
+    uint4 cw[RT];      // codes: dword g of the group's units 0..3, row i of row tile rt
+    uint2 sv[RT];      // s of the 4 units, row i
+    uint4 mv[RT];      // m of the 4 units (bf16 high ×4, low ×4), row i
     float4 xa[4], xb[4];   // input i of the tile, unit uu: columns 4g..4g+3 and 16+4g..16+4g+3
 };
 
-// SG > 0: every wave has at most SG unit groups (K ≤ SG·W groups), all
-// loaded up front, no loop (SG = 1 leaves few enough registers for several
-// workgroups per CU); SG = 0: any K, two groups in flight.
-template <int W, int SG>
+// RT row tiles per workgroup share its waves' inputs, their bf16 parts and
+// unit sums.  SG > 0: every wave has at most SG unit groups (K ≤ SG·W
+// groups), all loaded up front, no loop (SG = 1 leaves few enough registers
+// for several workgroups per CU); SG = 0: any K, two groups in flight.
+template <int W, int SG, int RT>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(SG == 1 ? 4 : 1)))
 void sb6_t16_gemv_rows_kernel(BatchArgs A, float* __restrict__ y, int ep) {
-    __shared__ f32x4 red[W][64];
+    __shared__ f32x4 red[W][RT][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, i = lane & 15;
-    const int64_t rtile = blockIdx.x;
-    const int64_t row0 = rtile * 16;
+    const int64_t rtile0 = (int64_t)blockIdx.x * RT;
+    const int64_t row0 = rtile0 * 16;
     const int n0 = 16 * (int)blockIdx.y, NL = min(16, A.N - n0);   // inputs of this tile
-    const int mat = (int)(row0 / A.out_per);
+    const int mat = (int)(row0 / A.out_per);   // (out_per % (16·RT) == 0: one matrix)
     const int NG = A.IN >> 7;
     const int S = wave < NG ? (NG - 1 - wave) / W + 1 : 0;   // unit groups of this wave
     // inputs past the tile's last read that one, never stored
     const float* xrow = A.x + ((int64_t)(n0 + min(i, NL - 1)) * A.NK + mat) * A.IN + 4 * g;
-    auto load = [&](RowBuf& b, int s) {
+    auto load = [&](RowBuf<RT>& b, int s) {
         s = min(s, S - 1);
         const int q = wave + s * W;
-        const int64_t tile = rtile * NG + q;
-        b.cw = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.q) + tile * 1024 + lane * 16);
-        b.sv = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(A.ts) + tile * 128 + i * 8);
-        b.mv = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.tm) + tile * 256 + i * 16);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const int64_t tile = (rtile0 + rt) * NG + q;
+            b.cw[rt] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.q) + tile * 1024 + lane * 16);
+            b.sv[rt] = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(A.ts) + tile * 128 + i * 8);
+            b.mv[rt] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(A.tm) + tile * 256 + i * 16);
+        }
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) {
             const float* src = xrow + (4 * q + uu) * 32;
@@ -604,20 +609,14 @@ void sb6_t16_gemv_rows_kernel(BatchArgs A, float* __restrict__ y, int ep) {
             b.xb[uu] = *reinterpret_cast<const float4*>(src + 16);
         }
     };
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
     const __bf16 one = (__bf16)1.0f;
     const bf16x8 ones = bf16x8{one, one, one, one, one, one, one, one};
-    auto step = [&](const RowBuf& b) {
-        const uint32_t cw[4] = {b.cw.x, b.cw.y, b.cw.z, b.cw.w};
-        const uint32_t mw[4] = {b.mv.x, b.mv.y, b.mv.z, b.mv.w};
+    auto step = [&](const RowBuf<RT>& b) {
 #pragma unroll
         for (int uu = 0; uu < 4; ++uu) {
-            const bf16x8 bc = codes_bf16(cw[uu]);
-            const uint32_t s2 = uu < 2 ? b.sv.x : b.sv.y;
-            const float sv = f16f(s2 >> (16 * (uu & 1)));
-            // m = high + low bf16 parts, exact in fp32
-            const uint32_t mh = mw[uu >> 1] >> (16 * (uu & 1)), ml = mw[2 + (uu >> 1)] >> (16 * (uu & 1));
-            const float mu = __uint_as_float(mh << 16) + __uint_as_float(ml << 16);
             const float4 xa = b.xa[uu], xb = b.xb[uu];
             const float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
             bf16x8 ap[3];
@@ -631,43 +630,54 @@ void sb6_t16_gemv_rows_kernel(BatchArgs A, float* __restrict__ y, int ep) {
                 ap[2][e] = (__bf16)(r1 - (float)h2);
             }
             const f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
-            f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap[0], bc, z, 0, 0, 0);
             f32x4 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap[0], ones, z, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap[1], bc, d, 0, 0, 0);
             sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap[1], ones, sx, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap[2], bc, d, 0, 0, 0);
             sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap[2], ones, sx, 0, 0, 0);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = fmaf(mu, sx[e], fmaf(sv, d[e], acc[e]));
+            for (int rt = 0; rt < RT; ++rt) {
+                const uint32_t cw[4] = {b.cw[rt].x, b.cw[rt].y, b.cw[rt].z, b.cw[rt].w};
+                const uint32_t mw[4] = {b.mv[rt].x, b.mv[rt].y, b.mv[rt].z, b.mv[rt].w};
+                const bf16x8 bc = codes_bf16(cw[uu]);
+                const uint32_t s2 = uu < 2 ? b.sv[rt].x : b.sv[rt].y;
+                const float sv = f16f(s2 >> (16 * (uu & 1)));
+                // m = high + low bf16 parts, exact in fp32
+                const uint32_t mh = mw[uu >> 1] >> (16 * (uu & 1)), ml = mw[2 + (uu >> 1)] >> (16 * (uu & 1));
+                const float mu = __uint_as_float(mh << 16) + __uint_as_float(ml << 16);
+                f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap[0], bc, z, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap[1], bc, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap[2], bc, d, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[rt][e] = fmaf(mu, sx[e], fmaf(sv, d[e], acc[rt][e]));
+            }
         }
     };
     if constexpr (SG == 1) {
         if (S == 1) {
-            RowBuf b0;
+            RowBuf<RT> b0;
             load(b0, 0);
             step(b0);
         }
     } else if constexpr (SG == 2) {
         if (S == 2) {
-            RowBuf b0, b1;
+            RowBuf<RT> b0, b1;
             load(b0, 0);
             load(b1, 1);
             step(b0);
             step(b1);
         } else if (S == 1) {
-            RowBuf b0;
+            RowBuf<RT> b0;
             load(b0, 0);
             step(b0);
         }
     } else if (S == 1) {
-        RowBuf b0;
+        RowBuf<RT> b0;
         load(b0, 0);
         step(b0);
     } else if (S > 1) {
         // two buffers, the next group's loads in flight while one is
         // multiplied; loads past the last group reload it (clamped, unused),
         // so the waits count statically
-        RowBuf b0, b1;
+        RowBuf<RT> b0, b1;
         load(b0, 0);
         for (int s = 0; s < S; s += 2) {
             load(b1, s + 1);
@@ -676,19 +686,20 @@ void sb6_t16_gemv_rows_kernel(BatchArgs A, float* __restrict__ y, int ep) {
             if (s + 1 < S) step(b1);
         }
     }
-    red[wave][lane] = acc;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) red[wave][rt][lane] = acc[rt];
     __syncthreads();
-    // output (input n, row r) of the tile: lane r + 16·(n / 4), component
+    // output (row tile rt, input n, row r): lane r + 16·(n / 4), component
     // n mod 4; waves summed in order
-    const float* rf = reinterpret_cast<const float*>(&red[0][0]);
-    if (tid < 256) {
-        const int r = tid & 15, n = tid >> 4;
+    const float* rf = reinterpret_cast<const float*>(&red[0][0][0]);
+    for (int o = tid; o < 256 * RT; o += 64 * W) {
+        const int r = o & 15, n = (o >> 4) & 15, rt = o >> 8;
         if (n < NL) {
-            const int off = (r + 16 * (n >> 2)) * 4 + (n & 3);
+            const int off = (rt * 64 + r + 16 * (n >> 2)) * 4 + (n & 3);
             float v = rf[off];
 #pragma unroll
-            for (int w = 1; w < W; ++w) v += rf[w * 256 + off];
-            float* yo = y + (int64_t)(n0 + n) * A.OUT + row0 + r;
+            for (int w = 1; w < W; ++w) v += rf[w * RT * 256 + off];
+            float* yo = y + (int64_t)(n0 + n) * A.OUT + row0 + rt * 16 + r;
             if (ep == 1) {
                 v = *yo + v;
             } else if (ep == 2) {
@@ -803,18 +814,24 @@ bool plan_batch(int64_t N, int64_t OUT, int64_t IN, int64_t out_per, BatchPlan& 
 }
 
 // The row-owned kernel: 4, 8 or 16 waves per (16-row, 16-input) tile with
-// at most two unit groups each up to K = 4096; beyond, 8 waves that loop.
-// Taken by the T16 entry up to 2^23 weights for K ≤ 2048, and up to 2^23
-// per 16-input tile for K ≤ 4096, where it measured faster per call than K
-// slices plus their reduction (graph-timed: 1024x1024 x32 4.3 vs 6.5 µs,
-// 2048x2048 x32 6.5 vs 8.7, 768x3072 x32 8.2 vs 9.9, 1024x4096 x8 8.1 vs 8.9);
-// past it every workgroup's conversion of its whole K into bf16 parts
-// outweighs the saved launch (1024x4096 x32 10.2 vs 9.4, 4096x4096 x16 10.7
-// vs 9.3, 8192x2048 x16 10.9 vs 9.6).
+// at most two unit groups each up to K = 4096 (beyond, 8 waves that loop),
+// two row tiles per workgroup once one per workgroup would be more
+// workgroups than CUs.  Taken by the T16 entry up to 2^24 weights for
+// K ≤ 3072, and for K ≤ 4096 where its grid is one round of up to 64
+// workgroups or pairs of row tiles, where it measured faster per call than
+// K slices plus their reduction (graph-timed: 1024x1024 x32 4.2 vs 6.5 µs,
+// 4096x1024 x32 5.6 vs 8.9, 12288x1024 x32 9.9 vs 14.5, 6144x2048 x16 8.4
+// vs 10.4, 3072x3072 x16 8.3 vs 10.3, 4096x4096 x32 12.9 vs 16.4,
+// 1024x4096 x8 8.1 vs 8.9); elsewhere every workgroup's conversion of its
+// whole K into bf16 parts outweighs the saved launch (1024x4096 x32 10.1 vs
+// 9.4, 4096x4096 x16 10.9 vs 9.5, 16384x2048 x16 15.6 vs 13.9, 65536x768 x8
+// 20.3 vs 17.6).
+constexpr int64_t kRowsPair = 257;
+
 bool rows_kernel_taken(int64_t N, int64_t OUT, int64_t IN) {
-    const int64_t w = OUT * IN;
-    if (IN <= 2048) return w <= ((int64_t)1 << 23);
-    return IN <= 4096 && w * ((N + 15) / 16) < ((int64_t)1 << 23);
+    const int64_t w = OUT * IN, wg = (OUT / 16) * ((N + 15) / 16);
+    if (IN > 4096 || w > ((int64_t)1 << 24)) return false;
+    return IN <= 3072 || wg <= 64 || wg >= kRowsPair;
 }
 
 rwkv_status launch_rows(BatchArgs a, int64_t N, float* y, int64_t OUT, int64_t IN, int64_t out_per, int epilogue,
@@ -835,18 +852,28 @@ rwkv_status launch_rows(BatchArgs a, int64_t N, float* y, int64_t OUT, int64_t I
     a.IN = (int)IN;
     a.out_per = (int)out_per;
     a.NK = (int)(OUT / out_per);
-    const dim3 grid((unsigned)(OUT / 16), (unsigned)((N + 15) / 16));
-    const int64_t NG = IN / 128;
-    if (NG <= 4)
-        rwkv::launch(sb6_t16_gemv_rows_kernel<4, 1>, grid, dim3(256), st, a, y, epilogue);
-    else if (NG <= 8)
-        rwkv::launch(sb6_t16_gemv_rows_kernel<8, 1>, grid, dim3(512), st, a, y, epilogue);
-    else if (NG <= 16)
-        rwkv::launch(sb6_t16_gemv_rows_kernel<16, 1>, grid, dim3(1024), st, a, y, epilogue);
-    else if (NG <= 32)
-        rwkv::launch(sb6_t16_gemv_rows_kernel<16, 2>, grid, dim3(1024), st, a, y, epilogue);
-    else
-        rwkv::launch(sb6_t16_gemv_rows_kernel<8, 0>, grid, dim3(512), st, a, y, epilogue);
+    const int64_t NT = (N + 15) / 16, NG = IN / 128;
+    // two row tiles per workgroup once one per workgroup would be more
+    // workgroups than CUs
+    const bool two = (OUT / 16) * NT >= kRowsPair;
+    const dim3 grid((unsigned)(OUT / (two ? 32 : 16)), (unsigned)NT);
+#define RWKV_ROWS(WV, SGV, BLK)                                                                  \
+    if (two)                                                                                     \
+        rwkv::launch(sb6_t16_gemv_rows_kernel<WV, SGV, 2>, grid, dim3(BLK), st, a, y, epilogue); \
+    else                                                                                         \
+        rwkv::launch(sb6_t16_gemv_rows_kernel<WV, SGV, 1>, grid, dim3(BLK), st, a, y, epilogue)
+    if (NG <= 4) {
+        RWKV_ROWS(4, 1, 256);
+    } else if (NG <= 8) {
+        RWKV_ROWS(8, 1, 512);
+    } else if (NG <= 16) {
+        RWKV_ROWS(16, 1, 1024);
+    } else if (NG <= 32) {
+        RWKV_ROWS(16, 2, 1024);
+    } else {
+        RWKV_ROWS(8, 0, 512);
+    }
+#undef RWKV_ROWS
     RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "%s: launch failed", who);
     rwkv::counters().sb6_batch.fetch_add(1);
     rwkv::clear_error();

@@ -401,22 +401,24 @@ def test_lora_orientation_naming_rule():
 
 
 def test_batched_gemv_kernel_choice_rules():
-    """The T16 batched GEMV's one-launch row-owned kernel: up to 2^23 weights for
-    K <= 2048, up to 2^23 per 16-input tile for K <= 4096; K slices plus their
-    reduction (two launches) elsewhere; 0 where the batched GEMV does not apply.
-    The decoder's preference for it keeps batches of up to 4 rows on the VALU
+    """The T16 batched GEMV's one-launch row-owned kernel: up to 2^24 weights
+    for K <= 3072, and for K <= 4096 where its grid is up to 64 workgroups or
+    more than 256 (row-tile pairs); K slices plus their reduction (two
+    launches) elsewhere; 0 where the batched GEMV does not apply.  The
+    decoder's preference for it keeps batches of up to 4 rows on the VALU
     kernel (bitwise each row alone)."""
     from swiftrwkv_amd import _lib
     L = _lib.lib()
     launches = lambda N, OUT, IN, per=None: int(L.rwkv_sb6_gemv_batch_t16_launches(N, OUT, IN, per or OUT))
     assert launches(32, 1024, 1024) == 1
-    assert launches(32, 8192, 1024) == 1            # 2^23 weights
-    assert launches(32, 16384, 768) == 2
-    assert launches(16, 2048, 2048) == 1 and launches(32, 4096, 2048) == 1
-    assert launches(16, 8192, 2048) == 2
-    assert launches(8, 1024, 4096) == 1 and launches(16, 1024, 4096) == 1
-    assert launches(17, 1024, 4096) == 2            # two input tiles: 2^23, not below
-    assert launches(16, 4096, 4096) == 2 and launches(16, 2048, 8192) == 2
+    assert launches(32, 16384, 1024) == 1           # 2^24 weights
+    assert launches(32, 32768, 768) == 2 and launches(8, 65536, 768) == 2
+    assert launches(16, 8192, 2048) == 1 and launches(16, 16384, 2048) == 2
+    assert launches(16, 3072, 3072) == 1
+    assert launches(8, 1024, 4096) == 1 and launches(16, 1024, 4096) == 1   # 64 workgroups
+    assert launches(17, 1024, 4096) == 2 and launches(16, 4096, 4096) == 2  # 128, 256
+    assert launches(32, 4096, 4096) == 1            # 512: pairs of row tiles
+    assert launches(16, 12288, 4096) == 2 and launches(16, 2048, 8192) == 2
     assert launches(8, 3 * 768, 768, 768) == 1      # fused r/k/v group
     assert launches(1, 768, 768) == 0 and launches(33, 768, 768) == 0 and launches(8, 768, 800) == 0
     pref = quant.rwkvq_sb6_gemv_batch_prefers
