@@ -815,7 +815,7 @@ bool plan_batch(int64_t N, int64_t OUT, int64_t IN, int64_t out_per, BatchPlan& 
 
 // The row-owned kernel: 4, 8 or 16 waves per (16-row, 16-input) tile with
 // at most two unit groups each up to K = 4096 (beyond, 8 waves that loop),
-// two row tiles per workgroup once one per workgroup would be more
+// two or four row tiles per workgroup once one per workgroup would be more
 // workgroups than CUs.  Taken by the T16 entry up to 2^24 weights for
 // K ≤ 3072, and for K ≤ 4096 where its grid is one round of up to 64
 // workgroups or pairs of row tiles, where it measured faster per call than
@@ -827,6 +827,7 @@ bool plan_batch(int64_t N, int64_t OUT, int64_t IN, int64_t out_per, BatchPlan& 
 // 9.4, 4096x4096 x16 10.9 vs 9.5, 16384x2048 x16 15.6 vs 13.9, 65536x768 x8
 // 20.3 vs 17.6).
 constexpr int64_t kRowsPair = 257;
+constexpr int64_t kRowsQuad = 1024;
 
 bool rows_kernel_taken(int64_t N, int64_t OUT, int64_t IN) {
     const int64_t w = OUT * IN, wg = (OUT / 16) * ((N + 15) / 16);
@@ -854,24 +855,28 @@ rwkv_status launch_rows(BatchArgs a, int64_t N, float* y, int64_t OUT, int64_t I
     a.NK = (int)(OUT / out_per);
     const int64_t NT = (N + 15) / 16, NG = IN / 128;
     // two row tiles per workgroup once one per workgroup would be more
-    // workgroups than CUs
-    const bool two = (OUT / 16) * NT >= kRowsPair;
-    const dim3 grid((unsigned)(OUT / (two ? 32 : 16)), (unsigned)NT);
-#define RWKV_ROWS(WV, SGV, BLK)                                                                  \
-    if (two)                                                                                     \
-        rwkv::launch(sb6_t16_gemv_rows_kernel<WV, SGV, 2>, grid, dim3(BLK), st, a, y, epilogue); \
-    else                                                                                         \
-        rwkv::launch(sb6_t16_gemv_rows_kernel<WV, SGV, 1>, grid, dim3(BLK), st, a, y, epilogue)
+    // workgroups than CUs, four (K ≤ 1024) from 1024 (8192x1024 x32 6.8 vs
+    // 7.4 µs, 16384x1024 x32 10.5 vs 13.5; 4096x1024 x32 6.6 vs 5.5)
+    const int64_t wg = (OUT / 16) * NT;
+    const int RT = NG <= 8 && wg >= kRowsQuad ? 4 : wg >= kRowsPair ? 2 : 1;
+    const dim3 grid((unsigned)(OUT / (16 * RT)), (unsigned)NT);
+#define RWKV_ROWS(WV, SGV)                                                                          \
+    if (RT == 2)                                                                                    \
+        rwkv::launch(sb6_t16_gemv_rows_kernel<WV, SGV, 2>, grid, dim3(64 * (WV)), st, a, y, epilogue); \
+    else                                                                                            \
+        rwkv::launch(sb6_t16_gemv_rows_kernel<WV, SGV, 1>, grid, dim3(64 * (WV)), st, a, y, epilogue)
     if (NG <= 4) {
-        RWKV_ROWS(4, 1, 256);
+        if (RT == 4) rwkv::launch(sb6_t16_gemv_rows_kernel<4, 1, 4>, grid, dim3(256), st, a, y, epilogue);
+        else RWKV_ROWS(4, 1);
     } else if (NG <= 8) {
-        RWKV_ROWS(8, 1, 512);
+        if (RT == 4) rwkv::launch(sb6_t16_gemv_rows_kernel<8, 1, 4>, grid, dim3(512), st, a, y, epilogue);
+        else RWKV_ROWS(8, 1);
     } else if (NG <= 16) {
-        RWKV_ROWS(16, 1, 1024);
+        RWKV_ROWS(16, 1);
     } else if (NG <= 32) {
-        RWKV_ROWS(16, 2, 1024);
+        RWKV_ROWS(16, 2);
     } else {
-        RWKV_ROWS(8, 0, 512);
+        RWKV_ROWS(8, 0);
     }
 #undef RWKV_ROWS
     RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "%s: launch failed", who);
