@@ -116,14 +116,16 @@ rwkv_status rwkv_wkv7_train_fwd(const void* r, const void* w, const void* k, con
 /* Backward from checkpoints.  Replaces ckptBwdKernelV2 / ckptBwdKernel
  * launched by the VJP of wkv7TrainWithState (WKV7Train.swift:99-339,410-420).
  * h_in: the forward's initial state [B,H,64,64] fp32 or NULL (zeros) — the
- * VJP's primal h0; the kernel recomputes each chunk's states forward from
- * h_in / the previous checkpoint instead of dividing by w.
+ * VJP's primal h0, from which variant 2 recomputes the first chunk's states.
  * h_ckpt, sa: the training forward's outputs.  d_out [B,T,H,64] fp32;
  * d_h_out [B,H,64,64] fp32 or NULL.  Gradients dr..db [B,T,H,64] are written
  * in g_dt (the primal's dtype, :440,462); dh_in [B,H,64,64] fp32.
- * variant: 2 = the default (wkv7BackwardV2 = true), 1 = the alternative;
- * both compute the same gradients and differ only in summation order, like
- * the reference's v1 / v2 pair. */
+ * variant: 2 = the default (wkv7BackwardV2 = true; column-owned, states
+ * recomputed forward from h_in / the previous checkpoint), 1 = the
+ * reference's row-owned ckptBwdKernel (WKV7Train.swift:99-205: one wave per
+ * head, states recovered by dividing by w, so the gradients formed from them,
+ * dr / dw / da, carry the forward's rounding amplified by up to Π 1/w over a
+ * 16-step chunk; h_in unused). */
 rwkv_status rwkv_wkv7_train_bwd(const void* r, const void* w, const void* k, const void* v,
                                 const void* a, const void* b, rwkv_dtype in_dt,
                                 const float* h_in, const float* h_ckpt, const float* sa,

@@ -32,6 +32,8 @@
 // vectors are staged per chunk in LDS (coalesced loads issued one chunk
 // ahead); dsa is the one quantity exchanged inside a step (one barrier per
 // step); every output is summed over the eight waves from an LDS ring.
+// Variant 1 is the reference's row-owned ckptBwdKernel (WKV7Train.swift:
+// 99-205), which does divide by w: wkv7_bwd_rows_kernel below.
 //
 // All arithmetic is fp32 with a fixed summation order: launches are bitwise
 // deterministic.
@@ -415,18 +417,15 @@ __device__ __forceinline__ void bwd_recompute8(const float (&S)[BJ], float (&N)[
           [u1] "v"(dR[o + 1]), [u2] "v"(dR[o + 2]), [u3] "v"(dR[o + 3]), [DS] "v"(DS), [A] "v"(A), [W] "v"(W),  \
           [dsi] "v"(dsa_i), [ai] "v"(ai))
 
-// Σ over the 8 waves' partials p[0..7] of one column (stride D floats).
-template <bool SEQ>
+// Σ over the 8 waves' partials p[0..7] of one column (stride D floats), pairwise.
 __device__ __forceinline__ float sum8(const float* p) {
     const float x0 = p[0], x1 = p[D], x2 = p[2 * D], x3 = p[3 * D];
     const float x4 = p[4 * D], x5 = p[5 * D], x6 = p[6 * D], x7 = p[7 * D];
-    if constexpr (SEQ) return (((((((x0 + x1) + x2) + x3) + x4) + x5) + x6) + x7);
     return ((x0 + x1) + (x2 + x3)) + ((x4 + x5) + (x6 + x7));
 }
 
-// SEQ = false: variant 2 (pairwise sums).  SEQ = true: variant 1 — identical
-// math, every sum taken sequentially (a different rounding order).
-template <int DT, int GT, bool SEQ>
+// Variant 2, the default.
+template <int DT, int GT>
 __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
     const void* __restrict__ r, const void* __restrict__ w, const void* __restrict__ k,
     const void* __restrict__ v, const void* __restrict__ a, const void* __restrict__ b,
@@ -507,7 +506,7 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
     const int fo = fidx >> 6, fcol = fidx & 63;
     auto flush = [&](int uu, int tt) {
         if (i < NOUT * D / BQ)
-            store1<GT>(outs[fo], base0 + (int64_t)tt * strideT + fcol, sum8<SEQ>(&ring[uu % 3][fo][0][fcol]));
+            store1<GT>(outs[fo], base0 + (int64_t)tt * strideT + fcol, sum8(&ring[uu % 3][fo][0][fcol]));
     };
 
     for (int c = NC - 1; c >= 0; --c) {
@@ -574,10 +573,7 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
                 float pdr = 0.0f, pdk = 0.0f, pdb = 0.0f, pdv = 0.0f, pds = 0.0f, pdw = 0.0f, pda = 0.0f;
                 RWKV_B1_BLOCK(0, 1, 2, 3, 0);
                 RWKV_B1_BLOCK(4, 5, 6, 7, 4);
-                if constexpr (SEQ) {
-#pragma unroll
-                    for (int jj = 0; jj < BJ; ++jj) pdw = fmaf(dT[jj], Sp[jj], pdw);
-                } else {
+                {
                     float w0 = 0.0f, w1 = 0.0f;
 #pragma unroll
                     for (int jj = 0; jj < BJ; jj += 2) { w0 = fmaf(dT[jj], Sp[jj], w0); w1 = fmaf(dT[jj + 1], Sp[jj + 1], w1); }
@@ -595,7 +591,7 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
                 StepVec nxt = cur;
                 if (m > 0) nxt = load_vec(s - 1);
                 __syncthreads();
-                const float dsa_i = sum8<SEQ>(&dsa_part[par][0][i]);
+                const float dsa_i = sum8(&dsa_part[par][0][i]);
                 const float DS = __shfl(dsa_i, jl, 64);   // dsa of row 8q + (i & 7)
                 float nR[BJ], nT[BJ];
                 RWKV_B3_BLOCK(0, 1, 2, 3, 0);
@@ -617,6 +613,137 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
     float4* dst = reinterpret_cast<float4*>(dh_in + hb + (int64_t)i * D + 8 * q);
     dst[0] = make_float4(dR[0], dR[1], dR[2], dR[3]);
     dst[1] = make_float4(dR[4], dR[5], dR[6], dR[7]);
+}
+
+// ─────────────────────────────── backward, row-owned (variant 1) ───────────────────────────────
+// The scheme of ckptBwdKernel (WKV7Train.swift:99-205): one wave per (b, h),
+// lane i owns value row i of the state S and of its gradient C = dL/dS, both
+// in VGPRs.  Each chunk starts from the state after it (the checkpoint) and
+// walks its steps backward, recovering the state before a step by dividing
+// by w: S_{t-1} = (S_t − v kᵀ − sa bᵀ) ⊘ w.  Per step (t descending)
+//   C += dy rᵀ;  dsa = C b;  dv = C k
+//   dr = S_tᵀ dy;  dw = Σ_i C ⊙ S_{t-1};  dk = Cᵀ v;  da = S_{t-1}ᵀ dsa;  db = Cᵀ sa
+//   C ← C diag(w) + dsa aᵀ
+// The column sums (over the lanes' rows, in row order) go through one LDS
+// transpose per step: every lane writes its row of the five products,
+// lane j sums column j.  A chunk's step vectors (and 1/w) are staged in LDS;
+// the next chunk's values and checkpoint row are loaded while this one runs.
+// Dividing by w amplifies the forward's rounding by up to Π 1/w over a chunk,
+// the reason the default (variant 2) recomputes the states instead.
+constexpr int kBwdRowsLds = (CH * 8 * D + 5 * D * (D + 1)) * 4;   // bytes of LDS
+
+template <int DT, int GT>
+__global__ __launch_bounds__(64) void wkv7_bwd_rows_kernel(
+    const void* __restrict__ r, const void* __restrict__ w, const void* __restrict__ k,
+    const void* __restrict__ v, const void* __restrict__ a, const void* __restrict__ b,
+    const float* __restrict__ h_ckpt, const float* __restrict__ sa, const float* __restrict__ d_out,
+    const float* __restrict__ d_h_out, void* __restrict__ dr, void* __restrict__ dw, void* __restrict__ dk,
+    void* __restrict__ dv, void* __restrict__ da, void* __restrict__ db, float* __restrict__ dh_in, int T, int H) {
+    extern __shared__ float lds[];
+    float* sv = lds;                   // [CH][8][64]: r, w, k, a, b, 1/w, v, sa of the chunk's steps
+    float* acc = lds + CH * 8 * D;     // [5][64][65]: the five products, row-major, padded rows
+    constexpr int AS = D * (D + 1);    // floats per product matrix
+    const int i = threadIdx.x;
+    const int bh = blockIdx.x, bi = bh / H, hi = bh - bi * H;
+    const int NC = T / CH;
+    auto elem = [&](int c, int t) { return (((int64_t)bi * T + (int64_t)c * CH + t) * H + hi) * D + i; };
+    const int64_t hb = (int64_t)bh * D * D + (int64_t)i * D;
+
+    float C[D], hr[D];
+#pragma unroll
+    for (int q = 0; q < D / 4; ++q) {
+        const float4 f = d_h_out ? reinterpret_cast<const float4*>(d_h_out + hb)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        C[4 * q] = f.x; C[4 * q + 1] = f.y; C[4 * q + 2] = f.z; C[4 * q + 3] = f.w;
+    }
+    // the chunk's per-lane values: r, w, k, a, b, v, sa, dy per step, and its
+    // checkpoint row; fetched one chunk ahead (clamped at chunk 0: its values
+    // again, unused)
+    float pf[CH][8];
+    float4 ph[D / 4];
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+            const int64_t e = elem(c, t);
+            pf[t][0] = load1<DT>(r, e);
+            pf[t][1] = load1<DT>(w, e);
+            pf[t][2] = load1<DT>(k, e);
+            pf[t][3] = load1<DT>(a, e);
+            pf[t][4] = load1<DT>(b, e);
+            pf[t][5] = load1<DT>(v, e);
+            pf[t][6] = sa[e];
+            pf[t][7] = d_out[e];
+        }
+        const float4* src = reinterpret_cast<const float4*>(h_ckpt + ((int64_t)bh * NC + c) * D * D + (int64_t)i * D);
+#pragma unroll
+        for (int q = 0; q < D / 4; ++q) ph[q] = src[q];
+    };
+    fetch(NC - 1);
+    for (int c = NC - 1; c >= 0; --c) {
+        float dyc[CH];
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+            float* V = sv + t * 8 * D;
+            V[0 * D + i] = pf[t][0];
+            V[1 * D + i] = pf[t][1];
+            V[2 * D + i] = pf[t][2];
+            V[3 * D + i] = pf[t][3];
+            V[4 * D + i] = pf[t][4];
+            V[5 * D + i] = 1.0f / pf[t][1];
+            V[6 * D + i] = pf[t][5];
+            V[7 * D + i] = pf[t][6];
+            dyc[t] = pf[t][7];
+        }
+#pragma unroll
+        for (int q = 0; q < D / 4; ++q) {
+            hr[4 * q] = ph[q].x; hr[4 * q + 1] = ph[q].y; hr[4 * q + 2] = ph[q].z; hr[4 * q + 3] = ph[q].w;
+        }
+        fetch(max(c - 1, 0));
+        __syncthreads();
+#pragma unroll 1
+        for (int t = CH - 1; t >= 0; --t) {
+            const float* V = sv + t * 8 * D;
+            const float dy = dyc[t], vi = V[6 * D + i], sai = V[7 * D + i];
+#pragma unroll
+            for (int j = 0; j < D; ++j) C[j] = fmaf(dy, V[0 * D + j], C[j]);
+            float dsa = 0.0f, dvv = 0.0f;
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                dsa = fmaf(C[j], V[4 * D + j], dsa);
+                dvv = fmaf(C[j], V[2 * D + j], dvv);
+            }
+            const int64_t e = elem(c, t);
+            store1<GT>(dv, e, dvv);
+            float* row = acc + i * (D + 1);
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                row[j] = dy * hr[j];
+                hr[j] = (hr[j] - vi * V[2 * D + j] - sai * V[4 * D + j]) * V[5 * D + j];
+                row[AS + j] = C[j] * hr[j];
+                row[2 * AS + j] = C[j] * vi;
+                row[3 * AS + j] = dsa * hr[j];
+                row[4 * AS + j] = sai * C[j];
+            }
+            __syncthreads();
+            float gs[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+            for (int s = 0; s < D; ++s) {
+                const float* col = acc + s * (D + 1) + i;
+#pragma unroll
+                for (int m = 0; m < 5; ++m) gs[m] += col[m * AS];
+            }
+            store1<GT>(dr, e, gs[0]);
+            store1<GT>(dw, e, gs[1]);
+            store1<GT>(dk, e, gs[2]);
+            store1<GT>(da, e, gs[3]);
+            store1<GT>(db, e, gs[4]);
+#pragma unroll
+            for (int j = 0; j < D; ++j) C[j] = fmaf(C[j], V[1 * D + j], dsa * V[3 * D + j]);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < D / 4; ++q)
+        reinterpret_cast<float4*>(dh_in + hb)[q] = make_float4(C[4 * q], C[4 * q + 1], C[4 * q + 2], C[4 * q + 3]);
 }
 
 // ─────────────────────────────── tmix tail ───────────────────────────────
@@ -810,26 +937,41 @@ rwkv_status rwkv_wkv7_train_bwd(const void* r, const void* w, const void* k, con
     RWKV_REQUIRE(variant == 1 || variant == 2, RWKV_E_UNSUPPORTED, "wkv7_train_bwd: variant %d not in {1, 2}", variant);
     dim3 grid((unsigned)(B * H)), block(512);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define RWKV_BWD_LAUNCH(DT, GT, SEQ)                                                                          \
-    rwkv::launch(wkv7_bwd_kernel<DT, GT, SEQ>, grid, block, st, r, w, k, v, a, b, h_in, h_ckpt, sa, \
+#define RWKV_BWD_LAUNCH(DT, GT)                                                                          \
+    rwkv::launch(wkv7_bwd_kernel<DT, GT>, grid, block, st, r, w, k, v, a, b, h_in, h_ckpt, sa, \
                        d_out, d_h_out, dr, dw, dk, dv, da, db, dh_in, (int)T, (int)H)
-#define RWKV_BWD_GT(DT, SEQ)                                         \
+#define RWKV_BWD_GT(DT)                                         \
     switch (g_dt) {                                                  \
-        case RWKV_F32: RWKV_BWD_LAUNCH(DT, RWKV_F32, SEQ); break;   \
-        case RWKV_BF16: RWKV_BWD_LAUNCH(DT, RWKV_BF16, SEQ); break; \
-        case RWKV_F16: RWKV_BWD_LAUNCH(DT, RWKV_F16, SEQ); break;   \
+        case RWKV_F32: RWKV_BWD_LAUNCH(DT, RWKV_F32); break;   \
+        case RWKV_BF16: RWKV_BWD_LAUNCH(DT, RWKV_BF16); break; \
+        case RWKV_F16: RWKV_BWD_LAUNCH(DT, RWKV_F16); break;   \
     }
-#define RWKV_BWD_DT(SEQ)                                  \
+#define RWKV_BWD_DT()                                  \
     switch (in_dt) {                                      \
-        case RWKV_F32: RWKV_BWD_GT(RWKV_F32, SEQ); break;   \
-        case RWKV_BF16: RWKV_BWD_GT(RWKV_BF16, SEQ); break; \
-        case RWKV_F16: RWKV_BWD_GT(RWKV_F16, SEQ); break;   \
+        case RWKV_F32: RWKV_BWD_GT(RWKV_F32); break;   \
+        case RWKV_BF16: RWKV_BWD_GT(RWKV_BF16); break; \
+        case RWKV_F16: RWKV_BWD_GT(RWKV_F16); break;   \
+    }
+#define RWKV_ROWS_LAUNCH(DT, GT)                                                                              \
+    rwkv::launch_lds(wkv7_bwd_rows_kernel<DT, GT>, dim3((unsigned)(B * H)), dim3(64), (size_t)kBwdRowsLds, st, r, \
+                     w, k, v, a, b, h_ckpt, sa, d_out, d_h_out, dr, dw, dk, dv, da, db, dh_in, (int)T, (int)H)
+#define RWKV_ROWS_GT(DT)                                           \
+    switch (g_dt) {                                                \
+        case RWKV_F32: RWKV_ROWS_LAUNCH(DT, RWKV_F32); break;   \
+        case RWKV_BF16: RWKV_ROWS_LAUNCH(DT, RWKV_BF16); break; \
+        case RWKV_F16: RWKV_ROWS_LAUNCH(DT, RWKV_F16); break;   \
     }
     if (variant == 2) {
-        RWKV_BWD_DT(false)
+        RWKV_BWD_DT()
     } else {
-        RWKV_BWD_DT(true)
+        switch (in_dt) {
+            case RWKV_F32: RWKV_ROWS_GT(RWKV_F32); break;
+            case RWKV_BF16: RWKV_ROWS_GT(RWKV_BF16); break;
+            case RWKV_F16: RWKV_ROWS_GT(RWKV_F16); break;
+        }
     }
+#undef RWKV_ROWS_GT
+#undef RWKV_ROWS_LAUNCH
 #undef RWKV_BWD_DT
 #undef RWKV_BWD_GT
 #undef RWKV_BWD_LAUNCH

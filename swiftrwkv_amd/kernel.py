@@ -196,8 +196,10 @@ def _train_forward(ins, dt, h0):
 
 
 class _WKV7Train(torch.autograd.Function):
-    """Forward: checkpointing kernel.  Backward: checkpoint kernel v2 (or v1),
-    the VJP of wkv7TrainWithState (WKV7Train.swift:410-467).  Gradients come
+    """Forward: checkpointing kernel.  Backward: checkpoint kernel v2, column-owned
+    with recomputed states (or v1, the row-owned kernel that recovers them by
+    dividing by w, WKV7Train.swift:99-205), the VJP of wkv7TrainWithState
+    (WKV7Train.swift:410-467).  Gradients come
     back in each primal's dtype; the state gradient in the state's dtype."""
 
     @staticmethod

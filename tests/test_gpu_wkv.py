@@ -275,6 +275,14 @@ def kernel_grads(x, h0, g, gh, v2=True, keep=True, dt=torch.float32):
 NAMES = ["dr", "dw", "dk", "dv", "da", "db", "dh_in"]
 
 
+# Variant 1 (the reference's row-owned ckptBwdKernel, WKV7Train.swift:99-205)
+# recovers each step's earlier state by dividing by w, which amplifies the
+# forward's rounding by up to Π 1/w over a 16-step chunk (w down to 0.55
+# here): the gradients formed from those states (dr, dw, da) get 5e-5, those
+# formed from dL/dS alone 1e-5; with mild decay every one meets 1e-5 (below).
+V1_STATE_GRADS = {"dr", "dw", "da"}
+
+
 @pytest.mark.parametrize("v2", [True, False])
 def test_backward_matches_fp64_oracle(orc, v2):
     case(f"backward v{2 if v2 else 1} vs fp64 oracle B2 T48 H3")
@@ -284,8 +292,20 @@ def test_backward_matches_fp64_oracle(orc, v2):
     errs = [rel(w_, host(g_)) for w_, g_ in zip(want, got)]
     print("bwd v%d rel: %s" % (2 if v2 else 1, ", ".join(f"{n} {e:.1e}" for n, e in zip(NAMES, errs))))
     for n, e, g_ in zip(NAMES, errs, got):
-        assert e < TOL, n
+        assert e < (5e-5 if not v2 and n in V1_STATE_GRADS else TOL), n
         assert g_.abs().max() > 0, n
+
+
+def test_backward_v1_mild_decay_meets_the_bound(orc):
+    case("backward v1 vs fp64 oracle, w in (0.95, 1)")
+    x, h0, g, gh = train_case(seed=8)
+    rng = np.random.default_rng(9)
+    x[1] = np.exp(-0.05 * rng.random(x[1].shape)).astype(np.float32)
+    got = kernel_grads(x, h0, g, gh, v2=False)
+    want = orc.wkv7_bwd_f64(*x, h0, g, gh)
+    errs = [rel(w_, host(g_)) for w_, g_ in zip(want, got)]
+    print("bwd v1 mild decay rel: " + ", ".join(f"{n} {e:.1e}" for n, e in zip(NAMES, errs)))
+    assert max(errs) < TOL
 
 
 def test_backward_after_sixteen_row_forward_matches_fp64_oracle(orc):
