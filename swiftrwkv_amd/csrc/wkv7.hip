@@ -639,7 +639,7 @@ __global__ __launch_bounds__(64) void wkv7_bwd_rows_kernel(
     const float* __restrict__ h_ckpt, const float* __restrict__ sa, const float* __restrict__ d_out,
     const float* __restrict__ d_h_out, void* __restrict__ dr, void* __restrict__ dw, void* __restrict__ dk,
     void* __restrict__ dv, void* __restrict__ da, void* __restrict__ db, float* __restrict__ dh_in, int T, int H) {
-    extern __shared__ float lds[];
+    extern __shared__ __attribute__((aligned(16))) float lds[];
     float* sv = lds;                   // [CH][8][64]: r, w, k, a, b, 1/w, v, sa of the chunk's steps
     float* acc = lds + CH * 8 * D;     // [5][64][65]: the five products, row-major, padded rows
     constexpr int AS = D * (D + 1);    // floats per product matrix
@@ -702,26 +702,49 @@ __global__ __launch_bounds__(64) void wkv7_bwd_rows_kernel(
 #pragma unroll 1
         for (int t = CH - 1; t >= 0; --t) {
             const float* V = sv + t * 8 * D;
+            // the step vectors are the same for every lane: 16-byte broadcast reads
+            const float4* V4 = reinterpret_cast<const float4*>(V);
+            auto vec = [&](int q, int j4) { return V4[q * (D / 4) + j4]; };
             const float dy = dyc[t], vi = V[6 * D + i], sai = V[7 * D + i];
 #pragma unroll
-            for (int j = 0; j < D; ++j) C[j] = fmaf(dy, V[0 * D + j], C[j]);
+            for (int j4 = 0; j4 < D / 4; ++j4) {
+                const float4 rr = vec(0, j4);
+                C[4 * j4] = fmaf(dy, rr.x, C[4 * j4]);
+                C[4 * j4 + 1] = fmaf(dy, rr.y, C[4 * j4 + 1]);
+                C[4 * j4 + 2] = fmaf(dy, rr.z, C[4 * j4 + 2]);
+                C[4 * j4 + 3] = fmaf(dy, rr.w, C[4 * j4 + 3]);
+            }
             float dsa = 0.0f, dvv = 0.0f;
 #pragma unroll
-            for (int j = 0; j < D; ++j) {
-                dsa = fmaf(C[j], V[4 * D + j], dsa);
-                dvv = fmaf(C[j], V[2 * D + j], dvv);
+            for (int j4 = 0; j4 < D / 4; ++j4) {
+                const float4 bb = vec(4, j4), kk = vec(2, j4);
+                dsa = fmaf(C[4 * j4], bb.x, dsa);
+                dvv = fmaf(C[4 * j4], kk.x, dvv);
+                dsa = fmaf(C[4 * j4 + 1], bb.y, dsa);
+                dvv = fmaf(C[4 * j4 + 1], kk.y, dvv);
+                dsa = fmaf(C[4 * j4 + 2], bb.z, dsa);
+                dvv = fmaf(C[4 * j4 + 2], kk.z, dvv);
+                dsa = fmaf(C[4 * j4 + 3], bb.w, dsa);
+                dvv = fmaf(C[4 * j4 + 3], kk.w, dvv);
             }
             const int64_t e = elem(c, t);
             store1<GT>(dv, e, dvv);
             float* row = acc + i * (D + 1);
 #pragma unroll
-            for (int j = 0; j < D; ++j) {
-                row[j] = dy * hr[j];
-                hr[j] = (hr[j] - vi * V[2 * D + j] - sai * V[4 * D + j]) * V[5 * D + j];
-                row[AS + j] = C[j] * hr[j];
-                row[2 * AS + j] = C[j] * vi;
-                row[3 * AS + j] = dsa * hr[j];
-                row[4 * AS + j] = sai * C[j];
+            for (int j4 = 0; j4 < D / 4; ++j4) {
+                const float4 kk = vec(2, j4), bb = vec(4, j4), iw = vec(5, j4);
+                const float kv[4] = {kk.x, kk.y, kk.z, kk.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
+                const float wv[4] = {iw.x, iw.y, iw.z, iw.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int j = 4 * j4 + u;
+                    row[j] = dy * hr[j];
+                    hr[j] = (hr[j] - vi * kv[u] - sai * bv[u]) * wv[u];
+                    row[AS + j] = C[j] * hr[j];
+                    row[2 * AS + j] = C[j] * vi;
+                    row[3 * AS + j] = dsa * hr[j];
+                    row[4 * AS + j] = sai * C[j];
+                }
             }
             __syncthreads();
             float gs[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
@@ -737,7 +760,13 @@ __global__ __launch_bounds__(64) void wkv7_bwd_rows_kernel(
             store1<GT>(da, e, gs[3]);
             store1<GT>(db, e, gs[4]);
 #pragma unroll
-            for (int j = 0; j < D; ++j) C[j] = fmaf(C[j], V[1 * D + j], dsa * V[3 * D + j]);
+            for (int j4 = 0; j4 < D / 4; ++j4) {
+                const float4 ww = vec(1, j4), aa = vec(3, j4);
+                C[4 * j4] = fmaf(C[4 * j4], ww.x, dsa * aa.x);
+                C[4 * j4 + 1] = fmaf(C[4 * j4 + 1], ww.y, dsa * aa.y);
+                C[4 * j4 + 2] = fmaf(C[4 * j4 + 2], ww.z, dsa * aa.z);
+                C[4 * j4 + 3] = fmaf(C[4 * j4 + 3], ww.w, dsa * aa.w);
+            }
             __syncthreads();
         }
     }
