@@ -625,12 +625,13 @@ __global__ __launch_bounds__(512) void wkv7_bwd_kernel(
 //   dr = S_tᵀ dy;  dw = Σ_i C ⊙ S_{t-1};  dk = Cᵀ v;  da = S_{t-1}ᵀ dsa;  db = Cᵀ sa
 //   C ← C diag(w) + dsa aᵀ
 // The column sums (over the lanes' rows, in row order) go through one LDS
-// transpose per step: every lane writes its row of the five products,
-// lane j sums column j.  A chunk's step vectors (and 1/w) are staged in LDS;
+// transpose per step: every lane writes its row of the five products as a
+// column, lane j sums row j (16-byte reads).  A chunk's step vectors (and 1/w) are staged in LDS;
 // the next chunk's values and checkpoint row are loaded while this one runs.
 // Dividing by w amplifies the forward's rounding by up to Π 1/w over a chunk,
 // the reason the default (variant 2) recomputes the states instead.
-constexpr int kBwdRowsLds = (CH * 8 * D + 5 * D * (D + 1)) * 4;   // bytes of LDS
+constexpr int kBwdRowsTS = D + 4;   // LDS row stride of the transposed products (16-byte rows)
+constexpr int kBwdRowsLds = (CH * 8 * D + 5 * D * kBwdRowsTS) * 4;   // bytes of LDS
 
 template <int DT, int GT>
 __global__ __launch_bounds__(64) void wkv7_bwd_rows_kernel(
@@ -641,8 +642,8 @@ __global__ __launch_bounds__(64) void wkv7_bwd_rows_kernel(
     void* __restrict__ dv, void* __restrict__ da, void* __restrict__ db, float* __restrict__ dh_in, int T, int H) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     float* sv = lds;                   // [CH][8][64]: r, w, k, a, b, 1/w, v, sa of the chunk's steps
-    float* acc = lds + CH * 8 * D;     // [5][64][65]: the five products, row-major, padded rows
-    constexpr int AS = D * (D + 1);    // floats per product matrix
+    float* acc = lds + CH * 8 * D;     // [5][64][68]: the five products transposed (column j of lane i's row at [j][i])
+    constexpr int TS = kBwdRowsTS, AS = D * TS;   // row stride, floats per product matrix
     const int i = threadIdx.x;
     const int bh = blockIdx.x, bi = bh / H, hi = bh - bi * H;
     const int NC = T / CH;
@@ -729,7 +730,7 @@ __global__ __launch_bounds__(64) void wkv7_bwd_rows_kernel(
             }
             const int64_t e = elem(c, t);
             store1<GT>(dv, e, dvv);
-            float* row = acc + i * (D + 1);
+            float* col = acc + i;   // lane i writes element i of every transposed row
 #pragma unroll
             for (int j4 = 0; j4 < D / 4; ++j4) {
                 const float4 kk = vec(2, j4), bb = vec(4, j4), iw = vec(5, j4);
@@ -738,21 +739,29 @@ __global__ __launch_bounds__(64) void wkv7_bwd_rows_kernel(
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int j = 4 * j4 + u;
-                    row[j] = dy * hr[j];
+                    col[j * TS] = dy * hr[j];
                     hr[j] = (hr[j] - vi * kv[u] - sai * bv[u]) * wv[u];
-                    row[AS + j] = C[j] * hr[j];
-                    row[2 * AS + j] = C[j] * vi;
-                    row[3 * AS + j] = dsa * hr[j];
-                    row[4 * AS + j] = sai * C[j];
+                    col[AS + j * TS] = C[j] * hr[j];
+                    col[2 * AS + j * TS] = C[j] * vi;
+                    col[3 * AS + j * TS] = dsa * hr[j];
+                    col[4 * AS + j * TS] = sai * C[j];
                 }
             }
             __syncthreads();
+            // column i of each product is row i of its transpose: 16-byte
+            // reads, summed over the lanes' rows in order
             float gs[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-            for (int s = 0; s < D; ++s) {
-                const float* col = acc + s * (D + 1) + i;
 #pragma unroll
-                for (int m = 0; m < 5; ++m) gs[m] += col[m * AS];
+            for (int m = 0; m < 5; ++m) {
+                const float4* tr = reinterpret_cast<const float4*>(acc + m * AS + i * TS);
+#pragma unroll
+                for (int s4 = 0; s4 < D / 4; ++s4) {
+                    const float4 f = tr[s4];
+                    gs[m] += f.x;
+                    gs[m] += f.y;
+                    gs[m] += f.z;
+                    gs[m] += f.w;
+                }
             }
             store1<GT>(dr, e, gs[0]);
             store1<GT>(dw, e, gs[1]);
