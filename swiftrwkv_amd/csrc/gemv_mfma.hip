@@ -559,14 +559,14 @@ __global__ __launch_bounds__(256) void sb6_t16_gemv_mfma_kernel(BatchArgs A) {
 
 // Row-owned kernel over T16 weights, for matrices whose K slices would
 // leave too little work per workgroup (a few units of a few row groups) and
-// a second launch to sum them: one workgroup per (16-row tile, 16-input
-// tile), its W waves splitting the tile's K (wave w takes unit groups w,
-// w + W, …) and loading their inputs straight into A-operand registers (no
-// LDS staging: no other wave reads them).  The W accumulators are summed in
-// LDS in wave order and the epilogue applied in the same launch; no
-// workspace.  Per unit the same MFMAs give Σ c·x (B = the codes) and Σ x
-// (B = ones) of the lane's four inputs, so acc += s·Σ c·x + m·Σ x is four
-// fmas each.
+// a second launch to sum them: one workgroup per (RT 16-row tiles, 16-input
+// tile), its W waves splitting K (wave w takes unit groups w, w + W, …) and
+// loading their inputs straight into A-operand registers (no LDS staging: no
+// other wave reads them).  The W accumulators are summed in LDS in wave
+// order and the epilogue applied in the same launch; no workspace.  Per
+// unit the MFMAs give Σ c·x (B = the codes, per row tile) and Σ x (B = ones,
+// shared by the row tiles) of the lane's four inputs, so
+// acc += s·Σ c·x + m·Σ x is two fmas per accumulator element.
 template <int RT>
 struct RowBuf {
     uint4 cw[RT];      // codes: dword g of the group's units 0..3, row i of row tile rt
