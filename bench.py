@@ -20,7 +20,8 @@ tokens, checked against the GPU head GEMV first.
 Also reported (`extra`): the 0.1B decode (GEMV + WKV chain of one token, and
 the whole step), WKV-7 forward tokens/s at B1 T1024 H12 fp32, forward and
 forward+backward at B8 T4096 H32 bf16 (checkpointed), the head-GEMV HBM GB/s,
-batched decode of the 0.1B and 0.4B shapes (batch 1 / 8 / 32), decode of the
+batched decode of the 0.1B and 0.4B shapes (batch 1 / 8 / 32) and of the 1.5B
+shape (batch 16), decode of the
 7B-class shape (32 layers, n_embd 4096, FFN 14336) at batch 1 and 16, the
 WKV-7 forward of one 7B-class prefill layer (B1 T8192 H64 fp32), and the CPU
 restatements.
@@ -962,9 +963,15 @@ def headline_1b5(args, dev):
              "gemv_launches_per_token": n_gemv, "gemv_avg_us": gemv_avg_ms * 1e3,
              "gemv_kernel_us_per_token": gemv_avg_ms * 1e3 * n_gemv}
     cpu = None if args.skip_cpu else cpu_baseline(model, step, args.cpu_seconds, dev)
+    # the same chain for 16 rows (batched decode: the matrix-core GEMVs over T16 copies)
+    del step
+    _, bwall, _ = run_decode(model, dev, 16, 30, 4, 1)
+    batch16 = {"tok_s": 16 * 30 / bwall, "ms_per_step": bwall * 1e3 / 30}
+    log(f"1.5B decode batch 16: {bwall * 1e3 / 30:.3f} ms per step")
     res = {"wall": wall, "gpu_ms": gpu_ms, "launches": launches, "achieved": achieved, "n_gemv": n_gemv,
-           "gemv_bytes": gemv_bytes, "chain": chain, "cpu": cpu, "bytes_per_token": model.bytes_per_token}
-    del model, step
+           "gemv_bytes": gemv_bytes, "chain": chain, "cpu": cpu, "bytes_per_token": model.bytes_per_token,
+           "batch16": batch16}
+    del model
     import torch
     torch.cuda.empty_cache()
     return res
@@ -1025,7 +1032,7 @@ def main():
         profile_batch(dev)
         return
     head = headline_1b5(args, dev)
-    extra = {"decode_1.5B_gemv_wkv_chain_batch1": head["chain"]}
+    extra = {"decode_1.5B_gemv_wkv_chain_batch1": head["chain"], "decode_1.5B_batch16": head["batch16"]}
     model01, more01 = config1_0b1(args, dev)
     extra.update(more01)
     if not args.skip_wkv:
