@@ -570,12 +570,14 @@ rwkv_status rwkv_wkv7_seq_fwd_chunked_static(const void* r, const void* w, const
     const char* who = "wkv7_seq_fwd_chunked_static";
     RWKV_REQUIRE(B >= 1 && T >= 1 && H >= 1, RWKV_E_SHAPE, "%s: B=%lld T=%lld H=%lld", who, (long long)B,
                  (long long)T, (long long)H);
-    RWKV_REQUIRE(B <= kScratchBytes && H <= kScratchBytes && B * H * ((T + CH - 1) / CH) * (int64_t)WS_CHUNK * 4 <=
-                                                                 kScratchBytes,
+    // compared by division: no product below can overflow, whatever B, T, H
+    const int64_t max_chunks = kScratchBytes / ((int64_t)WS_CHUNK * 4);
+    const int64_t chunks = (T - 1) / CH + 1;
+    RWKV_REQUIRE(B <= max_chunks && H <= max_chunks && B * H <= max_chunks && chunks <= max_chunks / (B * H),
                  RWKV_E_SHAPE,
-                 "%s: B·H·ceil(T/32) = %lld exceeds the static scratch (%lld chunks of 48 KiB, 64 MiB); use "
-                 "rwkv_wkv7_seq_fwd_chunked with a workspace",
-                 who, (long long)(B * H * ((T + CH - 1) / CH)), (long long)(kScratchBytes / (WS_CHUNK * 4)));
+                 "%s: B=%lld H=%lld ceil(T/32)=%lld exceed the static scratch (B·H·ceil(T/32) <= %lld chunks of "
+                 "48 KiB, 64 MiB); use rwkv_wkv7_seq_fwd_chunked with a workspace",
+                 who, (long long)B, (long long)H, (long long)chunks, (long long)max_chunks);
     void* ptr = nullptr;
     const rwkv_status st = scratch_on_current_device(&ptr);
     if (st != RWKV_OK) return st;

@@ -442,8 +442,14 @@ class X070Decoder:
     batch_mfma: Optional[bool] = None
 
     def _batch_ws(self, nbytes: int) -> torch.Tensor:
+        """The batched GEMV's shared workspace, grown when a call needs more.
+        A grown-out buffer is kept alive (not returned to the caching
+        allocator): a HIP graph captured through launch() before the growth
+        still holds its address and may be replayed."""
         ws = self._tmp.get("batch_ws")
         if ws is None or ws.numel() < nbytes:
+            if ws is not None:
+                self._tmp.setdefault("batch_ws_retired", []).append(ws)
             ws = self._tmp["batch_ws"] = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self.device)
         return ws
 

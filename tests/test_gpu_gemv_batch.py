@@ -173,9 +173,11 @@ def test_t16_fused_group_and_epilogues(D, N):
 # 24 (3: an odd count) and 32 per 16-row tile; one, two (3072, 4096 and 8192
 # rows) and four (8192 rows at 17+ inputs) row tiles per workgroup; past
 # K = 4096 the looping waves (8 and 5 unit groups each, the 4608-row matrix in
-# row-tile pairs)
+# row-tile pairs); K of 2 and 4 unit groups with four row tiles per workgroup
+# (8192x256 at 17+ inputs, 16384x512)
 @pytest.mark.parametrize("OUT,IN", [(64, 256), (768, 768), (3072, 768), (768, 3072), (1024, 1024), (4096, 1024),
-                                    (1024, 4096), (192, 2048), (8192, 768), (256, 8192), (4608, 5120)])
+                                    (1024, 4096), (192, 2048), (8192, 768), (256, 8192), (4608, 5120),
+                                    (8192, 256), (16384, 512)])
 @pytest.mark.parametrize("N", [2, 8, 16, 17, 32])
 def test_t16_rows_kernel_matches_single_rows_and_oracle(orc, OUT, IN, N):
     case(f"sb6 batched gemv T16 row-owned {OUT}x{IN} N={N}")

@@ -54,4 +54,10 @@ def test_static_scratch_refuses_passes_beyond_it():
     st = _lib.lib().rwkv_wkv7_seq_fwd_chunked_static(*[z.data_ptr() for z in x], _lib.F32, None,
                                                      x[0].data_ptr(), x[1].data_ptr(), 1, 32 * 1366, 1, None)
     assert st != 0 and b"static scratch" in _lib.lib().rwkv_last_error()
+    # sizes whose byte count would wrap a 64-bit product (T = 2^55 gives
+    # 2^50 chunks: × 48 KiB is 0 mod 2^64) are refused as well
+    for (b_, t_, h_) in [(1, 1 << 55, 1), (1 << 40, 32, 1 << 30), (1, (1 << 63) - 1, 1), (1366, 1, 1)]:
+        st = _lib.lib().rwkv_wkv7_seq_fwd_chunked_static(*[z.data_ptr() for z in x], _lib.F32, None,
+                                                         x[0].data_ptr(), x[1].data_ptr(), b_, t_, h_, None)
+        assert st != 0 and b"static scratch" in _lib.lib().rwkv_last_error(), (b_, t_, h_)
     assert _lib.counters()["seq_chunked"] == before
