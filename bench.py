@@ -9,10 +9,14 @@ relu², ffn value + residual; ln_out, head) captured in one HIP graph.  Weights
 are sb6 4-bit encoded from seeded N(0, 0.02): 776 MB of packed projections
 per token (> the 256 MB MALL), resident in HBM before the timed region.
 
-`roofline` is for the dominant kernel of that token, the sb6 GEMV: the
-token's algorithmic GEMV bytes per launch (packed weights + x + y, over the
-token's GEMV launches) over the kernel's average in-graph duration, measured
-live on a graph holding only those GEMV launches.  `cpu_baseline` times the
+`roofline` is for the token's GEMV-bearing launches (the r/k/v + low-rank,
+o_proj, ffn key and ffn value launches of every layer and the head: ~86 % of
+its kernel time): their algorithmic bytes (packed projections, the fp16
+low-rank inner matrices, the fp32 rows they read and write) over their
+average duration, measured live on a graph of the same step with its tmix
+cores and layer norms left out, so those launches run back to back in step
+order; `roofline.whole_token` is the whole token's algorithmic bytes over the
+headline's time per token.  `cpu_baseline` times the
 oracle's restatement of the reference's non-kernel decode path (dequantise
 to fp32, x·Wᵀ per projection; MLX-op WKV step) on a bounded sample of 1.5B
 tokens, checked against the GPU head GEMV first.
@@ -49,6 +53,10 @@ DECODE_GEMV_TRAFFIC_BYTES = 1744043
 # The same for the average GEMV launch of one 1.5B decode token (582 launches
 # of 6 eager tokens; profiles/hbm_traffic_decode_1.5B_gemv.md).
 DECODE_1B5_GEMV_TRAFFIC_BYTES = 8291062
+# The same for the average GEMV-bearing launch of the 1.5B x070 step (per layer
+# the r/k/v + low-rank, o_proj, ffn key and ffn value launches, and the head);
+# profiles/hbm_traffic_decode_1.5B_step.md.  None until measured.
+DECODE_1B5_STEP_GEMV_TRAFFIC_BYTES = None
 VALU_PEAK_TFLOPS = 157.3
 
 
@@ -401,6 +409,106 @@ def run_x070(model, dev, steps, warmup, copies=1, B=1):
     del decs, graphs
     torch.cuda.empty_cache()
     return wall, e0.elapsed_time(e1), launches
+
+
+def x070_step_bytes(dec):
+    """Algorithmic bytes of one batch-1 token of the row-forming x070 step
+    (X070Decoder._layer_ln_fused): (bytes of its GEMV-bearing launches,
+    bytes of the whole token).  Each buffer counts once per launch that must
+    read or write it: packed projections (K3 bytes), the fp16 low-rank
+    matrices, the fp32 rows (activations, layer-norm and lerp parameters,
+    shift rows) and the WKV state (read and written)."""
+    D, F, V, H = dec.D, dec.F, dec.V, dec.H
+    packed = lambda key: sum(int(b.numel()) * b.element_size() for b in dec.proj[key].bufs)
+    rw, ra, rv, rg = dec.ranks
+    gemv = whole = 0
+    for l in range(dec.L):
+        RT = rw + ra + rg + (rv if l > 0 else 0)
+        lora = RT * D * 2   # the branch matrices' inner (A) rows, fp16
+        # r/k/v + low-rank inner products: x, prev, 6 lerp rows, ln1 w/b in; y_rkv, la, xl1 out
+        rkv = packed(f"blocks.{l}.att.rkv") + lora + 4 * (10 * D + 3 * D + RT + D)
+        o = packed(f"blocks.{l}.att.output.weight") + 4 * (D + 2 * D)   # tout in; x read and written
+        # ffn key: x, prev, lerp row, ln2 w/b in; hk, xl2 out
+        key = packed(f"blocks.{l}.ffn.key.weight") + 4 * (5 * D + F + D)
+        # ffn value: hk in; x read and written; the shift row copied
+        val = packed(f"blocks.{l}.ffn.value.weight") + 4 * (F + 2 * D + 2 * D)
+        # tmix core: the branch matrices' outer (B) rows, y_rkv, la, per-head
+        # vectors (3 biases, k_k, k_a, r_k, ln_x w/b, v_first), the state twice, tout
+        core = lora + 4 * (3 * D + RT + 9 * D + 2 * H * 64 * 64 + D)
+        gemv += rkv + o + key + val
+        whole += rkv + o + key + val + core
+    head = packed("head.weight") + 4 * (D + V)
+    lnio = 2 * 4 * (3 * D) + 2 * D   # emb row (fp16) + ln0, ln_out: row, w, b in, row out
+    return gemv + head, whole + head + lnio
+
+
+class _SkipLaunches:
+    """The library with some entry points turned into no-ops (they return
+    RWKV_OK without launching): a graph captured through it holds the
+    other launches of a step, in the step's order."""
+
+    # the entry points that launch a GEMV-bearing kernel (one launch each here)
+    LAUNCHES = {"rwkv_x070_rkv_lora_ln", "rwkv_x070_ffn_key_ln", "rwkv_x070_ffn_value", "rwkv_x070_rkv_lora",
+                "rwkv_sb6_gemv_ep", "rwkv_sb6_gemv_fused", "rwkv_sb6_gemv"}
+
+    def __init__(self, lib, skip):
+        self._lib, self._skip, self.kept = lib, set(skip), 0
+
+    def __getattr__(self, name):
+        f = getattr(self._lib, name)
+        if name in self._skip:
+            return lambda *a: 0
+        if name in self.LAUNCHES:
+            def counted(*a):
+                self.kept += 1
+                return f(*a)
+            return counted
+        return f
+
+
+def bench_step_gemv_launches(model, dev, reps=100):
+    """In-step roofline of the 1.5B token's GEMV-bearing launches: the
+    X070Decoder step captured with its tmix cores and layer norms left out
+    (r/k/v + low-rank, o_proj + residual, ffn key, ffn value + residual per
+    layer, and the head: the step's own kernels, grids and bytes, back to back
+    in step order), replayed; returns (algorithmic bytes of those launches,
+    launches, average ms per launch, whole-token bytes)."""
+    import torch
+    from swiftrwkv_amd import _lib, synthetic as syn
+    from swiftrwkv_amd.x070 import X070Decoder
+
+    s = model.shape
+    dense = syn.x070_dense_params(s, seed=11)
+    dec = X070Decoder(s.n_layer, s.n_embd, s.ffn, s.vocab, dense, model.host, dev)
+    st = dec.new_state(1)
+    ids = torch.randint(0, s.vocab, (1,), dtype=torch.int32, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    lib = _lib.lib
+    proxy = _SkipLaunches(lib(), {"rwkv_x070_tmix_core", "rwkv_layer_norm"})
+    with torch.cuda.stream(stream):
+        dec.launch(ids, st)   # buffers exist before capture
+        torch.cuda.synchronize()
+        _lib.lib = lambda: proxy
+        try:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                dec.launch(ids, st)
+        finally:
+            _lib.lib = lib
+        n = proxy.kept
+        for _ in range(5):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    gemv_bytes, whole_bytes = x070_step_bytes(dec)
+    del dec, g
+    torch.cuda.empty_cache()
+    return gemv_bytes, n, e0.elapsed_time(e1) / (reps * n), whole_bytes
 
 
 def x070_line(model, dev, steps, warmup, copies=1, B=1):
@@ -838,7 +946,8 @@ def profile_kernels(dev, tokens=12):
     """The dominant kernels alone, for rocprofv3: eager 0.1B decode tokens over
     6 rotated weight copies (49 GEMV launches each, the head GEMV among them,
     and 12 WKV step+tail launches), 6 eager 1.5B decode tokens (97 GEMV
-    launches each), the WKV-7 forward at B1 T1024 H12 fp32 (20 launches), the
+    launches each), 4 eager tokens of the whole 1.5B x070 step (123 launches
+    each), the WKV-7 forward at B1 T1024 H12 fp32 (20 launches), the
     time-chunked forward at B1 T1024 H12 (5) and B1 T8192 H64 (2), the
     batched GEMV of a 14336x4096 matrix x 16 rows on the matrix cores over
     K3 weights, over T16 weights and on the VALU kernel (3 each), the
@@ -868,9 +977,21 @@ def profile_kernels(dev, tokens=12):
     for _ in range(6):
         step.launch(0, stream)
     torch.cuda.synchronize()
-    del model, step
-    torch.cuda.empty_cache()
+    del step
     log("1.5B decode tokens done")
+    # 4 eager tokens of the whole 1.5B x070 step (the headline's kernels:
+    # rkv_lora_ln, tmix_core, o_proj, gemv_ln, ffn value per layer, the head)
+    from swiftrwkv_amd.x070 import X070Decoder
+    s = syn.X070_1B5
+    dec = X070Decoder(s.n_layer, s.n_embd, s.ffn, s.vocab, syn.x070_dense_params(s, seed=11), model.host, dev)
+    st = dec.new_state(1)
+    ids = torch.randint(0, s.vocab, (1,), dtype=torch.int32, device=dev)
+    for _ in range(4):
+        dec.launch(ids, st)
+    torch.cuda.synchronize()
+    del model, dec, st
+    torch.cuda.empty_cache()
+    log("1.5B x070 step tokens done")
     x = [torch.from_numpy(z).to(dev) for z in syn.wkv_inputs_config0(1, 1024, 12, seed=0)]
     for _ in range(20):
         K.wkv7_sequence_forward(*x)
@@ -953,23 +1074,29 @@ def headline_1b5(args, dev):
     model = DecodeModel(syn.X070_1B5, 1, dev, nthreads=min(16, os.cpu_count() or 1))
     wall, gpu_ms, launches = run_x070(model, dev, args.steps, args.warmup)
     log(f"x070 decode 1.5B: {args.steps} tokens, wall {wall * 1e3:.2f} ms, gpu {gpu_ms:.2f} ms, {launches} launches")
+    # the roofline: the timed step's own GEMV-bearing launches, in step order
+    sb_bytes, n_sb, sb_avg_ms, token_bytes = bench_step_gemv_launches(model, dev)
+    achieved = sb_bytes / (n_sb * sb_avg_ms * 1e-3) / 1e9
+    log(f"1.5B step GEMV-bearing launches: {n_sb} per token, {sb_bytes / 1e6:.1f} MB, avg {sb_avg_ms * 1e3:.2f} us "
+        f"-> {achieved:.0f} GB/s; whole token {token_bytes / 1e6:.1f} MB")
     step, cwall, cgpu = run_decode(model, dev, 1, 100, 10, 1)
     gemv_bytes, gemv_avg_ms, n_gemv = bench_decode_gemv(model, step, dev)
-    achieved = gemv_bytes / (gemv_avg_ms * 1e-3) / 1e9
-    log(f"1.5B decode GEMV: {n_gemv} launches per token, {gemv_bytes / 1e6:.3f} MB per launch, "
-        f"avg {gemv_avg_ms * 1e3:.2f} us -> {achieved:.0f} GB/s")
+    gemv_only = gemv_bytes / (gemv_avg_ms * 1e-3) / 1e9
+    log(f"1.5B decode GEMV (plain launches): {n_gemv} launches per token, {gemv_bytes / 1e6:.3f} MB per launch, "
+        f"avg {gemv_avg_ms * 1e3:.2f} us -> {gemv_only:.0f} GB/s")
     chain = {"tok_s": 100 / cwall, "ms_per_token": cwall * 10, "gemv_bytes_per_token": model.bytes_per_token,
              "effective_GBps": model.bytes_per_token / (cwall * 1e-2) / 1e9,
              "gemv_launches_per_token": n_gemv, "gemv_avg_us": gemv_avg_ms * 1e3,
-             "gemv_kernel_us_per_token": gemv_avg_ms * 1e3 * n_gemv}
+             "gemv_kernel_us_per_token": gemv_avg_ms * 1e3 * n_gemv,
+             "gemv_hbm_frac": gemv_only / HBM_PEAK_GBPS, "gemv_traffic": DECODE_1B5_GEMV_TRAFFIC_BYTES}
     cpu = None if args.skip_cpu else cpu_baseline(model, step, args.cpu_seconds, dev)
     # the same chain for 16 rows (batched decode: the matrix-core GEMVs over T16 copies)
     del step
     _, bwall, _ = run_decode(model, dev, 16, 30, 4, 1)
     batch16 = {"tok_s": 16 * 30 / bwall, "ms_per_step": bwall * 1e3 / 30}
     log(f"1.5B decode batch 16: {bwall * 1e3 / 30:.3f} ms per step")
-    res = {"wall": wall, "gpu_ms": gpu_ms, "launches": launches, "achieved": achieved, "n_gemv": n_gemv,
-           "gemv_bytes": gemv_bytes, "chain": chain, "cpu": cpu, "bytes_per_token": model.bytes_per_token,
+    res = {"wall": wall, "gpu_ms": gpu_ms, "launches": launches, "achieved": achieved, "n_sb": n_sb,
+           "sb_bytes": sb_bytes, "sb_avg_ms": sb_avg_ms, "token_bytes": token_bytes, "chain": chain, "cpu": cpu,
            "batch16": batch16}
     del model
     import torch
@@ -1059,10 +1186,17 @@ def main():
                               "seeded, low-rank matrices fp16",
                    "launches_per_token": head["launches"], "hip_graph_per_token": True},
         "roofline": {"bound": "hbm", "achieved": head["achieved"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": head["achieved"] / HBM_PEAK_GBPS, "traffic": DECODE_1B5_GEMV_TRAFFIC_BYTES,
-                     "kernel": f"gemv_kernel (sb6 4-bit), in-graph average over the {head['n_gemv']} GEMV "
-                               f"launches of one 1.5B token; bytes per launch = the token's packed weights + "
-                               f"x + y / launches = {head['gemv_bytes']:.0f}"},
+                     "frac": head["achieved"] / HBM_PEAK_GBPS, "traffic": DECODE_1B5_STEP_GEMV_TRAFFIC_BYTES,
+                     "kernel": f"the timed step's own GEMV-bearing launches ({head['n_sb']} per token: per layer "
+                               f"rkv_lora_ln_kernel, o_proj + residual gemv_kernel, gemv_ln_kernel (ffn key), "
+                               f"ffn value + residual gemv_kernel; the head), replayed back to back in step order "
+                               f"from a graph of the step without its tmix cores and layer norms; average "
+                               f"{head['sb_avg_ms'] * 1e3:.2f} us per launch; bytes per launch = packed "
+                               f"projections + fp16 low-rank inner matrices + fp32 rows / launches = "
+                               f"{head['sb_bytes'] / head['n_sb']:.0f}",
+                     "whole_token": {"bytes": head["token_bytes"],
+                                     "achieved": head["token_bytes"] / (wall / args.steps) / 1e9,
+                                     "frac": head["token_bytes"] / (wall / args.steps) / 1e9 / HBM_PEAK_GBPS}},
         "cpu_baseline": head["cpu"],
         "extra": extra,
     }

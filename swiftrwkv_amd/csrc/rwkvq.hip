@@ -577,21 +577,15 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
         };
         if constexpr (LNC > 0) {
             // The input row formed here: LN(x) and its token-shift lerp.  All
-            // the row loads first (the statistics chunks of threads < T as
-            // the row kernel assigns them, then this thread's LNC staging
-            // chunks e = tid + i·nthr), then the weights; one input row
-            // (rows == 1), IN ≤ 4·LNC·nthr, LNC ≤ 2 and IN ≤ 4096 (checked by
-            // the host).
+            // the row loads first (the lane's statistics chunks of the whole
+            // row, row_chunks, then this thread's LNC staging chunks
+            // e = tid + i·nthr), then the weights; one input row (rows == 1),
+            // IN ≤ 4·LNC·nthr, LNC ≤ 2 and IN ≤ 4096 (checked by the host).
             using namespace rwkv_x070;
-            __shared__ float red[32];
             const int IN4 = IN >> 2;
-            int S_, T, PS;
-            row_geometry(IN, S_, T, PS);
-            const bool on = (int)threadIdx.x < T;
-            float4 sv[4], xo[LNC], pv[LNC], cv[LNC], wv[LNC], bv[LNC];
+            float4 sv[8], xo[LNC], pv[LNC], cv[LNC], wv[LNC], bv[LNC];
             const float* coef = lm.coef + (int64_t)kwg * IN;
-#pragma unroll
-            for (int p = 0; p < 4; ++p) sv[p] = *reinterpret_cast<const float4*>(lm.x + 4 * min((int)threadIdx.x + T * p, IN4 - 1));
+            row_chunks<8>(lm.x, IN, lane, sv);
 #pragma unroll
             for (int i = 0; i < LNC; ++i) {
                 const int e = min((int)threadIdx.x + i * nthr, IN4 - 1);
@@ -603,7 +597,7 @@ __device__ __forceinline__ void gemv_body(int bx, const float* __restrict__ x, i
             }
             load_pass(0, W);
             load_res(res, 0);
-            const float2 md = row_stats<4>(sv, PS, on, IN, lm.eps, red);
+            const float2 md = row_stats<8>(sv, lm.x, IN, lane, lm.eps);
             // chunks past the row repeat the last one (the same values to the
             // same addresses): no branch, so the row loads stay ahead of the
             // weight loads instead of being sunk behind them
@@ -761,7 +755,6 @@ __global__ __launch_bounds__(1024) void rkv_lora_ln_kernel(typename Sb6Fmt<0>::P
     }
     using namespace rwkv_x070;
     extern __shared__ float lds[];
-    __shared__ float red[32];
     const int RT = rw + ra + rv + rg, nthr = 64 * geo.WPB, IN4 = IN >> 2;
     const int job = (int)blockIdx.x * geo.WPB + (threadIdx.x >> 6);
     const int br = lora_branch(min((int)blockIdx.x * geo.WPB, RT - 1), rw, ra, rv);   // uniform
@@ -770,12 +763,8 @@ __global__ __launch_bounds__(1024) void rkv_lora_ln_kernel(typename Sb6Fmt<0>::P
     uint4 first[4];
     lora_in_first<true, 4>(min(job, RT - 1), threadIdx.x & 63, wcat, IN, first);
     const float* coef = lm.coef + (int64_t)(br == 0 ? 3 : br == 1 ? 4 : br == 2 ? 2 : 5) * IN;
-    int S_, T, PS;
-    row_geometry(IN, S_, T, PS);
-    const bool on = (int)threadIdx.x < T;
-    float4 sv[4], xo[LNC], pv[LNC], cv[LNC], wv[LNC], bv[LNC];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) sv[p] = *reinterpret_cast<const float4*>(lm.x + 4 * min((int)threadIdx.x + T * p, IN4 - 1));
+    float4 sv[8], xo[LNC], pv[LNC], cv[LNC], wv[LNC], bv[LNC];
+    row_chunks<8>(lm.x, IN, threadIdx.x & 63, sv);
 #pragma unroll
     for (int i = 0; i < LNC; ++i) {
         const int e = min((int)threadIdx.x + i * nthr, IN4 - 1);
@@ -785,7 +774,7 @@ __global__ __launch_bounds__(1024) void rkv_lora_ln_kernel(typename Sb6Fmt<0>::P
         wv[i] = *reinterpret_cast<const float4*>(lm.w + 4 * e);
         bv[i] = *reinterpret_cast<const float4*>(lm.b + 4 * e);
     }
-    const float2 md = row_stats<4>(sv, PS, on, IN, lm.eps, red);
+    const float2 md = row_stats<8>(sv, lm.x, IN, threadIdx.x & 63, lm.eps);
 #pragma unroll
     for (int i = 0; i < LNC; ++i) {   // past the row: the last chunk again, no branch
         const int e = min((int)threadIdx.x + i * nthr, IN4 - 1);

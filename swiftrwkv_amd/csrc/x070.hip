@@ -42,21 +42,12 @@ __device__ __forceinline__ float sum8_lanes(float v) {
 
 // Row kernels (row_geometry): all of a thread's loads are issued first.
 
-__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
-__device__ __forceinline__ float4 load4(const __half* p) {
-    const uint2 raw = *reinterpret_cast<const uint2*>(p);
-    const float2 a = __half22float2(*reinterpret_cast<const __half2*>(&raw.x));
-    const float2 c = __half22float2(*reinterpret_cast<const __half2*>(&raw.y));
-    return make_float4(a.x, a.y, c.x, c.y);
-}
-
 // y[n] = LN(src(n)); src(n) = x[n] or, with `ids`, row ids[n] of the table x
 // (fp32 or fp16); an id outside [0, rows) gives a NaN row.  Grid (S, N).
-template <typename T, int PS>
+template <typename T, int JH>
 __global__ __launch_bounds__(1024) void layer_norm_kernel(const T* __restrict__ x, const int32_t* ids, int64_t rows,
                                                           const float* __restrict__ w, const float* __restrict__ b,
                                                           float* __restrict__ y, int D, float eps) {
-    __shared__ float red[32];
     const int n = blockIdx.y, T4 = blockDim.x;
     int64_t src = n;
     bool bad = false;
@@ -67,11 +58,10 @@ __global__ __launch_bounds__(1024) void layer_norm_kernel(const T* __restrict__ 
     }
     const T* row = x + src * D;
     const int c = 4 * ((int)blockIdx.x * T4 + (int)threadIdx.x);
-    float4 v[PS];
-#pragma unroll
-    for (int p = 0; p < PS; ++p) v[p] = load4(row + 4 * (threadIdx.x + T4 * p));
+    float4 v[JH];
+    row_chunks<JH>(row, D, threadIdx.x & 63, v);
     const float4 xo = load4(row + c), wv = load4(w + c), bv = load4(b + c);
-    const float2 md = row_stats<PS>(v, PS, true, D, eps, red);
+    const float2 md = row_stats<JH>(v, row, D, threadIdx.x & 63, eps);
     const float nan = __builtin_nanf("");
     *reinterpret_cast<float4*>(y + (int64_t)n * D + c) = bad ? make_float4(nan, nan, nan, nan) : ln_apply(xo, md, wv, bv);
 }
@@ -81,23 +71,21 @@ __global__ __launch_bounds__(1024) void layer_norm_kernel(const T* __restrict__ 
 // coefficient c gives xl + xx·coef[c].  NC = 6 (coefficients r, k, v, w, a, g):
 // out0 [N, 3, D] ← (r, k, v), out1 [N, 4, D] ← (w, a, v, g), the low-rank
 // branches' inputs; NC = 1: out0 [N, D].  Grid (S, N).
-template <int NC, int PS>
+template <int NC, int JH>
 __global__ __launch_bounds__(1024) void shift_mix_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                          const float* __restrict__ b, float* __restrict__ prev,
                                                          const float* __restrict__ coef, float* __restrict__ out0,
                                                          float* __restrict__ out1, int D, float eps) {
-    __shared__ float red[32];
     const int n = blockIdx.y, T4 = blockDim.x;
     const float* row = x + (int64_t)n * D;
     const int c = 4 * ((int)blockIdx.x * T4 + (int)threadIdx.x);
-    float4 v[PS], cv[NC];
-#pragma unroll
-    for (int p = 0; p < PS; ++p) v[p] = load4(row + 4 * (threadIdx.x + T4 * p));
+    float4 v[JH], cv[NC];
+    row_chunks<JH>(row, D, threadIdx.x & 63, v);
     const float4 xo = load4(row + c), wv = load4(w + c), bv = load4(b + c);
     const float4 pv = load4(prev + (int64_t)n * D + c);
 #pragma unroll
     for (int k = 0; k < NC; ++k) cv[k] = load4(coef + (int64_t)k * D + c);
-    const float2 md = row_stats<PS>(v, PS, true, D, eps, red);
+    const float2 md = row_stats<JH>(v, row, D, threadIdx.x & 63, eps);
     const float4 xl = ln_apply(xo, md, wv, bv);
     const float4 xx = shift_delta(pv, xl);
     *reinterpret_cast<float4*>(prev + (int64_t)n * D + c) = xl;
@@ -377,17 +365,12 @@ rwkv_status rwkv_layer_norm(const void* x, rwkv_dtype x_dt, const int32_t* ids, 
     row_geometry(D, S, T, PS);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const dim3 grid((unsigned)S, (unsigned)N), block(T);
-#define RWKV_LN(TY, PV) \
-    rwkv::launch(layer_norm_kernel<TY, PV>, grid, block, st, reinterpret_cast<const TY*>(x), ids, rows, w, b, y, (int)D, eps)
-#define RWKV_LN_P(TY)                    \
-    switch (PS) {                        \
-        case 1: RWKV_LN(TY, 1); break;   \
-        case 2: RWKV_LN(TY, 2); break;   \
-        case 4: RWKV_LN(TY, 4); break;   \
-        default: RWKV_LN(TY, 8); break;  \
-    }
-    RWKV_REQUIRE(PS == 1 || PS == 2 || PS == 4 || PS == 8, RWKV_E_SHAPE,
-                 "layer_norm: D=%lld not taken (D/1024 must be 1, 2, 4 or 8)", (long long)D);
+    // row chunks held per lane for the statistics: D/256 up to 8
+#define RWKV_LN(TY, JV) \
+    rwkv::launch(layer_norm_kernel<TY, JV>, grid, block, st, reinterpret_cast<const TY*>(x), ids, rows, w, b, y, (int)D, eps)
+#define RWKV_LN_P(TY)            \
+    if (D <= 1024) RWKV_LN(TY, 4); \
+    else RWKV_LN(TY, 8);
     if (x_dt == RWKV_F16) {
         RWKV_LN_P(__half)
     } else {
@@ -407,19 +390,13 @@ rwkv_status rwkv_x070_shift_mix(const float* x, const float* lnw, const float* l
                  (long long)D, kRowMax);
     int S, T, PS;
     row_geometry(D, S, T, PS);
-    RWKV_REQUIRE(PS == 1 || PS == 2 || PS == 4 || PS == 8, RWKV_E_SHAPE,
-                 "x070_shift_mix: D=%lld not taken (D/1024 must be 1, 2, 4 or 8)", (long long)D);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const dim3 grid((unsigned)S, (unsigned)N), block(T);
-#define RWKV_SM(NCV, PV) \
-    rwkv::launch(shift_mix_kernel<NCV, PV>, grid, block, st, x, lnw, lnb, prev, coef, out0, out1, (int)D, eps)
-#define RWKV_SM_P(NCV)                    \
-    switch (PS) {                         \
-        case 1: RWKV_SM(NCV, 1); break;   \
-        case 2: RWKV_SM(NCV, 2); break;   \
-        case 4: RWKV_SM(NCV, 4); break;   \
-        default: RWKV_SM(NCV, 8); break;  \
-    }
+#define RWKV_SM(NCV, JV) \
+    rwkv::launch(shift_mix_kernel<NCV, JV>, grid, block, st, x, lnw, lnb, prev, coef, out0, out1, (int)D, eps)
+#define RWKV_SM_P(NCV)              \
+    if (D <= 1024) RWKV_SM(NCV, 4); \
+    else RWKV_SM(NCV, 8);
     if (nc == 6) {
         RWKV_SM_P(6)
     } else {

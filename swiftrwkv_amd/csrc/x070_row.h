@@ -5,6 +5,7 @@
 // arithmetic, so a row formed inside a GEMV launch is bitwise the row kernel's.
 #pragma once
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -13,27 +14,19 @@
 
 namespace rwkv_x070 {
 
-// Sum over the workgroup: per-wave butterfly, then the wave totals in wave
-// order; every thread gets the same value.  `red` (16 floats) is used once
-// per kernel, so no barrier is needed before it is written.  Waves whose
-// threads pass 0 add +0.0, which leaves the total unchanged.
-__device__ __forceinline__ float block_total(float v, float* red) {
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    v = rwkv_wkv::wave_total(v);
-    if ((threadIdx.x & 63) == 0) red[wave] = v;
-    __syncthreads();
-    float t = red[0];
-    for (int i = 1; i < nw; ++i) t += red[i];
-    return t;
-}
-
 __device__ __forceinline__ float sum4(float4 a) { return (a.x + a.y) + (a.z + a.w); }
+
+__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4(const __half* p) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(p);
+    const float2 a = __half22float2(*reinterpret_cast<const __half2*>(&raw.x));
+    const float2 c = __half22float2(*reinterpret_cast<const __half2*>(&raw.y));
+    return make_float4(a.x, a.y, c.x, c.y);
+}
 
 // Row kernels: a row of D is split over S workgroups of T threads (S = D/1024
 // with T = 256 when 1024 divides D, else S = 1 with T = D/4); thread t of
-// slice s writes the float4 chunk s·T + t.  Every workgroup forms the row's
-// statistics itself from the whole row (PS = D/(4T) chunks per thread, the
-// same order in every slice).
+// slice s writes the float4 chunk s·T + t.
 __host__ __device__ inline void row_geometry(int64_t D, int& S, int& T, int& PS) {
     if (D % 1024 == 0) {
         T = 256;
@@ -44,28 +37,40 @@ __host__ __device__ inline void row_geometry(int64_t D, int& S, int& T, int& PS)
     }
 }
 
-// layerNorm_ (X070Generation.swift:511-514): mean, then the mean of squared
-// deviations; the row's (mean, sqrt(var + eps)).  Thread t < T holds chunks
-// t + T·p (p < PS) in v; other threads pass `on` false and add nothing.
-// A chunk left out adds +0.0 (no branch, so a caller's loads of v are not
-// sunk past later ones); the sums are those of the chunks taken, in order.
-template <int PS>
-__device__ __forceinline__ float2 row_stats(const float4 (&v)[PS], int ps, bool on, int D, float eps, float* red) {
+// layerNorm_ (X070Generation.swift:511-514) statistics of a row of D floats
+// (D % 256 == 0), formed by every wave on its own from the whole row: lane l
+// takes the float4 chunks l + 64j (j < D/256) in order, each summed as
+// (x + y) + (z + w); the 64 lane sums meet in wave_total's fixed butterfly.
+// So every wave of every launch (row kernels and the GEMV launches that form
+// their input rows) gets the same bits, with no LDS and no barrier.  The
+// caller loads the first JH chunks with row_chunks ahead of its other loads
+// (chunks past the row repeat the last one: no branch around a load); chunks
+// beyond JH are read again here.
+template <int JH, typename TY>
+__device__ __forceinline__ void row_chunks(const TY* row, int D, int lane, float4 (&v)[JH]) {
+    const int nj = D >> 8;
+#pragma unroll
+    for (int j = 0; j < JH; ++j) v[j] = load4(row + 4 * (lane + 64 * min(j, nj - 1)));
+}
+
+// (mean, sqrt(var + eps)): the mean, then the mean of squared deviations.
+template <int JH, typename TY>
+__device__ __forceinline__ float2 row_stats(const float4 (&v)[JH], const TY* row, int D, int lane, float eps) {
+    const int nj = D >> 8;
     float s = 0.0f;
 #pragma unroll
-    for (int p = 0; p < PS; ++p) {
-        const float a = sum4(v[p]);
-        s += (on && p < ps) ? a : 0.0f;
-    }
-    const float mean = block_total(s, red) / (float)D;   // red[0..15], then red[16..31]
+    for (int j = 0; j < JH; ++j) s += j < nj ? sum4(v[j]) : 0.0f;
+    for (int j = JH; j < nj; ++j) s += sum4(load4(row + 4 * (lane + 64 * j)));
+    const float mean = rwkv_wkv::wave_total(s) / (float)D;
+    auto sq = [mean](float4 x) {
+        const float4 d = make_float4(x.x - mean, x.y - mean, x.z - mean, x.w - mean);
+        return (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+    };
     float q = 0.0f;
 #pragma unroll
-    for (int p = 0; p < PS; ++p) {
-        const float4 d = make_float4(v[p].x - mean, v[p].y - mean, v[p].z - mean, v[p].w - mean);
-        const float a = (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
-        q += (on && p < ps) ? a : 0.0f;
-    }
-    return make_float2(mean, sqrtf(block_total(q, red + 16) / (float)D + eps));
+    for (int j = 0; j < JH; ++j) q += j < nj ? sq(v[j]) : 0.0f;
+    for (int j = JH; j < nj; ++j) q += sq(load4(row + 4 * (lane + 64 * j)));
+    return make_float2(mean, sqrtf(rwkv_wkv::wave_total(q) / (float)D + eps));
 }
 
 __device__ __forceinline__ float4 ln_apply(float4 x, float2 md, float4 w, float4 b) {
