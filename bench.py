@@ -55,8 +55,8 @@ DECODE_GEMV_TRAFFIC_BYTES = 1744043
 DECODE_1B5_GEMV_TRAFFIC_BYTES = 8291062
 # The same for the average GEMV-bearing launch of the 1.5B x070 step (per layer
 # the r/k/v + low-rank, o_proj, ffn key and ffn value launches, and the head);
-# profiles/hbm_traffic_decode_1.5B_step.md.  None until measured.
-DECODE_1B5_STEP_GEMV_TRAFFIC_BYTES = None
+# profiles/counters_decode_1.5B_step.md.
+DECODE_1B5_STEP_GEMV_TRAFFIC_BYTES = 9027701
 VALU_PEAK_TFLOPS = 157.3
 
 
@@ -74,9 +74,10 @@ def parse():
     p.add_argument("--skip-wkv", action="store_true")
     p.add_argument("--skip-more", action="store_true", help="skip batched / 7B-class decode and the prefill pass")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--mode", choices=["bench", "kernels", "e2e", "batch"], default="bench",
+    p.add_argument("--mode", choices=["bench", "kernels", "e2e", "batch", "step"], default="bench",
                    help="kernels: run each dominant kernel alone (for rocprofv3 counter passes); "
-                        "e2e / batch: x070 decode tokens / batched GEMV + WKV decode steps only (for kernel traces)")
+                        "e2e / batch: x070 decode tokens / batched GEMV + WKV decode steps only (for kernel traces); "
+                        "step: the 1.5B headline step alone (eager tokens, then graph replays; counter passes)")
     return p.parse_args()
 
 
@@ -1034,6 +1035,49 @@ def profile_kernels(dev, tokens=12):
     log("kernels done")
 
 
+def profile_step(dev, tokens=4, replays=20):
+    """The 1.5B headline step alone, for rocprofv3 counter passes: a plain
+    256 MiB device copy (the counters' calibration), `tokens` eager x070
+    decode tokens of the 1.5B shape (123 launches each: per layer
+    rkv_lora_ln, tmix_core, o_proj, gemv_ln, ffn value; emb + ln0, ln_out,
+    head), then `replays` replays of the token's HIP graph, then 5 + `replays`
+    replays of the graph the headline's roofline is measured on (the same
+    step without its tmix cores and layer norms)."""
+    import torch
+    from swiftrwkv_amd import synthetic as syn
+    from swiftrwkv_amd.x070 import X070Decoder
+
+    src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    s = syn.X070_1B5
+    model = DecodeModel(s, 1, dev, nthreads=min(16, os.cpu_count() or 1))
+    dec = X070Decoder(s.n_layer, s.n_embd, s.ffn, s.vocab, syn.x070_dense_params(s, seed=11), model.host, dev)
+    st = dec.new_state(1)
+    ids = torch.randint(0, s.vocab, (1,), dtype=torch.int32, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        for _ in range(tokens):
+            dec.launch(ids, st)
+        torch.cuda.synchronize()
+        log("eager tokens done")
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            dec.launch(ids, st)
+        for _ in range(replays):
+            g.replay()
+        torch.cuda.synchronize()
+    log("graph replays done")
+    del dec, st, g
+    torch.cuda.empty_cache()
+    # the roofline's graph: the same step without its tmix cores and layer norms
+    _, n, avg_ms, _ = bench_step_gemv_launches(model, dev, reps=replays)
+    log(f"GEMV-bearing launches graph: {n} launches, {avg_ms * 1e3:.2f} us per launch")
+
+
 def profile_x070(dev, tokens=20):
     """End-to-end x070 decode tokens (HIP graph replays) of the 0.1B and
     7B-class shapes, batch 1, for kernel traces."""
@@ -1157,6 +1201,9 @@ def main():
         return
     if args.mode == "batch":
         profile_batch(dev)
+        return
+    if args.mode == "step":
+        profile_step(dev)
         return
     head = headline_1b5(args, dev)
     extra = {"decode_1.5B_gemv_wkv_chain_batch1": head["chain"], "decode_1.5B_batch16": head["batch16"]}

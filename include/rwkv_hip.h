@@ -299,8 +299,8 @@ rwkv_status rwkv_sym_gemv_ep(const float* x, int64_t N,
  * 733-739): y = fp16(fp16(x)·fp16(W)ᵀ) where fp16(W) is exactly the dequant
  * rwkv_sb6_dequant(out_dt = f16) stores, products summed in fp32, the sum
  * rounded to fp16 (the fp16 matmul's output) — computed from the K3 bytes
- * without writing the dense weight.  4-bit sb6 only; OUT and out_per
- * multiples of 256, IN of 256 (rwkv_sb6_gemm_applies).
+ * without writing the dense weight.  sb6 with 4, 5 or 6-bit codes (xbits
+ * 0..2); OUT and out_per multiples of 128, IN of 256 (rwkv_sb6_gemm_applies).
  * x [groups][M][lda] in x_dt (f32 or f16; groups = OUT / out_per, matrix g
  * at x + g·x_group_stride elements): output feature o reads group o / out_per,
  * so r/k/v with their own inputs run as one launch.  y [M][ldy]:
@@ -310,6 +310,16 @@ int rwkv_sb6_gemm_applies(int64_t OUT, int64_t IN, int xbits, int64_t out_per);
 rwkv_status rwkv_sb6_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda, int64_t x_group_stride,
                           const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, void* y, int64_t ldy,
                           int64_t OUT, int64_t IN, int xbits, int64_t out_per, int epilogue, void* stream);
+
+/* The same long pass for sym matrices (8-bit codes, or 6-bit in the loader's
+ * interleave; qs [OUT, IN/16] int8, d [OUT, IN/256] fp16): fp16(W) is exactly
+ * what rwkv_sym_dequant(out_dt = f16) stores (the fp16 branch of
+ * rwkvqDequantSym computes in half, RwkvqDequant.swift:350-388), the rest as
+ * rwkv_sb6_gemm (arguments, groups, epilogues, rwkv_sym_gemm_applies). */
+int rwkv_sym_gemm_applies(int64_t OUT, int64_t IN, int bits, int64_t out_per);
+rwkv_status rwkv_sym_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda, int64_t x_group_stride,
+                          const uint8_t* qblk, const uint8_t* qs, const uint16_t* d, void* y, int64_t ldy,
+                          int64_t OUT, int64_t IN, int bits, int64_t out_per, int epilogue, void* stream);
 
 /* ───────────────────────── x070 decode step around the hot path ───────────────────────── */
 /* fp32 activations; dense vector parameters fp32 (an fp16 file's values
@@ -584,6 +594,7 @@ typedef struct {
     int64_t sb6_gemm;       /* rwkv_sb6_gemm launches (no reference counter) */
     int64_t seq_chunked;    /* rwkv_wkv7_seq_fwd_chunked launches (no reference counter) */
     int64_t sb6_batch;      /* rwkv_sb6_gemv_batch calls (no reference counter) */
+    int64_t sym_gemm;       /* rwkv_sym_gemm launches (no reference counter) */
 } rwkv_counters;
 
 void rwkv_get_counters(rwkv_counters* out);

@@ -260,6 +260,16 @@ def sb6_matmul_f16_base(x, qblk, qsqm, ddm, OUT, IN, xbits=0):
     return x16 @ W16.T, np.abs(x16) @ np.abs(W16).T
 
 
+def sym_matmul_f16_base(x, qblk, qs, d, OUT, IN, bits):
+    """sb6_matmul_f16_base for a sym matrix: W16 = the fp16 dequant of
+    rwkvqDequantSym (RwkvqDequant.swift:350-388, its fp16 branch computing in
+    half), x rounded to fp16, the product summed exactly.  Returns (exact
+    [N, OUT], magnitude Σ|x16·w16| [N, OUT])."""
+    W16 = sym_dequant(qblk, qs, d, OUT, IN, bits, "f16").view(np.float16).astype(np.float64)
+    x16 = np.asarray(x, np.float32).reshape(-1, IN).astype(np.float16).astype(np.float64)
+    return x16 @ W16.T, np.abs(x16) @ np.abs(W16).T
+
+
 # ───────────────────────────── CPU baseline ─────────────────────────────
 
 def cpu_sb6_dequant_matvec(x, qblk, qsqm, ddm, OUT, IN, xbits, nthreads):

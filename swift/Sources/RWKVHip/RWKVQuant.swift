@@ -242,4 +242,20 @@ public final class RwkvqDeviceSidecar {
                                 Int64(info.inFeatures), Int32(info.xbits), Int64(info.outFeatures), 0, streamArg))
         return y
     }
+
+    /// sb6LongPass for a sym matrix (8-bit codes or the 6-bit interleave):
+    /// fp16(W) is the fp16 branch of rwkvqDequantSym (RwkvqDequant.swift:350-388).
+    public func symLongPass(_ key: String, _ x: DeviceArray) throws -> DeviceArray? {
+        guard let info = file.tensors[key], info.kind == .sym, x.shape.count == 2,
+              x.shape[1] == info.inFeatures, x.dtype == .float32 || x.dtype == .float16,
+              rwkv_sym_gemm_applies(Int64(info.outFeatures), Int64(info.inFeatures), Int32(info.bits),
+                                    Int64(info.outFeatures)) != 0,
+              let (qblk, qs, d) = arrays[key] else { return nil }
+        let M = x.shape[0]
+        let y = try DeviceArray(shape: [M, info.outFeatures], dtype: .float32)
+        try check(rwkv_sym_gemm(x.raw, x.dtype.code, Int64(M), Int64(info.inFeatures), Int64(M * info.inFeatures),
+                                qblk.u8, qs.u8, d.u16, y.raw, Int64(info.outFeatures), Int64(info.outFeatures),
+                                Int64(info.inFeatures), Int32(info.bits), Int64(info.outFeatures), 0, streamArg))
+        return y
+    }
 }

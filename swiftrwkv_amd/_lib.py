@@ -39,7 +39,7 @@ class Counters(ctypes.Structure):
     _fields_ = [(n, L) for n in ("seq_fwd", "chunk_fwd", "train_fwd", "train_bwd", "step", "tail",
                                  "sb6_dequant", "sym_dequant", "sb6_gemv", "sym_gemv", "sym_fused",
                                  "step_tail", "sb6_fused", "sym_rows", "x070", "sb6_gemm", "seq_chunked",
-                                 "sb6_batch")]
+                                 "sb6_batch", "sym_gemm")]
 
 
 class Finding(ctypes.Structure):
@@ -97,6 +97,8 @@ _SIGS = {
     "rwkv_sym_gemv_ep": (I, [P, L, P, P, P, P, L, L, I, I, P]),
     "rwkv_sb6_gemm_applies": (I, [L, L, I, L]),
     "rwkv_sb6_gemm": (I, [P, I, L, L, L, P, P, P, P, L, L, L, I, L, I, P]),
+    "rwkv_sym_gemm_applies": (I, [L, L, I, L]),
+    "rwkv_sym_gemm": (I, [P, I, L, L, L, P, P, P, P, L, L, L, I, L, I, P]),
     "rwkv_layer_norm": (I, [P, I, P, L, P, P, P, L, L, F, P]),
     "rwkv_x070_seq_shift_mix": (I, [P, P, P, P, P, I, I, P, I, L, L, P, L, L, L, L, L, P]),
     "rwkv_x070_seq_tmix_pre": (I, [P] * 10 + [I, P] + [P] * 7 + [L, L, L, P]),

@@ -18,7 +18,8 @@ void clear_error();
 
 struct Counters {
     std::atomic<int64_t> seq_fwd{0}, chunk_fwd{0}, train_fwd{0}, train_bwd{0}, step{0}, tail{0},
-        sb6_dequant{0}, sym_dequant{0}, sb6_gemv{0}, sym_gemv{0}, sym_fused{0}, step_tail{0}, sb6_fused{0}, sym_rows{0}, x070{0}, sb6_gemm{0}, seq_chunked{0}, sb6_batch{0};
+        sb6_dequant{0}, sym_dequant{0}, sb6_gemv{0}, sym_gemv{0}, sym_fused{0}, step_tail{0}, sb6_fused{0}, sym_rows{0}, x070{0}, sb6_gemm{0}, seq_chunked{0}, sb6_batch{0},
+        sym_gemm{0};
 };
 Counters& counters();
 

@@ -1,28 +1,30 @@
-// sb6 projections of a parallel (prefill) pass on the gfx950 matrix cores.
+// Quantised projections of a parallel (prefill) pass on the gfx950 matrix
+// cores: sb6 (4, 5 or 6-bit codes) and sym (8 or 6-bit codes).
 //
 // The reference's long pass dequantises the whole matrix to the fp16 base
 // type and runs an fp16 matmul, casting the result back to the input type
 // (X070Backbone.baseMatmul, Sources/RWKVGen/X070Backbone.swift:337-356,
-// 733-739; the dequant of RwkvqDequant.swift:116-140).  Here the dequant
+// 733-739; the dequant of RwkvqDequant.swift:116-140 (sb6) and :350-388,
+// 442-466 (sym, whose fp16 branch computes in half)).  Here the dequant
 // happens in the GEMM's operand path: no dense weight is written.  Per
-// element the numbers are the reference's: the weight is
-// fp16(fma(code, half(qs·d), half(qm·dm))) exactly as the dequant kernel
-// stores it, the input is rounded to fp16, products accumulate in fp32 on
-// v_mfma_f32_16x16x32_f16, and the sum is rounded to fp16 (the fp16 matmul's
-// output) before the epilogue.
+// element the numbers are the reference's: the weight is exactly what the
+// dequant kernels store in fp16 — sb6 fp16(fma(code, half(qs·d), half(qm·dm))),
+// sym fp16((code − bias)·half(qs·d)) — the input is rounded to fp16, products
+// accumulate in fp32 on v_mfma_f32_16x16x32_f16, and the sum is rounded to
+// fp16 (the fp16 matmul's output) before the epilogue.
 //
 // Tiling.  A workgroup of 4 waves computes a 128 (input rows) × 128 (output
-// features) tile in stages of 64 columns (two sb6 32-column units); two
+// features) tile in stages of 64 columns (two 32-column units); two
 // workgroups share a CU.  The input tile is staged in LDS as fp16
 // (double-buffered; rows padded to 144 B so the 16 lanes of a row group read
 // distinct banks).  Wave w owns 32 output features — its own weight rows,
 // which no other wave of the workgroup reads — and all 128 input rows: 8 × 2
 // tiles of 16 × 16 accumulators.  Each lane dequantises the 8 weights that
 // are its MFMA B operand (row 16j + (lane & 15), columns 8·(lane >> 4) .. +7
-// of a unit) straight from the K3 bytes (low or high nibbles of one 8-byte
-// load), so a weight is decoded once per workgroup.  The next stage's input
-// and weight bytes are loaded into registers before the current stage's
-// products, so one barrier per stage separates LDS reuse.
+// of a unit) straight from the packed bytes, so a weight is decoded once per
+// workgroup.  The next stage's input and weight bytes are loaded into
+// registers before the current stage's products, so one barrier per stage
+// separates LDS reuse.
 //
 // Operand layout of v_mfma_f32_16x16x32_f16 (lane l, g = l >> 4, i = l & 15):
 // A[m = i][k = 8g .. 8g+7], B[k = 8g .. 8g+7][n = i]; D[m = 4g + r][n = i],
@@ -48,48 +50,165 @@ __device__ __forceinline__ float hround(float x) { return (float)(_Float16)x; }
 struct GemmArgs {
     const void* x;        // inputs [groups][M][lda] (fp32 or fp16)
     int64_t lda, x_gstride;
-    const uint8_t* qblk;  // sb6 4-bit K3: [N][IN/32·16]
-    const uint8_t* qsqm;  // [N][IN/32·2]
-    const uint16_t* ddm;  // [N][IN/256·2]
+    const uint8_t* q;     // codes: sb6 K3 qblk [N][IN/32·(16+4·xbits)], sym qblk (interleaved)
+    const uint8_t* s1;    // sb6 qsqm [N][IN/32·2] / sym qs [N][IN/16]
+    const uint16_t* s2;   // sb6 ddm [N][IN/256·2] / sym d [N][IN/256]
     void* y;              // [M][ldy]: fp32 (epilogues 0, 1) or fp16 (epilogue 2)
     int64_t ldy;
     int M, N, K, out_per;
 };
 
-// One unit's B operand: 8 fp16 weights of one row (`nib`: the 8 bytes whose
-// low or high nibbles are this lane's columns), fp16(fma(code, s, m)) as the
-// dequant kernel stores it.  A 4-bit code byte read as fp8 E4M3 is code·2^-9
-// exactly, so two codes widen per instruction and s carries the 2^9.
-__device__ __forceinline__ half8 dequant8(uint2 nib, int shift, uint32_t sm, uint32_t dd) {
-    const float s = hround((float)(sm & 0xffu) * f16f(dd)) * 512.0f;
-    const float m = hround((float)(int8_t)((sm >> 8) & 0xffu) * f16f(dd >> 16));
-    const uint32_t c0 = (nib.x >> shift) & 0x0F0F0F0Fu, c1 = (nib.y >> shift) & 0x0F0F0F0Fu;
-    const auto p0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c0, false), p1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c0, true);
-    const auto p2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c1, false), p3 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c1, true);
+// 4 bits → the low bit of 4 bytes (RwkvqSb6GEMV.swift:58-67 multiply spread).
+__device__ __forceinline__ uint32_t spread4(uint32_t nib) { return (nib * 0x00204081u) & 0x01010101u; }
+
+// Byte E of w as a float (v_cvt_f32_ubyteE).
+template <int E>
+__device__ __forceinline__ float ubyte(uint32_t w) {
+    return (float)((w >> (8 * E)) & 0xffu);
+}
+
+// Eight code bytes (c0: columns 0..3, c1: 4..7 of the lane's 8) as
+// fp16(fma(code, s, m)): the product and the sum are exact in fp32 for every
+// format here, so the one rounding is the fp16 one.
+__device__ __forceinline__ half8 bytes8_fma(uint32_t c0, uint32_t c1, float s, float m) {
     half8 h;
-    h[0] = (_Float16)fmaf(p0[0], s, m);
-    h[1] = (_Float16)fmaf(p0[1], s, m);
-    h[2] = (_Float16)fmaf(p1[0], s, m);
-    h[3] = (_Float16)fmaf(p1[1], s, m);
-    h[4] = (_Float16)fmaf(p2[0], s, m);
-    h[5] = (_Float16)fmaf(p2[1], s, m);
-    h[6] = (_Float16)fmaf(p3[0], s, m);
-    h[7] = (_Float16)fmaf(p3[1], s, m);
+    h[0] = (_Float16)fmaf(ubyte<0>(c0), s, m);
+    h[1] = (_Float16)fmaf(ubyte<1>(c0), s, m);
+    h[2] = (_Float16)fmaf(ubyte<2>(c0), s, m);
+    h[3] = (_Float16)fmaf(ubyte<3>(c0), s, m);
+    h[4] = (_Float16)fmaf(ubyte<0>(c1), s, m);
+    h[5] = (_Float16)fmaf(ubyte<1>(c1), s, m);
+    h[6] = (_Float16)fmaf(ubyte<2>(c1), s, m);
+    h[7] = (_Float16)fmaf(ubyte<3>(c1), s, m);
     return h;
 }
 
-// A stage's weight bytes for one lane: NT row tiles × 2 units.
-template <int NT>
-struct BRaw {
-    uint2 nib[NT][2];
-    uint32_t sm[NT];   // qsqm of units (u, u+1): 2 bytes each
-    uint32_t dd[NT];   // ddm of the super-block holding both units
+// Weight formats.  A lane (row `row`, column group gq of 8) loads the bytes
+// of its 8 columns of the stage's two units u, u + 1 (Raw) and decodes unit
+// q ∈ {0, 1} into its B operand.
+//
+// sb6 (gs 32, super-block 8 units): unit = 16 B of nibbles (byte c: column c
+// low, c + 16 high) ‖ 4 B qh ‖ 4 B qh2 (bit c: bit 4 / 5 of column c) for
+// 4 + XB bit codes; qsqm (qs, qm − 31) per unit; ddm (d, dm) fp16 per
+// super-block (the K3 layout, RwkvqFile.swift:189-212).
+template <int XB>
+struct Sb6W {
+    static constexpr int UB = 16 + 4 * XB;
+    struct Raw {
+        uint2 nib[2];
+        uint32_t hi[2][XB > 0 ? XB : 1];
+        uint32_t sm;   // qsqm of units u, u + 1
+        uint32_t dd;   // ddm of their super-block
+    };
+    __device__ static Raw load(const GemmArgs& g, int64_t row, int u, int gq) {
+        const int NU = g.K >> 5, NSB = g.K >> 8;
+        Raw r;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint8_t* b = g.q + (row * NU + u + q) * UB;
+            // 4-byte aligned only for a 20-byte unit: two dword loads
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(b + 8 * (gq & 1));
+            r.nib[q] = make_uint2(w[0], w[1]);
+#pragma unroll
+            for (int e = 0; e < XB; ++e) r.hi[q][e] = *reinterpret_cast<const uint32_t*>(b + 16 + 4 * e);
+        }
+        r.sm = *reinterpret_cast<const uint32_t*>(g.s1 + (row * NU + u) * 2);
+        r.dd = *reinterpret_cast<const uint32_t*>(g.s2 + (row * NSB + (u >> 3)) * 2);
+        return r;
+    }
+    __device__ static half8 dequant(const Raw& r, int q, int gq) {
+        const uint32_t sm = r.sm >> (16 * q);
+        const int shift = (gq >> 1) * 4;   // columns 16..31 in the high nibbles
+        const uint32_t c0 = (r.nib[q].x >> shift) & 0x0F0F0F0Fu, c1 = (r.nib[q].y >> shift) & 0x0F0F0F0Fu;
+        const float m = hround((float)(int8_t)((sm >> 8) & 0xffu) * f16f(r.dd >> 16));
+        if constexpr (XB == 0) {
+            // a 4-bit code byte read as fp8 E4M3 is code·2^-9 exactly: two
+            // codes widen per instruction and s carries the 2^9
+            const float s = hround((float)(sm & 0xffu) * f16f(r.dd)) * 512.0f;
+            const auto p0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c0, false);
+            const auto p1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c0, true);
+            const auto p2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c1, false);
+            const auto p3 = __builtin_amdgcn_cvt_pk_f32_fp8((int)c1, true);
+            half8 h;
+            h[0] = (_Float16)fmaf(p0[0], s, m);
+            h[1] = (_Float16)fmaf(p0[1], s, m);
+            h[2] = (_Float16)fmaf(p1[0], s, m);
+            h[3] = (_Float16)fmaf(p1[1], s, m);
+            h[4] = (_Float16)fmaf(p2[0], s, m);
+            h[5] = (_Float16)fmaf(p2[1], s, m);
+            h[6] = (_Float16)fmaf(p3[0], s, m);
+            h[7] = (_Float16)fmaf(p3[1], s, m);
+            return h;
+        } else {
+            const float s = hround((float)(sm & 0xffu) * f16f(r.dd));
+            uint32_t a = c0, b = c1;
+#pragma unroll
+            for (int e = 0; e < XB; ++e) {
+                const uint32_t h8 = (r.hi[q][e] >> (8 * gq)) & 0xffu;   // bits of columns 8gq .. 8gq+7
+                a |= spread4(h8 & 0xFu) << (4 + e);
+                b |= spread4(h8 >> 4) << (4 + e);
+            }
+            return bytes8_fma(a, b, s, m);
+        }
+    }
+};
+
+// sym (gs = super-block = 16 columns, RwkvqFile.swift:437-449 interleave):
+// 8-bit: 32 int8 codes per unit (byte c = column c); 6-bit: 24 B per unit —
+// words 0..3 nibbles (register order l0, l1, h0, h1 | l2, l3, h2, h3: word
+// 2·(c / 16) + (c / 4) % 2, low nibbles for c % 8 < 4), word 4 qh, word 5 qh2,
+// codes stored + 32.  qs int8 per 16 columns, d fp16 per 256 columns;
+// w = (code − bias)·half(qs·d).
+template <int BITS>
+struct SymW {
+    static constexpr int UB = BITS == 8 ? 32 : 24;
+    struct Raw {
+        uint2 c[2];
+        uint32_t hi[2][BITS == 8 ? 1 : 2];
+        uint32_t qs;   // the four 16-column scales of units u, u + 1
+        uint32_t d;    // super-block scale (fp16)
+    };
+    __device__ static Raw load(const GemmArgs& g, int64_t row, int u, int gq) {
+        const int NU = g.K >> 5, NSB = g.K >> 8;
+        Raw r;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint8_t* b = g.q + (row * NU + u + q) * UB;
+            if constexpr (BITS == 8) {
+                r.c[q] = *reinterpret_cast<const uint2*>(b + 8 * gq);
+            } else {
+                r.c[q] = *reinterpret_cast<const uint2*>(b + 8 * (gq >> 1));
+                r.hi[q][0] = *reinterpret_cast<const uint32_t*>(b + 16);
+                r.hi[q][1] = *reinterpret_cast<const uint32_t*>(b + 20);
+            }
+        }
+        r.qs = *reinterpret_cast<const uint32_t*>(g.s1 + row * (g.K >> 4) + 2 * u);
+        r.d = g.s2[row * NSB + (u >> 3)];
+        return r;
+    }
+    __device__ static half8 dequant(const Raw& r, int q, int gq) {
+        const float s = hround((float)(int8_t)((r.qs >> (8 * (2 * q + (gq >> 1)))) & 0xffu) * f16f(r.d));
+        if constexpr (BITS == 8) {
+            // int8 codes as unsigned bytes code + 128: (u − 128)·s exactly
+            return bytes8_fma(r.c[q].x ^ 0x80808080u, r.c[q].y ^ 0x80808080u, s, -128.0f * s);
+        } else {
+            const int shift = (gq & 1) * 4;
+            uint32_t a = (r.c[q].x >> shift) & 0x0F0F0F0Fu, b = (r.c[q].y >> shift) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t h8 = (r.hi[q][e] >> (8 * gq)) & 0xffu;
+                a |= spread4(h8 & 0xFu) << (4 + e);
+                b |= spread4(h8 >> 4) << (4 + e);
+            }
+            return bytes8_fma(a, b, s, -32.0f * s);
+        }
+    }
 };
 
 // MT × 16 input rows × (4 waves × NT × 16) output features per workgroup.
 // A stage's inputs: thread t stages row t / TPR, EPT consecutive columns.
-template <typename TA, int EP, int MT, int NT>
-__global__ __launch_bounds__(256, 2) void sb6_gemm_kernel(GemmArgs g) {
+template <class F, typename TA, int EP, int MT, int NT>
+__global__ __launch_bounds__(256, 2) void quant_gemm_kernel(GemmArgs g) {
     constexpr int BM = 16 * MT, BN = 64 * NT;
     constexpr int TPR = 256 / BM;        // staging threads per row
     constexpr int EPT = BK / TPR;        // columns per staging thread
@@ -108,7 +227,6 @@ __global__ __launch_bounds__(256, 2) void sb6_gemm_kernel(GemmArgs g) {
     if (tile_m * BM >= g.M) return;
     const int n0 = tile_n * BN;
     const int m0 = tile_m * BM;
-    const int NU = g.K >> 5, NSB = g.K >> 8;
     const int nst = g.K / BK;
 
     // input rows of this tile come from the matrix group its output features belong to
@@ -117,8 +235,6 @@ __global__ __launch_bounds__(256, 2) void sb6_gemm_kernel(GemmArgs g) {
     const TA* xrow = xg + (int64_t)min(m0 + srow, g.M - 1) * g.lda + scol;
 
     const int nb = n0 + wave * (16 * NT) + li;   // weight row of tile j: nb + 16 j
-    const int shift = (gq >> 1) * 4;
-    const int nibo = 8 * (gq & 1);
 
     auto load_a = [&](int st) {
         uint4 a[AV];
@@ -148,23 +264,19 @@ __global__ __launch_bounds__(256, 2) void sb6_gemm_kernel(GemmArgs g) {
             for (int e = 0; e < AV; ++e) *reinterpret_cast<uint4*>(d + 8 * e) = a.v[e];
         }
     };
+    using Raw = typename F::Raw;
+    struct BRaw {
+        Raw t[NT];
+    };
     auto load_b = [&](int st) {
-        BRaw<NT> b;
-        const int u = st * 2;
+        BRaw b;
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const int64_t row = nb + 16 * j;
-            const uint8_t* q = g.qblk + (row * NU + u) * 16 + nibo;
-            b.nib[j][0] = *reinterpret_cast<const uint2*>(q);
-            b.nib[j][1] = *reinterpret_cast<const uint2*>(q + 16);
-            b.sm[j] = *reinterpret_cast<const uint32_t*>(g.qsqm + (row * NU + u) * 2);
-            b.dd[j] = *reinterpret_cast<const uint32_t*>(g.ddm + (row * NSB + (u >> 3)) * 2);
-        }
+        for (int j = 0; j < NT; ++j) b.t[j] = F::load(g, nb + 16 * j, st * 2, gq);
         return b;
     };
-    auto dequant = [&](const BRaw<NT>& b, int q, half8* bop) {
+    auto dequant = [&](const BRaw& b, int q, half8* bop) {
 #pragma unroll
-        for (int j = 0; j < NT; ++j) bop[j] = dequant8(b.nib[j][q], shift, b.sm[j] >> (16 * q), b.dd[j]);
+        for (int j = 0; j < NT; ++j) bop[j] = F::dequant(b.t[j], q, gq);
     };
     // MT × NT MFMAs of unit q of the staged buffer
     f32x4 acc[MT][NT];
@@ -183,7 +295,7 @@ __global__ __launch_bounds__(256, 2) void sb6_gemm_kernel(GemmArgs g) {
     };
 
     auto ar = load_a(0);
-    BRaw<NT> bcur = load_b(0);
+    BRaw bcur = load_b(0);
     store_a(0, ar);
     half8 b0[NT], b1[NT];
     dequant(bcur, 0, b0);
@@ -195,7 +307,7 @@ __global__ __launch_bounds__(256, 2) void sb6_gemm_kernel(GemmArgs g) {
     for (int st = 0; st < nst; ++st) {
         const int buf = st & 1;
         const bool more = st + 1 < nst;
-        BRaw<NT> bnxt = bcur;
+        BRaw bnxt = bcur;
         if (more) {
             ar = load_a(st + 1);
             bnxt = load_b(st + 1);
@@ -247,10 +359,42 @@ __global__ __launch_bounds__(256, 2) void sb6_gemm_kernel(GemmArgs g) {
 // One tile shape: 128 × 128 with two workgroups per CU measured fastest
 // (larger tiles cost occupancy: at one wave per SIMD the stage's loads are
 // not hidden).
-template <typename TA, int EP>
+template <class F, typename TA, int EP>
 void launch_gemm(const GemmArgs& g, hipStream_t s) {
     const int64_t blocks = (int64_t)((g.M + 8 * 128 - 1) / (8 * 128)) * 8 * (g.N / 128);
-    rwkv::launch(sb6_gemm_kernel<TA, EP, 8, 2>, dim3((unsigned)blocks), dim3(256), s, g);
+    rwkv::launch(quant_gemm_kernel<F, TA, EP, 8, 2>, dim3((unsigned)blocks), dim3(256), s, g);
+}
+
+template <class F>
+void launch_gemm_ep(const GemmArgs& g, bool f16, int epilogue, hipStream_t s) {
+    switch (epilogue) {
+        case 0: f16 ? launch_gemm<F, _Float16, 0>(g, s) : launch_gemm<F, float, 0>(g, s); break;
+        case 1: f16 ? launch_gemm<F, _Float16, 1>(g, s) : launch_gemm<F, float, 1>(g, s); break;
+        default: f16 ? launch_gemm<F, _Float16, 2>(g, s) : launch_gemm<F, float, 2>(g, s); break;
+    }
+}
+
+bool gemm_shape_ok(int64_t OUT, int64_t IN, int64_t out_per) {
+    return OUT >= 128 && OUT % 128 == 0 && IN >= 256 && IN % 256 == 0 && out_per >= 128 && out_per % 128 == 0 &&
+           OUT % out_per == 0 && OUT <= ((int64_t)1 << 30) && IN <= ((int64_t)1 << 24);
+}
+
+// Shared argument checks of the two entry points.
+rwkv_status gemm_check(const char* who, const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda,
+                       int64_t x_group_stride, int64_t ldy, int64_t OUT, int64_t IN, int64_t out_per, int epilogue) {
+    RWKV_REQUIRE(x_dt == RWKV_F32 || x_dt == RWKV_F16, RWKV_E_DTYPE, "%s: inputs must be f32 or f16", who);
+    RWKV_REQUIRE(epilogue >= 0 && epilogue <= 2, RWKV_E_SHAPE, "%s: epilogue %d", who, epilogue);
+    RWKV_REQUIRE(M >= 1 && M <= ((int64_t)1 << 24), RWKV_E_SHAPE, "%s: M (%lld) out of range", who, (long long)M);
+    const int64_t groups = OUT / out_per;
+    const int64_t xes = x_dt == RWKV_F32 ? 4 : 2;
+    RWKV_REQUIRE(lda >= IN && lda % 8 == 0 && (groups == 1 || x_group_stride >= M * lda), RWKV_E_SHAPE,
+                 "%s: lda (%lld) must be >= IN and a multiple of 8; groups need x_group_stride >= M·lda", who,
+                 (long long)lda);
+    RWKV_REQUIRE(ldy >= OUT && (epilogue == 2 ? ldy % 2 == 0 : true), RWKV_E_SHAPE, "%s: ldy (%lld) < OUT", who,
+                 (long long)ldy);
+    RWKV_REQUIRE((reinterpret_cast<uintptr_t>(x) % 16) == 0 && (x_group_stride * xes) % 16 == 0, RWKV_E_SHAPE,
+                 "%s: inputs must be 16-byte aligned", who);
+    return RWKV_OK;
 }
 
 }  // namespace
@@ -258,39 +402,50 @@ void launch_gemm(const GemmArgs& g, hipStream_t s) {
 extern "C" {
 
 int rwkv_sb6_gemm_applies(int64_t OUT, int64_t IN, int xbits, int64_t out_per) {
-    return xbits == 0 && OUT >= 128 && OUT % 128 == 0 && IN >= 256 && IN % 256 == 0 && out_per >= 128 &&
-           out_per % 128 == 0 && OUT % out_per == 0 && OUT <= ((int64_t)1 << 30) && IN <= ((int64_t)1 << 24);
+    return xbits >= 0 && xbits <= 2 && gemm_shape_ok(OUT, IN, out_per);
 }
 
 rwkv_status rwkv_sb6_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda, int64_t x_group_stride,
                           const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, void* y, int64_t ldy,
                           int64_t OUT, int64_t IN, int xbits, int64_t out_per, int epilogue, void* stream) {
     RWKV_REQUIRE(x && qblk && qsqm && ddm && y, RWKV_E_NULL, "sb6_gemm: null buffer");
-    RWKV_REQUIRE(x_dt == RWKV_F32 || x_dt == RWKV_F16, RWKV_E_DTYPE, "sb6_gemm: inputs must be f32 or f16");
-    RWKV_REQUIRE(epilogue >= 0 && epilogue <= 2, RWKV_E_SHAPE, "sb6_gemm: epilogue %d", epilogue);
     RWKV_REQUIRE(rwkv_sb6_gemm_applies(OUT, IN, xbits, out_per), RWKV_E_UNSUPPORTED,
-                 "sb6_gemm: 4-bit sb6 with OUT (%lld) and out_per (%lld) multiples of 128 and IN (%lld) of 256",
+                 "sb6_gemm: xbits %d (0..2), OUT (%lld) and out_per (%lld) multiples of 128, IN (%lld) of 256", xbits,
                  (long long)OUT, (long long)out_per, (long long)IN);
-    RWKV_REQUIRE(M >= 1 && M <= ((int64_t)1 << 24), RWKV_E_SHAPE, "sb6_gemm: M (%lld) out of range", (long long)M);
-    const int64_t groups = OUT / out_per;
-    const int64_t xes = x_dt == RWKV_F32 ? 4 : 2;
-    RWKV_REQUIRE(lda >= IN && lda % 8 == 0 && (groups == 1 || x_group_stride >= M * lda), RWKV_E_SHAPE,
-                 "sb6_gemm: lda (%lld) must be >= IN and a multiple of 8; groups need x_group_stride >= M·lda",
-                 (long long)lda);
-    RWKV_REQUIRE(ldy >= OUT && (epilogue == 2 ? ldy % 2 == 0 : true), RWKV_E_SHAPE, "sb6_gemm: ldy (%lld) < OUT",
-                 (long long)ldy);
-    RWKV_REQUIRE((reinterpret_cast<uintptr_t>(x) % 16) == 0 && (x_group_stride * xes) % 16 == 0, RWKV_E_SHAPE,
-                 "sb6_gemm: inputs must be 16-byte aligned");
+    const rwkv_status c = gemm_check("sb6_gemm", x, x_dt, M, lda, x_group_stride, ldy, OUT, IN, out_per, epilogue);
+    if (c != RWKV_OK) return c;
     GemmArgs g{x, lda, x_group_stride, qblk, qsqm, ddm, y, ldy, (int)M, (int)OUT, (int)IN, (int)out_per};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const bool f16 = x_dt == RWKV_F16;
-    switch (epilogue) {
-        case 0: f16 ? launch_gemm<_Float16, 0>(g, s) : launch_gemm<float, 0>(g, s); break;
-        case 1: f16 ? launch_gemm<_Float16, 1>(g, s) : launch_gemm<float, 1>(g, s); break;
-        default: f16 ? launch_gemm<_Float16, 2>(g, s) : launch_gemm<float, 2>(g, s); break;
-    }
+    if (xbits == 0) launch_gemm_ep<Sb6W<0>>(g, f16, epilogue, s);
+    else if (xbits == 1) launch_gemm_ep<Sb6W<1>>(g, f16, epilogue, s);
+    else launch_gemm_ep<Sb6W<2>>(g, f16, epilogue, s);
     RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "sb6_gemm: launch failed");
     rwkv::counters().sb6_gemm.fetch_add(1);
+    rwkv::clear_error();
+    return RWKV_OK;
+}
+
+int rwkv_sym_gemm_applies(int64_t OUT, int64_t IN, int bits, int64_t out_per) {
+    return (bits == 8 || bits == 6) && gemm_shape_ok(OUT, IN, out_per);
+}
+
+rwkv_status rwkv_sym_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda, int64_t x_group_stride,
+                          const uint8_t* qblk, const uint8_t* qs, const uint16_t* d, void* y, int64_t ldy,
+                          int64_t OUT, int64_t IN, int bits, int64_t out_per, int epilogue, void* stream) {
+    RWKV_REQUIRE(x && qblk && qs && d && y, RWKV_E_NULL, "sym_gemm: null buffer");
+    RWKV_REQUIRE(rwkv_sym_gemm_applies(OUT, IN, bits, out_per), RWKV_E_UNSUPPORTED,
+                 "sym_gemm: %d-bit codes (8 or 6), OUT (%lld) and out_per (%lld) multiples of 128, IN (%lld) of 256",
+                 bits, (long long)OUT, (long long)out_per, (long long)IN);
+    const rwkv_status c = gemm_check("sym_gemm", x, x_dt, M, lda, x_group_stride, ldy, OUT, IN, out_per, epilogue);
+    if (c != RWKV_OK) return c;
+    GemmArgs g{x, lda, x_group_stride, qblk, qs, d, y, ldy, (int)M, (int)OUT, (int)IN, (int)out_per};
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const bool f16 = x_dt == RWKV_F16;
+    if (bits == 8) launch_gemm_ep<SymW<8>>(g, f16, epilogue, s);
+    else launch_gemm_ep<SymW<6>>(g, f16, epilogue, s);
+    RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "sym_gemm: launch failed");
+    rwkv::counters().sym_gemm.fetch_add(1);
     rwkv::clear_error();
     return RWKV_OK;
 }

@@ -160,13 +160,14 @@ void rwkv_get_counters(rwkv_counters* out) {
     out->sb6_gemm = c.sb6_gemm.load();
     out->seq_chunked = c.seq_chunked.load();
     out->sb6_batch = c.sb6_batch.load();
+    out->sym_gemm = c.sym_gemm.load();
 }
 
 void rwkv_reset_counters(void) {
     auto& c = rwkv::counters();
     for (auto* a : {&c.seq_fwd, &c.chunk_fwd, &c.train_fwd, &c.train_bwd, &c.step, &c.tail, &c.sb6_dequant,
                     &c.sym_dequant, &c.sb6_gemv, &c.sym_gemv, &c.sym_fused, &c.step_tail, &c.sb6_fused,
-                    &c.sym_rows, &c.x070, &c.sb6_gemm, &c.seq_chunked, &c.sb6_batch})
+                    &c.sym_rows, &c.x070, &c.sb6_gemm, &c.seq_chunked, &c.sb6_batch, &c.sym_gemm})
         a->store(0);
 }
 

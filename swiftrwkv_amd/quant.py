@@ -550,44 +550,67 @@ def rwkvq_sb6_gemm_applies(out_features: int, in_features: int, xbits: int, out_
     return bool(_lib.lib().rwkv_sb6_gemm_applies(out_features, in_features, xbits, per))
 
 
+def rwkvq_sym_gemm_applies(out_features: int, in_features: int, bits: int, out_per: Optional[int] = None) -> bool:
+    """Whether the matrix-core long pass takes this sym matrix (group)."""
+    per = out_features if out_per is None else out_per
+    return bool(_lib.lib().rwkv_sym_gemm_applies(out_features, in_features, bits, per))
+
+
 _GEMM_EP = {"store": 0, "add": 1, "relu2_f16": 2}
+
+
+def _quant_gemm(entry: str, what: str, x, bufs, out_features: int, in_features: int, code_bits: int, per: int,
+                epilogue: str, out: Optional[torch.Tensor]) -> torch.Tensor:
+    G = out_features // per
+    if x.dim() == 2:
+        x = x.unsqueeze(0)
+    if x.dim() != 3 or x.shape[0] != G or x.shape[2] != in_features:
+        raise ValueError(f"{what} GEMM: input {tuple(x.shape)}, expected [{G}, M, {in_features}]")
+    if x.dtype not in (torch.float32, torch.float16):
+        x = x.float()
+    x = _aligned(x)
+    M = x.shape[1]
+    ep = _GEMM_EP[epilogue]
+    ydt = torch.float16 if ep == 2 else torch.float32
+    if out is None:
+        if ep == 1:
+            raise ValueError(f"{what} GEMM: the add epilogue needs `out`")
+        out = torch.empty((M, out_features), dtype=ydt, device=x.device)
+    elif out.dtype != ydt or tuple(out.shape) != (M, out_features) or not out.is_contiguous() or \
+            out.device != x.device:
+        raise ValueError(f"{what} GEMM: out must be a contiguous {ydt} [{M}, {out_features}] tensor on {x.device}")
+    _lib.call(entry, x.data_ptr(), _OUT_DT[x.dtype], M, in_features, M * in_features, *[b.data_ptr() for b in bufs],
+              out.data_ptr(), out_features, out_features, in_features, code_bits, per, ep, _stream(x))
+    return out
 
 
 def rwkvq_sb6_gemm(x, qblk, qsqm, ddm, out_features: int, in_features: int, xbits: int = 0,
                    out_per: Optional[int] = None, epilogue: str = "store",
                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The fp16-base long pass of baseMatmul (X070Backbone.swift:337-356) on
-    the matrix cores, straight from the K3 bytes: y [M, OUT] =
-    fp16(fp16(x)·fp16(W)ᵀ) with fp32 sums.  x [M, IN] (one matrix) or
-    [G, M, IN] (G = OUT / out_per row-concatenated matrices, matrix g reading
-    x[g]), fp32 or fp16.  epilogue "store" / "add" (fp32 `out`, added into) /
-    "relu2_f16" (relu(·)² in an fp16 `out`)."""
+    the matrix cores, straight from the K3 bytes (4, 5 or 6-bit codes): y
+    [M, OUT] = fp16(fp16(x)·fp16(W)ᵀ) with fp32 sums.  x [M, IN] (one matrix)
+    or [G, M, IN] (G = OUT / out_per row-concatenated matrices, matrix g
+    reading x[g]), fp32 or fp16.  epilogue "store" / "add" (fp32 `out`, added
+    into) / "relu2_f16" (relu(·)² in an fp16 `out`)."""
     per = out_features if out_per is None else out_per
     if not rwkvq_sb6_gemm_applies(out_features, in_features, xbits, per):
         raise ValueError(f"sb6 GEMM: [{out_features}, {in_features}] xbits={xbits} out_per={per} not taken")
-    G = out_features // per
-    if x.dim() == 2:
-        x = x.unsqueeze(0)
-    if x.dim() != 3 or x.shape[0] != G or x.shape[2] != in_features:
-        raise ValueError(f"sb6 GEMM: input {tuple(x.shape)}, expected [{G}, M, {in_features}]")
-    if x.dtype not in (torch.float32, torch.float16):
-        x = x.float()
-    x = _aligned(x)
-    M = x.shape[1]
-    qblk, qsqm, ddm = _sb6_bufs(qblk, qsqm, ddm, out_features, in_features, xbits)
-    ep = _GEMM_EP[epilogue]
-    ydt = torch.float16 if ep == 2 else torch.float32
-    if out is None:
-        if ep == 1:
-            raise ValueError("sb6 GEMM: the add epilogue needs `out`")
-        out = torch.empty((M, out_features), dtype=ydt, device=x.device)
-    elif out.dtype != ydt or tuple(out.shape) != (M, out_features) or not out.is_contiguous() or \
-            out.device != x.device:
-        raise ValueError(f"sb6 GEMM: out must be a contiguous {ydt} [{M}, {out_features}] tensor on {x.device}")
-    _lib.call("rwkv_sb6_gemm", x.data_ptr(), _OUT_DT[x.dtype], M, in_features, M * in_features, qblk.data_ptr(),
-              qsqm.data_ptr(), ddm.data_ptr(), out.data_ptr(), out_features, out_features, in_features, xbits, per,
-              ep, _stream(x))
-    return out
+    bufs = _sb6_bufs(qblk, qsqm, ddm, out_features, in_features, xbits)
+    return _quant_gemm("rwkv_sb6_gemm", "sb6", x, bufs, out_features, in_features, xbits, per, epilogue, out)
+
+
+def rwkvq_sym_gemm(x, qblk, qs, d, out_features: int, in_features: int, bits: int,
+                   out_per: Optional[int] = None, epilogue: str = "store",
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """rwkvq_sb6_gemm for sym matrices (8-bit codes, or 6-bit in the loader's
+    interleave): fp16(W) is exactly rwkvq_dequant_sym's fp16 output (the fp16
+    branch of rwkvqDequantSym, RwkvqDequant.swift:350-388)."""
+    per = out_features if out_per is None else out_per
+    if not rwkvq_sym_gemm_applies(out_features, in_features, bits, per):
+        raise ValueError(f"sym GEMM: [{out_features}, {in_features}] bits={bits} out_per={per} not taken")
+    bufs = _sym_bufs(qblk, qs, d, out_features, in_features, bits)
+    return _quant_gemm("rwkv_sym_gemm", "sym", x, bufs, out_features, in_features, bits, per, epilogue, out)
 
 
 def rwkvq_sb6_gemv_batch_applies(rows: int, out_features: int, in_features: int, xbits: int,
@@ -944,9 +967,11 @@ class RwkvqSidecar:
         X070Backbone.baseProj (X070Backbone.swift:676-746, 337-341): on the
         recurrent step (`decode`) or a short parallel pass (B·T ≤ `short_rows`,
         RWKVBlock.swift:418-423) the GEMV kernel on the packed codes; otherwise
-        dequantise to `base_dtype` and matmul in it.  The reference splits the
-        GEMV rows into launches of one (sb6) or four (sym); here all rows go in
-        one launch."""
+        dequantise to `base_dtype` and matmul in it — for an fp16 base and an
+        sb6 / sym matrix the matrix-core GEMM does both from the packed bytes
+        (the same fp16 weights, products and output rounding).  The reference
+        splits the GEMV rows into launches of one (sb6) or four (sym); here all
+        rows go in one launch."""
         info = self.tensors.get(key)
         if info is None:
             raise MissingBuffer(key, "manifest")
@@ -965,6 +990,17 @@ class RwkvqSidecar:
                 y = rwkvq_sym_gemv(x2d.float(), self._buf(key, "qblk"), self._buf(key, "qs"), self._buf(key, "d"),
                                    OUT, IN, info.bits)
             if y is not None:
+                return y.to(x.dtype).reshape(*lead, OUT)
+        if base_dtype == torch.float16:
+            # the fp16 long pass on the matrix cores, straight from the packed bytes
+            xin = x2d if x2d.dtype in (torch.float16, torch.float32) else x2d.float()
+            if info.kind == RwkvqKind.sb6 and rwkvq_sb6_gemm_applies(OUT, IN, info.xbits):
+                y = rwkvq_sb6_gemm(xin, self._buf(key, "qblk"), self._buf(key, "qsqm"), self._buf(key, "ddm"), OUT,
+                                   IN, info.xbits)
+                return y.to(x.dtype).reshape(*lead, OUT)
+            if info.kind == RwkvqKind.sym and rwkvq_sym_gemm_applies(OUT, IN, info.bits):
+                y = rwkvq_sym_gemm(xin, self._buf(key, "qblk"), self._buf(key, "qs"), self._buf(key, "d"), OUT, IN,
+                                   info.bits)
                 return y.to(x.dtype).reshape(*lead, OUT)
         W = self.dequantize(key, base_dtype)   # the transient dense weight, [OUT, IN]
         y = torch.nn.functional.linear(x2d.to(base_dtype), W)

@@ -743,18 +743,23 @@ class X070Decoder:
             return
         parts = q if isinstance(q, list) else [q]
         G = len(parts) if isinstance(q, list) else (q.OUT // q.out_per)
-        if (not isinstance(q, list) and q.kind == "sb6" and q.xbits == 0
-                and _lib.lib().rwkv_sb6_gemm_applies(q.OUT, q.IN, 0, q.out_per)):
-            xdt = _lib.F16 if x.dtype == torch.float16 else _lib.F32
-            _lib.check(_lib.lib().rwkv_sb6_gemm(x.data_ptr(), xdt, M, q.IN, M * q.IN, q.bufs[0].data_ptr(),
-                                                q.bufs[1].data_ptr(), q.bufs[2].data_ptr(), y.data_ptr(), q.OUT, q.OUT,
-                                                q.IN, 0, q.out_per, ep, s))
+        xdt = _lib.F16 if x.dtype == torch.float16 else _lib.F32
+        xs = x.reshape(G, M, -1) if G > 1 else x.reshape(1, M, -1)
+        ldy = y.shape[-1]
+        # the matrix-core long pass (rwkv_sb6_gemm / rwkv_sym_gemm) for every
+        # sb6 / sym matrix it takes: a fused group in one launch, the members
+        # of an unfused r/k/v list each into its columns of y
+        if not isinstance(q, list) and self._long_gemm(q, xs[0].data_ptr(), xdt, M, y.data_ptr(), ldy, ep, s):
             return
+        col, rest = 0, []
+        for g, qq in enumerate(self._split_group(q)):
+            if not (isinstance(q, list) and self._long_gemm(qq, xs[g].data_ptr(), xdt, M,
+                                                           y.data_ptr() + y.element_size() * col, ldy, ep, s)):
+                rest.append((g, col, qq))
+            col += qq.OUT
         # other layouts: the reference's long pass — dequantise to fp16, library GEMM in fp16
         from .quant import rwkvq_dequant_dense, rwkvq_dequant_sym
-        xs = x.reshape(G, M, -1) if G > 1 else x.reshape(1, M, -1)
-        col = 0
-        for g, qq in enumerate(self._split_group(q)):
+        for g, col, qq in rest:
             if qq.kind == "sb6":
                 W = rwkvq_dequant_dense(*qq.bufs, qq.OUT, qq.IN, 8, qq.xbits, torch.float16)
             elif qq.kind == "sym":
@@ -769,7 +774,21 @@ class X070Decoder:
                 dst.add_(prod)
             else:
                 dst.copy_(torch.relu(prod).square_().to(dst.dtype))
-            col += qq.OUT
+
+    @staticmethod
+    def _long_gemm(q, xp, xdt, M, yp, ldy, ep, s) -> bool:
+        """One matrix (group) of the long pass on the matrix cores, when the
+        kernels take its layout; False otherwise (nothing launched)."""
+        L = _lib.lib()
+        if q.kind == "sb6" and L.rwkv_sb6_gemm_applies(q.OUT, q.IN, q.xbits, q.out_per):
+            entry, bits = L.rwkv_sb6_gemm, q.xbits
+        elif q.kind == "sym" and L.rwkv_sym_gemm_applies(q.OUT, q.IN, q.bits, q.out_per):
+            entry, bits = L.rwkv_sym_gemm, q.bits
+        else:
+            return False
+        _lib.check(entry(xp, xdt, M, q.IN, M * q.IN, q.bufs[0].data_ptr(), q.bufs[1].data_ptr(), q.bufs[2].data_ptr(),
+                         yp, ldy, q.OUT, q.IN, bits, q.out_per, ep, s))
+        return True
 
     @staticmethod
     def _split_group(q):

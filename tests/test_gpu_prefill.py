@@ -61,6 +61,76 @@ def test_sb6_gemm_matches_f16_base_pass(orc, M, OUT, IN, xdt):
     assert frac < 5e-2
 
 
+def quant_matrix(orc, fmt, OUT, IN, rng):
+    """A random matrix of layout `fmt` ("sb6:<xbits>", "sym:<bits>") in the
+    loader layout, with the oracle's fp16-base product of it."""
+    from tests.test_gpu_rwkvq import sb6_tensor, sym_tensor
+    kind, b = fmt.split(":")
+    b = int(b)
+    seed = int(rng.integers(0, 1 << 30))
+    if kind == "sb6":
+        bufs = sb6_tensor(orc, OUT, IN, b, seed)
+        base = lambda x: orc.sb6_matmul_f16_base(x, bufs[0], bufs[1], bufs[2].view(np.uint16), OUT, IN, b)
+        gemm = lambda x, w, **kw: Q.rwkvq_sb6_gemm(x, *w, OUT, IN, b, **kw)
+    else:
+        bufs = sym_tensor(orc, OUT, IN, b, seed)
+        base = lambda x: orc.sym_matmul_f16_base(x, bufs[0], bufs[1], bufs[2].view(np.uint16), OUT, IN, b)
+        gemm = lambda x, w, **kw: Q.rwkvq_sym_gemm(x, *w, OUT, IN, b, **kw)
+    return bufs, base, gemm
+
+
+@pytest.mark.parametrize("fmt", ["sb6:1", "sb6:2", "sym:8", "sym:6"])
+@pytest.mark.parametrize("M,OUT,IN", [(1, 256, 256), (37, 768, 768), (300, 3072, 768), (130, 1024, 4096)])
+def test_quant_gemm_layouts_match_f16_base_pass(orc, fmt, M, OUT, IN):
+    """The long pass of the other layouts (sb6 5 / 6-bit, sym 8 / 6-bit) on
+    the matrix cores against the fp16-base oracle (the fp16 dequant's
+    weights, fp16 inputs, an exact sum): within ½ fp16 ulp + 2^-16·Σ|x·w|;
+    fp16 inputs equal fp32 inputs holding the same values."""
+    case(f"quant gemm {fmt} M={M} {OUT}x{IN}")
+    rng = np.random.default_rng(M * 7 + OUT + IN)
+    bufs, base, gemm = quant_matrix(orc, fmt, OUT, IN, rng)
+    w = [dev(z) for z in bufs]
+    x = rng.standard_normal((M, IN)).astype(np.float32)
+    y = gemm(dev(x), w)
+    exact, mag = base(x)
+    frac = check_f16_rounding(y.cpu().numpy(), exact, mag)
+    print(f"[gemm] {fmt} M={M} {OUT}x{IN}: {frac:.2e} of outputs on the other side of an fp16 boundary", flush=True)
+    assert frac < 5e-2
+    x16 = dev(x).to(torch.float16)
+    assert torch.equal(gemm(x16, w), gemm(x16.float(), w))
+
+
+@pytest.mark.parametrize("fmt", ["sb6:2", "sym:6"])
+def test_quant_gemm_layouts_epilogues_and_groups(orc, fmt):
+    """Fused groups equal their members bitwise, rows do not depend on the
+    other rows of the launch, and the add / relu² epilogues are the separate
+    operations' arithmetic."""
+    case(f"quant gemm {fmt} epilogues, groups, rows")
+    D, M = 512, 150
+    rng = np.random.default_rng(17)
+    bufs, _, _ = quant_matrix(orc, fmt, 3 * D, D, rng)
+    w = [dev(z) for z in bufs]
+    kind, b = fmt.split(":")
+    entry = Q.rwkvq_sb6_gemm if kind == "sb6" else Q.rwkvq_sym_gemm
+    x = dev(rng.standard_normal((3, M, D)).astype(np.float32))
+    fused = entry(x, *w, 3 * D, D, int(b), out_per=D)
+    for g in range(3):
+        rows = slice(g * D, (g + 1) * D)
+        part = [z[rows] for z in w]
+        sep = entry(x[g], *part, D, D, int(b))
+        assert torch.equal(fused[:, rows], sep), g
+        for m in (0, 77, 149):
+            assert torch.equal(entry(x[g, m:m + 1], *part, D, D, int(b))[0], sep[m])
+    part = [z[:D] for z in w]
+    y0 = entry(x[1], *part, D, D, int(b))
+    base = dev(rng.standard_normal((M, D)).astype(np.float32))
+    y1 = base.clone()
+    entry(x[1], *part, D, D, int(b), epilogue="add", out=y1)
+    assert torch.equal(y1, base + y0)
+    h = entry(x[1], *part, D, D, int(b), epilogue="relu2_f16")
+    assert h.dtype == torch.float16 and torch.equal(h, (torch.relu(y0) * torch.relu(y0)).to(torch.float16))
+
+
 def test_sb6_gemm_epilogues_groups_and_row_independence(orc):
     case("sb6 gemm epilogues, r/k/v group, rows")
     D, M = 1024, 200
@@ -208,6 +278,61 @@ def test_prefill_then_decode_continues_the_prompt(tiny_model):
         for i, o in enumerate(osts):
             ref = X.step(p, W, [step_ids[i]], o, TINY.n_layer, TINY.n_head)
             assert rel(ref, got[i]) < 1e-4, (step_ids, i)
+
+
+def _mixed_projections(shape, seed=61):
+    """A model whose projections take every long-pass layout of the matrix
+    cores: r/k/v sym 8-bit (one fused group), o_proj sb6 5-bit, ffn key sym
+    6-bit, ffn value sb6 6-bit, head sym 8-bit.  Returns (key → Proj on the
+    device, key → fp64 dense weight of the oracle)."""
+    from oracle import oracle as O
+    from swiftrwkv_amd.x070 import Proj
+    rng = np.random.default_rng(seed)
+    proj, W = {}, {}
+    for key, OUT, IN in shape.projections():
+        w = (rng.standard_normal((OUT, IN)) * 0.02).astype(np.float32)
+        if ".att.output." in key or ".ffn.value." in key:
+            bits = 5 if ".att.output." in key else 6
+            disk = Q.encode_sb6(w, bits, 8)
+            qblk, qsqm, ddm, xb = Q.rwkvq_sb6_to_k3(disk["codes_packed"], disk["gw_qsqm"], disk["gw_d"], disk["gw_dm"],
+                                                    disk.get("gw_qh"), disk.get("gw_qh2"), (OUT, IN))
+            assert xb == bits - 4
+            proj[key] = Proj("sb6", (dev(qblk), dev(qsqm), dev(ddm.view(np.float16))), OUT, IN, bits=bits, xbits=xb)
+            W[key] = O.sb6_dequant(qblk, qsqm, ddm.view(np.uint16), OUT, IN, xb).astype(np.float64)
+        else:
+            bits = 6 if ".ffn.key." in key else 8
+            disk = Q.encode_sym(w, bits, 8)
+            qblk = (disk["codes"].view(np.uint8) if bits == 8 else
+                    Q.rwkvq_sym_interleave(disk["codes_packed"], disk["gw_qh"], disk["gw_qh2"], (OUT, IN)))
+            qs, d = disk["gw_qs"].view(np.uint8), disk["gw_d"]
+            proj[key] = Proj("sym", (dev(qblk), dev(qs), dev(d)), OUT, IN, bits=bits)
+            W[key] = O.sym_dequant(qblk, qs, d.view(np.uint16), OUT, IN, bits).astype(np.float64)
+    return proj, W
+
+
+def test_prefill_fp16_base_sym_and_wide_sb6_layouts():
+    """The fp16 long pass of a model on the sym 8 / 6-bit and sb6 5 / 6-bit
+    layouts (the r/k/v group as one sym launch) against the oracle's parallel
+    pass with the same fp16 rounding points; every projection on the matrix
+    cores (launch counters), none through a dense weight."""
+    case("prefill fp16 base, sym + 5/6-bit sb6 model")
+    from swiftrwkv_amd import _lib
+    proj, W = _mixed_projections(TINY)
+    p = syn.x070_dense_params(TINY, seed=62, lora_dtype=np.float16)
+    dec = X070Decoder(TINY.n_layer, TINY.n_embd, TINY.ffn, TINY.vocab, p, proj, DEV)
+    assert dec.proj["blocks.0.att.rkv"].kind == "sym" and dec.proj["blocks.0.att.rkv"].out_per == TINY.n_embd
+    c0 = _lib.counters()
+    logits, st = dec.prefill_batch(PROMPTS, base_dtype=torch.float16, short_rows=0)
+    c1 = _lib.counters()
+    assert c1["sym_gemm"] - c0["sym_gemm"] == 2 * TINY.n_layer      # r/k/v group, ffn key
+    assert c1["sb6_gemm"] - c0["sb6_gemm"] == 2 * TINY.n_layer      # o_proj, ffn value
+    assert c1["sym_dequant"] == c0["sym_dequant"] and c1["sb6_dequant"] == c0["sb6_dequant"]
+    for i, pr in enumerate(PROMPTS):
+        ref, ost = X.prefill(p, W, pr, TINY.n_layer, TINY.n_head, f16_base=True)
+        e = rel(ref, logits[i].cpu().numpy())
+        ew = rel(ost.wkv[:, 0], st.wkv[:, i].cpu().numpy())
+        print(f"[prefill] sym/sb6 5-6 bit row {i} (T={len(pr)}): logits {e:.2e}, wkv {ew:.2e}", flush=True)
+        assert e < 2e-3 and ew < 2e-3, i
 
 
 def test_prefill_0b4_width_fp16_base(orc):
