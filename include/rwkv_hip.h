@@ -449,6 +449,19 @@ rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float
  * k = k0·(1 + (σ(aa + a_bias) − 1)·k_a), v mixed with v_first [B·T, D] or, at
  * layer 0, written to it), pad steps neutral (w = 1, k = 0, b = 0,
  * :232-237), and k_bonus = k unmasked for the tail. */
+/* The low-rank w / a / v / g branches of the parallel pass (rwkvTmixForward,
+ * Sources/RWKVGen/RWKVBlock.swift:185-226) for M rows: ww = tanh(x_w·A_wᵀ)·B_wᵀ,
+ * aa = (x_a·A_aᵀ)·B_aᵀ, vv = (x_v·A_vᵀ)·B_vᵀ (with_v; layer 0 has no v branch),
+ * gate = sigmoid(x_g·A_gᵀ)·B_gᵀ, in fp32 on the matrix cores (matrices f16 or
+ * f32, widened exactly; no fp16 narrowing on this path).  mix [6, M, D] fp32:
+ * the lerped rows in rwkv_x070_seq_shift_mix's coefficient order (r, k, v, w,
+ * a, g); wcat [rw + ra + rv + rg, D]: A_w, A_a, A_v, A_g stacked; w2 / a2 / v2 /
+ * g2 [D, rank]; la [M, rw + ra + rv + rg] fp32 holds the inner products.
+ * Ranks multiples of 16, D of 16. */
+rwkv_status rwkv_x070_seq_lora(const float* mix, int64_t M, int64_t D, const void* wcat, const void* w2,
+                               const void* a2, const void* v2, const void* g2, rwkv_dtype w_dt, int64_t rw,
+                               int64_t ra, int64_t rv, int64_t rg, int with_v, float* la, float* ww, float* aa,
+                               float* vv, float* gate, void* stream);
 rwkv_status rwkv_x070_seq_tmix_pre(const float* y_rkv, const float* ww, const float* aa, const float* vv,
                                    const float* w_bias, const float* a_bias, const float* v_bias, const float* k_k,
                                    const float* k_a, float* v_first, int layer0, const int32_t* lengths, float* r,

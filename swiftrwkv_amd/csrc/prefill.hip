@@ -122,6 +122,113 @@ __global__ __launch_bounds__(256) void seq_tmix_pre_kernel(
     b_o[e] = real ? kk * a : 0.0f;
 }
 
+// ── the low-rank branches of the parallel pass (rwkvTmixForward,
+// RWKVBlock.swift:185-226) on the matrix cores ──
+// Each branch is two products: h = act(x·Aᵀ) (A [rank, D]; tanh for w,
+// sigmoid for the gate, none for a and v), then h·Bᵀ (B [D, rank]).  The
+// activations are fp32 and the matrices fp16 or fp32: fp16 values widen
+// exactly, so these are fp32 products (MLX promotes the fp16 weight; no `lin`
+// narrowing on this path).  One launch forms a stage of all branches: a job
+// per branch (grid z), y = act(x·Wᵀ) for x [M, K] (row stride ldx), W [N, K].
+// A workgroup of 4 waves computes a 64 × 64 tile of y; wave w the 32 × 32
+// sub-tile (w >> 1, w & 1) as 2 × 2 tiles of v_mfma_f32_16x16x4_f32.  Four
+// MFMAs take 16 K at a time: lane i + 16g provides A[row i][k0 + 4g + r] and
+// B[k0 + 4g + r][col i] in MFMA r (the sum over k does not depend on which K
+// slot carries which k), so each lane reads 16 contiguous bytes of an x row
+// and 4 contiguous weights of a W row.  Sums in fp32, in a fixed order.
+struct LoraJob {
+    const float* x;
+    const void* w;
+    float* y;
+    int N, K, ldx, ldy, act;   // act: 0 none, 1 tanh, 2 sigmoid
+};
+struct LoraJobs {
+    LoraJob j[4];
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma4(float4 a, float4 b, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, c, 0, 0, 0);
+}
+
+template <typename TW>
+__device__ __forceinline__ float4 ldw4(const TW* p) {
+    if constexpr (sizeof(TW) == 4) {
+        return *reinterpret_cast<const float4*>(p);
+    } else {
+        const uint2 u = *reinterpret_cast<const uint2*>(p);
+        const float2 a = __half22float2(*reinterpret_cast<const __half2*>(&u.x));
+        const float2 c = __half22float2(*reinterpret_cast<const __half2*>(&u.y));
+        return make_float4(a.x, a.y, c.x, c.y);
+    }
+}
+
+// MT × NT tiles of 16 × 16 per wave; the four waves 2 × 2, so a workgroup
+// covers (32·MT) rows × (32·NT) columns.
+template <typename TW, int MT, int NT>
+__global__ __launch_bounds__(256) void seq_lora_kernel(LoraJobs jobs, int M) {
+    constexpr int BM = 32 * MT, BN = 32 * NT;
+    const LoraJob J = jobs.j[blockIdx.z];
+    if ((int)blockIdx.x * BN >= J.N) return;   // this job has fewer column tiles (uniform)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, i = lane & 15;
+    const int row0 = (int)blockIdx.y * BM + 16 * MT * (wave >> 1), col0 = (int)blockIdx.x * BN + 16 * NT * (wave & 1);
+    // rows / columns past the end read the last one (results not stored)
+    const float* xr[MT];
+    const TW* wr[NT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) xr[t] = J.x + (int64_t)min(row0 + 16 * t + i, M - 1) * J.ldx + 4 * g;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+        wr[t] = reinterpret_cast<const TW*>(J.w) + (int64_t)min(col0 + 16 * t + i, J.N - 1) * J.K + 4 * g;
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int b = 0; b < NT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // one K step of 16 loaded ahead
+    float4 xa[MT], wb[NT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) xa[t] = *reinterpret_cast<const float4*>(xr[t]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) wb[t] = ldw4(wr[t]);
+    for (int k0 = 0; k0 < J.K; k0 += 16) {
+        const int kn = min(k0 + 16, J.K - 16);   // the last step re-reads itself
+        float4 xn[MT], wn[NT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) xn[t] = *reinterpret_cast<const float4*>(xr[t] + kn);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) wn[t] = ldw4(wr[t] + kn);
+#pragma unroll
+        for (int a = 0; a < MT; ++a)
+#pragma unroll
+            for (int b = 0; b < NT; ++b) acc[a][b] = mfma4(xa[a], wb[b], acc[a][b]);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) xa[t] = xn[t];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) wb[t] = wn[t];
+    }
+    // accumulator lane i + 16g: rows 4g + r, column i of each 16 × 16 tile
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int b = 0; b < NT; ++b) {
+            const int col = col0 + 16 * b + i;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = row0 + 16 * a + 4 * g + r;
+                float v = acc[a][b][r];
+                if (J.act == 1) v = tanhf(v);
+                else if (J.act == 2) v = 1.0f / (1.0f + expf(-v));
+                if (row < M && col < J.N) J.y[(int64_t)row * J.ldy + col] = v;
+            }
+        }
+}
+
 }  // namespace
 
 extern "C" {
@@ -176,6 +283,69 @@ rwkv_status rwkv_x070_seq_tmix_pre(const float* y_rkv, const float* ww, const fl
                  a_bias, v_bias, k_k, k_a, v_first, layer0, lengths, r, w, k, v, a, b, k_bonus, (int)T, (int)H, units);
     RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "x070_seq_tmix_pre: launch failed");
     rwkv::counters().x070.fetch_add(1);
+    rwkv::clear_error();
+    return RWKV_OK;
+}
+
+rwkv_status rwkv_x070_seq_lora(const float* mix, int64_t M, int64_t D, const void* wcat, const void* w2,
+                               const void* a2, const void* v2, const void* g2, rwkv_dtype w_dt, int64_t rw,
+                               int64_t ra, int64_t rv, int64_t rg, int with_v, float* la, float* ww, float* aa,
+                               float* vv, float* gate, void* stream) {
+    RWKV_REQUIRE(mix && wcat && w2 && a2 && g2 && la && ww && aa && gate && (!with_v || (v2 && vv)), RWKV_E_NULL,
+                 "x070_seq_lora: null buffer");
+    RWKV_REQUIRE(w_dt == RWKV_F16 || w_dt == RWKV_F32, RWKV_E_DTYPE, "x070_seq_lora: matrices f16 or f32 (dtype %d)",
+                 (int)w_dt);
+    RWKV_REQUIRE(M >= 1 && M <= ((int64_t)1 << 24) && D >= 16 && D % 16 == 0 && D <= ((int64_t)1 << 20) &&
+                     M * D <= ((int64_t)1 << 31),
+                 RWKV_E_SHAPE, "x070_seq_lora: M=%lld D=%lld (D %% 16 == 0)", (long long)M, (long long)D);
+    RWKV_REQUIRE(rw >= 16 && ra >= 16 && rv >= 16 && rg >= 16 && rw % 16 == 0 && ra % 16 == 0 && rv % 16 == 0 &&
+                     rg % 16 == 0 && rw + ra + rv + rg <= 8192,
+                 RWKV_E_SHAPE, "x070_seq_lora: ranks %lld/%lld/%lld/%lld (multiples of 16)", (long long)rw,
+                 (long long)ra, (long long)rv, (long long)rg);
+    const int64_t RT = rw + ra + rv + rg;
+    RWKV_REQUIRE(M * RT <= ((int64_t)1 << 31), RWKV_E_SHAPE, "x070_seq_lora: M·ranks too large");
+    const int64_t es = w_dt == RWKV_F16 ? 2 : 4;
+    const uintptr_t al = (uintptr_t)mix | (uintptr_t)la | (uintptr_t)wcat | (uintptr_t)w2 | (uintptr_t)a2 |
+                         (uintptr_t)g2 | (uintptr_t)(with_v ? v2 : w2);
+    RWKV_REQUIRE(al % 16 == 0, RWKV_E_SHAPE, "x070_seq_lora: buffers must be 16-byte aligned");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int64_t md = M * D;
+    // mix rows: coefficient order r, k, v, w, a, g (rwkv_x070_seq_shift_mix)
+    const float* xin[4] = {mix + 3 * md, mix + 4 * md, mix + 2 * md, mix + 5 * md};
+    const int64_t rk[4] = {rw, ra, rv, rg};
+    const void* outer[4] = {w2, a2, v2, g2};
+    float* dst[4] = {ww, aa, vv, gate};
+    const int act[4] = {1, 0, 0, 2};
+    // stage 1: la[:, branch] = act(x_branch · A_branchᵀ); stage 2: dst = la[:, branch] · B_branchᵀ
+    LoraJobs s1{}, s2{};
+    int n = 0;
+    int64_t off = 0, maxn1 = 0;
+    for (int b = 0; b < 4; ++b) {
+        if (b == 2 && !with_v) {
+            off += rk[b];
+            continue;
+        }
+        s1.j[n] = LoraJob{xin[b], reinterpret_cast<const char*>(wcat) + off * D * es, la + off, (int)rk[b], (int)D,
+                          (int)D, (int)RT, act[b]};
+        s2.j[n] = LoraJob{la + off, outer[b], dst[b], (int)D, (int)rk[b], (int)RT, (int)D, 0};
+        maxn1 = rk[b] > maxn1 ? rk[b] : maxn1;
+        off += rk[b];
+        ++n;
+    }
+    // 2 × 2 tiles of 16 × 16 per wave (larger wave tiles measured faster only
+    // at the long passes, where the library GEMM is taken instead)
+    constexpr int MT = 2, NT = 2;
+    const dim3 grid1((unsigned)((maxn1 + 32 * NT - 1) / (32 * NT)), (unsigned)((M + 32 * MT - 1) / (32 * MT)), (unsigned)n);
+    const dim3 grid2((unsigned)((D + 32 * NT - 1) / (32 * NT)), (unsigned)((M + 32 * MT - 1) / (32 * MT)), (unsigned)n);
+    if (w_dt == RWKV_F16) {
+        rwkv::launch(seq_lora_kernel<__half, MT, NT>, grid1, dim3(256), st, s1, (int)M);
+        rwkv::launch(seq_lora_kernel<__half, MT, NT>, grid2, dim3(256), st, s2, (int)M);
+    } else {
+        rwkv::launch(seq_lora_kernel<float, MT, NT>, grid1, dim3(256), st, s1, (int)M);
+        rwkv::launch(seq_lora_kernel<float, MT, NT>, grid2, dim3(256), st, s2, (int)M);
+    }
+    RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "x070_seq_lora: launch failed");
+    rwkv::counters().x070.fetch_add(2);
     rwkv::clear_error();
     return RWKV_OK;
 }

@@ -37,6 +37,12 @@ HEAD = 64
 LN_EPS = 1e-5
 LNX_EPS = 64e-5
 _COEF_ORDER = ("r", "k", "v", "w", "a", "g")   # rwkv_x070_shift_mix's coefficient order
+# The parallel pass's low-rank branches take rwkv_x070_seq_lora (two launches,
+# activations fused) up to this many rows × width, the library's fp32 GEMM
+# (plus the activation kernels) above: measured per layer, 0.1B width × 128
+# rows 38 against 138 µs, 1024 × 1024 60 against 66 µs, 4096 × 8192 2.5 against
+# 0.96 ms (hipBLASLt's fp32 GEMM at 116 TFLOP/s there, ours 44).
+SEQ_LORA_MAX_MD = 1 << 21
 
 
 class RWKVState:
@@ -581,7 +587,7 @@ class X070Decoder:
         return self.step(ids, state)
 
     def prefill_batch(self, prompts, base_dtype=torch.float16, short_rows: int = 0,
-                      wkv_chunked: Optional[bool] = None) -> Tuple[torch.Tensor, RWKVState]:
+                      wkv_chunked: Optional[bool] = None, graph: bool = False) -> Tuple[torch.Tensor, RWKVState]:
         """prefillBatch (BatchGenerate.swift:37-53): every prompt in one
         parallel pass — right padding to the longest prompt, a mask that makes
         the pad steps neutral for the recurrence, each row's shift state taken
@@ -599,7 +605,10 @@ class X070Decoder:
         The WKV-7 pass runs in 32-token chunks in parallel over time
         (rwkv_wkv7_seq_fwd_chunked) when `wkv_chunked` is True, or when it is
         None and the pass has few (batch, head) rows and a long T
-        (wkv_chunked_prefers); otherwise step by step (rwkv_wkv7_seq_fwd)."""
+        (wkv_chunked_prefers); otherwise step by step (rwkv_wkv7_seq_fwd).
+        `graph`: the pass is captured into a HIP graph once per (B, T, kind)
+        and replayed (one host call instead of ~25 launches per layer; the
+        same launches, so the same results)."""
         if len(prompts) == 0:
             raise ValueError("prefill_batch: no prompts")
         if any(len(p) == 0 for p in prompts):
@@ -610,24 +619,42 @@ class X070Decoder:
         M = B * T
         if M > 65535:
             raise ValueError(f"prefill_batch: {M} rows in one pass (at most 65535)")
-        dev, D = self.device, self.D
+        dev = self.device
         ids = np.zeros((B, T), np.int32)
         for i, p in enumerate(prompts):
             ids[i, :len(p)] = np.asarray(p, np.int32)
         lens = [len(p) for p in prompts]
+        last = [i * T + n - 1 for i, n in enumerate(lens)]
+        long = base_dtype == torch.float16 and M > short_rows
+        chunked = wkv_chunked_prefers(B, T, self.H) if wkv_chunked is None else bool(wkv_chunked)
+        if graph:
+            return self._prefill_graphed(ids, lens, last, B, T, long, chunked)
         ids_t = torch.from_numpy(ids.reshape(-1)).to(dev)
         len_t = torch.tensor(lens, dtype=torch.int32, device=dev)
-        last_t = torch.tensor([i * T + n - 1 for i, n in enumerate(lens)], dtype=torch.int32, device=dev)
+        last_t = torch.tensor(last, dtype=torch.int32, device=dev)
         state = self.new_state(B)
-        s = torch.cuda.current_stream(dev).cuda_stream
-        long = base_dtype == torch.float16 and M > short_rows
-        bf = self._prefill_buffers(M, long)
-        chunked = wkv_chunked_prefers(B, T, self.H) if wkv_chunked is None else bool(wkv_chunked)
+        logits = torch.empty((B, self.V), dtype=torch.float32, device=dev)
+        bf = self._prefill_setup(B, T, long, chunked)
+        self._prefill_run(bf, ids_t, len_t, last_t, state, logits, B, T, long, torch.cuda.current_stream(dev).cuda_stream)
+        return logits, state
+
+    def _prefill_setup(self, B: int, T: int, long: bool, chunked: bool) -> dict:
+        """The pass's buffers (and the chunked WKV-7 workspace), made before
+        any launch so the pass can be captured."""
+        bf = self._prefill_buffers(B * T, long)
         if chunked:
             need = int(_lib.lib().rwkv_wkv7_chunked_workspace(B, T, self.H))
             if bf.get("wkv_ws") is None or bf["wkv_ws"].numel() < need:
-                bf["wkv_ws"] = torch.empty(need, dtype=torch.uint8, device=dev)
+                bf["wkv_ws"] = torch.empty(need, dtype=torch.uint8, device=self.device)
+        if bf.get("xo") is None or bf["xo"].shape[0] != B:
+            bf["xo"] = torch.empty((B, self.D), dtype=torch.float32, device=self.device)
         bf["chunked"] = chunked
+        return bf
+
+    def _prefill_run(self, bf, ids_t, len_t, last_t, state, logits, B, T, long, s) -> None:
+        """The device work of one parallel pass: every launch on stream s, no
+        allocation and no host synchronisation."""
+        M, D = B * T, self.D
         L, p = _lib.lib(), (lambda t: t.data_ptr())
         x = bf["x"]
         emb_dt = _lib.F16 if self.emb.dtype == torch.float16 else _lib.F32
@@ -635,12 +662,51 @@ class X070Decoder:
                                      p(self.ln0[1]), p(x), M, D, LN_EPS, s))
         for l in range(self.L):
             self._prefill_layer(l, state, bf, len_t, B, T, long, s)
-        xo = torch.empty((B, D), dtype=torch.float32, device=dev)
+        xo = bf["xo"]
         _lib.check(L.rwkv_layer_norm(p(x), _lib.F32, p(last_t), M, p(self.ln_out[0]), p(self.ln_out[1]), p(xo),
                                      B, D, LN_EPS, s))
-        logits = torch.empty((B, self.V), dtype=torch.float32, device=dev)
         self._gemv("head.weight", xo, logits, 0, B, s)
-        return logits, state
+
+    def _prefill_graphed(self, ids, lens, last, B, T, long, chunked):
+        """prefill_batch replayed from a HIP graph captured once per (B, T,
+        pass kind): the prompts' ids, lengths and last-token rows are copied
+        into the graph's own input buffers, the state starts from zeros inside
+        the graph, and the logits and state are returned as copies."""
+        key = ("prefill_graph", B, T, long, chunked)
+        gr = self._tmp.get(key)
+        dev = self.device
+        if gr is None:
+            gr = {"ids": torch.zeros(B * T, dtype=torch.int32, device=dev),
+                  "len": torch.ones(B, dtype=torch.int32, device=dev),
+                  "last": torch.zeros(B, dtype=torch.int32, device=dev),
+                  "state": self.new_state(B),
+                  "logits": torch.empty((B, self.V), dtype=torch.float32, device=dev)}
+        gr["ids"].copy_(torch.from_numpy(ids.reshape(-1)))
+        gr["len"].copy_(torch.tensor(lens, dtype=torch.int32))
+        gr["last"].copy_(torch.tensor(last, dtype=torch.int32))
+        st = gr["state"]
+
+        def run(s):
+            for t in (st.wkv, st.tmix_prev, st.cmix_prev, st.v_first):
+                t.zero_()
+            self._prefill_run(bf, gr["ids"], gr["len"], gr["last"], st, gr["logits"], B, T, long, s)
+
+        if "graph" not in gr:
+            # a copy of the buffer table: the graph keeps the tensors it was
+            # captured with alive even when a later eager pass replaces them
+            bf = dict(self._prefill_setup(B, T, long, chunked))
+            side = torch.cuda.Stream(device=dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                run(side.cuda_stream)   # eager once: plans and buffers exist before capture
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=side):
+                    run(torch.cuda.current_stream(dev).cuda_stream)
+            torch.cuda.current_stream(dev).wait_stream(side)
+            gr["graph"], gr["bf"] = g, bf
+            self._tmp[key] = gr
+        gr["graph"].replay()
+        return gr["logits"].clone(), st.clone()
 
     def _prefill_buffers(self, M: int, long: bool) -> dict:
         key = ("prefill", M, long)
@@ -656,6 +722,7 @@ class X070Decoder:
             bf["rkv_in"] = z(3, M, D, dt=torch.float16) if long else z(M, 3, D)
             bf["xk"] = z(M, D, dt=torch.float16) if long else z(M, D)
             bf["hk"] = z(M, F, dt=torch.float16) if long else z(M, F)
+            bf["la_seq"] = z(M, sum(self.ranks))
             self._tmp = {k: v for k, v in self._tmp.items() if not (isinstance(k, tuple) and k[0] == "prefill")}
             self._tmp[key] = bf
         return bf
@@ -692,13 +759,21 @@ class X070Decoder:
                                              p(y0[0]), y0[1], y0[2], y0[3], p(mix), D, M * D, B, T, D, s))
         state.tmix_prev[l].copy_(prev)
         self._prefill_proj(self.proj[f"blocks.{l}.att.rkv"], rkv_in, bf["y_rkv"], 0, M, long, s)
-        Aw, Aa, Av, Ag, Bw, Ba, Bv, Bg = self._lowrank_f32(l)
-        # mix rows: r, k, v, w, a, g
-        torch.mm(torch.tanh(torch.mm(mix[3], Aw.t())), Bw.t(), out=bf["ww"])
-        torch.mm(torch.mm(mix[4], Aa.t()), Ba.t(), out=bf["aa"])
-        if l > 0:
-            torch.mm(torch.mm(mix[2], Av.t()), Bv.t(), out=bf["vv"])
-        torch.mm(torch.sigmoid(torch.mm(mix[5], Ag.t())), Bg.t(), out=bf["gate"])
+        rw, ra, rv, rg = self.ranks
+        if all(r % 16 == 0 for r in self.ranks) and D % 16 == 0 and M * D <= SEQ_LORA_MAX_MD:
+            # the four low-rank branches on the matrix cores (two launches)
+            Bm = lay["B"]
+            _lib.check(L.rwkv_x070_seq_lora(p(mix), M, D, p(lay["wcat"]), p(Bm[0]), p(Bm[1]), p(Bm[2]), p(Bm[3]),
+                                            _dt(lay["wcat"]), rw, ra, rv, rg, int(l > 0), p(bf["la_seq"]),
+                                            p(bf["ww"]), p(bf["aa"]), p(bf["vv"]), p(bf["gate"]), s))
+        else:   # long passes (or ranks the kernel does not take): the same products on the library GEMM
+            Aw, Aa, Av, Ag, Bw, Ba, Bv, Bg = self._lowrank_f32(l)
+            # mix rows: r, k, v, w, a, g
+            torch.mm(torch.tanh(torch.mm(mix[3], Aw.t())), Bw.t(), out=bf["ww"])
+            torch.mm(torch.mm(mix[4], Aa.t()), Ba.t(), out=bf["aa"])
+            if l > 0:
+                torch.mm(torch.mm(mix[2], Av.t()), Bv.t(), out=bf["vv"])
+            torch.mm(torch.sigmoid(torch.mm(mix[5], Ag.t())), Bg.t(), out=bf["gate"])
         bias = lay["bias"]
         _lib.check(L.rwkv_x070_seq_tmix_pre(p(bf["y_rkv"]), p(bf["ww"]), p(bf["aa"]), p(bf["vv"]) if l > 0 else None,
                                             p(bias[0]), p(bias[1]), p(bias[2]) if l > 0 else None, p(lay["k_k"]),

@@ -131,6 +131,47 @@ def test_quant_gemm_layouts_epilogues_and_groups(orc, fmt):
     assert h.dtype == torch.float16 and torch.equal(h, (torch.relu(y0) * torch.relu(y0)).to(torch.float16))
 
 
+@pytest.mark.parametrize("D,M,ranks,wdt", [(256, 37, (32, 32, 32, 64), torch.float16),
+                                             (1024, 200, (64, 64, 32, 128), torch.float32),
+                                             (4096, 70, (128, 128, 96, 480), torch.float16)])
+@pytest.mark.parametrize("with_v", [1, 0])
+def test_seq_lora_matches_fp64(D, M, ranks, wdt, with_v):
+    """The parallel pass's four low-rank branches (rwkv_x070_seq_lora) against
+    fp64 products of the same values: ww = tanh(x_w·A_wᵀ)·B_wᵀ, aa, vv (not
+    written when the layer has no v branch), gate = sigmoid(x_g·A_gᵀ)·B_gᵀ."""
+    case(f"seq lora D={D} M={M} ranks={ranks} {wdt} with_v={with_v}")
+    from swiftrwkv_amd import _lib
+    rng = np.random.default_rng(D + M + with_v)
+    rw, ra, rv, rg = ranks
+    RT = sum(ranks)
+    mix = rng.standard_normal((6, M, D)).astype(np.float32)
+    A = (rng.standard_normal((RT, D)) / np.sqrt(D)).astype(np.float32)
+    Bs = [(rng.standard_normal((D, r)) * 0.5 / np.sqrt(r)).astype(np.float32) for r in ranks]
+    A_d = dev(A).to(wdt)
+    B_d = [dev(b).to(wdt) for b in Bs]
+    A64 = A_d.double().cpu().numpy()
+    B64 = [b.double().cpu().numpy() for b in B_d]
+    la = torch.empty((M, RT), device=DEV)
+    outs = [torch.full((M, D), 7.0, device=DEV) for _ in range(4)]
+    L = _lib.lib()
+    _lib.check(L.rwkv_x070_seq_lora(dev(mix).data_ptr(), M, D, A_d.data_ptr(), *[b.data_ptr() for b in B_d],
+                                    _lib.F16 if wdt == torch.float16 else _lib.F32, rw, ra, rv, rg, with_v,
+                                    la.data_ptr(), *[o.data_ptr() for o in outs], torch.cuda.current_stream().cuda_stream))
+    x = mix.astype(np.float64)
+    offs = np.cumsum((0,) + ranks)
+    inner = [x[c] @ A64[offs[b]:offs[b + 1]].T for b, c in enumerate((3, 4, 2, 5))]
+    acts = [np.tanh(inner[0]), inner[1], inner[2], 1.0 / (1.0 + np.exp(-inner[3]))]
+    want = [acts[b] @ B64[b].T for b in range(4)]
+    for b, name in enumerate(("ww", "aa", "vv", "gate")):
+        got = outs[b].cpu().numpy()
+        if b == 2 and not with_v:
+            assert np.all(got == 7.0), name   # layer 0: no v branch, vv untouched
+            continue
+        err = rel(want[b], got)
+        print(f"[seq lora] D={D} M={M} {name}: rel {err:.2e}", flush=True)
+        assert err < 2e-5, name
+
+
 def test_sb6_gemm_epilogues_groups_and_row_independence(orc):
     case("sb6 gemm epilogues, r/k/v group, rows")
     D, M = 1024, 200
@@ -278,6 +319,42 @@ def test_prefill_then_decode_continues_the_prompt(tiny_model):
         for i, o in enumerate(osts):
             ref = X.step(p, W, [step_ids[i]], o, TINY.n_layer, TINY.n_head)
             assert rel(ref, got[i]) < 1e-4, (step_ids, i)
+
+
+def _states_equal(a, b):
+    return all(torch.equal(x, y) for x, y in zip((a.wkv, a.tmix_prev, a.cmix_prev, a.v_first),
+                                                 (b.wkv, b.tmix_prev, b.cmix_prev, b.v_first)))
+
+
+@pytest.mark.parametrize("base,chunked", [(torch.float16, False), (torch.float32, True), (torch.float16, True)])
+def test_prefill_graph_replays_match_eager(tiny_model, base, chunked):
+    """prefill_batch(graph=True): the pass captured once per (B, T, kind) and
+    replayed for other prompts of the same shape gives the eager pass's
+    logits and state bitwise, every replay, with eager passes of other
+    shapes (which reuse and regrow the pass buffers) in between."""
+    case(f"prefill graph replays, base {base}, chunked WKV {chunked}")
+    proj, W = tiny_model
+    p = syn.x070_dense_params(TINY, seed=36, lora_dtype=np.float16)
+    dec = X070Decoder(TINY.n_layer, TINY.n_embd, TINY.ffn, TINY.vocab, p, proj, DEV)
+    rng = np.random.default_rng(36)
+    T = max(len(pr) for pr in PROMPTS)
+    sets = [PROMPTS] + [[[int(t) for t in rng.integers(0, TINY.vocab, n)] for n in rng.integers(1, T + 1, len(PROMPTS))]
+                        for _ in range(3)]
+    for pr in sets[1:]:
+        pr[0] = pr[0] + [1] * (T - len(pr[0]))   # the same (B, T) for every set
+    kw = dict(base_dtype=base, short_rows=0, wkv_chunked=chunked)
+    for rep, pr in enumerate(sets + sets[:1]):
+        eager, est = dec.prefill_batch(pr, **kw)
+        torch.cuda.synchronize()
+        got, gst = dec.prefill_batch(pr, graph=True, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager) and _states_equal(gst, est), rep
+        dec.prefill_batch([pr[0] * 2, pr[1]], **kw)   # another shape between replays
+        torch.cuda.synchronize()
+    # the graphed rows still agree with the oracle
+    ref, _ = X.prefill(p, W, sets[0][3], TINY.n_layer, TINY.n_head, f16_base=base == torch.float16)
+    got, _ = dec.prefill_batch(sets[0], graph=True, **kw)
+    assert rel(ref, got[3].cpu().numpy()) < (2e-3 if base == torch.float16 else 1e-4)
 
 
 def _mixed_projections(shape, seed=61):
