@@ -305,21 +305,29 @@ rwkv_status rwkv_sym_gemv_ep(const float* x, int64_t N,
  * at x + g·x_group_stride elements): output feature o reads group o / out_per,
  * so r/k/v with their own inputs run as one launch.  y [M][ldy]:
  * epilogue 0 stores, 1 adds into y (fp32; the residual update), 2 stores
- * relu(·)² as fp16 (y is then an fp16 buffer; cmix's key, exact in fp16). */
+ * relu(·)² as fp16 (y is then an fp16 buffer; cmix's key, exact in fp16).
+ * workspace: NULL, or device memory of rwkv_quant_gemm_workspace(M, OUT, IN)
+ * bytes (16-byte aligned) — shapes with few 128 × 128 output tiles then split
+ * the K sum into ranges summed in a fixed order by a second kernel (the same
+ * bound, deterministic, far faster for a few hundred rows); with NULL the
+ * launch is one range.  Launches sharing a workspace must not overlap. */
 int rwkv_sb6_gemm_applies(int64_t OUT, int64_t IN, int xbits, int64_t out_per);
+int64_t rwkv_quant_gemm_workspace(int64_t M, int64_t OUT, int64_t IN);
 rwkv_status rwkv_sb6_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda, int64_t x_group_stride,
                           const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, void* y, int64_t ldy,
-                          int64_t OUT, int64_t IN, int xbits, int64_t out_per, int epilogue, void* stream);
+                          int64_t OUT, int64_t IN, int xbits, int64_t out_per, int epilogue, void* workspace,
+                          int64_t workspace_bytes, void* stream);
 
 /* The same long pass for sym matrices (8-bit codes, or 6-bit in the loader's
  * interleave; qs [OUT, IN/16] int8, d [OUT, IN/256] fp16): fp16(W) is exactly
  * what rwkv_sym_dequant(out_dt = f16) stores (the fp16 branch of
  * rwkvqDequantSym computes in half, RwkvqDequant.swift:350-388), the rest as
- * rwkv_sb6_gemm (arguments, groups, epilogues, rwkv_sym_gemm_applies). */
+ * rwkv_sb6_gemm (arguments, groups, epilogues, workspace, rwkv_sym_gemm_applies). */
 int rwkv_sym_gemm_applies(int64_t OUT, int64_t IN, int bits, int64_t out_per);
 rwkv_status rwkv_sym_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda, int64_t x_group_stride,
                           const uint8_t* qblk, const uint8_t* qs, const uint16_t* d, void* y, int64_t ldy,
-                          int64_t OUT, int64_t IN, int bits, int64_t out_per, int epilogue, void* stream);
+                          int64_t OUT, int64_t IN, int bits, int64_t out_per, int epilogue, void* workspace,
+                          int64_t workspace_bytes, void* stream);
 
 /* ───────────────────────── x070 decode step around the hot path ───────────────────────── */
 /* fp32 activations; dense vector parameters fp32 (an fp16 file's values

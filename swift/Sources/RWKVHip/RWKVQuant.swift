@@ -226,6 +226,12 @@ public final class RwkvqDeviceSidecar {
                                 inFeatures: info.inFeatures, bits: info.bits)
     }
 
+    /// The split-K workspace a long pass of M rows takes (nil: one K range).
+    private func gemmWorkspace(_ M: Int, _ info: RwkvqTensorInfo) throws -> (DeviceArray?, Int64) {
+        let n = rwkv_quant_gemm_workspace(Int64(M), Int64(info.outFeatures), Int64(info.inFeatures))
+        return n > 0 ? (try DeviceArray(shape: [Int(n)], dtype: .uint8), n) : (nil, 0)
+    }
+
     /// The long pass of baseMatmul with an fp16 base (X070Backbone.swift:337-356):
     /// y = fp16(fp16(x)·fp16(W)ᵀ) on the matrix cores from the packed bytes;
     /// nil where the kernel does not take the matrix (the caller dequantises).
@@ -237,9 +243,11 @@ public final class RwkvqDeviceSidecar {
               let (qblk, qsqm, ddm) = arrays[key] else { return nil }
         let M = x.shape[0]
         let y = try DeviceArray(shape: [M, info.outFeatures], dtype: .float32)
+        let (ws, wsBytes) = try gemmWorkspace(M, info)
         try check(rwkv_sb6_gemm(x.raw, x.dtype.code, Int64(M), Int64(info.inFeatures), Int64(M * info.inFeatures),
                                 qblk.u8, qsqm.u8, ddm.u16, y.raw, Int64(info.outFeatures), Int64(info.outFeatures),
-                                Int64(info.inFeatures), Int32(info.xbits), Int64(info.outFeatures), 0, streamArg))
+                                Int64(info.inFeatures), Int32(info.xbits), Int64(info.outFeatures), 0,
+                                ws?.raw, wsBytes, streamArg))
         return y
     }
 
@@ -253,9 +261,11 @@ public final class RwkvqDeviceSidecar {
               let (qblk, qs, d) = arrays[key] else { return nil }
         let M = x.shape[0]
         let y = try DeviceArray(shape: [M, info.outFeatures], dtype: .float32)
+        let (ws, wsBytes) = try gemmWorkspace(M, info)
         try check(rwkv_sym_gemm(x.raw, x.dtype.code, Int64(M), Int64(info.inFeatures), Int64(M * info.inFeatures),
                                 qblk.u8, qs.u8, d.u16, y.raw, Int64(info.outFeatures), Int64(info.outFeatures),
-                                Int64(info.inFeatures), Int32(info.bits), Int64(info.outFeatures), 0, streamArg))
+                                Int64(info.inFeatures), Int32(info.bits), Int64(info.outFeatures), 0,
+                                ws?.raw, wsBytes, streamArg))
         return y
     }
 }

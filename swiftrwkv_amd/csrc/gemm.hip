@@ -32,6 +32,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "launch.h"
 
 namespace {
@@ -56,6 +58,8 @@ struct GemmArgs {
     void* y;              // [M][ldy]: fp32 (epilogues 0, 1) or fp16 (epilogue 2)
     int64_t ldy;
     int M, N, K, out_per;
+    float* part;          // splits > 1: the fp32 partial sums [splits][M][N]
+    int splits;           // K ranges the tile's stages are divided into
 };
 
 // 4 bits → the low bit of 4 bytes (RwkvqSb6GEMV.swift:58-67 multiply spread).
@@ -221,13 +225,15 @@ __global__ __launch_bounds__(256, 2) void quant_gemm_kernel(GemmArgs g) {
     // every feature tile of one block before the next, so an input block is
     // fetched into one L2 only.  The grid is padded to whole groups of 8 row
     // blocks; a padding workgroup exits before any barrier.
-    const int ntn = g.N / BN;
+    const int ntn = g.N / BN, S = g.splits;
+    const int total = ((g.M + BM - 1) / BM) * ntn * S;
     const int xcd = blockIdx.x & 7, loc = blockIdx.x >> 3;
-    const int tile_n = loc % ntn, tile_m = xcd + 8 * (loc / ntn);
-    if (tile_m * BM >= g.M) return;
+    const int t = xcd * (total >> 3) + min(xcd, total & 7) + loc;   // the tile's place in (m, n, split) order
+    const int kz = t % S, tile_n = (t / S) % ntn, tile_m = t / (S * ntn);
     const int n0 = tile_n * BN;
     const int m0 = tile_m * BM;
     const int nst = g.K / BK;
+    const int st0 = (int)((int64_t)kz * nst / S), st1 = (int)((int64_t)(kz + 1) * nst / S);
 
     // input rows of this tile come from the matrix group its output features belong to
     const TA* xg = reinterpret_cast<const TA*>(g.x) + (int64_t)(n0 / g.out_per) * g.x_gstride;
@@ -294,8 +300,8 @@ __global__ __launch_bounds__(256, 2) void quant_gemm_kernel(GemmArgs g) {
         }
     };
 
-    auto ar = load_a(0);
-    BRaw bcur = load_b(0);
+    auto ar = load_a(st0);
+    BRaw bcur = load_b(st0);
     store_a(0, ar);
     half8 b0[NT], b1[NT];
     dequant(bcur, 0, b0);
@@ -304,9 +310,9 @@ __global__ __launch_bounds__(256, 2) void quant_gemm_kernel(GemmArgs g) {
     // Per stage: the next stage's bytes are requested first; unit 0's
     // products run while unit 1 is decoded, unit 1's while the next stage's
     // unit 0 is (one MFMA, one VALU instruction, alternately).
-    for (int st = 0; st < nst; ++st) {
-        const int buf = st & 1;
-        const bool more = st + 1 < nst;
+    for (int st = st0; st < st1; ++st) {
+        const int buf = (st - st0) & 1;
+        const bool more = st + 1 < st1;
         BRaw bnxt = bcur;
         if (more) {
             ar = load_a(st + 1);
@@ -331,6 +337,19 @@ __global__ __launch_bounds__(256, 2) void quant_gemm_kernel(GemmArgs g) {
         __syncthreads();
     }
 
+    if (S > 1) {   // this K range's fp32 sums; gemm_split_reduce adds the ranges and applies the epilogue
+        float* part = g.part + (int64_t)kz * g.M * g.N;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + 16 * i + 4 * gq + r;
+                if (row >= g.M) continue;
+#pragma unroll
+                for (int j = 0; j < NT; ++j) part[(int64_t)row * g.N + nb + 16 * j] = acc[i][j][r];
+            }
+        return;
+    }
     // epilogue: fp16 rounding of the product, then store / add / relu² (fp16)
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -356,13 +375,69 @@ __global__ __launch_bounds__(256, 2) void quant_gemm_kernel(GemmArgs g) {
     }
 }
 
+// The K ranges of a split launch summed in range order (a fixed order: the
+// result does not depend on which workgroup finished first), then the
+// epilogue of the one-range kernel: fp16 rounding, store / add / relu².
+// Thread i takes 4 consecutive outputs of one row (N is a multiple of 128).
+template <int EP>
+__global__ __launch_bounds__(256) void gemm_split_reduce(const float* __restrict__ part, int S, int M, int N,
+                                                         void* y, int64_t ldy) {
+    const int64_t n4 = (int64_t)M * N / 4;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const float4* p = reinterpret_cast<const float4*>(part) + i;
+    float4 a = p[0];
+    for (int k = 1; k < S; ++k) {
+        const float4 b = p[(int64_t)k * n4];
+        a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+    }
+    const int64_t row = 4 * i / N, col = 4 * i % N;
+    const float v[4] = {hround(a.x), hround(a.y), hround(a.z), hround(a.w)};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        if constexpr (EP == 0) {
+            reinterpret_cast<float*>(y)[row * ldy + col + c] = v[c];
+        } else if constexpr (EP == 1) {
+            float* q = reinterpret_cast<float*>(y) + row * ldy + col + c;
+            *q = *q + v[c];
+        } else {
+            const float rl = fmaxf(v[c], 0.0f);
+            reinterpret_cast<_Float16*>(y)[row * ldy + col + c] = (_Float16)(rl * rl);
+        }
+    }
+}
+
+// K ranges per launch: one where the (row block, feature block) tiles
+// already fill the chip; otherwise enough to reach about 384 workgroups
+// (two per CU hold 512), each range at least 3 stages of 64 columns.  A
+// tile's stages run one after another, each waiting on its loads (about
+// 2 µs a stage at a few workgroups per XCD), so few tiles over a long K
+// take K/64 such waits: 128 rows × 768 features × K 3072, 6 tiles, took
+// 100 µs in one range.
+int gemm_splits(int64_t M, int64_t N, int64_t K) {
+    const int64_t tiles = ((M + 127) / 128) * (N / 128);
+    if (tiles >= 160) return 1;
+    const int64_t want = (384 + tiles - 1) / tiles, most = K / BK / 3;
+    return (int)std::max<int64_t>(1, std::min(want, most));
+}
+
+int64_t gemm_workspace(int64_t M, int64_t N, int64_t K) {
+    const int S = gemm_splits(M, N, K);
+    return S > 1 ? (int64_t)S * M * N * 4 : 0;
+}
+
 // One tile shape: 128 × 128 with two workgroups per CU measured fastest
 // (larger tiles cost occupancy: at one wave per SIMD the stage's loads are
 // not hidden).
 template <class F, typename TA, int EP>
 void launch_gemm(const GemmArgs& g, hipStream_t s) {
-    const int64_t blocks = (int64_t)((g.M + 8 * 128 - 1) / (8 * 128)) * 8 * (g.N / 128);
+    const int64_t blocks = (int64_t)((g.M + 127) / 128) * (g.N / 128) * g.splits;
     rwkv::launch(quant_gemm_kernel<F, TA, EP, 8, 2>, dim3((unsigned)blocks), dim3(256), s, g);
+    if (g.splits > 1) {
+        const int64_t n4 = (int64_t)g.M * g.N / 4;
+        rwkv::launch(gemm_split_reduce<EP>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), s, g.part, g.splits,
+                     g.M, g.N, g.y, g.ldy);
+    }
 }
 
 template <class F>
@@ -394,6 +469,24 @@ rwkv_status gemm_check(const char* who, const void* x, rwkv_dtype x_dt, int64_t 
                  (long long)ldy);
     RWKV_REQUIRE((reinterpret_cast<uintptr_t>(x) % 16) == 0 && (x_group_stride * xes) % 16 == 0, RWKV_E_SHAPE,
                  "%s: inputs must be 16-byte aligned", who);
+    RWKV_REQUIRE(((M + 127) / 128) * (OUT / 128) <= ((int64_t)1 << 26), RWKV_E_SHAPE,
+                 "%s: %lld x %lld outputs exceed one launch", who, (long long)M, (long long)OUT);
+    return RWKV_OK;
+}
+
+// The launch's K ranges: several where the shape asks for them and the
+// caller passed a workspace (which must then hold rwkv_quant_gemm_workspace
+// bytes), one otherwise.
+rwkv_status gemm_split_args(const char* who, GemmArgs& g, void* workspace, int64_t workspace_bytes) {
+    g.part = nullptr;
+    g.splits = 1;
+    const int64_t need = gemm_workspace(g.M, g.N, g.K);
+    if (workspace == nullptr || need == 0) return RWKV_OK;
+    RWKV_REQUIRE(workspace_bytes >= need && reinterpret_cast<uintptr_t>(workspace) % 16 == 0, RWKV_E_SHAPE,
+                 "%s: workspace of %lld bytes (16-byte aligned) needed, %lld given", who, (long long)need,
+                 (long long)workspace_bytes);
+    g.part = reinterpret_cast<float*>(workspace);
+    g.splits = gemm_splits(g.M, g.N, g.K);
     return RWKV_OK;
 }
 
@@ -401,20 +494,28 @@ rwkv_status gemm_check(const char* who, const void* x, rwkv_dtype x_dt, int64_t 
 
 extern "C" {
 
+int64_t rwkv_quant_gemm_workspace(int64_t M, int64_t OUT, int64_t IN) {
+    if (M < 1 || M > ((int64_t)1 << 24) || OUT < 128 || OUT % 128 != 0 || IN < 256 || IN % 256 != 0) return 0;
+    return gemm_workspace(M, OUT, IN);
+}
+
 int rwkv_sb6_gemm_applies(int64_t OUT, int64_t IN, int xbits, int64_t out_per) {
     return xbits >= 0 && xbits <= 2 && gemm_shape_ok(OUT, IN, out_per);
 }
 
 rwkv_status rwkv_sb6_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda, int64_t x_group_stride,
                           const uint8_t* qblk, const uint8_t* qsqm, const uint16_t* ddm, void* y, int64_t ldy,
-                          int64_t OUT, int64_t IN, int xbits, int64_t out_per, int epilogue, void* stream) {
+                          int64_t OUT, int64_t IN, int xbits, int64_t out_per, int epilogue, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
     RWKV_REQUIRE(x && qblk && qsqm && ddm && y, RWKV_E_NULL, "sb6_gemm: null buffer");
     RWKV_REQUIRE(rwkv_sb6_gemm_applies(OUT, IN, xbits, out_per), RWKV_E_UNSUPPORTED,
                  "sb6_gemm: xbits %d (0..2), OUT (%lld) and out_per (%lld) multiples of 128, IN (%lld) of 256", xbits,
                  (long long)OUT, (long long)out_per, (long long)IN);
-    const rwkv_status c = gemm_check("sb6_gemm", x, x_dt, M, lda, x_group_stride, ldy, OUT, IN, out_per, epilogue);
+    rwkv_status c = gemm_check("sb6_gemm", x, x_dt, M, lda, x_group_stride, ldy, OUT, IN, out_per, epilogue);
     if (c != RWKV_OK) return c;
     GemmArgs g{x, lda, x_group_stride, qblk, qsqm, ddm, y, ldy, (int)M, (int)OUT, (int)IN, (int)out_per};
+    c = gemm_split_args("sb6_gemm", g, workspace, workspace_bytes);
+    if (c != RWKV_OK) return c;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const bool f16 = x_dt == RWKV_F16;
     if (xbits == 0) launch_gemm_ep<Sb6W<0>>(g, f16, epilogue, s);
@@ -432,14 +533,17 @@ int rwkv_sym_gemm_applies(int64_t OUT, int64_t IN, int bits, int64_t out_per) {
 
 rwkv_status rwkv_sym_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda, int64_t x_group_stride,
                           const uint8_t* qblk, const uint8_t* qs, const uint16_t* d, void* y, int64_t ldy,
-                          int64_t OUT, int64_t IN, int bits, int64_t out_per, int epilogue, void* stream) {
+                          int64_t OUT, int64_t IN, int bits, int64_t out_per, int epilogue, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
     RWKV_REQUIRE(x && qblk && qs && d && y, RWKV_E_NULL, "sym_gemm: null buffer");
     RWKV_REQUIRE(rwkv_sym_gemm_applies(OUT, IN, bits, out_per), RWKV_E_UNSUPPORTED,
                  "sym_gemm: %d-bit codes (8 or 6), OUT (%lld) and out_per (%lld) multiples of 128, IN (%lld) of 256",
                  bits, (long long)OUT, (long long)out_per, (long long)IN);
-    const rwkv_status c = gemm_check("sym_gemm", x, x_dt, M, lda, x_group_stride, ldy, OUT, IN, out_per, epilogue);
+    rwkv_status c = gemm_check("sym_gemm", x, x_dt, M, lda, x_group_stride, ldy, OUT, IN, out_per, epilogue);
     if (c != RWKV_OK) return c;
     GemmArgs g{x, lda, x_group_stride, qblk, qs, d, y, ldy, (int)M, (int)OUT, (int)IN, (int)out_per};
+    c = gemm_split_args("sym_gemm", g, workspace, workspace_bytes);
+    if (c != RWKV_OK) return c;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const bool f16 = x_dt == RWKV_F16;
     if (bits == 8) launch_gemm_ep<SymW<8>>(g, f16, epilogue, s);

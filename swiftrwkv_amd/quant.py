@@ -559,8 +559,14 @@ def rwkvq_sym_gemm_applies(out_features: int, in_features: int, bits: int, out_p
 _GEMM_EP = {"store": 0, "add": 1, "relu2_f16": 2}
 
 
+def rwkvq_gemm_workspace(rows: int, out_features: int, in_features: int) -> int:
+    """Bytes of the workspace a long-pass GEMM of this shape splits its K sum
+    with (0: the shape runs as one range)."""
+    return int(_lib.lib().rwkv_quant_gemm_workspace(rows, out_features, in_features))
+
+
 def _quant_gemm(entry: str, what: str, x, bufs, out_features: int, in_features: int, code_bits: int, per: int,
-                epilogue: str, out: Optional[torch.Tensor]) -> torch.Tensor:
+                epilogue: str, out: Optional[torch.Tensor], split: bool = True) -> torch.Tensor:
     G = out_features // per
     if x.dim() == 2:
         x = x.unsqueeze(0)
@@ -579,30 +585,34 @@ def _quant_gemm(entry: str, what: str, x, bufs, out_features: int, in_features: 
     elif out.dtype != ydt or tuple(out.shape) != (M, out_features) or not out.is_contiguous() or \
             out.device != x.device:
         raise ValueError(f"{what} GEMM: out must be a contiguous {ydt} [{M}, {out_features}] tensor on {x.device}")
+    need = rwkvq_gemm_workspace(M, out_features, in_features) if split else 0
+    ws = torch.empty(need, dtype=torch.uint8, device=x.device) if need else None
     _lib.call(entry, x.data_ptr(), _OUT_DT[x.dtype], M, in_features, M * in_features, *[b.data_ptr() for b in bufs],
-              out.data_ptr(), out_features, out_features, in_features, code_bits, per, ep, _stream(x))
+              out.data_ptr(), out_features, out_features, in_features, code_bits, per, ep,
+              ws.data_ptr() if need else None, need, _stream(x))
     return out
 
 
 def rwkvq_sb6_gemm(x, qblk, qsqm, ddm, out_features: int, in_features: int, xbits: int = 0,
                    out_per: Optional[int] = None, epilogue: str = "store",
-                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   out: Optional[torch.Tensor] = None, split: bool = True) -> torch.Tensor:
     """The fp16-base long pass of baseMatmul (X070Backbone.swift:337-356) on
     the matrix cores, straight from the K3 bytes (4, 5 or 6-bit codes): y
     [M, OUT] = fp16(fp16(x)·fp16(W)ᵀ) with fp32 sums.  x [M, IN] (one matrix)
     or [G, M, IN] (G = OUT / out_per row-concatenated matrices, matrix g
     reading x[g]), fp32 or fp16.  epilogue "store" / "add" (fp32 `out`, added
-    into) / "relu2_f16" (relu(·)² in an fp16 `out`)."""
+    into) / "relu2_f16" (relu(·)² in an fp16 `out`).  `split`: shapes with few
+    output tiles sum K in ranges (a workspace per call; False: one range)."""
     per = out_features if out_per is None else out_per
     if not rwkvq_sb6_gemm_applies(out_features, in_features, xbits, per):
         raise ValueError(f"sb6 GEMM: [{out_features}, {in_features}] xbits={xbits} out_per={per} not taken")
     bufs = _sb6_bufs(qblk, qsqm, ddm, out_features, in_features, xbits)
-    return _quant_gemm("rwkv_sb6_gemm", "sb6", x, bufs, out_features, in_features, xbits, per, epilogue, out)
+    return _quant_gemm("rwkv_sb6_gemm", "sb6", x, bufs, out_features, in_features, xbits, per, epilogue, out, split)
 
 
 def rwkvq_sym_gemm(x, qblk, qs, d, out_features: int, in_features: int, bits: int,
                    out_per: Optional[int] = None, epilogue: str = "store",
-                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   out: Optional[torch.Tensor] = None, split: bool = True) -> torch.Tensor:
     """rwkvq_sb6_gemm for sym matrices (8-bit codes, or 6-bit in the loader's
     interleave): fp16(W) is exactly rwkvq_dequant_sym's fp16 output (the fp16
     branch of rwkvqDequantSym, RwkvqDequant.swift:350-388)."""
@@ -610,7 +620,7 @@ def rwkvq_sym_gemm(x, qblk, qs, d, out_features: int, in_features: int, bits: in
     if not rwkvq_sym_gemm_applies(out_features, in_features, bits, per):
         raise ValueError(f"sym GEMM: [{out_features}, {in_features}] bits={bits} out_per={per} not taken")
     bufs = _sym_bufs(qblk, qs, d, out_features, in_features, bits)
-    return _quant_gemm("rwkv_sym_gemm", "sym", x, bufs, out_features, in_features, bits, per, epilogue, out)
+    return _quant_gemm("rwkv_sym_gemm", "sym", x, bufs, out_features, in_features, bits, per, epilogue, out, split)
 
 
 def rwkvq_sb6_gemv_batch_applies(rows: int, out_features: int, in_features: int, xbits: int,

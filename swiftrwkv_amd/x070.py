@@ -448,7 +448,8 @@ class X070Decoder:
     batch_mfma: Optional[bool] = None
 
     def _batch_ws(self, nbytes: int) -> torch.Tensor:
-        """The batched GEMV's shared workspace, grown when a call needs more.
+        """The workspace the batched GEMV and the split long-pass GEMM share
+        (their launches are ordered on the stream), grown when a call needs more.
         A grown-out buffer is kept alive (not returned to the caching
         allocator): a HIP graph captured through launch() before the growth
         still holds its address and may be replayed."""
@@ -850,10 +851,10 @@ class X070Decoder:
             else:
                 dst.copy_(torch.relu(prod).square_().to(dst.dtype))
 
-    @staticmethod
-    def _long_gemm(q, xp, xdt, M, yp, ldy, ep, s) -> bool:
+    def _long_gemm(self, q, xp, xdt, M, yp, ldy, ep, s) -> bool:
         """One matrix (group) of the long pass on the matrix cores, when the
-        kernels take its layout; False otherwise (nothing launched)."""
+        kernels take its layout; False otherwise (nothing launched).  Shapes
+        with few output tiles split their K sum in the shared workspace."""
         L = _lib.lib()
         if q.kind == "sb6" and L.rwkv_sb6_gemm_applies(q.OUT, q.IN, q.xbits, q.out_per):
             entry, bits = L.rwkv_sb6_gemm, q.xbits
@@ -861,8 +862,10 @@ class X070Decoder:
             entry, bits = L.rwkv_sym_gemm, q.bits
         else:
             return False
+        need = int(L.rwkv_quant_gemm_workspace(M, q.OUT, q.IN))
+        ws = self._batch_ws(need).data_ptr() if need else None
         _lib.check(entry(xp, xdt, M, q.IN, M * q.IN, q.bufs[0].data_ptr(), q.bufs[1].data_ptr(), q.bufs[2].data_ptr(),
-                         yp, ldy, q.OUT, q.IN, bits, q.out_per, ep, s))
+                         yp, ldy, q.OUT, q.IN, bits, q.out_per, ep, ws, need, s))
         return True
 
     @staticmethod

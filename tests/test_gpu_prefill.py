@@ -101,34 +101,76 @@ def test_quant_gemm_layouts_match_f16_base_pass(orc, fmt, M, OUT, IN):
 
 
 @pytest.mark.parametrize("fmt", ["sb6:2", "sym:6"])
-def test_quant_gemm_layouts_epilogues_and_groups(orc, fmt):
-    """Fused groups equal their members bitwise, rows do not depend on the
-    other rows of the launch, and the add / relu² epilogues are the separate
+@pytest.mark.parametrize("split", [False, True])
+def test_quant_gemm_layouts_epilogues_and_groups(orc, fmt, split):
+    """One K range: fused groups equal their members bitwise and rows do not
+    depend on the other rows of the launch.  Split K sums (a few tiles): the
+    fp16-base oracle's bound (the sum's order is not the one range's),
+    deterministic.  Either way the add / relu² epilogues are the separate
     operations' arithmetic."""
-    case(f"quant gemm {fmt} epilogues, groups, rows")
+    case(f"quant gemm {fmt} epilogues, groups, rows, split {split}")
     D, M = 512, 150
     rng = np.random.default_rng(17)
-    bufs, _, _ = quant_matrix(orc, fmt, 3 * D, D, rng)
+    bufs, base_pass, _ = quant_matrix(orc, fmt, 3 * D, D, rng)
     w = [dev(z) for z in bufs]
     kind, b = fmt.split(":")
     entry = Q.rwkvq_sb6_gemm if kind == "sb6" else Q.rwkvq_sym_gemm
+    assert Q.rwkvq_gemm_workspace(M, 3 * D, D) > 0 and Q.rwkvq_gemm_workspace(M, D, D) > 0
     x = dev(rng.standard_normal((3, M, D)).astype(np.float32))
-    fused = entry(x, *w, 3 * D, D, int(b), out_per=D)
+    fused = entry(x, *w, 3 * D, D, int(b), out_per=D, split=split)
     for g in range(3):
         rows = slice(g * D, (g + 1) * D)
         part = [z[rows] for z in w]
-        sep = entry(x[g], *part, D, D, int(b))
+        sep = entry(x[g], *part, D, D, int(b), split=split)
+        one = entry(x[g], *part, D, D, int(b), split=False)
+        if split:
+            exact, mag = base_pass(x[g].cpu().numpy())
+            for got in (fused[:, rows], sep):
+                frac = check_f16_rounding(got.cpu().numpy(), exact[:, rows], mag[:, rows])
+                assert frac < 5e-2
+            assert torch.equal(entry(x[g], *part, D, D, int(b), split=True), sep)
+            assert not torch.equal(sep, one)   # the split ran (a different sum order somewhere)
+            continue
         assert torch.equal(fused[:, rows], sep), g
         for m in (0, 77, 149):
-            assert torch.equal(entry(x[g, m:m + 1], *part, D, D, int(b))[0], sep[m])
+            assert torch.equal(entry(x[g, m:m + 1], *part, D, D, int(b), split=False)[0], sep[m])
     part = [z[:D] for z in w]
-    y0 = entry(x[1], *part, D, D, int(b))
+    y0 = entry(x[1], *part, D, D, int(b), split=split)
     base = dev(rng.standard_normal((M, D)).astype(np.float32))
     y1 = base.clone()
-    entry(x[1], *part, D, D, int(b), epilogue="add", out=y1)
+    entry(x[1], *part, D, D, int(b), epilogue="add", out=y1, split=split)
     assert torch.equal(y1, base + y0)
-    h = entry(x[1], *part, D, D, int(b), epilogue="relu2_f16")
+    h = entry(x[1], *part, D, D, int(b), epilogue="relu2_f16", split=split)
     assert h.dtype == torch.float16 and torch.equal(h, (torch.relu(y0) * torch.relu(y0)).to(torch.float16))
+
+
+def test_quant_gemm_split_workspace_contract(orc):
+    """The split long pass through the C-ABI: a workspace smaller than
+    rwkv_quant_gemm_workspace is refused (nothing launched, y untouched), a
+    NULL one runs as one K range, an adequate one gives the split sums."""
+    case("quant gemm workspace contract")
+    from swiftrwkv_amd import _lib
+    M, OUT, IN = 96, 768, 3072
+    rng = np.random.default_rng(19)
+    bufs, base, gemm = quant_matrix(orc, "sb6:0", OUT, IN, rng)
+    w = [dev(z) for z in bufs]
+    x = dev(rng.standard_normal((M, IN)).astype(np.float32))
+    need = Q.rwkvq_gemm_workspace(M, OUT, IN)
+    assert need >= 2 * M * OUT * 4
+    L, s = _lib.lib(), torch.cuda.current_stream().cuda_stream
+    y = torch.full((M, OUT), 3.0, device=DEV)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    args = lambda: (x.data_ptr(), _lib.F32, M, IN, M * IN, *[b.data_ptr() for b in w], y.data_ptr(), OUT, OUT, IN, 0,
+                    OUT, 0)
+    assert L.rwkv_sb6_gemm(*args(), ws.data_ptr(), need - 16, s) != 0
+    torch.cuda.synchronize()
+    assert torch.all(y == 3.0)
+    _lib.check(L.rwkv_sb6_gemm(*args(), None, 0, s))
+    assert torch.equal(y, gemm(x, w, split=False))
+    _lib.check(L.rwkv_sb6_gemm(*args(), ws.data_ptr(), need, s))
+    assert torch.equal(y, gemm(x, w, split=True))
+    exact, mag = base(x.cpu().numpy())
+    check_f16_rounding(y.cpu().numpy(), exact, mag)
 
 
 @pytest.mark.parametrize("D,M,ranks,wdt", [(256, 37, (32, 32, 32, 64), torch.float16),
@@ -178,13 +220,14 @@ def test_sb6_gemm_epilogues_groups_and_row_independence(orc):
     rng = np.random.default_rng(7)
     qblk, qsqm, ddm = (dev(z) for z in random_k3(3 * D, D, rng))
     x = dev(rng.standard_normal((3, M, D)).astype(np.float32))
-    fused = Q.rwkvq_sb6_gemm(x, qblk, qsqm, ddm, 3 * D, D, out_per=D)
+    fused = Q.rwkvq_sb6_gemm(x, qblk, qsqm, ddm, 3 * D, D, out_per=D, split=False)
     for g in range(3):
         rows = slice(g * D, (g + 1) * D)
-        sep = Q.rwkvq_sb6_gemm(x[g], qblk[rows], qsqm[rows], ddm[rows], D, D)
+        sep = Q.rwkvq_sb6_gemm(x[g], qblk[rows], qsqm[rows], ddm[rows], D, D, split=False)
         assert torch.equal(fused[:, rows], sep), g
         for m in (0, 63, 199):   # a row alone gives the same bits as inside the launch
-            assert torch.equal(Q.rwkvq_sb6_gemm(x[g, m:m + 1], qblk[rows], qsqm[rows], ddm[rows], D, D)[0], sep[m])
+            assert torch.equal(Q.rwkvq_sb6_gemm(x[g, m:m + 1], qblk[rows], qsqm[rows], ddm[rows], D, D,
+                                                split=False)[0], sep[m])
     base = dev(rng.standard_normal((M, D)).astype(np.float32))
     y0 = Q.rwkvq_sb6_gemm(x[1], qblk[:D], qsqm[:D], ddm[:D], D, D)
     y1 = base.clone()
