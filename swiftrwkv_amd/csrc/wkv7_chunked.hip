@@ -50,7 +50,7 @@ constexpr int CH = 32;                             // tokens per chunk
 constexpr int RS = 68;                             // LDS row stride of 64-wide rows (16-byte rows, 4-bank steps)
 constexpr int MS = 36;                             // LDS row stride of the 32 × 32 matrices
 constexpr int WS_CHUNK = 2 * 64 * 64 + 2 * CH * 64;   // P, Q, G, E floats per chunk
-constexpr float kUnsafeDecay = 40.0f;              // e^{±40} keeps every scaled operand a normal float
+constexpr float kUnsafeDecay = 57.7f;              // 2^{±57.7} = e^{±40} keeps every scaled operand a normal float
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -75,6 +75,14 @@ __device__ __forceinline__ f32x4 mma4(float4 a, f32x4 b, f32x4 c) {
 __device__ __forceinline__ f32x4 mma4(f32x4 a, float4 b, f32x4 c) {
     return mma4(f4(a[0], a[1], a[2], a[3]), b, c);
 }
+__device__ __forceinline__ f32x4 mma4(f32x4 a, f32x4 b, f32x4 c) {
+    return mma4(f4(a[0], a[1], a[2], a[3]), f4(b[0], b[1], b[2], b[3]), c);
+}
+// 2^x and log2(x) of the hardware (v_exp_f32, v_log_f32: 1 ulp); every
+// argument here keeps them in the normal range.
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float lg2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float4 ex2(float4 x) { return f4(ex2(x.x), ex2(x.y), ex2(x.z), ex2(x.w)); }
 // Operand fetch for K block q (k = 16q + 4g + r): a row of M (k contiguous) or
 // a column of M (k down the rows).
 __device__ __forceinline__ float4 krow(const float* M, int ld, int row, int q, int g) {
@@ -144,8 +152,8 @@ __global__ __launch_bounds__(256, 2) void wkv7_chunk_prep_kernel(const TI* __res
             kv[u] = load4w(k + off);
             av[u] = load4w(a + off);
             bv[u] = load4w(b + off);
-            lw[u] = f4(logf(fmaxf(wv.x, 1e-35f)), logf(fmaxf(wv.y, 1e-35f)), logf(fmaxf(wv.z, 1e-35f)),
-                       logf(fmaxf(wv.w, 1e-35f)));
+            lw[u] = f4(lg2(fmaxf(wv.x, 1e-35f)), lg2(fmaxf(wv.y, 1e-35f)), lg2(fmaxf(wv.z, 1e-35f)),
+                       lg2(fmaxf(wv.w, 1e-35f)));
         }
     }
     float vreg[8];   // V[16q + 4g + u][col], q = 0..1
@@ -155,8 +163,8 @@ __global__ __launch_bounds__(256, 2) void wkv7_chunk_prep_kernel(const TI* __res
         vreg[e] = tg < T ? (float)v[(((int64_t)bb * T + tg) * H + h) * 64 + col] : 0.0f;
     }
 
-    // 2. L_t = Σ_{s≤t} log w_s: two-row sums, then each thread's prefix over
-    //    the earlier row pairs
+    // 2. L_t = Σ_{s≤t} log2 w_s (every decay factor below is a power of 2):
+    //    two-row sums, then each thread's prefix over the earlier row pairs
     at4(&Lx[rb * 64 + j4]) = f4(lw[0].x + lw[1].x, lw[0].y + lw[1].y, lw[0].z + lw[1].z, lw[0].w + lw[1].w);
     __syncthreads();
     float4 pre = f4(0, 0, 0, 0), tot = pre;
@@ -166,22 +174,21 @@ __global__ __launch_bounds__(256, 2) void wkv7_chunk_prep_kernel(const TI* __res
         if (q < rb) pre = f4(pre.x + x.x, pre.y + x.y, pre.z + x.z, pre.w + x.w);
         tot = f4(tot.x + x.x, tot.y + x.y, tot.z + x.z, tot.w + x.w);
     }
-    if (rb == 0) at4(&lam[j4]) = f4(expf(tot.x), expf(tot.y), expf(tot.z), expf(tot.w));
+    if (rb == 0) at4(&lam[j4]) = ex2(tot);
+    // every wave holds all 64 columns' totals, formed in the same order by
+    // every thread, so a wave vote gives each wave the same answer
     const int unsafe_cols = (-tot.x > kUnsafeDecay) | (-tot.y > kUnsafeDecay) | (-tot.z > kUnsafeDecay) |
                             (-tot.w > kUnsafeDecay);
-    const bool unsafe = __syncthreads_or(unsafe_cols);
+    const bool unsafe = __ballot(unsafe_cols) != 0;
     const float4 L0 = f4(pre.x + lw[0].x, pre.y + lw[0].y, pre.z + lw[0].z, pre.w + lw[0].w);
     const float4 L1 = f4(L0.x + lw[1].x, L0.y + lw[1].y, L0.z + lw[1].z, L0.w + lw[1].w);
 
     // 3. the four CH × CH matrices
     const int t0 = 2 * rb;
     if (!unsafe) {
-        // R̃ = r e^{L_t}, Ã = a e^{L_{t−1}}, K̃ = k e^{−L_t}, B̃ = b e^{−L_t}
-        const float4 e0 = f4(expf(L0.x), expf(L0.y), expf(L0.z), expf(L0.w));
-        const float4 e1 = f4(expf(L1.x), expf(L1.y), expf(L1.z), expf(L1.w));
-        const float4 em = f4(expf(pre.x), expf(pre.y), expf(pre.z), expf(pre.w));
-        const float4 i0 = f4(__frcp_rn(e0.x), __frcp_rn(e0.y), __frcp_rn(e0.z), __frcp_rn(e0.w));
-        const float4 i1 = f4(__frcp_rn(e1.x), __frcp_rn(e1.y), __frcp_rn(e1.z), __frcp_rn(e1.w));
+        // R̃ = r 2^{L_t}, Ã = a 2^{L_{t−1}}, K̃ = k 2^{−L_t}, B̃ = b 2^{−L_t}
+        const float4 e0 = ex2(L0), e1 = ex2(L1), em = ex2(pre);
+        const float4 i0 = ex2(f4(-L0.x, -L0.y, -L0.z, -L0.w)), i1 = ex2(f4(-L1.x, -L1.y, -L1.z, -L1.w));
         auto mul = [](float4 x, float4 y) { return f4(x.x * y.x, x.y * y.y, x.z * y.z, x.w * y.w); };
         at4(&R[t0 * RS + j4]) = mul(rv[0], e0);
         at4(&R[(t0 + 1) * RS + j4]) = mul(rv[1], e1);
@@ -215,6 +222,7 @@ __global__ __launch_bounds__(256, 2) void wkv7_chunk_prep_kernel(const TI* __res
             M[(16 + t) * MS + 16 + i] = keep ? d11[u] : 0.0f;
         }
     } else {
+        __syncthreads();   // the row-pair sums (Lx) are read above; L reuses them
         at4(&R[t0 * RS + j4]) = rv[0];
         at4(&R[(t0 + 1) * RS + j4]) = rv[1];
         at4(&A[t0 * RS + j4]) = av[0];
@@ -235,8 +243,8 @@ __global__ __launch_bounds__(256, 2) void wkv7_chunk_prep_kernel(const TI* __res
             float rk = 0.f, rb_ = 0.f, ak = 0.f, ab = 0.f;
             for (int j = 0; j < 64; ++j) {
                 const float ls = L[s * RS + j];
-                const float e1 = expf(L[t * RS + j] - ls);
-                const float e0 = t > 0 ? expf(L[(t - 1) * RS + j] - ls) : 0.0f;
+                const float e1 = exp2f(L[t * RS + j] - ls);
+                const float e0 = t > 0 ? exp2f(L[(t - 1) * RS + j] - ls) : 0.0f;
                 rk += R[t * RS + j] * K[s * RS + j] * e1;
                 rb_ += R[t * RS + j] * Bv[s * RS + j] * e1;
                 ak += A[t * RS + j] * K[s * RS + j] * e0;
@@ -250,21 +258,20 @@ __global__ __launch_bounds__(256, 2) void wkv7_chunk_prep_kernel(const TI* __res
             }
         }
         __syncthreads();
-        // R̃, Ã, K̂ = k e^{L_end − L_s}, B̂ likewise, with factors ≤ 1
+        // R̃, Ã, K̂ = k 2^{L_end − L_s}, B̂ likewise, with factors ≤ 1
         for (int e = tid; e < CH * 64; e += 256) {
             const int t = e >> 6, j = e & 63;
-            const float d = expf(L[(CH - 1) * RS + j] - L[t * RS + j]);
+            const float d = exp2f(L[(CH - 1) * RS + j] - L[t * RS + j]);
             K[t * RS + j] *= d;
             Bv[t * RS + j] *= d;
-            R[t * RS + j] *= expf(L[t * RS + j]);
-            A[t * RS + j] *= t > 0 ? expf(L[(t - 1) * RS + j]) : 1.0f;
+            R[t * RS + j] *= exp2f(L[t * RS + j]);
+            A[t * RS + j] *= t > 0 ? exp2f(L[(t - 1) * RS + j]) : 1.0f;
         }
     }
     __syncthreads();
 
-    // 4. K̂ = K̃ e^{L_end}, B̂ likewise (scaled branch); T11 and T22 by forward
-    //    substitution (four partial sums per dot product); each wave its slab
-    //    of Z = Mak·V
+    // 4. K̂ = K̃ 2^{L_end}, B̂ likewise (scaled branch); T11 and T22 on the
+    //    matrix cores; each wave its slab of Z = Mak·V
     if (!unsafe) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -275,17 +282,28 @@ __global__ __launch_bounds__(256, 2) void wkv7_chunk_prep_kernel(const TI* __res
             bq = f4(bq.x * lm.x, bq.y * lm.y, bq.z * lm.z, bq.w * lm.w);
         }
     }
-    if (wave < 2 && lane < 16) {
+    if (wave < 2) {
+        // N = the strictly lower diagonal block o of Mab, N^16 = 0, so
+        // (I − N)⁻¹ = (I + N⁸)(I + N⁴)(I + N²)(I + N).  An accumulator
+        // (lane i + 16g: rows 4g..4g+3 of column i) is the B operand of a
+        // product and, read as a transpose, its A operand; so the powers are
+        // formed with their transposes and every product stays in registers.
         const int o = 16 * wave;
-        float x[16];
+        const float4 nA = at4(&Mab[(o + i) * MS + o + 4 * g]);                   // N[i][4g + r]
+        const float4 nB = f4(Mab[(o + 4 * g) * MS + o + i], Mab[(o + 4 * g + 1) * MS + o + i],
+                             Mab[(o + 4 * g + 2) * MS + o + i], Mab[(o + 4 * g + 3) * MS + o + i]);   // N[4g + r][i]
+        const f32x4 n2 = mma4(nA, nB, zero4());     // N²
+        const f32x4 n2t = mma4(nB, nA, zero4());    // (N²)ᵀ
+        const f32x4 n4t = mma4(n2, n2t, zero4());   // (N⁴)ᵀ
+        const f32x4 n4 = mma4(n2t, n2, zero4());    // N⁴
+        const f32x4 n8t = mma4(n4, n4t, zero4());   // (N⁸)ᵀ
+        f32x4 x = {nB.x + (4 * g == i ? 1.0f : 0.0f), nB.y + (4 * g + 1 == i ? 1.0f : 0.0f),
+                   nB.z + (4 * g + 2 == i ? 1.0f : 0.0f), nB.w + (4 * g + 3 == i ? 1.0f : 0.0f)};   // I + N
+        x = mma4(n2t, x, x);   // (I + N²)·x
+        x = mma4(n4t, x, x);   // (I + N⁴)·x
+        x = mma4(n8t, x, x);   // (I + N⁸)·x
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            float part[4] = {t == lane ? 1.0f : 0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < t; ++s) part[s & 3] += Mab[(o + t) * MS + o + s] * x[s];
-            x[t] = (part[0] + part[1]) + (part[2] + part[3]);
-            Tm[(o + t) * MS + o + lane] = x[t];
-        }
+        for (int u = 0; u < 4; ++u) Tm[(o + 4 * g + u) * MS + o + i] = x[u];
     }
     const float4 v0 = f4(vreg[0], vreg[1], vreg[2], vreg[3]), v1 = f4(vreg[4], vreg[5], vreg[6], vreg[7]);
     f32x4 z0 = mma4(krow(Mak, MS, i, 0, g), v0, zero4());
@@ -359,38 +377,53 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // Where the scan's stores for steps past T go (never read).
 __device__ float g_scan_sink[512];
 
-// Operands of one chunk for one lane of the scan (lane i + 16g of wave w,
-// value-row slice sl).
-struct ScanOps {
+// Operands of one chunk for one lane of the scan's state waves (wave w < 4:
+// state columns 16w..16w+15, value-row slice sl, lane i + 16g) and of its
+// output waves (wave 4 + w: the K quarter 16w..16w+15 of the outputs).
+struct StateOps {
     float4 p[4];    // P[16q + 4g + r][16w + i], q = 0..3
     float4 q;       // Q[16 sl + 4g + r][16w + i]
+};
+struct OutOps {
     float4 gk[2];   // G[16tt + i][16w + 4g + r], tt = 0..1
     float2 e;       // E[token][row], this thread's two outputs
 };
 
-__device__ __forceinline__ void scan_load(ScanOps& o, const float* base, int c, int wave, int g, int i, int slice,
-                                          int tid) {
+__device__ __forceinline__ void load_state_ops(StateOps& o, const float* base, int c, int w, int g, int i, int slice) {
     const float* P = base + (int64_t)c * WS_CHUNK;
     const float* Q = P + 4096;
-    const float* G = P + 8192;
-    const float* E = G + CH * 64;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) o.p[q] = *reinterpret_cast<const float4*>(P + (((wave * 4 + q) * 4 + g) * 16 + i) * 4);
-    o.q = *reinterpret_cast<const float4*>(Q + (((slice * 4 + wave) * 4 + g) * 16 + i) * 4);
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-        o.gk[tt] = *reinterpret_cast<const float4*>(G + (((wave * 2 + tt) * 4 + g) * 16 + i) * 4);
-    o.e = *reinterpret_cast<const float2*>(E + (slice * 32 + (tid >> 3)) * 16 + (tid & 7) * 2);
+    for (int q = 0; q < 4; ++q) o.p[q] = *reinterpret_cast<const float4*>(P + (((w * 4 + q) * 4 + g) * 16 + i) * 4);
+    o.q = *reinterpret_cast<const float4*>(Q + (((slice * 4 + w) * 4 + g) * 16 + i) * 4);
 }
 
-// Kernel 2: the chunks in order for 16 value rows of one (b, h).  S and the
-// partial outputs are double-buffered in LDS, so one barrier per chunk
-// separates every write from its readers.
-__global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const float* __restrict__ ws,
+__device__ __forceinline__ void load_out_ops(OutOps& o, const float* base, int c, int w, int g, int i, int slice,
+                                             int ot, int orow) {
+    const float* G = base + (int64_t)c * WS_CHUNK + 8192;
+    const float* E = G + CH * 64;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+        o.gk[tt] = *reinterpret_cast<const float4*>(G + (((w * 2 + tt) * 4 + g) * 16 + i) * 4);
+    o.e = *reinterpret_cast<const float2*>(E + (slice * 32 + ot) * 16 + orow);
+}
+
+constexpr int YS = 36;   // LDS row stride of the partial outputs [wave][row][token] (conflict-free writes)
+
+// Kernel 2: the chunks in order for 16 value rows of one (b, h), with 8
+// waves.  Phase p (one barrier each): the state waves form
+// S_{p+1} = S_p·P_p + Q_p (wave w: state columns 16w..16w+15, 16 MFMAs); the
+// output waves, on the same SIMDs, form the partial outputs of chunk p from
+// the same S_p (wave 4 + w: the K quarter 16w..16w+15 for all 32 tokens, 8
+// MFMAs) and emit chunk p − 1's outputs from the partials of the previous
+// phase.  The output waves' products fill the matrix pipe while the state
+// chain waits for LDS and the barrier.  S and the partial outputs are
+// double-buffered in LDS.
+__global__ __launch_bounds__(512) void wkv7_chunk_scan_kernel(const float* ws,
                                                               const float* __restrict__ h_in, float* __restrict__ out,
                                                               float* __restrict__ h_out, int T, int H, int NC, int BH) {
     __shared__ __attribute__((aligned(16))) float S[2][16 * RS];
-    __shared__ __attribute__((aligned(16))) float Yp[2][4 * CH * 17];   // partial outputs [wave][token][row]
+    __shared__ __attribute__((aligned(16))) float Sspare[16 * RS];   // state of phantom chunks (never read)
+    __shared__ __attribute__((aligned(16))) float Yp[2][4 * 16 * YS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, li = lane & 15;
     // workgroups are dealt to the 8 XCDs round-robin (id mod 8); the four
@@ -403,71 +436,110 @@ __global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const float* __res
     const int h = bh % H, bb = bh / H;
     const int i0 = slice * 16;
     const int64_t hoff = (int64_t)bh * 4096;
-    for (int e = tid; e < 16 * 64; e += 256) {
+    for (int e = tid; e < 16 * 64; e += 512) {
         const int ii = e >> 6, j = e & 63;
         S[0][ii * RS + j] = h_in ? h_in[hoff + (i0 + ii) * 64 + j] : 0.0f;
     }
     const float* base = ws + (int64_t)bh * NC * WS_CHUNK;
-    const int col = 16 * wave + li;
-    const int ot = tid >> 3, orow = (tid & 7) * 2;   // this thread's two outputs: token ot, rows orow, orow + 1
+    const int w = wave & 3;
 
-    auto step = [&](int c, const ScanOps& o) {
-        const float* Sc = S[c & 1];
-        float* Sn = S[(c & 1) ^ 1];
-        float* Y = Yp[c & 1];
-        float4 av[4];
+    if (wave < 4) {
+        // state waves
+        const int col = 16 * w + li;
+        auto phase = [&](int p, StateOps& o) {
+            const float* Sc = S[p & 1];
+            float* Sn = p < NC ? S[(p & 1) ^ 1] : Sspare;
+            float4 av[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) av[q] = at4(const_cast<float*>(Sc) + li * RS + 16 * q + 4 * g);
-        const float4 aw = at4(const_cast<float*>(Sc) + li * RS + 16 * wave + 4 * g);   // this wave's K quarter
-        f32x4 acc0 = {o.q.x, o.q.y, o.q.z, o.q.w}, acc1 = zero4();
-        f32x4 y0 = mma4(aw, o.gk[0], zero4());
-        acc0 = mma4(av[0], o.p[0], acc0);
-        f32x4 y1 = mma4(aw, o.gk[1], zero4());
-        acc1 = mma4(av[1], o.p[1], acc1);
-        acc0 = mma4(av[2], o.p[2], acc0);
-        acc1 = mma4(av[3], o.p[3], acc1);
-        // partial Y[row 4g + r][token 16 tt + li] of this wave's K quarter
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            Y[(wave * CH + li) * 17 + 4 * g + r] = y0[r];
-            Y[(wave * CH + 16 + li) * 17 + 4 * g + r] = y1[r];
-        }
-        if (c < NC) {
+            for (int q = 0; q < 4; ++q) av[q] = at4(const_cast<float*>(Sc) + li * RS + 16 * q + 4 * g);
+            f32x4 acc0 = {o.q.x, o.q.y, o.q.z, o.q.w}, acc1 = zero4();
+            acc0 = mma4(av[0], o.p[0], acc0);
+            acc1 = mma4(av[1], o.p[1], acc1);
+            acc0 = mma4(av[2], o.p[2], acc0);
+            acc1 = mma4(av[3], o.p[3], acc1);
+            // the loads of chunk p + 3 into this slot, issued between the products
+            load_state_ops(o, base, min(p + 3, NC - 1), w, g, li, slice);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // LDS reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);   // loads
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) Sn[(4 * g + r) * RS + col] = acc0[r] + acc1[r];
-        }
+            lds_barrier();
+        };
+        // operands three chunks ahead; indexes past the end re-read the last
+        // chunk.  Issued in chunk order: the loop-head wait count is formed
+        // from the prologue too, so interleaved prologue loads would make
+        // every iteration wait for the loads it has just issued.
+        StateOps o0, o1, o2;
+        load_state_ops(o0, base, 0, w, g, li, slice);
+        asm volatile("" ::: "memory");
+        load_state_ops(o1, base, min(1, NC - 1), w, g, li, slice);
+        asm volatile("" ::: "memory");
+        load_state_ops(o2, base, min(2, NC - 1), w, g, li, slice);
+        asm volatile("" ::: "memory");
         lds_barrier();
-        float y[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            float sum = u == 0 ? o.e.x : o.e.y;
-#pragma unroll
-            for (int ww = 0; ww < 4; ++ww) sum += Y[(ww * CH + ot) * 17 + orow + u];
-            y[u] = sum;
+        for (int p = 0; p <= NC; p += 3) {
+            phase(p, o0);
+            phase(p + 1, o1);
+            phase(p + 2, o2);
         }
-        // steps past T (and phantom chunks past NC) store to a sink, so the
-        // loop body has no branch around its global memory operations
-        const int t = c * CH + ot;
-        float* dst = t < T ? out + (((int64_t)bb * T + t) * H + h) * 64 + i0 + orow : g_scan_sink + 2 * tid;
-        *reinterpret_cast<float2*>(dst) = make_float2(y[0], y[1]);
-    };
-
-    // operands three chunks ahead; indexes past the end re-read the last chunk
-    ScanOps o0, o1, o2;
-    scan_load(o0, base, 0, wave, g, li, slice, tid);
-    scan_load(o1, base, min(1, NC - 1), wave, g, li, slice, tid);
-    scan_load(o2, base, min(2, NC - 1), wave, g, li, slice, tid);
-    lds_barrier();
-    for (int c = 0; c < NC; c += 3) {
-        step(c, o0);
-        scan_load(o0, base, min(c + 3, NC - 1), wave, g, li, slice, tid);
-        step(c + 1, o1);
-        scan_load(o1, base, min(c + 4, NC - 1), wave, g, li, slice, tid);
-        step(c + 2, o2);
-        scan_load(o2, base, min(c + 5, NC - 1), wave, g, li, slice, tid);
+    } else {
+        // output waves: this thread's two outputs of a chunk are token ot,
+        // rows orow and orow + 1; chunk c's start at out0 + c·cstride
+        const int u = tid - 256;
+        const int ot = u >> 3, orow = (u & 7) * 2;
+        float* const out0 = out + (((int64_t)bb * T + ot) * H + h) * 64 + i0 + orow;
+        const int64_t cstride = (int64_t)CH * H * 64;
+        // phase p: chunk p's partials from `cur`, chunk p − 1's outputs from
+        // `prev`'s E, then `prev` is reloaded with chunk p + 2
+        auto phase = [&](int p, const OutOps& cur, OutOps& prev) {
+            const float* Sc = S[p & 1];
+            float* Y = Yp[p & 1];
+            const float* Ye = Yp[(p & 1) ^ 1];
+            const float4 aw = at4(const_cast<float*>(Sc) + li * RS + 16 * w + 4 * g);   // the K quarter
+            float y[2] = {prev.e.x, prev.e.y};
+#pragma unroll
+            for (int ww = 0; ww < 4; ++ww) {
+                y[0] += Ye[(ww * 16 + orow) * YS + ot];
+                y[1] += Ye[(ww * 16 + orow + 1) * YS + ot];
+            }
+            const f32x4 y0 = mma4(aw, cur.gk[0], zero4());
+            const f32x4 y1 = mma4(aw, cur.gk[1], zero4());
+            // chunk p − 1's outputs; steps past T (the phantom chunk −1 and
+            // chunks past NC) store to a sink
+            const int t = (p - 1) * CH + ot;
+            float* dst = (unsigned)t < (unsigned)T ? out0 + (int64_t)(p - 1) * cstride : g_scan_sink + 2 * u;
+            *reinterpret_cast<float2*>(dst) = make_float2(y[0], y[1]);
+            load_out_ops(prev, base, min(p + 2, NC - 1), w, g, li, slice, ot, orow);
+            // partial Yᵀ[row 4g + r][token 16 tt + li] of this wave's K quarter
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                Y[(w * 16 + 4 * g + r) * YS + li] = y0[r];
+                Y[(w * 16 + 4 * g + r) * YS + 16 + li] = y1[r];
+            }
+            lds_barrier();
+        };
+        OutOps o0, o1, o2;
+        load_out_ops(o0, base, 0, w, g, li, slice, ot, orow);
+        asm volatile("" ::: "memory");
+        load_out_ops(o1, base, min(1, NC - 1), w, g, li, slice, ot, orow);
+        asm volatile("" ::: "memory");
+        o2.gk[0] = o2.gk[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        o2.e = make_float2(0.f, 0.f);
+        lds_barrier();
+        for (int p = 0; p <= NC; p += 3) {
+            phase(p, o0, o2);
+            phase(p + 1, o1, o0);
+            phase(p + 2, o2, o1);
+        }
     }
     const float* Sf = S[NC & 1];
-    for (int e = tid; e < 16 * 64; e += 256) {
+    for (int e = tid; e < 16 * 64; e += 512) {
         const int ii = e >> 6, j = e & 63;
         h_out[hoff + (i0 + ii) * 64 + j] = Sf[ii * RS + j];
     }
@@ -479,7 +551,7 @@ rwkv_status run_chunked(const void* r, const void* w, const void* k, const void*
     const int NC = (T + CH - 1) / CH;
     rwkv::launch(wkv7_chunk_prep_kernel<TI>, dim3((unsigned)(B * H * NC)), dim3(256), s, (const TI*)r, (const TI*)w,
                  (const TI*)k, (const TI*)v, (const TI*)a, (const TI*)b, ws, T, H, NC);
-    rwkv::launch(wkv7_chunk_scan_kernel, dim3((unsigned)((B * H + 7) / 8 * 32)), dim3(256), s, (const float*)ws, h_in,
+    rwkv::launch(wkv7_chunk_scan_kernel, dim3((unsigned)((B * H + 7) / 8 * 32)), dim3(512), s, (const float*)ws, h_in,
                  out, h_out, T, H, NC, B * H);
     return hipGetLastError() == hipSuccess ? RWKV_OK : RWKV_E_HIP;
 }
