@@ -812,6 +812,56 @@ def bench_head_gemv(model, dev, reps=60):
     return nbytes, avg_ms, durs[len(durs) // 2]
 
 
+def bench_sym_gemv(dev, reps=60):
+    """The sym GEMV (rwkv_sym_gemv, batch 1) on the 1.5B FFN shapes, 8- and
+    6-bit: the average duration per launch (its own timestamps) over weight
+    copies rotated through more than the 256 MB MALL, so every launch streams
+    its matrix from HBM.  Bytes per launch = codes + group scales + super-block
+    scales + the fp32 input and output rows.  The codes are random bytes and
+    the scales small fp16 values (the kernel's work does not depend on them)."""
+    import torch
+    from swiftrwkv_amd import _lib
+
+    L = _lib.lib()
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    for OUT, IN in ((8192, 2048), (2048, 8192)):
+        for bits in (8, 6):
+            NB = IN // 16
+            qbytes = OUT * (IN if bits == 8 else IN // 32 * 24)
+            per_copy = qbytes + OUT * NB + OUT * ((NB + 15) // 16) * 2
+            copies = max(2, -(-300_000_000 // per_copy))
+            bufs = []
+            for _ in range(copies):
+                q = torch.randint(0, 256, (qbytes,), dtype=torch.uint8, device=dev, generator=g)
+                qs = torch.randint(0, 256, (OUT * NB,), dtype=torch.uint8, device=dev, generator=g)
+                d = (torch.rand(OUT * ((NB + 15) // 16), device=dev, generator=g) * 1e-3).to(torch.float16)
+                bufs.append((q, qs, d))
+            x = torch.randn((1, IN), device=dev, generator=g)
+            y = torch.empty((1, OUT), device=dev)
+
+            def launch(c):
+                q, qs, d = bufs[c % copies]
+                _lib.check(L.rwkv_sym_gemv(x.data_ptr(), 1, q.data_ptr(), qs.data_ptr(), d.data_ptr(), y.data_ptr(),
+                                           OUT, IN, bits, OUT, stream.cuda_stream))
+
+            for i in range(2 * copies):
+                launch(i)
+            torch.cuda.synchronize()
+            durs = [kernel_ms(lambda i=i: launch(i), stream) for i in range(reps)]
+            avg_ms = sum(durs) / len(durs)
+            nbytes = per_copy + 4 * (IN + OUT)
+            gbps = nbytes / (avg_ms * 1e-3) / 1e9
+            res[f"sym{bits}_gemv_{OUT}x{IN}"] = {"bytes": nbytes, "avg_us": avg_ms * 1e3, "GBps": gbps,
+                                                 "hbm_frac": gbps / HBM_PEAK_GBPS, "weight_copies_rotated": copies}
+            log(f"sym{bits} GEMV {OUT}x{IN}: {nbytes / 1e6:.2f} MB, avg {avg_ms * 1e3:.2f} us -> {gbps:.0f} GB/s")
+            del bufs
+            torch.cuda.empty_cache()
+    return res
+
+
 def bench_wkv(dev, reps=5):
     import numpy as np
     import torch
@@ -1214,6 +1264,7 @@ def main():
     extra = {"decode_1.5B_gemv_wkv_chain_batch1": head["chain"], "decode_1.5B_batch16": head["batch16"]}
     model01, more01 = config1_0b1(args, dev)
     extra.update(more01)
+    extra.update(bench_sym_gemv(dev))
     if not args.skip_wkv:
         extra.update(bench_wkv(dev))
         log("wkv done")
