@@ -68,6 +68,12 @@ def sigmoid(x):
     return 1.0 / (1.0 + np.exp(-np.asarray(x, np.float64)))
 
 
+def decay(ww):
+    """The per-step decay from the w branch's output (RWKVBlock.swift:207-210,
+    X070Generation.swift:274, X070Backbone.swift:1132): exp(-0.606531 · σ(ww))."""
+    return np.exp(-0.606531 * sigmoid(ww))
+
+
 @dataclass
 class State:
     """RWKVState (X070Generation.swift:27-45) for N rows: wkv [L, N, H, 64, 64],
@@ -123,7 +129,7 @@ def core(p, l, r, k0, v, la, v_first, wkv, H):
         v = v + (v_first - v) * vv
     a = sigmoid(lin(la_, p[t + "a_lora_B.weight"]) + p[t + "a_lora_B.bias"])
     ww = lin(lw, p[t + "w_lora_B.weight"]) + p[t + "w_lora_B.bias"]
-    w = np.exp(-0.606531 * sigmoid(ww))
+    w = decay(ww)
     kk = l2norm_heads(k0 * p[t + "k_k"], H)
     k = k0 * (1.0 + (a - 1.0) * p[t + "k_a"])
     sh = lambda z: np.asarray(z, np.float64).reshape(N, 1, H, HEAD)
@@ -192,7 +198,7 @@ def sequence(p, W, ids, n_layer, H):
             v = v + (v_first - v) * vv
         a = sigmoid(lin(lin(m["a"], p[t + "a_lora_A.weight"]), p[t + "a_lora_B.weight"]) + p[t + "a_lora_B.bias"])
         ww = lin(np.tanh(lin(m["w"], p[t + "w_lora_A.weight"])), p[t + "w_lora_B.weight"]) + p[t + "w_lora_B.bias"]
-        w = np.exp(-0.606531 * sigmoid(ww))
+        w = decay(ww)
         kk = l2norm_heads(k0 * p[t + "k_k"], H)
         k = k0 * (1.0 + (a - 1.0) * p[t + "k_a"])
         sh = lambda z: np.asarray(z, np.float64).reshape(1, T, H, HEAD)
@@ -256,7 +262,7 @@ def prefill(p, W, ids, n_layer, H, f16_base=False):
             v = v + (v_first - v) * vv
         a = sigmoid(wide(wide(m["a"], p[t + "a_lora_A.weight"]), p[t + "a_lora_B.weight"]) + p[t + "a_lora_B.bias"])
         ww = wide(np.tanh(wide(m["w"], p[t + "w_lora_A.weight"])), p[t + "w_lora_B.weight"]) + p[t + "w_lora_B.bias"]
-        w = np.exp(-0.606531 * sigmoid(ww))
+        w = decay(ww)
         kk = l2norm_heads(k0 * p[t + "k_k"], H)
         k = k0 * (1.0 + (a - 1.0) * p[t + "k_a"])
         sh = lambda z: np.asarray(z, np.float64).reshape(1, T, H, HEAD)

@@ -9,7 +9,9 @@
   (X070Generation.swift:369-376);
 * v_first does not cross a step (X070Generation.swift:50-57: zeroing it
   before `step` leaves the logits unchanged);
-* rows of a batch are independent.
+* rows of a batch are independent;
+* the decay constant, by RWKV-7's log-decay form (the step and the sequence
+  share `decay`, so their agreement cannot catch a wrong constant).
 """
 import numpy as np
 import pytest
@@ -19,6 +21,16 @@ from oracle import x070 as X
 from swiftrwkv_amd import synthetic as syn
 
 TINY = syn.X070Shape("tiny", 2, 256, 1024, vocab=512)
+
+
+def test_decay_matches_log_decay_form():
+    """RWKV-7 forms the log decay as w = −softplus(−z) − 1/2 and decays by
+    exp(−exp(w)); exp(−softplus(−z)) = σ(z), so the decay is exp(−e^{−1/2}·σ(z)),
+    and the reference's 0.606531 is e^{−1/2} to six figures.  A wrong constant,
+    a missing sigmoid or a sign slip fails at this tolerance."""
+    z = np.linspace(-30.0, 30.0, 2001)
+    want = np.exp(-np.exp(-np.logaddexp(0.0, -z) - 0.5))
+    np.testing.assert_allclose(X.decay(z), want, rtol=2e-6, atol=0.0)
 
 
 @pytest.fixture(scope="module")
