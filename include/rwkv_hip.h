@@ -153,6 +153,17 @@ rwkv_status rwkv_wkv_tail(const float* wkv, const float* r, const float* k, cons
                           const float* rk, const float* lnw, const float* lnb, const float* g,
                           float* out, int64_t N, int64_t H, int64_t S, float eps, void* stream);
 
+/* rwkv_wkv_tail with the output in out_dt: f32 (rwkv_wkv_tail) or f16, the
+ * rounding the fp16 long pass of the o_proj matmul applies to its input
+ * (X070Backbone.swift:337-356 casts x to the fp16 base), so a parallel pass
+ * hands the projection the values it would use, in half the bytes.  The same
+ * replaced interface: wkvTail (WKV7DecodeKernels.swift:106-178) feeding
+ * RWKVBlock's o_proj (RWKVBlock.swift:269-273). */
+rwkv_status rwkv_wkv_tail_to(const float* wkv, const float* r, const float* k, const float* v,
+                             const float* rk, const float* lnw, const float* lnb, const float* g,
+                             void* out, rwkv_dtype out_dt, int64_t N, int64_t H, int64_t S, float eps,
+                             void* stream);
+
 /* Decode step and tmix tail in one launch, fp32, head size 64: the state
  * update of rwkv_wkv7_step followed by rwkv_wkv_tail (S = 64) on its output,
  * bitwise equal to calling the two.  No single counterpart in the reference:
@@ -307,10 +318,15 @@ rwkv_status rwkv_sym_gemv_ep(const float* x, int64_t N,
  * epilogue 0 stores, 1 adds into y (fp32; the residual update), 2 stores
  * relu(·)² as fp16 (y is then an fp16 buffer; cmix's key, exact in fp16).
  * workspace: NULL, or device memory of rwkv_quant_gemm_workspace(M, OUT, IN)
- * bytes (16-byte aligned) — shapes with few 128 × 128 output tiles then split
- * the K sum into ranges summed in a fixed order by a second kernel (the same
- * bound, deterministic, far faster for a few hundred rows); with NULL the
- * launch is one range.  Launches sharing a workspace must not overlap. */
+ * bytes (16-byte aligned; a smaller one is refused before any launch).  With
+ * it, shapes with few 128 × 128 output tiles split the K sum into ranges
+ * summed in a fixed order by a second kernel (the same bound, deterministic,
+ * far faster for a few hundred rows), and shapes with at least 128 output
+ * tiles of 256 × 256 and f16 inputs dequantise the weight into the
+ * workspace (rwkv_sb6_dequant / rwkv_sym_dequant, f16) and run rwkv_f16_gemm
+ * over it — the same products in the same order, so bitwise the one-range
+ * result, at 2-2.5x its speed for M >= 4096.  With NULL the launch is one
+ * range.  Launches sharing a workspace must not overlap. */
 int rwkv_sb6_gemm_applies(int64_t OUT, int64_t IN, int xbits, int64_t out_per);
 int64_t rwkv_quant_gemm_workspace(int64_t M, int64_t OUT, int64_t IN);
 rwkv_status rwkv_sb6_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda, int64_t x_group_stride,
@@ -328,6 +344,18 @@ rwkv_status rwkv_sym_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda
                           const uint8_t* qblk, const uint8_t* qs, const uint16_t* d, void* y, int64_t ldy,
                           int64_t OUT, int64_t IN, int bits, int64_t out_per, int epilogue, void* workspace,
                           int64_t workspace_bytes, void* stream);
+
+/* The long pass's fp16 matmul on a dense fp16 weight w [OUT][IN] (K
+ * contiguous; the fp16 matmul of baseMatmul once the weight is dequantised,
+ * X070Backbone.swift:337-356): y = epilogue(fp16(x·wᵀ)), fp32 sums, x
+ * [groups][M][lda] f16 with groups = OUT / out_per as rwkv_sb6_gemm, the same
+ * epilogues.  256 × 256 output tiles: OUT and out_per multiples of 256, IN of
+ * 128, lda >= IN and a multiple of 8, x and w 16-byte aligned
+ * (rwkv_f16_gemm_applies for lda = IN).  Each output is rwkv_sb6_gemm's /
+ * rwkv_sym_gemm's bitwise when w is the fp16 weight those decode. */
+int rwkv_f16_gemm_applies(int64_t M, int64_t OUT, int64_t IN, int64_t out_per);
+rwkv_status rwkv_f16_gemm(const void* x, int64_t M, int64_t lda, int64_t x_group_stride, const void* w, void* y,
+                          int64_t ldy, int64_t OUT, int64_t IN, int64_t out_per, int epilogue, void* stream);
 
 /* ───────────────────────── x070 decode step around the hot path ───────────────────────── */
 /* fp32 activations; dense vector parameters fp32 (an fp16 file's values

@@ -85,6 +85,7 @@ _SIGS = {
     "rwkv_wkv7_step_tail": (I, [P] * 14 + [L, L, F, P]),
     "rwkv_wkv_tail_applies": (I, [L]),
     "rwkv_wkv_tail": (I, [P] * 9 + [L, L, L, F, P]),
+    "rwkv_wkv_tail_to": (I, [P] * 9 + [I, L, L, L, F, P]),
     "rwkv_sb6_dequant": (I, [P, P, P, P, I, L, L, I, P]),
     "rwkv_sym_dequant": (I, [P, P, P, P, I, L, L, I, P]),
     "rwkv_sym_rows": (I, [P, L, P, P, P, P, I, L, L, I, P]),
@@ -98,6 +99,8 @@ _SIGS = {
     "rwkv_sb6_gemm_applies": (I, [L, L, I, L]),
     "rwkv_sb6_gemm": (I, [P, I, L, L, L, P, P, P, P, L, L, L, I, L, I, P, L, P]),
     "rwkv_quant_gemm_workspace": (L, [L, L, L]),
+    "rwkv_f16_gemm_applies": (I, [L, L, L, L]),
+    "rwkv_f16_gemm": (I, [P, L, L, L, P, P, L, L, L, L, I, P]),
     "rwkv_sym_gemm_applies": (I, [L, L, I, L]),
     "rwkv_x070_seq_lora": (I, [P, L, L, P, P, P, P, P, I, L, L, L, L, I, P, P, P, P, P, P]),
     "rwkv_sym_gemm": (I, [P, I, L, L, L, P, P, P, P, L, L, L, I, L, I, P, L, P]),

@@ -6,7 +6,9 @@
 // (X070Backbone.baseMatmul, Sources/RWKVGen/X070Backbone.swift:337-356,
 // 733-739; the dequant of RwkvqDequant.swift:116-140 (sb6) and :350-388,
 // 442-466 (sym, whose fp16 branch computes in half)).  Here the dequant
-// happens in the GEMM's operand path: no dense weight is written.  Per
+// happens in the GEMM's operand path (quant_gemm_kernel: no dense weight is
+// written), or, for shapes with many output tiles, once per matrix into a
+// workspace that dense_gemm_kernel then multiplies (below).  Per
 // element the numbers are the reference's: the weight is exactly what the
 // dequant kernels store in fp16 — sb6 fp16(fma(code, half(qs·d), half(qm·dm))),
 // sym fp16((code − bias)·half(qs·d)) — the input is rounded to fp16, products
@@ -61,6 +63,22 @@ struct GemmArgs {
     float* part;          // splits > 1: the fp32 partial sums [splits][M][N]
     int splits;           // K ranges the tile's stages are divided into
 };
+
+// The epilogue of one output: fp16 rounding of the fp32 sum (the fp16
+// matmul's output), then store (fp32), add into y (fp32) or relu² (fp16).
+template <int EP>
+__device__ __forceinline__ void store_out(void* y, int64_t idx, float acc) {
+    const float v = hround(acc);
+    if constexpr (EP == 0) {
+        reinterpret_cast<float*>(y)[idx] = v;
+    } else if constexpr (EP == 1) {
+        float* p = reinterpret_cast<float*>(y) + idx;
+        *p = *p + v;
+    } else {
+        const float rl = fmaxf(v, 0.0f);
+        reinterpret_cast<_Float16*>(y)[idx] = (_Float16)(rl * rl);
+    }
+}
 
 // 4 bits → the low bit of 4 bytes (RwkvqSb6GEMV.swift:58-67 multiply spread).
 __device__ __forceinline__ uint32_t spread4(uint32_t nib) { return (nib * 0x00204081u) & 0x01010101u; }
@@ -350,7 +368,6 @@ __global__ __launch_bounds__(256, 2) void quant_gemm_kernel(GemmArgs g) {
             }
         return;
     }
-    // epilogue: fp16 rounding of the product, then store / add / relu² (fp16)
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
@@ -358,19 +375,151 @@ __global__ __launch_bounds__(256, 2) void quant_gemm_kernel(GemmArgs g) {
             const int row = m0 + 16 * i + 4 * gq + r;
             if (row >= g.M) continue;
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                const int64_t col = nb + 16 * j;
-                const float v = hround(acc[i][j][r]);
-                if constexpr (EP == 0) {
-                    reinterpret_cast<float*>(g.y)[(int64_t)row * g.ldy + col] = v;
-                } else if constexpr (EP == 1) {
-                    float* p = reinterpret_cast<float*>(g.y) + (int64_t)row * g.ldy + col;
-                    *p = *p + v;
-                } else {
-                    const float rl = fmaxf(v, 0.0f);
-                    reinterpret_cast<_Float16*>(g.y)[(int64_t)row * g.ldy + col] = (_Float16)(rl * rl);
-                }
-            }
+            for (int j = 0; j < NT; ++j) store_out<EP>(g.y, (int64_t)row * g.ldy + nb + 16 * j, acc[i][j][r]);
+        }
+    }
+}
+
+// ── dense fp16 weights ──
+//
+// y = epilogue(fp16(x · wᵀ)) for x [groups][M][lda] fp16 and w [N][K] fp16
+// (rows K-contiguous): the long pass once the weight is fp16 — a dense fp16
+// base, or a quantised one dequantised into a workspace (the quantised entry
+// points do that for shapes with many output tiles: one dequant per matrix
+// costs 10-35 µs against milliseconds of products at M ≥ 4096).
+//
+// A workgroup of 8 waves computes a 256 (input rows) × 256 (output features)
+// tile in stages of 64 columns.  Both operands are staged in LDS as rows of
+// 128 B whose 16-byte chunk c is stored at chunk c ^ (row & 7): the 8 lanes
+// reading one chunk column of 8 consecutive rows (an MFMA operand) or
+// writing 8 chunks of one row hit distinct banks.  Wave w takes input rows
+// 128·(w & 1) .. +127 and features 64·(w >> 1) .. +63: 8 × 4 accumulator
+// tiles of 16 × 16, 32 MFMAs per 32-column unit against 12 LDS operand reads
+// (the fused kernel's waves: 16 MFMAs against 8).  Each thread moves 8
+// chunks a stage (4 input rows, 4 weight rows) with buffer loads: one offset
+// register per input row and one for the weights (the stage and the row
+// group ride in the scalar offset), which leaves room at two waves per SIMD
+// for two register sets.  The loop body is two stages, each set loaded at
+// the top of one stage and written to LDS at the end of the next, so loads
+// have two stages to land and no register is copied (a copy of a register
+// whose load is in flight waits for the load).
+//
+// Per output the products and their order are the fused kernel's
+// (v_mfma_f32_16x16x32_f16 over the same 32-column units, first to last, the
+// same lane layout), so with w = the fp16 weight the fused kernel decodes,
+// the result is quant_gemm_kernel's bitwise.
+constexpr int DT = 256;         // dense tile: input rows = output features
+constexpr int DKS = 64;         // columns per stage
+constexpr int DENSE_MIN_TILES = 128;   // dense route from this many 256 × 256 tiles
+
+struct DenseArgs {
+    const _Float16* x;    // [groups][M][lda]
+    int64_t lda, x_gstride;
+    const _Float16* w;    // [N][K]
+    void* y;              // [M][ldy]
+    int64_t ldy;
+    int M, N, K, out_per;
+};
+
+template <int EP>
+__global__ __launch_bounds__(512, 1) void dense_gemm_kernel(DenseArgs g) {
+    __shared__ uint4 lds[2][2 * DT * 8];   // per stage: 256 input rows then 256 weight rows, 8 chunks each
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int gq = lane >> 4, li = lane & 15;
+    // Tiles in groups of 4 row blocks × every feature block, feature-major
+    // within a group; XCD x (workgroups x, x + 8, ...) takes a contiguous run
+    // of that order, so the 32 workgroups an XCD holds at once share 4 input
+    // row blocks and 8 weight blocks in its L2.
+    const int ntm = (g.M + DT - 1) / DT, ntn = g.N / DT, total = ntm * ntn;
+    const int xcd = blockIdx.x & 7, loc = blockIdx.x >> 3;
+    const int t = xcd * (total >> 3) + min(xcd, total & 7) + loc;
+    const int grp = t / (4 * ntn), first = 4 * grp, gm = min(4, ntm - first);
+    const int rr = t - grp * 4 * ntn;
+    const int m0 = (first + rr % gm) * DT, n0 = (rr / gm) * DT;
+    const int nst = g.K / DKS;
+
+    // staging: thread → chunk c of rows r0 + 64p (p < 4 input rows, clamped
+    // to the last row; p >= 4 weight rows), offsets from the tile's first row
+    const int c = tid & 7, r0 = tid >> 3;
+    const int mrows = min(DT, g.M - m0);
+    const _Float16* xt = g.x + (int64_t)(n0 / g.out_per) * g.x_gstride + (int64_t)m0 * g.lda;
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(xt), 0, (int)(mrows * g.lda * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(g.w + (int64_t)n0 * g.K), 0, (int)((int64_t)DT * g.K * 2), 0x00020000);
+    uint32_t xo[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) xo[p] = (uint32_t)((min(r0 + 64 * p, mrows - 1) * (int)g.lda + 8 * c) * 2);
+    const uint32_t wo = (uint32_t)((r0 * g.K + 8 * c) * 2), wrow64 = (uint32_t)(64 * g.K * 2);
+    const int dst0 = r0 * 8 + (c ^ (r0 & 7));   // row r0 + 64p: + 512p chunks, the same swizzle
+    auto gload = [&](uint4 (&v)[8], int st) {
+        const uint32_t so = (uint32_t)(min(st, nst - 1) * DKS * 2);
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+            v[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo[p], so, 0));
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+            v[4 + p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, so + p * wrow64, 0));
+    };
+    auto swrite = [&](int buf, const uint4 (&v)[8]) {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) lds[buf][dst0 + 512 * p] = v[p];
+    };
+
+    const int wm = wave & 1, wn = wave >> 1;
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // operand rows: li + 16·tile (row & 7 = li & 7 for every tile)
+    const int ra = (128 * wm + li) * 8, rb = (DT + 64 * wn + li) * 8;
+    auto products = [&](int buf) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int ch = (4 * kk + gq) ^ (li & 7);
+            half8 av[8], bv[4];
+#pragma unroll
+            for (int a = 0; a < 8; ++a) av[a] = __builtin_bit_cast(half8, lds[buf][ra + 128 * a + ch]);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) bv[b] = __builtin_bit_cast(half8, lds[buf][rb + 128 * b + ch]);
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[a], bv[b], acc[a][b], 0, 0, 0);
+        }
+    };
+
+    // nst is even; the last pair's loads repeat the last stage and its final
+    // LDS write lands in a buffer no later stage reads
+    uint4 va[8], vb[8];
+    gload(va, 0);
+    swrite(0, va);
+    gload(va, 1);
+    __syncthreads();
+    for (int st = 0; st < nst; st += 2) {
+        gload(vb, st + 2);
+        __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the products
+        products(0);
+        swrite(1, va);
+        __syncthreads();
+        gload(va, st + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        products(1);
+        swrite(0, vb);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = m0 + 128 * wm + 16 * a + 4 * gq + r;
+            if (row >= g.M) continue;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                store_out<EP>(g.y, (int64_t)row * g.ldy + n0 + 64 * wn + 16 * b + li, acc[a][b][r]);
         }
     }
 }
@@ -392,19 +541,9 @@ __global__ __launch_bounds__(256) void gemm_split_reduce(const float* __restrict
         a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
     }
     const int64_t row = 4 * i / N, col = 4 * i % N;
-    const float v[4] = {hround(a.x), hround(a.y), hround(a.z), hround(a.w)};
+    const float v[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        if constexpr (EP == 0) {
-            reinterpret_cast<float*>(y)[row * ldy + col + c] = v[c];
-        } else if constexpr (EP == 1) {
-            float* q = reinterpret_cast<float*>(y) + row * ldy + col + c;
-            *q = *q + v[c];
-        } else {
-            const float rl = fmaxf(v[c], 0.0f);
-            reinterpret_cast<_Float16*>(y)[row * ldy + col + c] = (_Float16)(rl * rl);
-        }
-    }
+    for (int c = 0; c < 4; ++c) store_out<EP>(y, row * ldy + col + c, v[c]);
 }
 
 // K ranges per launch: one where the (row block, feature block) tiles
@@ -421,9 +560,41 @@ int gemm_splits(int64_t M, int64_t N, int64_t K) {
     return (int)std::max<int64_t>(1, std::min(want, most));
 }
 
+// The dense kernel's shapes (x rows lda halves apart, group g at x + g·x_gstride).
+bool dense_shape_ok(int64_t M, int64_t OUT, int64_t IN, int64_t out_per, int64_t lda) {
+    return M >= 1 && M <= ((int64_t)1 << 24) && OUT >= DT && OUT % DT == 0 && OUT <= ((int64_t)1 << 30) &&
+           out_per >= DT && out_per % DT == 0 && OUT % out_per == 0 && IN >= 2 * DKS && IN % (2 * DKS) == 0 &&
+           lda >= IN && lda % 8 == 0 && (int64_t)DT * lda * 2 < ((int64_t)1 << 31) &&
+           ((M + DT - 1) / DT) * (OUT / DT) < ((int64_t)1 << 31);
+}
+
+// The quantised entry points take the dense route (dequantise into the
+// workspace, then dense_gemm_kernel) from DENSE_MIN_TILES tiles: half a round
+// of the 256 CUs.  Below it the fused kernel's 128 × 128 tiles (and its K
+// split) keep more CUs busy and no dequant is paid: 4096 rows × 1024 × 1024
+// took 34 µs fused against 9.5 + 34 µs dequant + dense.
+bool dense_prefers(int64_t M, int64_t OUT, int64_t IN) {
+    return dense_shape_ok(M, OUT, IN, OUT, IN) && ((M + DT - 1) / DT) * (OUT / DT) >= DENSE_MIN_TILES;
+}
+
 int64_t gemm_workspace(int64_t M, int64_t N, int64_t K) {
+    if (dense_prefers(M, N, K)) return N * K * 2;   // the fp16 weight
     const int S = gemm_splits(M, N, K);
     return S > 1 ? (int64_t)S * M * N * 4 : 0;
+}
+
+template <int EP>
+void launch_dense_ep(const DenseArgs& g, hipStream_t s) {
+    const int64_t tiles = (int64_t)((g.M + DT - 1) / DT) * (g.N / DT);
+    rwkv::launch(dense_gemm_kernel<EP>, dim3((unsigned)tiles), dim3(512), s, g);
+}
+
+void launch_dense(const DenseArgs& g, int epilogue, hipStream_t s) {
+    switch (epilogue) {
+        case 0: launch_dense_ep<0>(g, s); break;
+        case 1: launch_dense_ep<1>(g, s); break;
+        default: launch_dense_ep<2>(g, s); break;
+    }
 }
 
 // One tile shape: 128 × 128 with two workgroups per CU measured fastest
@@ -474,20 +645,35 @@ rwkv_status gemm_check(const char* who, const void* x, rwkv_dtype x_dt, int64_t 
     return RWKV_OK;
 }
 
-// The launch's K ranges: several where the shape asks for them and the
-// caller passed a workspace (which must then hold rwkv_quant_gemm_workspace
-// bytes), one otherwise.
-rwkv_status gemm_split_args(const char* who, GemmArgs& g, void* workspace, int64_t workspace_bytes) {
-    g.part = nullptr;
-    g.splits = 1;
-    const int64_t need = gemm_workspace(g.M, g.N, g.K);
-    if (workspace == nullptr || need == 0) return RWKV_OK;
+// A caller's workspace: NULL, or at least rwkv_quant_gemm_workspace bytes,
+// 16-byte aligned (checked before anything is launched).
+rwkv_status gemm_workspace_check(const char* who, int64_t M, int64_t N, int64_t K, const void* workspace,
+                                 int64_t workspace_bytes) {
+    if (workspace == nullptr) return RWKV_OK;
+    const int64_t need = gemm_workspace(M, N, K);
     RWKV_REQUIRE(workspace_bytes >= need && reinterpret_cast<uintptr_t>(workspace) % 16 == 0, RWKV_E_SHAPE,
                  "%s: workspace of %lld bytes (16-byte aligned) needed, %lld given", who, (long long)need,
                  (long long)workspace_bytes);
-    g.part = reinterpret_cast<float*>(workspace);
-    g.splits = gemm_splits(g.M, g.N, g.K);
     return RWKV_OK;
+}
+
+// The dense route of a quantised entry point: fp16 inputs, a workspace, and
+// a shape the dense kernel takes with enough tiles.
+bool take_dense(rwkv_dtype x_dt, int64_t M, int64_t OUT, int64_t IN, int64_t out_per, int64_t lda,
+                const void* workspace) {
+    return workspace != nullptr && x_dt == RWKV_F16 && dense_prefers(M, OUT, IN) &&
+           dense_shape_ok(M, OUT, IN, out_per, lda);
+}
+
+// The fused launch's K ranges: several where the shape asks for them and the
+// caller passed a workspace, one otherwise.
+void gemm_split_args(GemmArgs& g, void* workspace) {
+    g.part = nullptr;
+    g.splits = 1;
+    const int S = gemm_splits(g.M, g.N, g.K);
+    if (workspace == nullptr || S == 1 || dense_prefers(g.M, g.N, g.K)) return;
+    g.part = reinterpret_cast<float*>(workspace);
+    g.splits = S;
 }
 
 }  // namespace
@@ -513,14 +699,24 @@ rwkv_status rwkv_sb6_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda
                  (long long)OUT, (long long)out_per, (long long)IN);
     rwkv_status c = gemm_check("sb6_gemm", x, x_dt, M, lda, x_group_stride, ldy, OUT, IN, out_per, epilogue);
     if (c != RWKV_OK) return c;
-    GemmArgs g{x, lda, x_group_stride, qblk, qsqm, ddm, y, ldy, (int)M, (int)OUT, (int)IN, (int)out_per};
-    c = gemm_split_args("sb6_gemm", g, workspace, workspace_bytes);
+    c = gemm_workspace_check("sb6_gemm", M, OUT, IN, workspace, workspace_bytes);
     if (c != RWKV_OK) return c;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const bool f16 = x_dt == RWKV_F16;
-    if (xbits == 0) launch_gemm_ep<Sb6W<0>>(g, f16, epilogue, s);
-    else if (xbits == 1) launch_gemm_ep<Sb6W<1>>(g, f16, epilogue, s);
-    else launch_gemm_ep<Sb6W<2>>(g, f16, epilogue, s);
+    if (take_dense(x_dt, M, OUT, IN, out_per, lda, workspace)) {
+        c = rwkv_sb6_dequant(qblk, qsqm, ddm, workspace, RWKV_F16, OUT, IN, xbits, stream);
+        if (c != RWKV_OK) return c;
+        launch_dense(DenseArgs{reinterpret_cast<const _Float16*>(x), lda, x_group_stride,
+                               reinterpret_cast<const _Float16*>(workspace), y, ldy, (int)M, (int)OUT, (int)IN,
+                               (int)out_per},
+                     epilogue, s);
+    } else {
+        GemmArgs g{x, lda, x_group_stride, qblk, qsqm, ddm, y, ldy, (int)M, (int)OUT, (int)IN, (int)out_per};
+        gemm_split_args(g, workspace);
+        const bool f16 = x_dt == RWKV_F16;
+        if (xbits == 0) launch_gemm_ep<Sb6W<0>>(g, f16, epilogue, s);
+        else if (xbits == 1) launch_gemm_ep<Sb6W<1>>(g, f16, epilogue, s);
+        else launch_gemm_ep<Sb6W<2>>(g, f16, epilogue, s);
+    }
     RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "sb6_gemm: launch failed");
     rwkv::counters().sb6_gemm.fetch_add(1);
     rwkv::clear_error();
@@ -541,15 +737,47 @@ rwkv_status rwkv_sym_gemm(const void* x, rwkv_dtype x_dt, int64_t M, int64_t lda
                  bits, (long long)OUT, (long long)out_per, (long long)IN);
     rwkv_status c = gemm_check("sym_gemm", x, x_dt, M, lda, x_group_stride, ldy, OUT, IN, out_per, epilogue);
     if (c != RWKV_OK) return c;
-    GemmArgs g{x, lda, x_group_stride, qblk, qs, d, y, ldy, (int)M, (int)OUT, (int)IN, (int)out_per};
-    c = gemm_split_args("sym_gemm", g, workspace, workspace_bytes);
+    c = gemm_workspace_check("sym_gemm", M, OUT, IN, workspace, workspace_bytes);
     if (c != RWKV_OK) return c;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const bool f16 = x_dt == RWKV_F16;
-    if (bits == 8) launch_gemm_ep<SymW<8>>(g, f16, epilogue, s);
-    else launch_gemm_ep<SymW<6>>(g, f16, epilogue, s);
+    if (take_dense(x_dt, M, OUT, IN, out_per, lda, workspace)) {
+        c = rwkv_sym_dequant(qblk, qs, d, workspace, RWKV_F16, OUT, IN, bits, stream);
+        if (c != RWKV_OK) return c;
+        launch_dense(DenseArgs{reinterpret_cast<const _Float16*>(x), lda, x_group_stride,
+                               reinterpret_cast<const _Float16*>(workspace), y, ldy, (int)M, (int)OUT, (int)IN,
+                               (int)out_per},
+                     epilogue, s);
+    } else {
+        GemmArgs g{x, lda, x_group_stride, qblk, qs, d, y, ldy, (int)M, (int)OUT, (int)IN, (int)out_per};
+        gemm_split_args(g, workspace);
+        const bool f16 = x_dt == RWKV_F16;
+        if (bits == 8) launch_gemm_ep<SymW<8>>(g, f16, epilogue, s);
+        else launch_gemm_ep<SymW<6>>(g, f16, epilogue, s);
+    }
     RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "sym_gemm: launch failed");
     rwkv::counters().sym_gemm.fetch_add(1);
+    rwkv::clear_error();
+    return RWKV_OK;
+}
+
+int rwkv_f16_gemm_applies(int64_t M, int64_t OUT, int64_t IN, int64_t out_per) {
+    return dense_shape_ok(M, OUT, IN, out_per, IN);
+}
+
+rwkv_status rwkv_f16_gemm(const void* x, int64_t M, int64_t lda, int64_t x_group_stride, const void* w, void* y,
+                          int64_t ldy, int64_t OUT, int64_t IN, int64_t out_per, int epilogue, void* stream) {
+    RWKV_REQUIRE(x && w && y, RWKV_E_NULL, "f16_gemm: null buffer");
+    RWKV_REQUIRE(dense_shape_ok(M, OUT, IN, out_per, lda), RWKV_E_UNSUPPORTED,
+                 "f16_gemm: M %lld, OUT (%lld) and out_per (%lld) multiples of 256, IN (%lld) of 128, lda (%lld) >= "
+                 "IN and a multiple of 8",
+                 (long long)M, (long long)OUT, (long long)out_per, (long long)IN, (long long)lda);
+    rwkv_status c = gemm_check("f16_gemm", x, RWKV_F16, M, lda, x_group_stride, ldy, OUT, IN, out_per, epilogue);
+    if (c != RWKV_OK) return c;
+    RWKV_REQUIRE(reinterpret_cast<uintptr_t>(w) % 16 == 0, RWKV_E_SHAPE, "f16_gemm: weights must be 16-byte aligned");
+    launch_dense(DenseArgs{reinterpret_cast<const _Float16*>(x), lda, x_group_stride,
+                           reinterpret_cast<const _Float16*>(w), y, ldy, (int)M, (int)OUT, (int)IN, (int)out_per},
+                 epilogue, reinterpret_cast<hipStream_t>(stream));
+    RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "f16_gemm: launch failed");
     rwkv::clear_error();
     return RWKV_OK;
 }

@@ -786,15 +786,31 @@ __global__ __launch_bounds__(64) void wkv7_bwd_rows_kernel(
 
 // ─────────────────────────────── tmix tail ───────────────────────────────
 
-__global__ __launch_bounds__(64) void wkv_tail_kernel(
+// y·g rounded to fp32, then converted to TO: for fp16 the fp32 output's
+// value rounded once more.  The empty asm keeps the fp32 product: without it
+// the compiler folds multiply and conversion into one v_fma_mixlo_f16, which
+// rounds the exact product straight to fp16.
+template <typename TO>
+__device__ __forceinline__ TO tail_out(float y, float g) {
+    float o = y * g;
+    asm("" : "+v"(o));
+    return (TO)o;
+}
+
+// One wave per (row, head), four to a workgroup; the output fp32, or fp16
+// (TO = _Float16: the rounding the fp16 long pass of o_proj applies to its
+// input, so the projection reads the same values from half the bytes).
+template <typename TO>
+__global__ __launch_bounds__(256) void wkv_tail_kernel(
     const float* __restrict__ wkv, const float* __restrict__ r, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ rk, const float* __restrict__ lnw,
-    const float* __restrict__ lnb, const float* __restrict__ g, float* __restrict__ out,
-    int H, int S, float eps) {
-    const int tg = blockIdx.x;          // row * H + head
+    const float* __restrict__ lnb, const float* __restrict__ g, TO* __restrict__ out,
+    int NH, int H, int S, float eps) {
+    const int tg = blockIdx.x * 4 + (threadIdx.x >> 6);   // row * H + head
+    if (tg >= NH) return;   // whole waves; no barrier below
     const int h = tg % H;
     const int64_t base = (int64_t)tg * S, hb = (int64_t)h * S;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     float s1 = 0.0f;
     for (int e = lane; e < S; e += 64) s1 += wkv[base + e];
     const float mean = wave_total(s1) / (float)S;
@@ -810,7 +826,7 @@ __global__ __launch_bounds__(64) void wkv_tail_kernel(
     for (int e = lane; e < S; e += 64) {
         const float nrm = (wkv[base + e] - mean) * inv;
         const float y = fmaf(dp, v[base + e], fmaf(nrm, lnw[hb + e], lnb[hb + e]));
-        out[base + e] = y * g[base + e];
+        out[base + e] = tail_out<TO>(y, g[base + e]);
     }
 }
 
@@ -1041,17 +1057,31 @@ rwkv_status rwkv_wkv7_step_tail(const float* r, const float* w, const float* k, 
 
 int rwkv_wkv_tail_applies(int64_t S) { return S > 0 && S % 32 == 0; }
 
-rwkv_status rwkv_wkv_tail(const float* wkv, const float* r, const float* k, const float* v, const float* rk,
-                          const float* lnw, const float* lnb, const float* g, float* out, int64_t N, int64_t H,
-                          int64_t S, float eps, void* stream) {
+rwkv_status rwkv_wkv_tail_to(const float* wkv, const float* r, const float* k, const float* v, const float* rk,
+                             const float* lnw, const float* lnb, const float* g, void* out, rwkv_dtype out_dt,
+                             int64_t N, int64_t H, int64_t S, float eps, void* stream) {
     RWKV_REQUIRE(wkv && r && k && v && rk && lnw && lnb && g && out, RWKV_E_NULL, "wkv_tail: null buffer");
+    RWKV_REQUIRE(out_dt == RWKV_F32 || out_dt == RWKV_F16, RWKV_E_DTYPE, "wkv_tail: output dtype %d not f32/f16",
+                 (int)out_dt);
     RWKV_REQUIRE(rwkv_wkv_tail_applies(S), RWKV_E_SHAPE, "wkv_tail: S=%lld is not a multiple of 32", (long long)S);
-    RWKV_REQUIRE(N >= 1 && H >= 1 && N * H <= INT32_MAX && S <= 1 << 20, RWKV_E_SHAPE, "wkv_tail: bad N/H/S");
-    rwkv::launch(wkv_tail_kernel, dim3((unsigned)(N * H)), dim3(64), reinterpret_cast<hipStream_t>(stream),
-                       wkv, r, k, v, rk, lnw, lnb, g, out, (int)H, (int)S, eps);
+    RWKV_REQUIRE(N >= 1 && H >= 1 && N * H <= INT32_MAX - 3 && S <= 1 << 20, RWKV_E_SHAPE, "wkv_tail: bad N/H/S");
+    const dim3 grid((unsigned)((N * H + 3) / 4)), block(256);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (out_dt == RWKV_F16)
+        rwkv::launch(wkv_tail_kernel<_Float16>, grid, block, st, wkv, r, k, v, rk, lnw, lnb, g,
+                     reinterpret_cast<_Float16*>(out), (int)(N * H), (int)H, (int)S, eps);
+    else
+        rwkv::launch(wkv_tail_kernel<float>, grid, block, st, wkv, r, k, v, rk, lnw, lnb, g,
+                     reinterpret_cast<float*>(out), (int)(N * H), (int)H, (int)S, eps);
     rwkv_status s = launch_status("wkv_tail launch");
     if (s == RWKV_OK) rwkv::counters().tail++;
     return s;
+}
+
+rwkv_status rwkv_wkv_tail(const float* wkv, const float* r, const float* k, const float* v, const float* rk,
+                          const float* lnw, const float* lnb, const float* g, float* out, int64_t N, int64_t H,
+                          int64_t S, float eps, void* stream) {
+    return rwkv_wkv_tail_to(wkv, r, k, v, rk, lnw, lnb, g, out, RWKV_F32, N, H, S, eps, stream);
 }
 
 }  // extern "C"

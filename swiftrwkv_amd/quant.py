@@ -623,6 +623,46 @@ def rwkvq_sym_gemm(x, qblk, qs, d, out_features: int, in_features: int, bits: in
     return _quant_gemm("rwkv_sym_gemm", "sym", x, bufs, out_features, in_features, bits, per, epilogue, out, split)
 
 
+def rwkvq_f16_gemm_applies(rows: int, out_features: int, in_features: int, out_per: Optional[int] = None) -> bool:
+    """Whether rwkv_f16_gemm takes this dense fp16 weight (group): OUT and
+    out_per multiples of 256, IN of 128."""
+    per = out_features if out_per is None else out_per
+    return bool(_lib.lib().rwkv_f16_gemm_applies(rows, out_features, in_features, per))
+
+
+def rwkvq_f16_gemm(x, w, out_per: Optional[int] = None, epilogue: str = "store",
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The fp16 matmul of the long pass on a dense fp16 weight w [OUT, IN]
+    (X070Backbone.swift:337-356 after the dequant): y [M, OUT] =
+    fp16(x·wᵀ) with fp32 sums, x [M, IN] or [G, M, IN] fp16 (G = OUT /
+    out_per, matrix g reading x[g]); epilogues as rwkvq_sb6_gemm.  Bitwise
+    the quantised GEMMs' result when w is the fp16 weight they decode."""
+    OUT, IN = w.shape
+    per = OUT if out_per is None else out_per
+    G = OUT // per
+    if x.dim() == 2:
+        x = x.unsqueeze(0)
+    if x.dim() != 3 or x.shape[0] != G or x.shape[2] != IN or x.dtype != torch.float16:
+        raise ValueError(f"f16 GEMM: input {tuple(x.shape)} {x.dtype}, expected fp16 [{G}, M, {IN}]")
+    if w.dtype != torch.float16:
+        raise ValueError(f"f16 GEMM: weight {w.dtype}, expected fp16")
+    M = x.shape[1]
+    if not rwkvq_f16_gemm_applies(M, OUT, IN, per):
+        raise ValueError(f"f16 GEMM: M {M}, [{OUT}, {IN}] out_per={per} not taken")
+    x, w = _aligned(x), _aligned(w)
+    ep = _GEMM_EP[epilogue]
+    ydt = torch.float16 if ep == 2 else torch.float32
+    if out is None:
+        if ep == 1:
+            raise ValueError("f16 GEMM: the add epilogue needs `out`")
+        out = torch.empty((M, OUT), dtype=ydt, device=x.device)
+    elif out.dtype != ydt or tuple(out.shape) != (M, OUT) or not out.is_contiguous() or out.device != x.device:
+        raise ValueError(f"f16 GEMM: out must be a contiguous {ydt} [{M}, {OUT}] tensor on {x.device}")
+    _lib.call("rwkv_f16_gemm", x.data_ptr(), M, IN, M * IN, w.data_ptr(), out.data_ptr(), OUT, OUT, IN, per, ep,
+              _stream(x))
+    return out
+
+
 def rwkvq_sb6_gemv_batch_applies(rows: int, out_features: int, in_features: int, xbits: int,
                                  out_per: Optional[int] = None) -> bool:
     """Whether the matrix-core batched GEMV takes `rows` input rows of this
@@ -1002,8 +1042,10 @@ class RwkvqSidecar:
             if y is not None:
                 return y.to(x.dtype).reshape(*lead, OUT)
         if base_dtype == torch.float16:
-            # the fp16 long pass on the matrix cores, straight from the packed bytes
-            xin = x2d if x2d.dtype in (torch.float16, torch.float32) else x2d.float()
+            # the fp16 long pass on the matrix cores, from the packed bytes (the
+            # input rounded to fp16 here as the kernels would round it, so that
+            # shapes with many tiles can take the dense route)
+            xin = x2d.to(torch.float16)
             if info.kind == RwkvqKind.sb6 and rwkvq_sb6_gemm_applies(OUT, IN, info.xbits):
                 y = rwkvq_sb6_gemm(xin, self._buf(key, "qblk"), self._buf(key, "qsqm"), self._buf(key, "ddm"), OUT,
                                    IN, info.xbits)
@@ -1013,6 +1055,8 @@ class RwkvqSidecar:
                                    info.bits)
                 return y.to(x.dtype).reshape(*lead, OUT)
         W = self.dequantize(key, base_dtype)   # the transient dense weight, [OUT, IN]
+        if base_dtype == torch.float16 and rwkvq_f16_gemm_applies(rows, OUT, IN):
+            return rwkvq_f16_gemm(x2d.to(torch.float16), W).to(x.dtype).reshape(*lead, OUT)
         y = torch.nn.functional.linear(x2d.to(base_dtype), W)
         return y.to(x.dtype).reshape(*lead, OUT)
 

@@ -721,6 +721,8 @@ class X070Decoder:
             for n in ("r", "w", "k", "v", "a", "b", "kb"):
                 bf[n] = z(M, D)
             bf["rkv_in"] = z(3, M, D, dt=torch.float16) if long else z(M, 3, D)
+            if long:   # the tail's output in the fp16 the o_proj long pass reads
+                bf["tout"] = z(M, D, dt=torch.float16)
             bf["xk"] = z(M, D, dt=torch.float16) if long else z(M, D)
             bf["hk"] = z(M, F, dt=torch.float16) if long else z(M, F)
             bf["la_seq"] = z(M, sum(self.ranks))
@@ -790,8 +792,10 @@ class X070Decoder:
         else:
             _lib.check(L.rwkv_wkv7_seq_fwd(p(bf["r"]), p(bf["w"]), p(bf["k"]), p(bf["v"]), p(bf["a"]), p(bf["b"]),
                                            _lib.F32, p(st), p(bf["wkv"]), p(st), B, T, H, s))
-        _lib.check(L.rwkv_wkv_tail(p(bf["wkv"]), p(bf["r"]), p(bf["kb"]), p(bf["v"]), p(lay["r_k"]), p(lay["lnx"][0]),
-                                   p(lay["lnx"][1]), p(bf["gate"]), p(bf["tout"]), M, H, HEAD, LNX_EPS, s))
+        tdt = _lib.F16 if bf["tout"].dtype == torch.float16 else _lib.F32
+        _lib.check(L.rwkv_wkv_tail_to(p(bf["wkv"]), p(bf["r"]), p(bf["kb"]), p(bf["v"]), p(lay["r_k"]),
+                                      p(lay["lnx"][0]), p(lay["lnx"][1]), p(bf["gate"]), p(bf["tout"]), tdt, M, H,
+                                      HEAD, LNX_EPS, s))
         self._prefill_proj(self.proj[f"blocks.{l}.att.output.weight"], bf["tout"], x, 1, M, long, s)
         # ── channel mix ──
         _lib.check(L.rwkv_layer_norm(p(x), _lib.F32, None, 0, p(lay["ln2"][0]), p(lay["ln2"][1]), p(xl), M, D,
@@ -833,16 +837,23 @@ class X070Decoder:
                                                            y.data_ptr() + y.element_size() * col, ldy, ep, s)):
                 rest.append((g, col, qq))
             col += qq.OUT
-        # other layouts: the reference's long pass — dequantise to fp16, library GEMM in fp16
+        # other layouts: the reference's long pass — the weight in fp16, then
+        # the fp16 matmul (rwkv_f16_gemm where it takes the shape)
         from .quant import rwkvq_dequant_dense, rwkvq_dequant_sym
+        L = _lib.lib()
         for g, col, qq in rest:
             if qq.kind == "sb6":
                 W = rwkvq_dequant_dense(*qq.bufs, qq.OUT, qq.IN, 8, qq.xbits, torch.float16)
             elif qq.kind == "sym":
                 W = rwkvq_dequant_sym(*qq.bufs, qq.OUT, qq.IN, qq.bits, torch.float16)
             else:
-                W = qq.bufs[0].to(torch.float16)
-            prod = torch.mm(xs[g].to(torch.float16), W.t()).float()
+                W = qq.bufs[0].to(torch.float16).contiguous()
+            x16 = xs[g].to(torch.float16).contiguous()
+            if L.rwkv_f16_gemm_applies(M, qq.OUT, qq.IN, qq.OUT):
+                _lib.check(L.rwkv_f16_gemm(x16.data_ptr(), M, qq.IN, M * qq.IN, W.data_ptr(),
+                                           y.data_ptr() + y.element_size() * col, ldy, qq.OUT, qq.IN, qq.OUT, ep, s))
+                continue
+            prod = torch.mm(x16, W.t()).float()
             dst = y[:, col:col + qq.OUT] if y.dim() == 2 else y
             if ep == 0:
                 dst.copy_(prod)

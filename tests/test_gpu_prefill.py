@@ -173,6 +173,67 @@ def test_quant_gemm_split_workspace_contract(orc):
     check_f16_rounding(y.cpu().numpy(), exact, mag)
 
 
+@pytest.mark.parametrize("fmt", ["sb6:0", "sb6:2", "sym:8", "sym:6"])
+def test_quant_gemm_dense_route_bitwise(orc, fmt):
+    """Shapes with at least 128 output tiles of 256 × 256 and fp16 inputs:
+    given a workspace, the quantised entry points dequantise the weight into
+    it and run the dense fp16 kernel — bitwise the one-range fused launch
+    (the same products in the same order) for a fused group of three
+    matrices with a partial last row block, for every epilogue; and within
+    the fp16-base oracle's bound on a sample of rows."""
+    case(f"quant gemm dense route {fmt}")
+    from swiftrwkv_amd import _lib
+    M, D, IN = 2000, 1536, 512   # 8 row blocks × 18 feature blocks
+    rng = np.random.default_rng(23)
+    bufs, base_pass, _ = quant_matrix(orc, fmt, 3 * D, IN, rng)
+    w = [dev(z) for z in bufs]
+    kind, b = fmt.split(":")
+    entry = Q.rwkvq_sb6_gemm if kind == "sb6" else Q.rwkvq_sym_gemm
+    dq = "sb6_dequant" if kind == "sb6" else "sym_dequant"
+    assert Q.rwkvq_gemm_workspace(M, 3 * D, IN) == 3 * D * IN * 2
+    x = dev(rng.standard_normal((3, M, IN)).astype(np.float32)).to(torch.float16)
+    n0 = _lib.counters()[dq]
+    dense = entry(x, *w, 3 * D, IN, int(b), out_per=D, split=True)
+    assert _lib.counters()[dq] == n0 + 1   # the dense route ran
+    one = entry(x, *w, 3 * D, IN, int(b), out_per=D, split=False)
+    assert _lib.counters()[dq] == n0 + 1
+    assert torch.equal(dense, one)
+    base = dev(rng.standard_normal((M, 3 * D)).astype(np.float32))
+    y1 = base.clone()
+    entry(x, *w, 3 * D, IN, int(b), out_per=D, epilogue="add", out=y1, split=True)
+    assert torch.equal(y1, base + one)
+    h = entry(x, *w, 3 * D, IN, int(b), out_per=D, epilogue="relu2_f16", split=True)
+    assert torch.equal(h, (torch.relu(one) * torch.relu(one)).to(torch.float16))
+    rows = np.r_[0:24, M - 24:M]
+    for g in range(3):
+        exact, mag = base_pass(x[g].float().cpu().numpy()[rows])
+        cols = slice(g * D, (g + 1) * D)
+        assert check_f16_rounding(dense[rows][:, cols].cpu().numpy(), exact[:, cols], mag[:, cols]) < 5e-2
+
+
+@pytest.mark.parametrize("M", [1, 257, 1000])
+def test_f16_gemm_matches_exact_products(M):
+    """rwkv_f16_gemm on a dense fp16 weight: every output within ½ fp16 ulp +
+    2^-16·Σ|x·w| of the exact product of the fp16 operands; a fused pair of
+    matrices equals its members; shapes off the 256-feature tiles refused."""
+    case(f"f16 gemm M={M}")
+    rng = np.random.default_rng(M)
+    OUT, IN = 768, 384
+    x = (rng.standard_normal((M, IN)) * 0.5).astype(np.float16)
+    wt = (rng.standard_normal((OUT, IN)) * 0.1).astype(np.float16)
+    y = Q.rwkvq_f16_gemm(dev(x), dev(wt))
+    xd, wd = x.astype(np.float64), wt.astype(np.float64)
+    check_f16_rounding(y.cpu().numpy(), xd @ wd.T, np.abs(xd) @ np.abs(wd).T)
+    w2 = np.concatenate([wt, wt[::-1].copy()])
+    x2 = np.stack([x, x[::-1].copy()])
+    pair = Q.rwkvq_f16_gemm(dev(x2), dev(w2), out_per=OUT)
+    assert torch.equal(pair[:, :OUT], y)
+    assert torch.equal(pair[:, OUT:], Q.rwkvq_f16_gemm(dev(x2[1]), dev(wt[::-1].copy())))
+    assert not Q.rwkvq_f16_gemm_applies(M, 640, IN) and not Q.rwkvq_f16_gemm_applies(M, OUT, 320)
+    with pytest.raises(ValueError):
+        Q.rwkvq_f16_gemm(dev(x[:, :320].copy()), dev(wt[:, :320].copy()))
+
+
 @pytest.mark.parametrize("D,M,ranks,wdt", [(256, 37, (32, 32, 32, 64), torch.float16),
                                              (1024, 200, (64, 64, 32, 128), torch.float32),
                                              (4096, 70, (128, 128, 96, 480), torch.float16)])

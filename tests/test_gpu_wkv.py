@@ -195,7 +195,7 @@ def test_step_input_types_and_in_place():
 
 def test_tail_matches_oracle(orc):
     rng = np.random.default_rng(7)
-    for H, N in ((12, 1), (32, 1), (12, 37)):
+    for H, N in ((12, 1), (32, 1), (12, 37), (3, 5)):
         case(f"tail H={H} N={N}")
         S, D = 64, H * 64
         wkv = (rng.standard_normal((N, H, S)) * 3).astype(np.float32)
@@ -208,6 +208,12 @@ def test_tail_matches_oracle(orc):
         want = orc.wkv_tail_f64(wkv, r, k, v, rk, lnw, lnb, g, N, H, S)
         assert got.shape == (N, D)
         assert rel(want, host(got)) < TOL
+        # the fp16 output (a parallel pass's o_proj input): the fp32 output rounded
+        o16 = torch.full((N, D), 7.0, dtype=torch.float16, device=DEV)
+        bufs = [dev(z) for z in (wkv, r, k, v, rk, lnw, lnb, g)]
+        _lib.call("rwkv_wkv_tail_to", *[b.data_ptr() for b in bufs], o16.data_ptr(), _lib.F16, N, H, S, 64e-5,
+                  torch.cuda.current_stream().cuda_stream)
+        assert same(o16, got.to(torch.float16))
     with pytest.raises(ValueError):
         K.wkv_tail(dev(wkv), dev(r), dev(k), dev(v), dev(rk), dev(lnw), dev(lnb), dev(g), H, 48, rows=N)
 
