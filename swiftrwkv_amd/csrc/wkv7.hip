@@ -811,6 +811,22 @@ __global__ __launch_bounds__(256) void wkv_tail_kernel(
     const int h = tg % H;
     const int64_t base = (int64_t)tg * S, hb = (int64_t)h * S;
     const int lane = threadIdx.x & 63;
+    if (S == 64) {
+        // one element per lane, every load issued up front; the operations
+        // of the loops below for their single pass, so the same bits
+        const int64_t i = base + lane, j = hb + lane;
+        const float wv = wkv[i], rv = r[i], kv = k[i], vv = v[i], gv = g[i];
+        const float rkv = rk[j], lw = lnw[j], lb = lnb[j];
+        float t1 = 0.0f;
+        t1 += wv;
+        const float mean = wave_total(t1) / 64.0f;
+        const float d = wv - mean;
+        const float inv = 1.0f / sqrtf(wave_total(fmaf(d, d, 0.0f)) / 64.0f + eps);
+        const float dp = wave_total(fmaf(rv * kv, rkv, 0.0f));
+        const float y = fmaf(dp, vv, fmaf((wv - mean) * inv, lw, lb));
+        out[i] = tail_out<TO>(y, gv);
+        return;
+    }
     float s1 = 0.0f;
     for (int e = lane; e < S; e += 64) s1 += wkv[base + e];
     const float mean = wave_total(s1) / (float)S;

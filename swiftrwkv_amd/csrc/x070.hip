@@ -66,6 +66,45 @@ __global__ __launch_bounds__(1024) void layer_norm_kernel(const T* __restrict__ 
     *reinterpret_cast<float4*>(y + (int64_t)n * D + c) = bad ? make_float4(nan, nan, nan, nan) : ln_apply(xo, md, wv, bv);
 }
 
+// The same rows for many rows (a parallel pass): one wave per row, four rows
+// per workgroup.  The wave holds its whole row (JH >= D/256 chunks) and forms
+// the statistics with row_stats, so every row is bitwise layer_norm_kernel's,
+// while the row is read from memory once (layer_norm_kernel's D/256 waves per
+// row each read the whole row for the statistics).  Grid N/4.
+template <typename T, int JH>
+__global__ __launch_bounds__(256) void layer_norm_rows_kernel(const T* __restrict__ x, const int32_t* ids,
+                                                              int64_t rows, const float* __restrict__ w,
+                                                              const float* __restrict__ b, float* __restrict__ y,
+                                                              int N, int D, float eps) {
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (n >= N) return;   // whole waves; no barrier below
+    int64_t src = n;
+    bool bad = false;
+    if (ids) {
+        const int32_t id = ids[n];
+        bad = id < 0 || (int64_t)id >= rows;
+        src = bad ? 0 : id;
+    }
+    const T* row = x + src * D;
+    float4 v[JH];
+    row_chunks<JH>(row, D, lane, v);
+    const float2 md = row_stats<JH>(v, row, D, lane, eps);
+    const float nan = __builtin_nanf("");
+    float* yr = y + (int64_t)n * D;
+    const int nj = D >> 8;
+#pragma unroll
+    for (int j = 0; j < JH; ++j) {
+        if (j >= nj) break;
+        const int c = 4 * (lane + 64 * j);
+        *reinterpret_cast<float4*>(yr + c) =
+            bad ? make_float4(nan, nan, nan, nan) : ln_apply(v[j], md, load4(w + c), load4(b + c));
+    }
+}
+
+// Rows from which rwkv_layer_norm takes layer_norm_rows_kernel (256
+// workgroups of four rows).
+constexpr int64_t kLnRowsMin = 1024;
+
 // Token shift with its lerps (tmixStep :214-239, cmixStep :303-308) on the
 // layer-normed row: xl = LN(x[n]); xx = prev[n] − xl; prev[n] ← xl;
 // coefficient c gives xl + xx·coef[c].  NC = 6 (coefficients r, k, v, w, a, g):
@@ -356,14 +395,33 @@ rwkv_status rwkv_layer_norm(const void* x, rwkv_dtype x_dt, const int32_t* ids, 
                             const float* b, float* y, int64_t N, int64_t D, float eps, void* stream) {
     RWKV_REQUIRE(N == 0 || (x && w && b && y), RWKV_E_NULL, "layer_norm: null buffer");
     RWKV_REQUIRE(x_dt == RWKV_F32 || x_dt == RWKV_F16, RWKV_E_DTYPE, "layer_norm: input dtype %d not f32/f16", (int)x_dt);
-    RWKV_REQUIRE(N >= 0 && N <= 65535 && row_width_ok(D), RWKV_E_SHAPE,
-                 "layer_norm: N=%lld D=%lld (D %% 256 == 0, D <= 4096 or a multiple of 1024 <= %d)", (long long)N,
-                 (long long)D, kRowMax);
+    RWKV_REQUIRE(N >= 0 && (N <= 65535 || (N >= kLnRowsMin && N <= INT32_MAX - 3)) && row_width_ok(D),
+                 RWKV_E_SHAPE, "layer_norm: N=%lld D=%lld (D %% 256 == 0, D <= 4096 or a multiple of 1024 <= %d)",
+                 (long long)N, (long long)D, kRowMax);
     RWKV_REQUIRE(!ids || rows >= 1, RWKV_E_SHAPE, "layer_norm: gather from a table of %lld rows", (long long)rows);
     if (N == 0) return RWKV_OK;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (N >= kLnRowsMin) {
+        const dim3 grid((unsigned)((N + 3) / 4)), block(256);
+#define RWKV_LNR(TY, JV)                                                                                        \
+    rwkv::launch(layer_norm_rows_kernel<TY, JV>, grid, block, st, reinterpret_cast<const TY*>(x), ids, rows, w, b, \
+                 y, (int)N, (int)D, eps)
+#define RWKV_LNR_P(TY)                \
+    if (D <= 1024) RWKV_LNR(TY, 4);   \
+    else if (D <= 2048) RWKV_LNR(TY, 8); \
+    else if (D <= 4096) RWKV_LNR(TY, 16); \
+    else RWKV_LNR(TY, 32);
+        if (x_dt == RWKV_F16) {
+            RWKV_LNR_P(__half)
+        } else {
+            RWKV_LNR_P(float)
+        }
+#undef RWKV_LNR_P
+#undef RWKV_LNR
+        return status_of("layer_norm launch");
+    }
     int S, T, PS;
     row_geometry(D, S, T, PS);
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const dim3 grid((unsigned)S, (unsigned)N), block(T);
     // row chunks held per lane for the statistics: D/256 up to 8
 #define RWKV_LN(TY, JV) \

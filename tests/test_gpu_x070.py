@@ -84,6 +84,41 @@ def test_layer_norm_gather_f16_table_and_bad_ids():
     _lib.call("rwkv_layer_norm", None, _lib.F32, None, 0, None, None, None, 0, D, LN_EPS, None)   # N = 0: no-op
 
 
+@pytest.mark.parametrize("D", [768, 4096, 8192])
+def test_layer_norm_many_rows_bitwise(D):
+    """From 1024 rows rwkv_layer_norm takes one wave per row: every row equals
+    the row of a short launch bitwise (rows are independent), within 1e-5 of
+    the oracle; a gather with ids outside the table gives NaN rows."""
+    case(f"layer_norm many rows D={D}")
+    rng = np.random.default_rng(D + 1)
+    N = 1030
+
+    def ln(xd, dt, ids, rows, n):
+        y = torch.empty((n, D), device=DEV)
+        _lib.call("rwkv_layer_norm", xd.data_ptr(), dt, None if ids is None else ids.data_ptr(), rows, wd.data_ptr(),
+                  bd.data_ptr(), y.data_ptr(), n, D, LN_EPS, None)
+        return y
+
+    x = (rng.standard_normal((N, D)) * 2 + 0.5).astype(np.float32)
+    w, b = rng.standard_normal(D).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    xd, wd, bd = dev(x), dev(w), dev(b)
+    y = ln(xd, _lib.F32, None, 0, N)
+    for lo in (0, N - 300):
+        assert torch.equal(y[lo:lo + 300], ln(xd[lo:lo + 300].contiguous(), _lib.F32, None, 0, 300))
+    rows = [0, 1, 517, N - 1]
+    assert rel(X.layer_norm(x[rows], w, b), y[rows].cpu().numpy()) < 1e-5
+    V = 40
+    tab = (rng.standard_normal((V, D)) * 0.5).astype(np.float16)
+    ids = rng.integers(0, V, N).astype(np.int32)
+    ids[[3, 700]] = [-1, V]
+    td, idd = dev(tab), dev(ids)
+    g = ln(td, _lib.F16, idd, V, N).cpu().numpy()
+    assert np.isnan(g[[3, 700]]).all()
+    good = np.setdiff1d(np.arange(N), [3, 700])
+    short = ln(td, _lib.F16, dev(ids[good[:200]].copy()), V, 200).cpu().numpy()
+    assert np.array_equal(short, g[good[:200]])
+
+
 @pytest.mark.parametrize("nc", [6, 1])
 def test_shift_mix(nc):
     case(f"shift_mix nc={nc}")
