@@ -493,11 +493,19 @@ rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float
  * the lerped rows in rwkv_x070_seq_shift_mix's coefficient order (r, k, v, w,
  * a, g); wcat [rw + ra + rv + rg, D]: A_w, A_a, A_v, A_g stacked; w2 / a2 / v2 /
  * g2 [D, rank]; la [M, rw + ra + rv + rg] fp32 holds the inner products.
- * Ranks multiples of 16, D of 16. */
+ * Ranks multiples of 16, D of 16.  Long passes (M·D above 2^21) with f16
+ * matrices, ranks and D multiples of 32 (rwkv_x070_seq_lora_split) carry
+ * each fp32 activation as two fp16 parts, hi = fp16(x) and lo = fp16(x − hi),
+ * on the fp16 matrix cores: every product is exact in fp32 and the sums are
+ * fp32, the activation enters with 22 of its 24 significant bits (error at
+ * most 2^-22·|x|, 2^-25 absolute below fp16's normal range); activations
+ * must stay below 65504 in magnitude. */
 rwkv_status rwkv_x070_seq_lora(const float* mix, int64_t M, int64_t D, const void* wcat, const void* w2,
                                const void* a2, const void* v2, const void* g2, rwkv_dtype w_dt, int64_t rw,
                                int64_t ra, int64_t rv, int64_t rg, int with_v, float* la, float* ww, float* aa,
                                float* vv, float* gate, void* stream);
+/* Whether rwkv_x070_seq_lora takes the two-part fp16 kernel for this pass. */
+int rwkv_x070_seq_lora_split(int64_t M, int64_t D, rwkv_dtype w_dt, int64_t rw, int64_t ra, int64_t rv, int64_t rg);
 rwkv_status rwkv_x070_seq_tmix_pre(const float* y_rkv, const float* ww, const float* aa, const float* vv,
                                    const float* w_bias, const float* a_bias, const float* v_bias, const float* k_k,
                                    const float* k_a, float* v_first, int layer0, const int32_t* lengths, float* r,

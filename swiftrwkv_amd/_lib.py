@@ -103,6 +103,7 @@ _SIGS = {
     "rwkv_f16_gemm": (I, [P, L, L, L, P, P, L, L, L, L, I, P]),
     "rwkv_sym_gemm_applies": (I, [L, L, I, L]),
     "rwkv_x070_seq_lora": (I, [P, L, L, P, P, P, P, P, I, L, L, L, L, I, P, P, P, P, P, P]),
+    "rwkv_x070_seq_lora_split": (I, [L, L, I, L, L, L, L]),
     "rwkv_sym_gemm": (I, [P, I, L, L, L, P, P, P, P, L, L, L, I, L, I, P, L, P]),
     "rwkv_layer_norm": (I, [P, I, P, L, P, P, P, L, L, F, P]),
     "rwkv_x070_seq_shift_mix": (I, [P, P, P, P, P, I, I, P, I, L, L, P, L, L, L, L, L, P]),

@@ -229,9 +229,155 @@ __global__ __launch_bounds__(256) void seq_lora_kernel(LoraJobs jobs, int M) {
         }
 }
 
+// ── long passes: the fp32 activations as two fp16 parts on the fp16 matrix cores ──
+// The same y = act(x·Wᵀ) for fp16 W [N, K] with x [M, K] fp32 written
+// x = hi + lo, hi = fp16(x), lo = fp16(x − hi) (x − hi is exact in fp32):
+// hi·w and lo·w are exact in fp32 (11-bit significands) and both sum into
+// one fp32 accumulator on v_mfma_f32_16x16x32_f16, at 2 fp16 MFMAs where the
+// fp32 path takes 8 fp32 ones for the same products.  x enters with 22 of
+// its 24 significant bits (error ≤ 2^-22·|x|; ≤ 2^-25 absolute where lo is
+// an fp16 subnormal), below the fp32 sum's own rounding over these K; |x|
+// must stay below 65504 (layer-normed rows and the branch activations are
+// far below).  A workgroup of 4 waves computes a 128 × 128 tile of y in
+// stages of 32 columns: hi, lo and W staged in LDS (rows of 80 B: 8
+// consecutive rows read one 16-byte column from distinct banks), wave w the
+// 64 × 64 sub-tile (w >> 1, w & 1) as 4 × 4 accumulator tiles.  Two
+// register sets alternate (the loop body is two stages), so a stage's loads
+// are issued more than a stage before they are written to LDS.
+constexpr int LT = 128;    // tile rows = tile columns
+constexpr int LK = 32;     // columns per stage
+constexpr int LROW = 40;   // halves per LDS row
+
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+
+struct SplitJob {
+    const float* x;
+    const _Float16* w;
+    float* y;
+    int N, K, ldx, ldy, act;   // act: 0 none, 1 tanh, 2 sigmoid
+};
+struct SplitJobs {
+    SplitJob j[4];
+};
+
+__global__ __launch_bounds__(256, 2) void lora_split_kernel(SplitJobs jobs, int M) {
+    __shared__ __attribute__((aligned(16))) _Float16 sm[2][3][LT][LROW];   // [buffer][hi, lo, W][row][column]
+    const SplitJob J = jobs.j[blockIdx.z];
+    const int n0 = (int)blockIdx.x * LT;
+    if (n0 >= J.N) return;   // this job has fewer column tiles (uniform, before any barrier)
+    const int m0 = (int)blockIdx.y * LT;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int gq = lane >> 4, li = lane & 15;
+    const int nst = J.K / LK;
+    // staging: thread t → row t >> 1, columns 16·(t & 1) .. +15 of the stage
+    // (rows past the end read the last one; their results are not stored)
+    const int sr = tid >> 1, sc = 16 * (tid & 1);
+    const float* xrow = J.x + (int64_t)min(m0 + sr, M - 1) * J.ldx + sc;
+    const _Float16* wrow = J.w + (int64_t)min(n0 + sr, J.N - 1) * J.K + sc;
+    struct Set {
+        float4 a[4];
+        uint4 b[2];
+    };
+    auto gload = [&](Set& s, int st) {
+        st = min(st, nst - 1);
+        const float4* p = reinterpret_cast<const float4*>(xrow + st * LK);
+        const uint4* q = reinterpret_cast<const uint4*>(wrow + st * LK);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s.a[e] = p[e];
+        s.b[0] = q[0];
+        s.b[1] = q[1];
+    };
+    auto swrite = [&](int buf, const Set& s) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float v[8] = {s.a[2 * e].x, s.a[2 * e].y, s.a[2 * e].z, s.a[2 * e].w,
+                                s.a[2 * e + 1].x, s.a[2 * e + 1].y, s.a[2 * e + 1].z, s.a[2 * e + 1].w};
+            half8v hi, lo;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                hi[c] = (_Float16)v[c];
+                lo[c] = (_Float16)(v[c] - (float)hi[c]);
+            }
+            *reinterpret_cast<half8v*>(&sm[buf][0][sr][sc + 8 * e]) = hi;
+            *reinterpret_cast<half8v*>(&sm[buf][1][sr][sc + 8 * e]) = lo;
+            *reinterpret_cast<uint4*>(&sm[buf][2][sr][sc + 8 * e]) = s.b[e];
+        }
+    };
+    const int wm = wave >> 1, wn = wave & 1;
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto products = [&](int buf) {
+        half8v bv[4], hv[4], lv[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) bv[b] = *reinterpret_cast<const half8v*>(&sm[buf][2][64 * wn + 16 * b + li][8 * gq]);
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            hv[a] = *reinterpret_cast<const half8v*>(&sm[buf][0][64 * wm + 16 * a + li][8 * gq]);
+            lv[a] = *reinterpret_cast<const half8v*>(&sm[buf][1][64 * wm + 16 * a + li][8 * gq]);
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hv[a], bv[b], acc[a][b], 0, 0, 0);
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lv[a], bv[b], acc[a][b], 0, 0, 0);
+            }
+    };
+    // buffer `buf` holds stage st; `ld` receives stage st + 2; `wr` (stage
+    // st + 1, loaded a stage ago) goes to the other buffer
+    auto stage = [&](int buf, Set& ld, int st, const Set& wr) {
+        gload(ld, st + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        products(buf);
+        swrite(buf ^ 1, wr);
+        __syncthreads();
+    };
+    Set sa, sb;
+    gload(sa, 0);
+    swrite(0, sa);
+    gload(sa, 1);
+    __syncthreads();
+    int st = 0;
+    for (; st + 1 < nst; st += 2) {
+        stage(0, sb, st, sa);
+        stage(1, sa, st + 1, sb);
+    }
+    if (st < nst) stage(0, sb, st, sa);   // an odd stage count: the last stage (its LDS write is unused)
+
+    // accumulator lane i + 16g: rows 4g + r, column i of each 16 × 16 tile
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int col = n0 + 64 * wn + 16 * b + li;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + 64 * wm + 16 * a + 4 * gq + r;
+                float v = acc[a][b][r];
+                if (J.act == 1) v = tanhf(v);
+                else if (J.act == 2) v = 1.0f / (1.0f + expf(-v));
+                if (row < M && col < J.N) J.y[(int64_t)row * J.ldy + col] = v;
+            }
+        }
+}
+
+// The two-part kernel takes long passes (M·D above 2^21) with fp16
+// matrices, ranks and D multiples of 32; the fp32 kernel everything else.
+bool lora_split_takes(int64_t M, int64_t D, rwkv_dtype w_dt, int64_t rw, int64_t ra, int64_t rv, int64_t rg) {
+    return w_dt == RWKV_F16 && M * D > ((int64_t)1 << 21) && D % 32 == 0 && rw % 32 == 0 && ra % 32 == 0 &&
+           rv % 32 == 0 && rg % 32 == 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+int rwkv_x070_seq_lora_split(int64_t M, int64_t D, rwkv_dtype w_dt, int64_t rw, int64_t ra, int64_t rv, int64_t rg) {
+    return lora_split_takes(M, D, w_dt, rw, ra, rv, rg);
+}
 
 rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float* prev_out, const int32_t* lengths,
                                     const float* coef, int nc, int n0, void* y0, rwkv_dtype y0_dt, int64_t y0_row,
@@ -332,8 +478,26 @@ rwkv_status rwkv_x070_seq_lora(const float* mix, int64_t M, int64_t D, const voi
         off += rk[b];
         ++n;
     }
+    if (lora_split_takes(M, D, w_dt, rw, ra, rv, rg)) {
+        SplitJobs t1{}, t2{};
+        for (int j = 0; j < n; ++j) {
+            const LoraJob& a = s1.j[j];
+            const LoraJob& b = s2.j[j];
+            t1.j[j] = SplitJob{a.x, reinterpret_cast<const _Float16*>(a.w), a.y, a.N, a.K, a.ldx, a.ldy, a.act};
+            t2.j[j] = SplitJob{b.x, reinterpret_cast<const _Float16*>(b.w), b.y, b.N, b.K, b.ldx, b.ldy, b.act};
+        }
+        const unsigned mt = (unsigned)((M + LT - 1) / LT);
+        rwkv::launch(lora_split_kernel, dim3((unsigned)((maxn1 + LT - 1) / LT), mt, (unsigned)n), dim3(256), st, t1,
+                     (int)M);
+        rwkv::launch(lora_split_kernel, dim3((unsigned)((D + LT - 1) / LT), mt, (unsigned)n), dim3(256), st, t2,
+                     (int)M);
+        RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "x070_seq_lora: launch failed");
+        rwkv::counters().x070.fetch_add(2);
+        rwkv::clear_error();
+        return RWKV_OK;
+    }
     // 2 × 2 tiles of 16 × 16 per wave (larger wave tiles measured faster only
-    // at the long passes, where the library GEMM is taken instead)
+    // at the long passes, which take the two-part kernel)
     constexpr int MT = 2, NT = 2;
     const dim3 grid1((unsigned)((maxn1 + 32 * NT - 1) / (32 * NT)), (unsigned)((M + 32 * MT - 1) / (32 * MT)), (unsigned)n);
     const dim3 grid2((unsigned)((D + 32 * NT - 1) / (32 * NT)), (unsigned)((M + 32 * MT - 1) / (32 * MT)), (unsigned)n);

@@ -37,11 +37,12 @@ HEAD = 64
 LN_EPS = 1e-5
 LNX_EPS = 64e-5
 _COEF_ORDER = ("r", "k", "v", "w", "a", "g")   # rwkv_x070_shift_mix's coefficient order
-# The parallel pass's low-rank branches take rwkv_x070_seq_lora (two launches,
-# activations fused) up to this many rows × width, the library's fp32 GEMM
-# (plus the activation kernels) above: measured per layer, 0.1B width × 128
-# rows 38 against 138 µs, 1024 × 1024 60 against 66 µs, 4096 × 8192 2.5 against
-# 0.96 ms (hipBLASLt's fp32 GEMM at 116 TFLOP/s there, ours 44).
+# The parallel pass's low-rank branches take rwkv_x070_seq_lora's fp32 kernel
+# (two launches, activations fused) up to this many rows × width: measured per
+# layer, 0.1B width × 128 rows 38 against 138 µs for the library GEMM, 1024 ×
+# 1024 60 against 66 µs.  Above it, passes with fp16 matrices take its
+# two-part fp16 kernel (rwkv_x070_seq_lora_split); fp32 matrices the
+# library's fp32 GEMM (4096 × 8192: 0.96 ms against 2.5 for the fp32 kernel).
 SEQ_LORA_MAX_MD = 1 << 21
 
 
@@ -763,13 +764,16 @@ class X070Decoder:
         state.tmix_prev[l].copy_(prev)
         self._prefill_proj(self.proj[f"blocks.{l}.att.rkv"], rkv_in, bf["y_rkv"], 0, M, long, s)
         rw, ra, rv, rg = self.ranks
-        if all(r % 16 == 0 for r in self.ranks) and D % 16 == 0 and M * D <= SEQ_LORA_MAX_MD:
-            # the four low-rank branches on the matrix cores (two launches)
+        wdt = _dt(lay["wcat"])
+        if all(r % 16 == 0 for r in self.ranks) and D % 16 == 0 and (
+                M * D <= SEQ_LORA_MAX_MD or L.rwkv_x070_seq_lora_split(M, D, wdt, rw, ra, rv, rg)):
+            # the four low-rank branches on the matrix cores (two launches;
+            # long passes with fp16 matrices as two fp16 parts per activation)
             Bm = lay["B"]
             _lib.check(L.rwkv_x070_seq_lora(p(mix), M, D, p(lay["wcat"]), p(Bm[0]), p(Bm[1]), p(Bm[2]), p(Bm[3]),
-                                            _dt(lay["wcat"]), rw, ra, rv, rg, int(l > 0), p(bf["la_seq"]),
+                                            wdt, rw, ra, rv, rg, int(l > 0), p(bf["la_seq"]),
                                             p(bf["ww"]), p(bf["aa"]), p(bf["vv"]), p(bf["gate"]), s))
-        else:   # long passes (or ranks the kernel does not take): the same products on the library GEMM
+        else:   # long passes with fp32 matrices (or ranks the kernels do not take): the library's fp32 GEMM
             Aw, Aa, Av, Ag, Bw, Ba, Bv, Bg = self._lowrank_f32(l)
             # mix rows: r, k, v, w, a, g
             torch.mm(torch.tanh(torch.mm(mix[3], Aw.t())), Bw.t(), out=bf["ww"])

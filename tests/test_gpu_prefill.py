@@ -236,16 +236,24 @@ def test_f16_gemm_matches_exact_products(M):
 
 @pytest.mark.parametrize("D,M,ranks,wdt", [(256, 37, (32, 32, 32, 64), torch.float16),
                                              (1024, 200, (64, 64, 32, 128), torch.float32),
-                                             (4096, 70, (128, 128, 96, 480), torch.float16)])
+                                             (4096, 70, (128, 128, 96, 480), torch.float16),
+                                             (1024, 2100, (64, 64, 32, 160), torch.float16),
+                                             (4096, 600, (128, 128, 96, 480), torch.float16),
+                                             (2048, 1100, (96, 96, 64, 256), torch.float32)])
 @pytest.mark.parametrize("with_v", [1, 0])
 def test_seq_lora_matches_fp64(D, M, ranks, wdt, with_v):
     """The parallel pass's four low-rank branches (rwkv_x070_seq_lora) against
     fp64 products of the same values: ww = tanh(x_w·A_wᵀ)·B_wᵀ, aa, vv (not
-    written when the layer has no v branch), gate = sigmoid(x_g·A_gᵀ)·B_gᵀ."""
+    written when the layer has no v branch), gate = sigmoid(x_g·A_gᵀ)·B_gᵀ.
+    Long passes with fp16 matrices (M·D above 2^21) take the two-part fp16
+    kernel: the same bound (its activations keep 22 of 24 bits); odd stage
+    counts (ranks 96, 160) and partial row / column tiles included."""
     case(f"seq lora D={D} M={M} ranks={ranks} {wdt} with_v={with_v}")
     from swiftrwkv_amd import _lib
     rng = np.random.default_rng(D + M + with_v)
     rw, ra, rv, rg = ranks
+    wcode = _lib.F16 if wdt == torch.float16 else _lib.F32
+    assert bool(_lib.lib().rwkv_x070_seq_lora_split(M, D, wcode, *ranks)) == (wdt == torch.float16 and M * D > 1 << 21)
     RT = sum(ranks)
     mix = rng.standard_normal((6, M, D)).astype(np.float32)
     A = (rng.standard_normal((RT, D)) / np.sqrt(D)).astype(np.float32)
