@@ -738,9 +738,22 @@ def bench_prefill(dev, seconds_cap=60.0):
         if q is None:
             return None
         x = torch.randn((M, IN), device=dev).to(torch.float16)
+        fl = 2 * M * OUT * IN
+        # the long pass as the prefill calls it (with a workspace: the dequant
+        # plus the dense kernel where the shape takes that route)
         ms = timed(lambda: Q.rwkvq_sb6_gemm(x, q[0], q[1], q[2], OUT, IN), 10) * 1e3
-        tf = 2 * M * OUT * IN / (ms * 1e-3) / 1e12
-        return {"shape": f"{M}x{OUT}x{IN}", "ms": ms, "TFLOPs": tf, "mfma_fp16_peak_frac": tf / 2500.0}
+        tf = fl / (ms * 1e-3) / 1e12
+        line = {"shape": f"{M}x{OUT}x{IN}", "ms": ms, "TFLOPs": tf, "mfma_fp16_peak_frac": tf / 2500.0,
+                "route": "dequant + dense" if Q.rwkvq_gemm_workspace(M, OUT, IN) == OUT * IN * 2 else "fused"}
+        # the fused kernel alone (no workspace) and the dense kernel alone
+        ms_f = timed(lambda: Q.rwkvq_sb6_gemm(x, q[0], q[1], q[2], OUT, IN, split=False), 10) * 1e3
+        line["fused_ms"], line["fused_peak_frac"] = ms_f, fl / (ms_f * 1e-3) / 1e12 / 2500.0
+        if Q.rwkvq_f16_gemm_applies(M, OUT, IN):
+            W = Q.rwkvq_dequant_dense(q[0], q[1], q[2], OUT, IN, 8, 0, torch.float16)
+            ms_d = timed(lambda: Q.rwkvq_f16_gemm(x, W), 10) * 1e3
+            line["dense_kernel_ms"], line["dense_peak_frac"] = ms_d, fl / (ms_d * 1e-3) / 1e12 / 2500.0
+            del W
+        return line
 
     nthreads = min(16, os.cpu_count() or 1)
     for shape in (syn.X070_0B1, syn.X070_0B4):
