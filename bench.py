@@ -74,10 +74,11 @@ def parse():
     p.add_argument("--skip-wkv", action="store_true")
     p.add_argument("--skip-more", action="store_true", help="skip batched / 7B-class decode and the prefill pass")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--mode", choices=["bench", "kernels", "e2e", "batch", "step"], default="bench",
+    p.add_argument("--mode", choices=["bench", "kernels", "e2e", "batch", "step", "prefill"], default="bench",
                    help="kernels: run each dominant kernel alone (for rocprofv3 counter passes); "
                         "e2e / batch: x070 decode tokens / batched GEMV + WKV decode steps only (for kernel traces); "
-                        "step: the 1.5B headline step alone (eager tokens, then graph replays; counter passes)")
+                        "step: the 1.5B headline step alone (eager tokens, then graph replays; counter passes); "
+                        "prefill: two passes of the 7B-class T8192 prefill (kernel traces)")
     return p.parse_args()
 
 
@@ -798,6 +799,28 @@ def bench_prefill(dev, seconds_cap=60.0):
     return res
 
 
+def profile_prefill(dev):
+    """Two passes of the 7B-class prefill over one 8192-token prompt (fp16
+    base, 32 layers sharing packed bytes): the first makes the pass's buffers,
+    the second is the one to read in a kernel trace."""
+    import numpy as np
+    import torch
+    from swiftrwkv_amd import synthetic as syn
+    from swiftrwkv_amd.x070 import X070Decoder
+
+    shape = syn.X070_7B
+    model = DecodeModel(shape, 1, dev, nthreads=min(16, os.cpu_count() or 1), share_layers=True)
+    dense = syn.x070_dense_params(shape, seed=11)
+    dec = X070Decoder(shape.n_layer, shape.n_embd, shape.ffn, shape.vocab, dense, model.host, dev)
+    prompt = [list(np.random.default_rng(0).integers(0, shape.vocab, 8192))]
+    for i in range(2):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.prefill_batch(prompt, base_dtype=torch.float16)
+        torch.cuda.synchronize()
+        log(f"prefill 7B T8192 pass {i}: {(time.perf_counter() - t0) * 1e3:.1f} ms")
+
+
 def bench_head_gemv(model, dev, reps=60):
     """Average duration of the head GEMV over rotated weight copies (HBM)."""
     import torch
@@ -1272,6 +1295,9 @@ def main():
         return
     if args.mode == "step":
         profile_step(dev)
+        return
+    if args.mode == "prefill":
+        profile_prefill(dev)
         return
     head = headline_1b5(args, dev)
     extra = {"decode_1.5B_gemv_wkv_chain_batch1": head["chain"], "decode_1.5B_batch16": head["batch16"]}

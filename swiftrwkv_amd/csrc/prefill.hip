@@ -239,14 +239,21 @@ __global__ __launch_bounds__(256) void seq_lora_kernel(LoraJobs jobs, int M) {
 // an fp16 subnormal), below the fp32 sum's own rounding over these K; |x|
 // must stay below 65504 (layer-normed rows and the branch activations are
 // far below).  A workgroup of 4 waves computes a 128 × 128 tile of y in
-// stages of 32 columns: hi, lo and W staged in LDS (rows of 80 B: 8
-// consecutive rows read one 16-byte column from distinct banks), wave w the
-// 64 × 64 sub-tile (w >> 1, w & 1) as 4 × 4 accumulator tiles.  Two
-// register sets alternate (the loop body is two stages), so a stage's loads
-// are issued more than a stage before they are written to LDS.
+// stages of 32 columns: hi, lo and W staged in LDS as 64-byte rows whose
+// 16-byte chunk c sits at c ^ ((row >> 1) & 3) (8 consecutive rows read one
+// chunk column from distinct banks; padded 80-byte rows counted 5.5
+// conflict cycles per LDS instruction), wave w the 64 × 64 sub-tile
+// (w >> 1, w & 1) as 4 × 4 accumulator tiles.  Two register sets alternate
+// (the loop body is two stages), so a stage's loads are issued more than a
+// stage before they are written to LDS.  Tiles run row block by row block,
+// every job's column tiles of a row block together, the XCDs (workgroups
+// x, x + 8, ...) each taking a contiguous run: a row block's activations
+// are fetched into one L2, and every XCD gets its share of each job (the
+// jobs' depths differ: 3 to 15 stages in the second launch at 7B-class
+// width; job by job, the deep one landed on two XCDs and took 405 against
+// 269 µs).
 constexpr int LT = 128;    // tile rows = tile columns
 constexpr int LK = 32;     // columns per stage
-constexpr int LROW = 40;   // halves per LDS row
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 
@@ -258,22 +265,30 @@ struct SplitJob {
 };
 struct SplitJobs {
     SplitJob j[4];
+    int first[5];   // column tiles of jobs before j within a row block; first[4] = all of them
 };
 
+__device__ __forceinline__ int lswz(int row, int c) { return 8 * (c ^ ((row >> 1) & 3)); }
+
 __global__ __launch_bounds__(256, 2) void lora_split_kernel(SplitJobs jobs, int M) {
-    __shared__ __attribute__((aligned(16))) _Float16 sm[2][3][LT][LROW];   // [buffer][hi, lo, W][row][column]
-    const SplitJob J = jobs.j[blockIdx.z];
-    const int n0 = (int)blockIdx.x * LT;
-    if (n0 >= J.N) return;   // this job has fewer column tiles (uniform, before any barrier)
-    const int m0 = (int)blockIdx.y * LT;
+    __shared__ __attribute__((aligned(16))) _Float16 sm[2][3][LT][LK];   // [buffer][hi, lo, W][row][column]
+    const int per = jobs.first[4], total = ((M + LT - 1) / LT) * per;
+    const int xcd = blockIdx.x & 7, loc = blockIdx.x >> 3;
+    const int t = xcd * (total >> 3) + min(xcd, total & 7) + loc;
+    const int rb = t / per, rem = t - rb * per;
+    int jb = 0;
+#pragma unroll
+    for (int q = 1; q < 4; ++q) jb += rem >= jobs.first[q] ? 1 : 0;
+    const SplitJob J = jobs.j[jb];
+    const int n0 = (rem - jobs.first[jb]) * LT, m0 = rb * LT;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int gq = lane >> 4, li = lane & 15;
     const int nst = J.K / LK;
-    // staging: thread t → row t >> 1, columns 16·(t & 1) .. +15 of the stage
+    // staging: thread t → row t >> 1, chunks 2·(t & 1), +1 of the stage
     // (rows past the end read the last one; their results are not stored)
-    const int sr = tid >> 1, sc = 16 * (tid & 1);
-    const float* xrow = J.x + (int64_t)min(m0 + sr, M - 1) * J.ldx + sc;
-    const _Float16* wrow = J.w + (int64_t)min(n0 + sr, J.N - 1) * J.K + sc;
+    const int sr = tid >> 1, sh = tid & 1;
+    const float* xrow = J.x + (int64_t)min(m0 + sr, M - 1) * J.ldx + 16 * sh;
+    const _Float16* wrow = J.w + (int64_t)min(n0 + sr, J.N - 1) * J.K + 16 * sh;
     struct Set {
         float4 a[4];
         uint4 b[2];
@@ -298,12 +313,14 @@ __global__ __launch_bounds__(256, 2) void lora_split_kernel(SplitJobs jobs, int 
                 hi[c] = (_Float16)v[c];
                 lo[c] = (_Float16)(v[c] - (float)hi[c]);
             }
-            *reinterpret_cast<half8v*>(&sm[buf][0][sr][sc + 8 * e]) = hi;
-            *reinterpret_cast<half8v*>(&sm[buf][1][sr][sc + 8 * e]) = lo;
-            *reinterpret_cast<uint4*>(&sm[buf][2][sr][sc + 8 * e]) = s.b[e];
+            const int off = lswz(sr, 2 * sh + e);
+            *reinterpret_cast<half8v*>(&sm[buf][0][sr][off]) = hi;
+            *reinterpret_cast<half8v*>(&sm[buf][1][sr][off]) = lo;
+            *reinterpret_cast<uint4*>(&sm[buf][2][sr][off]) = s.b[e];
         }
     };
     const int wm = wave >> 1, wn = wave & 1;
+    const int rc = lswz(li, gq);   // operand rows li + 16·tile: (row >> 1) & 3 = (li >> 1) & 3
     f32x4 acc[4][4];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -312,18 +329,20 @@ __global__ __launch_bounds__(256, 2) void lora_split_kernel(SplitJobs jobs, int 
     auto products = [&](int buf) {
         half8v bv[4], hv[4], lv[4];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) bv[b] = *reinterpret_cast<const half8v*>(&sm[buf][2][64 * wn + 16 * b + li][8 * gq]);
+        for (int b = 0; b < 4; ++b) bv[b] = *reinterpret_cast<const half8v*>(&sm[buf][2][64 * wn + 16 * b + li][rc]);
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
-            hv[a] = *reinterpret_cast<const half8v*>(&sm[buf][0][64 * wm + 16 * a + li][8 * gq]);
-            lv[a] = *reinterpret_cast<const half8v*>(&sm[buf][1][64 * wm + 16 * a + li][8 * gq]);
+            hv[a] = *reinterpret_cast<const half8v*>(&sm[buf][0][64 * wm + 16 * a + li][rc]);
+            lv[a] = *reinterpret_cast<const half8v*>(&sm[buf][1][64 * wm + 16 * a + li][rc]);
         }
+        // W as the A operand: accumulator tile (a, b) holds y columns 16b + 4g + r
+        // of row 16a + i in lane i + 16g, four consecutive columns per lane
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hv[a], bv[b], acc[a][b], 0, 0, 0);
-                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lv[a], bv[b], acc[a][b], 0, 0, 0);
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bv[b], hv[a], acc[a][b], 0, 0, 0);
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bv[b], lv[a], acc[a][b], 0, 0, 0);
             }
     };
     // buffer `buf` holds stage st; `ld` receives stage st + 2; `wr` (stage
@@ -347,21 +366,25 @@ __global__ __launch_bounds__(256, 2) void lora_split_kernel(SplitJobs jobs, int 
     }
     if (st < nst) stage(0, sb, st, sa);   // an odd stage count: the last stage (its LDS write is unused)
 
-    // accumulator lane i + 16g: rows 4g + r, column i of each 16 × 16 tile
+    // lane i + 16g: row 16a + i, columns 16b + 4g .. +3 (N and ldy are
+    // multiples of 16 and 4: a column group is wholly in or out)
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 4; ++a) {
+        const int row = m0 + 64 * wm + 16 * a + li;
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            const int col = n0 + 64 * wn + 16 * b + li;
+            const int col = n0 + 64 * wn + 16 * b + 4 * gq;
+            float v[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = m0 + 64 * wm + 16 * a + 4 * gq + r;
-                float v = acc[a][b][r];
-                if (J.act == 1) v = tanhf(v);
-                else if (J.act == 2) v = 1.0f / (1.0f + expf(-v));
-                if (row < M && col < J.N) J.y[(int64_t)row * J.ldy + col] = v;
+                v[r] = acc[a][b][r];
+                if (J.act == 1) v[r] = tanhf(v[r]);
+                else if (J.act == 2) v[r] = 1.0f / (1.0f + expf(-v[r]));
             }
+            if (row < M && col < J.N)
+                *reinterpret_cast<float4*>(J.y + (int64_t)row * J.ldy + col) = make_float4(v[0], v[1], v[2], v[3]);
         }
+    }
 }
 
 // The two-part kernel takes long passes (M·D above 2^21) with fp16
@@ -479,18 +502,27 @@ rwkv_status rwkv_x070_seq_lora(const float* mix, int64_t M, int64_t D, const voi
         ++n;
     }
     if (lora_split_takes(M, D, w_dt, rw, ra, rv, rg)) {
+        const uintptr_t ao = (uintptr_t)ww | (uintptr_t)aa | (uintptr_t)gate | (uintptr_t)(with_v ? vv : ww);
+        RWKV_REQUIRE(ao % 16 == 0, RWKV_E_SHAPE, "x070_seq_lora: outputs must be 16-byte aligned");
         SplitJobs t1{}, t2{};
-        for (int j = 0; j < n; ++j) {
+        int c1 = 0, c2 = 0;
+        for (int j = 0; j < 4; ++j) {
+            t1.first[j] = c1;
+            t2.first[j] = c2;
+            if (j >= n) continue;   // fewer jobs: first[j] = all tiles, never selected
             const LoraJob& a = s1.j[j];
             const LoraJob& b = s2.j[j];
             t1.j[j] = SplitJob{a.x, reinterpret_cast<const _Float16*>(a.w), a.y, a.N, a.K, a.ldx, a.ldy, a.act};
             t2.j[j] = SplitJob{b.x, reinterpret_cast<const _Float16*>(b.w), b.y, b.N, b.K, b.ldx, b.ldy, b.act};
+            c1 += (a.N + LT - 1) / LT;
+            c2 += (b.N + LT - 1) / LT;
         }
-        const unsigned mt = (unsigned)((M + LT - 1) / LT);
-        rwkv::launch(lora_split_kernel, dim3((unsigned)((maxn1 + LT - 1) / LT), mt, (unsigned)n), dim3(256), st, t1,
-                     (int)M);
-        rwkv::launch(lora_split_kernel, dim3((unsigned)((D + LT - 1) / LT), mt, (unsigned)n), dim3(256), st, t2,
-                     (int)M);
+        t1.first[4] = c1;
+        t2.first[4] = c2;
+        const int64_t mt = (M + LT - 1) / LT;
+        RWKV_REQUIRE(mt * c2 < INT32_MAX, RWKV_E_SHAPE, "x070_seq_lora: too many tiles");
+        rwkv::launch(lora_split_kernel, dim3((unsigned)(mt * c1)), dim3(256), st, t1, (int)M);
+        rwkv::launch(lora_split_kernel, dim3((unsigned)(mt * c2)), dim3(256), st, t2, (int)M);
         RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "x070_seq_lora: launch failed");
         rwkv::counters().x070.fetch_add(2);
         rwkv::clear_error();
