@@ -92,12 +92,15 @@ __global__ __launch_bounds__(256) void layer_norm_rows_kernel(const T* __restric
     const float nan = __builtin_nanf("");
     float* yr = y + (int64_t)n * D;
     const int nj = D >> 8;
+    // a predicate, not a break: the loop unrolls and v stays in registers
+    // (with a break the compiler indexed v at run time from scratch memory)
 #pragma unroll
     for (int j = 0; j < JH; ++j) {
-        if (j >= nj) break;
-        const int c = 4 * (lane + 64 * j);
-        *reinterpret_cast<float4*>(yr + c) =
-            bad ? make_float4(nan, nan, nan, nan) : ln_apply(v[j], md, load4(w + c), load4(b + c));
+        if (j < nj) {
+            const int c = 4 * (lane + 64 * j);
+            *reinterpret_cast<float4*>(yr + c) =
+                bad ? make_float4(nan, nan, nan, nan) : ln_apply(v[j], md, load4(w + c), load4(b + c));
+        }
     }
 }
 
