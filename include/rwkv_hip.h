@@ -469,12 +469,13 @@ rwkv_status rwkv_x070_ffn_value(const float* hk, const uint8_t* qblk, const uint
  * 300-307): for layer-normed rows xl [B·T, D], prev_t = xl[n − 1] (t > 0) or
  * prev_in[b] (the carried shift state; NULL = zeros); m_c = xl + (prev_t − xl)·coef[c].
  * Coefficients [0, n0) → y0 (f32 or f16; element (n, c) at n·y0_row + c·y0_coef);
- * y1 (f32, may be NULL) receives every coefficient at n·y1_row + c·y1_coef; prev_out [B, D] ← xl of
- * each row's last real token (gatherLast, :320-335).  nc = 6 (r, k, v, w, a, g)
- * or 1.  prev_out must not alias prev_in. */
+ * y1 (f32, may be NULL) receives the coefficients [y1_first, nc) at n·y1_row + c·y1_coef (the
+ * low-rank branches read v, w, a, g: y1_first = 2 leaves r and k to y0 alone); prev_out [B, D] ← xl
+ * of each row's last real token (gatherLast, :320-335).  nc = 6 (r, k, v, w, a, g) or 1.
+ * prev_out must not alias prev_in. */
 rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float* prev_out, const int32_t* lengths,
                                     const float* coef, int nc, int n0, void* y0, rwkv_dtype y0_dt, int64_t y0_row,
-                                    int64_t y0_coef, float* y1, int64_t y1_row, int64_t y1_coef, int64_t B, int64_t T,
+                                    int64_t y0_coef, float* y1, int64_t y1_row, int64_t y1_coef, int y1_first, int64_t B, int64_t T,
                                     int64_t D, void* stream);
 
 /* The time-mix arithmetic between the projections and the recurrence

@@ -106,7 +106,7 @@ _SIGS = {
     "rwkv_x070_seq_lora_split": (I, [L, L, I, L, L, L, L]),
     "rwkv_sym_gemm": (I, [P, I, L, L, L, P, P, P, P, L, L, L, I, L, I, P, L, P]),
     "rwkv_layer_norm": (I, [P, I, P, L, P, P, P, L, L, F, P]),
-    "rwkv_x070_seq_shift_mix": (I, [P, P, P, P, P, I, I, P, I, L, L, P, L, L, L, L, L, P]),
+    "rwkv_x070_seq_shift_mix": (I, [P, P, P, P, P, I, I, P, I, L, L, P, L, L, I, L, L, L, P]),
     "rwkv_x070_seq_tmix_pre": (I, [P] * 10 + [I, P] + [P] * 7 + [L, L, L, P]),
     "rwkv_x070_shift_mix": (I, [P, P, P, P, P, I, P, P, L, L, F, P]),
     "rwkv_x070_lora_in": (I, [P, P, I, L, L, L, L, I, P, L, L, P]),

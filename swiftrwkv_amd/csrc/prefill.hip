@@ -31,15 +31,16 @@ __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast
 // lerps of rwkvTmixForward / rwkvCmixForward): for the layer-normed rows xl,
 // prev_t = xl[t − 1] (t > 0) or the carried shift state prev_in[b] (zeros when
 // NULL); m_c = xl + (prev_t − xl)·coef[c].  Coefficients [0, n0) go to y0
-// (fp16 or fp32, element (n, c) at n·y0_row + c·y0_coef); with y1, every
-// coefficient also goes to y1 (fp32).  prev_out[b] ← xl[b, lengths[b] − 1] (the shift state of the row's
+// (fp16 or fp32, element (n, c) at n·y0_row + c·y0_coef); with y1, the
+// coefficients from y1_first on also go to y1 (fp32).  prev_out[b] ← xl[b, lengths[b] − 1] (the shift state of the row's
 // last real token, gatherLast).  One thread per 4 columns of one row.
 template <int NC, bool F16>
 __global__ __launch_bounds__(256) void seq_shift_kernel(const float* __restrict__ xl, const float* __restrict__ prev_in,
                                                         float* __restrict__ prev_out, const int32_t* __restrict__ lengths,
                                                         const float* __restrict__ coef, int n0, void* __restrict__ y0,
                                                         int64_t y0_row, int64_t y0_coef, float* __restrict__ y1,
-                                                        int64_t y1_row, int64_t y1_coef, int T, int D, int64_t total) {
+                                                        int64_t y1_row, int64_t y1_coef, int y1_first, int T, int D,
+                                                        int64_t total) {
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= total) return;
     const int D4 = D >> 2;
@@ -66,7 +67,7 @@ __global__ __launch_bounds__(256) void seq_shift_kernel(const float* __restrict_
                 *reinterpret_cast<float4*>(reinterpret_cast<float*>(y0) + o) = m;
             }
         }
-        if (y1) *reinterpret_cast<float4*>(y1 + n * y1_row + k * y1_coef + c) = m;
+        if (y1 && k >= y1_first) *reinterpret_cast<float4*>(y1 + n * y1_row + k * y1_coef + c) = m;
     }
 }
 
@@ -404,7 +405,8 @@ int rwkv_x070_seq_lora_split(int64_t M, int64_t D, rwkv_dtype w_dt, int64_t rw, 
 
 rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float* prev_out, const int32_t* lengths,
                                     const float* coef, int nc, int n0, void* y0, rwkv_dtype y0_dt, int64_t y0_row,
-                                    int64_t y0_coef, float* y1, int64_t y1_row, int64_t y1_coef, int64_t B, int64_t T,
+                                    int64_t y0_coef, float* y1, int64_t y1_row, int64_t y1_coef, int y1_first,
+                                    int64_t B, int64_t T,
                                     int64_t D, void* stream) {
     RWKV_REQUIRE(xl && prev_out && coef && y0, RWKV_E_NULL, "x070_seq_shift_mix: null buffer");
     RWKV_REQUIRE(nc == 1 || nc == 6, RWKV_E_SHAPE, "x070_seq_shift_mix: %d coefficients (1 or 6)", nc);
@@ -415,13 +417,14 @@ rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float
     RWKV_REQUIRE(y0_row % 4 == 0 && y0_coef % 4 == 0 && (!y1 || (y1_row % 4 == 0 && y1_coef % 4 == 0)),
                  RWKV_E_SHAPE, "x070_seq_shift_mix: output strides must be multiples of 4");
     RWKV_REQUIRE(prev_out != prev_in, RWKV_E_SHAPE, "x070_seq_shift_mix: prev_out must not alias prev_in");
+    RWKV_REQUIRE(y1_first >= 0 && y1_first <= nc, RWKV_E_SHAPE, "x070_seq_shift_mix: y1_first = %d", y1_first);
     const int64_t total = B * T * (D / 4);
     const dim3 grid((unsigned)((total + 255) / 256)), block(256);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const bool f16 = y0_dt == RWKV_F16;
 #define RWKV_SHIFT(NCV, F)                                                                                          \
     rwkv::launch(seq_shift_kernel<NCV, F>, grid, block, s, xl, prev_in, prev_out, lengths, coef, n0, y0, y0_row,   \
-                 y0_coef, y1, y1_row, y1_coef, (int)T, (int)D, total)
+                 y0_coef, y1, y1_row, y1_coef, y1_first, (int)T, (int)D, total)
     if (nc == 6) {
         if (f16) RWKV_SHIFT(6, true);
         else RWKV_SHIFT(6, false);

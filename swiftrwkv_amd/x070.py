@@ -760,7 +760,7 @@ class X070Decoder:
         else:      # fp32 [M, 3, D] for the fused GEMV
             y0 = (rkv_in, _lib.F32, 3 * D, D)
         _lib.check(L.rwkv_x070_seq_shift_mix(p(xl), p(state.tmix_prev[l]), p(prev), p(len_t), p(lay["coef6"]), 6, 3,
-                                             p(y0[0]), y0[1], y0[2], y0[3], p(mix), D, M * D, B, T, D, s))
+                                             p(y0[0]), y0[1], y0[2], y0[3], p(mix), D, M * D, 2, B, T, D, s))
         state.tmix_prev[l].copy_(prev)
         self._prefill_proj(self.proj[f"blocks.{l}.att.rkv"], rkv_in, bf["y_rkv"], 0, M, long, s)
         rw, ra, rv, rg = self.ranks
@@ -806,7 +806,8 @@ class X070Decoder:
                                      LN_EPS, s))
         xk, hk = bf["xk"], bf["hk"]
         _lib.check(L.rwkv_x070_seq_shift_mix(p(xl), p(state.cmix_prev[l]), p(prev), p(len_t), p(lay["ck"]), 1, 1,
-                                             p(xk), _lib.F16 if long else _lib.F32, D, M * D, None, 0, 0, B, T, D, s))
+                                             p(xk), _lib.F16 if long else _lib.F32, D, M * D, None, 0, 0, 0, B, T, D,
+                                             s))
         state.cmix_prev[l].copy_(prev)
         self._prefill_proj(self.proj[f"blocks.{l}.ffn.key.weight"], xk, hk, 2, M, long, s)
         self._prefill_proj(self.proj[f"blocks.{l}.ffn.value.weight"], hk, x, 1, M, long, s)
