@@ -76,32 +76,67 @@ __device__ __forceinline__ void store4(void* out, int64_t idx, float a, float b,
 }
 
 // ─────────────────────────────── sb6 dequant ───────────────────────────────
-// One thread per (row, block, part): part p covers columns 4p..4p+3 of the
-// block (p < 4: low nibbles of word p; p >= 4: high nibbles of word p-4), so 8
-// consecutive threads write one block's 32 outputs contiguously.
+// Four threads per (row, block): quarter q writes columns 8q..8q+7 as parts
+// p = 2q, 2q + 1, part p covering columns 4p..4p+3 (p < 4: low nibbles of
+// word p; p >= 4: high nibbles of word p-4) — so a wave's stores cover 16
+// blocks contiguously.  Index math in 32 bits (rows × blocks × 4 < 2^31 is
+// checked on the host): one thread per part with a 64-bit division each ran
+// at 0.37 of HBM.
+template <int DT>
+__device__ __forceinline__ void store8(void* out, int64_t idx, const float (&f)[8]) {
+    if constexpr (DT == RWKV_F32) {
+        float4* o = reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + idx);
+        o[0] = make_float4(f[0], f[1], f[2], f[3]);
+        o[1] = make_float4(f[4], f[5], f[6], f[7]);
+    } else {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            if constexpr (DT == RWKV_BF16) {
+                const uint32_t u = __float_as_uint(f[e]);
+                h[e] = ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu))
+                           ? ((u >> 16) | 0x40u)
+                           : ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+            } else {
+                h[e] = __builtin_bit_cast(uint16_t, (_Float16)f[e]);
+            }
+        }
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + idx) =
+            make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+    }
+}
+
 template <int XB, int DT>
 __global__ __launch_bounds__(256) void sb6_dequant_kernel(
     const uint8_t* __restrict__ qblk, const uint8_t* __restrict__ qsqm, const uint16_t* __restrict__ ddm,
     void* __restrict__ out, int64_t OUT, int64_t IN) {
     constexpr int SUW = 4 + XB;  // 32-bit words per block
-    const int64_t NB = IN >> 5, NSB = NB >> 3;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= OUT * NB * 8) return;
-    const int p = (int)(gid & 7);
-    const int64_t rb = gid >> 3;   // row * NB + blk
-    const int64_t row = rb / NB, blk = rb - row * NB;
-    const uint32_t* qb = reinterpret_cast<const uint32_t*>(qblk) + rb * SUW;
-    const uint32_t wd = qb[p & 3];
-    uint32_t q4 = (p < 4) ? (wd & 0x0F0F0F0Fu) : ((wd >> 4) & 0x0F0F0F0Fu);
-    if constexpr (XB >= 1) q4 |= spread4((qb[4] >> (4 * p)) & 0xFu) << 4;
-    if constexpr (XB >= 2) q4 |= spread4((qb[5] >> (4 * p)) & 0xFu) << 5;
+    const uint32_t NB = (uint32_t)(IN >> 5), NSB = NB >> 3;
+    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+    if (gid >= (uint32_t)OUT * NB * 4u) return;
+    const uint32_t q = gid & 3u, rb = gid >> 2;   // quarter, row * NB + blk
+    const uint32_t row = rb / NB, blk = rb - row * NB;
+    const uint32_t* qb = reinterpret_cast<const uint32_t*>(qblk) + (int64_t)rb * SUW;
+    const uint32_t w0 = qb[2 * (q & 1)], w1 = qb[2 * (q & 1) + 1];   // words of parts 2q, 2q + 1
+    const uint32_t h1 = XB >= 1 ? qb[4] : 0u, h2 = XB >= 2 ? qb[5] : 0u;
     const uint16_t sm = reinterpret_cast<const uint16_t*>(qsqm)[rb];
-    const uint32_t dd = reinterpret_cast<const uint32_t*>(ddm)[row * NSB + (blk >> 3)];
+    const uint32_t dd = reinterpret_cast<const uint32_t*>(ddm)[(int64_t)row * NSB + (blk >> 3)];
     const float s = hround((float)(sm & 0xffu) * f16f(dd));
     const float m = hround((float)(int8_t)(sm >> 8) * f16f(dd >> 16));
-    store4<DT>(out, row * IN + blk * 32 + 4 * p,
-               fmaf((float)(q4 & 0xffu), s, m), fmaf((float)((q4 >> 8) & 0xffu), s, m),
-               fmaf((float)((q4 >> 16) & 0xffu), s, m), fmaf((float)(q4 >> 24), s, m));
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int p = 2 * (int)q + e;
+        const uint32_t wd = e ? w1 : w0;
+        uint32_t q4 = (p < 4) ? (wd & 0x0F0F0F0Fu) : ((wd >> 4) & 0x0F0F0F0Fu);
+        if constexpr (XB >= 1) q4 |= spread4((h1 >> (4 * p)) & 0xFu) << 4;
+        if constexpr (XB >= 2) q4 |= spread4((h2 >> (4 * p)) & 0xFu) << 5;
+        f[4 * e] = fmaf((float)(q4 & 0xffu), s, m);
+        f[4 * e + 1] = fmaf((float)((q4 >> 8) & 0xffu), s, m);
+        f[4 * e + 2] = fmaf((float)((q4 >> 16) & 0xffu), s, m);
+        f[4 * e + 3] = fmaf((float)(q4 >> 24), s, m);
+    }
+    store8<DT>(out, (int64_t)row * IN + blk * 32 + 8 * q, f);
 }
 
 // ─────────────────────────────── sym dequant ───────────────────────────────
@@ -1203,8 +1238,8 @@ rwkv_status rwkv_sb6_dequant(const uint8_t* qblk, const uint8_t* qsqm, const uin
     RWKV_REQUIRE(rwkv::dtype_ok(out_dt), RWKV_E_DTYPE, "sb6_dequant: output dtype code %d", out_dt);
     RWKV_REQUIRE(OUT >= 1 && IN >= 256 && IN % 256 == 0, RWKV_E_SHAPE,
                  "sb6_dequant: IN (%lld) must be a positive multiple of 256 (block 32 x super-block 8)", (long long)IN);
-    const int64_t total = OUT * (IN / 32) * 8;
-    RWKV_REQUIRE(total / 256 < INT32_MAX, RWKV_E_SHAPE, "sb6_dequant: tensor too large");
+    const int64_t total = OUT * (IN / 32) * 4;   // four threads per (row, block)
+    RWKV_REQUIRE(total < INT32_MAX, RWKV_E_SHAPE, "sb6_dequant: tensor too large");
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 #define RWKV_DQ(XB, DT) rwkv::launch(sb6_dequant_kernel<XB, DT>, grid, block, st, qblk, qsqm, ddm, out, OUT, IN)
