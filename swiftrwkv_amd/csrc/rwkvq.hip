@@ -142,18 +142,29 @@ __global__ __launch_bounds__(256) void sb6_dequant_kernel(
 // ─────────────────────────────── sym dequant ───────────────────────────────
 // 8-bit: one thread per 4 columns.  6-bit: one thread per (pair, part p),
 // part p = columns 4p..4p+3 of the pair in register order l0,l1,h0,h1,l2,l3,h2,h3.
-template <int BITS, int DT>
 // With `ids` (n rows): output row o is matrix row ids[o] (the embedding row
-// gather); an id outside [0, OUT) gives a row of NaN.
+// gather); an id outside [0, OUT) gives a row of NaN.  I32: the thread index
+// and the row division in 32 bits (fewer than 2^31 threads; a 64-bit
+// division per 4 outputs costs more than their loads).
+template <int BITS, int DT, bool I32>
 __global__ __launch_bounds__(256) void sym_dequant_kernel(
     const uint8_t* __restrict__ qblk, const uint8_t* __restrict__ qs, const uint16_t* __restrict__ d,
     void* __restrict__ out, int64_t OUT, int64_t IN, const int32_t* __restrict__ ids, int64_t n) {
     const int64_t NB = IN >> 4, NSB = (NB + 15) >> 4;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t rows = ids ? n : OUT;
-    if (gid >= rows * (IN >> 2)) return;
-    const int64_t orow = gid / (IN >> 2);
-    const int64_t col = (gid - orow * (IN >> 2)) * 4;
+    int64_t orow, col;
+    if constexpr (I32) {
+        const uint32_t gid = blockIdx.x * 256u + threadIdx.x, q = (uint32_t)(IN >> 2);
+        if (gid >= (uint32_t)(rows * (IN >> 2))) return;
+        const uint32_t o = gid / q;
+        orow = o;
+        col = (int64_t)(gid - o * q) * 4;
+    } else {
+        const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (gid >= rows * (IN >> 2)) return;
+        orow = gid / (IN >> 2);
+        col = (gid - orow * (IN >> 2)) * 4;
+    }
     int64_t row = orow;
     if (ids) {
         row = ids[orow];
@@ -1272,8 +1283,14 @@ rwkv_status rwkv_sym_dequant(const uint8_t* qblk, const uint8_t* qs, const uint1
     RWKV_REQUIRE(total / 256 < INT32_MAX, RWKV_E_SHAPE, "sym_dequant: tensor too large");
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define RWKV_DQ(BITS, DT) \
-    rwkv::launch(sym_dequant_kernel<BITS, DT>, grid, block, st, qblk, qs, d, out, OUT, IN, (const int32_t*)nullptr, (int64_t)0)
+    const bool i32 = total < INT32_MAX;
+#define RWKV_DQ(BITS, DT)                                                                                             \
+    if (i32)                                                                                                          \
+        rwkv::launch(sym_dequant_kernel<BITS, DT, true>, grid, block, st, qblk, qs, d, out, OUT, IN,                  \
+                     (const int32_t*)nullptr, (int64_t)0);                                                            \
+    else                                                                                                              \
+        rwkv::launch(sym_dequant_kernel<BITS, DT, false>, grid, block, st, qblk, qs, d, out, OUT, IN,                 \
+                     (const int32_t*)nullptr, (int64_t)0)
 #define RWKV_DQ_DT(BITS)                                  \
     switch (out_dt) {                                     \
         case RWKV_F32: RWKV_DQ(BITS, RWKV_F32); break;    \
@@ -1306,7 +1323,12 @@ rwkv_status rwkv_sym_rows(const int32_t* ids, int64_t n, const uint8_t* qblk, co
     const int64_t total = n * (IN / 4);
     dim3 grid((unsigned)((total + 255) / 256)), block(256);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define RWKV_DQ(BITS, DT) rwkv::launch(sym_dequant_kernel<BITS, DT>, grid, block, st, qblk, qs, d, out, OUT, IN, ids, n)
+    const bool i32 = total < INT32_MAX;
+#define RWKV_DQ(BITS, DT)                                                                                    \
+    if (i32)                                                                                                 \
+        rwkv::launch(sym_dequant_kernel<BITS, DT, true>, grid, block, st, qblk, qs, d, out, OUT, IN, ids, n); \
+    else                                                                                                     \
+        rwkv::launch(sym_dequant_kernel<BITS, DT, false>, grid, block, st, qblk, qs, d, out, OUT, IN, ids, n)
 #define RWKV_DQ_DT(BITS)                                  \
     switch (out_dt) {                                     \
         case RWKV_F32: RWKV_DQ(BITS, RWKV_F32); break;    \
