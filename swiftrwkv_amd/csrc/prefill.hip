@@ -34,19 +34,34 @@ __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast
 // (fp16 or fp32, element (n, c) at n·y0_row + c·y0_coef); with y1, the
 // coefficients from y1_first on also go to y1 (fp32).  prev_out[b] ← xl[b, lengths[b] − 1] (the shift state of the row's
 // last real token, gatherLast).  One thread per 4 columns of one row.
-template <int NC, bool F16>
+// I32: the thread index and its divisions in 32 bits (fewer than 2^31
+// threads; two 64-bit divisions per 4 columns cost more than the loads).
+template <int NC, bool F16, bool I32>
 __global__ __launch_bounds__(256) void seq_shift_kernel(const float* __restrict__ xl, const float* __restrict__ prev_in,
                                                         float* __restrict__ prev_out, const int32_t* __restrict__ lengths,
                                                         const float* __restrict__ coef, int n0, void* __restrict__ y0,
                                                         int64_t y0_row, int64_t y0_coef, float* __restrict__ y1,
                                                         int64_t y1_row, int64_t y1_coef, int y1_first, int T, int D,
                                                         int64_t total) {
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= total) return;
-    const int D4 = D >> 2;
-    const int64_t n = gid / D4;
-    const int c = (int)(gid - n * D4) * 4;
-    const int b = (int)(n / T), t = (int)(n - (int64_t)b * T);
+    int64_t n;
+    int c, b, t;
+    if constexpr (I32) {
+        const uint32_t gid = blockIdx.x * 256u + threadIdx.x, D4 = (uint32_t)(D >> 2);
+        if (gid >= (uint32_t)total) return;
+        const uint32_t n32 = gid / D4, b32 = n32 / (uint32_t)T;
+        n = n32;
+        c = (int)(gid - n32 * D4) * 4;
+        b = (int)b32;
+        t = (int)(n32 - b32 * (uint32_t)T);
+    } else {
+        const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (gid >= total) return;
+        const int D4 = D >> 2;
+        n = gid / D4;
+        c = (int)(gid - n * D4) * 4;
+        b = (int)(n / T);
+        t = (int)(n - (int64_t)b * T);
+    }
     const float4 x = ld4(xl + n * D + c);
     float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
     if (t > 0) p = ld4(xl + (n - 1) * D + c);
@@ -90,14 +105,16 @@ __global__ __launch_bounds__(256) void seq_tmix_pre_kernel(
     float* __restrict__ v_first, int layer0, const int32_t* __restrict__ lengths, float* __restrict__ r_o,
     float* __restrict__ w_o, float* __restrict__ k_o, float* __restrict__ v_o, float* __restrict__ a_o,
     float* __restrict__ b_o, float* __restrict__ kb_o, int T, int H, int64_t units) {
-    const int64_t unit = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (unit >= units) return;   // uniform per wave
+    // units < 2^30 (checked on the host): 32-bit index math
+    const uint32_t unit = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (unit >= (uint32_t)units) return;   // uniform per wave
     const int lane = threadIdx.x & 63;
     const int D = H * 64;
-    const int64_t n = unit / H;
-    const int h = (int)(unit - n * H);
+    const uint32_t n32 = unit / (uint32_t)H, b32 = n32 / (uint32_t)T;
+    const int64_t n = n32;
+    const int h = (int)(unit - n32 * (uint32_t)H);
     const int ch = h * 64 + lane;
-    const int b = (int)(n / T), t = (int)(n - (int64_t)b * T);
+    const int b = (int)b32, t = (int)(n32 - b32 * (uint32_t)T);
     const bool real = t < (lengths ? lengths[b] : T);
     const int64_t e = n * D + ch;
     const float* yr = y_rkv + n * 3 * D;
@@ -422,9 +439,16 @@ rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float
     const dim3 grid((unsigned)((total + 255) / 256)), block(256);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const bool f16 = y0_dt == RWKV_F16;
-#define RWKV_SHIFT(NCV, F)                                                                                          \
-    rwkv::launch(seq_shift_kernel<NCV, F>, grid, block, s, xl, prev_in, prev_out, lengths, coef, n0, y0, y0_row,   \
-                 y0_coef, y1, y1_row, y1_coef, y1_first, (int)T, (int)D, total)
+    const bool i32 = total < INT32_MAX;
+#define RWKV_SHIFT(NCV, F)                                                                                            \
+    do {                                                                                                              \
+        if (i32)                                                                                                      \
+            rwkv::launch(seq_shift_kernel<NCV, F, true>, grid, block, s, xl, prev_in, prev_out, lengths, coef, n0,    \
+                         y0, y0_row, y0_coef, y1, y1_row, y1_coef, y1_first, (int)T, (int)D, total);                  \
+        else                                                                                                          \
+            rwkv::launch(seq_shift_kernel<NCV, F, false>, grid, block, s, xl, prev_in, prev_out, lengths, coef, n0,   \
+                         y0, y0_row, y0_coef, y1, y1_row, y1_coef, y1_first, (int)T, (int)D, total);                  \
+    } while (0)
     if (nc == 6) {
         if (f16) RWKV_SHIFT(6, true);
         else RWKV_SHIFT(6, false);
