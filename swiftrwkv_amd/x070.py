@@ -619,16 +619,21 @@ class X070Decoder:
             raise ValueError(f"prefill_batch: base dtype {base_dtype} (float16 or float32)")
         B, T = len(prompts), max(len(p) for p in prompts)
         M = B * T
-        if M > 65535:
-            raise ValueError(f"prefill_batch: {M} rows in one pass (at most 65535)")
+        long = base_dtype == torch.float16 and M > short_rows
+        # the long pass's kernels take up to 2^24 rows; the fp32 GEMV's
+        # batched plan (short passes and the fp32 base) 65535
+        most = (1 << 24) if long else 65535
+        if M > most:
+            raise ValueError(f"prefill_batch: {M} rows in one pass (at most {most})")
         dev = self.device
         ids = np.zeros((B, T), np.int32)
         for i, p in enumerate(prompts):
             ids[i, :len(p)] = np.asarray(p, np.int32)
         lens = [len(p) for p in prompts]
         last = [i * T + n - 1 for i, n in enumerate(lens)]
-        long = base_dtype == torch.float16 and M > short_rows
-        chunked = wkv_chunked_prefers(B, T, self.H) if wkv_chunked is None else bool(wkv_chunked)
+        # the chunk transforms' workspace (48 KiB per (row, head, chunk)) at most 16 GiB
+        chunked = (wkv_chunked_prefers(B, T, self.H) and B * self.H * ((T + 31) // 32) * 49152 <= (16 << 30)
+                   if wkv_chunked is None else bool(wkv_chunked))
         if graph:
             return self._prefill_graphed(ids, lens, last, B, T, long, chunked)
         ids_t = torch.from_numpy(ids.reshape(-1)).to(dev)

@@ -412,6 +412,26 @@ def test_prefill_time_chunked_wkv_matches_oracle(tiny_model):
     assert e < 1e-4 and ew < 1e-4
 
 
+def test_prefill_past_65535_rows_rows_independent(tiny_model):
+    """A long pass of more than 65535 rows (two prompts of 35,000 tokens: the
+    many-row layer norm, the dense GEMM route, the two-part low-rank kernel,
+    the time-chunked WKV): each row's logits and states equal that prompt
+    prefilled alone bitwise (every kernel on this path computes a row from
+    that row alone, in the same order for both launches)."""
+    case("prefill fp16 base, 70,000 rows")
+    proj, W = tiny_model
+    p = syn.x070_dense_params(TINY, seed=36, lora_dtype=np.float16)
+    dec = X070Decoder(TINY.n_layer, TINY.n_embd, TINY.ffn, TINY.vocab, p, proj, DEV)
+    rng = np.random.default_rng(36)
+    prompts = [[int(t) for t in rng.integers(0, TINY.vocab, 35000)] for _ in range(2)]
+    logits, st = dec.prefill_batch(prompts, base_dtype=torch.float16)
+    assert torch.isfinite(logits).all()
+    for i, pr in enumerate(prompts):
+        alone, st1 = dec.prefill_batch([pr], base_dtype=torch.float16)
+        assert torch.equal(alone[0], logits[i]), i
+        assert torch.equal(st1.wkv[:, 0], st.wkv[:, i]), i
+
+
 def test_prefill_then_decode_continues_the_prompt(tiny_model):
     """The state a parallel prefill leaves continues by decode steps exactly
     as decoding the prompt token by token does (fp32 base, 1e-4)."""
