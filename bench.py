@@ -793,6 +793,13 @@ def bench_prefill(dev, seconds_cap=60.0):
     sec = timed(lambda: dec.prefill_batch(prompt, base_dtype=torch.float16), 3)
     res["prefill_7B_B1_T8192_fp16base"] = {"ms": sec * 1e3, "tok_s": 8192 / sec, "reps": 3}
     log(f"prefill 7B T8192: {sec * 1e3:.1f} ms")
+    # batch 16 (the batched decode's prompts): 131,072 rows in one pass, ~61 GB of pass buffers
+    prompts16 = [list(rng.integers(0, shape.vocab, 8192)) for _ in range(16)]
+    sec16 = timed(lambda: dec.prefill_batch(prompts16, base_dtype=torch.float16), 1)
+    res["prefill_7B_B16_T8192_fp16base"] = {"ms": sec16 * 1e3, "tok_s": 16 * 8192 / sec16, "reps": 1}
+    log(f"prefill 7B B16 T8192: {sec16 * 1e3:.1f} ms")
+    dec._tmp.clear()
+    torch.cuda.empty_cache()
     res["gemm_7B_ffn_key_M8192"] = gemm_line(model, "blocks.0.ffn.key.weight", 8192)
     del dec, model
     torch.cuda.empty_cache()
