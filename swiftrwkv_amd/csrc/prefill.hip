@@ -247,6 +247,121 @@ __global__ __launch_bounds__(256) void seq_lora_kernel(LoraJobs jobs, int M) {
         }
 }
 
+// Few rows (short prompts): the tiles above leave most of the GPU idle and
+// each wave walks the whole K (768–4096 for the inner products) one step of
+// loads ahead.  Here a workgroup computes a 32 × 32 tile of y and its four
+// waves split K: wave q takes the K steps [q·S/4, (q+1)·S/4) of the S = K/16
+// steps as 2 × 2 tiles of 16 × 16 (the MFMA lane layout of seq_lora_kernel),
+// with groups of four steps loaded one group ahead in two register sets (fp16
+// weights stay packed until their group is used).  The four partial tiles are
+// summed through LDS in wave order, ((p0 + p1) + p2) + p3, then activated.
+// Every output's arithmetic depends only on its row of x, its row of W and K.
+template <typename TW>
+struct LoraRaw {
+    using T = float4;
+};
+template <>
+struct LoraRaw<__half> {
+    using T = uint2;
+};
+
+template <typename TW>
+__device__ __forceinline__ typename LoraRaw<TW>::T ldraw(const TW* p) {
+    return *reinterpret_cast<const typename LoraRaw<TW>::T*>(p);
+}
+__device__ __forceinline__ float4 widen(float4 v) { return v; }
+__device__ __forceinline__ float4 widen(uint2 u) {
+    const float2 a = __half22float2(*reinterpret_cast<const __half2*>(&u.x));
+    const float2 c = __half22float2(*reinterpret_cast<const __half2*>(&u.y));
+    return make_float4(a.x, a.y, c.x, c.y);
+}
+
+constexpr int64_t kLoraKsMaxRows = 512;
+
+template <typename TW>
+__global__ __launch_bounds__(256) void seq_lora_ks_kernel(LoraJobs jobs, int M) {
+    using WR = typename LoraRaw<TW>::T;
+    const LoraJob J = jobs.j[blockIdx.z];
+    if ((int)blockIdx.x * 32 >= J.N) return;   // this job has fewer column tiles (uniform)
+    __shared__ float red[4 * 16 * 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, i = lane & 15;
+    const int row0 = (int)blockIdx.y * 32, col0 = (int)blockIdx.x * 32;
+    // rows / columns past the end read the last one (results not stored)
+    const float* xr[2];
+    const TW* wr[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        xr[t] = J.x + (int64_t)min(row0 + 16 * t + i, M - 1) * J.ldx + 4 * g;
+        wr[t] = reinterpret_cast<const TW*>(J.w) + (int64_t)min(col0 + 16 * t + i, J.N - 1) * J.K + 4 * g;
+    }
+    const int S = J.K >> 4;
+    const int s0 = wave * S / 4, s1 = (wave + 1) * S / 4;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float4 xa[4][2], xb[4][2];
+    WR wa[4][2], wb[4][2];
+    // a group: steps s .. s + 3, the ones past s1 re-read step s1 − 1 and are
+    // skipped when used (wave-uniform)
+    auto load = [&](float4 (&x)[4][2], WR (&w)[4][2], int s) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = 16 * min(s + j, s1 - 1);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                x[j][t] = *reinterpret_cast<const float4*>(xr[t] + k);
+                w[j][t] = ldraw(wr[t] + k);
+            }
+        }
+    };
+    auto use = [&](const float4 (&x)[4][2], const WR (&w)[4][2], int s) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (s + j < s1) {
+                const float4 w0 = widen(w[j][0]), w1 = widen(w[j][1]);
+#pragma unroll
+                for (int a = 0; a < 2; ++a) {
+                    acc[a][0] = mfma4(x[j][a], w0, acc[a][0]);
+                    acc[a][1] = mfma4(x[j][a], w1, acc[a][1]);
+                }
+            }
+        }
+    };
+    if (s0 < s1) {
+        load(xa, wa, s0);
+        for (int s = s0; s < s1; s += 8) {
+            if (s + 4 < s1) load(xb, wb, s + 4);
+            use(xa, wa, s);
+            if (s + 4 >= s1) break;
+            if (s + 8 < s1) load(xa, wa, s + 8);
+            use(xb, wb, s + 4);
+        }
+    }
+    // partial tiles: red[wave][a][b][r][lane]
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[((wave * 4 + a * 2 + b) * 4 + r) * 64 + lane] = acc[a][b][r];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int e = threadIdx.x + 256 * u;   // (a, b, r, lane) of the tile
+        const int ln = e & 63, r = (e >> 6) & 3, b = (e >> 8) & 1, a = e >> 9;
+        float v = red[e];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) v += red[q * 1024 + e];
+        const int row = row0 + 16 * a + 4 * (ln >> 4) + r, col = col0 + 16 * b + (ln & 15);
+        if (J.act == 1) v = tanhf(v);
+        else if (J.act == 2) v = 1.0f / (1.0f + expf(-v));
+        if (row < M && col < J.N) J.y[(int64_t)row * J.ldy + col] = v;
+    }
+}
+
 // ── long passes: the fp32 activations as two fp16 parts on the fp16 matrix cores ──
 // The same y = act(x·Wᵀ) for fp16 W [N, K] with x [M, K] fp32 written
 // x = hi + lo, hi = fp16(x), lo = fp16(x − hi) (x − hi is exact in fp32):
@@ -550,6 +665,25 @@ rwkv_status rwkv_x070_seq_lora(const float* mix, int64_t M, int64_t D, const voi
         RWKV_REQUIRE(mt * c2 < INT32_MAX, RWKV_E_SHAPE, "x070_seq_lora: too many tiles");
         rwkv::launch(lora_split_kernel, dim3((unsigned)(mt * c1)), dim3(256), st, t1, (int)M);
         rwkv::launch(lora_split_kernel, dim3((unsigned)(mt * c2)), dim3(256), st, t2, (int)M);
+        RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "x070_seq_lora: launch failed");
+        rwkv::counters().x070.fetch_add(2);
+        rwkv::clear_error();
+        return RWKV_OK;
+    }
+    // few rows: the K-split tiles (both stages, MI355X): 0.1B-wide (D 768) at
+    // 128 rows 33 → 16 µs, 7B-class (D 4096) at 128 / 512 rows 158 → 56 /
+    // 186 → 165 µs; from ~1024 rows on the 64 × 64 tiles below are as fast or
+    // faster (D 2048, 1024 rows: 109 against 126 µs)
+    if (M <= kLoraKsMaxRows) {
+        const dim3 k1((unsigned)((maxn1 + 31) / 32), (unsigned)((M + 31) / 32), (unsigned)n);
+        const dim3 k2((unsigned)((D + 31) / 32), (unsigned)((M + 31) / 32), (unsigned)n);
+        if (w_dt == RWKV_F16) {
+            rwkv::launch(seq_lora_ks_kernel<__half>, k1, dim3(256), st, s1, (int)M);
+            rwkv::launch(seq_lora_ks_kernel<__half>, k2, dim3(256), st, s2, (int)M);
+        } else {
+            rwkv::launch(seq_lora_ks_kernel<float>, k1, dim3(256), st, s1, (int)M);
+            rwkv::launch(seq_lora_ks_kernel<float>, k2, dim3(256), st, s2, (int)M);
+        }
         RWKV_REQUIRE(hipGetLastError() == hipSuccess, RWKV_E_HIP, "x070_seq_lora: launch failed");
         rwkv::counters().x070.fetch_add(2);
         rwkv::clear_error();

@@ -235,6 +235,8 @@ def test_f16_gemm_matches_exact_products(M):
 
 
 @pytest.mark.parametrize("D,M,ranks,wdt", [(256, 37, (32, 32, 32, 64), torch.float16),
+                                             (768, 512, (16, 32, 16, 64), torch.float16),
+                                             (768, 513, (16, 32, 16, 64), torch.float32),
                                              (1024, 200, (64, 64, 32, 128), torch.float32),
                                              (4096, 70, (128, 128, 96, 480), torch.float16),
                                              (1024, 2100, (64, 64, 32, 160), torch.float16),
@@ -247,7 +249,9 @@ def test_seq_lora_matches_fp64(D, M, ranks, wdt, with_v):
     written when the layer has no v branch), gate = sigmoid(x_g·A_gᵀ)·B_gᵀ.
     Long passes with fp16 matrices (M·D above 2^21) take the two-part fp16
     kernel: the same bound (its activations keep 22 of 24 bits); odd stage
-    counts (ranks 96, 160) and partial row / column tiles included."""
+    counts (ranks 96, 160) and partial row / column tiles included.  Up to
+    512 rows the K-split kernel runs (ranks 16 and 32 leave some of its
+    waves without K steps); 513 rows take the 64 × 64 tiles."""
     case(f"seq lora D={D} M={M} ranks={ranks} {wdt} with_v={with_v}")
     from swiftrwkv_amd import _lib
     rng = np.random.default_rng(D + M + with_v)
