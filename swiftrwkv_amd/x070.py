@@ -39,8 +39,8 @@ LNX_EPS = 64e-5
 _COEF_ORDER = ("r", "k", "v", "w", "a", "g")   # rwkv_x070_shift_mix's coefficient order
 # The parallel pass's low-rank branches take rwkv_x070_seq_lora's fp32 kernel
 # (two launches, activations fused) up to this many rows × width: measured per
-# layer, 0.1B width × 128 rows 38 against 138 µs for the library GEMM, 1024 ×
-# 1024 60 against 66 µs.  Above it, passes with fp16 matrices take its
+# layer, 0.1B width × 128 rows 16 µs (its K-split tiles) against 138 µs for the
+# library GEMM, 1024 × 1024 60 against 66 µs.  Above it, passes with fp16 matrices take its
 # two-part fp16 kernel (rwkv_x070_seq_lora_split); fp32 matrices the
 # library's fp32 GEMM (4096 × 8192: 0.96 ms against 2.5 for the fp32 kernel).
 SEQ_LORA_MAX_MD = 1 << 21
@@ -123,10 +123,11 @@ def wkv_chunked_prefers(B: int, T: int, H: int) -> bool:
     """Whether the time-chunked WKV-7 forward beats the step-by-step kernel
     for a [B, T, H] pass on MI355X: the step kernel runs B·H·4 workgroups
     for T steps each, the chunked one B·H·⌈T/32⌉ workgroups and then a scan
-    of ⌈T/32⌉ steps, so it wins where B·H is small and T long (measured: B1
-    T1024 H12 48 vs 139 µs, B1 T8192 H64 0.77 vs 1.2 ms; B32 T128 H16 loses,
-    114 vs 63 µs)."""
-    return B * H <= 128 and T >= 512
+    of ⌈T/32⌉ steps, so it wins where B·H is small (measured, chunked vs
+    step: B1 T128 H12 15.4 vs 19.4 µs, B1 T128 H64 20.6 vs 22.2, B8 T128 H12
+    28.1 vs 33.3, B1 T256 H12 18.3 vs 36.4, B1 T1024 H12 48 vs 139, B1 T8192
+    H64 0.77 vs 1.2 ms; B32 T128 H16 loses, 114 vs 63 µs)."""
+    return B * H <= 128 and T >= 128
 
 
 class X070Decoder:
