@@ -472,7 +472,8 @@ rwkv_status rwkv_x070_ffn_value(const float* hk, const uint8_t* qblk, const uint
  * y1 (f32, may be NULL) receives the coefficients [y1_first, nc) at n·y1_row + c·y1_coef (the
  * low-rank branches read v, w, a, g: y1_first = 2 leaves r and k to y0 alone); prev_out [B, D] ← xl
  * of each row's last real token (gatherLast, :320-335).  nc = 6 (r, k, v, w, a, g) or 1.
- * prev_out must not alias prev_in. */
+ * prev_out may alias prev_in (the carried state of a row is updated in place;
+ * a row with lengths[b] = 0 keeps it). */
 rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float* prev_out, const int32_t* lengths,
                                     const float* coef, int nc, int n0, void* y0, rwkv_dtype y0_dt, int64_t y0_row,
                                     int64_t y0_coef, float* y1, int64_t y1_row, int64_t y1_coef, int y1_first, int64_t B, int64_t T,

@@ -33,12 +33,12 @@ __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast
 // NULL); m_c = xl + (prev_t − xl)·coef[c].  Coefficients [0, n0) go to y0
 // (fp16 or fp32, element (n, c) at n·y0_row + c·y0_coef); with y1, the
 // coefficients from y1_first on also go to y1 (fp32).  prev_out[b] ← xl[b, lengths[b] − 1] (the shift state of the row's
-// last real token, gatherLast).  One thread per 4 columns of one row.
+// last real token, gatherLast; may be prev_in).  One thread per 4 columns of one row.
 // I32: the thread index and its divisions in 32 bits (fewer than 2^31
 // threads; two 64-bit divisions per 4 columns cost more than the loads).
 template <int NC, bool F16, bool I32>
-__global__ __launch_bounds__(256) void seq_shift_kernel(const float* __restrict__ xl, const float* __restrict__ prev_in,
-                                                        float* __restrict__ prev_out, const int32_t* __restrict__ lengths,
+__global__ __launch_bounds__(256) void seq_shift_kernel(const float* __restrict__ xl, const float* prev_in,
+                                                        float* prev_out, const int32_t* __restrict__ lengths,
                                                         const float* __restrict__ coef, int n0, void* __restrict__ y0,
                                                         int64_t y0_row, int64_t y0_coef, float* __restrict__ y1,
                                                         int64_t y1_row, int64_t y1_coef, int y1_first, int T, int D,
@@ -66,8 +66,12 @@ __global__ __launch_bounds__(256) void seq_shift_kernel(const float* __restrict_
     float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
     if (t > 0) p = ld4(xl + (n - 1) * D + c);
     else if (prev_in) p = ld4(prev_in + (int64_t)b * D + c);
-    const int len = lengths ? lengths[b] : T;
-    if (t == len - 1) *reinterpret_cast<float4*>(prev_out + (int64_t)b * D + c) = x;
+    // the thread at t = 0 both reads the carried state and writes the new
+    // one (xl of the row's last real token), so prev_out may be prev_in;
+    // lengths past T read the row's last token (every read stays in the row)
+    const int len = lengths ? min(lengths[b], T) : T;
+    if (t == 0 && len > 0)
+        *reinterpret_cast<float4*>(prev_out + (int64_t)b * D + c) = len == 1 ? x : ld4(xl + (n + len - 1) * D + c);
     const float4 xx = make_float4(p.x - x.x, p.y - x.y, p.z - x.z, p.w - x.w);
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
@@ -548,7 +552,6 @@ rwkv_status rwkv_x070_seq_shift_mix(const float* xl, const float* prev_in, float
                  "x070_seq_shift_mix: B=%lld T=%lld D=%lld", (long long)B, (long long)T, (long long)D);
     RWKV_REQUIRE(y0_row % 4 == 0 && y0_coef % 4 == 0 && (!y1 || (y1_row % 4 == 0 && y1_coef % 4 == 0)),
                  RWKV_E_SHAPE, "x070_seq_shift_mix: output strides must be multiples of 4");
-    RWKV_REQUIRE(prev_out != prev_in, RWKV_E_SHAPE, "x070_seq_shift_mix: prev_out must not alias prev_in");
     RWKV_REQUIRE(y1_first >= 0 && y1_first <= nc, RWKV_E_SHAPE, "x070_seq_shift_mix: y1_first = %d", y1_first);
     const int64_t total = B * T * (D / 4);
     const dim3 grid((unsigned)((total + 255) / 256)), block(256);

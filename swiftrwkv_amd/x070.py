@@ -723,8 +723,7 @@ class X070Decoder:
             dev, D, F = self.device, self.D, self.F
             z = lambda *sh, dt=torch.float32: torch.empty(sh, dtype=dt, device=dev)
             bf = {"x": z(M, D), "xl": z(M, D), "mix": z(6, M, D), "y_rkv": z(M, 3 * D), "v_first": z(M, D),
-                  "ww": z(M, D), "aa": z(M, D), "vv": z(M, D), "gate": z(M, D), "wkv": z(M, D), "tout": z(M, D),
-                  "prev": z(max(1, M), D)}
+                  "ww": z(M, D), "aa": z(M, D), "vv": z(M, D), "gate": z(M, D), "wkv": z(M, D), "tout": z(M, D)}
             for n in ("r", "w", "k", "v", "a", "b", "kb"):
                 bf[n] = z(M, D)
             bf["rkv_in"] = z(3, M, D, dt=torch.float16) if long else z(M, 3, D)
@@ -759,15 +758,15 @@ class X070Decoder:
         # ── time mix ──
         _lib.check(L.rwkv_layer_norm(p(x), _lib.F32, None, 0, p(lay["ln1"][0]), p(lay["ln1"][1]), p(xl), M, D,
                                      LN_EPS, s))
-        prev = bf["prev"][:B]
         rkv_in = bf["rkv_in"]
         if long:   # r/k/v inputs fp16 [3, M, D] for the GEMM
             y0 = (rkv_in, _lib.F16, D, M * D)
         else:      # fp32 [M, 3, D] for the fused GEMV
             y0 = (rkv_in, _lib.F32, 3 * D, D)
-        _lib.check(L.rwkv_x070_seq_shift_mix(p(xl), p(state.tmix_prev[l]), p(prev), p(len_t), p(lay["coef6"]), 6, 3,
-                                             p(y0[0]), y0[1], y0[2], y0[3], p(mix), D, M * D, 2, B, T, D, s))
-        state.tmix_prev[l].copy_(prev)
+        # the carried shift state is updated in place
+        _lib.check(L.rwkv_x070_seq_shift_mix(p(xl), p(state.tmix_prev[l]), p(state.tmix_prev[l]), p(len_t),
+                                             p(lay["coef6"]), 6, 3, p(y0[0]), y0[1], y0[2], y0[3], p(mix), D, M * D,
+                                             2, B, T, D, s))
         self._prefill_proj(self.proj[f"blocks.{l}.att.rkv"], rkv_in, bf["y_rkv"], 0, M, long, s)
         rw, ra, rv, rg = self.ranks
         wdt = _dt(lay["wcat"])
@@ -811,10 +810,9 @@ class X070Decoder:
         _lib.check(L.rwkv_layer_norm(p(x), _lib.F32, None, 0, p(lay["ln2"][0]), p(lay["ln2"][1]), p(xl), M, D,
                                      LN_EPS, s))
         xk, hk = bf["xk"], bf["hk"]
-        _lib.check(L.rwkv_x070_seq_shift_mix(p(xl), p(state.cmix_prev[l]), p(prev), p(len_t), p(lay["ck"]), 1, 1,
-                                             p(xk), _lib.F16 if long else _lib.F32, D, M * D, None, 0, 0, 0, B, T, D,
-                                             s))
-        state.cmix_prev[l].copy_(prev)
+        _lib.check(L.rwkv_x070_seq_shift_mix(p(xl), p(state.cmix_prev[l]), p(state.cmix_prev[l]), p(len_t),
+                                             p(lay["ck"]), 1, 1, p(xk), _lib.F16 if long else _lib.F32, D, M * D,
+                                             None, 0, 0, 0, B, T, D, s))
         self._prefill_proj(self.proj[f"blocks.{l}.ffn.key.weight"], xk, hk, 2, M, long, s)
         self._prefill_proj(self.proj[f"blocks.{l}.ffn.value.weight"], hk, x, 1, M, long, s)
 

@@ -269,7 +269,8 @@ def test_seq_lora_matches_fp64(D, M, ranks, wdt, with_v):
     la = torch.empty((M, RT), device=DEV)
     outs = [torch.full((M, D), 7.0, device=DEV) for _ in range(4)]
     L = _lib.lib()
-    _lib.check(L.rwkv_x070_seq_lora(dev(mix).data_ptr(), M, D, A_d.data_ptr(), *[b.data_ptr() for b in B_d],
+    mix_d = dev(mix)   # held: the kernels run after the call returns
+    _lib.check(L.rwkv_x070_seq_lora(mix_d.data_ptr(), M, D, A_d.data_ptr(), *[b.data_ptr() for b in B_d],
                                     _lib.F16 if wdt == torch.float16 else _lib.F32, rw, ra, rv, rg, with_v,
                                     la.data_ptr(), *[o.data_ptr() for o in outs], torch.cuda.current_stream().cuda_stream))
     x = mix.astype(np.float64)
@@ -285,6 +286,48 @@ def test_seq_lora_matches_fp64(D, M, ranks, wdt, with_v):
         err = rel(want[b], got)
         print(f"[seq lora] D={D} M={M} {name}: rel {err:.2e}", flush=True)
         assert err < 2e-5, name
+
+
+@pytest.mark.parametrize("nc,f16", [(6, False), (1, True)])
+def test_seq_shift_mix_updates_state_in_place(nc, f16):
+    """rwkv_x070_seq_shift_mix with prev_out = prev_in (how the parallel pass
+    calls it): the carried state of each row becomes xl of its last real
+    token (rwkvTokenShift's gatherLast) and stays as it was for a row with no
+    tokens, bitwise as with separate buffers; t = 0 lerps against the old
+    state, t > 0 against the previous row."""
+    case(f"seq shift mix in place nc={nc} f16={f16}")
+    from swiftrwkv_amd import _lib
+    B, T, D = 4, 9, 256
+    rng = np.random.default_rng(nc)
+    xl = rng.standard_normal((B * T, D)).astype(np.float32)
+    prev = rng.standard_normal((B, D)).astype(np.float32)
+    coef = rng.random((nc, D)).astype(np.float32)
+    lens = np.array([T, 1, T - 3, 0], dtype=np.int32)
+    outs = {}
+    xl_d, lens_d, coef_d = dev(xl), dev(lens), dev(coef)   # held: the kernel runs after the call returns
+    for alias in (True, False):
+        st = dev(prev)
+        dst = st if alias else torch.full((B, D), 5.0, device=DEV)
+        if not alias:
+            dst[3] = st[3]   # a row with no tokens keeps its state
+        y0 = torch.empty((B * T, nc, D), dtype=torch.float16 if f16 else torch.float32, device=DEV)
+        _lib.check(_lib.lib().rwkv_x070_seq_shift_mix(
+            xl_d.data_ptr(), st.data_ptr(), dst.data_ptr(), lens_d.data_ptr(), coef_d.data_ptr(), nc, nc,
+            y0.data_ptr(), _lib.F16 if f16 else _lib.F32, nc * D, D, None, 0, 0, 0, B, T, D,
+            torch.cuda.current_stream().cuda_stream))
+        outs[alias] = (dst.cpu().numpy(), y0.float().cpu().numpy())
+    assert np.array_equal(outs[True][0], outs[False][0])
+    assert np.array_equal(outs[True][1], outs[False][1])
+    want_state = prev.copy()
+    for b in range(3):
+        want_state[b] = xl[b * T + lens[b] - 1]
+    assert np.array_equal(outs[True][0], want_state)
+    x = xl.reshape(B, T, D).astype(np.float64)
+    p = np.concatenate([prev[:, None].astype(np.float64), x[:, :-1]], axis=1)
+    want = x[:, :, None] + (p - x)[:, :, None] * coef.astype(np.float64)[None, None]
+    got = outs[True][1].reshape(B, T, nc, D)
+    tol = 2e-3 if f16 else 1e-6
+    assert np.abs(got - want).max() <= tol * max(1.0, np.abs(want).max())
 
 
 def test_sb6_gemm_epilogues_groups_and_row_independence(orc):
