@@ -74,7 +74,7 @@ def parse():
     p.add_argument("--skip-wkv", action="store_true")
     p.add_argument("--skip-more", action="store_true", help="skip batched / 7B-class decode and the prefill pass")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--mode", choices=["bench", "kernels", "e2e", "batch", "step", "prefill"], default="bench",
+    p.add_argument("--mode", choices=["bench", "kernels", "e2e", "batch", "step", "prefill", "prefill_short"], default="bench",
                    help="kernels: run each dominant kernel alone (for rocprofv3 counter passes); "
                         "e2e / batch: x070 decode tokens / batched GEMV + WKV decode steps only (for kernel traces); "
                         "step: the 1.5B headline step alone (eager tokens, then graph replays; counter passes); "
@@ -828,6 +828,30 @@ def profile_prefill(dev):
         log(f"prefill 7B T8192 pass {i}: {(time.perf_counter() - t0) * 1e3:.1f} ms")
 
 
+def profile_prefill_short(dev):
+    """The 0.1B prefill of one 128-token prompt (fp16 base): two eager passes
+    (the first makes the buffers), then 20 replays of the pass's HIP graph,
+    the ones to read in a kernel trace."""
+    import numpy as np
+    import torch
+    from swiftrwkv_amd import synthetic as syn
+    from swiftrwkv_amd.x070 import X070Decoder
+
+    shape = syn.X070_0B1
+    model = DecodeModel(shape, 1, dev, nthreads=min(16, os.cpu_count() or 1))
+    dense = syn.x070_dense_params(shape, seed=11)
+    dec = X070Decoder(shape.n_layer, shape.n_embd, shape.ffn, shape.vocab, dense, model.host, dev)
+    prompt = [list(np.random.default_rng(5).integers(0, shape.vocab, 128))]
+    for i in range(2):
+        dec.prefill_batch(prompt, base_dtype=torch.float16)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(20):
+        dec.prefill_batch(prompt, base_dtype=torch.float16, graph=True)
+    torch.cuda.synchronize()
+    log(f"prefill 0.1B B1 T128: {(time.perf_counter() - t0) / 20 * 1e3:.3f} ms per graph replay (with the first capture)")
+
+
 def bench_head_gemv(model, dev, reps=60):
     """Average duration of the head GEMV over rotated weight copies (HBM)."""
     import torch
@@ -1305,6 +1329,9 @@ def main():
         return
     if args.mode == "prefill":
         profile_prefill(dev)
+        return
+    if args.mode == "prefill_short":
+        profile_prefill_short(dev)
         return
     head = headline_1b5(args, dev)
     extra = {"decode_1.5B_gemv_wkv_chain_batch1": head["chain"], "decode_1.5B_batch16": head["batch16"]}
